@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Throughput of the reduction / scan hot path on one MI355X.
+
+Metric: achieved HBM GB/s (and fraction of the 8 TB/s peak)
+for the u32 exclusive scan and the f32 sum-reduce at 2^28 elements.  A step
+is one exclusive scan of the 2^28-element u32 operand; inputs
+are generated in HBM before timing, and every step is one launch of the
+single-pass look-back scan kernel.  The f32 sum-reduce at 2^28 is timed the
+same way and reported under "secondary".
+
+`value` and `roofline.achieved` are algorithmic bytes (read 4n + write 4n
+for the scan) divided by the mean launch time, measured with HIP events on
+the stream the kernels run on.  `cpu_baseline` times the CPU oracle (a
+sequential port of the same semantics) on this host over the same input.
+
+Usage: python bench.py [--steps K] [--warmup W] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_plan(dev, run, steps: int, warmup: int) -> float:
+    """Mean milliseconds per launch of `run` over `steps` back-to-back launches."""
+    for _ in range(warmup):
+        run()
+    dev.synchronize()
+    start, stop = dev.event(), dev.event()
+    start.record()
+    for _ in range(steps):
+        run()
+    stop.record()
+    stop.synchronize()
+    dev.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
+def traffic_for(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    f = REPO / "profiles" / "pmc_traffic.json"
+    if not f.exists():
+        return None
+    data = json.loads(f.read_text())
+    entry = data.get(name)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def roofline(bytes_per_launch: float, ms: float, name: str) -> dict:
+    achieved = bytes_per_launch / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_for(name)}
+
+
+def bench_scan_u32(hx, dev, args):
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.uint32, n)
+    dev.fill_uniform_int(x, seed=2, lo=0, hi=255)
+    out = dev.alloc_uninitialized(np.uint32, n)
+    lay = Layout.c_contiguous([n])
+    plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                                              StridedView(out, lay), hx.ScanKind.Exclusive)
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    nbytes = 2 * 4 * n
+    return {"n": n, "ms": ms, "bytes": nbytes, "x": x, "out": out}
+
+
+def bench_sum_f32(hx, dev, args):
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(x, seed=1, lo=-1.0, hi=1.0)
+    out = dev.alloc_zeroed(np.float32, 1)
+    plan = hx.RocmFullReductionOps().prepare_reduce_full(dev, hx.SumOp, StridedView(x, Layout.c_contiguous([n])),
+                                                         StridedView(out, Layout.c_contiguous([1])))
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    return {"n": n, "ms": ms, "bytes": 4 * n + 4, "x": x, "out": out}
+
+
+def bench_rows_f32(hx, dev, args):
+    rows, cols = 65536, 4096
+    x = dev.alloc_uninitialized(np.float32, rows * cols)
+    dev.fill_normal(x, seed=3)
+    s = dev.alloc_uninitialized(np.float32, rows)
+    m = dev.alloc_uninitialized(np.float32, rows)
+    i = dev.alloc_uninitialized(np.uint32, rows)
+    ops = hx.RocmAxisReductionOps()
+    run = lambda: ops.reduce_rows_fused(dev, x, rows, cols, prologue=(0.5, 0.25), out_sum=s, out_max=m, out_argmax=i)
+    ms = time_plan(dev, run, args.steps, args.warmup)
+    return {"n": rows * cols, "ms": ms, "bytes": 4 * rows * cols + 12 * rows}
+
+
+def bench_segmented_i32(hx, dev, args):
+    from oracle import oracle  # geometric offsets are generated on the host
+
+    n = 1 << 27
+    x = dev.alloc_uninitialized(np.int32, n)
+    dev.fill_uniform_int(x, seed=4, lo=-1000, hi=1000)
+    off = oracle.geometric_offsets(n, 300.0, seed=5)
+    ob = dev.upload(off)
+    out = dev.alloc_uninitialized(np.int32, off.size - 1)
+    plan = hx.RocmSegmentedReductionOps().prepare_segmented_sum(dev, x, ob, out)
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    s = off.size - 1
+    return {"n": n, "ms": ms, "bytes": 4 * n + 4 * (s + 1) + 4 * s}
+
+
+def bench_scan_f32_2_30(hx, dev, args):
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 30
+    x = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(x, seed=6, lo=0.0, hi=1.0)
+    out = dev.alloc_uninitialized(np.float32, n)
+    lay = Layout.c_contiguous([n])
+    plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                                              StridedView(out, lay))
+    ms = time_plan(dev, plan.dispatch, max(1, args.steps // 4), max(1, args.warmup // 2))
+    return {"n": n, "ms": ms, "bytes": 8 * n}
+
+
+def cpu_baseline(dev, scan, seconds: float) -> dict:
+    """Time the oracle's sequential exclusive scan on this host's cores over
+    the same 2^28-element input; verify the GPU output against it."""
+    from oracle import oracle
+
+    x = dev.download_owned(scan["x"])
+    got = dev.download_owned(scan["out"])
+    n = x.size
+    out = np.empty_like(x)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.lib().hxo_scan_sum_u32(x.ctypes.data, n, 1, 0, out.ctypes.data)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 50:
+            break
+    per = el / reps
+    verified = bool(np.array_equal(got, out))
+    threads = min(16, os.cpu_count() or 1)
+    t1 = time.perf_counter()
+    oracle.scan_excl_u32_threads(x, out, threads)
+    tt = time.perf_counter() - t1
+    return {
+        "value": round(8 * n / per / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"the full 2^28-element u32 exclusive scan, {reps} sequential passes of the C oracle "
+                  f"(oracle/hx_oracle.c hxo_scan_sum_u32), {per * 1e3:.1f} ms per pass",
+        "multithread": {"value": round(8 * n / tt / 1e9, 3), "cores": threads,
+                        "sample": "one pass of the two-pass pthread scan hxo_scan_excl_u32_threads"},
+        "gpu_output_verified": verified,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=("default", "all") + WORKLOADS, default="default")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        return 2
+
+    import hephaestus_amd as hx
+
+    dev = hx.RocmDevice.try_default()
+    topo = dev.topology()
+    log(f"device {topo.name} {topo.arch} CUs={topo.compute_units} lib={hx.native_library_path()}")
+
+    if args.workload not in ("default", "all"):
+        fn = globals()[f"bench_{args.workload}"]
+        r = fn(hx, dev, args)
+        gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        print(json.dumps({"workload": args.workload, "n": r["n"], "ms": round(r["ms"], 5),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                          "elements_per_s": round(r["n"] / (r["ms"] * 1e-3), 1)}))
+        return 0
+
+    scan = bench_scan_u32(hx, dev, args)
+    log(f"scan u32 2^28: {scan['ms']:.4f} ms/launch")
+    ssum = bench_sum_f32(hx, dev, args)
+    log(f"sum f32 2^28: {ssum['ms']:.4f} ms/launch")
+
+    value = scan["bytes"] / (scan["ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "achieved HBM GB/s (% of peak) for f32 sum-reduce and u32 scan at 2^28 elems",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(scan["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic (SplitMix64 seed 2, uniform integers in [0,256), generated in HBM)",
+        "config": {"workload": "u32 exclusive prefix scan, n=2^28 (BASELINE configs[1])",
+                   "n": scan["n"], "algorithmic_bytes_per_step": scan["bytes"],
+                   "elements_per_s": round(scan["n"] / (scan["ms"] * 1e-3), 1)},
+        "roofline": roofline(scan["bytes"], scan["ms"], "scan_u32_2_28"),
+        "secondary": {
+            "f32_sum_reduce_2_28": {
+                "value": round(ssum["bytes"] / (ssum["ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
+                "ms_per_launch": round(ssum["ms"], 5),
+                "elements_per_s": round(ssum["n"] / (ssum["ms"] * 1e-3), 1),
+                "roofline": roofline(ssum["bytes"], ssum["ms"], "sum_f32_2_28"),
+            }
+        },
+    }
+    if args.workload == "all":
+        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30"):
+            r = globals()[f"bench_{name}"](hx, dev, args)
+            gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+            line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
+                                       "frac": round(gbs / PEAK_GBS, 4)}
+            log(f"{name}: {r['ms']:.4f} ms/launch {gbs:.1f} GB/s")
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(dev, scan, args.cpu_seconds)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,207 @@
+// Device-side building blocks shared by every gfx950 kernel of the library:
+// wave64 reductions and scans, order-preserving keys for max/argmax, the
+// combining operators with their identities, and the counter-based
+// generator.  Header-only; included by the .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hx {
+
+constexpr int kWave = 64;
+
+// 16-byte vectors (one global_load_dwordx4 per lane).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct Vec4 { using type = u32x4; };
+template <> struct Vec4<float> { using type = f32x4; };
+
+// ----------------------------------------------------------------- lanes
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+// ------------------------------------------------------------ operators
+// Combining operators of crates/hephaestus-core/src/domain/ops.rs:735-803
+// with the identities of ops.rs:926-983.  `Acc` is the accumulation type:
+// f32 sums and products accumulate in f64 so the per-output error of a
+// reduction is one final rounding; integer sums and products wrap mod 2^32
+// exactly like `unsigned int` / `int` arithmetic in the reference kernels.
+
+template <typename T> struct SumAcc { using type = T; };
+template <> struct SumAcc<float> { using type = double; };
+
+struct OpSum {
+    template <typename A> __device__ __forceinline__ static A identity() { return A(0); }
+    template <typename A> __device__ __forceinline__ static A combine(A a, A b) { return a + b; }
+};
+struct OpProd {
+    template <typename A> __device__ __forceinline__ static A identity() { return A(1); }
+    template <typename A> __device__ __forceinline__ static A combine(A a, A b) { return a * b; }
+};
+
+// Integer sums and products use unsigned arithmetic so overflow wraps
+// (defined behaviour); the bits equal the reference's two's complement.
+template <typename T> struct Wrap { using type = T; };
+template <> struct Wrap<int32_t> { using type = uint32_t; };
+
+// -------------------------------------------------------- ordered keys
+// Max and min are computed on order-preserving 32-bit keys, which makes
+// them exact and independent of combination order:
+//   f32: key = bits ^ (sign ? 0xFFFFFFFF : 0x80000000), the IEEE total order
+//        (-inf < ... < -0 < +0 < ... < +inf); NaN maps to the key that
+//        never wins (0 for max, 0xFFFFFFFF for min), so NaN is ignored like
+//        HIP fmaxf/fminf, the reference's `max(lhs, rhs)` (ops.rs:902-919).
+//   i32: key = bits ^ 0x80000000;  u32: key = value.
+// The MaxOp identity f32::MIN (ops.rs:956-958) is folded in by the caller.
+
+__device__ __forceinline__ uint32_t f32_key_max(float x) {
+    uint32_t b = __float_as_uint(x);
+    uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+    return (x != x) ? 0u : k;
+}
+__device__ __forceinline__ uint32_t f32_key_min(float x) {
+    uint32_t b = __float_as_uint(x);
+    uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+    return (x != x) ? 0xFFFFFFFFu : k;
+}
+__device__ __forceinline__ float f32_from_key(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k;
+    return __uint_as_float(b);
+}
+
+template <typename T> struct Key;
+template <> struct Key<float> {
+    __device__ __forceinline__ static uint32_t max_key(float x) { return f32_key_max(x); }
+    __device__ __forceinline__ static uint32_t min_key(float x) { return f32_key_min(x); }
+    __device__ __forceinline__ static float decode(uint32_t k) { return f32_from_key(k); }
+    // key of f32::MIN / f32::MAX (the MaxOp / MinOp identities)
+    __device__ __forceinline__ static uint32_t max_identity() { return f32_key_max(-3.40282347e+38f); }
+    __device__ __forceinline__ static uint32_t min_identity() { return f32_key_min(3.40282347e+38f); }
+};
+template <> struct Key<uint32_t> {
+    __device__ __forceinline__ static uint32_t max_key(uint32_t x) { return x; }
+    __device__ __forceinline__ static uint32_t min_key(uint32_t x) { return x; }
+    __device__ __forceinline__ static uint32_t decode(uint32_t k) { return k; }
+    __device__ __forceinline__ static uint32_t max_identity() { return 0u; }
+    __device__ __forceinline__ static uint32_t min_identity() { return 0xFFFFFFFFu; }
+};
+template <> struct Key<int32_t> {
+    __device__ __forceinline__ static uint32_t max_key(int32_t x) { return (uint32_t)x ^ 0x80000000u; }
+    __device__ __forceinline__ static uint32_t min_key(int32_t x) { return (uint32_t)x ^ 0x80000000u; }
+    __device__ __forceinline__ static int32_t decode(uint32_t k) { return (int32_t)(k ^ 0x80000000u); }
+    __device__ __forceinline__ static uint32_t max_identity() { return 0u; }
+    __device__ __forceinline__ static uint32_t min_identity() { return 0xFFFFFFFFu; }
+};
+
+// Argmax packs (key, index) into one u64 so that an unsigned max picks the
+// largest key and, among equal keys, the LOWEST index:
+//   packed = key << 32 | ~index.
+// Packed 0 means "no element" (empty input, or only NaN for f32).
+__device__ __forceinline__ uint64_t pack_arg(uint32_t key, uint32_t index) {
+    return ((uint64_t)key << 32) | (uint64_t)(~index);
+}
+__device__ __forceinline__ uint32_t arg_index(uint64_t packed) {
+    return ~(uint32_t)(packed & 0xFFFFFFFFull);
+}
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// ---------------------------------------------------- wave64 collectives
+// Butterfly (xor) reductions: every lane ends with the same bits, and the
+// combination tree is fixed, so results are deterministic.
+
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, kWave);
+    return v;
+}
+template <typename T> __device__ __forceinline__ T wave_prod(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v * __shfl_xor(v, m, kWave);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) { uint32_t o = __shfl_xor(v, m, kWave); v = v > o ? v : o; }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) { uint32_t o = __shfl_xor(v, m, kWave); v = v < o ? v : o; }
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_umax64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = umax64(v, __shfl_xor(v, m, kWave));
+    return v;
+}
+
+template <typename Op, typename A> __device__ __forceinline__ A wave_reduce(A v);
+template <> __device__ __forceinline__ double wave_reduce<OpSum, double>(double v) { return wave_sum(v); }
+template <> __device__ __forceinline__ uint32_t wave_reduce<OpSum, uint32_t>(uint32_t v) { return wave_sum(v); }
+template <> __device__ __forceinline__ float wave_reduce<OpSum, float>(float v) { return wave_sum(v); }
+template <> __device__ __forceinline__ double wave_reduce<OpProd, double>(double v) { return wave_prod(v); }
+template <> __device__ __forceinline__ uint32_t wave_reduce<OpProd, uint32_t>(uint32_t v) { return wave_prod(v); }
+
+// Inclusive Hillis-Steele scan across the 64 lanes (6 steps).
+template <typename Op, typename A> __device__ __forceinline__ A wave_inclusive_scan(A v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        A t = __shfl_up(v, d, kWave);
+        if (lane >= d) v = Op::combine(t, v);
+    }
+    return v;
+}
+
+template <typename A> __device__ __forceinline__ A wave_broadcast(A v, int src) { return __shfl(v, src, kWave); }
+
+// 64-bit lane masks from wave-wide predicates.
+__device__ __forceinline__ uint64_t ballot(bool p) { return (uint64_t)__ballot(p); }
+
+// ---------------------------------------------------- agent-scope atomics
+// Look-back status words are read and written with agent-scope atomics so
+// every XCD's L2 observes them coherently.
+
+__device__ __forceinline__ uint64_t ld_relaxed(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_acquire(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_relaxed32(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_relaxed(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_release32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_relaxed32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t fetch_add32(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t fetch_add32_acqrel(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_relaxed_f64(double *p, double v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_relaxed_f64(const double *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------ generator
+// SplitMix64 (Steele, Lea, Flood, "Fast splittable pseudorandom number
+// generators", OOPSLA 2014): output i for seed s is mix(s + (i+1)*gamma).
+__host__ __device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + (i + 1ull) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+} // namespace hx

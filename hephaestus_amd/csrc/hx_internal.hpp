@@ -1,0 +1,190 @@
+// Host-side internals shared by the runtime, the planners and the kernel
+// launchers.  Nothing here crosses the C ABI.
+#pragma once
+
+#include "../../include/hx.h"
+
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+
+// The device handle behind hx_device* (RocmDevice analog:
+// crates/hephaestus-rocm/src/infrastructure/device.rs:109-165).
+struct hx_device {
+    int32_t ordinal = -1;
+    hipStream_t stream = nullptr;
+    hx_device_info info{};
+
+    // Pinned double-buffered staging for host<->device transfers.
+    std::mutex staging_mu;
+    void *pinned[2] = {nullptr, nullptr};
+    uint64_t pinned_bytes = 0;
+    hipEvent_t pinned_ev[2] = {nullptr, nullptr};
+
+    // Workspace for the immediate (un-prepared) entry points.
+    std::mutex ws_mu;
+    void *ws = nullptr;
+    uint64_t ws_bytes = 0;
+    int ws_format = 0;
+};
+
+namespace hx {
+
+// ------------------------------------------------------------- errors
+
+hx_status ok();
+hx_status fail(hx_status status, const char *fmt, ...)
+    __attribute__((format(printf, 2, 3)));
+hx_status length_mismatch(uint64_t host_len, uint64_t device_len);
+// Map a HIP error to `status` with "<what>: <hip error string>".
+hx_status hip_fail(hx_status status, hipError_t err, const char *what);
+
+#define HX_TRY(expr)                                                         \
+    do {                                                                     \
+        hx_status hx_try_status_ = (expr);                                   \
+        if (hx_try_status_ != HX_OK) return hx_try_status_;                  \
+    } while (0)
+
+#define HX_HIP(call, status, what)                                           \
+    do {                                                                     \
+        hipError_t hx_hip_err_ = (call);                                     \
+        if (hx_hip_err_ != hipSuccess)                                       \
+            return ::hx::hip_fail((status), hx_hip_err_, (what));            \
+    } while (0)
+
+hx_status bind_device(const hx_device *dev);
+hipStream_t pick_stream(const hx_device *dev, hx_stream stream);
+// Map the status of a kernel launch (hipGetLastError) to DispatchFailed.
+hx_status check_launch(const char *kernel);
+
+// ------------------------------------------------------------- layouts
+
+std::string shape_string(const hx_layout &l);
+// Row-major (C-contiguous) over every extent > 1: the view is the flat
+// element range [offset, offset + size).
+bool layout_is_c_contiguous(const hx_layout &l);
+// Strides are a permutation of a dense row-major stride set (all positive):
+// the view covers exactly [offset, offset + size) in some order.
+bool layout_is_permuted_dense(const hx_layout &l);
+hx_status layout_basic_check(const hx_layout *l, const char *what);
+
+// ----------------------------------------------------------- workspace
+// Header of every workspace (256 bytes), followed by kernel-specific data.
+struct WorkspaceHeader {
+    uint32_t reduce_done;  // full reduce: blocks finished (reset by the last)
+    uint32_t pad0[3];
+    uint32_t tile_counter; // look-back: virtual tile ticket
+    uint32_t tile_done;    // look-back: tiles finished (reset by the last)
+    uint32_t epoch;        // look-back: launch counter, tags status words
+    uint32_t pad1[57];
+};
+static_assert(sizeof(WorkspaceHeader) == 256, "workspace header is 256 bytes");
+constexpr uint64_t kWorkspaceHeader = 256;
+
+enum WorkspaceFormat {
+    kWsNone = 0,
+    kWsReduce = 1,
+    kWsLookbackPacked = 2, // 64-bit (tag|flag|value) words
+    kWsLookbackF64 = 3,    // flag words + f64 aggregate + f64 prefix arrays
+};
+
+// Immediate-mode workspace of `dev`, grown (and zeroed) on demand.  When a
+// look-back kernel of another status format last used it, the status area is
+// cleared so stale words cannot be misread.
+hx_status device_workspace(hx_device *dev, uint64_t bytes, int format,
+                           hipStream_t stream, void **ws);
+hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws);
+
+// ------------------------------------------------------------- kernels
+
+struct FullReduceArgs {
+    hx_op op;
+    hx_dtype dtype;
+    const void *base;    // buffer base pointer
+    hx_layout layout;    // logical view
+    uint64_t n;          // logical size
+    bool flat;           // view is the flat range [flat_offset, +n)
+    uint64_t flat_offset;
+    bool affine;
+    float a, b;
+    void *out_value;     // T[1] (may be null for argmax)
+    uint32_t *out_index; // u32[1] (argmax only)
+};
+uint64_t full_reduce_workspace_bytes(uint64_t n);
+hx_status launch_full_reduce(const FullReduceArgs &args, void *ws,
+                             hipStream_t stream);
+
+struct RowsArgs {
+    hx_dtype dtype;
+    const void *base;
+    uint64_t rows, cols, row_stride, offset;
+    bool affine;
+    float a, b;
+    void *out_sum, *out_max;
+    uint32_t *out_argmax;
+};
+hx_status launch_rows(const RowsArgs &args, hipStream_t stream);
+
+struct AxisArgs {
+    hx_op op;
+    hx_dtype dtype;
+    const void *in;
+    void *out;
+    uint64_t outer;      // number of outputs
+    uint64_t axis_len;   // reduced extent
+    int64_t in_outer_stride, in_axis_stride;
+    uint64_t in_offset;
+    int64_t out_stride;
+    uint64_t out_offset;
+};
+hx_status launch_axis_reduce(const AxisArgs &args, hipStream_t stream);
+
+struct ScanArgs {
+    hx_op op;
+    hx_dtype dtype;
+    bool exclusive, reverse;
+    const void *in;
+    void *out;
+    uint64_t lines, len;
+    int64_t in_line_stride, in_elem_stride;
+    uint64_t in_offset;
+    int64_t out_line_stride, out_elem_stride;
+    uint64_t out_offset;
+};
+uint64_t scan_workspace_bytes(const ScanArgs &args, int *format);
+hx_status launch_scan(const ScanArgs &args, void *ws, hipStream_t stream);
+
+struct SegmentedArgs {
+    hx_op op;
+    hx_dtype dtype;
+    const void *values;
+    uint64_t n;
+    const uint32_t *offsets;
+    uint64_t num_segments; // S (num_offsets - 1)
+    void *out;
+};
+uint64_t segmented_workspace_bytes(const SegmentedArgs &args, int *format);
+hx_status launch_segmented(const SegmentedArgs &args, void *ws,
+                           hipStream_t stream);
+hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,
+                                     uint64_t num_offsets, uint64_t n);
+
+hx_status launch_fill_random(void *dst, uint64_t n, hx_dtype dtype,
+                             hx_distribution dist, uint64_t seed, double p0,
+                             double p1, hipStream_t stream);
+
+// Grid sizing shared by the launchers.
+inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+} // namespace hx
+
+// A prepared dispatch (the reference's Prepared associated types, e.g.
+// crates/hephaestus-rocm/src/application/full_reduction_seam.rs:33-43).
+struct hx_plan {
+    hx_device *dev = nullptr;
+    void *ws = nullptr;
+    uint64_t ws_bytes = 0;
+    virtual ~hx_plan();
+    virtual hx_status dispatch(hipStream_t stream) = 0;
+};

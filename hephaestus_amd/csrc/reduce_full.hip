@@ -1,0 +1,319 @@
+// Full (whole-operand) reductions for gfx950: FullReductionOps
+// (crates/hephaestus-core/src/domain/reduction.rs:243-309).
+//
+// The reference runs a 256-lane LDS halving tree with one element per thread
+// and one launch per tree pass (crates/hephaestus-rocm/src/application/
+// reduction.rs:16-52, prepared_reduction.rs:39-132), after a strided staging
+// copy (full_reduction_seam.rs:102-120).  Here ONE launch does the whole
+// job and reads the operand exactly once:
+//   pass 1  every block grid-strides over the operand with 16-byte loads,
+//           folds into registers (f32 sums in f64), reduces its 4 waves with
+//           xor-butterflies and writes one partial;
+//   pass 2  the block that finishes last (agent-scope acq_rel ticket) folds
+//           the partials in index order and writes the result.
+// The grid size is a function of n only, so the combination order and the
+// result bits do not depend on the GPU's CU count.
+#include "hx_device.hpp"
+#include "hx_internal.hpp"
+
+#include <type_traits>
+
+namespace hx {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxBlocks = 2048;
+constexpr uint64_t kReduceArea = 64 * 1024; // partials area after the header
+
+enum Kind { kSum = 0, kProd = 1, kMin = 2, kMax = 3, kArgmax = 4, kMean = 5 };
+
+// Per-kind accumulation policy.
+template <typename T, int K> struct Policy;
+
+template <typename T> struct Policy<T, kSum> {
+    using Acc = typename SumAcc<typename Wrap<T>::type>::type;
+    __device__ static Acc identity() { return Acc(0); }
+    template <typename Y> __device__ static Acc lift(Y y, uint64_t) { return (Acc)(typename Wrap<T>::type)y; }
+    __device__ static Acc combine(Acc a, Acc b) { return a + b; }
+    __device__ static Acc wave(Acc a) { return wave_sum(a); }
+};
+template <> struct Policy<float, kSum> {
+    using Acc = double;
+    __device__ static Acc identity() { return 0.0; }
+    __device__ static Acc lift(float y, uint64_t) { return (double)y; }
+    __device__ static Acc combine(Acc a, Acc b) { return a + b; }
+    __device__ static Acc wave(Acc a) { return wave_sum(a); }
+};
+template <typename T> struct Policy<T, kMean> : Policy<T, kSum> {};
+
+template <typename T> struct Policy<T, kProd> {
+    using W = typename Wrap<T>::type;
+    using Acc = W;
+    __device__ static Acc identity() { return Acc(1); }
+    __device__ static Acc lift(T y, uint64_t) { return (W)y; }
+    __device__ static Acc combine(Acc a, Acc b) { return a * b; }
+    __device__ static Acc wave(Acc a) { return wave_prod(a); }
+};
+template <> struct Policy<float, kProd> {
+    using Acc = double;
+    __device__ static Acc identity() { return 1.0; }
+    __device__ static Acc lift(float y, uint64_t) { return (double)y; }
+    __device__ static Acc combine(Acc a, Acc b) { return a * b; }
+    __device__ static Acc wave(Acc a) { return wave_prod(a); }
+};
+
+template <typename T> struct Policy<T, kMax> {
+    using Acc = uint32_t;
+    __device__ static Acc identity() { return Key<T>::max_identity(); }
+    __device__ static Acc lift(T y, uint64_t) { return Key<T>::max_key(y); }
+    __device__ static Acc combine(Acc a, Acc b) { return a > b ? a : b; }
+    __device__ static Acc wave(Acc a) { return wave_umax(a); }
+};
+template <typename T> struct Policy<T, kMin> {
+    using Acc = uint32_t;
+    __device__ static Acc identity() { return Key<T>::min_identity(); }
+    __device__ static Acc lift(T y, uint64_t) { return Key<T>::min_key(y); }
+    __device__ static Acc combine(Acc a, Acc b) { return a < b ? a : b; }
+    __device__ static Acc wave(Acc a) { return wave_umin(a); }
+};
+template <typename T> struct Policy<T, kArgmax> {
+    using Acc = uint64_t;
+    __device__ static Acc identity() { return 0ull; }
+    __device__ static Acc lift(T y, uint64_t i) { return pack_arg(Key<T>::max_key(y), (uint32_t)i); }
+    __device__ static Acc combine(Acc a, Acc b) { return umax64(a, b); }
+    __device__ static Acc wave(Acc a) { return wave_umax64(a); }
+};
+
+struct FullParams {
+    const void *base;
+    uint64_t n;
+    uint64_t offset; // element offset of the view (flat) / layout offset
+    uint32_t rank;
+    uint64_t shape[4];
+    int64_t strides[4];
+    float a, b;
+    void *out_value;
+    uint32_t *out_index;
+    WorkspaceHeader *hdr;
+    void *partials;
+};
+
+template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
+template <> __device__ __forceinline__ float prologue<float, true>(float x, float a, float b) {
+    return __builtin_fmaf(a, x, b);
+}
+
+// Address of logical (row-major) element i of a rank<=4 strided view.
+__device__ __forceinline__ int64_t strided_offset(const FullParams &p, uint64_t i) {
+    int64_t off = (int64_t)p.offset;
+    for (int d = (int)p.rank - 1; d >= 0; --d) {
+        uint64_t s = p.shape[d];
+        uint64_t q = i / s;
+        off += (int64_t)(i - q * s) * p.strides[d];
+        i = q;
+    }
+    return off;
+}
+
+template <typename P>
+__device__ __forceinline__ typename P::Acc block_reduce(typename P::Acc v,
+                                                        typename P::Acc *lds) {
+    v = P::wave(v);
+    const int w = threadIdx.x / kWave;
+    if (lane_id() == 0) lds[w] = v;
+    __syncthreads();
+    typename P::Acc r = lds[0];
+#pragma unroll
+    for (int k = 1; k < kBlock / kWave; ++k) r = P::combine(r, lds[k]);
+    __syncthreads();
+    return r;
+}
+
+template <typename T, int K>
+__device__ __forceinline__ void write_result_impl(const FullParams &p, typename Policy<T, K>::Acc r) {
+    if constexpr (K == kSum || K == kProd) {
+        *(T *)p.out_value = (T)r;
+    } else if constexpr (K == kMean) {
+        if constexpr (std::is_same<T, float>::value) {
+            *(float *)p.out_value = (float)(r / (double)p.n);
+        } else if constexpr (std::is_same<T, int32_t>::value) {
+            *(int32_t *)p.out_value = (int32_t)r / (int32_t)p.n;
+        } else {
+            *(uint32_t *)p.out_value = (uint32_t)r / (uint32_t)p.n;
+        }
+    } else if constexpr (K == kMax || K == kMin) {
+        *(T *)p.out_value = Key<T>::decode(r);
+    } else { // argmax
+        uint32_t key = (uint32_t)(r >> 32);
+        bool none = std::is_same<T, float>::value ? (key == 0u) : (r == 0ull);
+        if (p.out_index) *p.out_index = none ? 0xFFFFFFFFu : arg_index(r);
+        if (p.out_value) {
+            uint32_t mk = Key<T>::max_identity();
+            if (!none && key > mk) mk = key;
+            *(T *)p.out_value = Key<T>::decode(mk);
+        }
+    }
+}
+
+// FLAT: the view is the contiguous element range [offset, offset + n).
+template <typename T, int K, bool AFFINE, bool FLAT>
+__global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
+    using P = Policy<T, K>;
+    using Acc = typename P::Acc;
+    __shared__ Acc lds[kBlock / kWave];
+    __shared__ uint32_t s_last;
+
+    const uint64_t n = p.n;
+    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
+    Acc acc = P::identity();
+
+    if constexpr (FLAT) {
+        const T *src = (const T *)p.base + p.offset;
+        // Peel up to 3 leading elements so the body is 16-byte aligned.
+        uint64_t mis = ((uintptr_t)src >> 2) & 3u;
+        uint64_t head = mis ? (4 - mis) : 0;
+        if (head > n) head = n;
+        if (tid < head) acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[tid], p.a, p.b), tid));
+        const uint64_t nvec = (n - head) >> 2;
+        using V = typename Vec4<T>::type;
+        const V *vsrc = (const V *)(src + head);
+        uint64_t vi = tid;
+        // Four independent 16-byte loads in flight per thread per trip.
+        for (; vi + 3 * nthreads < nvec; vi += 4 * nthreads) {
+            V v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(&vsrc[vi + u * nthreads]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint64_t e = head + 4 * (vi + u * nthreads);
+                Acc a0 = P::lift(prologue<T, AFFINE>((T)v[u].x, p.a, p.b), e);
+                Acc a1 = P::lift(prologue<T, AFFINE>((T)v[u].y, p.a, p.b), e + 1);
+                Acc a2 = P::lift(prologue<T, AFFINE>((T)v[u].z, p.a, p.b), e + 2);
+                Acc a3 = P::lift(prologue<T, AFFINE>((T)v[u].w, p.a, p.b), e + 3);
+                acc = P::combine(acc, P::combine(P::combine(a0, a1), P::combine(a2, a3)));
+            }
+        }
+        for (; vi < nvec; vi += nthreads) {
+            V v = __builtin_nontemporal_load(&vsrc[vi]);
+            const uint64_t e = head + 4 * vi;
+            Acc a0 = P::lift(prologue<T, AFFINE>((T)v.x, p.a, p.b), e);
+            Acc a1 = P::lift(prologue<T, AFFINE>((T)v.y, p.a, p.b), e + 1);
+            Acc a2 = P::lift(prologue<T, AFFINE>((T)v.z, p.a, p.b), e + 2);
+            Acc a3 = P::lift(prologue<T, AFFINE>((T)v.w, p.a, p.b), e + 3);
+            acc = P::combine(acc, P::combine(P::combine(a0, a1), P::combine(a2, a3)));
+        }
+        const uint64_t tail0 = head + 4 * nvec;
+        if (tail0 + tid < n) {
+            const uint64_t e = tail0 + tid;
+            acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[e], p.a, p.b), e));
+        }
+    } else {
+        const T *src = (const T *)p.base;
+        for (uint64_t i = tid; i < n; i += nthreads)
+            acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[strided_offset(p, i)], p.a, p.b), i));
+    }
+
+    Acc part = block_reduce<P>(acc, lds);
+    Acc *partials = (Acc *)p.partials;
+    if (threadIdx.x == 0) {
+        partials[blockIdx.x] = part;
+        // Release this block's partial; the RMW chain makes every partial
+        // visible to the block that observes the final count.
+        uint32_t prev = fetch_add32_acqrel(&p.hdr->reduce_done, 1u);
+        s_last = (prev == gridDim.x - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;
+
+    // Pass 2: fixed-order fold of the partials by the last block.
+    Acc r = P::identity();
+    for (uint32_t k = threadIdx.x; k < gridDim.x; k += kBlock) {
+        Acc v;
+        if constexpr (sizeof(Acc) == 8) {
+            v = __builtin_bit_cast(Acc, ld_relaxed((const uint64_t *)&partials[k]));
+        } else {
+            v = __builtin_bit_cast(Acc, ld_relaxed32((const uint32_t *)&partials[k]));
+        }
+        r = P::combine(r, v);
+    }
+    r = block_reduce<P>(r, lds);
+    if (threadIdx.x == 0) {
+        write_result_impl<T, K>(p, r);
+        st_relaxed32(&p.hdr->reduce_done, 0u); // ready for the next launch
+    }
+}
+
+// n == 0: the result is the operator identity (ops.rs:926-983); empty
+// argmax has no index.
+template <typename T, int K> __global__ void full_reduce_empty_kernel(FullParams p) {
+    using P = Policy<T, K>;
+    if (threadIdx.x == 0 && blockIdx.x == 0) write_result_impl<T, K>(p, P::identity());
+}
+
+template <typename T, int K, bool AFFINE>
+hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+    FullParams p{};
+    p.base = a.base;
+    p.n = a.n;
+    p.offset = a.flat ? a.flat_offset : a.layout.offset;
+    p.rank = a.layout.rank;
+    for (uint32_t d = 0; d < 4; ++d) {
+        p.shape[d] = d < a.layout.rank ? a.layout.shape[d] : 1;
+        p.strides[d] = d < a.layout.rank ? a.layout.strides[d] : 0;
+    }
+    p.a = a.a;
+    p.b = a.b;
+    p.out_value = a.out_value;
+    p.out_index = a.out_index;
+    p.hdr = (WorkspaceHeader *)ws;
+    p.partials = (char *)ws + kWorkspaceHeader;
+    if (a.n == 0) {
+        if constexpr (K == kMean) {
+            return fail(HX_ERR_DISPATCH_FAILED, "mean is undefined for an empty operand");
+        } else {
+            hipLaunchKernelGGL((full_reduce_empty_kernel<T, K>), dim3(1), dim3(64), 0, stream, p);
+            return check_launch("full_reduce_empty_kernel");
+        }
+    }
+    uint64_t blocks = ceil_div(a.n, 8192);
+    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+    if (blocks < 1) blocks = 1;
+    if (a.flat)
+        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, true>), dim3((uint32_t)blocks),
+                           dim3(kBlock), 0, stream, p);
+    else
+        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, false>), dim3((uint32_t)blocks),
+                           dim3(kBlock), 0, stream, p);
+    return check_launch("full_reduce_kernel");
+}
+
+template <typename T, bool AFFINE>
+hx_status launch_kind(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+    switch (a.op) {
+    case HX_OP_SUM: return launch_typed<T, kSum, AFFINE>(a, ws, stream);
+    case HX_OP_PROD: return launch_typed<T, kProd, AFFINE>(a, ws, stream);
+    case HX_OP_MIN: return launch_typed<T, kMin, AFFINE>(a, ws, stream);
+    case HX_OP_MAX: return launch_typed<T, kMax, AFFINE>(a, ws, stream);
+    case HX_OP_ARGMAX: return launch_typed<T, kArgmax, AFFINE>(a, ws, stream);
+    case HX_OP_MEAN: return launch_typed<T, kMean, AFFINE>(a, ws, stream);
+    }
+    return fail(HX_ERR_INVALID_CONFIGURATION, "unknown reduction operator %d", (int)a.op);
+}
+
+} // namespace
+
+uint64_t full_reduce_workspace_bytes(uint64_t) { return kWorkspaceHeader + kReduceArea; }
+
+hx_status launch_full_reduce(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+    switch (a.dtype) {
+    case HX_DTYPE_F32:
+        return a.affine ? launch_kind<float, true>(a, ws, stream)
+                        : launch_kind<float, false>(a, ws, stream);
+    case HX_DTYPE_U32: return launch_kind<uint32_t, false>(a, ws, stream);
+    case HX_DTYPE_I32: return launch_kind<int32_t, false>(a, ws, stream);
+    }
+    return fail(HX_ERR_INVALID_CONFIGURATION, "unknown dtype %d", (int)a.dtype);
+}
+
+} // namespace hx

@@ -1,0 +1,328 @@
+// Segmented sum for gfx950 (north-star config 4).  Offsets follow the CSR
+// row_ptr convention (crates/hephaestus-core/src/domain/sparse.rs:179-220):
+// S+1 entries, offsets[0] = 0, offsets[S] = n, non-decreasing, and
+//   out[s] = sum of values[offsets[s] .. offsets[s+1])   (mod 2^32).
+//
+// The reference's nearest kernel is CSR SpMV with one thread per row and a
+// serial inner loop (crates/hephaestus-rocm/src/application/sparse/
+// spmv.rs:17-42), which leaves neighbouring lanes hundreds of elements
+// apart.  Here the work is cut by ELEMENTS, not by segments, so every block
+// streams the same 16 KiB with 16-byte loads whatever the segment lengths:
+//
+//   * a block takes a virtual tile ticket and loads 4096 values, wave-striped
+//     like the scan;
+//   * while those loads are in flight, three waves run 64-ary searches over
+//     the offsets for the segment boundaries the tile touches;
+//   * the tile's inclusive prefix goes to LDS; every segment that ENDS in the
+//     tile gets E[end] - E[start] (plus the carry for the segment that began
+//     in an earlier tile);
+//   * the carry is a segmented decoupled look-back: a tile that contains a
+//     segment start publishes its carry-out at once as a "prefix", so the
+//     look-back almost always stops at the nearest predecessor.
+// Integer addition mod 2^32 is associative, so every output is bit-exact.
+#include "hx_device.hpp"
+#include "hx_internal.hpp"
+
+namespace hx {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kSteps = 4;
+constexpr int kWaveElems = kWave * 4 * kSteps; // 1024
+constexpr int kTile = kWaves * kWaveElems;     // 4096
+constexpr uint64_t kLookbackOffset = 256 + 64 * 1024;
+
+constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
+
+__device__ __forceinline__ uint32_t epoch_tag(uint32_t epoch) { return (epoch % 0x3FFFFFFFu) + 1u; }
+
+struct SegParams {
+    const uint32_t *values;
+    uint64_t n;
+    const uint32_t *offsets;
+    uint64_t segments; // S
+    uint32_t *out;
+    uint64_t total_tiles;
+    WorkspaceHeader *hdr;
+    uint64_t *status;
+};
+
+// Offsets clamped into [0, n]: malformed offsets can never address values
+// out of bounds.
+__device__ __forceinline__ uint64_t off_at(const SegParams &p, uint64_t k) {
+    const uint64_t o = p.offsets[k];
+    return o < p.n ? o : p.n;
+}
+
+// First k in [0, S] with off(k) > v, or S+1 if none (upper bound).  Each
+// round probes 64 evenly spaced positions, one per lane, and keeps the gap
+// between the last "<= v" and the first "> v" probe.  Terminates for any
+// offset contents because the range strictly shrinks.
+__device__ uint64_t wave_upper_bound(const SegParams &p, uint64_t v) {
+    const int lane = lane_id();
+    uint64_t lo = 0, hi = p.segments + 1;
+    while (hi > lo) {
+        const uint64_t len = hi - lo;
+        const uint64_t step = (len + kWave - 1) / kWave;
+        uint64_t pos = lo + (uint64_t)(lane + 1) * step - 1;
+        if (pos > hi - 1) pos = hi - 1;
+        const bool pred = off_at(p, pos) > v;
+        const uint64_t m = ballot(pred);
+        if (m == 0ull) return hi;
+        const int f = __ffsll((long long)m) - 1;
+        const uint64_t pf = __shfl(pos, f, kWave);
+        if (step == 1) return pf; // every position in the range was probed
+        const uint64_t pprev = f > 0 ? __shfl(pos, f - 1, kWave) : 0;
+        lo = f > 0 ? pprev + 1 : lo;
+        hi = pf + 1;
+        if (hi - lo == 1) return lo;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
+    __shared__ uint32_t s_ticket, s_tag;
+    __shared__ uint64_t s_bound[3];
+    __shared__ uint32_t s_wave_tot[kWaves];
+    __shared__ uint32_t s_carry;
+    __shared__ uint32_t E[kTile + 1];
+
+    if (threadIdx.x == 0) {
+        s_ticket = fetch_add32(&p.hdr->tile_counter, 1u);
+        s_tag = epoch_tag(ld_relaxed32(&p.hdr->epoch));
+    }
+    __syncthreads();
+    const uint64_t tile = s_ticket;
+    const uint32_t tag = s_tag;
+    const int w = threadIdx.x / kWave;
+    const int lane = lane_id();
+    const uint64_t t0 = tile * kTile;
+    const uint64_t t1 = (t0 + kTile < p.n) ? t0 + kTile : p.n;
+    const uint64_t e0 = t0 + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+
+    // Issue the value loads first; the searches below overlap them.
+    uint32_t x[kSteps][4];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+        if (e + 3 < p.n) {
+            const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(p.values + e));
+            x[j][0] = v.x;
+            x[j][1] = v.y;
+            x[j][2] = v.z;
+            x[j][3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[j][c] = (e + c < p.n) ? p.values[e + c] : 0u;
+        }
+    }
+
+    // k_lo = ub(t0): first offset past the tile start (segment of t0 is
+    // k_lo - 1); k_hi1 = ub(t1); k_star = ub(t1 - 1) (segment of t1-1 is
+    // k_star - 1).
+    if (w >= 1) {
+        const uint64_t v = (w == 1) ? t0 : (w == 2) ? t1 : t1 - 1;
+        const uint64_t r = wave_upper_bound(p, v);
+        if (lane == 0) s_bound[w - 1] = r;
+    }
+
+    // Tile-local inclusive prefix of the values (mod 2^32).
+    uint32_t carry = 0;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const uint32_t p0 = x[j][0];
+        const uint32_t p1 = p0 + x[j][1];
+        const uint32_t p2 = p1 + x[j][2];
+        const uint32_t p3 = p2 + x[j][3];
+        const uint32_t incl = wave_inclusive_scan<OpSum, uint32_t>(p3);
+        uint32_t lex = __shfl_up(incl, 1, kWave);
+        if (lane == 0) lex = 0;
+        const uint32_t step_tot = __shfl(incl, kWave - 1, kWave);
+        const uint32_t base = carry + lex;
+        x[j][0] = base + p0;
+        x[j][1] = base + p1;
+        x[j][2] = base + p2;
+        x[j][3] = base + p3;
+        carry += step_tot;
+    }
+    if (lane == 0) s_wave_tot[w] = carry;
+    __syncthreads();
+    uint32_t wave_excl = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k)
+        if (k < w) wave_excl += s_wave_tot[k];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const int le = w * kWaveElems + j * (kWave * 4) + lane * 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) E[le + c + 1] = wave_excl + x[j][c];
+    }
+    if (threadIdx.x == 0) E[0] = 0;
+    __syncthreads();
+
+    const uint64_t k_lo = s_bound[0];
+    const uint64_t k_hi1 = s_bound[1];
+    const uint64_t k_star = s_bound[2];
+    const uint64_t tlen = t1 - t0;
+    const uint32_t total = E[tlen];
+
+    if (w == 0) {
+        // Start of the segment holding t1-1, and of the one holding t0.
+        uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
+        if (h > t1 - 1) h = t1 - 1; // only reachable with malformed offsets
+        const uint64_t first_start = k_lo >= 1 ? off_at(p, k_lo - 1) : 0;
+        const bool has_head = h >= t0;
+        const bool needs_carry = tile > 0 && first_start < t0;
+        uint32_t c_in = 0;
+        if (has_head) {
+            const uint32_t out_val = total - E[h - t0];
+            if (lane == 0) {
+                const uint64_t word = ((uint64_t)((tag << 2) | kPrefix) << 32) | out_val;
+                st_relaxed(&p.status[tile], word);
+            }
+        } else if (tile > 0 && lane == 0) {
+            const uint64_t word = ((uint64_t)((tag << 2) | kAggregate) << 32) | total;
+            st_relaxed(&p.status[tile], word);
+        }
+        if (needs_carry || (!has_head && tile > 0)) {
+            // Look back over predecessors until a prefix (a tile holding a
+            // segment start, or one that already resolved its carry).
+            int64_t pred = (int64_t)tile - 1;
+            for (;;) {
+                const int64_t idx = pred - lane;
+                uint32_t flag = kPrefix, val = 0;
+                for (;;) {
+                    if (idx >= 0) {
+                        const uint64_t wd = ld_relaxed(&p.status[idx]);
+                        const uint32_t hi = (uint32_t)(wd >> 32);
+                        flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
+                        val = (uint32_t)wd;
+                    }
+                    const uint64_t pm = ballot(flag == kPrefix);
+                    const uint64_t im = ballot(flag == kInvalid);
+                    const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
+                    if ((im & need) == 0ull) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                const uint64_t pm = ballot(flag == kPrefix);
+                const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
+                c_in += wave_sum((lane <= first) ? val : 0u);
+                if (pm) break;
+                pred -= kWave;
+            }
+        }
+        if (!has_head && tile > 0 && lane == 0) {
+            const uint64_t word = ((uint64_t)((tag << 2) | kPrefix) << 32) | (uint32_t)(c_in + total);
+            st_relaxed(&p.status[tile], word);
+        }
+        if (lane == 0) s_carry = c_in;
+    }
+    __syncthreads();
+    const uint32_t c_in = s_carry;
+
+    // Segments s = k-1 whose end offset off(k) lies in (t0, t1]; tile 0 also
+    // owns the empty segments that end at 0.
+    uint64_t k_first = tile == 0 ? 1 : (k_lo > 1 ? k_lo : 1);
+    uint64_t k_last = k_hi1 >= 1 ? k_hi1 - 1 : 0;
+    if (k_last > p.segments) k_last = p.segments;
+    for (uint64_t k = k_first + threadIdx.x; k <= k_last; k += kBlock) {
+        const uint64_t b = off_at(p, k);
+        uint64_t a = off_at(p, k - 1);
+        if (a > b) a = b; // malformed: treat as empty
+        if (b < t0 || b > t1) continue; // malformed (non-monotonic) offsets
+        const uint64_t a_loc = (a > t0 ? a : t0) - t0;
+        uint32_t v = E[b - t0] - E[a_loc];
+        if (a < t0) v += c_in;
+        p.out[k - 1] = v;
+    }
+
+    if (threadIdx.x == 0) {
+        const uint32_t d = fetch_add32_acqrel(&p.hdr->tile_done, 1u);
+        if (d == (uint32_t)(p.total_tiles - 1)) {
+            st_relaxed32(&p.hdr->tile_counter, 0u);
+            st_relaxed32(&p.hdr->tile_done, 0u);
+            st_relaxed32(&p.hdr->epoch, ld_relaxed32(&p.hdr->epoch) + 1u);
+        }
+    }
+}
+
+// n == 0: every segment is empty.
+__global__ void segmented_zero_kernel(uint32_t *out, uint64_t s) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < s;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = 0u;
+}
+
+// Bit 0: offsets[0] != 0 or offsets[S] != n.  Bit 1: a decrease.
+__global__ void validate_offsets_kernel(const uint32_t *offsets, uint64_t count, uint64_t n,
+                                        uint32_t *flags) {
+    const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < count; k += nthreads) {
+        const uint32_t o = offsets[k];
+        if ((k == 0 && o != 0u) || (k == count - 1 && (uint64_t)o != n)) atomicOr(&flags[0], 1u);
+        if (k + 1 < count && offsets[k + 1] < o) atomicOr(&flags[0], 2u);
+    }
+}
+
+} // namespace
+
+uint64_t segmented_workspace_bytes(const SegmentedArgs &a, int *format) {
+    *format = kWsLookbackPacked;
+    return kLookbackOffset + ceil_div(a.n, kTile) * 8;
+}
+
+hx_status launch_segmented(const SegmentedArgs &a, void *ws, hipStream_t stream) {
+    if (a.num_segments == 0) return HX_OK;
+    if (a.n == 0) {
+        uint64_t blocks = ceil_div(a.num_segments, kBlock);
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(segmented_zero_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                           (uint32_t *)a.out, a.num_segments);
+        return check_launch("segmented_zero_kernel");
+    }
+    SegParams p{};
+    p.values = (const uint32_t *)a.values;
+    p.n = a.n;
+    p.offsets = a.offsets;
+    p.segments = a.num_segments;
+    p.out = (uint32_t *)a.out;
+    p.total_tiles = ceil_div(a.n, kTile);
+    p.hdr = (WorkspaceHeader *)ws;
+    p.status = (uint64_t *)((char *)ws + kLookbackOffset);
+    if (p.total_tiles >= 0xFFFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the u32 ticket range",
+                    (unsigned long long)p.total_tiles);
+    if (((uintptr_t)a.values) % 16 != 0)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 16-byte aligned");
+    hipLaunchKernelGGL(segmented_sum_kernel, dim3((uint32_t)p.total_tiles), dim3(kBlock), 0, stream, p);
+    return check_launch("segmented_sum_kernel");
+}
+
+hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets, uint64_t count,
+                                     uint64_t n) {
+    uint32_t *flags = nullptr;
+    HX_HIP(hipMalloc(&flags, 4), HX_ERR_ALLOCATION_FAILED, "validation flag hipMalloc");
+    hipError_t err = hipMemsetAsync(flags, 0, 4, dev->stream);
+    if (err == hipSuccess) {
+        uint64_t blocks = ceil_div(count, kBlock);
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(validate_offsets_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           dev->stream, offsets, count, n, flags);
+        err = hipGetLastError();
+    }
+    uint32_t host = 0;
+    if (err == hipSuccess) err = hipMemcpyAsync(&host, flags, 4, hipMemcpyDeviceToHost, dev->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(dev->stream);
+    (void)hipFree(flags);
+    if (err != hipSuccess) return hip_fail(HX_ERR_DISPATCH_FAILED, err, "offset validation");
+    // Messages follow validate_csr (core sparse.rs:186-212).
+    if (host & 1u)
+        return fail(HX_ERR_DISPATCH_FAILED,
+                    "invalid segment offsets: offsets must start at 0 and end at the element count");
+    if (host & 2u)
+        return fail(HX_ERR_DISPATCH_FAILED, "invalid segment offsets: offsets must be non-decreasing");
+    return HX_OK;
+}
+
+} // namespace hx

@@ -1,0 +1,257 @@
+"""`RocmDevice` / `RocmBuffer`: the ComputeDevice and DeviceBuffer<T> seams
+(crates/hephaestus-core/src/domain/device.rs:90-224, buffer.rs:7-19) over
+the C ABI.  Host data is exchanged as numpy arrays of float32 / uint32 /
+int32; device memory is owned by `RocmBuffer` and freed when it is
+garbage-collected (the reference frees in Drop: crates/hephaestus-rocm/src/
+infrastructure/buffer.rs:16-80).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _ffi, errors
+
+DTYPES = {
+    np.dtype(np.float32): _ffi.DTYPE_F32,
+    np.dtype(np.uint32): _ffi.DTYPE_U32,
+    np.dtype(np.int32): _ffi.DTYPE_I32,
+}
+
+
+def hx_dtype(dtype) -> int:
+    try:
+        return DTYPES[np.dtype(dtype)]
+    except KeyError:
+        raise errors.InvalidConfiguration(f"unsupported element type {np.dtype(dtype)}") from None
+
+
+@dataclass(frozen=True)
+class Topology:
+    """Probed hardware topology (query_topology, rocm query.rs:104-177)."""
+
+    name: str
+    arch: str
+    compute_units: int
+    warp_width: int
+    max_threads_per_block: int
+    max_threads_per_unit: int
+    lds_bytes_per_block: int
+    l2_bytes: int
+    total_memory_bytes: int
+    free_memory_bytes: int
+    clock_khz: int
+    memory_clock_khz: int
+    memory_bus_width_bits: int
+
+
+class RocmBuffer:
+    """A typed, device-resident linear buffer of `len` elements."""
+
+    def __init__(self, device: "RocmDevice", ptr: int | None, length: int, dtype):
+        self.device = device
+        self.ptr = ptr or None
+        self._len = int(length)
+        self.dtype = np.dtype(dtype)
+
+    def __len__(self) -> int:
+        return self._len
+
+    def len(self) -> int:
+        return self._len
+
+    def is_empty(self) -> bool:
+        return self._len == 0
+
+    def tier(self) -> str:
+        return "device-hbm"
+
+    @property
+    def itemsize(self) -> int:
+        return self.dtype.itemsize
+
+    def free(self) -> None:
+        if self.ptr and self.device is not None and self.device.handle:
+            _ffi.check(_ffi.lib().hx_free(self.device.handle, self.ptr))
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class RocmDevice:
+    """An acquired AMD GPU (RocmDevice::try_with_ordinal, rocm device.rs:109-165)."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+        info = _ffi.HxDeviceInfo()
+        _ffi.check(_ffi.lib().hx_device_get_info(self.handle, ctypes.byref(info)))
+        self._topology = Topology(
+            name=info.name.decode(errors="replace"),
+            arch=info.arch.decode(errors="replace"),
+            compute_units=info.compute_units,
+            warp_width=info.warp_size,
+            max_threads_per_block=info.max_threads_per_block,
+            max_threads_per_unit=info.max_threads_per_cu,
+            lds_bytes_per_block=info.lds_bytes_per_block,
+            l2_bytes=info.l2_bytes,
+            total_memory_bytes=info.total_memory_bytes,
+            free_memory_bytes=info.free_memory_bytes,
+            clock_khz=info.clock_khz,
+            memory_clock_khz=info.memory_clock_khz,
+            memory_bus_width_bits=info.memory_bus_width_bits,
+        )
+        stream = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().hx_device_stream(self.handle, ctypes.byref(stream)))
+        self.stream = stream.value
+
+    # -- acquisition ---------------------------------------------------
+    @staticmethod
+    def device_count() -> int:
+        count = ctypes.c_int32()
+        _ffi.check(_ffi.lib().hx_device_count(ctypes.byref(count)))
+        return count.value
+
+    @classmethod
+    def try_with_ordinal(cls, ordinal: int) -> "RocmDevice":
+        handle = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().hx_device_open(int(ordinal), ctypes.byref(handle)))
+        return cls(handle.value)
+
+    @classmethod
+    def try_default(cls) -> "RocmDevice":
+        return cls.try_with_ordinal(0)
+
+    def close(self) -> None:
+        if self.handle:
+            _ffi.check(_ffi.lib().hx_device_close(self.handle))
+            self.handle = None
+
+    # -- ComputeDevice -------------------------------------------------
+    def backend_name(self) -> str:
+        return "rocm"
+
+    def topology(self) -> Topology:
+        return self._topology
+
+    def synchronize(self) -> None:
+        _ffi.check(_ffi.lib().hx_synchronize(self.handle))
+
+    def _alloc(self, dtype, length: int, zeroed: bool) -> RocmBuffer:
+        hx_dtype(dtype)
+        ptr = ctypes.c_void_p()
+        nbytes = int(length) * np.dtype(dtype).itemsize
+        _ffi.check(_ffi.lib().hx_alloc(self.handle, nbytes, 1 if zeroed else 0, ctypes.byref(ptr)))
+        return RocmBuffer(self, ptr.value, length, dtype)
+
+    def alloc_zeroed(self, dtype, length: int) -> RocmBuffer:
+        return self._alloc(dtype, length, True)
+
+    def alloc_uninitialized(self, dtype, length: int) -> RocmBuffer:
+        return self._alloc(dtype, length, False)
+
+    def upload(self, host) -> RocmBuffer:
+        host = np.ascontiguousarray(host)
+        buf = self.alloc_uninitialized(host.dtype, host.size)
+        self.write_buffer(buf, host)
+        return buf
+
+    def write_buffer(self, buffer: RocmBuffer, host) -> None:
+        host = np.ascontiguousarray(host, dtype=buffer.dtype)
+        _ffi.check(
+            _ffi.lib().hx_upload(
+                self.handle, buffer.ptr, len(buffer), host.ctypes.data, host.size, buffer.itemsize
+            )
+        )
+
+    def write_sub_buffer(self, buffer: RocmBuffer, offset: int, host) -> None:
+        host = np.ascontiguousarray(host, dtype=buffer.dtype)
+        _ffi.check(
+            _ffi.lib().hx_write_sub(
+                self.handle, buffer.ptr, len(buffer), int(offset), host.ctypes.data, host.size,
+                buffer.itemsize,
+            )
+        )
+
+    def download(self, buffer: RocmBuffer, out: np.ndarray) -> None:
+        if not (isinstance(out, np.ndarray) and out.flags.c_contiguous and out.dtype == buffer.dtype):
+            raise errors.InvalidConfiguration("download target must be a C-contiguous array of the buffer dtype")
+        _ffi.check(
+            _ffi.lib().hx_download(
+                self.handle, buffer.ptr, len(buffer), out.ctypes.data, out.size, buffer.itemsize
+            )
+        )
+
+    def download_owned(self, buffer: RocmBuffer) -> np.ndarray:
+        out = np.empty(len(buffer), dtype=buffer.dtype)
+        self.download(buffer, out)
+        return out
+
+    def copy_buffer(self, src: RocmBuffer, dst: RocmBuffer) -> None:
+        if src.dtype != dst.dtype:
+            raise errors.InvalidConfiguration("copy_buffer between different element types")
+        _ffi.check(
+            _ffi.lib().hx_copy(self.handle, src.ptr, len(src), dst.ptr, len(dst), src.itemsize)
+        )
+
+    # -- synthetic inputs (RandomInitOps analog) -----------------------
+    def fill_uniform_int(self, buffer: RocmBuffer, seed: int, lo: int, hi: int, stream=None) -> None:
+        _ffi.check(
+            _ffi.lib().hx_fill_random(
+                self.handle, buffer.ptr, len(buffer), hx_dtype(buffer.dtype), _ffi.DIST_UNIFORM_INT,
+                int(seed), float(lo), float(hi), stream,
+            )
+        )
+
+    def fill_uniform_real(self, buffer: RocmBuffer, seed: int, lo: float, hi: float, stream=None) -> None:
+        _ffi.check(
+            _ffi.lib().hx_fill_random(
+                self.handle, buffer.ptr, len(buffer), hx_dtype(buffer.dtype), _ffi.DIST_UNIFORM_REAL,
+                int(seed), float(lo), float(hi), stream,
+            )
+        )
+
+    def fill_normal(self, buffer: RocmBuffer, seed: int, mean: float = 0.0, std: float = 1.0, stream=None) -> None:
+        _ffi.check(
+            _ffi.lib().hx_fill_random(
+                self.handle, buffer.ptr, len(buffer), hx_dtype(buffer.dtype), _ffi.DIST_NORMAL,
+                int(seed), float(mean), float(std), stream,
+            )
+        )
+
+    # -- events ---------------------------------------------------------
+    def event(self) -> "Event":
+        return Event(self)
+
+
+class Event:
+    """A HIP event recorded on a stream (timing of kernels on that stream)."""
+
+    def __init__(self, device: RocmDevice):
+        self.device = device
+        ev = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().hx_event_create(device.handle, ctypes.byref(ev)))
+        self.handle = ev.value
+
+    def record(self, stream=None) -> None:
+        _ffi.check(_ffi.lib().hx_event_record(self.device.handle, self.handle, stream))
+
+    def synchronize(self) -> None:
+        _ffi.check(_ffi.lib().hx_event_synchronize(self.handle))
+
+    def elapsed_ms(self, stop: "Event") -> float:
+        ms = ctypes.c_float()
+        _ffi.check(_ffi.lib().hx_event_elapsed_ms(self.handle, stop.handle, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                _ffi.lib().hx_event_destroy(self.handle)
+        except Exception:
+            pass

@@ -1,0 +1,369 @@
+/*
+ * hx.h — C ABI of hephaestus-amd, the MI355X (gfx950) reduction / scan backend.
+ *
+ * Every entry point takes plain pointers, sizes and small POD structs; no C++
+ * or framework types cross this boundary.  Device pointers are the values
+ * returned by hx_alloc (a hipMalloc allocation); a zero-byte allocation is the
+ * null pointer and every operation accepts it for an empty operand.
+ *
+ * Status codes map one-to-one onto the reference error vocabulary
+ * (crates/hephaestus-core/src/domain/error.rs:8-58).  On failure the entry
+ * point stores a message in thread-local storage (hx_last_error_message) and
+ * leaves every output untouched: validation always runs before the first
+ * write (conformance clauses crates/hephaestus-conformance/src/
+ * full_reduction.rs:213-231 and scan.rs:129-149).
+ *
+ * Element counts are uint64_t throughout; the kernels index with 64-bit
+ * offsets, so operands of 2^30 elements (4 GiB) and beyond are addressable.
+ *
+ * Streams: every operation takes an hx_stream (a hipStream_t).  NULL selects
+ * the device's own stream, created at hx_device_open with default priority.
+ * Operations are stream-ordered and asynchronous; hx_download, hx_upload,
+ * hx_write_sub, hx_copy and hx_synchronize are synchronous, like the
+ * reference's transfers (crates/hephaestus-rocm/src/infrastructure/
+ * memory.rs:102-131,207-258).
+ */
+#ifndef HX_H
+#define HX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HX_ABI_VERSION 1u
+#define HX_MAX_RANK 4u
+
+/* ---------------------------------------------------------------- status */
+
+/* crates/hephaestus-core/src/domain/error.rs:8-58 (HephaestusError). */
+typedef enum hx_status {
+    HX_OK = 0,
+    HX_ERR_ADAPTER_UNAVAILABLE = 1,   /* AdapterUnavailable   error.rs:11-15 */
+    HX_ERR_DEVICE_UNAVAILABLE = 2,    /* DeviceUnavailable    error.rs:17-21 */
+    HX_ERR_ALLOCATION_FAILED = 3,     /* AllocationFailed     error.rs:24-28 */
+    HX_ERR_LENGTH_MISMATCH = 4,       /* LengthMismatch       error.rs:30-36 */
+    HX_ERR_DISPATCH_FAILED = 5,       /* DispatchFailed       error.rs:38-42 */
+    HX_ERR_INVALID_CONFIGURATION = 6, /* InvalidConfiguration error.rs:45-49 */
+    HX_ERR_TRANSFER_FAILED = 7        /* TransferFailed       error.rs:51-55 */
+} hx_status;
+
+typedef enum hx_dtype {
+    HX_DTYPE_F32 = 0, /* DialectScalar<HipC> "float"        core dialect.rs:116-126 */
+    HX_DTYPE_U32 = 1, /* "unsigned int"; sums wrap mod 2^32 */
+    HX_DTYPE_I32 = 2  /* "int"; two's complement wrap       */
+} hx_dtype;
+
+/* Combining operators: crates/hephaestus-core/src/domain/ops.rs:735-803
+ * (SumOp, ProdOp, MinOp, MaxOp) with identities ops.rs:926-983.  ARGMAX is
+ * the north-star addition (index of the maximum, ties to the lowest index);
+ * MEAN mirrors mean_axis_kernel (crates/hephaestus-rocm/src/application/
+ * axis_reduction.rs:67-112). */
+typedef enum hx_op {
+    HX_OP_SUM = 0,
+    HX_OP_PROD = 1,
+    HX_OP_MIN = 2,
+    HX_OP_MAX = 3,
+    HX_OP_ARGMAX = 4,
+    HX_OP_MEAN = 5
+} hx_op;
+
+typedef enum hx_scan_kind {
+    HX_SCAN_INCLUSIVE = 0, /* reference form: core accelerator/scan.rs:56-155 */
+    HX_SCAN_EXCLUSIVE = 1  /* north-star addition: out[i] = fold(x[0..i))    */
+} hx_scan_kind;
+
+/* crates/hephaestus-core/src/domain/scan.rs:36-43 (ScanDirection). */
+typedef enum hx_scan_direction {
+    HX_SCAN_FORWARD = 0,
+    HX_SCAN_REVERSE = 1
+} hx_scan_direction;
+
+/* Strided view of a linear buffer: the leto Layout<N> that
+ * crates/hephaestus-core/src/domain/view.rs:27-41 pairs with a buffer.
+ * Element (i0..i{r-1}) lives at offset + sum(i_k * strides[k]). */
+typedef struct hx_layout {
+    uint32_t rank;
+    uint32_t reserved;
+    uint64_t shape[HX_MAX_RANK];
+    int64_t strides[HX_MAX_RANK];
+    uint64_t offset;
+} hx_layout;
+
+/* Fused elementwise prologue y = fmaf(a, x, b), applied to every f32 element
+ * before it is combined.  The reference spells this as a separate
+ * ParameterizedUnaryExpr launch "x * first + second" (core parameterized.rs:
+ * 16-45) writing a temporary; here it is fused into the reduction's load. */
+typedef struct hx_affine {
+    float a;
+    float b;
+    uint32_t enabled;
+    uint32_t reserved;
+} hx_affine;
+
+/* Limits and topology: crates/hephaestus-rocm/src/infrastructure/
+ * query.rs:29-177 (query_device_limits, query_topology). */
+typedef struct hx_device_info {
+    char name[96];
+    char arch[64];
+    int32_t ordinal;
+    uint32_t compute_units;
+    uint32_t warp_size;
+    uint32_t max_threads_per_block;
+    uint32_t max_threads_per_cu;
+    uint32_t lds_bytes_per_block;
+    uint32_t regs_per_block;
+    uint32_t clock_khz;
+    uint32_t memory_clock_khz;
+    uint32_t memory_bus_width_bits;
+    uint64_t l2_bytes;
+    uint64_t total_memory_bytes;
+    uint64_t free_memory_bytes;
+} hx_device_info;
+
+typedef struct hx_device hx_device; /* opaque: RocmDevice */
+typedef struct hx_plan hx_plan;     /* opaque: a prepared dispatch */
+typedef void *hx_stream;            /* hipStream_t; NULL = device stream */
+typedef void *hx_event;             /* hipEvent_t */
+
+/* ---------------------------------------------------------- diagnostics */
+
+uint32_t hx_abi_version(void);
+const char *hx_status_name(hx_status status);
+/* Message of the last failed call on this thread ("" after a success). */
+const char *hx_last_error_message(void);
+/* Lengths carried by the last HX_ERR_LENGTH_MISMATCH on this thread
+ * (error.rs:30-36: host_len, device_len). */
+void hx_last_length_mismatch(uint64_t *host_len, uint64_t *device_len);
+
+/* ------------------------------------------------- device (ComputeDevice) */
+
+/* hipGetDeviceCount; 0 devices is HX_OK with *count = 0. */
+hx_status hx_device_count(int32_t *count);
+/* RocmDevice::try_with_ordinal (crates/hephaestus-rocm/src/infrastructure/
+ * device.rs:109-165), including the 42 sanity round trip (:141-163).
+ * No device / bad ordinal -> HX_ERR_ADAPTER_UNAVAILABLE. */
+hx_status hx_device_open(int32_t ordinal, hx_device **out);
+hx_status hx_device_close(hx_device *dev);
+hx_status hx_device_get_info(const hx_device *dev, hx_device_info *out);
+/* The device's own stream (what a NULL hx_stream selects). */
+hx_status hx_device_stream(const hx_device *dev, hx_stream *out);
+/* ComputeDevice::synchronize (core device.rs:218-223). */
+hx_status hx_synchronize(hx_device *dev);
+
+/* alloc_zeroed / alloc_uninitialized (core device.rs:96-121).  A zero-byte
+ * request returns NULL and makes no HIP call (rocm memory.rs:75-88). */
+hx_status hx_alloc(hx_device *dev, uint64_t bytes, uint32_t zeroed, void **out);
+hx_status hx_free(hx_device *dev, void *ptr);
+
+/* write_buffer (core device.rs:178-184): dst_len must equal src_len
+ * (elements of elem_size bytes) or HX_ERR_LENGTH_MISMATCH. Staged through
+ * pinned host memory. */
+hx_status hx_upload(hx_device *dev, void *dst, uint64_t dst_len,
+                    const void *src, uint64_t src_len, uint32_t elem_size);
+/* write_sub_buffer (core device.rs:186-195; host semantics
+ * crates/hephaestus-host/src/lib.rs:151-172). */
+hx_status hx_write_sub(hx_device *dev, void *dst, uint64_t dst_len,
+                       uint64_t offset, const void *src, uint64_t src_len,
+                       uint32_t elem_size);
+/* download (core device.rs:137-144): rejects a length mismatch before any
+ * transfer. */
+hx_status hx_download(hx_device *dev, const void *src, uint64_t src_len,
+                      void *dst, uint64_t dst_len, uint32_t elem_size);
+/* copy_buffer (core device.rs:197-211): device-local, complete on return;
+ * src == dst is a no-op (host lib.rs:174-183). */
+hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len,
+                  void *dst, uint64_t dst_len, uint32_t elem_size);
+
+/* ------------------------------------------------------------- timing */
+
+hx_status hx_event_create(hx_device *dev, hx_event *out);
+hx_status hx_event_destroy(hx_event ev);
+hx_status hx_event_record(hx_device *dev, hx_event ev, hx_stream stream);
+hx_status hx_event_synchronize(hx_event ev);
+hx_status hx_event_elapsed_ms(hx_event start, hx_event stop, float *ms);
+
+/* ------------------------------------------------- host-side planners */
+/* Pure host functions: no device needed; they are what every device entry
+ * point runs first. */
+
+/* validate_reduction_width (core reduction.rs:339-349). */
+hx_status hx_validate_reduction_width(uint32_t width);
+/* reduction_pass_count (core reduction.rs:356-366). */
+uint64_t hx_reduction_pass_count(uint64_t len, uint32_t width);
+/* Layout::checked_size / validate_storage_len / has_zero_stride_aliasing,
+ * as the planners use them (core reduction.rs:449-462). */
+hx_status hx_layout_checked_size(const hx_layout *layout, uint64_t *size);
+hx_status hx_layout_validate_storage_len(const hx_layout *layout,
+                                         uint64_t buf_len);
+int32_t hx_layout_has_zero_stride_aliasing(const hx_layout *layout);
+
+/* plan_axis_reduction (core reduction.rs:410-500).  On success *groups is
+ * the number of outputs (0 = empty no-op) and *axis_len the reduced
+ * extent. */
+hx_status hx_plan_axis_reduction(const hx_layout *in, uint64_t in_buf_len,
+                                 const hx_layout *out, uint64_t out_buf_len,
+                                 uint32_t axis, uint32_t width,
+                                 int32_t buffers_alias, uint64_t *out_len,
+                                 uint64_t *axis_len);
+/* plan_axis_scan (core scan.rs:87-178) generalised to rank 1 and 2:
+ * *lines = number of scan lines (0 = empty no-op), *line_len their
+ * length. */
+hx_status hx_plan_axis_scan(const hx_layout *in, uint64_t in_buf_len,
+                            const hx_layout *out, uint64_t out_buf_len,
+                            uint32_t axis, uint32_t width,
+                            int32_t buffers_alias, uint64_t *lines,
+                            uint64_t *line_len);
+
+/* ----------------------------------------- FullReductionOps (a1-a3, a9) */
+
+/* FullReductionOps::reduce_full_into (core reduction.rs:267-279;
+ * ROCm impl crates/hephaestus-rocm/src/application/
+ * full_reduction_seam.rs:55-120).  `out` must be a 1-element view
+ * (full_reduction_seam.rs:65-73).  op is SUM, PROD, MIN or MAX (MEAN divides
+ * the sum by the element count).  `prologue` (may be NULL) applies
+ * y = fmaf(a,x,b) to f32 inputs first.  Immediate form: uses a
+ * device-owned workspace, so calls on one device must be stream-ordered. */
+hx_status hx_reduce_full(hx_device *dev, hx_op op, hx_dtype dtype,
+                         const void *in, uint64_t in_buf_len,
+                         const hx_layout *in_layout, void *out,
+                         uint64_t out_buf_len, const hx_layout *out_layout,
+                         const hx_affine *prologue, hx_stream stream);
+
+/* Full argmax (north-star; no reference counterpart — SURVEY row a9): index
+ * of the maximum of the (prologue-mapped) view in logical row-major order,
+ * ties to the lowest index, NaN elements ignored.  out_index (u32[1]) gets
+ * the index (UINT32_MAX when there is no non-NaN element); out_value (T[1],
+ * may be NULL) gets the MaxOp result (ops.rs:956-958: identity f32::MIN).
+ * The logical length must be < 2^32. */
+hx_status hx_argmax_full(hx_device *dev, hx_dtype dtype, const void *in,
+                         uint64_t in_buf_len, const hx_layout *in_layout,
+                         void *out_value, uint32_t *out_index,
+                         const hx_affine *prologue, hx_stream stream);
+
+/* FullReductionOps::prepare_reduce_full (core reduction.rs:289-297): binds
+ * the operands and owns the workspace, so hx_plan_dispatch allocates
+ * nothing and re-reads the bound input each time (rebind contract,
+ * conformance full_reduction.rs:173-208). */
+hx_status hx_prepare_reduce_full(hx_device *dev, hx_op op, hx_dtype dtype,
+                                 const void *in, uint64_t in_buf_len,
+                                 const hx_layout *in_layout, void *out,
+                                 uint64_t out_buf_len,
+                                 const hx_layout *out_layout,
+                                 const hx_affine *prologue, hx_plan **plan);
+
+/* ------------------------------------ AxisReductionOps (a5) + fused rows */
+
+/* AxisReductionOps::reduce_axis_into / prod / min / max / mean_axis_into
+ * (core reduction.rs:97-197): rank-2 input, `axis` collapsed to length 1 in
+ * `out`.  MIN/MAX/MEAN reject an empty axis with "{min,max,mean}_axis is
+ * undefined for empty axis {axis}" (rocm axis_reduction.rs:125-136). */
+hx_status hx_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype,
+                         const void *in, uint64_t in_buf_len,
+                         const hx_layout *in_layout, uint32_t axis, void *out,
+                         uint64_t out_buf_len, const hx_layout *out_layout,
+                         hx_stream stream);
+/* AxisReductionOps::prepare_reduce_axis_into (core reduction.rs:206-215). */
+hx_status hx_prepare_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype,
+                                 const void *in, uint64_t in_buf_len,
+                                 const hx_layout *in_layout, uint32_t axis,
+                                 void *out, uint64_t out_buf_len,
+                                 const hx_layout *out_layout, hx_plan **plan);
+
+/* Fused row-wise reduce (north-star config 3): for each of `rows` rows of
+ * `cols` elements (row r starts at in + offset + r*row_stride, unit column
+ * stride), ONE read computes any of
+ *   out_sum[r]    = sum of y          (T; f32 accumulates in f64)
+ *   out_max[r]    = MaxOp fold of y   (T)
+ *   out_argmax[r] = lowest index of the max of y (u32; UINT32_MAX if none)
+ * with y = fmaf(a, x, b) when `prologue` is enabled (f32 only).  Any output
+ * may be NULL.  Replaces separate sum_axis/max_axis launches
+ * (rocm axis_reduction.rs:16-65, one serial thread per row). */
+hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in,
+                         uint64_t in_buf_len, uint64_t rows, uint64_t cols,
+                         uint64_t row_stride, uint64_t offset,
+                         const hx_affine *prologue, void *out_sum,
+                         void *out_max, uint32_t *out_argmax,
+                         uint64_t out_len, hx_stream stream);
+
+/* ------------------------------------------------------- ScanOps (a6, a10) */
+
+/* ScanOps::scan_axis_into (core scan.rs:219-233) over rank-1 or rank-2
+ * views; op is SUM (CumSumOp) or PROD (CumProdOp); kind adds the exclusive
+ * form; direction REVERSE is the suffix scan (accelerator/scan.rs:430-435).
+ * A contiguous line runs the single-pass decoupled look-back scan; f32 sums
+ * carry the inter-tile prefix in f64. */
+hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
+                  hx_scan_direction direction, const void *in,
+                  uint64_t in_buf_len, const hx_layout *in_layout,
+                  uint32_t axis, void *out, uint64_t out_buf_len,
+                  const hx_layout *out_layout, hx_stream stream);
+/* ScanOps::prepare_scan_axis (core scan.rs:242-252). */
+hx_status hx_prepare_scan(hx_device *dev, hx_op op, hx_dtype dtype,
+                          hx_scan_kind kind, hx_scan_direction direction,
+                          const void *in, uint64_t in_buf_len,
+                          const hx_layout *in_layout, uint32_t axis, void *out,
+                          uint64_t out_buf_len, const hx_layout *out_layout,
+                          hx_plan **plan);
+
+/* ------------------------------------------------ segmented reduce (a11) */
+
+/* Segmented sum (north-star config 4; offsets follow the CSR row_ptr
+ * convention of core sparse.rs:179-220: num_offsets = S+1 entries,
+ * offsets[0] = 0, offsets[S] = n, non-decreasing):
+ *   out[s] = sum of values[offsets[s] .. offsets[s+1])   (mod 2^32 for ints)
+ * Offsets live in device memory and are not re-validated on the hot path;
+ * the kernel clamps every offset into [0, n] so malformed offsets cannot
+ * read out of bounds.  hx_validate_segment_offsets checks them. */
+hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype,
+                              const void *values, uint64_t n,
+                              const uint32_t *offsets, uint64_t num_offsets,
+                              void *out, uint64_t out_len, hx_stream stream);
+hx_status hx_prepare_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype,
+                                      const void *values, uint64_t n,
+                                      const uint32_t *offsets,
+                                      uint64_t num_offsets, void *out,
+                                      uint64_t out_len, hx_plan **plan);
+/* Synchronous device check of the row_ptr rules (validate_csr,
+ * core sparse.rs:179-220); HX_ERR_DISPATCH_FAILED names the first rule
+ * broken. */
+hx_status hx_validate_segment_offsets(hx_device *dev, const uint32_t *offsets,
+                                      uint64_t num_offsets, uint64_t n);
+
+/* ---------------------------------------------------------------- plans */
+
+/* dispatch_full / dispatch_prepared / dispatch_scan (core reduction.rs:
+ * 222,304-308; scan.rs:259-263): re-run a prepared plan on `stream`.
+ * Allocates nothing.  Plans must not be dispatched concurrently with
+ * themselves. */
+hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream);
+hx_status hx_plan_destroy(hx_plan *plan);
+/* Bytes of device workspace the plan owns. */
+hx_status hx_plan_workspace_bytes(const hx_plan *plan, uint64_t *bytes);
+
+/* --------------------------------------------------- synthetic inputs */
+
+/* RandomInitOps analog (core random.rs), counter-based so every element is
+ * a pure function of (seed, index): h_i = SplitMix64 output i for `seed`
+ * (state seed + (i+1)*0x9E3779B97F4A7C15, Steele-Lea-Flood 2014 mixer).
+ *   HX_DIST_UNIFORM_INT  : lo + ((h_i >> 32) * (hi-lo+1) >> 32), ints in
+ *                          [p0, p1]
+ *   HX_DIST_UNIFORM_REAL : fmaf(p1-p0, u, p0), u = (h_i >> 40) * 2^-24
+ *   HX_DIST_NORMAL       : Box-Muller in f64 from h_{2i}, h_{2i+1}, mean p0,
+ *                          std p1, rounded to f32. */
+typedef enum hx_distribution {
+    HX_DIST_UNIFORM_INT = 0,
+    HX_DIST_UNIFORM_REAL = 1,
+    HX_DIST_NORMAL = 2
+} hx_distribution;
+hx_status hx_fill_random(hx_device *dev, void *dst, uint64_t n, hx_dtype dtype,
+                         hx_distribution dist, uint64_t seed, double p0,
+                         double p1, hx_stream stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* HX_H */

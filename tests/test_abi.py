@@ -1,0 +1,201 @@
+"""The C-ABI boundary without a GPU: the library loads, exports every entry
+point include/hx.h declares, and its host-side planners reproduce the
+reference planners' results and messages (crates/hephaestus-core/src/
+domain/reduction.rs:339-570, scan.rs:87-344).  CPU only."""
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import hephaestus_amd as hx
+from hephaestus_amd import _ffi
+
+REPO = Path(__file__).resolve().parent.parent
+KATS = json.loads((REPO / "tests" / "golden" / "reference_kats.json").read_text())
+MSG = KATS["messages"]
+
+
+def declared_symbols() -> set[str]:
+    text = (REPO / "include" / "hx.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(hx_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _ffi.LIB_PATH
+    assert lib.exists(), "native library not built"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    declared = declared_symbols()
+    assert len(declared) >= 40
+    assert declared <= exported, sorted(declared - exported)
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert declared_symbols() == set(_ffi.SIGNATURES)
+    hx.load_native()  # every signature resolves
+
+
+def test_library_embeds_gfx950_code_objects_only():
+    blob = _ffi.LIB_PATH.read_bytes()  # the library built in this tree
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+    for other in (b"--gfx942", b"--gfx90a", b"--gfx1100"):
+        assert other not in blob
+
+
+def test_abi_version_and_status_names():
+    lib = hx.load_native()
+    assert lib.hx_abi_version() == 1
+    names = [lib.hx_status_name(i).decode() for i in range(8)]
+    assert names == ["Ok", "AdapterUnavailable", "DeviceUnavailable", "AllocationFailed",
+                     "LengthMismatch", "DispatchFailed", "InvalidConfiguration", "TransferFailed"]
+
+
+def test_device_acquisition_without_gpu_is_adapter_unavailable():
+    if hx.RocmDevice.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(hx.AdapterUnavailable) as err:
+        hx.RocmDevice.try_default()
+    assert "ROCm device ordinal 0 unavailable; device count 0" in str(err.value)
+
+
+# ------------------------------------------------------------------ planners
+def test_reduction_pass_count_matches_reference_table():
+    for n, want in KATS["planner"]["pass_count_w256"]:
+        assert hx.reduction_pass_count(n, 256) == want
+    for n, want in KATS["planner"]["pass_count_w128"]:
+        assert hx.reduction_pass_count(n, 128) == want
+
+
+def test_reduction_width_must_be_power_of_two():
+    hx.validate_reduction_width(128)
+    with pytest.raises(hx.DispatchFailed) as err:
+        hx.validate_reduction_width(192)
+    assert err.value.message == MSG["width_192"]
+
+
+L = hx.Layout.c_contiguous
+
+
+def test_plan_axis_reduction_dense_and_empty():
+    # reduction.rs:510-521 and :539-545
+    assert hx.plan_axis_reduction(L([3, 4]), 12, L([3, 1]), 3, 1) == (3, 4)
+    assert hx.plan_axis_reduction(L([0, 4]), 0, L([0, 1]), 0, 1) == (0, 4)
+
+
+def test_plan_axis_reduction_rejections():
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([3, 4]), 12, L([3, 4]), 12, 1)
+    assert e.value.message.startswith(MSG["axis_shape_prefix"])
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([2, 2]), 4, L([1, 2]), 2, 0, buffers_alias=True)
+    assert e.value.message == MSG["axis_alias"]
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([2, 2]), 4, L([1, 2]), 2, 2)
+    assert e.value.message == "axis 2 is out of bounds for rank-2 reduction"
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([3, 4]), 12, L([3, 1]), 3, 1, width=192)
+    assert e.value.message == MSG["width_192"]
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([2, 2]), 4, hx.Layout.try_new([1, 2], [0, 0]), 2, 0)
+    assert "zero-stride aliasing" in e.value.message
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_reduction(L([3, 4]), 11, L([3, 1]), 3, 1)
+    assert e.value.message.startswith("layout rejected:")
+
+
+def test_plan_axis_scan_matches_reference_planner_tests():
+    # scan.rs:278-343
+    assert hx.plan_axis_scan(L([3, 4]), 12, L([3, 4]), 12, 1) == (3, 4)
+    assert hx.plan_axis_scan(L([2, 5]), 10, L([2, 5]), 10, 0) == (5, 2)
+    assert hx.plan_axis_scan(L([0, 4]), 0, L([0, 4]), 0, 1)[0] == 0
+    assert hx.plan_axis_scan(L([3, 1024]), 3072, L([3, 1024]), 3072, 1) == (3, 1024)
+    assert hx.plan_axis_scan(L([100]), 100, L([100]), 100, 0) == (1, 100)
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_scan(L([2, 2]), 4, L([2, 2]), 4, 0, buffers_alias=True)
+    assert e.value.message == MSG["scan_alias"]
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_scan(L([2, 2]), 4, L([2, 2]), 4, 0, width=3)
+    assert e.value.message == "scan block width 3 must be a power of two"
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_scan(L([2, 4]), 8, L([4, 2]), 8, 1)
+    assert e.value.message.startswith(MSG["scan_shape_prefix"])
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_scan(L([3, 4]), 12, L([3, 4]), 12, 2)
+    assert e.value.message == "scan axis 2 is out of bounds for rank-2 scan"
+    with pytest.raises(hx.DispatchFailed) as e:
+        hx.plan_axis_scan(L([2, 2, 2]), 8, L([2, 2, 2]), 8, 0)
+    assert "rank 1 and 2 only" in e.value.message
+
+
+def test_layout_queries():
+    assert L([3, 4]).checked_size() == 12
+    assert L([0, 4]).checked_size() == 0
+    t = hx.Layout.try_new([4, 3], [1, 4], 0)
+    t.validate_storage_len(12)
+    with pytest.raises(hx.DispatchFailed):
+        t.validate_storage_len(11)
+    d = hx.Layout.try_new([3], [4], 0)  # the diagonal view of a 3x3
+    d.validate_storage_len(9)
+    neg = hx.Layout.try_new([3], [-1], 2)
+    neg.validate_storage_len(3)
+    with pytest.raises(hx.DispatchFailed):
+        hx.Layout.try_new([3], [-1], 1).validate_storage_len(3)
+    assert hx.Layout.try_new([2, 2], [0, 1]).has_zero_stride_aliasing()
+    assert not hx.Layout.try_new([1, 2], [0, 1]).has_zero_stride_aliasing()
+    with pytest.raises(hx.DispatchFailed):
+        hx.Layout.try_new([2**40, 2**40], [1, 1]).checked_size()
+
+
+def test_length_mismatch_carries_both_lengths():
+    err = hx.LengthMismatch(3, 4)
+    assert (err.host_len, err.device_len) == (3, 4)
+    assert str(err) == "host length 3 does not match device buffer length 4"
+    assert issubclass(hx.DispatchFailed, hx.HephaestusError)
+
+
+def test_null_device_handles_are_rejected_on_the_host():
+    lib = hx.load_native()
+    st = lib.hx_synchronize(None)
+    assert st == _ffi.INVALID_CONFIGURATION
+    assert _ffi.last_message() == "null device handle"
+    out = ctypes.c_void_p()
+    assert lib.hx_alloc(None, 16, 1, ctypes.byref(out)) == _ffi.INVALID_CONFIGURATION
+
+
+def test_entry_points_validate_before_touching_the_device():
+    """Every device entry point rejects a bad operand before it needs the
+    device, so these run without a GPU (and leave outputs untouched)."""
+    lib = hx.load_native()
+    lay = _ffi.layout_struct(L([3, 4]))
+    out2 = _ffi.layout_struct(L([2]))
+    st = lib.hx_reduce_full(None, _ffi.OP_SUM, _ffi.DTYPE_F32, 0x1000, 12, ctypes.byref(lay),
+                            0x2000, 2, ctypes.byref(out2), None, None)
+    assert st == _ffi.DISPATCH_FAILED and _ffi.last_message() == MSG["full_multi_output"]
+    scan_lay = _ffi.layout_struct(L([3, 4]))
+    st = lib.hx_scan(None, _ffi.OP_SUM, _ffi.DTYPE_F32, 0, 0, 0x1000, 12, ctypes.byref(scan_lay), 2,
+                     0x2000, 12, ctypes.byref(scan_lay), None)
+    assert st == _ffi.DISPATCH_FAILED
+    assert _ffi.last_message() == "scan axis 2 is out of bounds for rank-2 scan"
+    st = lib.hx_scan(None, _ffi.OP_MAX, _ffi.DTYPE_F32, 0, 0, 0x1000, 12, ctypes.byref(scan_lay), 1,
+                     0x2000, 12, ctypes.byref(scan_lay), None)
+    assert st == _ffi.DISPATCH_FAILED and "CumSumOp" in _ffi.last_message()
+    empty = _ffi.layout_struct(hx.Layout.c_contiguous([3, 0]))
+    out31 = _ffi.layout_struct(hx.Layout.c_contiguous([3, 1]))
+    st = lib.hx_reduce_axis(None, _ffi.OP_MEAN, _ffi.DTYPE_U32, None, 0, ctypes.byref(empty), 1,
+                            0x2000, 3, ctypes.byref(out31), None)
+    assert st == _ffi.DISPATCH_FAILED and _ffi.last_message() == MSG["mean_empty_axis1"]
+    st = lib.hx_reduce_axis(None, _ffi.OP_SUM, _ffi.DTYPE_U32, 0x1000, 12, ctypes.byref(lay), 1,
+                            0x1000, 3, ctypes.byref(out31), None)
+    assert st == _ffi.DISPATCH_FAILED and _ffi.last_message() == MSG["axis_alias"]
+    st = lib.hx_segmented_reduce(None, _ffi.OP_SUM, _ffi.DTYPE_I32, 0x1000, 10, 0x2000, 4, 0x3000, 2, None)
+    assert st == _ffi.LENGTH_MISMATCH
+    aff = _ffi.HxAffine(0.5, 0.25, 1, 0)
+    st = lib.hx_reduce_full(None, _ffi.OP_SUM, _ffi.DTYPE_U32, 0x1000, 12, ctypes.byref(lay),
+                            0x2000, 1, ctypes.byref(_ffi.layout_struct(L([1]))), ctypes.byref(aff), None)
+    assert st == _ffi.INVALID_CONFIGURATION and "f32" in _ffi.last_message()

@@ -1,0 +1,433 @@
+"""Parity of every kernel family with the CPU oracle on the same seeded
+inputs, at sizes the oracle checks in seconds: ragged lengths around the
+tile and vector boundaries, misaligned views, every dtype, the prologue,
+special values and empty operands.  Integer results must be bit-exact; f32
+sums and scans must satisfy |err| <= 2*ceil(log2 n)*eps_f32*sum|y| against
+the oracle's f64 accumulation."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import hephaestus_amd as hx
+from hephaestus_amd import Layout, StridedView
+
+pytestmark = pytest.mark.gpu
+
+FULL = hx.RocmFullReductionOps()
+AXIS = hx.RocmAxisReductionOps()
+SCAN = hx.RocmScanOps()
+SEG = hx.RocmSegmentedReductionOps()
+EPS = 2.0**-23
+SIZES = [1, 2, 3, 4, 5, 63, 64, 65, 255, 256, 257, 1023, 1024, 1025, 4095, 4096, 4097,
+         8191, 8192, 8193, 12345, 65536 + 17, 1 << 20, (1 << 20) + 3]
+
+
+def f32_bound(n, abs_sum):
+    """North-star bound 2*ceil(log2 n)*eps_f32*sum|y| (0 for n <= 1: exact)."""
+    return 2 * (int(n) - 1).bit_length() * EPS * abs_sum
+
+
+def inputs(oracle, dtype, n, seed):
+    if dtype == np.float32:
+        return oracle.uniform_real(n, seed, -1.0, 1.0)
+    if dtype == np.int32:
+        return oracle.uniform_int(n, seed, -1000, 1000, dtype=np.int32)
+    return oracle.uniform_int(n, seed, 0, 2**32 - 1)
+
+
+def full(device, op, host, layout=None, prologue=None):
+    buf = device.upload(host)
+    out = device.alloc_zeroed(host.dtype, 1)
+    lay = layout or Layout.c_contiguous([host.size])
+    FULL.reduce_full_into(device, op, StridedView(buf, lay), StridedView(out, Layout.c_contiguous([1])),
+                          prologue=prologue)
+    return device.download_owned(out)[0]
+
+
+# ------------------------------------------------------------ generator
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_device_generator_matches_oracle_bits(device, oracle, n):
+    u = device.alloc_uninitialized(np.uint32, n)
+    device.fill_uniform_int(u, seed=42, lo=0, hi=255)
+    assert np.array_equal(device.download_owned(u), oracle.uniform_int(n, 42, 0, 255))
+    i = device.alloc_uninitialized(np.int32, n)
+    device.fill_uniform_int(i, seed=7, lo=-1000, hi=1000)
+    assert np.array_equal(device.download_owned(i), oracle.uniform_int(n, 7, -1000, 1000, dtype=np.int32))
+    f = device.alloc_uninitialized(np.float32, n)
+    device.fill_uniform_real(f, seed=1, lo=-1.0, hi=1.0)
+    assert np.array_equal(device.download_owned(f).view(np.uint32),
+                          oracle.uniform_real(n, 1, -1.0, 1.0).view(np.uint32))
+
+
+def test_device_normal_generator_is_close_to_oracle(device, oracle):
+    n = 1 << 16
+    f = device.alloc_uninitialized(np.float32, n)
+    device.fill_normal(f, seed=3)
+    got = device.download_owned(f)
+    want = oracle.normal(n, 3)
+    # device and host libm may differ in the last f64 ulp of log/cos/sqrt
+    assert np.max(np.abs(got - want)) <= 4e-7 * np.max(np.abs(want))
+
+
+# ------------------------------------------------------------ full reduce
+@pytest.mark.parametrize("n", SIZES)
+def test_full_sum_f32_within_bound(device, oracle, n):
+    x = inputs(oracle, np.float32, n, seed=n)
+    ref, ab = oracle.full_sum(x)
+    got = float(full(device, hx.SumOp, x))
+    assert abs(got - ref) <= f32_bound(n, ab), (n, got, ref)
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.int32])
+@pytest.mark.parametrize("n", SIZES)
+def test_full_integer_reductions_bit_exact(device, oracle, dtype, n):
+    x = inputs(oracle, dtype, n, seed=n + 1)
+    assert full(device, hx.SumOp, x) == oracle.full_sum(x)
+    assert full(device, hx.ProdOp, x) == oracle.full_prod(x)
+    assert full(device, hx.MaxOp, x) == oracle.full_max(x)
+    assert full(device, hx.MinOp, x) == oracle.full_min(x)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4097, 1 << 20])
+def test_full_max_min_f32_bit_exact(device, oracle, n):
+    x = oracle.normal(n, seed=n)
+    assert full(device, hx.MaxOp, x).view(np.uint32) == oracle.full_max(x).view(np.uint32)
+    assert full(device, hx.MinOp, x).view(np.uint32) == oracle.full_min(x).view(np.uint32)
+
+
+@pytest.mark.parametrize("offset", [0, 1, 2, 3, 5])
+def test_full_reduce_misaligned_views(device, oracle, offset):
+    n = 100003
+    host = inputs(oracle, np.uint32, n + offset + 7, seed=9)
+    buf = device.upload(host)
+    out = device.alloc_zeroed(np.uint32, 1)
+    lay = Layout.try_new([n], [1], offset)
+    FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, lay), StridedView(out, Layout.c_contiguous([1])))
+    assert device.download_owned(out)[0] == oracle.full_sum(host[offset:offset + n])
+
+
+def test_full_reduce_strided_views(device, oracle):
+    host = inputs(oracle, np.int32, 3000, seed=4)
+    for shape, strides, offset in (([10, 30], [1, 100], 5), ([1000], [3], 0), ([50, 20], [20, 1], 0),
+                                   ([7, 11], [-11, 1], 66), ([2, 3, 4, 5], [60, 20, 5, 1], 0)):
+        lay = Layout.try_new(shape, strides, offset)
+        idx = offset + sum(np.indices(shape)[d] * strides[d] for d in range(len(shape)))
+        sel = host[idx.ravel()]
+        buf = device.upload(host)
+        out = device.alloc_zeroed(np.int32, 1)
+        FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, lay), StridedView(out, Layout.c_contiguous([1])))
+        assert device.download_owned(out)[0] == oracle.full_sum(np.ascontiguousarray(sel))
+        FULL.reduce_full_into(device, hx.MaxOp, StridedView(buf, lay), StridedView(out, Layout.c_contiguous([1])))
+        assert device.download_owned(out)[0] == oracle.full_max(np.ascontiguousarray(sel))
+
+
+def test_full_reduce_output_offset(device):
+    buf = device.upload(np.arange(10, dtype=np.uint32))
+    out = device.upload(np.full(4, 99, np.uint32))
+    FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, Layout.c_contiguous([10])),
+                          StridedView(out, Layout.try_new([1], [1], 2)))
+    assert list(device.download_owned(out)) == [99, 99, 45, 99]
+
+
+def test_full_sum_with_prologue(device, oracle):
+    x = oracle.uniform_real((1 << 20) + 5, seed=2, lo=-1.0, hi=1.0)
+    ref, ab = oracle.full_sum(x, prologue=(0.5, 0.25))
+    got = float(full(device, hx.SumOp, x, prologue=(0.5, 0.25)))
+    assert abs(got - ref) <= f32_bound(x.size, ab)
+    assert full(device, hx.MaxOp, x, prologue=(0.5, 0.25)) == oracle.full_max(x, prologue=(0.5, 0.25))
+
+
+def test_full_special_values(device):
+    nan, inf = np.float32("nan"), np.float32("inf")
+    assert full(device, hx.MaxOp, np.array([nan, 1.0, nan, -2.0], np.float32)) == 1.0
+    assert full(device, hx.MaxOp, np.array([nan, nan], np.float32)) == np.float32(-3.4028235e38)
+    assert full(device, hx.MaxOp, np.array([-inf, -inf], np.float32)) == np.float32(-3.4028235e38)
+    assert full(device, hx.MinOp, np.array([inf], np.float32)) == np.float32(3.4028235e38)
+    z = np.array([-0.0, 0.0, -0.0], np.float32)
+    assert full(device, hx.MaxOp, z).view(np.uint32) == 0
+    assert full(device, hx.MinOp, z).view(np.uint32) == 0x80000000
+    assert full(device, hx.MaxOp, np.zeros(0, np.int32)) == np.iinfo(np.int32).min
+    assert full(device, hx.ProdOp, np.zeros(0, np.uint32)) == 1
+    assert full(device, hx.MinOp, np.zeros(0, np.uint32)) == 0xFFFFFFFF
+
+
+# ------------------------------------------------------------ argmax
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("n", [1, 2, 65, 4097, 1 << 20])
+def test_full_argmax_matches_oracle(device, oracle, dtype, n):
+    x = inputs(oracle, dtype, n, seed=n + 3)
+    if dtype != np.float32:
+        x = (x % 97).astype(dtype)  # many ties: lowest index must win
+    buf = device.upload(x)
+    idx = device.alloc_zeroed(np.uint32, 1)
+    val = device.alloc_zeroed(dtype, 1)
+    FULL.argmax_full_into(device, StridedView(buf, Layout.c_contiguous([n])), idx, val)
+    want = oracle.full_argmax(x)
+    assert int(device.download_owned(idx)[0]) == want
+    assert device.download_owned(val)[0] == x[want]
+
+
+def test_argmax_special_cases(device):
+    def am(host, prologue=None):
+        buf = device.upload(host)
+        idx = device.alloc_zeroed(np.uint32, 1)
+        FULL.argmax_full_into(device, StridedView(buf, Layout.c_contiguous([host.size])), idx, prologue=prologue)
+        return int(device.download_owned(idx)[0])
+
+    nan = np.float32("nan")
+    assert am(np.array([nan, 1.0, 5.0, 5.0], np.float32)) == 2
+    assert am(np.array([nan, nan], np.float32)) == 0xFFFFFFFF
+    assert am(np.array([-0.0, 0.0], np.float32)) == 1
+    assert am(np.zeros(0, np.float32)) == 0xFFFFFFFF
+    assert am(np.array([3.0, -1.0], np.float32), prologue=(-1.0, 0.0)) == 1
+
+
+# ------------------------------------------------------------ rows
+@pytest.mark.parametrize("rows,cols,ld,offset", [
+    (1, 1, 1, 0), (3, 4, 4, 0), (7, 63, 63, 0), (5, 64, 68, 4), (33, 4096, 4096, 0),
+    (17, 4099, 4103, 1), (256, 1000, 1000, 0), (1000, 257, 260, 8), (2, 70000, 70000, 0)])
+def test_rows_fused_f32(device, oracle, rows, cols, ld, offset):
+    host = oracle.normal(offset + (rows - 1) * ld + cols + 3, seed=rows * cols)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, cols, ld, prologue=(0.5, 0.25))
+    buf = device.upload(host)
+    s = device.alloc_zeroed(np.float32, rows)
+    m = device.alloc_zeroed(np.float32, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    AXIS.reduce_rows_fused(device, buf, rows, cols, ld, offset, (0.5, 0.25), s, m, i)
+    gs, gm, gi = device.download_owned(s), device.download_owned(m), device.download_owned(i)
+    assert np.array_equal(gi, i_ref)
+    assert np.array_equal(gm.view(np.uint32), m_ref.view(np.uint32))
+    bound = np.array([f32_bound(cols, a) for a in a_ref])
+    assert np.all(np.abs(gs.astype(np.float64) - s_ref) <= bound)
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.int32])
+def test_rows_fused_integers(device, oracle, dtype):
+    rows, cols = 300, 777
+    host = (inputs(oracle, dtype, rows * cols, seed=5) % 50).astype(dtype)
+    s_ref, _, m_ref, i_ref = oracle.rows(host, rows, cols)
+    buf = device.upload(host)
+    s = device.alloc_zeroed(dtype, rows)
+    m = device.alloc_zeroed(dtype, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    AXIS.reduce_rows_fused(device, buf, rows, cols, out_sum=s, out_max=m, out_argmax=i)
+    assert np.array_equal(device.download_owned(s), s_ref)
+    assert np.array_equal(device.download_owned(m), m_ref)
+    assert np.array_equal(device.download_owned(i), i_ref)
+
+
+@pytest.mark.parametrize("subset", ["sum", "max", "argmax", "sum+argmax", "max+argmax"])
+def test_rows_output_subsets(device, oracle, subset):
+    rows, cols = 40, 300
+    host = oracle.normal(rows * cols, seed=8)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host, rows, cols)
+    buf = device.upload(host)
+    want = subset.split("+")
+    s = device.upload(np.full(rows, 7.0, np.float32)) if "sum" in want else None
+    m = device.upload(np.full(rows, 7.0, np.float32)) if "max" in want else None
+    i = device.upload(np.full(rows, 7, np.uint32)) if "argmax" in want else None
+    AXIS.reduce_rows_fused(device, buf, rows, cols, out_sum=s, out_max=m, out_argmax=i)
+    if s is not None:
+        assert np.all(np.abs(device.download_owned(s) - s_ref) <= [f32_bound(cols, a) for a in a_ref])
+    if m is not None:
+        assert np.array_equal(device.download_owned(m), m_ref)
+    if i is not None:
+        assert np.array_equal(device.download_owned(i), i_ref)
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("op", ["sum", "max", "min", "prod", "argmax"])
+def test_axis_reduce_matches_oracle(device, oracle, axis, op):
+    r, c = 123, 517
+    host = (oracle.uniform_int(r * c, seed=11, lo=0, hi=9)).astype(np.uint32)
+    mat = host.reshape(r, c)
+    lines = mat if axis == 1 else np.ascontiguousarray(mat.T)
+    if op == "sum":
+        want = np.array([oracle.full_sum(l) for l in lines], np.uint32)
+    elif op == "max":
+        want = np.array([oracle.full_max(l) for l in lines], np.uint32)
+    elif op == "min":
+        want = np.array([oracle.full_min(l) for l in lines], np.uint32)
+    elif op == "prod":
+        want = np.array([oracle.full_prod(l) for l in lines], np.uint32)
+    else:
+        want = np.array([oracle.full_argmax(l) for l in lines], np.uint32)
+    opcls = {"sum": hx.SumOp, "max": hx.MaxOp, "min": hx.MinOp, "prod": hx.ProdOp, "argmax": hx.ArgMaxOp}[op]
+    buf = device.upload(host)
+    out_shape = [r, 1] if axis == 1 else [1, c]
+    out = device.alloc_zeroed(np.uint32, want.size)
+    AXIS.reduce_axis_into(device, opcls, StridedView(buf, Layout.c_contiguous([r, c])), axis,
+                          StridedView(out, Layout.c_contiguous(out_shape)))
+    assert np.array_equal(device.download_owned(out), want)
+
+
+# ------------------------------------------------------------ scans
+@pytest.mark.parametrize("exclusive", [False, True])
+@pytest.mark.parametrize("n", SIZES)
+def test_scan_u32_bit_exact(device, oracle, n, exclusive):
+    x = inputs(oracle, np.uint32, n, seed=n + 5)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, n)
+    kind = hx.ScanKind.Exclusive if exclusive else hx.ScanKind.Inclusive
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.c_contiguous([n])), 0,
+                        hx.ScanDirection.Forward, StridedView(out, Layout.c_contiguous([n])), kind)
+    assert np.array_equal(device.download_owned(out), oracle.scan_sum(x, exclusive=exclusive))
+
+
+@pytest.mark.parametrize("exclusive", [False, True])
+@pytest.mark.parametrize("n", [1, 2, 5, 4096, 4097, 65536 + 17, (1 << 20) + 3])
+def test_scan_f32_within_bound(device, oracle, n, exclusive):
+    x = oracle.uniform_real(n, seed=n, lo=0.0, hi=1.0)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.float32, n)
+    kind = hx.ScanKind.Exclusive if exclusive else hx.ScanKind.Inclusive
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.c_contiguous([n])), 0,
+                        hx.ScanDirection.Forward, StridedView(out, Layout.c_contiguous([n])), kind)
+    ref, ab = oracle.scan_sum(x, exclusive=exclusive)
+    bad, worst = oracle.check_f32_bound(device.download_owned(out), ref, ab, n)
+    assert bad == 0, worst
+
+
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+@pytest.mark.parametrize("op", ["sum", "prod"])
+def test_scan_directions_kinds_and_ops(device, oracle, kind, direction, op):
+    n = 50001
+    x = (oracle.uniform_int(n, seed=12, lo=0, hi=2**32 - 1) | 1).astype(np.uint32)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, n)
+    opcls = hx.CumSumOp if op == "sum" else hx.CumProdOp
+    SCAN.scan_axis_into(device, opcls, StridedView(buf, Layout.c_contiguous([n])), 0, direction,
+                        StridedView(out, Layout.c_contiguous([n])), kind)
+    fn = oracle.scan_sum if op == "sum" else oracle.scan_prod
+    want = fn(x, exclusive=kind == hx.ScanKind.Exclusive, reverse=direction == hx.ScanDirection.Reverse)
+    assert np.array_equal(device.download_owned(out), want)
+
+
+@pytest.mark.parametrize("shape,axis", [((512, 4096), 1), ((3, 10000), 1), ((4096, 300), 0), ((40, 7), 0),
+                                        ((1000, 1001), 1), ((257, 5), 1)])
+def test_scan_rank2_lines(device, oracle, shape, axis):
+    r, c = shape
+    host = oracle.uniform_int(r * c, seed=r + c, lo=-1000, hi=1000, dtype=np.int32)
+    mat = host.reshape(r, c)
+    buf = device.upload(host)
+    out = device.alloc_zeroed(np.int32, r * c)
+    lay = Layout.c_contiguous([r, c])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), axis, hx.ScanDirection.Forward,
+                        StridedView(out, lay))
+    want = np.cumsum(mat, axis=axis, dtype=np.int32)
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+
+
+def test_scan_strided_rank1_views(device, oracle):
+    n = 20000
+    host = oracle.uniform_int(3 * n + 10, seed=13, lo=0, hi=100)
+    buf = device.upload(host)
+    out = device.alloc_zeroed(np.uint32, 2 * n + 1)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.try_new([n], [3], 1)), 0,
+                        hx.ScanDirection.Forward, StridedView(out, Layout.try_new([n], [2], 1)))
+    got = device.download_owned(out)
+    assert np.array_equal(got[1::2][:n], oracle.scan_sum(np.ascontiguousarray(host[1:3 * n:3])))
+    assert np.all(got[0::2] == 0)  # untouched gaps
+
+
+def test_scan_repeated_launches_reuse_workspace(device, oracle):
+    """The look-back status words are tagged per launch: many launches in a
+    row, switching sizes and dtypes, must each be exact."""
+    for rep in range(6):
+        n = [5000000, 4097, 1 << 20, 123457, 5000000, 7][rep]
+        x = oracle.uniform_int(n, seed=rep, lo=0, hi=255)
+        buf = device.upload(x)
+        out = device.alloc_zeroed(np.uint32, n)
+        SCAN.exclusive_scan_into(device, buf, out)
+        assert np.array_equal(device.download_owned(out), oracle.scan_sum(x, exclusive=True)), rep
+        xf = oracle.uniform_real(n, seed=rep, lo=0.0, hi=1.0)
+        fb = device.upload(xf)
+        fo = device.alloc_zeroed(np.float32, n)
+        SCAN.inclusive_scan_into(device, fb, fo)
+        bad, _ = oracle.check_scan_f32(xf, device.download_owned(fo))
+        assert bad == 0, rep
+
+
+# ------------------------------------------------------------ segmented
+def _segmented(device, values, offsets):
+    vb = device.upload(values)
+    ob = device.upload(offsets.astype(np.uint32))
+    out = device.upload(np.full(offsets.size - 1, 0x5A5A5A5A, np.uint32).view(values.dtype))
+    SEG.segmented_sum_into(device, vb, ob, out)
+    return device.download_owned(out)
+
+
+def test_segmented_sum_edge_offsets(device, oracle):
+    x = oracle.uniform_int(20000, seed=14, lo=-1000, hi=1000, dtype=np.int32)
+    cases = [
+        [0, 20000],
+        [0, 0, 0, 20000, 20000],
+        [0, 1, 2, 3, 4096, 4096, 4097, 8191, 8192, 8193, 20000],
+        list(range(0, 20001, 1)),  # every element its own segment
+        [0] + list(range(4096, 20000, 4096)) + [20000],  # boundaries on tile edges
+        [0, 3, 3, 3, 19999, 20000],
+    ]
+    for off in cases:
+        off = np.array(off, np.uint32)
+        assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
+
+
+@pytest.mark.parametrize("n,mean", [(1, 300.0), (4096, 300.0), (1 << 20, 300.0), ((1 << 20) + 9, 3.0),
+                                    (1 << 20, 50000.0)])
+def test_segmented_sum_geometric(device, oracle, n, mean):
+    x = oracle.uniform_int(n, seed=n, lo=-1000, hi=1000, dtype=np.int32)
+    off = oracle.geometric_offsets(n, mean, seed=n + 1)
+    assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
+
+
+def test_segmented_sum_empty_values(device):
+    vb = device.alloc_zeroed(np.int32, 16)  # aligned allocation, but n = 0 values
+    ob = device.upload(np.zeros(4, np.uint32))
+    out = device.upload(np.full(3, 9, np.int32))
+    from hephaestus_amd import _ffi
+    _ffi.check(_ffi.lib().hx_segmented_reduce(device.handle, _ffi.OP_SUM, _ffi.DTYPE_I32, vb.ptr, 0,
+                                              ob.ptr, 4, out.ptr, 3, None))
+    assert list(device.download_owned(out)) == [0, 0, 0]
+
+
+def test_segment_offsets_validation(device):
+    ob = device.upload(np.array([0, 5, 3, 10], np.uint32))
+    with pytest.raises(hx.DispatchFailed) as e:
+        SEG.validate_offsets(device, ob, 10)
+    assert e.value.message == "invalid segment offsets: offsets must be non-decreasing"
+    ob = device.upload(np.array([0, 5, 9], np.uint32))
+    with pytest.raises(hx.DispatchFailed) as e:
+        SEG.validate_offsets(device, ob, 10)
+    assert "start at 0 and end at the element count" in e.value.message
+    SEG.validate_offsets(device, device.upload(np.array([0, 5, 10], np.uint32)), 10)
+
+
+def test_segmented_malformed_offsets_stay_in_bounds(device, oracle):
+    """Offsets beyond n are clamped; the call completes and never faults."""
+    x = oracle.uniform_int(10000, seed=15, lo=0, hi=10)
+    off = np.array([0, 5000, 20000, 30000], np.uint32)
+    got = _segmented(device, x, off)
+    assert got[0] == oracle.full_sum(x[:5000])
+    assert got[1] == oracle.full_sum(x[5000:])
+    assert got[2] == 0
+
+
+# ------------------------------------------------------------ prepared plans
+def test_prepared_plans_allocate_once_and_rebind(device, oracle):
+    n = 1 << 20
+    x = oracle.uniform_int(n, seed=16, lo=0, hi=255)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, n)
+    lay = Layout.c_contiguous([n])
+    plan = SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(buf, lay), 0, hx.ScanDirection.Forward,
+                                  StridedView(out, lay), hx.ScanKind.Exclusive)
+    assert plan.workspace_bytes() > 0
+    for _ in range(3):
+        plan.dispatch()
+    assert np.array_equal(device.download_owned(out), oracle.scan_sum(x, exclusive=True))
+    y = oracle.uniform_int(n, seed=17, lo=0, hi=255)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), oracle.scan_sum(y, exclusive=True))

@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/hx_oracle.c) before it is trusted as the
+parity checker: against the reference's own known-answer vectors
+(tests/golden/reference_kats.json), closed forms, library routines (numpy,
+math.fsum, fractions) and hand-built special cases.  CPU only."""
+from __future__ import annotations
+
+import json
+import math
+import struct
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+F32_MIN = np.float32(-3.4028235e38)
+F32_MAX = np.float32(3.4028235e38)
+
+
+def bits(x) -> int:
+    return struct.unpack("<I", struct.pack("<f", float(x)))[0]
+
+
+# ---------------------------------------------------------------- generator
+def test_splitmix64_matches_published_stream(oracle):
+    k = KATS["splitmix64"]
+    got = [oracle.splitmix64_at(k["seed"], i) for i in range(5)]
+    assert got == [int(v) for v in k["outputs"]]
+
+
+def test_splitmix64_python_restatement_agrees(oracle):
+    mask = (1 << 64) - 1
+
+    def sm(seed, i):
+        z = (seed + (i + 1) * 0x9E3779B97F4A7C15) & mask
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        return z ^ (z >> 31)
+
+    for seed in (0, 1, 42, 2**63 + 5):
+        for i in (0, 1, 2, 1000, 2**40):
+            assert oracle.splitmix64_at(seed, i) == sm(seed, i)
+
+
+def test_uniform_int_range_and_formula(oracle):
+    x = oracle.uniform_int(1 << 16, seed=7, lo=0, hi=255)
+    assert x.min() == 0 and x.max() == 255
+    h = np.array([oracle.splitmix64_at(7, i) for i in range(64)], dtype=np.uint64)
+    assert np.array_equal(x[:64], (h >> np.uint64(56)).astype(np.uint32))
+    y = oracle.uniform_int(1 << 16, seed=3, lo=-1000, hi=1000, dtype=np.int32)
+    assert y.min() == -1000 and y.max() == 1000
+    assert abs(float(y.mean())) < 10
+
+
+def test_uniform_real_is_exact_grid(oracle):
+    x = oracle.uniform_real(1 << 16, seed=1, lo=-1.0, hi=1.0)
+    assert x.min() >= -1.0 and x.max() < 1.0
+    # every value is k * 2^-23 for an integer k (2u - 1 is exact in f32)
+    k = x.astype(np.float64) * 2.0**23
+    assert np.array_equal(k, np.round(k))
+    h = oracle.splitmix64_at(1, 5)
+    assert x[5] == np.float32((h >> 40) * 2.0**-24 * 2.0 - 1.0)
+
+
+def test_normal_moments(oracle):
+    z = oracle.normal(1 << 18, seed=11)
+    assert abs(float(z.mean())) < 0.01
+    assert abs(float(z.std()) - 1.0) < 0.01
+
+
+# ------------------------------------------------------ reference fixtures
+def test_full_reduction_kats(oracle):
+    k = KATS["full_reduction"]
+    xf = np.array(k["input"], dtype=np.float32)
+    xu = np.array(k["input"], dtype=np.uint32)
+    s, a = oracle.full_sum(xf)
+    assert s == k["sum"] and a == k["sum"]
+    assert oracle.full_sum(xu) == k["sum"]
+    assert oracle.full_prod(xu) == k["prod"]
+    assert oracle.full_min(xf) == k["min"] and oracle.full_max(xf) == k["max"]
+    diag = np.array(k["diagonal"]["input"], dtype=np.float32)[::4]
+    assert oracle.full_sum(diag)[0] == k["diagonal"]["sum"]
+    assert oracle.full_prod(np.full(12, 2, np.uint32)) == k["rebind_all_twos_prod"]["value"]
+
+
+def test_axis_reduction_kats(oracle):
+    k = KATS["axis_reduction"]
+    x = np.array(k["input"], dtype=np.float32).reshape(3, 4)
+    s1, _, m1, _ = oracle.rows(x.ravel(), 3, 4)
+    assert list(s1) == [10, 26, 42] and list(m1) == k["max_axis1"]
+    xt = np.ascontiguousarray(x.T)
+    s0, _, m0, _ = oracle.rows(xt.ravel(), 4, 3)
+    assert list(s0) == k["sum_axis0"] and list(m0) == k["max_axis0"]
+    assert list(s0 / 3) == k["mean_axis0"] and list(s1 / 4) == k["mean_axis1"]
+    assert [oracle.full_min(r) for r in x] == k["min_axis1"]
+    assert [oracle.full_min(c) for c in xt] == k["min_axis0"]
+    xu = np.array(k["input"], dtype=np.uint32).reshape(3, 4)
+    assert [int(oracle.full_prod(c)) for c in xu.T.copy()] == k["prod_axis0"]
+    assert [int(oracle.full_prod(r)) for r in xu] == k["prod_axis1"]
+
+
+def test_rocm_axis_u32_kats(oracle):
+    k = KATS["rocm_axis_u32"]
+    x = np.array(k["input"], dtype=np.uint32).reshape(3, 4)
+    s, _, m, _ = oracle.rows(x.ravel(), 3, 4)
+    assert list(s) == k["sum_rows"] and list(m) == k["max_rows"]
+    sc, _, _, _ = oracle.rows(x.T.copy().ravel(), 4, 3)
+    assert list(sc) == k["sum_cols"]
+    assert [int(oracle.full_min(r)) for r in x] == k["min_rows"]
+    assert [int(oracle.full_prod(r)) for r in x] == k["prod_rows"]
+    assert [int(oracle.full_prod(c)) for c in x.T.copy()] == k["prod_cols"]
+    # The reference asserts 17_600 for column 3; 4 * 40 * 11 is 1760.
+    assert 4 * 40 * 11 == k["prod_cols"][3] != k["prod_cols_as_asserted_by_reference"][3]
+    assert int(oracle.full_prod(np.zeros(0, np.uint32))) == 1  # empty product = identity
+
+
+def test_scan_kats(oracle):
+    k = KATS["scan"]
+    x = np.array(k["input"], dtype=np.uint32).reshape(3, 4)
+    fwd = np.concatenate([oracle.scan_sum(r) for r in x])
+    rev = np.concatenate([oracle.scan_sum(r, reverse=True) for r in x])
+    prod = np.concatenate([oracle.scan_prod(r) for r in x])
+    col = np.stack([oracle.scan_sum(c) for c in x.T.copy()], axis=1).ravel()
+    assert list(fwd) == k["cumsum_axis1_forward"]
+    assert list(rev) == k["cumsum_axis1_reverse"]
+    assert list(prod) == k["cumprod_axis1_forward"]
+    assert list(col) == k["cumsum_axis0_forward"]
+    xf = x.astype(np.float32)
+    ref, _ = oracle.scan_sum(xf[0])
+    assert list(ref) == k["cumsum_axis1_forward"][:4]
+
+
+def test_rocm_scan_i32_kats(oracle):
+    k = KATS["rocm_scan_i32"]
+    x = np.array(k["input"], dtype=np.int32).reshape(2, 4)
+
+    def rows(fn, **kw):
+        return list(np.concatenate([fn(r, **kw) for r in x]))
+
+    def cols(fn, **kw):
+        return list(np.stack([fn(c, **kw) for c in x.T.copy()], axis=1).ravel())
+
+    assert rows(oracle.scan_sum) == k["cumsum_axis1"]
+    assert rows(oracle.scan_sum, reverse=True) == k["reverse_axis1"]
+    assert cols(oracle.scan_sum, reverse=True) == k["suffix_axis0"]
+    assert cols(oracle.scan_sum) == k["cumsum_axis0"]
+    assert rows(oracle.scan_prod) == k["cumprod_axis1"]
+    assert cols(oracle.scan_prod) == k["cumprod_axis0"]
+    assert rows(oracle.scan_prod, reverse=True) == k["suffix_prod_axis1"]
+    assert cols(oracle.scan_prod, reverse=True) == k["suffix_prod_axis0"]
+    long = np.array([i % 7 - 3 for i in range(1025)], dtype=np.int32)
+    acc, expect = 0, []
+    for v in long:
+        acc += int(v)
+        expect.append(acc)
+    assert list(oracle.scan_sum(long)) == expect
+
+
+def test_rocm_reduce_u32_kats(oracle):
+    for n in KATS["rocm_reduce_u32"]["sizes"]:
+        x = np.array([i % 17 for i in range(n)], dtype=np.uint32)
+        assert int(oracle.full_sum(x)) == sum(i % 17 for i in range(n))
+        assert int(oracle.full_min(x)) == 0 and int(oracle.full_max(x)) == 16
+    assert int(oracle.full_sum(np.zeros(0, np.uint32))) == 0
+
+
+# ------------------------------------------------------------- closed forms
+def test_u32_sum_wraps_mod_2_32(oracle):
+    n = 1 << 20
+    x = np.arange(n, dtype=np.uint32)
+    assert int(oracle.full_sum(x)) == (n * (n - 1) // 2) % 2**32
+    y = np.full(1000, 0xFFFFFFFF, dtype=np.uint32)
+    assert int(oracle.full_sum(y)) == (1000 * 0xFFFFFFFF) % 2**32
+    z = np.array([2**31 - 1, 1], dtype=np.int32)
+    assert int(oracle.full_sum(z)) == -(2**31)  # two's complement wrap
+
+
+def test_scan_closed_forms(oracle):
+    n = 5000
+    ones = np.ones(n, dtype=np.uint32)
+    assert np.array_equal(oracle.scan_sum(ones), np.arange(1, n + 1, dtype=np.uint32))
+    assert np.array_equal(oracle.scan_sum(ones, exclusive=True), np.arange(n, dtype=np.uint32))
+    assert np.array_equal(oracle.scan_sum(ones, reverse=True), np.arange(n, 0, -1, dtype=np.uint32))
+    x = np.random.default_rng(0).integers(0, 2**32, n, dtype=np.uint32)
+    inc = oracle.scan_sum(x)
+    exc = oracle.scan_sum(x, exclusive=True)
+    assert np.array_equal(inc - x, exc)  # exclusive = inclusive - x (mod 2^32)
+    assert np.array_equal(inc, np.cumsum(x, dtype=np.uint32))  # numpy wraps the same way
+    rev = oracle.scan_sum(x, reverse=True)
+    assert np.array_equal(rev, np.cumsum(x[::-1], dtype=np.uint32)[::-1])
+    p = oracle.scan_prod(np.full(40, 3, np.uint32))
+    assert int(p[-1]) == pow(3, 40, 2**32)
+    pe = oracle.scan_prod(np.full(5, 3, np.uint32), exclusive=True)
+    assert list(pe) == [1, 3, 9, 27, 81]
+
+
+def test_f32_sum_matches_fsum(oracle):
+    x = oracle.uniform_real(1 << 16, seed=5, lo=-1.0, hi=1.0)
+    s, a = oracle.full_sum(x)
+    assert s == pytest.approx(math.fsum(map(float, x)), abs=1e-12)
+    assert a == pytest.approx(math.fsum(abs(float(v)) for v in x), rel=1e-15)
+    ref, ab = oracle.scan_sum(x[:4096])
+    assert ref[-1] == pytest.approx(math.fsum(map(float, x[:4096])), abs=1e-12)
+    assert np.all(np.diff(ab) >= 0)
+    refx, _ = oracle.scan_sum(x[:10], exclusive=True)
+    assert refx[0] == 0.0 and refx[1] == float(x[0])
+
+
+def test_max_min_argmax_match_numpy_on_plain_data(oracle):
+    rng = np.random.default_rng(1)
+    for dtype in (np.float32, np.int32, np.uint32):
+        if dtype == np.float32:
+            x = rng.standard_normal(10007).astype(np.float32)
+        else:
+            x = rng.integers(np.iinfo(dtype).min, np.iinfo(dtype).max, 10007, dtype=dtype)
+        assert oracle.full_max(x) == x.max()
+        assert oracle.full_min(x) == x.min()
+        assert oracle.full_argmax(x) == int(np.argmax(x))
+
+
+def test_argmax_ties_go_to_lowest_index(oracle):
+    x = np.array([1, 5, 3, 5, 5, 0], dtype=np.float32)
+    assert oracle.full_argmax(x) == 1
+    assert oracle.full_argmax(np.full(100, 7, np.uint32)) == 0
+    assert oracle.full_argmax(np.arange(100, dtype=np.int32)) == 99
+
+
+def test_special_values(oracle):
+    nan = np.float32("nan")
+    inf = np.float32("inf")
+    x = np.array([nan, 1.0, nan, -2.0], dtype=np.float32)
+    assert oracle.full_max(x) == 1.0 and oracle.full_argmax(x) == 1
+    assert oracle.full_min(x) == -2.0
+    allnan = np.array([nan, nan], dtype=np.float32)
+    assert oracle.full_max(allnan) == F32_MIN  # MaxOp identity f32::MIN
+    assert oracle.full_argmax(allnan) == 0xFFFFFFFF
+    ninf = np.array([-inf, -inf], dtype=np.float32)
+    assert oracle.full_max(ninf) == F32_MIN  # identity dominates -inf
+    assert oracle.full_argmax(ninf) == 0
+    assert oracle.full_min(np.array([inf], np.float32)) == F32_MAX
+    z = np.array([-0.0, 0.0, -0.0], dtype=np.float32)
+    assert bits(oracle.full_max(z)) == 0x00000000  # +0 above -0
+    assert oracle.full_argmax(z) == 1
+    assert bits(oracle.full_min(z)) == 0x80000000
+    assert oracle.full_argmax(np.zeros(0, np.float32)) == 0xFFFFFFFF
+    assert oracle.full_max(np.zeros(0, np.int32)) == np.iinfo(np.int32).min
+    assert oracle.full_max(np.zeros(0, np.uint32)) == 0
+
+
+def test_prologue_is_correctly_rounded_fma(oracle):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(200).astype(np.float32) * np.float32(1e3)
+    for a, b in ((0.5, 0.25), (1.0 / 3.0, -7.1), (3.0, 1e-8)):
+        a32, b32 = np.float32(a), np.float32(b)
+        for i, v in enumerate(x[:50]):
+            exact = Fraction(float(a32)) * Fraction(float(v)) + Fraction(float(b32))
+            want = np.float32(float(exact))  # one rounding from an exact rational
+            # float(Fraction) rounds to f64 first; re-check for the f32 tie cases
+            if abs(Fraction(float(want)) - exact) > abs(Fraction(float(np.nextafter(want, np.float32(np.inf)))) - exact):
+                want = np.nextafter(want, np.float32(np.inf))
+            if abs(Fraction(float(want)) - exact) > abs(Fraction(float(np.nextafter(want, np.float32(-np.inf)))) - exact):
+                want = np.nextafter(want, np.float32(-np.inf))
+            got = oracle.full_max(np.array([v], np.float32), prologue=(a32, b32))
+            assert bits(got) == bits(want), (a, b, v)
+        s, _ = oracle.full_sum(x, prologue=(a32, b32))
+        expect = math.fsum(float(np.float32(float(Fraction(float(a32)) * Fraction(float(v)) + Fraction(float(b32))))) for v in x)
+        assert s == pytest.approx(expect, rel=1e-9)
+
+
+def test_bound_checker_flags_planted_errors(oracle):
+    x = oracle.uniform_real(4096, seed=9, lo=0.0, hi=1.0)
+    ref, ab = oracle.scan_sum(x)
+    got = ref.astype(np.float32)  # correctly rounded: within bound
+    bad, worst = oracle.check_f32_bound(got, ref, ab, 4096)
+    assert bad == 0 and worst <= 0.5
+    planted = got.copy()
+    # dropped term at position 1000: error |x[1000]| far above 24 eps * sum
+    planted[1000] = np.float32(ref[1000] - x[1000])
+    assert oracle.check_f32_bound(planted, ref, ab, 4096)[0] == 1
+    planted = got.copy()
+    planted[7] = np.float32("nan")
+    assert oracle.check_f32_bound(planted, ref, ab, 4096)[0] == 1
+    # the bound itself: 2 * ceil(log2 n) * eps * sum|x|
+    n = 4096
+    tol = 2 * oracle.ceil_log2(n) * 2.0**-23 * ab[-1]
+    edge = got.copy()
+    edge[-1] = np.float32(ref[-1] + 1.5 * tol)
+    assert oracle.check_f32_bound(edge, ref, ab, n)[0] == 1
+    assert oracle.ceil_log2(1) == 0 and oracle.ceil_log2(2) == 1
+    assert oracle.ceil_log2(2**28) == 28 and oracle.ceil_log2(2**28 + 1) == 29
+
+
+def test_segmented_sum_brute_force(oracle):
+    rng = np.random.default_rng(3)
+    x = rng.integers(-1000, 1001, 5000, dtype=np.int32)
+    offsets = np.array([0, 0, 3, 3, 4, 1000, 1000, 4999, 5000, 5000], dtype=np.uint32)
+    got = oracle.segmented_sum(x, offsets)
+    want = [int(x[offsets[s]:offsets[s + 1]].astype(np.int64).sum()) for s in range(len(offsets) - 1)]
+    assert list(got.astype(np.int64)) == want
+
+
+def test_geometric_offsets(oracle):
+    n = 1 << 22
+    off = oracle.geometric_offsets(n, 300.0, seed=4)
+    lens = np.diff(off.astype(np.int64))
+    assert off[0] == 0 and off[-1] == n
+    assert lens.min() >= 1
+    assert abs(float(lens[:-1].mean()) - 300.0) < 5.0
