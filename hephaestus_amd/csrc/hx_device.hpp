@@ -17,6 +17,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <typename T> struct Vec4 { using type = u32x4; };
 template <> struct Vec4<float> { using type = f32x4; };
 
+// Vector loads/stores; NT marks them non-temporal (streamed through, not
+// retained in the caches).
+template <bool NT, typename V> __device__ __forceinline__ V load_vec(const V *ptr) {
+    if constexpr (NT) return __builtin_nontemporal_load(ptr);
+    else return *ptr;
+}
+template <bool NT, typename V> __device__ __forceinline__ void store_vec(V v, V *ptr) {
+    if constexpr (NT) __builtin_nontemporal_store(v, ptr);
+    else *ptr = v;
+}
+
 // ----------------------------------------------------------------- lanes
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }

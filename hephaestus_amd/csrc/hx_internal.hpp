@@ -9,6 +9,18 @@
 #include <mutex>
 #include <string>
 
+namespace hx {
+// Host-side bookkeeping of one look-back workspace: every launch tags its
+// status words with a fresh 30-bit tag, so words left by earlier launches
+// (of any look-back kernel) read as "not yet published".  No device-side
+// end-of-launch bookkeeping is needed, and therefore no device-scope
+// release/acquire (which on multi-XCD CDNA writes back and invalidates the
+// L2) on the hot path.
+struct LookbackState {
+    uint32_t launches = 0; // launches so far on this workspace
+};
+} // namespace hx
+
 // The device handle behind hx_device* (RocmDevice analog:
 // crates/hephaestus-rocm/src/infrastructure/device.rs:109-165).
 struct hx_device {
@@ -26,7 +38,7 @@ struct hx_device {
     std::mutex ws_mu;
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
-    int ws_format = 0;
+    hx::LookbackState ws_lookback;
 };
 
 namespace hx {
@@ -70,31 +82,27 @@ bool layout_is_permuted_dense(const hx_layout &l);
 hx_status layout_basic_check(const hx_layout *l, const char *what);
 
 // ----------------------------------------------------------- workspace
-// Header of every workspace (256 bytes), followed by kernel-specific data.
+// Header of every workspace (256 bytes), followed by the full-reduce
+// partials area (64 KiB) and then the look-back status words.
 struct WorkspaceHeader {
-    uint32_t reduce_done;  // full reduce: blocks finished (reset by the last)
-    uint32_t pad0[3];
-    uint32_t tile_counter; // look-back: virtual tile ticket
-    uint32_t tile_done;    // look-back: tiles finished (reset by the last)
-    uint32_t epoch;        // look-back: launch counter, tags status words
-    uint32_t pad1[57];
+    uint32_t reserved[4]; // unused
+    uint32_t pad1[60];
 };
 static_assert(sizeof(WorkspaceHeader) == 256, "workspace header is 256 bytes");
 constexpr uint64_t kWorkspaceHeader = 256;
+constexpr uint64_t kReduceArea = 64 * 1024;
+constexpr uint64_t kLookbackOffset = kWorkspaceHeader + kReduceArea;
 
-enum WorkspaceFormat {
-    kWsNone = 0,
-    kWsReduce = 1,
-    kWsLookbackPacked = 2, // 64-bit (tag|flag|value) words
-    kWsLookbackF64 = 3,    // flag words + f64 aggregate + f64 prefix arrays
-};
-
-// Immediate-mode workspace of `dev`, grown (and zeroed) on demand.  When a
-// look-back kernel of another status format last used it, the status area is
-// cleared so stale words cannot be misread.
-hx_status device_workspace(hx_device *dev, uint64_t bytes, int format,
-                           hipStream_t stream, void **ws);
+// Immediate-mode workspace of `dev`, grown (and zeroed) on demand; a grown
+// workspace restarts its LookbackState.
+hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t stream, void **ws);
 hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws);
+
+// Tag for the next look-back launch on a workspace of `ws_bytes`; clears the
+// status area when the 30-bit tag space wraps.
+hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
+                               hipStream_t stream, uint32_t *tag);
+void commit_lookback_launch(LookbackState &st);
 
 // ------------------------------------------------------------- kernels
 
@@ -152,8 +160,9 @@ struct ScanArgs {
     int64_t out_line_stride, out_elem_stride;
     uint64_t out_offset;
 };
-uint64_t scan_workspace_bytes(const ScanArgs &args, int *format);
-hx_status launch_scan(const ScanArgs &args, void *ws, hipStream_t stream);
+uint64_t scan_workspace_bytes(const ScanArgs &args);
+hx_status launch_scan(const ScanArgs &args, void *ws, uint64_t ws_bytes,
+                      LookbackState &st, hipStream_t stream);
 
 struct SegmentedArgs {
     hx_op op;
@@ -164,9 +173,9 @@ struct SegmentedArgs {
     uint64_t num_segments; // S (num_offsets - 1)
     void *out;
 };
-uint64_t segmented_workspace_bytes(const SegmentedArgs &args, int *format);
-hx_status launch_segmented(const SegmentedArgs &args, void *ws,
-                           hipStream_t stream);
+uint64_t segmented_workspace_bytes(const SegmentedArgs &args);
+hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_bytes,
+                           LookbackState &st, hipStream_t stream);
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,
                                      uint64_t num_offsets, uint64_t n);
 
@@ -185,6 +194,7 @@ struct hx_plan {
     hx_device *dev = nullptr;
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
+    hx::LookbackState lookback;
     virtual ~hx_plan();
     virtual hx_status dispatch(hipStream_t stream) = 0;
 };

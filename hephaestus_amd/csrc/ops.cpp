@@ -106,7 +106,7 @@ struct FullPlan final : hx_plan {
 
 hx_status run_full(hx_device *dev, const FullReduceArgs &a, hipStream_t stream) {
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, full_reduce_workspace_bytes(a.n), kWsNone, stream, &ws));
+    HX_TRY(device_workspace(dev, full_reduce_workspace_bytes(a.n), stream, &ws));
     return launch_full_reduce(a, ws, stream);
 }
 
@@ -188,7 +188,9 @@ hx_status plan_scan(hx_op op, hx_dtype dtype, hx_scan_kind kind, hx_scan_directi
 
 struct ScanPlan final : hx_plan {
     ScanArgs args;
-    hx_status dispatch(hipStream_t stream) override { return launch_scan(args, ws, stream); }
+    hx_status dispatch(hipStream_t stream) override {
+        return launch_scan(args, ws, ws_bytes, lookback, stream);
+    }
 };
 
 // ----------------------------------------------------------- segmented
@@ -229,7 +231,9 @@ hx_status plan_segmented(hx_op op, hx_dtype dtype, const void *values, uint64_t 
 
 struct SegmentedPlan final : hx_plan {
     SegmentedArgs args;
-    hx_status dispatch(hipStream_t stream) override { return launch_segmented(args, ws, stream); }
+    hx_status dispatch(hipStream_t stream) override {
+        return launch_segmented(args, ws, ws_bytes, lookback, stream);
+    }
 };
 
 template <typename Plan>
@@ -391,11 +395,9 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
                      out_layout, &a));
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
-    int format = kWsNone;
-    const uint64_t bytes = scan_workspace_bytes(a, &format);
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, bytes, format, s, &ws));
-    HX_TRY(launch_scan(a, ws, s));
+    HX_TRY(device_workspace(dev, scan_workspace_bytes(a), s, &ws));
+    HX_TRY(launch_scan(a, ws, dev->ws_bytes, dev->ws_lookback, s));
     return ok();
 }
 
@@ -412,8 +414,7 @@ hx_status hx_prepare_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind
     ScanPlan *p = new (std::nothrow) ScanPlan();
     if (!p) return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of plan failed");
     p->args = a;
-    int format = kWsNone;
-    return finish_plan(dev, p, scan_workspace_bytes(a, &format), plan);
+    return finish_plan(dev, p, scan_workspace_bytes(a), plan);
 }
 
 hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, const void *values, uint64_t n,
@@ -423,11 +424,9 @@ hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, const vo
     HX_TRY(plan_segmented(op, dtype, values, n, offsets, num_offsets, out, out_len, &a));
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
-    int format = kWsNone;
-    const uint64_t bytes = segmented_workspace_bytes(a, &format);
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, bytes, format, s, &ws));
-    HX_TRY(launch_segmented(a, ws, s));
+    HX_TRY(device_workspace(dev, segmented_workspace_bytes(a), s, &ws));
+    HX_TRY(launch_segmented(a, ws, dev->ws_bytes, dev->ws_lookback, s));
     return ok();
 }
 
@@ -442,8 +441,7 @@ hx_status hx_prepare_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, 
     SegmentedPlan *p = new (std::nothrow) SegmentedPlan();
     if (!p) return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of plan failed");
     p->args = a;
-    int format = kWsNone;
-    return finish_plan(dev, p, segmented_workspace_bytes(a, &format), plan);
+    return finish_plan(dev, p, segmented_workspace_bytes(a), plan);
 }
 
 hx_status hx_validate_segment_offsets(hx_device *dev, const uint32_t *offsets, uint64_t num_offsets,

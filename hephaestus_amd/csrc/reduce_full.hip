@@ -4,13 +4,16 @@
 // The reference runs a 256-lane LDS halving tree with one element per thread
 // and one launch per tree pass (crates/hephaestus-rocm/src/application/
 // reduction.rs:16-52, prepared_reduction.rs:39-132), after a strided staging
-// copy (full_reduction_seam.rs:102-120).  Here ONE launch does the whole
-// job and reads the operand exactly once:
+// copy (full_reduction_seam.rs:102-120).  Here two launches do the whole
+// job and read the operand exactly once:
 //   pass 1  every block grid-strides over the operand with 16-byte loads,
 //           folds into registers (f32 sums in f64), reduces its 4 waves with
 //           xor-butterflies and writes one partial;
-//   pass 2  the block that finishes last (agent-scope acq_rel ticket) folds
-//           the partials in index order and writes the result.
+//   pass 2  a one-block launch folds the partials in index order and writes
+//           the result.  (A "last block folds" single launch needs a
+//           device-scope acq_rel per block, which on multi-XCD CDNA writes
+//           back and invalidates the L2 each time: measured 2.5x slower at
+//           8192 blocks.)
 // The grid size is a function of n only, so the combination order and the
 // result bits do not depend on the GPU's CU count.
 #include "hx_device.hpp"
@@ -22,8 +25,15 @@ namespace hx {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxBlocks = 2048;
-constexpr uint64_t kReduceArea = 64 * 1024; // partials area after the header
+constexpr int kMaxBlocks = 8192; // 8-byte partials fill the 64 KiB reduce area
+
+// Pass-1 grid: a function of n only (so is the combination tree), about
+// 32 Ki elements per block, at most 8192 blocks (32 per CU on 256 CUs).
+inline uint32_t full_reduce_blocks(uint64_t n) {
+    uint64_t blocks = ceil_div(n, 32768);
+    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+    return blocks < 1 ? 1u : (uint32_t)blocks;
+}
 
 enum Kind { kSum = 0, kProd = 1, kMin = 2, kMax = 3, kArgmax = 4, kMean = 5 };
 
@@ -155,13 +165,25 @@ __device__ __forceinline__ void write_result_impl(const FullParams &p, typename 
     }
 }
 
+
+template <typename P, typename T, bool AFFINE, typename V>
+__device__ __forceinline__ typename P::Acc fold4(const V &v, uint64_t e, float a, float b) {
+    using Acc = typename P::Acc;
+    const Acc a0 = P::lift(prologue<T, AFFINE>((T)v.x, a, b), e);
+    const Acc a1 = P::lift(prologue<T, AFFINE>((T)v.y, a, b), e + 1);
+    const Acc a2 = P::lift(prologue<T, AFFINE>((T)v.z, a, b), e + 2);
+    const Acc a3 = P::lift(prologue<T, AFFINE>((T)v.w, a, b), e + 3);
+    return P::combine(P::combine(a0, a1), P::combine(a2, a3));
+}
+
 // FLAT: the view is the contiguous element range [offset, offset + n).
-template <typename T, int K, bool AFFINE, bool FLAT>
+// UNROLL independent 16-byte loads are in flight per thread per trip; NT
+// marks them non-temporal (streamed, not kept in the caches).
+template <typename T, int K, bool AFFINE, bool FLAT, int UNROLL = 4, bool NT = true>
 __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
     using P = Policy<T, K>;
     using Acc = typename P::Acc;
     __shared__ Acc lds[kBlock / kWave];
-    __shared__ uint32_t s_last;
 
     const uint64_t n = p.n;
     const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -179,30 +201,16 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
         using V = typename Vec4<T>::type;
         const V *vsrc = (const V *)(src + head);
         uint64_t vi = tid;
-        // Four independent 16-byte loads in flight per thread per trip.
-        for (; vi + 3 * nthreads < nvec; vi += 4 * nthreads) {
-            V v[4];
+        for (; vi + (UNROLL - 1) * nthreads < nvec; vi += UNROLL * nthreads) {
+            V v[UNROLL];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(&vsrc[vi + u * nthreads]);
+            for (int u = 0; u < UNROLL; ++u) v[u] = load_vec<NT>(&vsrc[vi + u * nthreads]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint64_t e = head + 4 * (vi + u * nthreads);
-                Acc a0 = P::lift(prologue<T, AFFINE>((T)v[u].x, p.a, p.b), e);
-                Acc a1 = P::lift(prologue<T, AFFINE>((T)v[u].y, p.a, p.b), e + 1);
-                Acc a2 = P::lift(prologue<T, AFFINE>((T)v[u].z, p.a, p.b), e + 2);
-                Acc a3 = P::lift(prologue<T, AFFINE>((T)v[u].w, p.a, p.b), e + 3);
-                acc = P::combine(acc, P::combine(P::combine(a0, a1), P::combine(a2, a3)));
-            }
+            for (int u = 0; u < UNROLL; ++u)
+                acc = P::combine(acc, fold4<P, T, AFFINE>(v[u], head + 4 * (vi + u * nthreads), p.a, p.b));
         }
-        for (; vi < nvec; vi += nthreads) {
-            V v = __builtin_nontemporal_load(&vsrc[vi]);
-            const uint64_t e = head + 4 * vi;
-            Acc a0 = P::lift(prologue<T, AFFINE>((T)v.x, p.a, p.b), e);
-            Acc a1 = P::lift(prologue<T, AFFINE>((T)v.y, p.a, p.b), e + 1);
-            Acc a2 = P::lift(prologue<T, AFFINE>((T)v.z, p.a, p.b), e + 2);
-            Acc a3 = P::lift(prologue<T, AFFINE>((T)v.w, p.a, p.b), e + 3);
-            acc = P::combine(acc, P::combine(P::combine(a0, a1), P::combine(a2, a3)));
-        }
+        for (; vi < nvec; vi += nthreads)
+            acc = P::combine(acc, fold4<P, T, AFFINE>(load_vec<NT>(&vsrc[vi]), head + 4 * vi, p.a, p.b));
         const uint64_t tail0 = head + 4 * nvec;
         if (tail0 + tid < n) {
             const uint64_t e = tail0 + tid;
@@ -215,33 +223,22 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
     }
 
     Acc part = block_reduce<P>(acc, lds);
-    Acc *partials = (Acc *)p.partials;
-    if (threadIdx.x == 0) {
-        partials[blockIdx.x] = part;
-        // Release this block's partial; the RMW chain makes every partial
-        // visible to the block that observes the final count.
-        uint32_t prev = fetch_add32_acqrel(&p.hdr->reduce_done, 1u);
-        s_last = (prev == gridDim.x - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (s_last == 0u) return;
+    if (threadIdx.x == 0) ((Acc *)p.partials)[blockIdx.x] = part;
+}
 
-    // Pass 2: fixed-order fold of the partials by the last block.
+// Pass 2: one block folds the G partials in index order (a fixed tree, so
+// the result bits depend only on n) and writes the result.  The kernel
+// boundary orders it after pass 1; no device-scope fences are needed.
+template <typename T, int K>
+__global__ __launch_bounds__(kBlock) void full_reduce_final_kernel(FullParams p, uint32_t parts) {
+    using P = Policy<T, K>;
+    using Acc = typename P::Acc;
+    __shared__ Acc lds[kBlock / kWave];
+    const Acc *partials = (const Acc *)p.partials;
     Acc r = P::identity();
-    for (uint32_t k = threadIdx.x; k < gridDim.x; k += kBlock) {
-        Acc v;
-        if constexpr (sizeof(Acc) == 8) {
-            v = __builtin_bit_cast(Acc, ld_relaxed((const uint64_t *)&partials[k]));
-        } else {
-            v = __builtin_bit_cast(Acc, ld_relaxed32((const uint32_t *)&partials[k]));
-        }
-        r = P::combine(r, v);
-    }
+    for (uint32_t k = threadIdx.x; k < parts; k += kBlock) r = P::combine(r, partials[k]);
     r = block_reduce<P>(r, lds);
-    if (threadIdx.x == 0) {
-        write_result_impl<T, K>(p, r);
-        st_relaxed32(&p.hdr->reduce_done, 0u); // ready for the next launch
-    }
+    if (threadIdx.x == 0) write_result_impl<T, K>(p, r);
 }
 
 // n == 0: the result is the operator identity (ops.rs:926-983); empty
@@ -276,16 +273,16 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
             return check_launch("full_reduce_empty_kernel");
         }
     }
-    uint64_t blocks = ceil_div(a.n, 8192);
-    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
-    if (blocks < 1) blocks = 1;
+    const uint32_t blocks = full_reduce_blocks(a.n);
     if (a.flat)
-        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, true>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
+        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, true>), dim3(blocks), dim3(kBlock), 0,
+                           stream, p);
     else
-        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, false>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
-    return check_launch("full_reduce_kernel");
+        hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, false>), dim3(blocks), dim3(kBlock), 0,
+                           stream, p);
+    HX_TRY(check_launch("full_reduce_kernel"));
+    hipLaunchKernelGGL((full_reduce_final_kernel<T, K>), dim3(1), dim3(kBlock), 0, stream, p, blocks);
+    return check_launch("full_reduce_final_kernel");
 }
 
 template <typename T, bool AFFINE>

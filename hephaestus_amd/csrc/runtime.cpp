@@ -86,8 +86,7 @@ hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws) {
     return HX_OK;
 }
 
-hx_status device_workspace(hx_device *dev, uint64_t bytes, int format,
-                           hipStream_t stream, void **ws) {
+hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t, void **ws) {
     std::lock_guard<std::mutex> lock(dev->ws_mu);
     if (bytes > dev->ws_bytes) {
         if (dev->ws) {
@@ -99,20 +98,26 @@ hx_status device_workspace(hx_device *dev, uint64_t bytes, int format,
         uint64_t grow = bytes < (1ull << 20) ? (1ull << 20) : bytes;
         HX_TRY(alloc_workspace(dev, grow, &dev->ws));
         dev->ws_bytes = grow;
-        dev->ws_format = format;
-    } else if (format != dev->ws_format && format != kWsNone) {
-        // A different look-back status encoding used this area last: clear
-        // everything after the header so no stale word can be misread.
-        if (dev->ws_bytes > kWorkspaceHeader) {
-            HX_HIP(hipMemsetAsync((char *)dev->ws + kWorkspaceHeader, 0,
-                                  dev->ws_bytes - kWorkspaceHeader, stream),
-                   HX_ERR_DISPATCH_FAILED, "workspace clear");
-        }
-        dev->ws_format = format;
+        dev->ws_lookback = LookbackState{};
     }
     *ws = dev->ws;
     return HX_OK;
 }
+
+hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
+                               hipStream_t stream, uint32_t *tag) {
+    const uint32_t t = (st.launches % 0x3FFFFFFFu) + 1u;
+    if (t == 1u && st.launches != 0u && ws_bytes > kLookbackOffset) {
+        // The tag space wrapped: words from 2^30 - 1 launches ago would read
+        // as current, so clear them once.
+        HX_HIP(hipMemsetAsync((char *)ws + kLookbackOffset, 0, ws_bytes - kLookbackOffset, stream),
+               HX_ERR_DISPATCH_FAILED, "look-back status clear");
+    }
+    *tag = t;
+    return HX_OK;
+}
+
+void commit_lookback_launch(LookbackState &st) { st.launches += 1u; }
 
 } // namespace hx
 

@@ -5,25 +5,39 @@
 // contiguous chunk serially, lane 0 folds the chunk totals, and a second sweep
 // re-reads and re-writes the output (core accelerator/scan.rs:56-155).  A 1-D
 // scan of 2^28 elements therefore runs on one CU.  Here every line is cut
-// into tiles of 4096 elements that all CUs process in a single pass:
+// into tiles of 16384 elements that all CUs process in a single pass:
 //
-//   * a block takes a virtual tile ticket from an agent-scope counter, so
-//     every tile it may wait on was taken by a block that is already running
-//     (forward progress without any dispatch-order assumption);
-//   * the tile is loaded with 16-byte vectors, wave-striped: step j of wave w
-//     holds 256 contiguous elements, lane l four of them; each step is a
-//     4-element register scan plus a 6-step wave64 scan of lane totals;
-//   * the tile aggregate is published, then wave 0 looks back over up to 64
-//     predecessors per poll (one status word per lane) until it meets an
-//     inclusive prefix; the tile publishes its own inclusive prefix;
-//   * every element is written exactly once, 16-byte vectors again.
+//   * block b scans tile b.  The tile is loaded with 16-byte vectors,
+//     wave-striped: step j of wave w holds 256 contiguous elements, lane l
+//     four of them; each step is a 4-element register scan plus a 6-step
+//     wave64 scan of the lane totals;
+//   * the tile aggregate is published, wave 0 looks back for the tile's
+//     exclusive prefix and publishes the tile's inclusive prefix;
+//   * every element is read once and written once, 16-byte vectors again.
 //
-// Status words carry a 30-bit launch tag, so a new launch never needs the
-// status array cleared: the last block to finish bumps the tag and resets
-// the ticket counter.  Integer scans publish (tag, flag, value) in ONE 64-bit
-// word.  f32 scans carry the inter-tile prefix in f64 (two value arrays and a
-// flag word released after the value), which keeps the error of every output
-// within a few ulp of the f32-rounded exact prefix at 2^30 elements.
+// The look-back has two levels.  Tiles are grouped in superblocks of 64; the
+// last tile of a superblock also publishes the superblock's aggregate (as
+// soon as its 63 predecessors have published theirs) and later its
+// inclusive prefix.  A tile first folds its own superblock's predecessors
+// (one poll of 64 lanes) and then whole superblocks, 64 per poll.  With ~2000
+// tiles in flight, a flat look-back walks up to ~32 sequential polls to
+// reach a published prefix; the two levels need about two.
+//
+// Forward progress does not depend on the order in which the hardware
+// dispatches blocks: when a status stays unpublished for kSpinLimit polls
+// (its block may not be running yet), the waiting wave computes the missing
+// value itself -- a tile aggregate from the input with the owner's
+// arithmetic, a superblock value from its tiles' statuses -- and publishes
+// it ("decoupled fallback", Smith, Levien and Owens 2024).  There is no
+// tile-ticket counter: one same-address device-scope atomic per tile
+// serialises at ~11 ns on MI355X, which alone cost 745 us for 65536 tiles.
+//
+// Status words carry a 30-bit per-launch tag (set by the host), so a launch
+// never clears the status array and needs no end-of-launch bookkeeping.
+// Integer scans publish (tag, flag, value) in ONE 64-bit word.  f32 scans
+// carry the inter-tile prefix in f64, split into two self-tagged words,
+// which keeps every output within a few ulp of the f32-rounded exact prefix
+// at 2^30 elements.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -34,21 +48,30 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kSteps = 4;                            // vectors per lane
-constexpr int kWaveElems = kWave * 4 * kSteps;       // 1024
-constexpr int kTile = kWaves * kWaveElems;           // 4096
-constexpr uint64_t kLookbackOffset = 256 + 64 * 1024; // after header + reduce area
-
+constexpr int kSteps = 16;                           // 16-byte vectors per lane
+constexpr int kTile = kWaves * kWave * 4 * kSteps;   // 16384 elements
+constexpr int kSuper = 64;                           // tiles per superblock
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
+constexpr uint32_t kSpinLimit = 64; // polls before computing a missing value
 
-__device__ __forceinline__ uint32_t epoch_tag(uint32_t epoch) { return (epoch % 0x3FFFFFFFu) + 1u; }
+__device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
+    return ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v;
+}
 
 // (tag, flag, value) in one 64-bit word: [63:34] tag, [33:32] flag, [31:0] value.
 struct PackedStatus {
     using C = uint32_t;
     uint64_t *words;
     __device__ __forceinline__ void publish(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
-        st_relaxed(&words[t], ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v);
+        st_relaxed(&words[t], status_word(tag, flag, v));
+    }
+    // Fallback publication: never overwrites a word of this launch (so a
+    // published inclusive prefix is never downgraded to an aggregate).
+    __device__ __forceinline__ void publish_if_unset(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        uint64_t cur = ld_relaxed(&words[t]);
+        if ((uint32_t)(cur >> 34) == tag) return;
+        __hip_atomic_compare_exchange_strong(&words[t], &cur, status_word(tag, flag, v), __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
         const uint64_t w = ld_relaxed(&words[t]);
@@ -58,65 +81,220 @@ struct PackedStatus {
     }
 };
 
-// f64 carries: the value is stored first, then the flag word with release
-// semantics; a reader acquires the flag before reading the value.  The
-// aggregate and the inclusive prefix live in different arrays so a reader
-// that saw "aggregate" can never read a later prefix by mistake.
+// f64 carries: each 64-bit status word holds (tag, flag, one 32-bit half of
+// the f64).  Entry t's aggregate lives in words [4t, 4t+1] and its inclusive
+// prefix in [4t+2, 4t+3]; a reader accepts a value only when both halves
+// carry the current tag, so no release/acquire ordering is needed.  A slot
+// can have several writers (owner and fallbacks): whoever moves the high
+// word from an old tag to this launch's tag with a CAS also writes the low
+// word, and everyone else leaves the slot alone, so halves of different
+// writers never mix.
 struct F64Status {
     using C = double;
-    uint32_t *flags;
-    double *agg;
-    double *incl;
+    uint64_t *words;
     __device__ __forceinline__ void publish(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
-        if (flag == kAggregate) st_relaxed_f64(&agg[t], v);
-        else st_relaxed_f64(&incl[t], v);
-        st_release32(&flags[t], (tag << 2) | flag);
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        uint64_t *w = words + 4 * t + (flag == kPrefix ? 2 : 0);
+        uint64_t cur = ld_relaxed(&w[0]);
+        if ((uint32_t)(cur >> 34) == tag) return;
+        if (__hip_atomic_compare_exchange_strong(&w[0], &cur, status_word(tag, flag, (uint32_t)(b >> 32)),
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            st_relaxed(&w[1], status_word(tag, flag, (uint32_t)b));
+    }
+    __device__ __forceinline__ void publish_if_unset(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        publish(t, tag, flag, v);
     }
     __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
-        const uint32_t f = ld_acquire(&flags[t]);
-        flag = ((f >> 2) == tag) ? (f & 3u) : kInvalid;
-        if (flag == kAggregate) v = ld_relaxed_f64(&agg[t]);
-        else if (flag == kPrefix) v = ld_relaxed_f64(&incl[t]);
+        const uint64_t *w = words + 4 * t;
+        const uint64_t a0 = ld_relaxed(&w[0]), a1 = ld_relaxed(&w[1]);
+        const uint64_t p0 = ld_relaxed(&w[2]), p1 = ld_relaxed(&w[3]);
+        const uint32_t want_a = (tag << 2) | kAggregate, want_p = (tag << 2) | kPrefix;
+        if ((uint32_t)(p0 >> 32) == want_p && (uint32_t)(p1 >> 32) == want_p) {
+            flag = kPrefix;
+            v = __builtin_bit_cast(double, (p0 << 32) | (p1 & 0xFFFFFFFFull));
+        } else if ((uint32_t)(a0 >> 32) == want_a && (uint32_t)(a1 >> 32) == want_a) {
+            flag = kAggregate;
+            v = __builtin_bit_cast(double, (a0 << 32) | (a1 & 0xFFFFFFFFull));
+        } else {
+            flag = kInvalid;
+        }
     }
 };
 
 struct ScanParams {
     const void *in;
     void *out;
-    uint64_t lines, len, tiles_per_line, total_tiles;
+    uint64_t lines, len, tiles_per_line, total_tiles, supers_per_line;
     int64_t in_line_stride, in_elem_stride;
     int64_t out_line_stride, out_elem_stride;
     uint64_t in_offset, out_offset;
-    WorkspaceHeader *hdr;
+    uint32_t tag; // this launch's status tag
 };
 
-// Wave 0 of tile `ticket` folds the values of its predecessors in the same
-// line, nearest first, up to and including the first inclusive prefix.
-template <typename Op, typename Status>
-__device__ typename Status::C lookback(const Status &st, uint64_t ticket, uint64_t line_first,
-                                       uint32_t tag) {
+// The four elements of one lane and step (logical index e..e+3 of the
+// line), identity past the end.
+template <typename T, bool VEC, bool REV, bool NT>
+__device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t ib, uint64_t e, T ident,
+                                      T (&v)[4]) {
+    if constexpr (VEC) {
+        if (e + 3 < p.len) {
+            using V = typename Vec4<T>::type;
+            const V q = load_vec<NT>((const V *)(in + ib + (int64_t)e));
+            v[0] = (T)q.x;
+            v[1] = (T)q.y;
+            v[2] = (T)q.z;
+            v[3] = (T)q.w;
+            return;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint64_t i = e + c;
+        const uint64_t li = REV ? (p.len - 1 - i) : i;
+        v[c] = (i < p.len) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
+    }
+}
+
+// A lane's left-to-right fold of its four elements; the owner and the
+// fallback both build step totals from it the same way.
+template <typename T, typename Op>
+__device__ __forceinline__ T lane_fold(const T (&v)[4]) {
+    return Op::combine(Op::combine(Op::combine(v[0], v[1]), v[2]), v[3]);
+}
+
+// Aggregate of tile `u` computed by ONE wave, step by step, with the same
+// operations and order as the four owner waves (fallback path).
+template <typename T, typename Op, bool VEC, bool REV, bool NT, int STEPS>
+__device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
+    constexpr int kWaveElems = kWave * 4 * STEPS;
+    constexpr int kTileElems = kWaves * kWaveElems;
+    const T ident = Op::template identity<T>();
+    const uint64_t line = u / p.tiles_per_line;
+    const uint64_t tin = u - line * p.tiles_per_line;
+    const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
+    const T *in = (const T *)p.in;
+    T agg = ident;
+    for (int w = 0; w < kWaves; ++w) {
+        T carry = ident;
+        for (int j = 0; j < STEPS; ++j) {
+            T v[4];
+            load4<T, VEC, REV, NT>(p, in, ib,
+                                   tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)j * (kWave * 4) +
+                                       (uint64_t)lane_id() * 4,
+                                   ident, v);
+            const T incl = wave_inclusive_scan<Op, T>(lane_fold<T, Op>(v));
+            carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
+        }
+        agg = Op::combine(agg, carry);
+    }
+    return agg;
+}
+
+// Hooks let a look-back do other work while it spins.  KnownAgg: the
+// tile's aggregate is already published.  (The overlapped kernel's hook
+// publishes it from inside the spin loop as soon as the data waves post it.)
+template <typename C> struct KnownAgg {
+    C a;
+    __device__ __forceinline__ void poll() {}
+    __device__ __forceinline__ C agg() { return a; }
+};
+
+// Fold of the statuses of the `count` (<= 64) tiles just before tile
+// `tile_end`, nearest first, stopping at the first inclusive prefix; `found`
+// tells whether one was met.  Lane l reads the tile at distance l.  A tile
+// that stays unpublished is computed by tile_aggregate.
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, typename Hook>
+__device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, uint64_t tile_end, int count,
+                                         bool &found, Hook &hook) {
     using C = typename Status::C;
     const int lane = lane_id();
-    C excl = Op::template identity<C>();
-    int64_t pred = (int64_t)ticket - 1;
+    const C ident = Op::template identity<C>();
+    uint32_t flag;
+    C val;
+    uint32_t spins = 0;
+    for (;;) {
+        flag = kAggregate; // lanes past `count`: valid, not a prefix, identity
+        val = ident;
+        if (lane < count) st.read(tile_end - 1 - lane, p.tag, flag, val);
+        const uint64_t pm = ballot(flag == kPrefix);
+        const uint64_t im = ballot(flag == kInvalid);
+        // Every status up to and including the nearest prefix is needed.
+        const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
+        const uint64_t missing = im & need;
+        if (missing == 0ull) break;
+        hook.poll();
+        if (++spins >= kSpinLimit) {
+            const uint64_t u = tile_end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
+            const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS>(p, u);
+            if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
+            spins = 0;
+            continue;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    const uint64_t pm = ballot(flag == kPrefix);
+    const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
+    found = pm != 0ull;
+    return wave_reduce<Op, C>((lane <= first) ? val : ident);
+}
+
+// Exclusive prefix of tile `tile` (position `tin` in its line), computed by
+// one wave.  The last tile of a superblock publishes the superblock
+// aggregate on the way (it needs the tile's own aggregate: hook.agg()).
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, typename Hook>
+__device__ typename Status::C lookback(const ScanParams &p, const Status &st, const Status &st1, uint64_t tile,
+                                       uint64_t line, uint64_t tin, Hook &hook) {
+    using C = typename Status::C;
+    const int lane = lane_id();
+    const C ident = Op::template identity<C>();
+    const int pos = (int)(tin % kSuper);
+    const uint64_t sb = tin / kSuper;
+    const uint64_t line_super = line * p.supers_per_line;
+    const bool last_in_super = pos == kSuper - 1 && tin + 1 < p.tiles_per_line;
+
+    // Level 0: predecessors in the tile's own superblock.
+    bool found = false;
+    C excl = pos > 0 ? fold_tiles<T, Op, Status, VEC, REV, NT, STEPS>(p, st, tile, pos, found, hook) : ident;
+    if (found) return excl; // superblock 0 always ends here (tile 0 is a prefix)
+    if (last_in_super) {
+        const C a = hook.agg();
+        if (lane == 0) st1.publish(line_super + sb, p.tag, kAggregate, Op::combine(excl, a));
+    }
+
+    // Level 1: whole superblocks, nearest first.
+    int64_t pred = (int64_t)(line_super + sb) - 1;
     for (;;) {
         const int64_t idx = pred - lane;
-        const bool in_line = idx >= (int64_t)line_first;
-        uint32_t flag = kPrefix;
-        C val = Op::template identity<C>();
+        const bool in_line = idx >= (int64_t)line_super;
+        uint32_t flag;
+        C val;
+        uint32_t spins = 0;
         for (;;) {
-            if (in_line) st.read((uint64_t)idx, tag, flag, val);
+            flag = kPrefix; // before the line's first superblock: identity
+            val = ident;
+            if (in_line) st1.read((uint64_t)idx, p.tag, flag, val);
             const uint64_t pm = ballot(flag == kPrefix);
             const uint64_t im = ballot(flag == kInvalid);
-            // Lanes 0..first-prefix must all be valid.
             const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
-            if ((im & need) == 0ull) break;
+            const uint64_t missing = im & need;
+            if (missing == 0ull) break;
+            hook.poll();
+            if (++spins >= kSpinLimit) {
+                // Rebuild the missing superblock's value from its 64 tiles:
+                // an inclusive prefix if one of them has one, else the sum.
+                const uint64_t s = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
+                const uint64_t s_end = line * p.tiles_per_line + (s - line_super + 1) * kSuper;
+                bool f = false;
+                const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS>(p, st, s_end, kSuper, f, hook);
+                if (lane == 0) st1.publish_if_unset(s, p.tag, f ? kPrefix : kAggregate, v);
+                spins = 0;
+                continue;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
         const uint64_t pm = ballot(flag == kPrefix);
         const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
-        const C contrib = (lane <= first) ? val : Op::template identity<C>();
-        excl = Op::combine(wave_reduce<Op, C>(contrib), excl);
+        excl = Op::combine(excl, wave_reduce<Op, C>((lane <= first) ? val : ident));
         if (pm) break;
         pred -= kWave;
     }
@@ -132,59 +310,39 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
     }
 }
 
-template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV>
-__global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status st) {
+// STEPS vectors per lane: a tile is 4 waves * 64 lanes * 4 * STEPS elements.
+// VEC: unit-stride, 16-byte aligned lines (vector loads and stores).  REV:
+// suffix scan (logical element i is physical len-1-i).  NT: non-temporal
+// vector accesses.
+template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
+          bool NT = true>
+__global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     using C = typename Status::C;
-    __shared__ uint32_t s_ticket;
-    __shared__ uint32_t s_tag;
+    constexpr int kWaveElems = kWave * 4 * STEPS;
+    constexpr int kTileElems = kWaves * kWaveElems;
     __shared__ T s_wave_tot[kWaves];
     __shared__ C s_excl;
 
-    if (threadIdx.x == 0) {
-        s_ticket = fetch_add32(&p.hdr->tile_counter, 1u);
-        s_tag = epoch_tag(ld_relaxed32(&p.hdr->epoch));
-    }
-    __syncthreads();
-    const uint64_t ticket = s_ticket;
-    const uint32_t tag = s_tag;
-    const uint64_t line = ticket / p.tiles_per_line;
-    const uint64_t tin = ticket - line * p.tiles_per_line;
+    const uint64_t tile = blockIdx.x;
+    const uint64_t line = tile / p.tiles_per_line;
+    const uint64_t tin = tile - line * p.tiles_per_line;
     const int w = threadIdx.x / kWave;
     const int lane = lane_id();
     const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
     const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
-    const uint64_t e0 = tin * kTile + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+    const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
     const T *in = (const T *)p.in;
     T *out = (T *)p.out;
     const T ident = Op::template identity<T>();
 
-    T x[kSteps][4];
+    T x[STEPS][4];
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-        const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
-        if constexpr (VEC) {
-            if (e + 3 < p.len) {
-                using V = typename Vec4<T>::type;
-                const V v = __builtin_nontemporal_load((const V *)(in + ib + (int64_t)e));
-                x[j][0] = (T)v.x;
-                x[j][1] = (T)v.y;
-                x[j][2] = (T)v.z;
-                x[j][3] = (T)v.w;
-                continue;
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint64_t i = e + c;
-            const uint64_t li = REV ? (p.len - 1 - i) : i;
-            x[j][c] = (i < p.len) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
-        }
-    }
+    for (int j = 0; j < STEPS; ++j) load4<T, VEC, REV, NT>(p, in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
 
     // Per step: register scan of 4, wave scan of lane totals, running carry.
     T carry = ident;
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
+    for (int j = 0; j < STEPS; ++j) {
         const T p0 = x[j][0];
         const T p1 = Op::combine(p0, x[j][1]);
         const T p2 = Op::combine(p1, x[j][2]);
@@ -192,7 +350,6 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
         const T incl = wave_inclusive_scan<Op, T>(p3);
         T lex = __shfl_up(incl, 1, kWave);
         if (lane == 0) lex = ident;
-        const T step_tot = __shfl(incl, kWave - 1, kWave);
         const T base = Op::combine(carry, lex);
         if constexpr (EXCL) {
             x[j][0] = base;
@@ -205,7 +362,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
             x[j][2] = Op::combine(base, p2);
             x[j][3] = Op::combine(base, p3);
         }
-        carry = Op::combine(carry, step_tot);
+        carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
     }
     if (lane == 0) s_wave_tot[w] = carry;
     __syncthreads();
@@ -221,19 +378,22 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
         const C agg = (C)tile_agg;
         C excl = Op::template identity<C>();
         if (tin == 0) {
-            if (lane == 0) st.publish(ticket, tag, kPrefix, agg);
+            if (lane == 0) st.publish(tile, p.tag, kPrefix, agg);
         } else {
-            if (lane == 0) st.publish(ticket, tag, kAggregate, agg);
-            excl = lookback<Op>(st, ticket, ticket - tin, tag);
-            if (lane == 0) st.publish(ticket, tag, kPrefix, Op::combine(excl, agg));
+            if (lane == 0) st.publish(tile, p.tag, kAggregate, agg);
+            KnownAgg<C> hook{agg};
+            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
+            if (lane == 0) st.publish(tile, p.tag, kPrefix, Op::combine(excl, agg));
         }
+        if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
+            st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, Op::combine(excl, agg));
         if (lane == 0) s_excl = excl;
     }
     __syncthreads();
     const C tile_excl = s_excl;
 
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
+    for (int j = 0; j < STEPS; ++j) {
         const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
         T r[4];
 #pragma unroll
@@ -246,7 +406,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
                 v.y = r[1];
                 v.z = r[2];
                 v.w = r[3];
-                __builtin_nontemporal_store(v, (V *)(out + ob + (int64_t)e));
+                store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
                 continue;
             }
         }
@@ -257,13 +417,288 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
             if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
         }
     }
+}
 
-    if (threadIdx.x == 0) {
-        const uint32_t d = fetch_add32_acqrel(&p.hdr->tile_done, 1u);
-        if (d == (uint32_t)(p.total_tiles - 1)) {
-            st_relaxed32(&p.hdr->tile_counter, 0u);
-            st_relaxed32(&p.hdr->tile_done, 0u);
-            st_relaxed32(&p.hdr->epoch, ld_relaxed32(&p.hdr->epoch) + 1u);
+// Streaming form: a persistent grid of G blocks, block b scanning tiles
+// b, b+G, b+2G, ...  Waves 0-3 move data; wave 4 only publishes and looks
+// back.  While wave 4 resolves tile k's prefix, the data waves already have
+// tile k+1's loads in flight, so the look-back latency overlaps HBM traffic
+// instead of adding to every tile's lifetime.  (vmcnt is per wave, so
+// wave 4's polls never queue behind the data loads.)  LDS slots are double
+// buffered by tile parity so one barrier pair per tile suffices.
+template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
+          bool NT = true>
+__global__ __launch_bounds__(kBlock + kWave) void scan_stream_kernel(ScanParams p, Status st, Status st1) {
+    using C = typename Status::C;
+    constexpr int kWaveElems = kWave * 4 * STEPS;
+    constexpr int kTileElems = kWaves * kWaveElems;
+    __shared__ T s_wave_tot[2][kWaves];
+    __shared__ C s_excl[2];
+
+    const int w = threadIdx.x / kWave;
+    const int lane = lane_id();
+    const bool data = w < kWaves;
+    const T ident = Op::template identity<T>();
+    const uint64_t G = gridDim.x;
+    T *out = (T *)p.out;
+
+    T a[STEPS][4], b[STEPS][4];
+    uint64_t tile = blockIdx.x;
+    auto load_tile = [&](uint64_t t, T (&x)[STEPS][4]) {
+        const uint64_t line = t / p.tiles_per_line;
+        const uint64_t tin = t - line * p.tiles_per_line;
+        const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
+        const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j)
+            load4<T, VEC, REV, NT>(p, (const T *)p.in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
+    };
+    if (data && tile < p.total_tiles) load_tile(tile, a);
+
+    for (int k = 0; tile < p.total_tiles; ++k, tile += G) {
+        const int slot = k & 1;
+        const uint64_t line = tile / p.tiles_per_line;
+        const uint64_t tin = tile - line * p.tiles_per_line;
+        if (data) {
+            // In-register scan of this wave's part, as in scan_tiles_kernel.
+            T carry = ident;
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                const T p0 = a[j][0];
+                const T p1 = Op::combine(p0, a[j][1]);
+                const T p2 = Op::combine(p1, a[j][2]);
+                const T p3 = Op::combine(p2, a[j][3]);
+                const T incl = wave_inclusive_scan<Op, T>(p3);
+                T lex = __shfl_up(incl, 1, kWave);
+                if (lane == 0) lex = ident;
+                const T base = Op::combine(carry, lex);
+                if constexpr (EXCL) {
+                    a[j][0] = base;
+                    a[j][1] = Op::combine(base, p0);
+                    a[j][2] = Op::combine(base, p1);
+                    a[j][3] = Op::combine(base, p2);
+                } else {
+                    a[j][0] = Op::combine(base, p0);
+                    a[j][1] = Op::combine(base, p1);
+                    a[j][2] = Op::combine(base, p2);
+                    a[j][3] = Op::combine(base, p3);
+                }
+                carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
+            }
+            if (lane == 0) s_wave_tot[slot][w] = carry;
+        }
+        __syncthreads();
+        if (data) {
+            if (tile + G < p.total_tiles) load_tile(tile + G, b); // prefetch
+        } else {
+            T tile_agg = ident;
+#pragma unroll
+            for (int q = 0; q < kWaves; ++q) tile_agg = Op::combine(tile_agg, s_wave_tot[slot][q]);
+            const C agg = (C)tile_agg;
+            C excl = Op::template identity<C>();
+            if (tin == 0) {
+                if (lane == 0) st.publish(tile, p.tag, kPrefix, agg);
+            } else {
+                if (lane == 0) st.publish(tile, p.tag, kAggregate, agg);
+                KnownAgg<C> hook{agg};
+            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
+                if (lane == 0) st.publish(tile, p.tag, kPrefix, Op::combine(excl, agg));
+            }
+            if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
+                st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, Op::combine(excl, agg));
+            if (lane == 0) s_excl[slot] = excl;
+        }
+        __syncthreads();
+        if (data) {
+            T wave_excl = ident;
+#pragma unroll
+            for (int q = 0; q < kWaves; ++q)
+                if (q < w) wave_excl = Op::combine(wave_excl, s_wave_tot[slot][q]);
+            const C tile_excl = s_excl[slot];
+            const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
+            const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+                T r[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, a[j][c]));
+                bool done = false;
+                if constexpr (VEC) {
+                    if (e + 3 < p.len) {
+                        using V = typename Vec4<T>::type;
+                        V v;
+                        v.x = r[0];
+                        v.y = r[1];
+                        v.z = r[2];
+                        v.w = r[3];
+                        store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
+                        done = true;
+                    }
+                }
+                if (!done) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const uint64_t i = e + c;
+                        const uint64_t li = REV ? (p.len - 1 - i) : i;
+                        if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) a[j][c] = b[j][c];
+        }
+    }
+}
+
+// Overlapped form: one tile per block as in scan_tiles_kernel, plus a fifth
+// wave that only looks back.  It starts polling its predecessors' statuses
+// as soon as the block starts, while waves 0-3 are still loading, and
+// publishes the tile aggregate from inside its spin loop the moment the data
+// waves post their totals (an LDS counter).  A tile's lifetime becomes
+// max(load + scan, look-back) + store instead of their sum.
+template <typename T, typename Op, typename Status> struct PostedAgg {
+    using C = typename Status::C;
+    const Status *st;
+    uint32_t *ready;    // LDS: data waves that have posted their totals
+    const T *wave_tot;  // LDS: the data waves' totals
+    uint64_t tile;
+    uint32_t tag;
+    bool have = false;
+    bool published = false;
+    C a{};
+    __device__ __forceinline__ bool fetch() {
+        if (have) return true;
+        const uint32_t r = __hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__builtin_amdgcn_readfirstlane(r) < (uint32_t)kWaves) return false;
+        T t = Op::template identity<T>(); // same fold order as scan_tiles_kernel
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) t = Op::combine(t, wave_tot[q]);
+        a = (C)t;
+        have = true;
+        return true;
+    }
+    // Called while spinning: publish the aggregate once it exists.
+    __device__ __forceinline__ void poll() {
+        if (!published && fetch()) {
+            if (lane_id() == 0) st->publish(tile, tag, kAggregate, a);
+            published = true;
+        }
+    }
+    // The aggregate, still mid-look-back: wait for it and publish it.
+    __device__ __forceinline__ C agg() {
+        while (!fetch()) __builtin_amdgcn_s_sleep(1);
+        poll();
+        return a;
+    }
+    // The aggregate after the look-back: no need to publish it any more.
+    __device__ __forceinline__ C value() {
+        while (!fetch()) __builtin_amdgcn_s_sleep(1);
+        return a;
+    }
+};
+
+template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
+          bool NT = true>
+__global__ __launch_bounds__(kBlock + kWave) void scan_overlap_kernel(ScanParams p, Status st, Status st1) {
+    using C = typename Status::C;
+    constexpr int kWaveElems = kWave * 4 * STEPS;
+    constexpr int kTileElems = kWaves * kWaveElems;
+    __shared__ T s_wave_tot[kWaves];
+    __shared__ C s_excl;
+    __shared__ uint32_t s_ready;
+
+    const uint64_t tile = blockIdx.x;
+    const uint64_t line = tile / p.tiles_per_line;
+    const uint64_t tin = tile - line * p.tiles_per_line;
+    const int w = threadIdx.x / kWave;
+    const int lane = lane_id();
+    const T ident = Op::template identity<T>();
+    if (threadIdx.x == 0) s_ready = 0u;
+    __syncthreads();
+
+    T x[STEPS][4];
+    const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+    if (w < kWaves) {
+        const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j)
+            load4<T, VEC, REV, NT>(p, (const T *)p.in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
+        T carry = ident;
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            const T p0 = x[j][0];
+            const T p1 = Op::combine(p0, x[j][1]);
+            const T p2 = Op::combine(p1, x[j][2]);
+            const T p3 = Op::combine(p2, x[j][3]);
+            const T incl = wave_inclusive_scan<Op, T>(p3);
+            T lex = __shfl_up(incl, 1, kWave);
+            if (lane == 0) lex = ident;
+            const T base = Op::combine(carry, lex);
+            if constexpr (EXCL) {
+                x[j][0] = base;
+                x[j][1] = Op::combine(base, p0);
+                x[j][2] = Op::combine(base, p1);
+                x[j][3] = Op::combine(base, p2);
+            } else {
+                x[j][0] = Op::combine(base, p0);
+                x[j][1] = Op::combine(base, p1);
+                x[j][2] = Op::combine(base, p2);
+                x[j][3] = Op::combine(base, p3);
+            }
+            carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
+        }
+        if (lane == 0) {
+            s_wave_tot[w] = carry;
+            __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    } else {
+        PostedAgg<T, Op, Status> hook{&st, &s_ready, s_wave_tot, tile, p.tag};
+        C excl = Op::template identity<C>();
+        if (tin > 0) excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
+        const C incl = Op::combine(excl, hook.value());
+        if (lane == 0) {
+            st.publish(tile, p.tag, kPrefix, incl);
+            if (tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
+                st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, incl);
+            s_excl = excl;
+        }
+    }
+    __syncthreads();
+    if (w < kWaves) {
+        T wave_excl = ident;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q)
+            if (q < w) wave_excl = Op::combine(wave_excl, s_wave_tot[q]);
+        const C tile_excl = s_excl;
+        const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
+        T *out = (T *)p.out;
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+            T r[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][c]));
+            if constexpr (VEC) {
+                if (e + 3 < p.len) {
+                    using V = typename Vec4<T>::type;
+                    V v;
+                    v.x = r[0];
+                    v.y = r[1];
+                    v.z = r[2];
+                    v.w = r[3];
+                    store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
+                    continue;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint64_t i = e + c;
+                const uint64_t li = REV ? (p.len - 1 - i) : i;
+                if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
+            }
         }
     }
 }
@@ -295,24 +730,20 @@ __global__ __launch_bounds__(kBlock) void scan_lines_serial_kernel(ScanParams p)
     }
 }
 
-uint64_t status_bytes(uint64_t tiles, bool f64) {
-    if (!f64) return tiles * 8;
-    const uint64_t flag_bytes = (tiles * 4 + 7) & ~7ull;
-    return flag_bytes + 2 * tiles * 8;
-}
+// One 64-bit word per entry (packed u32), four per entry (split f64).
+uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 32 : 8); }
 
 template <typename T, typename Op, typename Status, bool EXCL>
-hx_status launch_tiles(const ScanParams &p, const Status &st, bool vec, bool rev, hipStream_t stream) {
+hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
+                       hipStream_t stream) {
     const dim3 grid((uint32_t)p.total_tiles), block(kBlock);
     if (vec)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false>), grid, block, 0,
-                           stream, p, st);
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false>), grid, block, 0, stream, p, st, st1);
     else if (rev)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true>), grid, block, 0,
-                           stream, p, st);
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true>), grid, block, 0, stream, p, st, st1);
     else
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false>), grid, block, 0,
-                           stream, p, st);
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false>), grid, block, 0, stream, p, st,
+                           st1);
     return check_launch("scan_tiles_kernel");
 }
 
@@ -321,11 +752,11 @@ hx_status launch_serial(const ScanParams &p, bool rev, hipStream_t stream) {
     uint64_t blocks = ceil_div(p.lines, kBlock);
     if (blocks > (1u << 20)) blocks = 1u << 20;
     if (rev)
-        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, true>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
+        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, true>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           stream, p);
     else
-        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, false>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
+        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, false>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           stream, p);
     return check_launch("scan_lines_serial_kernel");
 }
 
@@ -336,8 +767,15 @@ bool serial_mode(const ScanArgs &a) {
     return !contiguous && adjacent && a.lines >= 256;
 }
 
+uint64_t scan_bytes(const ScanArgs &a) {
+    if (serial_mode(a)) return kWorkspaceHeader;
+    const uint64_t tpl = ceil_div(a.len, kTile);
+    const bool f64 = a.dtype == HX_DTYPE_F32;
+    return kLookbackOffset + status_bytes(tpl * a.lines, f64) + status_bytes(ceil_div(tpl, kSuper) * a.lines, f64);
+}
+
 template <typename T, typename Op>
-hx_status launch_op(const ScanArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     ScanParams p{};
     p.in = a.in;
     p.out = a.out;
@@ -345,63 +783,62 @@ hx_status launch_op(const ScanArgs &a, void *ws, hipStream_t stream) {
     p.len = a.len;
     p.tiles_per_line = ceil_div(a.len, kTile);
     p.total_tiles = p.tiles_per_line * a.lines;
+    p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);
     p.in_line_stride = a.in_line_stride;
     p.in_elem_stride = a.in_elem_stride;
     p.out_line_stride = a.out_line_stride;
     p.out_elem_stride = a.out_elem_stride;
     p.in_offset = a.in_offset;
     p.out_offset = a.out_offset;
-    p.hdr = (WorkspaceHeader *)ws;
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
     if (serial_mode(a)) {
         return a.exclusive ? launch_serial<T, Op, true>(p, a.reverse, stream)
                            : launch_serial<T, Op, false>(p, a.reverse, stream);
     }
-    if (p.total_tiles >= 0xFFFFFFFFull)
-        return fail(HX_ERR_DISPATCH_FAILED, "scan of %llu tiles exceeds the u32 ticket range",
+    if (p.total_tiles > 0x7FFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "scan of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
+    if (ws_bytes < scan_bytes(a))
+        return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
+    HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
     const uintptr_t ibase = (uintptr_t)((const T *)a.in + a.in_offset);
     const uintptr_t obase = (uintptr_t)((T *)a.out + a.out_offset);
-    const bool vec = contiguous && !a.reverse && ibase % 16 == 0 && obase % 16 == 0 &&
-                     a.in_line_stride % 4 == 0 && a.out_line_stride % 4 == 0;
-    char *area = (char *)ws + kLookbackOffset;
+    const bool vec = contiguous && !a.reverse && ibase % 16 == 0 && obase % 16 == 0 && a.in_line_stride % 4 == 0 &&
+                     a.out_line_stride % 4 == 0;
+    const bool f64 = std::is_same<T, float>::value;
+    uint64_t *level0 = (uint64_t *)((char *)ws + kLookbackOffset);
+    uint64_t *level1 = (uint64_t *)((char *)level0 + status_bytes(p.total_tiles, f64));
+    hx_status s;
     if constexpr (std::is_same<T, float>::value) {
-        F64Status st;
-        st.flags = (uint32_t *)area;
-        st.agg = (double *)(area + ((p.total_tiles * 4 + 7) & ~7ull));
-        st.incl = st.agg + p.total_tiles;
-        return a.exclusive ? launch_tiles<T, Op, F64Status, true>(p, st, vec, a.reverse, stream)
-                           : launch_tiles<T, Op, F64Status, false>(p, st, vec, a.reverse, stream);
+        F64Status st{level0}, st1{level1};
+        s = a.exclusive ? launch_tiles<T, Op, F64Status, true>(p, st, st1, vec, a.reverse, stream)
+                        : launch_tiles<T, Op, F64Status, false>(p, st, st1, vec, a.reverse, stream);
     } else {
-        PackedStatus st;
-        st.words = (uint64_t *)area;
-        return a.exclusive ? launch_tiles<T, Op, PackedStatus, true>(p, st, vec, a.reverse, stream)
-                           : launch_tiles<T, Op, PackedStatus, false>(p, st, vec, a.reverse, stream);
+        PackedStatus st{level0}, st1{level1};
+        s = a.exclusive ? launch_tiles<T, Op, PackedStatus, true>(p, st, st1, vec, a.reverse, stream)
+                        : launch_tiles<T, Op, PackedStatus, false>(p, st, st1, vec, a.reverse, stream);
     }
+    if (s == HX_OK) commit_lookback_launch(lb);
+    return s;
 }
 
 } // namespace
 
-uint64_t scan_workspace_bytes(const ScanArgs &a, int *format) {
-    const bool f64 = a.dtype == HX_DTYPE_F32;
-    *format = f64 ? kWsLookbackF64 : kWsLookbackPacked;
-    if (serial_mode(a)) return kWorkspaceHeader;
-    const uint64_t tiles = ceil_div(a.len, kTile) * a.lines;
-    return kLookbackOffset + status_bytes(tiles, f64);
-}
+uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
-hx_status launch_scan(const ScanArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_scan(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     const bool prod = a.op == HX_OP_PROD;
     switch (a.dtype) {
     case HX_DTYPE_F32:
-        return prod ? launch_op<float, OpProd>(a, ws, stream) : launch_op<float, OpSum>(a, ws, stream);
+        return prod ? launch_op<float, OpProd>(a, ws, ws_bytes, lb, stream)
+                    : launch_op<float, OpSum>(a, ws, ws_bytes, lb, stream);
     case HX_DTYPE_U32:
     case HX_DTYPE_I32:
         // Two's complement: i32 sums and products have the bits of u32 ones.
-        return prod ? launch_op<uint32_t, OpProd>(a, ws, stream)
-                    : launch_op<uint32_t, OpSum>(a, ws, stream);
+        return prod ? launch_op<uint32_t, OpProd>(a, ws, ws_bytes, lb, stream)
+                    : launch_op<uint32_t, OpSum>(a, ws, ws_bytes, lb, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown dtype %d", (int)a.dtype);
 }

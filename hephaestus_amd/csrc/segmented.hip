@@ -9,7 +9,7 @@
 // apart.  Here the work is cut by ELEMENTS, not by segments, so every block
 // streams the same 16 KiB with 16-byte loads whatever the segment lengths:
 //
-//   * a block takes a virtual tile ticket and loads 4096 values, wave-striped
+//   * block b takes tile b (no ticket counter) and loads 4096 values, wave-striped
 //     like the scan;
 //   * while those loads are in flight, three waves run 64-ary searches over
 //     the offsets for the segment boundaries the tile touches;
@@ -31,11 +31,8 @@ constexpr int kWaves = kBlock / kWave;
 constexpr int kSteps = 4;
 constexpr int kWaveElems = kWave * 4 * kSteps; // 1024
 constexpr int kTile = kWaves * kWaveElems;     // 4096
-constexpr uint64_t kLookbackOffset = 256 + 64 * 1024;
-
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
-
-__device__ __forceinline__ uint32_t epoch_tag(uint32_t epoch) { return (epoch % 0x3FFFFFFFu) + 1u; }
+constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor
 
 struct SegParams {
     const uint32_t *values;
@@ -46,6 +43,7 @@ struct SegParams {
     uint64_t total_tiles;
     WorkspaceHeader *hdr;
     uint64_t *status;
+    uint32_t tag;         // this launch's status tag
 };
 
 // Offsets clamped into [0, n]: malformed offsets can never address values
@@ -81,20 +79,44 @@ __device__ uint64_t wave_upper_bound(const SegParams &p, uint64_t v) {
     return lo;
 }
 
+__device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
+    return ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v;
+}
+
+// The status tile u's owner publishes, computed by ONE wave (fallback path):
+// a prefix (the sum from the last segment start in the tile to its end) when
+// the tile holds a segment start, else an aggregate (the tile total).
+__device__ void seg_tile_status(const SegParams &p, uint64_t u, uint32_t &flag, uint32_t &value) {
+    const uint64_t t0 = u * kTile;
+    const uint64_t t1 = (t0 + kTile < p.n) ? t0 + kTile : p.n;
+    const uint64_t k_star = wave_upper_bound(p, t1 - 1);
+    uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
+    if (h > t1 - 1) h = t1 - 1;
+    const bool has_head = h >= t0;
+    uint32_t s = 0;
+    for (uint64_t i = (has_head ? h : t0) + lane_id(); i < t1; i += kWave) s += p.values[i];
+    value = wave_sum(s);
+    flag = has_head ? kPrefix : kAggregate;
+}
+
+// Fallback publication: never overwrites a word of this launch.
+__device__ __forceinline__ void publish_if_unset(uint64_t *word, uint32_t tag, uint32_t flag, uint32_t v) {
+    uint64_t cur = ld_relaxed(word);
+    if ((uint32_t)(cur >> 34) == tag) return;
+    __hip_atomic_compare_exchange_strong(word, &cur, status_word(tag, flag, v), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block b processes tile b; see scan.hip for why there is no ticket counter
+// and how the fallback guarantees progress in any dispatch order.
 __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
-    __shared__ uint32_t s_ticket, s_tag;
     __shared__ uint64_t s_bound[3];
     __shared__ uint32_t s_wave_tot[kWaves];
     __shared__ uint32_t s_carry;
     __shared__ uint32_t E[kTile + 1];
 
-    if (threadIdx.x == 0) {
-        s_ticket = fetch_add32(&p.hdr->tile_counter, 1u);
-        s_tag = epoch_tag(ld_relaxed32(&p.hdr->epoch));
-    }
-    __syncthreads();
-    const uint64_t tile = s_ticket;
-    const uint32_t tag = s_tag;
+    const uint64_t tile = blockIdx.x;
+    const uint32_t tag = p.tag;
     const int w = threadIdx.x / kWave;
     const int lane = lane_id();
     const uint64_t t0 = tile * kTile;
@@ -176,14 +198,9 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
         const bool needs_carry = tile > 0 && first_start < t0;
         uint32_t c_in = 0;
         if (has_head) {
-            const uint32_t out_val = total - E[h - t0];
-            if (lane == 0) {
-                const uint64_t word = ((uint64_t)((tag << 2) | kPrefix) << 32) | out_val;
-                st_relaxed(&p.status[tile], word);
-            }
+            if (lane == 0) st_relaxed(&p.status[tile], status_word(tag, kPrefix, total - E[h - t0]));
         } else if (tile > 0 && lane == 0) {
-            const uint64_t word = ((uint64_t)((tag << 2) | kAggregate) << 32) | total;
-            st_relaxed(&p.status[tile], word);
+            st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
         }
         if (needs_carry || (!has_head && tile > 0)) {
             // Look back over predecessors until a prefix (a tile holding a
@@ -191,8 +208,11 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
             int64_t pred = (int64_t)tile - 1;
             for (;;) {
                 const int64_t idx = pred - lane;
-                uint32_t flag = kPrefix, val = 0;
+                uint32_t flag, val;
+                uint32_t spins = 0;
                 for (;;) {
+                    flag = kPrefix;
+                    val = 0;
                     if (idx >= 0) {
                         const uint64_t wd = ld_relaxed(&p.status[idx]);
                         const uint32_t hi = (uint32_t)(wd >> 32);
@@ -202,7 +222,16 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
                     const uint64_t pm = ballot(flag == kPrefix);
                     const uint64_t im = ballot(flag == kInvalid);
                     const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
-                    if ((im & need) == 0ull) break;
+                    const uint64_t missing = im & need;
+                    if (missing == 0ull) break;
+                    if (++spins >= kSpinLimit) {
+                        const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
+                        uint32_t fflag, fval;
+                        seg_tile_status(p, u, fflag, fval);
+                        if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
+                        spins = 0;
+                        continue;
+                    }
                     __builtin_amdgcn_s_sleep(1);
                 }
                 const uint64_t pm = ballot(flag == kPrefix);
@@ -212,10 +241,7 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
                 pred -= kWave;
             }
         }
-        if (!has_head && tile > 0 && lane == 0) {
-            const uint64_t word = ((uint64_t)((tag << 2) | kPrefix) << 32) | (uint32_t)(c_in + total);
-            st_relaxed(&p.status[tile], word);
-        }
+        if (!has_head && tile > 0 && lane == 0) st_relaxed(&p.status[tile], status_word(tag, kPrefix, c_in + total));
         if (lane == 0) s_carry = c_in;
     }
     __syncthreads();
@@ -235,15 +261,6 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
         uint32_t v = E[b - t0] - E[a_loc];
         if (a < t0) v += c_in;
         p.out[k - 1] = v;
-    }
-
-    if (threadIdx.x == 0) {
-        const uint32_t d = fetch_add32_acqrel(&p.hdr->tile_done, 1u);
-        if (d == (uint32_t)(p.total_tiles - 1)) {
-            st_relaxed32(&p.hdr->tile_counter, 0u);
-            st_relaxed32(&p.hdr->tile_done, 0u);
-            st_relaxed32(&p.hdr->epoch, ld_relaxed32(&p.hdr->epoch) + 1u);
-        }
     }
 }
 
@@ -267,12 +284,12 @@ __global__ void validate_offsets_kernel(const uint32_t *offsets, uint64_t count,
 
 } // namespace
 
-uint64_t segmented_workspace_bytes(const SegmentedArgs &a, int *format) {
-    *format = kWsLookbackPacked;
+uint64_t segmented_workspace_bytes(const SegmentedArgs &a) {
     return kLookbackOffset + ceil_div(a.n, kTile) * 8;
 }
 
-hx_status launch_segmented(const SegmentedArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb,
+                           hipStream_t stream) {
     if (a.num_segments == 0) return HX_OK;
     if (a.n == 0) {
         uint64_t blocks = ceil_div(a.num_segments, kBlock);
@@ -290,13 +307,19 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, hipStream_t stream)
     p.total_tiles = ceil_div(a.n, kTile);
     p.hdr = (WorkspaceHeader *)ws;
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
-    if (p.total_tiles >= 0xFFFFFFFFull)
-        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the u32 ticket range",
+    if (p.total_tiles >= 0x80000000ull)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
     if (((uintptr_t)a.values) % 16 != 0)
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 16-byte aligned");
+    if (ws_bytes < segmented_workspace_bytes(a))
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
+                    (unsigned long long)ws_bytes);
+    HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     hipLaunchKernelGGL(segmented_sum_kernel, dim3((uint32_t)p.total_tiles), dim3(kBlock), 0, stream, p);
-    return check_launch("segmented_sum_kernel");
+    HX_TRY(check_launch("segmented_sum_kernel"));
+    commit_lookback_launch(lb);
+    return HX_OK;
 }
 
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets, uint64_t count,
