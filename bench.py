@@ -30,7 +30,11 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30")
+WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32")
+# Dominant kernel of each workload (substring of its name in rocprofv3 output).
+KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
+             "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
+             "copy_u32": "copy_vec_kernel"}
 
 
 def log(msg: str) -> None:
@@ -138,6 +142,73 @@ def bench_scan_f32_2_30(hx, dev, args):
     return {"n": n, "ms": ms, "bytes": 8 * n}
 
 
+def bench_copy_u32(hx, dev, args):
+    """The device copy kernel behind copy_buffer over 2^28 u32: the yardstick
+    (read B + write B) for the HBM byte counters, and the streaming ceiling."""
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.uint32, n)
+    dev.fill_uniform_int(x, seed=7, lo=0, hi=255)
+    y = dev.alloc_uninitialized(np.uint32, n)
+    ms = time_plan(dev, lambda: dev.copy_buffer(x, y), args.steps, args.warmup)
+    return {"n": n, "ms": ms, "bytes": 8 * n}
+
+
+def _counter_csv(path: Path) -> dict:
+    """{kernel name: [per-dispatch values]} from one rocprofv3 --pmc run (CSV)."""
+    import csv
+
+    files = sorted(path.rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {path}")
+    out: dict = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def pmc_summary(root: Path) -> int:
+    """Turn rocprofv3 --pmc runs into profiles/pmc_traffic.json.
+
+    Expects root/<workload>/fetch and root/<workload>/write, each the output
+    directory of `rocprofv3 --pmc FETCH_SIZE` (resp. WRITE_SIZE) over
+    `bench.py --workload <workload>`.  Counters are KiB per dispatch; each
+    is scaled by the factor that maps the copy kernel's reading to its known
+    traffic (read 4n, write 4n bytes)."""
+    import statistics
+
+    raw = {}
+    for w in WORKLOADS:
+        if not (root / w).exists():
+            continue
+        entry = {}
+        for which in ("fetch", "write"):
+            rows = _counter_csv(root / w / which)
+            vals = [v for k, vs in rows.items() if KERNEL_OF[w] in k for v in vs]
+            if not vals:
+                raise SystemExit(f"{w}/{which}: no dispatch of {KERNEL_OF[w]}")
+            entry[which + "_kib"] = statistics.median(vals)
+            entry["dispatches"] = len(vals)
+        raw[w] = entry
+    if "copy_u32" not in raw:
+        raise SystemExit("copy_u32 calibration run missing")
+    copy_bytes = 4 * (1 << 28)
+    f_fetch = copy_bytes / (raw["copy_u32"]["fetch_kib"] * 1024)
+    f_write = copy_bytes / (raw["copy_u32"]["write_kib"] * 1024)
+    out = {"_calibration": {"kernel": "copy_vec_kernel, 2^28 u32 (read 1 GiB, write 1 GiB)",
+                            "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)}}
+    for w, e in raw.items():
+        fetch = e["fetch_kib"] * 1024 * f_fetch
+        write = e["write_kib"] * 1024 * f_write
+        out[w] = {"kernel": KERNEL_OF[w], "fetch_kib": e["fetch_kib"], "write_kib": e["write_kib"],
+                  "dispatches": e["dispatches"], "hbm_bytes_per_launch": round(fetch + write)}
+    dst = REPO / "profiles" / "pmc_traffic.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 def cpu_baseline(dev, scan, seconds: float) -> dict:
     """Time the oracle's sequential exclusive scan on this host's cores over
     the same 2^28-element input; verify the GPU output against it."""
@@ -181,7 +252,10 @@ def main() -> int:
     ap.add_argument("--workload", choices=("default", "all") + WORKLOADS, default="default")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc runs under DIR and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        return pmc_summary(Path(args.pmc_summary))
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -226,22 +300,23 @@ def main() -> int:
         "config": {"workload": "u32 exclusive prefix scan, n=2^28 (BASELINE configs[1])",
                    "n": scan["n"], "algorithmic_bytes_per_step": scan["bytes"],
                    "elements_per_s": round(scan["n"] / (scan["ms"] * 1e-3), 1)},
-        "roofline": roofline(scan["bytes"], scan["ms"], "scan_u32_2_28"),
+        "roofline": roofline(scan["bytes"], scan["ms"], "scan_u32"),
         "secondary": {
             "f32_sum_reduce_2_28": {
                 "value": round(ssum["bytes"] / (ssum["ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
                 "ms_per_launch": round(ssum["ms"], 5),
                 "elements_per_s": round(ssum["n"] / (ssum["ms"] * 1e-3), 1),
-                "roofline": roofline(ssum["bytes"], ssum["ms"], "sum_f32_2_28"),
+                "roofline": roofline(ssum["bytes"], ssum["ms"], "sum_f32"),
             }
         },
     }
     if args.workload == "all":
-        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30"):
+        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
             line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
-                                       "frac": round(gbs / PEAK_GBS, 4)}
+                                       "elements_per_s": round(r["n"] / (r["ms"] * 1e-3), 1),
+                                       "roofline": roofline(r["bytes"], r["ms"], name)}
             log(f"{name}: {r['ms']:.4f} ms/launch {gbs:.1f} GB/s")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dev, scan, args.cpu_seconds)

@@ -26,6 +26,7 @@ SOURCES = [
     "csrc/scan.hip",
     "csrc/segmented.hip",
     "csrc/random.hip",
+    "csrc/copy.hip",
 ]
 HEADERS = ["csrc/hx_device.hpp", "csrc/hx_internal.hpp"]
 ARCH = "gfx950"

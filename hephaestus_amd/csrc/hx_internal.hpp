@@ -179,6 +179,9 @@ hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_byte
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,
                                      uint64_t num_offsets, uint64_t n);
 
+// Stream-ordered device-to-device copy of `bytes` bytes (a streaming kernel).
+hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t stream);
+
 hx_status launch_fill_random(void *dst, uint64_t n, hx_dtype dtype,
                              hx_distribution dist, uint64_t seed, double p0,
                              double p1, hipStream_t stream);

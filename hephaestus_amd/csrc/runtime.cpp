@@ -444,8 +444,7 @@ hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len, void *dst,
     HX_TRY(bind_device(dev));
     uint64_t bytes = src_len * elem_size;
     if (bytes == 0) return ok();
-    HX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream),
-           HX_ERR_TRANSFER_FAILED, "hipMemcpyAsync D2D");
+    HX_TRY(launch_copy(src, dst, bytes, dev->stream));
     HX_HIP(hipStreamSynchronize(dev->stream), HX_ERR_TRANSFER_FAILED, "D2D synchronize");
     return ok();
 }

@@ -190,9 +190,12 @@ __device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
     return agg;
 }
 
-// Hooks let a look-back do other work while it spins.  KnownAgg: the
-// tile's aggregate is already published.  (The overlapped kernel's hook
-// publishes it from inside the spin loop as soon as the data waves post it.)
+// The look-back reaches the tile's own aggregate through a hook: poll() runs
+// on every spin, agg() yields the aggregate.  KnownAgg: the aggregate is
+// already computed and published when the look-back starts.  (A variant
+// whose fifth wave starts looking back while the data waves still load, and
+// publishes the aggregate from poll(), measured 19% slower at 2^28 u32: the
+// extra wave's registers cut occupancy and its polls span the whole load.)
 template <typename C> struct KnownAgg {
     C a;
     __device__ __forceinline__ void poll() {}
@@ -415,290 +418,6 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
             const uint64_t i = e + c;
             const uint64_t li = REV ? (p.len - 1 - i) : i;
             if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
-        }
-    }
-}
-
-// Streaming form: a persistent grid of G blocks, block b scanning tiles
-// b, b+G, b+2G, ...  Waves 0-3 move data; wave 4 only publishes and looks
-// back.  While wave 4 resolves tile k's prefix, the data waves already have
-// tile k+1's loads in flight, so the look-back latency overlaps HBM traffic
-// instead of adding to every tile's lifetime.  (vmcnt is per wave, so
-// wave 4's polls never queue behind the data loads.)  LDS slots are double
-// buffered by tile parity so one barrier pair per tile suffices.
-template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
-          bool NT = true>
-__global__ __launch_bounds__(kBlock + kWave) void scan_stream_kernel(ScanParams p, Status st, Status st1) {
-    using C = typename Status::C;
-    constexpr int kWaveElems = kWave * 4 * STEPS;
-    constexpr int kTileElems = kWaves * kWaveElems;
-    __shared__ T s_wave_tot[2][kWaves];
-    __shared__ C s_excl[2];
-
-    const int w = threadIdx.x / kWave;
-    const int lane = lane_id();
-    const bool data = w < kWaves;
-    const T ident = Op::template identity<T>();
-    const uint64_t G = gridDim.x;
-    T *out = (T *)p.out;
-
-    T a[STEPS][4], b[STEPS][4];
-    uint64_t tile = blockIdx.x;
-    auto load_tile = [&](uint64_t t, T (&x)[STEPS][4]) {
-        const uint64_t line = t / p.tiles_per_line;
-        const uint64_t tin = t - line * p.tiles_per_line;
-        const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
-        const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
-#pragma unroll
-        for (int j = 0; j < STEPS; ++j)
-            load4<T, VEC, REV, NT>(p, (const T *)p.in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
-    };
-    if (data && tile < p.total_tiles) load_tile(tile, a);
-
-    for (int k = 0; tile < p.total_tiles; ++k, tile += G) {
-        const int slot = k & 1;
-        const uint64_t line = tile / p.tiles_per_line;
-        const uint64_t tin = tile - line * p.tiles_per_line;
-        if (data) {
-            // In-register scan of this wave's part, as in scan_tiles_kernel.
-            T carry = ident;
-#pragma unroll
-            for (int j = 0; j < STEPS; ++j) {
-                const T p0 = a[j][0];
-                const T p1 = Op::combine(p0, a[j][1]);
-                const T p2 = Op::combine(p1, a[j][2]);
-                const T p3 = Op::combine(p2, a[j][3]);
-                const T incl = wave_inclusive_scan<Op, T>(p3);
-                T lex = __shfl_up(incl, 1, kWave);
-                if (lane == 0) lex = ident;
-                const T base = Op::combine(carry, lex);
-                if constexpr (EXCL) {
-                    a[j][0] = base;
-                    a[j][1] = Op::combine(base, p0);
-                    a[j][2] = Op::combine(base, p1);
-                    a[j][3] = Op::combine(base, p2);
-                } else {
-                    a[j][0] = Op::combine(base, p0);
-                    a[j][1] = Op::combine(base, p1);
-                    a[j][2] = Op::combine(base, p2);
-                    a[j][3] = Op::combine(base, p3);
-                }
-                carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
-            }
-            if (lane == 0) s_wave_tot[slot][w] = carry;
-        }
-        __syncthreads();
-        if (data) {
-            if (tile + G < p.total_tiles) load_tile(tile + G, b); // prefetch
-        } else {
-            T tile_agg = ident;
-#pragma unroll
-            for (int q = 0; q < kWaves; ++q) tile_agg = Op::combine(tile_agg, s_wave_tot[slot][q]);
-            const C agg = (C)tile_agg;
-            C excl = Op::template identity<C>();
-            if (tin == 0) {
-                if (lane == 0) st.publish(tile, p.tag, kPrefix, agg);
-            } else {
-                if (lane == 0) st.publish(tile, p.tag, kAggregate, agg);
-                KnownAgg<C> hook{agg};
-            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
-                if (lane == 0) st.publish(tile, p.tag, kPrefix, Op::combine(excl, agg));
-            }
-            if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
-                st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, Op::combine(excl, agg));
-            if (lane == 0) s_excl[slot] = excl;
-        }
-        __syncthreads();
-        if (data) {
-            T wave_excl = ident;
-#pragma unroll
-            for (int q = 0; q < kWaves; ++q)
-                if (q < w) wave_excl = Op::combine(wave_excl, s_wave_tot[slot][q]);
-            const C tile_excl = s_excl[slot];
-            const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
-            const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
-#pragma unroll
-            for (int j = 0; j < STEPS; ++j) {
-                const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
-                T r[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, a[j][c]));
-                bool done = false;
-                if constexpr (VEC) {
-                    if (e + 3 < p.len) {
-                        using V = typename Vec4<T>::type;
-                        V v;
-                        v.x = r[0];
-                        v.y = r[1];
-                        v.z = r[2];
-                        v.w = r[3];
-                        store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
-                        done = true;
-                    }
-                }
-                if (!done) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const uint64_t i = e + c;
-                        const uint64_t li = REV ? (p.len - 1 - i) : i;
-                        if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < STEPS; ++j)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) a[j][c] = b[j][c];
-        }
-    }
-}
-
-// Overlapped form: one tile per block as in scan_tiles_kernel, plus a fifth
-// wave that only looks back.  It starts polling its predecessors' statuses
-// as soon as the block starts, while waves 0-3 are still loading, and
-// publishes the tile aggregate from inside its spin loop the moment the data
-// waves post their totals (an LDS counter).  A tile's lifetime becomes
-// max(load + scan, look-back) + store instead of their sum.
-template <typename T, typename Op, typename Status> struct PostedAgg {
-    using C = typename Status::C;
-    const Status *st;
-    uint32_t *ready;    // LDS: data waves that have posted their totals
-    const T *wave_tot;  // LDS: the data waves' totals
-    uint64_t tile;
-    uint32_t tag;
-    bool have = false;
-    bool published = false;
-    C a{};
-    __device__ __forceinline__ bool fetch() {
-        if (have) return true;
-        const uint32_t r = __hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (__builtin_amdgcn_readfirstlane(r) < (uint32_t)kWaves) return false;
-        T t = Op::template identity<T>(); // same fold order as scan_tiles_kernel
-#pragma unroll
-        for (int q = 0; q < kWaves; ++q) t = Op::combine(t, wave_tot[q]);
-        a = (C)t;
-        have = true;
-        return true;
-    }
-    // Called while spinning: publish the aggregate once it exists.
-    __device__ __forceinline__ void poll() {
-        if (!published && fetch()) {
-            if (lane_id() == 0) st->publish(tile, tag, kAggregate, a);
-            published = true;
-        }
-    }
-    // The aggregate, still mid-look-back: wait for it and publish it.
-    __device__ __forceinline__ C agg() {
-        while (!fetch()) __builtin_amdgcn_s_sleep(1);
-        poll();
-        return a;
-    }
-    // The aggregate after the look-back: no need to publish it any more.
-    __device__ __forceinline__ C value() {
-        while (!fetch()) __builtin_amdgcn_s_sleep(1);
-        return a;
-    }
-};
-
-template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
-          bool NT = true>
-__global__ __launch_bounds__(kBlock + kWave) void scan_overlap_kernel(ScanParams p, Status st, Status st1) {
-    using C = typename Status::C;
-    constexpr int kWaveElems = kWave * 4 * STEPS;
-    constexpr int kTileElems = kWaves * kWaveElems;
-    __shared__ T s_wave_tot[kWaves];
-    __shared__ C s_excl;
-    __shared__ uint32_t s_ready;
-
-    const uint64_t tile = blockIdx.x;
-    const uint64_t line = tile / p.tiles_per_line;
-    const uint64_t tin = tile - line * p.tiles_per_line;
-    const int w = threadIdx.x / kWave;
-    const int lane = lane_id();
-    const T ident = Op::template identity<T>();
-    if (threadIdx.x == 0) s_ready = 0u;
-    __syncthreads();
-
-    T x[STEPS][4];
-    const uint64_t e0 = tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
-    if (w < kWaves) {
-        const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
-#pragma unroll
-        for (int j = 0; j < STEPS; ++j)
-            load4<T, VEC, REV, NT>(p, (const T *)p.in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
-        T carry = ident;
-#pragma unroll
-        for (int j = 0; j < STEPS; ++j) {
-            const T p0 = x[j][0];
-            const T p1 = Op::combine(p0, x[j][1]);
-            const T p2 = Op::combine(p1, x[j][2]);
-            const T p3 = Op::combine(p2, x[j][3]);
-            const T incl = wave_inclusive_scan<Op, T>(p3);
-            T lex = __shfl_up(incl, 1, kWave);
-            if (lane == 0) lex = ident;
-            const T base = Op::combine(carry, lex);
-            if constexpr (EXCL) {
-                x[j][0] = base;
-                x[j][1] = Op::combine(base, p0);
-                x[j][2] = Op::combine(base, p1);
-                x[j][3] = Op::combine(base, p2);
-            } else {
-                x[j][0] = Op::combine(base, p0);
-                x[j][1] = Op::combine(base, p1);
-                x[j][2] = Op::combine(base, p2);
-                x[j][3] = Op::combine(base, p3);
-            }
-            carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
-        }
-        if (lane == 0) {
-            s_wave_tot[w] = carry;
-            __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-    } else {
-        PostedAgg<T, Op, Status> hook{&st, &s_ready, s_wave_tot, tile, p.tag};
-        C excl = Op::template identity<C>();
-        if (tin > 0) excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
-        const C incl = Op::combine(excl, hook.value());
-        if (lane == 0) {
-            st.publish(tile, p.tag, kPrefix, incl);
-            if (tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
-                st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, incl);
-            s_excl = excl;
-        }
-    }
-    __syncthreads();
-    if (w < kWaves) {
-        T wave_excl = ident;
-#pragma unroll
-        for (int q = 0; q < kWaves; ++q)
-            if (q < w) wave_excl = Op::combine(wave_excl, s_wave_tot[q]);
-        const C tile_excl = s_excl;
-        const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
-        T *out = (T *)p.out;
-#pragma unroll
-        for (int j = 0; j < STEPS; ++j) {
-            const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
-            T r[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][c]));
-            if constexpr (VEC) {
-                if (e + 3 < p.len) {
-                    using V = typename Vec4<T>::type;
-                    V v;
-                    v.x = r[0];
-                    v.y = r[1];
-                    v.z = r[2];
-                    v.w = r[3];
-                    store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
-                    continue;
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint64_t i = e + c;
-                const uint64_t li = REV ? (p.len - 1 - i) : i;
-                if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
-            }
         }
     }
 }

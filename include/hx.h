@@ -173,7 +173,8 @@ hx_status hx_write_sub(hx_device *dev, void *dst, uint64_t dst_len,
 hx_status hx_download(hx_device *dev, const void *src, uint64_t src_len,
                       void *dst, uint64_t dst_len, uint32_t elem_size);
 /* copy_buffer (core device.rs:197-211): device-local, complete on return;
- * src == dst is a no-op (host lib.rs:174-183). */
+ * src == dst is a no-op (host lib.rs:174-183); otherwise the two ranges must
+ * not overlap (distinct buffers, as the reference's &src / &mut dst). */
 hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len,
                   void *dst, uint64_t dst_len, uint32_t elem_size);
 
