@@ -1,9 +1,9 @@
 #!/usr/bin/env python3
 """Throughput of the reduction / scan hot path on one MI355X.
 
-Metric (BASELINE.json): achieved HBM GB/s (and fraction of the 8 TB/s peak)
+Metric: achieved HBM GB/s (and fraction of the 8 TB/s peak)
 for the u32 exclusive scan and the f32 sum-reduce at 2^28 elements.  A step
-is one exclusive scan of the 2^28-element u32 operand; inputs
+is one exclusive scan of the 2^28-element u32 operand (the headline configuration); inputs
 are generated in HBM before timing, and every step is one launch of the
 single-pass look-back scan kernel.  The f32 sum-reduce at 2^28 is timed the
 same way and reported under "secondary".
@@ -297,7 +297,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "u32",
         "data": "synthetic (SplitMix64 seed 2, uniform integers in [0,256), generated in HBM)",
-        "config": {"workload": "u32 exclusive prefix scan, n=2^28 (BASELINE configs[1])",
+        "config": {"workload": "u32 exclusive prefix scan, n=2^28 (the headline configuration)",
                    "n": scan["n"], "algorithmic_bytes_per_step": scan["bytes"],
                    "elements_per_s": round(scan["n"] / (scan["ms"] * 1e-3), 1)},
         "roofline": roofline(scan["bytes"], scan["ms"], "scan_u32"),

@@ -1,7 +1,7 @@
 // Row-wise and axis reductions for gfx950: AxisReductionOps
 // (crates/hephaestus-core/src/domain/reduction.rs:74-223) plus the fused
-// row reduce of the north star (sum, max and argmax of y = fmaf(a, x, b)
-// out of ONE read of each row).
+// row reduce: sum, max and argmax of y = fmaf(a, x, b) out of ONE read of
+// each row.
 //
 // The reference runs one thread per output with a serial loop along the
 // axis (crates/hephaestus-rocm/src/application/axis_reduction.rs:16-65): for

@@ -1,4 +1,4 @@
-// Segmented sum for gfx950 (north-star config 4).  Offsets follow the CSR
+// Segmented sum for gfx950.  Offsets follow the CSR
 // row_ptr convention (crates/hephaestus-core/src/domain/sparse.rs:179-220):
 // S+1 entries, offsets[0] = 0, offsets[S] = n, non-decreasing, and
 //   out[s] = sum of values[offsets[s] .. offsets[s+1])   (mod 2^32).

@@ -7,7 +7,7 @@ against them reads the same:
 * `RocmAxisReductionOps`  AxisReductionOps  (core reduction.rs:74-223)
 * `RocmScanOps`           ScanOps           (core scan.rs:197-264)
 
-plus the north-star operations the reference does not have: full and row
+plus operations the reference does not have: full and row
 argmax, the fused row reduce with the `y = fmaf(a, x, b)` prologue,
 exclusive scans and the segmented sum.  Operators are passed as the marker
 classes below instead of type parameters.  Every call validates in the
@@ -252,7 +252,7 @@ class RocmScanOps:
     def dispatch_scan(self, device: RocmDevice, prepared: PreparedPlan, stream=None) -> None:
         prepared.dispatch(stream)
 
-    # Flat 1-D conveniences (the north-star configs).
+    # Flat 1-D conveniences.
     def exclusive_scan_into(self, device, input: RocmBuffer, output: RocmBuffer, stream=None):
         lay = Layout.c_contiguous([len(input)])
         self.scan_axis_into(device, CumSumOp, StridedView(input, lay), 0, ScanDirection.Forward,
@@ -267,7 +267,7 @@ class RocmScanOps:
 
 
 class RocmSegmentedReductionOps:
-    """Segmented sum over CSR-style offsets (north-star config 4)."""
+    """Segmented sum over CSR-style offsets."""
 
     def segmented_sum_into(self, device: RocmDevice, values: RocmBuffer, offsets: RocmBuffer,
                            output: RocmBuffer, stream=None) -> None:

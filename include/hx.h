@@ -58,8 +58,8 @@ typedef enum hx_dtype {
 
 /* Combining operators: crates/hephaestus-core/src/domain/ops.rs:735-803
  * (SumOp, ProdOp, MinOp, MaxOp) with identities ops.rs:926-983.  ARGMAX is
- * the north-star addition (index of the maximum, ties to the lowest index);
- * MEAN mirrors mean_axis_kernel (crates/hephaestus-rocm/src/application/
+ * an addition to the reference's operators (index of the maximum, ties to
+ * the lowest index); MEAN mirrors mean_axis_kernel (crates/hephaestus-rocm/src/application/
  * axis_reduction.rs:67-112). */
 typedef enum hx_op {
     HX_OP_SUM = 0,
@@ -72,7 +72,7 @@ typedef enum hx_op {
 
 typedef enum hx_scan_kind {
     HX_SCAN_INCLUSIVE = 0, /* reference form: core accelerator/scan.rs:56-155 */
-    HX_SCAN_EXCLUSIVE = 1  /* north-star addition: out[i] = fold(x[0..i))    */
+    HX_SCAN_EXCLUSIVE = 1  /* addition to the reference: out[i] = fold(x[0..i)) */
 } hx_scan_kind;
 
 /* crates/hephaestus-core/src/domain/scan.rs:36-43 (ScanDirection). */
@@ -218,7 +218,7 @@ hx_status hx_plan_axis_scan(const hx_layout *in, uint64_t in_buf_len,
                             int32_t buffers_alias, uint64_t *lines,
                             uint64_t *line_len);
 
-/* ----------------------------------------- FullReductionOps (a1-a3, a9) */
+/* ------------------------------------------------------ FullReductionOps */
 
 /* FullReductionOps::reduce_full_into (core reduction.rs:267-279;
  * ROCm impl crates/hephaestus-rocm/src/application/
@@ -233,7 +233,7 @@ hx_status hx_reduce_full(hx_device *dev, hx_op op, hx_dtype dtype,
                          uint64_t out_buf_len, const hx_layout *out_layout,
                          const hx_affine *prologue, hx_stream stream);
 
-/* Full argmax (north-star; no reference counterpart — SURVEY row a9): index
+/* Full argmax (no reference counterpart): index
  * of the maximum of the (prologue-mapped) view in logical row-major order,
  * ties to the lowest index, NaN elements ignored.  out_index (u32[1]) gets
  * the index (UINT32_MAX when there is no non-NaN element); out_value (T[1],
@@ -255,7 +255,7 @@ hx_status hx_prepare_reduce_full(hx_device *dev, hx_op op, hx_dtype dtype,
                                  const hx_layout *out_layout,
                                  const hx_affine *prologue, hx_plan **plan);
 
-/* ------------------------------------ AxisReductionOps (a5) + fused rows */
+/* ----------------------------------------- AxisReductionOps + fused rows */
 
 /* AxisReductionOps::reduce_axis_into / prod / min / max / mean_axis_into
  * (core reduction.rs:97-197): rank-2 input, `axis` collapsed to length 1 in
@@ -273,9 +273,9 @@ hx_status hx_prepare_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype,
                                  void *out, uint64_t out_buf_len,
                                  const hx_layout *out_layout, hx_plan **plan);
 
-/* Fused row-wise reduce (north-star config 3): for each of `rows` rows of
- * `cols` elements (row r starts at in + offset + r*row_stride, unit column
- * stride), ONE read computes any of
+/* Fused row-wise reduce (no single reference counterpart): for each of
+ * `rows` rows of `cols` elements (row r starts at in + offset +
+ * r*row_stride, unit column stride), ONE read computes any of
  *   out_sum[r]    = sum of y          (T; f32 accumulates in f64)
  *   out_max[r]    = MaxOp fold of y   (T)
  *   out_argmax[r] = lowest index of the max of y (u32; UINT32_MAX if none)
@@ -289,7 +289,7 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in,
                          void *out_max, uint32_t *out_argmax,
                          uint64_t out_len, hx_stream stream);
 
-/* ------------------------------------------------------- ScanOps (a6, a10) */
+/* ---------------------------------------------------------------- ScanOps */
 
 /* ScanOps::scan_axis_into (core scan.rs:219-233) over rank-1 or rank-2
  * views; op is SUM (CumSumOp) or PROD (CumProdOp); kind adds the exclusive
@@ -309,9 +309,9 @@ hx_status hx_prepare_scan(hx_device *dev, hx_op op, hx_dtype dtype,
                           uint64_t out_buf_len, const hx_layout *out_layout,
                           hx_plan **plan);
 
-/* ------------------------------------------------ segmented reduce (a11) */
+/* ------------------------------------------------------- segmented reduce */
 
-/* Segmented sum (north-star config 4; offsets follow the CSR row_ptr
+/* Segmented sum (no reference counterpart; offsets follow the CSR row_ptr
  * convention of core sparse.rs:179-220: num_offsets = S+1 entries,
  * offsets[0] = 0, offsets[S] = n, non-decreasing):
  *   out[s] = sum of values[offsets[s] .. offsets[s+1])   (mod 2^32 for ints)

@@ -10,7 +10,7 @@
  * CPU oracles compute for this path (the `iter().sum()/min()/max()/scan()`
  * folds of crates/hephaestus-rocm/tests/contract.rs:829-831,1673-1680) and
  * what the reference's seams promise (crates/hephaestus-core/src/domain/
- * reduction.rs, scan.rs, ops.rs:735-983), plus the north-star additions
+ * reduction.rs, scan.rs, ops.rs:735-983), plus the additions
  * (argmax, exclusive scan, segmented sum, affine prologue).  The reference
  * itself is Rust and cannot be built in this image (no cargo/rustc), so
  * there is no oracle/_ref build.

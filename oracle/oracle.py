@@ -203,7 +203,7 @@ def ceil_log2(n: int) -> int:
 
 
 def check_f32_bound(got: np.ndarray, ref: np.ndarray, abs_prefix: np.ndarray, n_for_log: int):
-    """(violations, worst |err|/(eps*sum|x|)) for the north-star f32 bound."""
+    """(violations, worst |err|/(eps*sum|x|)) for the f32 bound 2*ceil(log2 n)*eps_f32*sum|x|."""
     got = np.ascontiguousarray(got, dtype=np.float32)
     ref = np.ascontiguousarray(ref, dtype=np.float64)
     abs_prefix = np.ascontiguousarray(abs_prefix, dtype=np.float64)

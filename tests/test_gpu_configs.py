@@ -1,4 +1,4 @@
-"""The BASELINE.json configurations at their full sizes on one MI355X.
+"""The five benchmark configurations at their full sizes on one MI355X.
 
 Inputs are generated in HBM by the library's SplitMix64 fill kernels (whose
 bits tests/test_gpu_parity.py pins to the oracle's), downloaded, and checked
@@ -33,7 +33,7 @@ def note(msg):
 
 @pytest.mark.parametrize("log2n", [20, 28])
 def test_f32_full_sum(device, oracle, log2n):
-    """configs[0] (n = 2^20) and the metric's f32 sum-reduce (n = 2^28)."""
+    """Config 1 (n = 2^20) and the metric's f32 sum-reduce (n = 2^28)."""
     n = 1 << log2n
     note(f"f32 sum n=2^{log2n}")
     x = device.alloc_uninitialized(np.float32, n)
@@ -54,7 +54,7 @@ def test_f32_full_sum(device, oracle, log2n):
 
 
 def test_u32_exclusive_scan_2_28(device, oracle):
-    """u32 exclusive scan of 2^28 values in [0, 256)."""
+    """Config 2: u32 exclusive scan of 2^28 values in [0, 256)."""
     n = 1 << 28
     note("u32 exclusive scan n=2^28")
     x = device.alloc_uninitialized(np.uint32, n)
@@ -73,7 +73,7 @@ def test_u32_exclusive_scan_2_28(device, oracle):
 
 
 def test_f32_rows_sum_max_argmax_with_prologue(device, oracle):
-    """[65536 x 4096] N(0,1), y = fmaf(0.5, x, 0.25), per-row
+    """Config 3: [65536 x 4096] N(0,1), y = fmaf(0.5, x, 0.25), per-row
     sum, max and argmax from one read."""
     rows, cols = 65536, 4096
     note("rows 65536x4096")
@@ -92,7 +92,7 @@ def test_f32_rows_sum_max_argmax_with_prologue(device, oracle):
 
 
 def test_i32_segmented_sum_2_27(device, oracle):
-    """2^27 values in [-1000, 1000], geometric segments (mean
+    """Config 4: 2^27 values in [-1000, 1000], geometric segments (mean
     300, min 1), u32 offsets."""
     n = 1 << 27
     note("segmented n=2^27")
@@ -112,7 +112,7 @@ def test_i32_segmented_sum_2_27(device, oracle):
 
 
 def test_f32_inclusive_scan_2_30(device, oracle):
-    """f32 inclusive scan of 2^30 uniform[0,1) values (4 GiB in,
+    """Config 5: f32 inclusive scan of 2^30 uniform[0,1) values (4 GiB in,
     4 GiB out), every output within the bound."""
     n = 1 << 30
     note("f32 inclusive scan n=2^30")
