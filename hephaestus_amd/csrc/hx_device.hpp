@@ -154,15 +154,61 @@ template <> __device__ __forceinline__ float wave_reduce<OpSum, float>(float v) 
 template <> __device__ __forceinline__ double wave_reduce<OpProd, double>(double v) { return wave_prod(v); }
 template <> __device__ __forceinline__ uint32_t wave_reduce<OpProd, uint32_t>(uint32_t v) { return wave_prod(v); }
 
-// Inclusive Hillis-Steele scan across the 64 lanes (6 steps).
+// ------------------------------------------------------- DPP lane moves
+// GFX9 data-parallel-primitive controls.  A DPP move reads another lane's
+// register inside the VALU instruction itself (no LDS round trip, unlike a
+// generic shuffle).  Lanes whose source is outside the pattern, and lanes of
+// rows masked off, receive `fill`.
+constexpr int kDppRowShr1 = 0x111;    // lane l <- l-1 within its row of 16
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppWaveShr1 = 0x138;   // lane l <- l-1 across the wave
+constexpr int kDppRowBcast15 = 0x142; // row r <- lane 15 of row r-1
+constexpr int kDppRowBcast31 = 0x143; // rows 2,3 <- lane 31
+
+template <int CTRL, int ROW_MASK = 0xf, typename A> __device__ __forceinline__ A dpp_move(A fill, A v) {
+    static_assert(sizeof(A) == 4, "DPP moves are 32-bit");
+    const int r = __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, v), CTRL,
+                                              ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(A, r);
+}
+
+// Value of lane `src` (uniform result).
+template <typename A> __device__ __forceinline__ A read_lane(A v, int src) {
+    static_assert(sizeof(A) == 4, "32-bit lanes");
+    return __builtin_bit_cast(A, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+// Inclusive scan across the 64 lanes: Hillis-Steele inside each row of 16
+// lanes (shifts 1, 2, 4, 8), then the row totals are carried forward with
+// the two row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2
+// and 3).  Six DPP steps for 32-bit values; other widths use shuffles.
 template <typename Op, typename A> __device__ __forceinline__ A wave_inclusive_scan(A v) {
-    const int lane = lane_id();
+    if constexpr (sizeof(A) == 4) {
+        const A id = Op::template identity<A>();
+        v = Op::combine(dpp_move<kDppRowShr1>(id, v), v);
+        v = Op::combine(dpp_move<kDppRowShr2>(id, v), v);
+        v = Op::combine(dpp_move<kDppRowShr4>(id, v), v);
+        v = Op::combine(dpp_move<kDppRowShr8>(id, v), v);
+        v = Op::combine(dpp_move<kDppRowBcast15, 0xa>(id, v), v);
+        v = Op::combine(dpp_move<kDppRowBcast31, 0xc>(id, v), v);
+        return v;
+    } else {
+        const int lane = lane_id();
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        A t = __shfl_up(v, d, kWave);
-        if (lane >= d) v = Op::combine(t, v);
+        for (int d = 1; d < kWave; d <<= 1) {
+            A t = __shfl_up(v, d, kWave);
+            if (lane >= d) v = Op::combine(t, v);
+        }
+        return v;
     }
-    return v;
+}
+
+// Exclusive form of an inclusive wave scan: lane l gets lane l-1's value,
+// lane 0 the identity.
+template <typename Op, typename A> __device__ __forceinline__ A wave_shift_right(A incl) {
+    return dpp_move<kDppWaveShr1>(Op::template identity<A>(), incl);
 }
 
 template <typename A> __device__ __forceinline__ A wave_broadcast(A v, int src) { return __shfl(v, src, kWave); }

@@ -183,7 +183,7 @@ __device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
                                        (uint64_t)lane_id() * 4,
                                    ident, v);
             const T incl = wave_inclusive_scan<Op, T>(lane_fold<T, Op>(v));
-            carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
+            carry = Op::combine(carry, read_lane(incl, kWave - 1));
         }
         agg = Op::combine(agg, carry);
     }
@@ -313,6 +313,23 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
     }
 }
 
+// Full tiles of unit-stride, 16-byte aligned lines (every tile but a line's
+// ragged last one): a block-uniform base pointer plus one 32-bit lane offset,
+// so each step is a single base + offset + immediate vector access with no
+// bounds check and no per-step 64-bit address held in registers.
+template <typename T, bool NT, int STEPS>
+__device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off, T (&x)[STEPS][4]) {
+    using V = typename Vec4<T>::type;
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+        const V q = load_vec<NT>((const V *)((const char *)base + lane_off + (uint32_t)j * (kWave * 16)));
+        x[j][0] = (T)q.x;
+        x[j][1] = (T)q.y;
+        x[j][2] = (T)q.z;
+        x[j][3] = (T)q.w;
+    }
+}
+
 // STEPS vectors per lane: a tile is 4 waves * 64 lanes * 4 * STEPS elements.
 // VEC: unit-stride, 16-byte aligned lines (vector loads and stores).  REV:
 // suffix scan (logical element i is physical len-1-i).  NT: non-temporal
@@ -338,9 +355,20 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
     T *out = (T *)p.out;
     const T ident = Op::template identity<T>();
 
+    // Wave index made explicitly uniform so lane offsets stay 32-bit.
+    const uint32_t lane_off =
+        ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * (uint32_t)sizeof(T);
+    const bool full = VEC && (tin + 1) * kTileElems <= p.len;
     T x[STEPS][4];
+    if (full) {
+        load_full_tile<T, NT, STEPS>(in + ib + (int64_t)(tin * kTileElems), lane_off, x);
+        // All STEPS loads are issued before any arithmetic is scheduled.
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
 #pragma unroll
-    for (int j = 0; j < STEPS; ++j) load4<T, VEC, REV, NT>(p, in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
+        for (int j = 0; j < STEPS; ++j)
+            load4<T, VEC, REV, NT>(p, in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
+    }
 
     // Per step: register scan of 4, wave scan of lane totals, running carry.
     T carry = ident;
@@ -351,8 +379,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
         const T p2 = Op::combine(p1, x[j][2]);
         const T p3 = Op::combine(p2, x[j][3]);
         const T incl = wave_inclusive_scan<Op, T>(p3);
-        T lex = __shfl_up(incl, 1, kWave);
-        if (lane == 0) lex = ident;
+        const T lex = wave_shift_right<Op, T>(incl);
         const T base = Op::combine(carry, lex);
         if constexpr (EXCL) {
             x[j][0] = base;
@@ -365,7 +392,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
             x[j][2] = Op::combine(base, p2);
             x[j][3] = Op::combine(base, p3);
         }
-        carry = Op::combine(carry, __shfl(incl, kWave - 1, kWave));
+        carry = Op::combine(carry, read_lane(incl, kWave - 1));
     }
     if (lane == 0) s_wave_tot[w] = carry;
     __syncthreads();
@@ -395,6 +422,20 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
     __syncthreads();
     const C tile_excl = s_excl;
 
+    if (full) {
+        using V = typename Vec4<T>::type;
+        char *obase = (char *)(out + ob + (int64_t)(tin * kTileElems));
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            V v;
+            v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
+            v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
+            v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
+            v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
+            store_vec<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
         const uint64_t e = e0 + (uint64_t)j * (kWave * 4);

@@ -158,9 +158,8 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
         const uint32_t p2 = p1 + x[j][2];
         const uint32_t p3 = p2 + x[j][3];
         const uint32_t incl = wave_inclusive_scan<OpSum, uint32_t>(p3);
-        uint32_t lex = __shfl_up(incl, 1, kWave);
-        if (lane == 0) lex = 0;
-        const uint32_t step_tot = __shfl(incl, kWave - 1, kWave);
+        const uint32_t lex = wave_shift_right<OpSum, uint32_t>(incl);
+        const uint32_t step_tot = read_lane(incl, kWave - 1);
         const uint32_t base = carry + lex;
         x[j][0] = base + p0;
         x[j][1] = base + p1;
