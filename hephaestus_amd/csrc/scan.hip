@@ -46,10 +46,10 @@
 namespace hx {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / kWave;
+constexpr int kBlock = 256;                          // serial-lines kernel
+constexpr int kWaves = 8;                            // waves per tile block
 constexpr int kSteps = 16;                           // 16-byte vectors per lane
-constexpr int kTile = kWaves * kWave * 4 * kSteps;   // 16384 elements
+constexpr int kTile = kWaves * kWave * 4 * kSteps;   // 32768 elements
 constexpr int kSuper = 64;                           // tiles per superblock
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a missing value
@@ -164,17 +164,17 @@ __device__ __forceinline__ T lane_fold(const T (&v)[4]) {
 
 // Aggregate of tile `u` computed by ONE wave, step by step, with the same
 // operations and order as the four owner waves (fallback path).
-template <typename T, typename Op, bool VEC, bool REV, bool NT, int STEPS>
+template <typename T, typename Op, bool VEC, bool REV, bool NT, int STEPS, int WAVES>
 __device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
     constexpr int kWaveElems = kWave * 4 * STEPS;
-    constexpr int kTileElems = kWaves * kWaveElems;
+    constexpr int kTileElems = WAVES * kWaveElems;
     const T ident = Op::template identity<T>();
     const uint64_t line = u / p.tiles_per_line;
     const uint64_t tin = u - line * p.tiles_per_line;
     const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
     const T *in = (const T *)p.in;
     T agg = ident;
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
         T carry = ident;
         for (int j = 0; j < STEPS; ++j) {
             T v[4];
@@ -206,7 +206,8 @@ template <typename C> struct KnownAgg {
 // `tile_end`, nearest first, stopping at the first inclusive prefix; `found`
 // tells whether one was met.  Lane l reads the tile at distance l.  A tile
 // that stays unpublished is computed by tile_aggregate.
-template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, typename Hook>
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES,
+          typename Hook>
 __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, uint64_t tile_end, int count,
                                          bool &found, Hook &hook) {
     using C = typename Status::C;
@@ -228,7 +229,7 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
         hook.poll();
         if (++spins >= kSpinLimit) {
             const uint64_t u = tile_end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
-            const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS>(p, u);
+            const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS, WAVES>(p, u);
             if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
             spins = 0;
             continue;
@@ -244,7 +245,8 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
 // Exclusive prefix of tile `tile` (position `tin` in its line), computed by
 // one wave.  The last tile of a superblock publishes the superblock
 // aggregate on the way (it needs the tile's own aggregate: hook.agg()).
-template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, typename Hook>
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES,
+          typename Hook>
 __device__ typename Status::C lookback(const ScanParams &p, const Status &st, const Status &st1, uint64_t tile,
                                        uint64_t line, uint64_t tin, Hook &hook) {
     using C = typename Status::C;
@@ -257,7 +259,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
 
     // Level 0: predecessors in the tile's own superblock.
     bool found = false;
-    C excl = pos > 0 ? fold_tiles<T, Op, Status, VEC, REV, NT, STEPS>(p, st, tile, pos, found, hook) : ident;
+    C excl = pos > 0 ? fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, tile, pos, found, hook) : ident;
     if (found) return excl; // superblock 0 always ends here (tile 0 is a prefix)
     if (last_in_super) {
         const C a = hook.agg();
@@ -288,7 +290,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
                 const uint64_t s = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
                 const uint64_t s_end = line * p.tiles_per_line + (s - line_super + 1) * kSuper;
                 bool f = false;
-                const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS>(p, st, s_end, kSuper, f, hook);
+                const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, s_end, kSuper, f, hook);
                 if (lane == 0) st1.publish_if_unset(s, p.tag, f ? kPrefix : kAggregate, v);
                 spins = 0;
                 continue;
@@ -335,12 +337,12 @@ __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off,
 // suffix scan (logical element i is physical len-1-i).  NT: non-temporal
 // vector accesses.
 template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
-          bool NT = true>
-__global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
+          bool NT = true, int WAVES = kWaves>
+__global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     using C = typename Status::C;
     constexpr int kWaveElems = kWave * 4 * STEPS;
-    constexpr int kTileElems = kWaves * kWaveElems;
-    __shared__ T s_wave_tot[kWaves];
+    constexpr int kTileElems = WAVES * kWaveElems;
+    __shared__ T s_wave_tot[WAVES];
     __shared__ C s_excl;
 
     const uint64_t tile = blockIdx.x;
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
     T wave_excl = ident;
     T tile_agg = ident;
 #pragma unroll
-    for (int k = 0; k < kWaves; ++k) {
+    for (int k = 0; k < WAVES; ++k) {
         if (k < w) wave_excl = Op::combine(wave_excl, s_wave_tot[k]);
         tile_agg = Op::combine(tile_agg, s_wave_tot[k]);
     }
@@ -412,7 +414,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(ScanParams p, Status
         } else {
             if (lane == 0) st.publish(tile, p.tag, kAggregate, agg);
             KnownAgg<C> hook{agg};
-            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS>(p, st, st1, tile, line, tin, hook);
+            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, st1, tile, line, tin, hook);
             if (lane == 0) st.publish(tile, p.tag, kPrefix, Op::combine(excl, agg));
         }
         if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
@@ -496,7 +498,7 @@ uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 32 :
 template <typename T, typename Op, typename Status, bool EXCL>
 hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
                        hipStream_t stream) {
-    const dim3 grid((uint32_t)p.total_tiles), block(kBlock);
+    const dim3 grid((uint32_t)p.total_tiles), block(kWaves * kWave);
     if (vec)
         hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false>), grid, block, 0, stream, p, st, st1);
     else if (rev)
