@@ -34,7 +34,7 @@ WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30"
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
              "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
-             "copy_u32": "copy_vec_kernel"}
+             "copy_u32": "copy_tiles_kernel"}
 
 
 def log(msg: str) -> None:
@@ -196,7 +196,7 @@ def pmc_summary(root: Path) -> int:
     copy_bytes = 4 * (1 << 28)
     f_fetch = copy_bytes / (raw["copy_u32"]["fetch_kib"] * 1024)
     f_write = copy_bytes / (raw["copy_u32"]["write_kib"] * 1024)
-    out = {"_calibration": {"kernel": "copy_vec_kernel, 2^28 u32 (read 1 GiB, write 1 GiB)",
+    out = {"_calibration": {"kernel": "copy_tiles_kernel, 2^28 u32 (read 1 GiB, write 1 GiB)",
                             "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)}}
     for w, e in raw.items():
         fetch = e["fetch_kib"] * 1024 * f_fetch

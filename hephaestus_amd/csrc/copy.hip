@@ -12,6 +12,27 @@ namespace {
 constexpr int kBlock = 256;
 constexpr uint32_t kMaxBlocks = 2048;
 
+// Streaming copy in the load pattern of the scan tiles: a block of 8 waves
+// moves one 128 KiB tile, every lane issuing all 16 of its 16-byte loads
+// before its first store (a block-uniform base plus one 32-bit lane offset
+// per access).  Whole tiles only; the remainder goes to copy_vec_kernel.
+constexpr int kTileWaves = 8;
+constexpr int kTileSteps = 16;
+constexpr uint64_t kTileBytes = (uint64_t)kTileWaves * kWave * 16 * kTileSteps;
+
+__global__ __launch_bounds__(kTileWaves * kWave) void copy_tiles_kernel(const char *src, char *dst) {
+    const uint64_t base = (uint64_t)blockIdx.x * kTileBytes;
+    const uint32_t lane_off =
+        ((uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave * kTileSteps + lane_id()) * 16u;
+    u32x4 v[kTileSteps];
+#pragma unroll
+    for (int j = 0; j < kTileSteps; ++j)
+        v[j] = load_vec<true>((const u32x4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
+#pragma unroll
+    for (int j = 0; j < kTileSteps; ++j)
+        store_vec<true>(v[j], (u32x4 *)(dst + base + lane_off + (uint32_t)j * (kWave * 16)));
+}
+
 // 16-byte body (both pointers 16-byte aligned), two vectors in flight per
 // lane, grid-stride; the tail (< 16 bytes) is copied bytewise.
 __global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4 *src, u32x4 *dst, uint64_t nvec,
@@ -41,13 +62,27 @@ hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t st
     if (bytes == 0) return ok();
     const bool aligned = (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
     if (aligned) {
-        const uint64_t nvec = bytes / 16;
-        const uint32_t tail = (uint32_t)(bytes - nvec * 16);
+        const uint64_t tiles = bytes / kTileBytes;
+        if (tiles >= 0x80000000ull)
+            return fail(HX_ERR_DISPATCH_FAILED, "copy of %llu bytes exceeds the grid range",
+                        (unsigned long long)bytes);
+        if (tiles > 0) {
+            hipLaunchKernelGGL(copy_tiles_kernel, dim3((uint32_t)tiles), dim3(kTileWaves * kWave), 0, stream,
+                               (const char *)src, (char *)dst);
+            HX_TRY(check_launch("copy_tiles_kernel"));
+        }
+        const uint64_t done = tiles * kTileBytes;
+        const uint64_t rest = bytes - done;
+        if (rest == 0) return ok();
+        const uint64_t nvec = rest / 16;
+        const uint32_t tail = (uint32_t)(rest - nvec * 16);
         uint64_t blocks = ceil_div(nvec, 2 * kBlock);
         if (blocks > kMaxBlocks) blocks = kMaxBlocks;
         if (blocks < 1) blocks = 1;
-        hipLaunchKernelGGL(copy_vec_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, (const u32x4 *)src,
-                           (u32x4 *)dst, nvec, (const uint8_t *)src + nvec * 16, (uint8_t *)dst + nvec * 16, tail);
+        const char *s0 = (const char *)src + done;
+        char *d0 = (char *)dst + done;
+        hipLaunchKernelGGL(copy_vec_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, (const u32x4 *)s0,
+                           (u32x4 *)d0, nvec, (const uint8_t *)s0 + nvec * 16, (uint8_t *)d0 + nvec * 16, tail);
         return check_launch("copy_vec_kernel");
     }
     uint64_t blocks = ceil_div(bytes, kBlock);

@@ -26,11 +26,15 @@
 namespace hx {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / kWave;
-constexpr int kSteps = 4;
-constexpr int kWaveElems = kWave * 4 * kSteps; // 1024
-constexpr int kTile = kWaves * kWaveElems;     // 4096
+constexpr int kBlock = 256; // helper kernels
+// Tile geometry of segmented_sum_kernel: WAVES waves, each lane holding
+// STEPS 16-byte vectors; the tile's inclusive prefix lives in LDS.
+template <int WAVES, int STEPS> struct SegTile {
+    static constexpr int kWaveElems = kWave * 4 * STEPS;
+    static constexpr int kElems = WAVES * kWaveElems;
+};
+constexpr int kSegWaves = 8, kSegSteps = 8; // 16384-element tiles (64 KiB of LDS prefix)
+constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor
 
@@ -86,9 +90,10 @@ __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uin
 // The status tile u's owner publishes, computed by ONE wave (fallback path):
 // a prefix (the sum from the last segment start in the tile to its end) when
 // the tile holds a segment start, else an aggregate (the tile total).
+template <int TILE>
 __device__ void seg_tile_status(const SegParams &p, uint64_t u, uint32_t &flag, uint32_t &value) {
-    const uint64_t t0 = u * kTile;
-    const uint64_t t1 = (t0 + kTile < p.n) ? t0 + kTile : p.n;
+    const uint64_t t0 = u * TILE;
+    const uint64_t t1 = (t0 + TILE < p.n) ? t0 + TILE : p.n;
     const uint64_t k_star = wave_upper_bound(p, t1 - 1);
     uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
     if (h > t1 - 1) h = t1 - 1;
@@ -109,9 +114,14 @@ __device__ __forceinline__ void publish_if_unset(uint64_t *word, uint32_t tag, u
 
 // Block b processes tile b; see scan.hip for why there is no ticket counter
 // and how the fallback guarantees progress in any dispatch order.
-__global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
+template <int WAVES, int STEPS>
+__global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams p) {
+    static_assert(WAVES >= 4, "waves 1-3 run the boundary searches");
+    constexpr int kWaveElems = SegTile<WAVES, STEPS>::kWaveElems;
+    constexpr int kTile = SegTile<WAVES, STEPS>::kElems;
+    constexpr int kThreads = WAVES * kWave;
     __shared__ uint64_t s_bound[3];
-    __shared__ uint32_t s_wave_tot[kWaves];
+    __shared__ uint32_t s_wave_tot[WAVES];
     __shared__ uint32_t s_carry;
     __shared__ uint32_t E[kTile + 1];
 
@@ -123,20 +133,35 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
     const uint64_t t1 = (t0 + kTile < p.n) ? t0 + kTile : p.n;
     const uint64_t e0 = t0 + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
 
-    // Issue the value loads first; the searches below overlap them.
-    uint32_t x[kSteps][4];
+    // Issue the value loads first; the searches below overlap them.  Whole
+    // tiles use a block-uniform base and one 32-bit lane offset.
+    uint32_t x[STEPS][4];
+    if (t1 - t0 == (uint64_t)kTile) {
+        const char *base = (const char *)(p.values + t0);
+        const uint32_t lane_off =
+            ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * 4u;
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-        const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
-        if (e + 3 < p.n) {
-            const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(p.values + e));
+        for (int j = 0; j < STEPS; ++j) {
+            const u32x4 v = load_vec<true>((const u32x4 *)(base + lane_off + (uint32_t)j * (kWave * 16)));
             x[j][0] = v.x;
             x[j][1] = v.y;
             x[j][2] = v.z;
             x[j][3] = v.w;
-        } else {
+        }
+    } else {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) x[j][c] = (e + c < p.n) ? p.values[e + c] : 0u;
+        for (int j = 0; j < STEPS; ++j) {
+            const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+            if (e + 3 < p.n) {
+                const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(p.values + e));
+                x[j][0] = v.x;
+                x[j][1] = v.y;
+                x[j][2] = v.z;
+                x[j][3] = v.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) x[j][c] = (e + c < p.n) ? p.values[e + c] : 0u;
+            }
         }
     }
 
@@ -152,7 +177,7 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
     // Tile-local inclusive prefix of the values (mod 2^32).
     uint32_t carry = 0;
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
+    for (int j = 0; j < STEPS; ++j) {
         const uint32_t p0 = x[j][0];
         const uint32_t p1 = p0 + x[j][1];
         const uint32_t p2 = p1 + x[j][2];
@@ -171,10 +196,10 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
     __syncthreads();
     uint32_t wave_excl = 0;
 #pragma unroll
-    for (int k = 0; k < kWaves; ++k)
+    for (int k = 0; k < WAVES; ++k)
         if (k < w) wave_excl += s_wave_tot[k];
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
+    for (int j = 0; j < STEPS; ++j) {
         const int le = w * kWaveElems + j * (kWave * 4) + lane * 4;
 #pragma unroll
         for (int c = 0; c < 4; ++c) E[le + c + 1] = wave_excl + x[j][c];
@@ -226,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
                     if (++spins >= kSpinLimit) {
                         const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
                         uint32_t fflag, fval;
-                        seg_tile_status(p, u, fflag, fval);
+                        seg_tile_status<kTile>(p, u, fflag, fval);
                         if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
                         spins = 0;
                         continue;
@@ -251,7 +276,7 @@ __global__ __launch_bounds__(kBlock) void segmented_sum_kernel(SegParams p) {
     uint64_t k_first = tile == 0 ? 1 : (k_lo > 1 ? k_lo : 1);
     uint64_t k_last = k_hi1 >= 1 ? k_hi1 - 1 : 0;
     if (k_last > p.segments) k_last = p.segments;
-    for (uint64_t k = k_first + threadIdx.x; k <= k_last; k += kBlock) {
+    for (uint64_t k = k_first + threadIdx.x; k <= k_last; k += kThreads) {
         const uint64_t b = off_at(p, k);
         uint64_t a = off_at(p, k - 1);
         if (a > b) a = b; // malformed: treat as empty
@@ -315,7 +340,8 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
         return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
-    hipLaunchKernelGGL(segmented_sum_kernel, dim3((uint32_t)p.total_tiles), dim3(kBlock), 0, stream, p);
+    hipLaunchKernelGGL((segmented_sum_kernel<kSegWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
+                       dim3(kSegWaves * kWave), 0, stream, p);
     HX_TRY(check_launch("segmented_sum_kernel"));
     commit_lookback_launch(lb);
     return HX_OK;

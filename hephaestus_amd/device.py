@@ -143,7 +143,10 @@ class RocmDevice:
         _ffi.check(_ffi.lib().hx_synchronize(self.handle))
 
     def _alloc(self, dtype, length: int, zeroed: bool) -> RocmBuffer:
-        hx_dtype(dtype)
+        # Any plain-old-data element type can be stored and moved (the
+        # reference's Buffer<T: Pod>); compute entry points check theirs.
+        if np.dtype(dtype).hasobject:
+            raise errors.InvalidConfiguration(f"unsupported element type {np.dtype(dtype)}")
         ptr = ctypes.c_void_p()
         nbytes = int(length) * np.dtype(dtype).itemsize
         _ffi.check(_ffi.lib().hx_alloc(self.handle, nbytes, 1 if zeroed else 0, ctypes.byref(ptr)))

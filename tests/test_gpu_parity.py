@@ -275,6 +275,39 @@ def test_scan_u32_bit_exact(device, oracle, n, exclusive):
     assert np.array_equal(device.download_owned(out), oracle.scan_sum(x, exclusive=exclusive))
 
 
+# Scan tiles are 32768 elements and superblocks 64 tiles (2^21 elements):
+# sizes on either side of both edges, and several superblocks with a
+# ragged tail, in every direction and kind.
+SCAN_EDGES = [32767, 32768, 32769, 3 * 32768 + 1, (1 << 21) - 1, 1 << 21, (1 << 21) + 1,
+              3 * (1 << 21) + 32768 + 7]
+
+
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+@pytest.mark.parametrize("n", SCAN_EDGES)
+def test_scan_u32_tile_and_superblock_edges(device, oracle, n, kind, direction):
+    x = oracle.uniform_int(n, seed=n ^ 0x5A, lo=0, hi=2**32 - 1)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, n)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.c_contiguous([n])), 0, direction,
+                        StridedView(out, Layout.c_contiguous([n])), kind)
+    want = oracle.scan_sum(x, exclusive=kind == hx.ScanKind.Exclusive,
+                           reverse=direction == hx.ScanDirection.Reverse)
+    assert np.array_equal(device.download_owned(out), want)
+
+
+@pytest.mark.parametrize("n", SCAN_EDGES)
+def test_scan_f32_tile_and_superblock_edges(device, oracle, n):
+    x = oracle.uniform_real(n, seed=n + 3, lo=-1.0, hi=1.0)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.float32, n)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.c_contiguous([n])), 0,
+                        hx.ScanDirection.Forward, StridedView(out, Layout.c_contiguous([n])))
+    ref, ab = oracle.scan_sum(x)
+    bad, worst = oracle.check_f32_bound(device.download_owned(out), ref, ab, n)
+    assert bad == 0, worst
+
+
 @pytest.mark.parametrize("exclusive", [False, True])
 @pytest.mark.parametrize("n", [1, 2, 5, 4096, 4097, 65536 + 17, (1 << 20) + 3])
 def test_scan_f32_within_bound(device, oracle, n, exclusive):
@@ -382,6 +415,26 @@ def test_segmented_sum_geometric(device, oracle, n, mean):
     assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
 
 
+def test_segmented_sum_16k_tile_edges(device, oracle):
+    """Segmented tiles hold 16384 values: boundaries on and beside tile
+    edges, empty segments at an edge, a segment spanning several tiles (the
+    carry crosses tiles without a head), and runs of one-element segments
+    across an edge."""
+    t = 16384
+    n = 4 * t + 77
+    x = oracle.uniform_int(n, seed=16, lo=-1000, hi=1000, dtype=np.int32)
+    cases = [
+        [0, t - 1, t, t + 1, 2 * t, 2 * t, 2 * t, n],
+        [0, 5, n - 3, n],                                   # spans every tile
+        [0] + list(range(t - 40, t + 40)) + [3 * t, n],      # unit segments across an edge
+        [0, t, 2 * t, 3 * t, 4 * t, n, n, n],               # exact tile edges, empties at n
+        [0, 0, 0, 1, 2 * t + 3, 2 * t + 3, 4 * t, 4 * t + 1, n],
+    ]
+    for off in cases:
+        off = np.array(off, np.uint32)
+        assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
+
+
 def test_segmented_sum_empty_values(device):
     vb = device.alloc_zeroed(np.int32, 16)  # aligned allocation, but n = 0 values
     ob = device.upload(np.zeros(4, np.uint32))
@@ -431,3 +484,32 @@ def test_prepared_plans_allocate_once_and_rebind(device, oracle):
     device.write_buffer(buf, y)
     plan.dispatch()
     assert np.array_equal(device.download_owned(out), oracle.scan_sum(y, exclusive=True))
+
+
+# ------------------------------------------------------------ copy_buffer
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 32767, 32768, 32769, 3 * 32768 + 5, (1 << 20) + 3])
+def test_copy_buffer_bit_exact(device, oracle, n):
+    """copy_buffer runs a streaming kernel: 128 KiB tiles, a 16-byte body for
+    the remainder and a byte tail."""
+    x = oracle.uniform_int(n, seed=n + 77, lo=0, hi=2**32 - 1)
+    src = device.upload(x)
+    dst = device.alloc_zeroed(np.uint32, n)
+    device.copy_buffer(src, dst)
+    assert np.array_equal(device.download_owned(dst), x)
+
+
+@pytest.mark.parametrize("skew,nbytes", [(1, 1), (1, 17), (3, 4099), (4, 131072 + 20), (8, 3 * 131072), (0, 131072 + 15)])
+def test_copy_unaligned_ranges(device, oracle, skew, nbytes):
+    """hx_copy on raw byte ranges: misaligned starts take the bytewise kernel,
+    aligned ones the tiles plus a remainder; bytes outside the range stay."""
+    from hephaestus_amd import _ffi
+
+    total = nbytes + 64
+    x = oracle.uniform_int((total + 3) // 4, seed=nbytes, lo=0, hi=2**32 - 1).view(np.uint8)[:total].copy()
+    src = device.upload(x)
+    dst = device.alloc_zeroed(np.uint8, total)
+    _ffi.check(_ffi.lib().hx_copy(device.handle, src.ptr + skew, nbytes, dst.ptr + skew, nbytes, 1))
+    got = device.download_owned(dst)
+    want = np.zeros(total, np.uint8)
+    want[skew:skew + nbytes] = x[skew:skew + nbytes]
+    assert np.array_equal(got, want)
