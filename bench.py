@@ -153,8 +153,9 @@ def bench_copy_u32(hx, dev, args):
     return {"n": n, "ms": ms, "bytes": 8 * n}
 
 
-def _counter_csv(path: Path) -> dict:
-    """{kernel name: [per-dispatch values]} from one rocprofv3 --pmc run (CSV)."""
+def _counter_csv(path: Path, counter: str | None = None) -> dict:
+    """{kernel name: [per-dispatch values]} of one counter (or of the only
+    counter) from one rocprofv3 --pmc run (CSV)."""
     import csv
 
     files = sorted(path.rglob("*counter_collection.csv"))
@@ -164,7 +165,27 @@ def _counter_csv(path: Path) -> dict:
     for f in files:
         with open(f, newline="") as fh:
             for row in csv.DictReader(fh):
-                out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+                if counter is None or row["Counter_Name"] == counter:
+                    out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def _lds_summary(root: Path) -> dict:
+    """LDS instructions and bank-conflict cycles per dispatch of each
+    workload's kernel, from root/<workload>/lds runs of
+    `rocprofv3 --pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT`."""
+    import statistics
+
+    out = {}
+    for w in WORKLOADS:
+        d = root / w / "lds"
+        if not d.exists():
+            continue
+        entry = {"kernel": KERNEL_OF[w]}
+        for c in ("SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT"):
+            vals = [v for k, vs in _counter_csv(d, c).items() if KERNEL_OF[w] in k for v in vs]
+            entry[c] = statistics.median(vals) if vals else None
+        out[w] = entry
     return out
 
 
@@ -173,7 +194,8 @@ def pmc_summary(root: Path) -> int:
 
     Expects root/<workload>/fetch and root/<workload>/write, each the output
     directory of `rocprofv3 --pmc FETCH_SIZE` (resp. WRITE_SIZE) over
-    `bench.py --workload <workload>`.  Counters are KiB per dispatch; each
+    `bench.py --workload <workload>`; optional root/<workload>/lds runs of
+    `--pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT` go to profiles/pmc_lds.json.  Counters are KiB per dispatch; each
     is scaled by the factor that maps the copy kernel's reading to its known
     traffic (read 4n, write 4n bytes)."""
     import statistics
@@ -203,6 +225,9 @@ def pmc_summary(root: Path) -> int:
         write = e["write_kib"] * 1024 * f_write
         out[w] = {"kernel": KERNEL_OF[w], "fetch_kib": e["fetch_kib"], "write_kib": e["write_kib"],
                   "dispatches": e["dispatches"], "hbm_bytes_per_launch": round(fetch + write)}
+    lds = _lds_summary(root)
+    if lds:
+        (REPO / "profiles" / "pmc_lds.json").write_text(json.dumps(lds, indent=1) + "\n")
     dst = REPO / "profiles" / "pmc_traffic.json"
     dst.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out, indent=1))

@@ -1,0 +1,409 @@
+// hephaestus.hpp — C++17 host interface over the C ABI (include/hx.h).
+//
+// Mirrors the reference's Rust seams so C++ callers read like the
+// reference's own code:
+//   ComputeDevice / ComputeDeviceAcquisition  crates/hephaestus-core/src/domain/device.rs:90-281
+//   DeviceBuffer<T>                           crates/hephaestus-core/src/domain/buffer.rs:7-19
+//   StridedView / Layout                      crates/hephaestus-core/src/domain/view.rs:27-41
+//   FullReductionOps                          crates/hephaestus-core/src/domain/reduction.rs:243-309
+//   AxisReductionOps                          crates/hephaestus-core/src/domain/reduction.rs:74-223
+//   ScanOps / ScanDirection                   crates/hephaestus-core/src/domain/scan.rs:36-264
+//   HephaestusError                           crates/hephaestus-core/src/domain/error.rs:8-58
+// Errors are thrown as hephaestus::Error carrying the variant and the
+// native message; every entry point validates before it writes, so a
+// thrown call leaves its outputs untouched.  Header-only; link
+// libhephaestus_amd.so.
+#pragma once
+
+#include "../../include/hx.h"
+
+#include <array>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+namespace hephaestus {
+
+// ------------------------------------------------------------------ errors
+enum class ErrorKind {
+    AdapterUnavailable = HX_ERR_ADAPTER_UNAVAILABLE,
+    DeviceUnavailable = HX_ERR_DEVICE_UNAVAILABLE,
+    AllocationFailed = HX_ERR_ALLOCATION_FAILED,
+    LengthMismatch = HX_ERR_LENGTH_MISMATCH,
+    DispatchFailed = HX_ERR_DISPATCH_FAILED,
+    InvalidConfiguration = HX_ERR_INVALID_CONFIGURATION,
+    TransferFailed = HX_ERR_TRANSFER_FAILED,
+};
+
+class Error : public std::runtime_error {
+  public:
+    Error(ErrorKind kind, const std::string &msg, uint64_t host_len = 0, uint64_t device_len = 0)
+        : std::runtime_error(msg), kind_(kind), host_len_(host_len), device_len_(device_len) {}
+    ErrorKind kind() const { return kind_; }
+    // LengthMismatch { host_len, device_len } (error.rs:30-36).
+    uint64_t host_len() const { return host_len_; }
+    uint64_t device_len() const { return device_len_; }
+
+  private:
+    ErrorKind kind_;
+    uint64_t host_len_, device_len_;
+};
+
+inline void check(hx_status s) {
+    if (s == HX_OK) return;
+    uint64_t h = 0, d = 0;
+    if (s == HX_ERR_LENGTH_MISMATCH) hx_last_length_mismatch(&h, &d);
+    throw Error(static_cast<ErrorKind>(s), hx_last_error_message(), h, d);
+}
+
+// ------------------------------------------------------------ element types
+template <typename T> struct Scalar;
+template <> struct Scalar<float> { static constexpr hx_dtype dtype = HX_DTYPE_F32; };
+template <> struct Scalar<uint32_t> { static constexpr hx_dtype dtype = HX_DTYPE_U32; };
+template <> struct Scalar<int32_t> { static constexpr hx_dtype dtype = HX_DTYPE_I32; };
+
+// ------------------------------------------------------- operator markers
+// core ops.rs:735-803 (SumOp ... CumProdOp); MeanOp and ArgMaxOp select the
+// mean / argmax kernels.
+struct SumOp { static constexpr hx_op code = HX_OP_SUM; };
+struct ProdOp { static constexpr hx_op code = HX_OP_PROD; };
+struct MinOp { static constexpr hx_op code = HX_OP_MIN; };
+struct MaxOp { static constexpr hx_op code = HX_OP_MAX; };
+struct MeanOp { static constexpr hx_op code = HX_OP_MEAN; };
+struct ArgMaxOp { static constexpr hx_op code = HX_OP_ARGMAX; };
+struct CumSumOp { static constexpr hx_op code = HX_OP_SUM; };
+struct CumProdOp { static constexpr hx_op code = HX_OP_PROD; };
+
+enum class ScanDirection { Forward = HX_SCAN_FORWARD, Reverse = HX_SCAN_REVERSE };
+enum class ScanKind { Inclusive = HX_SCAN_INCLUSIVE, Exclusive = HX_SCAN_EXCLUSIVE };
+
+// Fused prologue y = fmaf(a, x, b) (f32 only).
+struct Affine {
+    float a = 1.0f, b = 0.0f;
+};
+
+// ------------------------------------------------------------------ layout
+// Shape, strides (elements, may be negative) and offset of a view over a
+// linear buffer; rank <= 4.
+class Layout {
+  public:
+    static Layout c_contiguous(std::vector<uint64_t> shape) {
+        Layout l;
+        l.raw_.rank = static_cast<uint32_t>(shape.size());
+        int64_t stride = 1;
+        for (size_t d = shape.size(); d-- > 0;) {
+            l.raw_.shape[d] = shape[d];
+            l.raw_.strides[d] = stride;
+            stride *= static_cast<int64_t>(shape[d]);
+        }
+        return l;
+    }
+    static Layout strided(std::vector<uint64_t> shape, std::vector<int64_t> strides, uint64_t offset) {
+        if (shape.size() != strides.size() || shape.size() > HX_MAX_RANK)
+            throw Error(ErrorKind::InvalidConfiguration, "layout rejected: rank mismatch");
+        Layout l;
+        l.raw_.rank = static_cast<uint32_t>(shape.size());
+        for (size_t d = 0; d < shape.size(); ++d) {
+            l.raw_.shape[d] = shape[d];
+            l.raw_.strides[d] = strides[d];
+        }
+        l.raw_.offset = offset;
+        return l;
+    }
+    uint32_t rank() const { return raw_.rank; }
+    uint64_t size() const {
+        uint64_t n = 1;
+        for (uint32_t d = 0; d < raw_.rank; ++d) n *= raw_.shape[d];
+        return n;
+    }
+    const hx_layout *raw() const { return &raw_; }
+
+  private:
+    hx_layout raw_{};
+};
+
+class RocmDevice;
+
+// ------------------------------------------------------------------ buffer
+// RocmBuffer<T> (rocm infrastructure/buffer.rs:16-80): owns one device
+// allocation of len() elements; a zero-length buffer holds no allocation.
+template <typename T> class RocmBuffer {
+  public:
+    RocmBuffer() = default;
+    RocmBuffer(const RocmBuffer &) = delete;
+    RocmBuffer &operator=(const RocmBuffer &) = delete;
+    RocmBuffer(RocmBuffer &&o) noexcept { *this = std::move(o); }
+    RocmBuffer &operator=(RocmBuffer &&o) noexcept {
+        release();
+        dev_ = o.dev_;
+        ptr_ = o.ptr_;
+        len_ = o.len_;
+        o.ptr_ = nullptr;
+        o.len_ = 0;
+        return *this;
+    }
+    ~RocmBuffer() { release(); }
+
+    uint64_t len() const { return len_; }
+    bool is_empty() const { return len_ == 0; }
+    T *device_ptr() const { return ptr_; }
+
+  private:
+    friend class RocmDevice;
+    RocmBuffer(hx_device *dev, T *ptr, uint64_t len) : dev_(dev), ptr_(ptr), len_(len) {}
+    void release() {
+        if (ptr_ && dev_) hx_free(dev_, ptr_);
+        ptr_ = nullptr;
+    }
+    hx_device *dev_ = nullptr;
+    T *ptr_ = nullptr;
+    uint64_t len_ = 0;
+};
+
+template <typename T> struct StridedView {
+    const RocmBuffer<T> &buffer;
+    const Layout &layout;
+};
+
+struct Topology {
+    std::string name, arch;
+    uint32_t compute_units = 0, warp_size = 0;
+    uint64_t total_memory_bytes = 0;
+};
+
+// ------------------------------------------------------------------ device
+class RocmDevice {
+  public:
+    // ComputeDeviceAcquisition: the first device / a given ordinal.
+    static RocmDevice try_default() { return try_with_ordinal(0); }
+    static RocmDevice try_with_ordinal(int32_t ordinal) {
+        hx_device *d = nullptr;
+        check(hx_device_open(ordinal, &d));
+        return RocmDevice(d);
+    }
+    static int32_t device_count() {
+        int32_t n = 0;
+        check(hx_device_count(&n));
+        return n;
+    }
+
+    RocmDevice(RocmDevice &&o) noexcept : dev_(o.dev_) { o.dev_ = nullptr; }
+    RocmDevice(const RocmDevice &) = delete;
+    ~RocmDevice() {
+        if (dev_) hx_device_close(dev_);
+    }
+
+    const char *backend_name() const { return "rocm"; }
+    hx_device *raw() const { return dev_; }
+
+    Topology topology() const {
+        hx_device_info i{};
+        check(hx_device_get_info(dev_, &i));
+        return Topology{i.name, i.arch, i.compute_units, i.warp_size, i.total_memory_bytes};
+    }
+    void synchronize() { check(hx_synchronize(dev_)); }
+
+    template <typename T> RocmBuffer<T> alloc_zeroed(uint64_t len) { return alloc<T>(len, true); }
+    template <typename T> RocmBuffer<T> alloc_uninitialized(uint64_t len) { return alloc<T>(len, false); }
+
+    template <typename T> RocmBuffer<T> upload(const std::vector<T> &host) {
+        RocmBuffer<T> b = alloc_uninitialized<T>(host.size());
+        write_buffer(b, host);
+        return b;
+    }
+    template <typename T> void write_buffer(RocmBuffer<T> &b, const std::vector<T> &host) {
+        check(hx_upload(dev_, b.device_ptr(), b.len(), host.data(), host.size(), sizeof(T)));
+    }
+    template <typename T> void write_sub_buffer(RocmBuffer<T> &b, uint64_t offset, const std::vector<T> &host) {
+        check(hx_write_sub(dev_, b.device_ptr(), b.len(), offset, host.data(), host.size(), sizeof(T)));
+    }
+    template <typename T> void download(const RocmBuffer<T> &b, std::vector<T> &host) {
+        check(hx_download(dev_, b.device_ptr(), b.len(), host.data(), host.size(), sizeof(T)));
+    }
+    template <typename T> std::vector<T> download_owned(const RocmBuffer<T> &b) {
+        std::vector<T> host(b.len());
+        download(b, host);
+        return host;
+    }
+    template <typename T> void copy_buffer(const RocmBuffer<T> &src, RocmBuffer<T> &dst) {
+        check(hx_copy(dev_, src.device_ptr(), src.len(), dst.device_ptr(), dst.len(), sizeof(T)));
+    }
+
+  private:
+    explicit RocmDevice(hx_device *d) : dev_(d) {}
+    template <typename T> RocmBuffer<T> alloc(uint64_t len, bool zeroed) {
+        void *p = nullptr;
+        check(hx_alloc(dev_, len * sizeof(T), zeroed ? 1u : 0u, &p));
+        return RocmBuffer<T>(dev_, static_cast<T *>(p), len);
+    }
+    hx_device *dev_ = nullptr;
+};
+
+// ------------------------------------------------------------------- plans
+// The Prepared associated types: a dispatch bound to its operands, owning
+// its workspace; dispatch() re-reads the bound buffers every time.
+class PreparedPlan {
+  public:
+    explicit PreparedPlan(hx_plan *p) : plan_(p) {}
+    PreparedPlan(PreparedPlan &&o) noexcept : plan_(o.plan_) { o.plan_ = nullptr; }
+    PreparedPlan(const PreparedPlan &) = delete;
+    ~PreparedPlan() {
+        if (plan_) hx_plan_destroy(plan_);
+    }
+    void dispatch(hx_stream stream = nullptr) const { check(hx_plan_dispatch(plan_, stream)); }
+    uint64_t workspace_bytes() const {
+        uint64_t b = 0;
+        check(hx_plan_workspace_bytes(plan_, &b));
+        return b;
+    }
+
+  private:
+    hx_plan *plan_ = nullptr;
+};
+
+namespace detail {
+inline const hx_affine *affine(const Affine *p, hx_affine &storage) {
+    if (!p) return nullptr;
+    storage = hx_affine{p->a, p->b, 1u, 0u};
+    return &storage;
+}
+} // namespace detail
+
+// ---------------------------------------------------------- FullReductionOps
+class RocmFullReductionOps {
+  public:
+    template <typename Op, typename T>
+    void reduce_full_into(RocmDevice &dev, StridedView<T> input, StridedView<T> output,
+                          const Affine *prologue = nullptr, hx_stream stream = nullptr) const {
+        hx_affine a;
+        check(hx_reduce_full(dev.raw(), Op::code, Scalar<T>::dtype, input.buffer.device_ptr(), input.buffer.len(),
+                             input.layout.raw(), output.buffer.device_ptr(), output.buffer.len(),
+                             output.layout.raw(), detail::affine(prologue, a), stream));
+    }
+    template <typename Op, typename T>
+    PreparedPlan prepare_reduce_full(RocmDevice &dev, StridedView<T> input, StridedView<T> output,
+                                     const Affine *prologue = nullptr) const {
+        hx_affine a;
+        hx_plan *p = nullptr;
+        check(hx_prepare_reduce_full(dev.raw(), Op::code, Scalar<T>::dtype, input.buffer.device_ptr(),
+                                     input.buffer.len(), input.layout.raw(), output.buffer.device_ptr(),
+                                     output.buffer.len(), output.layout.raw(), detail::affine(prologue, a), &p));
+        return PreparedPlan(p);
+    }
+    void dispatch_full(RocmDevice &, const PreparedPlan &plan, hx_stream stream = nullptr) const {
+        plan.dispatch(stream);
+    }
+    // Index of the maximum (ties to the lowest index, NaN ignored).
+    template <typename T>
+    void argmax_full_into(RocmDevice &dev, StridedView<T> input, RocmBuffer<uint32_t> &index,
+                          RocmBuffer<T> *value = nullptr, const Affine *prologue = nullptr,
+                          hx_stream stream = nullptr) const {
+        if (index.len() != 1) throw Error(ErrorKind::DispatchFailed, "argmax index output must hold 1 element");
+        if (value && value->len() != 1) throw Error(ErrorKind::DispatchFailed, "argmax value output must hold 1 element");
+        hx_affine a;
+        check(hx_argmax_full(dev.raw(), Scalar<T>::dtype, input.buffer.device_ptr(), input.buffer.len(),
+                             input.layout.raw(), value ? value->device_ptr() : nullptr, index.device_ptr(),
+                             detail::affine(prologue, a), stream));
+    }
+};
+
+// ---------------------------------------------------------- AxisReductionOps
+class RocmAxisReductionOps {
+  public:
+    template <typename Op, typename T, typename U>
+    void reduce_axis_into(RocmDevice &dev, StridedView<T> input, uint32_t axis, StridedView<U> output,
+                          hx_stream stream = nullptr) const {
+        static_assert(std::is_same<T, U>::value || std::is_same<Op, ArgMaxOp>::value,
+                      "output element type must match the input (u32 for argmax)");
+        check(hx_reduce_axis(dev.raw(), Op::code, Scalar<T>::dtype, input.buffer.device_ptr(), input.buffer.len(),
+                             input.layout.raw(), axis, output.buffer.device_ptr(), output.buffer.len(),
+                             output.layout.raw(), stream));
+    }
+    template <typename T> void prod_axis_into(RocmDevice &d, StridedView<T> in, uint32_t axis, StridedView<T> out) const {
+        reduce_axis_into<ProdOp>(d, in, axis, out);
+    }
+    template <typename T> void min_axis_into(RocmDevice &d, StridedView<T> in, uint32_t axis, StridedView<T> out) const {
+        reduce_axis_into<MinOp>(d, in, axis, out);
+    }
+    template <typename T> void max_axis_into(RocmDevice &d, StridedView<T> in, uint32_t axis, StridedView<T> out) const {
+        reduce_axis_into<MaxOp>(d, in, axis, out);
+    }
+    template <typename T> void mean_axis_into(RocmDevice &d, StridedView<T> in, uint32_t axis, StridedView<T> out) const {
+        reduce_axis_into<MeanOp>(d, in, axis, out);
+    }
+    template <typename Op, typename T, typename U>
+    PreparedPlan prepare_reduce_axis_into(RocmDevice &dev, StridedView<T> input, uint32_t axis,
+                                          StridedView<U> output) const {
+        hx_plan *p = nullptr;
+        check(hx_prepare_reduce_axis(dev.raw(), Op::code, Scalar<T>::dtype, input.buffer.device_ptr(),
+                                     input.buffer.len(), input.layout.raw(), axis, output.buffer.device_ptr(),
+                                     output.buffer.len(), output.layout.raw(), &p));
+        return PreparedPlan(p);
+    }
+    // Sum, max and argmax of y = fmaf(a, x, b) per row from ONE read; any
+    // output may be null.
+    template <typename T>
+    void reduce_rows_fused(RocmDevice &dev, const RocmBuffer<T> &input, uint64_t rows, uint64_t cols,
+                           uint64_t row_stride, const Affine *prologue, RocmBuffer<T> *out_sum,
+                           RocmBuffer<T> *out_max, RocmBuffer<uint32_t> *out_argmax,
+                           hx_stream stream = nullptr) const {
+        uint64_t out_len = rows;
+        if (out_sum) out_len = out_sum->len();
+        else if (out_max) out_len = out_max->len();
+        else if (out_argmax) out_len = out_argmax->len();
+        hx_affine a;
+        check(hx_reduce_rows(dev.raw(), Scalar<T>::dtype, input.device_ptr(), input.len(), rows, cols, row_stride, 0,
+                             detail::affine(prologue, a), out_sum ? out_sum->device_ptr() : nullptr,
+                             out_max ? out_max->device_ptr() : nullptr,
+                             out_argmax ? out_argmax->device_ptr() : nullptr, out_len, stream));
+    }
+};
+
+// ------------------------------------------------------------------ ScanOps
+class RocmScanOps {
+  public:
+    template <typename Op, typename T>
+    void scan_axis_into(RocmDevice &dev, StridedView<T> input, uint32_t axis, ScanDirection direction,
+                        StridedView<T> output, ScanKind kind = ScanKind::Inclusive,
+                        hx_stream stream = nullptr) const {
+        check(hx_scan(dev.raw(), Op::code, Scalar<T>::dtype, static_cast<hx_scan_kind>(kind),
+                      static_cast<hx_scan_direction>(direction), input.buffer.device_ptr(), input.buffer.len(),
+                      input.layout.raw(), axis, output.buffer.device_ptr(), output.buffer.len(),
+                      output.layout.raw(), stream));
+    }
+    template <typename Op, typename T>
+    PreparedPlan prepare_scan_axis(RocmDevice &dev, StridedView<T> input, uint32_t axis, ScanDirection direction,
+                                   StridedView<T> output, ScanKind kind = ScanKind::Inclusive) const {
+        hx_plan *p = nullptr;
+        check(hx_prepare_scan(dev.raw(), Op::code, Scalar<T>::dtype, static_cast<hx_scan_kind>(kind),
+                              static_cast<hx_scan_direction>(direction), input.buffer.device_ptr(),
+                              input.buffer.len(), input.layout.raw(), axis, output.buffer.device_ptr(),
+                              output.buffer.len(), output.layout.raw(), &p));
+        return PreparedPlan(p);
+    }
+    void dispatch_scan(RocmDevice &, const PreparedPlan &plan, hx_stream stream = nullptr) const {
+        plan.dispatch(stream);
+    }
+};
+
+// ------------------------------------------------------ segmented reduction
+// out[s] = sum of values[offsets[s] .. offsets[s+1]) (CSR row_ptr offsets,
+// core sparse.rs:179-220), integer sums wrapping mod 2^32.
+class RocmSegmentedReductionOps {
+  public:
+    template <typename T>
+    void segmented_sum_into(RocmDevice &dev, const RocmBuffer<T> &values, const RocmBuffer<uint32_t> &offsets,
+                            RocmBuffer<T> &out, hx_stream stream = nullptr) const {
+        check(hx_segmented_reduce(dev.raw(), HX_OP_SUM, Scalar<T>::dtype, values.device_ptr(), values.len(),
+                                  offsets.device_ptr(), offsets.len(), out.device_ptr(), out.len(), stream));
+    }
+    void validate_offsets(RocmDevice &dev, const RocmBuffer<uint32_t> &offsets, uint64_t n) const {
+        check(hx_validate_segment_offsets(dev.raw(), offsets.device_ptr(), offsets.len(), n));
+    }
+};
+
+} // namespace hephaestus

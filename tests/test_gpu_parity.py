@@ -487,9 +487,9 @@ def test_prepared_plans_allocate_once_and_rebind(device, oracle):
 
 
 # ------------------------------------------------------------ copy_buffer
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 32767, 32768, 32769, 3 * 32768 + 5, (1 << 20) + 3])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 65535, 65536, 65537, 3 * 65536 + 5, (1 << 20) + 3])
 def test_copy_buffer_bit_exact(device, oracle, n):
-    """copy_buffer runs a streaming kernel: 128 KiB tiles, a 16-byte body for
+    """copy_buffer runs a streaming kernel: 256 KiB tiles, a 16-byte body for
     the remainder and a byte tail."""
     x = oracle.uniform_int(n, seed=n + 77, lo=0, hi=2**32 - 1)
     src = device.upload(x)
@@ -498,7 +498,7 @@ def test_copy_buffer_bit_exact(device, oracle, n):
     assert np.array_equal(device.download_owned(dst), x)
 
 
-@pytest.mark.parametrize("skew,nbytes", [(1, 1), (1, 17), (3, 4099), (4, 131072 + 20), (8, 3 * 131072), (0, 131072 + 15)])
+@pytest.mark.parametrize("skew,nbytes", [(1, 1), (1, 17), (3, 4099), (4, 262144 + 20), (8, 3 * 262144), (0, 262144 + 15)])
 def test_copy_unaligned_ranges(device, oracle, skew, nbytes):
     """hx_copy on raw byte ranges: misaligned starts take the bytewise kernel,
     aligned ones the tiles plus a remainder; bytes outside the range stay."""
