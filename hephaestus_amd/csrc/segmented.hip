@@ -7,21 +7,21 @@
 // serial inner loop (crates/hephaestus-rocm/src/application/sparse/
 // spmv.rs:17-42), which leaves neighbouring lanes hundreds of elements
 // apart.  Here the work is cut by ELEMENTS, not by segments, so every block
-// streams the same 64 KiB with 16-byte loads whatever the segment lengths:
+// streams the same 32 KiB with 16-byte loads whatever the segment lengths.
+// Two launches:
 //
-//   * block b takes tile b (no ticket counter) and loads its 16384 values
-//     (8 waves x 8 vectors per lane), wave-striped like the scan;
-//   * while those loads are in flight, three waves run 64-ary searches over
-//     the offsets for the segment boundaries the tile touches;
-//   * the tile's inclusive prefix goes to LDS; every segment that ENDS in the
-//     tile gets E[end] - E[start] (plus the carry for the segment that began
-//     in an earlier tile);
-//   * the carry is a segmented decoupled look-back: a tile that contains a
-//     segment start publishes its carry-out at once as a "prefix", so the
-//     look-back almost always stops at the nearest predecessor.
-// The 64 KiB LDS prefix caps residency at two blocks per CU; at 2^27 values
-// the 8x8 tile ran 151 us against 187 us for 4 waves x 4 vectors (4096-value
-// tiles).
+//   1. seg_tile_map_kernel: one coalesced pass over the offsets records, for
+//      every tile edge, the offset indices around it (upper and lower bound),
+//      so no block searches the offsets;
+//   2. segmented_sum_kernel: block b loads tile b (4 waves x 8 vectors per
+//      lane = 8192 values) and the offsets that end in it, scans the values
+//      in registers, marks segment ends in an LDS bitmask and writes every
+//      segment that ends in the tile.  The segment open at the tile start
+//      takes the sum of earlier tiles from a segmented decoupled look-back:
+//      a tile that holds a segment start publishes its tail at once as a
+//      prefix, so a look-back almost always stops at the nearest
+//      predecessor.
+//
 // Integer addition mod 2^32 is associative, so every output is bit-exact.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
@@ -31,13 +31,17 @@ namespace {
 
 constexpr int kBlock = 256; // helper kernels
 // Tile geometry of segmented_sum_kernel: WAVES waves, each lane holding
-// STEPS 16-byte vectors; the tile's inclusive prefix lives in LDS.
+// STEPS 16-byte vectors of values in registers.
 template <int WAVES, int STEPS> struct SegTile {
     static constexpr int kWaveElems = kWave * 4 * STEPS;
     static constexpr int kElems = WAVES * kWaveElems;
 };
-constexpr int kSegWaves = 8, kSegSteps = 8; // 16384-element tiles (64 KiB of LDS prefix)
+// 4 x 8 measured best at 2^27 (8192-value tiles, six blocks per CU): larger
+// tiles leave fewer blocks per CU to overlap one block's barriers with
+// another's loads (8 x 16: 230 us; 8 x 8: 120 us; 4 x 8: 118 us).
+constexpr int kSegWaves = 4, kSegSteps = 8;
 constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
+constexpr int kSlots = 2048; // segment values compacted per round
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor
 
@@ -48,9 +52,9 @@ struct SegParams {
     uint64_t segments; // S
     uint32_t *out;
     uint64_t total_tiles;
-    WorkspaceHeader *hdr;
-    uint64_t *status;
-    uint32_t tag;         // this launch's status tag
+    uint64_t *status;          // look-back words, one per tile
+    uint32_t *ub_map, *lb_map; // tile edges -> offset indices (total_tiles + 1 each)
+    uint32_t tag;              // this launch's status tag
 };
 
 // Offsets clamped into [0, n]: malformed offsets can never address values
@@ -58,32 +62,6 @@ struct SegParams {
 __device__ __forceinline__ uint64_t off_at(const SegParams &p, uint64_t k) {
     const uint64_t o = p.offsets[k];
     return o < p.n ? o : p.n;
-}
-
-// First k in [0, S] with off(k) > v, or S+1 if none (upper bound).  Each
-// round probes 64 evenly spaced positions, one per lane, and keeps the gap
-// between the last "<= v" and the first "> v" probe.  Terminates for any
-// offset contents because the range strictly shrinks.
-__device__ uint64_t wave_upper_bound(const SegParams &p, uint64_t v) {
-    const int lane = lane_id();
-    uint64_t lo = 0, hi = p.segments + 1;
-    while (hi > lo) {
-        const uint64_t len = hi - lo;
-        const uint64_t step = (len + kWave - 1) / kWave;
-        uint64_t pos = lo + (uint64_t)(lane + 1) * step - 1;
-        if (pos > hi - 1) pos = hi - 1;
-        const bool pred = off_at(p, pos) > v;
-        const uint64_t m = ballot(pred);
-        if (m == 0ull) return hi;
-        const int f = __ffsll((long long)m) - 1;
-        const uint64_t pf = __shfl(pos, f, kWave);
-        if (step == 1) return pf; // every position in the range was probed
-        const uint64_t pprev = f > 0 ? __shfl(pos, f - 1, kWave) : 0;
-        lo = f > 0 ? pprev + 1 : lo;
-        hi = pf + 1;
-        if (hi - lo == 1) return lo;
-    }
-    return lo;
 }
 
 __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
@@ -97,7 +75,8 @@ template <int TILE>
 __device__ void seg_tile_status(const SegParams &p, uint64_t u, uint32_t &flag, uint32_t &value) {
     const uint64_t t0 = u * TILE;
     const uint64_t t1 = (t0 + TILE < p.n) ? t0 + TILE : p.n;
-    const uint64_t k_star = wave_upper_bound(p, t1 - 1);
+    uint64_t k_star = p.lb_map[u + 1];
+    k_star = k_star < p.segments + 1 ? k_star : p.segments + 1;
     uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
     if (h > t1 - 1) h = t1 - 1;
     const bool has_head = h >= t0;
@@ -115,22 +94,114 @@ __device__ __forceinline__ void publish_if_unset(uint64_t *word, uint32_t tag, u
                                          __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// "Last marked value" scan across the 64 lanes: lane l ends with the (h, v)
+// of the highest lane <= l whose h is set (h = 0 when there is none).  Same
+// DPP pattern as wave_inclusive_scan with the associative operator
+// "a later entry that has a value wins".
+__device__ __forceinline__ void wave_last_scan(uint32_t &h, uint32_t &v) {
+#define HX_LAST_STEP(CTRL, MASK)                                                                           \
+    {                                                                                                      \
+        const uint32_t oh = dpp_move<CTRL, MASK>(0u, h), ov = dpp_move<CTRL, MASK>(0u, v);                 \
+        if (!h) {                                                                                          \
+            h = oh;                                                                                        \
+            v = ov;                                                                                        \
+        }                                                                                                  \
+    }
+    HX_LAST_STEP(kDppRowShr1, 0xf)
+    HX_LAST_STEP(kDppRowShr2, 0xf)
+    HX_LAST_STEP(kDppRowShr4, 0xf)
+    HX_LAST_STEP(kDppRowShr8, 0xf)
+    HX_LAST_STEP(kDppRowBcast15, 0xa)
+    HX_LAST_STEP(kDppRowBcast31, 0xc)
+#undef HX_LAST_STEP
+}
+
+// Exclusive prefix of segment sums carried in from earlier tiles: folds
+// predecessor statuses until one is a prefix (a tile that holds a segment
+// start, or that already resolved its own carry), computing any status that
+// stays unpublished (decoupled fallback).  One wave.
+template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_t tile, uint32_t tag) {
+    const int lane = lane_id();
+    uint32_t c_in = 0;
+    int64_t pred = (int64_t)tile - 1;
+    for (;;) {
+        const int64_t idx = pred - lane;
+        uint32_t flag, val;
+        uint32_t spins = 0;
+        for (;;) {
+            flag = kPrefix;
+            val = 0;
+            if (idx >= 0) {
+                const uint64_t wd = ld_relaxed(&p.status[idx]);
+                const uint32_t hi = (uint32_t)(wd >> 32);
+                flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
+                val = (uint32_t)wd;
+            }
+            const uint64_t pm = ballot(flag == kPrefix);
+            const uint64_t im = ballot(flag == kInvalid);
+            const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
+            const uint64_t missing = im & need;
+            if (missing == 0ull) break;
+            if (++spins >= kSpinLimit) {
+                const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
+                uint32_t fflag, fval;
+                seg_tile_status<TILE>(p, u, fflag, fval);
+                if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
+                spins = 0;
+                continue;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        const uint64_t pm = ballot(flag == kPrefix);
+        const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
+        c_in += wave_sum((lane <= first) ? val : 0u);
+        if (pm) break;
+        pred -= kWave;
+    }
+    return c_in;
+}
+
 // Block b processes tile b; see scan.hip for why there is no ticket counter
 // and how the fallback guarantees progress in any dispatch order.
+//
+// Per tile, LDS holds only segment bookkeeping (about 0.5 byte per value
+// plus kSlots words), never the values themselves:
+//   s_mask   bit q set when tile element q is the LAST element of a segment
+//            (q + 1 + t0 is an offset in (t0, t1]);
+//   s_wrank  per mask word, the popcount of the earlier words of its wave,
+//            so a set bit's rank among all set bits is a few LDS reads;
+//   s_val    the segment values, compacted by rank, kSlots per round.
+// Each lane keeps its elements' tile-local inclusive prefixes x in
+// registers.  A segment ending at element q is x(q) minus x at the previous
+// set bit, found with a "last set bit" scan (lanes by DPP, steps and waves
+// by carries); with no earlier set bit the segment began at or before the
+// tile start and takes the look-back carry.  Threads assigned to the
+// offsets then read their segment's value by rank and write it.
+//
+// The tile's offset range comes from the map built by seg_tile_map_kernel,
+// so the offsets a block needs are loaded once, right after its values,
+// with no search on the critical path.  Only the segment already open at the
+// tile start needs the carry from earlier tiles: every other output is
+// written first, and wave 0 looks back last, when the rest of the block is
+// done (polling earlier, between two barriers, held every wave of the block
+// and cost ~15% at 2^27 values).
 template <int WAVES, int STEPS>
 __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams p) {
-    static_assert(WAVES >= 4, "waves 1-3 run the boundary searches");
+    static_assert(STEPS % 8 == 0, "each lane ranks whole mask words");
     constexpr int kWaveElems = SegTile<WAVES, STEPS>::kWaveElems;
     constexpr int kTile = SegTile<WAVES, STEPS>::kElems;
     constexpr int kThreads = WAVES * kWave;
-    __shared__ uint64_t s_bound[3];
+    constexpr int kWords = kTile / 32;
+    constexpr int kWaveWords = kWaveElems / 32;
+    constexpr int kLaneWords = kWaveWords / kWave;
     __shared__ uint32_t s_wave_tot[WAVES];
-    __shared__ uint32_t s_carry;
-    // Eb[4 + i] = tile-local inclusive prefix at element i, Eb[3] = 0, so
-    // the exclusive prefix at i is Eb[3 + i].  The 4-word offset keeps every
-    // lane's four prefixes one aligned 16-byte LDS store (conflict-free;
-    // four scalar stores at a 4-word lane stride conflicted 4-way).
-    __shared__ __attribute__((aligned(16))) uint32_t Eb[kTile + 4];
+    __shared__ uint32_t s_wave_pop[WAVES];
+    __shared__ uint32_t s_wave_last[WAVES]; // x at the wave's last set bit
+    __shared__ uint32_t s_hpref;
+    __shared__ uint32_t s_open; // in-tile part of the open segment
+    __shared__ uint32_t s_mask[kWords];
+    __shared__ uint32_t s_wrank[kWords];
+    __shared__ uint32_t s_val[kSlots];
 
     const uint64_t tile = blockIdx.x;
     const uint32_t tag = p.tag;
@@ -138,12 +209,24 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
     const int lane = lane_id();
     const uint64_t t0 = tile * kTile;
     const uint64_t t1 = (t0 + kTile < p.n) ? t0 + kTile : p.n;
+    const uint64_t tlen = t1 - t0;
     const uint64_t e0 = t0 + (uint64_t)w * kWaveElems + (uint64_t)lane * 4;
+    const uint64_t kmax = p.segments + 1;
 
-    // Issue the value loads first; the searches below overlap them.  Whole
-    // tiles use a block-uniform base and one 32-bit lane offset.
+    // Offsets of the tile: k_lo = ub(t0) (segment of t0 is k_lo - 1),
+    // k_hi1 = ub(t1), k_star = lb(t1) = ub(t1 - 1) (segment of t1-1 is
+    // k_star - 1).  Clamped so malformed offsets stay in bounds.
+    uint64_t k_lo = p.ub_map[tile], k_hi1 = p.ub_map[tile + 1], k_star = p.lb_map[tile + 1];
+    k_lo = k_lo < kmax ? k_lo : kmax;
+    k_hi1 = k_hi1 < k_lo ? k_lo : (k_hi1 < kmax ? k_hi1 : kmax);
+    k_star = k_star < kmax ? k_star : kmax;
+
+    for (int i = threadIdx.x; i < kWords; i += kThreads) s_mask[i] = 0u;
+    if (threadIdx.x == 0) s_open = 0u;
+
+    // Values first, with a block-uniform base for whole tiles.
     uint32_t x[STEPS][4];
-    if (t1 - t0 == (uint64_t)kTile) {
+    if (tlen == (uint64_t)kTile) {
         const char *base = (const char *)(p.values + t0);
         const uint32_t lane_off =
             ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * 4u;
@@ -171,17 +254,16 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
             }
         }
     }
+    // Then the first kThreads segment ends of the tile (k = k_lo + thread)
+    // and their starts, plus the starts of the segments holding t0 and t1-1.
+    const uint64_t kq = k_lo + threadIdx.x;
+    const bool have_q = kq < k_hi1 && kq >= 1;
+    const uint64_t ob_q = have_q ? off_at(p, kq) : 0, oa_q = have_q ? off_at(p, kq - 1) : 0;
+    const uint64_t first_start = k_lo >= 1 ? off_at(p, k_lo - 1) : 0;
+    uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
+    if (h > t1 - 1) h = t1 - 1; // only reachable with malformed offsets
 
-    // k_lo = ub(t0): first offset past the tile start (segment of t0 is
-    // k_lo - 1); k_hi1 = ub(t1); k_star = ub(t1 - 1) (segment of t1-1 is
-    // k_star - 1).
-    if (w >= 1) {
-        const uint64_t v = (w == 1) ? t0 : (w == 2) ? t1 : t1 - 1;
-        const uint64_t r = wave_upper_bound(p, v);
-        if (lane == 0) s_bound[w - 1] = r;
-    }
-
-    // Tile-local inclusive prefix of the values (mod 2^32).
+    // Wave-local inclusive prefix of the values (mod 2^32).
     uint32_t carry = 0;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
@@ -201,102 +283,206 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
     }
     if (lane == 0) s_wave_tot[w] = carry;
     __syncthreads();
-    uint32_t wave_excl = 0;
+
+    // Tile-local prefixes, and the segment-end marks.
+    uint32_t wave_excl = 0, total = 0;
 #pragma unroll
-    for (int k = 0; k < WAVES; ++k)
-        if (k < w) wave_excl += s_wave_tot[k];
-#pragma unroll
-    for (int j = 0; j < STEPS; ++j) {
-        const int le = w * kWaveElems + j * (kWave * 4) + lane * 4;
-        u32x4 v;
-        v.x = wave_excl + x[j][0];
-        v.y = wave_excl + x[j][1];
-        v.z = wave_excl + x[j][2];
-        v.w = wave_excl + x[j][3];
-        *(u32x4 *)&Eb[4 + le] = v;
+    for (int k = 0; k < WAVES; ++k) {
+        const uint32_t t = s_wave_tot[k];
+        if (k < w) wave_excl += t;
+        total += t;
     }
-    if (threadIdx.x == 0) Eb[3] = 0;
-    __syncthreads();
-    const uint32_t *E = Eb + 3; // E[i]: exclusive prefix at element i
-
-    const uint64_t k_lo = s_bound[0];
-    const uint64_t k_hi1 = s_bound[1];
-    const uint64_t k_star = s_bound[2];
-    const uint64_t tlen = t1 - t0;
-    const uint32_t total = E[tlen];
-
-    if (w == 0) {
-        // Start of the segment holding t1-1, and of the one holding t0.
-        uint64_t h = k_star >= 1 ? off_at(p, k_star - 1) : 0;
-        if (h > t1 - 1) h = t1 - 1; // only reachable with malformed offsets
-        const uint64_t first_start = k_lo >= 1 ? off_at(p, k_lo - 1) : 0;
-        const bool has_head = h >= t0;
-        const bool needs_carry = tile > 0 && first_start < t0;
-        uint32_t c_in = 0;
-        if (has_head) {
-            if (lane == 0) st_relaxed(&p.status[tile], status_word(tag, kPrefix, total - E[h - t0]));
-        } else if (tile > 0 && lane == 0) {
-            st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) x[j][c] += wave_excl;
+    for (uint64_t k = kq; k < k_hi1; k += kThreads) {
+        const uint64_t b = k == kq ? ob_q : off_at(p, k);
+        if (b > t0 && b <= t1) {
+            const uint32_t q = (uint32_t)(b - 1 - t0);
+            atomicOr(&s_mask[q >> 5], 1u << (q & 31));
         }
-        if (needs_carry || (!has_head && tile > 0)) {
-            // Look back over predecessors until a prefix (a tile holding a
-            // segment start, or one that already resolved its carry).
-            int64_t pred = (int64_t)tile - 1;
-            for (;;) {
-                const int64_t idx = pred - lane;
-                uint32_t flag, val;
-                uint32_t spins = 0;
-                for (;;) {
-                    flag = kPrefix;
-                    val = 0;
-                    if (idx >= 0) {
-                        const uint64_t wd = ld_relaxed(&p.status[idx]);
-                        const uint32_t hi = (uint32_t)(wd >> 32);
-                        flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
-                        val = (uint32_t)wd;
-                    }
-                    const uint64_t pm = ballot(flag == kPrefix);
-                    const uint64_t im = ballot(flag == kInvalid);
-                    const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
-                    const uint64_t missing = im & need;
-                    if (missing == 0ull) break;
-                    if (++spins >= kSpinLimit) {
-                        const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
-                        uint32_t fflag, fval;
-                        seg_tile_status<kTile>(p, u, fflag, fval);
-                        if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
-                        spins = 0;
-                        continue;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                const uint64_t pm = ballot(flag == kPrefix);
-                const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
-                c_in += wave_sum((lane <= first) ? val : 0u);
-                if (pm) break;
-                pred -= kWave;
+    }
+    // The segment holding t1-1 starts at h; its tile-local start prefix
+    // x(h - 1) is published with the tile's status.
+    if (h > t0) {
+        const uint32_t q = (uint32_t)(h - 1 - t0);
+        if ((int)(q / kWaveElems) == w && (int)((q % (kWave * 4)) / 4) == lane) {
+            const int jq = (int)((q % kWaveElems) / (kWave * 4)), cq = (int)(q % 4);
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (j == jq && c == cq) s_hpref = x[j][c];
+        }
+    }
+    __syncthreads();
+
+    const bool has_head = h >= t0;
+    const bool needs_carry = tile > 0 && first_start < t0;
+    if (w == 0 && lane == 0) {
+        if (has_head)
+            st_relaxed(&p.status[tile], status_word(tag, kPrefix, total - (h > t0 ? s_hpref : 0u)));
+        else if (tile > 0)
+            st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
+    }
+
+    // Per wave: popcounts for ranking, and the value at its last set bit.
+    {
+        uint32_t words[kLaneWords];
+        uint32_t lane_pop = 0;
+#pragma unroll
+        for (int i = 0; i < kLaneWords; ++i) {
+            words[i] = s_mask[w * kWaveWords + lane * kLaneWords + i];
+            lane_pop += __builtin_popcount(words[i]);
+        }
+        const uint32_t pop_incl = wave_inclusive_scan<OpSum, uint32_t>(lane_pop);
+        uint32_t run = pop_incl - lane_pop;
+#pragma unroll
+        for (int i = 0; i < kLaneWords; ++i) {
+            s_wrank[w * kWaveWords + lane * kLaneWords + i] = run;
+            run += __builtin_popcount(words[i]);
+        }
+        if (lane == kWave - 1) s_wave_pop[w] = pop_incl;
+        // Highest set bit of the wave's range (wave-local position).
+        const uint64_t m = ballot(lane_pop != 0u);
+        if (m != 0ull) {
+            const int L = 63 - __builtin_clzll(m);
+            int top = -1;
+#pragma unroll
+            for (int i = 0; i < kLaneWords; ++i)
+                if (words[i]) top = (lane * kLaneWords + i) * 32 + 31 - __builtin_clz(words[i]);
+            const int qq = __builtin_amdgcn_readlane(top, L);
+            if ((qq % (kWave * 4)) / 4 == lane) {
+                const int jq = qq / (kWave * 4), cq = qq % 4;
+#pragma unroll
+                for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (j == jq && c == cq) s_wave_last[w] = x[j][c];
             }
         }
-        if (!has_head && tile > 0 && lane == 0) st_relaxed(&p.status[tile], status_word(tag, kPrefix, c_in + total));
-        if (lane == 0) s_carry = c_in;
     }
     __syncthreads();
-    const uint32_t c_in = s_carry;
 
-    // Segments s = k-1 whose end offset off(k) lies in (t0, t1]; tile 0 also
-    // owns the empty segments that end at 0.
-    uint64_t k_first = tile == 0 ? 1 : (k_lo > 1 ? k_lo : 1);
-    uint64_t k_last = k_hi1 >= 1 ? k_hi1 - 1 : 0;
-    if (k_last > p.segments) k_last = p.segments;
-    for (uint64_t k = k_first + threadIdx.x; k <= k_last; k += kThreads) {
-        const uint64_t b = off_at(p, k);
-        uint64_t a = off_at(p, k - 1);
-        if (a > b) a = b; // malformed: treat as empty
-        if (b < t0 || b > t1) continue; // malformed (non-monotonic) offsets
-        const uint64_t a_loc = (a > t0 ? a : t0) - t0;
-        uint32_t v = E[b - t0] - E[a_loc];
-        if (a < t0) v += c_in;
-        p.out[k - 1] = v;
+    // The last set bit before this wave's range, and this wave's rank base.
+    uint32_t in_has = 0, in_val = 0, rank_base = 0, marks = 0;
+#pragma unroll
+    for (int k = 0; k < WAVES; ++k) {
+        const uint32_t pk = s_wave_pop[k];
+        if (k < w) {
+            rank_base += pk;
+            if (pk) {
+                in_has = 1u;
+                in_val = s_wave_last[k];
+            }
+        }
+        marks += pk;
+    }
+
+    // Tile 0 owns the empty segments that end at offset 0.
+    if (tile == 0)
+        for (uint64_t k = 1 + threadIdx.x; k < k_lo && k <= p.segments; k += kThreads) p.out[k - 1] = 0u;
+
+    const uint32_t rounds = marks == 0 ? 1u : (marks + kSlots - 1) / kSlots;
+    for (uint32_t round = 0; round < rounds; ++round) {
+        const uint32_t r0 = round * kSlots;
+        // Segment values of this wave's set bits whose rank is in the round.
+        uint32_t sc_has = in_has, sc_val = in_val; // last set bit before the step
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            const int word = w * kWaveWords + j * (kWave * 4 / 32) + (lane >> 3);
+            const uint32_t mw = s_mask[word];
+            const int sh = (lane & 7) * 4;
+            const uint32_t nib = (mw >> sh) & 0xFu;
+            // This lane's last set bit in the step, scanned across lanes.
+            uint32_t lh = nib != 0u;
+            uint32_t lv = (nib & 8u) ? x[j][3] : (nib & 4u) ? x[j][2] : (nib & 2u) ? x[j][1] : x[j][0];
+            wave_last_scan(lh, lv);
+            uint32_t eh = dpp_move<kDppWaveShr1>(0u, lh), ev = dpp_move<kDppWaveShr1>(0u, lv);
+            if (!eh) {
+                eh = sc_has;
+                ev = sc_val;
+            }
+            if (nib) {
+                const uint32_t rb = rank_base + s_wrank[word];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (nib & (1u << c)) {
+                        const uint32_t rank = rb + __builtin_popcount(mw & ((1u << (sh + c)) - 1u));
+                        if (rank >= r0 && rank - r0 < (uint32_t)kSlots) s_val[rank - r0] = x[j][c] - (eh ? ev : 0u);
+                        eh = 1u;
+                        ev = x[j][c];
+                    }
+                }
+            }
+            const uint32_t th = read_lane(lh, kWave - 1), tv = read_lane(lv, kWave - 1);
+            if (th) {
+                sc_has = 1u;
+                sc_val = tv;
+            }
+        }
+        __syncthreads();
+        // Segments s = k-1 whose end offset off(k) lies in (t0, t1].
+        for (uint64_t k = kq; k < k_hi1; k += kThreads) {
+            if (k == 0) continue;
+            const uint64_t b = k == kq ? ob_q : off_at(p, k);
+            uint64_t a = k == kq ? oa_q : off_at(p, k - 1);
+            if (a > b) a = b; // malformed: treat as empty
+            if (b <= t0 || b > t1) continue; // malformed (non-monotonic) offsets
+            if (a == b) {
+                if (round == 0) p.out[k - 1] = 0u;
+                continue;
+            }
+            const uint32_t q = (uint32_t)(b - 1 - t0);
+            const int qw = (int)(q / kWaveElems);
+            uint32_t rank = s_wrank[q >> 5] + __builtin_popcount(s_mask[q >> 5] & ((1u << (q & 31)) - 1u));
+            for (int k2 = 0; k2 < qw; ++k2) rank += s_wave_pop[k2];
+            if (rank < r0 || rank - r0 >= (uint32_t)kSlots) continue;
+            if (a < t0)
+                s_open = s_val[rank - r0]; // written after the look-back
+            else
+                p.out[k - 1] = s_val[rank - r0];
+        }
+        if (round + 1 < rounds) __syncthreads();
+    }
+
+    // The carry into the open segment, and the final status of a tile with
+    // no segment start (so later look-backs stop here).
+    if (needs_carry || (!has_head && tile > 0)) {
+        __syncthreads(); // s_open
+        if (w == 0) {
+            const uint32_t c_in = seg_lookback<kTile>(p, tile, tag);
+            if (lane == 0) {
+                if (!has_head) st_relaxed(&p.status[tile], status_word(tag, kPrefix, c_in + total));
+                if (needs_carry && k_lo < k_hi1 && k_lo >= 1 && k_lo <= p.segments) p.out[k_lo - 1] = s_open + c_in;
+            }
+        }
+    }
+}
+
+// The tile map: for every tile edge B_t = t * TILE (t < tiles) and for
+// B_tiles = n, ub_map[t] = #{k : off(k) <= B_t} and lb_map[t] =
+// #{k : off(k) < B_t}.  With sorted offsets, the edges with ub = k are those
+// in [off(k-1), off(k)) and those with lb = k are in (off(k-1), off(k)]
+// (off(-1) = 0 resp. -1, off(S+1) = infinity), so each thread takes one k
+// and writes the few edges of its interval: one coalesced pass over the
+// offsets instead of a search per tile.
+template <int TILE>
+__global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
+    const uint64_t tiles = p.total_tiles;
+    const uint64_t S = p.segments;
+    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
+    for (uint64_t k = (uint64_t)blockIdx.x * kBlock + threadIdx.x; k <= S + 1; k += nthreads) {
+        const uint64_t lo = k == 0 ? 0 : off_at(p, k - 1);
+        const uint64_t hi = k <= S ? off_at(p, k) : p.n + 1; // off_at clamps into [0, n]
+        // ub: edges in [lo, hi) (lo for k == 0 is 0: edges below off(0)).
+        for (uint64_t t = (lo + TILE - 1) / TILE; t < tiles && t * TILE < hi; ++t) p.ub_map[t] = (uint32_t)k;
+        if (lo <= p.n && p.n < hi) p.ub_map[tiles] = (uint32_t)k;
+        // lb: edges in (lo', hi] with lo' = off(k-1), or -1 for k == 0.
+        const uint64_t t_first = k == 0 ? 0 : lo / TILE + 1;
+        for (uint64_t t = t_first; t < tiles && t * TILE <= hi; ++t) p.lb_map[t] = (uint32_t)k;
+        if ((k == 0 || lo < p.n) && p.n <= hi) p.lb_map[tiles] = (uint32_t)k;
     }
 }
 
@@ -320,8 +506,10 @@ __global__ void validate_offsets_kernel(const uint32_t *offsets, uint64_t count,
 
 } // namespace
 
+// Look-back status words (8 bytes per tile), then the two tile maps.
 uint64_t segmented_workspace_bytes(const SegmentedArgs &a) {
-    return kLookbackOffset + ceil_div(a.n, kTile) * 8;
+    const uint64_t tiles = ceil_div(a.n, kTile);
+    return kLookbackOffset + tiles * 8 + 2 * (tiles + 1) * 4;
 }
 
 hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb,
@@ -341,8 +529,12 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     p.segments = a.num_segments;
     p.out = (uint32_t *)a.out;
     p.total_tiles = ceil_div(a.n, kTile);
-    p.hdr = (WorkspaceHeader *)ws;
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
+    p.ub_map = (uint32_t *)(p.status + p.total_tiles);
+    p.lb_map = p.ub_map + p.total_tiles + 1;
+    if (a.num_segments >= 0xFFFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu segments exceeds the u32 offset range",
+                    (unsigned long long)a.num_segments);
     if (p.total_tiles >= 0x80000000ull)
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
@@ -352,6 +544,10 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
         return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
+    uint64_t map_blocks = ceil_div(a.num_segments + 2, kBlock);
+    if (map_blocks > 2048) map_blocks = 2048;
+    hipLaunchKernelGGL((seg_tile_map_kernel<kTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream, p);
+    HX_TRY(check_launch("seg_tile_map_kernel"));
     hipLaunchKernelGGL((segmented_sum_kernel<kSegWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
                        dim3(kSegWaves * kWave), 0, stream, p);
     HX_TRY(check_launch("segmented_sum_kernel"));
