@@ -73,6 +73,10 @@ struct PackedStatus {
         __hip_atomic_compare_exchange_strong(&words[t], &cur, status_word(tag, flag, v), __ATOMIC_RELAXED,
                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Tile-level owner publication (same single store).
+    __device__ __forceinline__ void publish_tile(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        publish(t, tag, flag, v);
+    }
     __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
         const uint64_t w = ld_relaxed(&words[t]);
         const uint32_t hi = (uint32_t)(w >> 32);
@@ -84,11 +88,13 @@ struct PackedStatus {
 // f64 carries: each 64-bit status word holds (tag, flag, one 32-bit half of
 // the f64).  Entry t's aggregate lives in words [4t, 4t+1] and its inclusive
 // prefix in [4t+2, 4t+3]; a reader accepts a value only when both halves
-// carry the current tag, so no release/acquire ordering is needed.  A slot
-// can have several writers (owner and fallbacks): whoever moves the high
-// word from an old tag to this launch's tag with a CAS also writes the low
-// word, and everyone else leaves the slot alone, so halves of different
-// writers never mix.
+// carry the current tag, so no release/acquire ordering is needed.  A
+// superblock slot can have writers whose values differ in the last bits (its
+// owner, and fallbacks that rebuild it from its tiles in another order):
+// whoever moves the high word from an old tag to this launch's tag with a
+// CAS also writes the low word, and everyone else leaves the slot alone, so
+// halves of different writers never mix (publish).  Tile slots need no CAS
+// (publish_tile).
 struct F64Status {
     using C = double;
     uint64_t *words;
@@ -103,6 +109,16 @@ struct F64Status {
     }
     __device__ __forceinline__ void publish_if_unset(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
         publish(t, tag, flag, v);
+    }
+    // Tile-level owner publication, two plain stores and no CAS round trip.
+    // Safe without the CAS: a tile's inclusive prefix has one writer (its
+    // owner), and every writer of a tile's aggregate (owner or fallback)
+    // computes bit-identical values, so halves of different writers agree.
+    __device__ __forceinline__ void publish_tile(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        uint64_t *w = words + 4 * t + (flag == kPrefix ? 2 : 0);
+        st_relaxed(&w[0], status_word(tag, flag, (uint32_t)(b >> 32)));
+        st_relaxed(&w[1], status_word(tag, flag, (uint32_t)b));
     }
     __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
         const uint64_t *w = words + 4 * t;
@@ -410,12 +426,12 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
         const C agg = (C)tile_agg;
         C excl = Op::template identity<C>();
         if (tin == 0) {
-            if (lane == 0) st.publish(tile, p.tag, kPrefix, agg);
+            if (lane == 0) st.publish_tile(tile, p.tag, kPrefix, agg);
         } else {
-            if (lane == 0) st.publish(tile, p.tag, kAggregate, agg);
+            if (lane == 0) st.publish_tile(tile, p.tag, kAggregate, agg);
             KnownAgg<C> hook{agg};
             excl = lookback<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, st1, tile, line, tin, hook);
-            if (lane == 0) st.publish(tile, p.tag, kPrefix, Op::combine(excl, agg));
+            if (lane == 0) st.publish_tile(tile, p.tag, kPrefix, Op::combine(excl, agg));
         }
         if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
             st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, Op::combine(excl, agg));
