@@ -21,6 +21,17 @@ from .errors import (
     TransferFailed,
 )
 from .layout import Layout, StridedView
+from .vector_ops import (
+    PreparedMapReduction,
+    RocmDenseVectorOps,
+    dot,
+    norm_l1,
+    norm_l2,
+    norm_max,
+    prepare_dot,
+    prepare_norm_l2,
+    trace,
+)
 from .ops import (
     ArgMaxOp,
     CumProdOp,

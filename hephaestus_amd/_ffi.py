@@ -51,6 +51,8 @@ SCAN_INCLUSIVE, SCAN_EXCLUSIVE = 0, 1
 SCAN_FORWARD, SCAN_REVERSE = 0, 1
 # hx_distribution
 DIST_UNIFORM_INT, DIST_UNIFORM_REAL, DIST_NORMAL = 0, 1, 2
+MAP_SUM, MAP_DOT, MAP_NORM_L1, MAP_NORM_L2, MAP_NORM_MAX = 0, 1, 2, 3, 4
+VEC_SCALE, VEC_AXPY, VEC_XPAY, VEC_ADD, VEC_SUB, VEC_MUL, VEC_DIV = 0, 1, 2, 3, 4, 5, 6
 
 
 class HxLayout(Structure):
@@ -135,6 +137,11 @@ SIGNATURES = {
     "hx_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),
     "hx_prepare_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, POINTER(P)]),
     "hx_validate_segment_offsets": (I32, [P, P, U64, U64]),
+    "hx_map_reduce": (I32, [P, I32, I32, P, U64, LP, P, U64, LP, P, U64, P]),
+    "hx_prepare_map_reduce": (I32, [P, I32, I32, P, U64, LP, P, U64, LP, P, U64, POINTER(P)]),
+    "hx_trace": (I32, [P, I32, P, U64, LP, P, U64, P]),
+    "hx_vector_update": (I32, [P, I32, I32, P, U64, P, U64, c_float, P]),
+    "hx_vector_binary": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),
     "hx_plan_dispatch": (I32, [P, P]),
     "hx_plan_destroy": (I32, [P]),
     "hx_plan_workspace_bytes": (I32, [P, POINTER(U64)]),

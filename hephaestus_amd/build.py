@@ -27,6 +27,9 @@ SOURCES = [
     "csrc/segmented.hip",
     "csrc/random.hip",
     "csrc/copy.hip",
+    "csrc/map_reduce.hip",
+    "csrc/vector.hip",
+    "csrc/dense_vector.cpp",
 ]
 HEADERS = ["csrc/hx_device.hpp", "csrc/hx_internal.hpp"]
 ARCH = "gfx950"

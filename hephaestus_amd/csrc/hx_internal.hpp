@@ -179,6 +179,22 @@ hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_byte
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,
                                      uint64_t num_offsets, uint64_t n);
 
+struct MapReduceArgs {
+    hx_map_reduction map;
+    hx_dtype dtype;
+    const void *a, *b;
+    hx_layout a_layout, b_layout;
+    uint64_t n;
+    bool flat; // both operands dense row-major with agreeing 16-byte phase
+    void *out;
+};
+uint64_t map_reduce_workspace_bytes(uint64_t n);
+hx_status launch_map_reduce(const MapReduceArgs &args, void *ws, hipStream_t stream);
+
+// Elementwise f32 vector forms: out[i] = op(t[i], s[i], factor).
+hx_status launch_vector_op(hx_vector_op op, const float *t, const float *s, float *out, uint64_t n,
+                           float factor, hipStream_t stream);
+
 // Stream-ordered device-to-device copy of `bytes` bytes (a streaming kernel).
 hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t stream);
 

@@ -8,6 +8,8 @@
 //   FullReductionOps                          crates/hephaestus-core/src/domain/reduction.rs:243-309
 //   AxisReductionOps                          crates/hephaestus-core/src/domain/reduction.rs:74-223
 //   ScanOps / ScanDirection                   crates/hephaestus-core/src/domain/scan.rs:36-264
+//   DenseVectorOps                            crates/hephaestus-core/src/domain/vector.rs:57-200
+//   dot / trace / norms                       crates/hephaestus-rocm/src/application/linalg/norms.rs:394-490
 //   HephaestusError                           crates/hephaestus-core/src/domain/error.rs:8-58
 // Errors are thrown as hephaestus::Error carrying the variant and the
 // native message; every entry point validates before it writes, so a
@@ -403,6 +405,129 @@ class RocmSegmentedReductionOps {
     }
     void validate_offsets(RocmDevice &dev, const RocmBuffer<uint32_t> &offsets, uint64_t n) const {
         check(hx_validate_segment_offsets(dev.raw(), offsets.device_ptr(), offsets.len(), n));
+    }
+};
+
+// --------------------------------------------------------- map-reductions
+// dot / trace / norm_l1 / norm_l2 / norm_max (rocm linalg/norms.rs:394-490):
+// strided views in, a new one-element device buffer out.
+template <typename T> RocmBuffer<T> dot(RocmDevice &dev, StridedView<T> a, StridedView<T> b, hx_stream stream = nullptr) {
+    RocmBuffer<T> out = dev.alloc_uninitialized<T>(1);
+    check(hx_map_reduce(dev.raw(), HX_MAP_DOT, Scalar<T>::dtype, a.buffer.device_ptr(), a.buffer.len(), a.layout.raw(),
+                        b.buffer.device_ptr(), b.buffer.len(), b.layout.raw(), out.device_ptr(), 1, stream));
+    return out;
+}
+template <typename T> RocmBuffer<T> trace(RocmDevice &dev, StridedView<T> m, hx_stream stream = nullptr) {
+    RocmBuffer<T> out = dev.alloc_uninitialized<T>(1);
+    check(hx_trace(dev.raw(), Scalar<T>::dtype, m.buffer.device_ptr(), m.buffer.len(), m.layout.raw(),
+                   out.device_ptr(), 1, stream));
+    return out;
+}
+namespace detail {
+template <typename T> RocmBuffer<T> norm(RocmDevice &dev, hx_map_reduction kind, StridedView<T> v, hx_stream stream) {
+    RocmBuffer<T> out = dev.alloc_uninitialized<T>(1);
+    check(hx_map_reduce(dev.raw(), kind, Scalar<T>::dtype, v.buffer.device_ptr(), v.buffer.len(), v.layout.raw(),
+                        nullptr, 0, nullptr, out.device_ptr(), 1, stream));
+    return out;
+}
+} // namespace detail
+template <typename T> RocmBuffer<T> norm_l1(RocmDevice &d, StridedView<T> v, hx_stream s = nullptr) {
+    return detail::norm(d, HX_MAP_NORM_L1, v, s);
+}
+template <typename T> RocmBuffer<T> norm_l2(RocmDevice &d, StridedView<T> v, hx_stream s = nullptr) {
+    return detail::norm(d, HX_MAP_NORM_L2, v, s);
+}
+template <typename T> RocmBuffer<T> norm_max(RocmDevice &d, StridedView<T> v, hx_stream s = nullptr) {
+    return detail::norm(d, HX_MAP_NORM_MAX, v, s);
+}
+
+// ------------------------------------------------------- DenseVectorOps
+// DenseVectorOps<RocmDevice, f32> (core vector.rs:57-200): whole buffers as
+// vectors, scalar results returned to the host.
+class RocmDenseVectorOps {
+  public:
+    // A prepared dot / L2 norm: the plan, its output and the allocations it
+    // was prepared against.
+    struct Prepared {
+        PreparedPlan plan;
+        RocmBuffer<float> output;
+        const float *a, *b;
+    };
+
+    void copy_vector(RocmDevice &dev, const RocmBuffer<float> &source, RocmBuffer<float> &target) const {
+        if (source.len() != target.len())
+            throw Error(ErrorKind::LengthMismatch, "copy_vector length mismatch", source.len(), target.len());
+        if (source.len()) dev.copy_buffer(source, target);
+    }
+    void scale_vector(RocmDevice &dev, RocmBuffer<float> &target, float factor) const {
+        check(hx_vector_update(dev.raw(), HX_VEC_SCALE, HX_DTYPE_F32, target.device_ptr(), target.len(), nullptr, 0,
+                               factor, nullptr));
+    }
+    void axpy(RocmDevice &dev, RocmBuffer<float> &target, const RocmBuffer<float> &source, float factor) const {
+        check(hx_vector_update(dev.raw(), HX_VEC_AXPY, HX_DTYPE_F32, target.device_ptr(), target.len(),
+                               source.device_ptr(), source.len(), factor, nullptr));
+    }
+    void xpay(RocmDevice &dev, RocmBuffer<float> &target, const RocmBuffer<float> &source, float factor) const {
+        check(hx_vector_update(dev.raw(), HX_VEC_XPAY, HX_DTYPE_F32, target.device_ptr(), target.len(),
+                               source.device_ptr(), source.len(), factor, nullptr));
+    }
+    void subtract_into(RocmDevice &d, const RocmBuffer<float> &l, const RocmBuffer<float> &r, RocmBuffer<float> &o) const {
+        binary(d, HX_VEC_SUB, l, r, o);
+    }
+    void add_into(RocmDevice &d, const RocmBuffer<float> &l, const RocmBuffer<float> &r, RocmBuffer<float> &o) const {
+        binary(d, HX_VEC_ADD, l, r, o);
+    }
+    void multiply_into(RocmDevice &d, const RocmBuffer<float> &l, const RocmBuffer<float> &r, RocmBuffer<float> &o) const {
+        binary(d, HX_VEC_MUL, l, r, o);
+    }
+    void divide_into(RocmDevice &d, const RocmBuffer<float> &l, const RocmBuffer<float> &r, RocmBuffer<float> &o) const {
+        binary(d, HX_VEC_DIV, l, r, o);
+    }
+    Prepared prepare_dot(RocmDevice &dev, const RocmBuffer<float> &left, const RocmBuffer<float> &right) const {
+        if (left.len() != right.len())
+            throw Error(ErrorKind::LengthMismatch, "dot length mismatch", left.len(), right.len());
+        return prepare(dev, HX_MAP_DOT, left, &right);
+    }
+    float dot_prepared(RocmDevice &dev, const Prepared &p, const RocmBuffer<float> &left,
+                       const RocmBuffer<float> &right) const {
+        if (p.a != left.device_ptr() || p.b != right.device_ptr())
+            throw Error(ErrorKind::DispatchFailed, "prepared dot received different device allocations");
+        p.plan.dispatch();
+        return dev.download_owned(p.output)[0];
+    }
+    Prepared prepare_norm_l2(RocmDevice &dev, const RocmBuffer<float> &v) const {
+        return prepare(dev, HX_MAP_NORM_L2, v, nullptr);
+    }
+    float norm_l2_prepared(RocmDevice &dev, const Prepared &p, const RocmBuffer<float> &v) const {
+        if (p.a != v.device_ptr())
+            throw Error(ErrorKind::DispatchFailed, "prepared norm received a different device allocation");
+        p.plan.dispatch();
+        return dev.download_owned(p.output)[0];
+    }
+    float norm_l1(RocmDevice &dev, const RocmBuffer<float> &v) const {
+        const Layout l = Layout::c_contiguous({v.len()});
+        return dev.download_owned(hephaestus::norm_l1<float>(dev, {v, l}))[0];
+    }
+    float norm_max(RocmDevice &dev, const RocmBuffer<float> &v) const {
+        const Layout l = Layout::c_contiguous({v.len()});
+        return dev.download_owned(hephaestus::norm_max<float>(dev, {v, l}))[0];
+    }
+
+  private:
+    void binary(RocmDevice &d, hx_vector_op op, const RocmBuffer<float> &l, const RocmBuffer<float> &r,
+                RocmBuffer<float> &o) const {
+        check(hx_vector_binary(d.raw(), op, HX_DTYPE_F32, l.device_ptr(), l.len(), r.device_ptr(), r.len(),
+                               o.device_ptr(), o.len(), nullptr));
+    }
+    Prepared prepare(RocmDevice &dev, hx_map_reduction kind, const RocmBuffer<float> &a,
+                     const RocmBuffer<float> *b) const {
+        const Layout la = Layout::c_contiguous({a.len()});
+        RocmBuffer<float> out = dev.alloc_uninitialized<float>(1);
+        hx_plan *plan = nullptr;
+        check(hx_prepare_map_reduce(dev.raw(), kind, HX_DTYPE_F32, a.device_ptr(), a.len(), la.raw(),
+                                    b ? b->device_ptr() : nullptr, b ? b->len() : 0, b ? la.raw() : nullptr,
+                                    out.device_ptr(), 1, &plan));
+        return Prepared{PreparedPlan(plan), std::move(out), a.device_ptr(), b ? b->device_ptr() : nullptr};
     }
 };
 

@@ -333,6 +333,71 @@ hx_status hx_prepare_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype,
 hx_status hx_validate_segment_offsets(hx_device *dev, const uint32_t *offsets,
                                       uint64_t num_offsets, uint64_t n);
 
+/* ------------------------------------- map-reductions (dot, norms, trace) */
+
+/* rocm linalg/norms.rs:32-490: a map fused into a full reduction.  `out`
+ * receives one element of `dtype`.  DOT needs b with the same logical shape
+ * as a ("dot product shape mismatch: lhs [..], rhs [..]", norms.rs:402-411);
+ * the other maps read a only (b may be NULL).  NORM_L2 is f32 only
+ * (norms.rs:452-456: L2NormScalar is implemented for f32).  f32 sums
+ * accumulate in f64 (products and squares of f32 values are exact there);
+ * integer sums and products wrap mod 2^32.  Empty operands give the
+ * identity: 0, or for NORM_MAX the MaxOp identity (ops.rs:956-958). */
+typedef enum hx_map_reduction {
+    HX_MAP_SUM = 0,      /* IdentityMap + SumOp (trace)                  */
+    HX_MAP_DOT = 1,      /* DotMap: sum of a[i] * b[i]                   */
+    HX_MAP_NORM_L1 = 2,  /* AbsMap: sum of |a[i]|                        */
+    HX_MAP_NORM_L2 = 3,  /* SquareMap + sqrt: sqrt(sum of a[i]^2)        */
+    HX_MAP_NORM_MAX = 4  /* MaxAbsMap + MaxOp: max of |a[i]|             */
+} hx_map_reduction;
+hx_status hx_map_reduce(hx_device *dev, hx_map_reduction map, hx_dtype dtype,
+                        const void *a, uint64_t a_buf_len,
+                        const hx_layout *a_layout, const void *b,
+                        uint64_t b_buf_len, const hx_layout *b_layout,
+                        void *out, uint64_t out_buf_len, hx_stream stream);
+/* prepare_map_reduction (rocm prepared_map_reduction.rs:63-213): binds the
+ * operands; dispatch re-reads them. */
+hx_status hx_prepare_map_reduce(hx_device *dev, hx_map_reduction map,
+                                hx_dtype dtype, const void *a,
+                                uint64_t a_buf_len, const hx_layout *a_layout,
+                                const void *b, uint64_t b_buf_len,
+                                const hx_layout *b_layout, void *out,
+                                uint64_t out_buf_len, hx_plan **plan);
+/* trace (norms.rs:416-444): rank-2 square view ("trace requires a square
+ * matrix, got shape [r, c]"), summed along the diagonal view with stride
+ * strides[0] + strides[1]; an empty matrix gives 0. */
+hx_status hx_trace(hx_device *dev, hx_dtype dtype, const void *in,
+                   uint64_t in_buf_len, const hx_layout *in_layout, void *out,
+                   uint64_t out_buf_len, hx_stream stream);
+
+/* ------------------------------------------- dense f32 vector recurrences */
+
+/* DenseVectorOps (core vector.rs:57-200; rocm vector.rs:36-72, 141-271), f32
+ * only like the reference's ROCm implementation.  Lengths must agree
+ * (HX_ERR_LENGTH_MISMATCH with (left, right) lengths, vector.rs:119-128);
+ * empty vectors are a no-op.
+ *   SCALE  target = target * factor              (source unused)
+ *   AXPY   target = fmaf(factor, source, target)
+ *   XPAY   target = fmaf(factor, target, source)
+ * hx_vector_binary: out = left op right, op one of ADD SUB MUL DIV. */
+typedef enum hx_vector_op {
+    HX_VEC_SCALE = 0,
+    HX_VEC_AXPY = 1,
+    HX_VEC_XPAY = 2,
+    HX_VEC_ADD = 3,
+    HX_VEC_SUB = 4,
+    HX_VEC_MUL = 5,
+    HX_VEC_DIV = 6
+} hx_vector_op;
+hx_status hx_vector_update(hx_device *dev, hx_vector_op op, hx_dtype dtype,
+                           void *target, uint64_t target_len,
+                           const void *source, uint64_t source_len,
+                           float factor, hx_stream stream);
+hx_status hx_vector_binary(hx_device *dev, hx_vector_op op, hx_dtype dtype,
+                           const void *left, uint64_t left_len,
+                           const void *right, uint64_t right_len, void *out,
+                           uint64_t out_len, hx_stream stream);
+
 /* ---------------------------------------------------------------- plans */
 
 /* dispatch_full / dispatch_prepared / dispatch_scan (core reduction.rs:

@@ -79,6 +79,75 @@ static void kadd(kacc *k, double v) {
 }
 static double kval(const kacc *k) { return k->s + k->c; }
 
+/* --------------------------------------------------- map-reductions
+ * crates/hephaestus-rocm/src/application/linalg/norms.rs:32-490: DotMap
+ * "lhs * rhs", AbsMap "abs(lhs)", SquareMap + sqrt, MaxAbsMap with MaxOp.
+ * Integer forms wrap mod 2^32 (abs(INT_MIN) = INT_MIN as in C); f32 forms
+ * return the compensated f64 value of the exact mapped terms, together with
+ * the sum of their magnitudes for the error bound. */
+
+uint32_t hxo_dot_u32(const uint32_t *a, const uint32_t *b, uint64_t n) {
+    uint32_t s = 0;
+    for (uint64_t i = 0; i < n; ++i) s += a[i] * b[i];
+    return s;
+}
+
+double hxo_dot_f32(const float *a, const float *b, uint64_t n, double *abs_sum) {
+    kacc s = {0, 0}, m = {0, 0};
+    for (uint64_t i = 0; i < n; ++i) {
+        const double t = (double)a[i] * (double)b[i]; /* exact in f64 */
+        kadd(&s, t);
+        kadd(&m, fabs(t));
+    }
+    if (abs_sum) *abs_sum = kval(&m);
+    return kval(&s);
+}
+
+static uint32_t wrap_abs_i32(int32_t x) { return x < 0 ? 0u - (uint32_t)x : (uint32_t)x; }
+
+uint32_t hxo_norm_l1_i32(const int32_t *x, uint64_t n) {
+    uint32_t s = 0;
+    for (uint64_t i = 0; i < n; ++i) s += wrap_abs_i32(x[i]);
+    return s;
+}
+
+double hxo_norm_l1_f32(const float *x, uint64_t n) {
+    kacc s = {0, 0};
+    for (uint64_t i = 0; i < n; ++i) kadd(&s, fabs((double)x[i]));
+    return kval(&s);
+}
+
+/* sum of squares (exact terms), compensated; the caller takes the root. */
+double hxo_sum_squares_f32(const float *x, uint64_t n) {
+    kacc s = {0, 0};
+    for (uint64_t i = 0; i < n; ++i) kadd(&s, (double)x[i] * (double)x[i]);
+    return kval(&s);
+}
+
+int32_t hxo_norm_max_i32(const int32_t *x, uint64_t n) {
+    int32_t m = INT32_MIN; /* MaxOp identity */
+    for (uint64_t i = 0; i < n; ++i) {
+        const int32_t a = (int32_t)wrap_abs_i32(x[i]);
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+float hxo_norm_max_f32(const float *x, uint64_t n) {
+    float m = -FLT_MAX; /* f32::MIN */
+    for (uint64_t i = 0; i < n; ++i) {
+        const float a = fabsf(x[i]);
+        if (!isnan(a) && a > m) m = a;
+    }
+    return m;
+}
+
+/* out[i] = fmaf(f, x[i], y[i]) (C99 fmaf, one rounding): axpy is
+ * (x, y) = (source, target), xpay (target, source); rocm vector.rs:36-72. */
+void hxo_fma_arrays(const float *x, const float *y, float f, uint64_t n, float *out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = fmaf(f, x[i], y[i]);
+}
+
 /* ------------------------------------------------------ full reductions */
 
 uint32_t hxo_sum_u32(const uint32_t *x, uint64_t n) {

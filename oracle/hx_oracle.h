@@ -98,6 +98,16 @@ void hxo_segmented_sum_u32(const uint32_t *x, uint64_t n, const uint32_t *offset
  * (capacity `cap` >= S+1 entries). */
 uint64_t hxo_geometric_offsets(uint64_t n, double mean, uint64_t seed, uint32_t *offsets, uint64_t cap);
 
+/* ---- map-reductions (dot, norms) ---- */
+uint32_t hxo_dot_u32(const uint32_t *a, const uint32_t *b, uint64_t n);
+double hxo_dot_f32(const float *a, const float *b, uint64_t n, double *abs_sum);
+uint32_t hxo_norm_l1_i32(const int32_t *x, uint64_t n);
+double hxo_norm_l1_f32(const float *x, uint64_t n);
+double hxo_sum_squares_f32(const float *x, uint64_t n);
+int32_t hxo_norm_max_i32(const int32_t *x, uint64_t n);
+float hxo_norm_max_f32(const float *x, uint64_t n);
+void hxo_fma_arrays(const float *x, const float *y, float f, uint64_t n, float *out);
+
 /* ---- CPU baselines (timed, not checkers) ---- */
 double hxo_sum_f32_threads(const float *x, uint64_t n, int threads);
 void hxo_scan_excl_u32_threads(const uint32_t *x, uint64_t n, uint32_t *out, int threads);

@@ -52,6 +52,14 @@ _SIG = {
     "hxo_check_scan_f32": (c_uint64, [c_void_p, c_void_p, c_uint64, c_int, c_uint64, POINTER(c_double)]),
     "hxo_segmented_sum_u32": (None, [c_void_p, c_uint64, c_void_p, c_uint64, c_void_p]),
     "hxo_geometric_offsets": (c_uint64, [c_uint64, c_double, c_uint64, c_void_p, c_uint64]),
+    "hxo_dot_u32": (c_uint32, [c_void_p, c_void_p, c_uint64]),
+    "hxo_dot_f32": (c_double, [c_void_p, c_void_p, c_uint64, POINTER(c_double)]),
+    "hxo_norm_l1_i32": (c_uint32, [c_void_p, c_uint64]),
+    "hxo_norm_l1_f32": (c_double, [c_void_p, c_uint64]),
+    "hxo_sum_squares_f32": (c_double, [c_void_p, c_uint64]),
+    "hxo_norm_max_i32": (c_int32, [c_void_p, c_uint64]),
+    "hxo_norm_max_f32": (c_float, [c_void_p, c_uint64]),
+    "hxo_fma_arrays": (None, [c_void_p, c_void_p, c_float, c_uint64, c_void_p]),
     "hxo_sum_f32_threads": (c_double, [c_void_p, c_uint64, c_int]),
     "hxo_scan_excl_u32_threads": (None, [c_void_p, c_uint64, c_void_p, c_int]),
 }
@@ -110,6 +118,55 @@ def uniform_real(n: int, seed: int, lo: float, hi: float) -> np.ndarray:
 def normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     lib().hxo_fill_normal(_ptr(out), n, seed, mean, std)
+    return out
+
+
+# ---- map-reductions (norms.rs:32-490) ----------------------------------------
+def dot(a: np.ndarray, b: np.ndarray):
+    """u32/i32: wrapped Σ a·b (same dtype).  f32: (f64 Σ a·b of exact products,
+    Σ|a·b|)."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype
+    if a.dtype == np.float32:
+        m = c_double()
+        return float(lib().hxo_dot_f32(_ptr(a), _ptr(b), a.size, ctypes.byref(m))), float(m.value)
+    v = lib().hxo_dot_u32(_ptr(a.view(np.uint32)), _ptr(b.view(np.uint32)), a.size)
+    return np.array([v], dtype=np.uint32).view(a.dtype)[0]
+
+
+def norm_l1(x: np.ndarray):
+    """u32: wrapped Σx; i32: wrapped Σ|x| (|INT_MIN| = INT_MIN); f32: f64 Σ|x|."""
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.float32:
+        return float(lib().hxo_norm_l1_f32(_ptr(x), x.size))
+    if x.dtype == np.int32:
+        return np.array([lib().hxo_norm_l1_i32(_ptr(x), x.size)], np.uint32).view(np.int32)[0]
+    return np.uint32(lib().hxo_sum_u32(_ptr(x), x.size))
+
+
+def norm_l2(x: np.ndarray) -> float:
+    """f32: sqrt of the f64 sum of exact squares."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(np.sqrt(lib().hxo_sum_squares_f32(_ptr(x), x.size)))
+
+
+def norm_max(x: np.ndarray):
+    """max |x| with the MaxOp identity (f32::MIN, i32::MIN, 0) when empty."""
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.float32:
+        return np.float32(lib().hxo_norm_max_f32(_ptr(x), x.size))
+    if x.dtype == np.int32:
+        return np.int32(lib().hxo_norm_max_i32(_ptr(x), x.size))
+    return np.uint32(lib().hxo_max_u32(_ptr(x), x.size))
+
+
+def fma_arrays(x: np.ndarray, y: np.ndarray, f: float) -> np.ndarray:
+    """fmaf(f, x[i], y[i]) for every i (axpy: x = source, y = target)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.ascontiguousarray(y, np.float32)
+    out = np.empty_like(x)
+    lib().hxo_fma_arrays(_ptr(x), _ptr(y), float(f), x.size, _ptr(out))
     return out
 
 

@@ -261,6 +261,74 @@ void rocm_reduce_contract(RocmDevice &dev) {
     CHECK(dev.download_owned(out)[0] == 0u); // empty sum -> identity (:848-857)
 }
 
+// --------------------------------------------- dense_vector.rs:36-184
+void dense_vector_contract(RocmDevice &dev) {
+    RocmDenseVectorOps ops;
+    using V = std::vector<float>;
+    auto source = dev.upload(V{1, 2, 3, 4});
+    auto target = dev.alloc_zeroed<float>(4);
+    ops.copy_vector(dev, source, target);
+    CHECK(same(dev.download_owned(target), V{1, 2, 3, 4}));
+    auto short_target = dev.alloc_zeroed<float>(3);
+    expect_error(ErrorKind::LengthMismatch, "", [&] { ops.copy_vector(dev, source, short_target); });
+    ops.scale_vector(dev, target, 2.0f);
+    CHECK(same(dev.download_owned(target), V{2, 4, 6, 8}));
+    auto y = dev.upload(V{4, 5, 6, 8});
+    ops.axpy(dev, y, source, 2.0f);
+    CHECK(same(dev.download_owned(y), V{6, 9, 12, 16}));
+    auto z = dev.upload(V{4, 5, 6, 8});
+    ops.xpay(dev, z, source, 2.0f);
+    CHECK(same(dev.download_owned(z), V{9, 12, 15, 20}));
+    auto left = dev.upload(V{8, 6, 4, 2}), right = dev.upload(V{2, 4, 8, 0.5f});
+    auto out = dev.alloc_zeroed<float>(4);
+    ops.subtract_into(dev, left, right, out);
+    CHECK(same(dev.download_owned(out), V{6, 2, -4, 1.5f}));
+    ops.add_into(dev, left, right, out);
+    CHECK(same(dev.download_owned(out), V{10, 10, 12, 2.5f}));
+    ops.multiply_into(dev, left, right, out);
+    CHECK(same(dev.download_owned(out), V{16, 24, 32, 1}));
+    ops.divide_into(dev, left, right, out);
+    CHECK(same(dev.download_owned(out), V{4, 1.5f, 0.5f, 4}));
+    auto a = dev.upload(V{1, 2, 3, 4}), b = dev.upload(V{8, 4, 2, 1});
+    auto pd = ops.prepare_dot(dev, a, b);
+    CHECK(ops.dot_prepared(dev, pd, a, b) == 26.0f);
+    CHECK(ops.dot_prepared(dev, pd, a, b) == 26.0f);
+    dev.write_buffer(a, V{2, 2, 2, 2});
+    CHECK(ops.dot_prepared(dev, pd, a, b) == 30.0f);
+    auto foreign = dev.upload(V{1, 1, 1, 1});
+    expect_error(ErrorKind::DispatchFailed, "prepared dot received different device allocations",
+                 [&] { ops.dot_prepared(dev, pd, foreign, b); });
+    auto v = dev.upload(V{2, 3, 6, 0});
+    CHECK(ops.norm_l1(dev, v) == 11.0f);
+    CHECK(ops.norm_max(dev, v) == 6.0f);
+    auto pn = ops.prepare_norm_l2(dev, v);
+    CHECK(std::fabs(ops.norm_l2_prepared(dev, pn, v) - 7.0f) <= 7.0f * 1.1920929e-7f);
+    dev.write_buffer(v, V{9, 12, 20, 0});
+    CHECK(std::fabs(ops.norm_l2_prepared(dev, pn, v) - 25.0f) <= 25.0f * 1.1920929e-7f);
+}
+
+// ----------------------------------- rocm tests/contract.rs:2615-2737
+void map_reduction_contract(RocmDevice &dev) {
+    auto m = dev.upload(std::vector<int32_t>{-3, 4, -5, 6, -7, 8});
+    const Layout lm = Layout::c_contiguous({2, 3});
+    CHECK(dev.download_owned(norm_l1<int32_t>(dev, {m, lm}))[0] == 33);
+    CHECK(dev.download_owned(norm_max<int32_t>(dev, {m, lm}))[0] == 8);
+    auto lhs = dev.upload(std::vector<int32_t>{99, 1, 2, 3, 4, 5});
+    auto rhs = dev.upload(std::vector<int32_t>{6, 7, 8, 9, 10});
+    const Layout ll = Layout::strided({5}, {1}, 1), lr = Layout::c_contiguous({5});
+    CHECK(dev.download_owned(dot<int32_t>(dev, {lhs, ll}, {rhs, lr}))[0] == 130);
+    auto t = dev.upload(std::vector<int32_t>{1, 2, 3, 4, 5, 6, 7, 8, 9});
+    const Layout l33 = Layout::c_contiguous({3, 3});
+    CHECK(dev.download_owned(trace<int32_t>(dev, {t, l33}))[0] == 15);
+    auto l2 = dev.upload(std::vector<float>{3, 4});
+    const Layout l2l = Layout::c_contiguous({2});
+    CHECK(dev.download_owned(norm_l2<float>(dev, {l2, l2l}))[0] == 5.0f);
+    const Layout wrong = Layout::c_contiguous({4});
+    expect_error(ErrorKind::DispatchFailed, "dot product shape mismatch",
+                 [&] { dot<int32_t>(dev, {lhs, ll}, {rhs, wrong}); });
+    expect_error(ErrorKind::DispatchFailed, "trace requires a square matrix", [&] { trace<int32_t>(dev, {m, lm}); });
+}
+
 // ------------------------------------------ the path's additions, at size
 uint64_t splitmix(uint64_t seed, uint64_t i) {
     uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
@@ -383,6 +451,8 @@ int main() {
         {"scan", scan_contract},
         {"rocm_scan_i32", rocm_scan_contract},
         {"rocm_reduce_u32", rocm_reduce_contract},
+        {"dense_vector", dense_vector_contract},
+        {"rocm_map_reduction", map_reduction_contract},
         {"additions_at_size", additions_at_size},
     };
     for (const auto &c : clauses) {

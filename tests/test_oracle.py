@@ -307,3 +307,63 @@ def test_geometric_offsets(oracle):
     assert off[0] == 0 and off[-1] == n
     assert lens.min() >= 1
     assert abs(float(lens[:-1].mean()) - 300.0) < 5.0
+
+
+# ---- map-reductions (dot, norms) -------------------------------------------
+def test_map_reduction_kats(oracle):
+    k = KATS["map_reduction"]
+    m = np.array(k["matrix_i32"], np.int32)
+    assert oracle.norm_l1(m) == k["norm_l1"]
+    assert oracle.norm_max(m) == k["norm_max"]
+    lhs = np.array(k["dot_lhs_i32"], np.int32)[k["dot_lhs_offset"]:]
+    assert oracle.dot(lhs, np.array(k["dot_rhs_i32"], np.int32)) == k["dot"]
+    tr = np.array(k["trace_i32"], np.int32).reshape(3, 3)
+    assert oracle.full_sum(np.ascontiguousarray(np.diagonal(tr))) == k["trace"]
+    assert oracle.norm_l2(np.array(k["l2_f32"], np.float32)) == k["norm_l2"]
+    dv = KATS["dense_vector"]
+    assert oracle.dot(np.array(dv["dot_a"], np.float32), np.array(dv["dot_b"], np.float32))[0] == dv["dot"]
+    v = np.array(dv["norm_vector"], np.float32)
+    assert oracle.norm_l1(v) == dv["norm_l1"] and oracle.norm_max(v) == dv["norm_max"]
+    assert oracle.norm_l2(v) == dv["norm_l2"]
+    assert oracle.norm_l2(np.array(dv["norm_vector_rebound"], np.float32)) == dv["norm_l2_rebound"]
+
+
+def test_map_reductions_against_library_routines(oracle):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(10007).astype(np.float32)
+    b = rng.standard_normal(10007).astype(np.float32)
+    got, mags = oracle.dot(a, b)
+    want = math.fsum(float(x) * float(y) for x, y in zip(a, b))  # exact products, exact sum
+    assert got == pytest.approx(want, rel=0, abs=1e-12 * mags)
+    assert oracle.norm_l1(a) == pytest.approx(math.fsum(abs(float(x)) for x in a), rel=1e-15)
+    assert oracle.norm_l2(a) == pytest.approx(float(np.linalg.norm(a.astype(np.float64))), rel=1e-14)
+    assert oracle.norm_max(a) == np.max(np.abs(a))
+    # Cauchy-Schwarz and the dot of a vector with itself.
+    assert abs(got) <= oracle.norm_l2(a) * oracle.norm_l2(b) * (1 + 1e-12)
+    assert oracle.dot(a, a)[0] == pytest.approx(oracle.norm_l2(a) ** 2, rel=1e-12)
+    # Integer forms wrap mod 2^32, |INT_MIN| = INT_MIN.
+    i = rng.integers(-2**31, 2**31, 5000, dtype=np.int64).astype(np.int32)
+    j = rng.integers(-2**31, 2**31, 5000, dtype=np.int64).astype(np.int32)
+    wrap = lambda v: np.array([v & 0xFFFFFFFF], np.uint32).view(np.int32)[0]
+    assert oracle.dot(i, j) == wrap(sum(int(x) * int(y) for x, y in zip(i, j)))
+    assert oracle.norm_l1(i) == wrap(sum(abs(int(x)) for x in i))
+    edge = np.array([-2**31, 5, -7], np.int32)
+    assert oracle.norm_max(edge) == 7  # |INT_MIN| stays INT_MIN and never wins
+    assert oracle.norm_max(np.array([-2**31], np.int32)) == -2**31
+    assert oracle.norm_max(np.zeros(0, np.float32)) == np.float32(-3.4028234663852886e38)
+    nan = np.array([1.0, np.nan, -3.0], np.float32)
+    assert oracle.norm_max(nan) == 3.0
+
+
+def test_fma_arrays_is_single_rounding(oracle):
+    """fmaf(f, x, y) rounds once: checked against exact rational arithmetic
+    on values whose separately rounded product would differ."""
+    x = np.array([1.0 + 2.0**-23, 3.0, 0.1], np.float32)
+    y = np.array([-1.0, 1e-8, -0.3], np.float32)
+    f = np.float32(1.0 - 2.0**-24)
+    got = oracle.fma_arrays(x, y, float(f))
+    for i in range(3):
+        exact = Fraction(float(f)) * Fraction(float(x[i])) + Fraction(float(y[i]))
+        assert got[i] == np.float32(float(exact)), i
+    # the separately rounded form differs on the first element
+    assert np.float32(f * x[0]) + y[0] != got[0]
