@@ -30,11 +30,12 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32")
+WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32",
+             "axpy_f32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
              "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
-             "copy_u32": "copy_tiles_kernel"}
+             "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1"}
 
 
 def log(msg: str) -> None:
@@ -140,6 +141,33 @@ def bench_scan_f32_2_30(hx, dev, args):
                                               StridedView(out, lay))
     ms = time_plan(dev, plan.dispatch, max(1, args.steps // 4), max(1, args.warmup // 2))
     return {"n": n, "ms": ms, "bytes": 8 * n}
+
+
+def bench_dot_f32(hx, dev, args):
+    """Prepared f32 dot of two 2^28 vectors (DenseVectorOps::prepare_dot):
+    reads 8n bytes; f64 accumulation of exact products."""
+    n = 1 << 28
+    a = dev.alloc_uninitialized(np.float32, n)
+    b = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(a, seed=11, lo=-1.0, hi=1.0)
+    dev.fill_uniform_real(b, seed=12, lo=-1.0, hi=1.0)
+    lay = hx.Layout.c_contiguous([n])
+    plan = hx.prepare_dot(dev, hx.StridedView(a, lay), hx.StridedView(b, lay))
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    return {"n": n, "ms": ms, "bytes": 8 * n + 4}
+
+
+def bench_axpy_f32(hx, dev, args):
+    """axpy over 2^28 f32 (target = fmaf(f, source, target)): reads 8n,
+    writes 4n bytes."""
+    n = 1 << 28
+    t = dev.alloc_uninitialized(np.float32, n)
+    s = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(t, seed=13, lo=-1.0, hi=1.0)
+    dev.fill_uniform_real(s, seed=14, lo=-1.0, hi=1.0)
+    ops = hx.RocmDenseVectorOps()
+    ms = time_plan(dev, lambda: ops.axpy(dev, t, s, 0.5), args.steps, args.warmup)
+    return {"n": n, "ms": ms, "bytes": 12 * n}
 
 
 def bench_copy_u32(hx, dev, args):
@@ -336,7 +364,7 @@ def main() -> int:
         },
     }
     if args.workload == "all":
-        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32"):
+        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32", "axpy_f32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
             line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

@@ -193,8 +193,10 @@ def test_trace_views(device, oracle):
     assert one(device, out) == 0
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 1000003])
+@pytest.mark.parametrize("n", [1, 3, 4, 4096, 4096 * 3 + 5, 1000003])
 def test_vector_forms_bit_exact(device, oracle, n):
+    # 4096 elements is one whole tile of the tiled kernel; the other sizes
+    # exercise the tile/remainder split and the remainder-only path.
     t = oracle.uniform_real(n, seed=n + 5, lo=-3.0, hi=3.0)
     s = oracle.uniform_real(n, seed=n + 6, lo=0.5, hi=3.0)
     f = np.float32(0.7)
