@@ -143,6 +143,7 @@ SIGNATURES = {
     "hx_vector_update": (I32, [P, I32, I32, P, U64, P, U64, c_float, P]),
     "hx_vector_binary": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),
     "hx_plan_dispatch": (I32, [P, P]),
+    "hx_plan_dispatch_batch": (I32, [P, U64, P]),
     "hx_plan_destroy": (I32, [P]),
     "hx_plan_workspace_bytes": (I32, [P, POINTER(U64)]),
     "hx_fill_random": (I32, [P, P, U64, I32, I32, U64, c_double, c_double, P]),

@@ -39,6 +39,12 @@ struct hx_device {
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
     hx::LookbackState ws_lookback;
+
+    // Scratch for the immediate entry points that stage partials outside
+    // any look-back protocol (split axis reductions, chunked column scans).
+    // Kept apart from `ws` so those writes never land on status words.
+    void *scratch = nullptr;
+    uint64_t scratch_bytes = 0;
 };
 
 namespace hx {
@@ -97,6 +103,9 @@ constexpr uint64_t kLookbackOffset = kWorkspaceHeader + kReduceArea;
 // workspace restarts its LookbackState.
 hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t stream, void **ws);
 hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws);
+// Immediate-mode scratch of `dev` (see hx_device::scratch), grown on demand;
+// nothing is returned for 0 bytes.
+hx_status device_scratch(hx_device *dev, uint64_t bytes, void **scratch);
 
 // Tag for the next look-back launch on a workspace of `ws_bytes`; clears the
 // status area when the 30-bit tag space wraps.
@@ -132,7 +141,10 @@ struct RowsArgs {
     void *out_sum, *out_max;
     uint32_t *out_argmax;
 };
-hx_status launch_rows(const RowsArgs &args, hipStream_t stream);
+// Split forms (few long rows, or column tiles over a tall matrix) fold
+// per-chunk partials through `ws`; 0 bytes when no split is needed.
+uint64_t rows_workspace_bytes(const RowsArgs &args);
+hx_status launch_rows(const RowsArgs &args, void *ws, uint64_t ws_bytes, hipStream_t stream);
 
 struct AxisArgs {
     hx_op op;
@@ -146,7 +158,8 @@ struct AxisArgs {
     int64_t out_stride;
     uint64_t out_offset;
 };
-hx_status launch_axis_reduce(const AxisArgs &args, hipStream_t stream);
+uint64_t axis_reduce_workspace_bytes(const AxisArgs &args);
+hx_status launch_axis_reduce(const AxisArgs &args, void *ws, uint64_t ws_bytes, hipStream_t stream);
 
 struct ScanArgs {
     hx_op op;

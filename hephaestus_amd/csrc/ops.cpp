@@ -149,7 +149,7 @@ hx_status plan_axis(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
 
 struct AxisPlan final : hx_plan {
     AxisArgs args;
-    hx_status dispatch(hipStream_t stream) override { return launch_axis_reduce(args, stream); }
+    hx_status dispatch(hipStream_t stream) override { return launch_axis_reduce(args, ws, ws_bytes, stream); }
 };
 
 // ---------------------------------------------------------------- scan
@@ -318,7 +318,10 @@ hx_status hx_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype, const void *i
     AxisArgs a;
     HX_TRY(plan_axis(op, dtype, in, in_buf_len, in_layout, axis, out, out_buf_len, out_layout, &a));
     HX_TRY(bind_device(dev));
-    HX_TRY(launch_axis_reduce(a, pick_stream(dev, stream)));
+    const uint64_t bytes = axis_reduce_workspace_bytes(a);
+    void *scratch = nullptr;
+    HX_TRY(device_scratch(dev, bytes, &scratch));
+    HX_TRY(launch_axis_reduce(a, scratch, bytes, pick_stream(dev, stream)));
     return ok();
 }
 
@@ -334,7 +337,7 @@ hx_status hx_prepare_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype, const
     AxisPlan *p = new (std::nothrow) AxisPlan();
     if (!p) return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of plan failed");
     p->args = a;
-    return finish_plan(dev, p, 0, plan);
+    return finish_plan(dev, p, axis_reduce_workspace_bytes(a), plan);
 }
 
 hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_t in_buf_len,
@@ -382,7 +385,10 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_
     a.out_max = out_max;
     a.out_argmax = out_argmax;
     HX_TRY(bind_device(dev));
-    HX_TRY(launch_rows(a, pick_stream(dev, stream)));
+    const uint64_t bytes = rows_workspace_bytes(a);
+    void *scratch = nullptr;
+    HX_TRY(device_scratch(dev, bytes, &scratch));
+    HX_TRY(launch_rows(a, scratch, bytes, pick_stream(dev, stream)));
     return ok();
 }
 

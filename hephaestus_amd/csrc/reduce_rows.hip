@@ -8,15 +8,21 @@
 // a row-major matrix reduced along axis 1, neighbouring lanes are a whole
 // row apart, so no load is coalesced, and sum and max are two full passes.
 // Here:
-//   rows_kernel  one wave64 per row: lane l reads 16-byte vectors l, l+64,
-//                ... of the row (every load instruction covers 1 KiB of
-//                contiguous memory), keeps every requested statistic in
-//                registers, then combines them with xor-butterflies.  Used
-//                whenever the reduced axis has unit stride (or no stride is
-//                unit).
-//   cols_kernel  one thread per output when the OTHER axis has unit stride
-//                (axis-0 reduction of a row-major matrix): each load
-//                instruction of a wave covers 64 adjacent outputs.
+//   rows_kernel        one wave64 per row: lane l reads 16-byte vectors l,
+//                      l+64, ... of the row (every load instruction covers
+//                      1 KiB of contiguous memory), keeps every requested
+//                      statistic in registers, then combines them with
+//                      xor-butterflies.  Used whenever the reduced axis has
+//                      unit stride (or no stride is unit).
+//   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
+//                      chunk statistics to partial planes.
+//   cols_tiles_kernel  the outputs are adjacent and the reduced axis strided
+//                      (axis-0 reduction of a row-major matrix): a wave owns
+//                      256 adjacent outputs (one 16-byte load per lane per
+//                      line) and a chunk of the axis, so the chip gets
+//                      thousands of waves however tall the matrix is.
+//   split_fold_kernel  folds the chunk partials of either split form in
+//                      chunk order, so f32 sums do not depend on scheduling.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -118,6 +124,43 @@ template <typename T, int FLAGS> struct Stats {
         }
         if constexpr ((FLAGS & F_MIN) != 0) ((T *)p.out_min)[o] = Key<T>::decode(mink);
     }
+
+    // Partial statistics of one chunk of the reduced axis, one 8-byte word
+    // per statistic, each statistic in its own plane `plane` words apart.
+    template <typename A> static __device__ __forceinline__ uint64_t to_word(A v) {
+        if constexpr (std::is_same<A, double>::value) return (uint64_t)__double_as_longlong(v);
+        else return (uint64_t)v;
+    }
+    template <typename A> static __device__ __forceinline__ A from_word(uint64_t w) {
+        if constexpr (std::is_same<A, double>::value) return __longlong_as_double((long long)w);
+        else return (A)w;
+    }
+    __device__ __forceinline__ void store_partial(uint64_t *w, uint64_t plane) const {
+        int q = 0;
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) w[(q++) * plane] = to_word(sum);
+        if constexpr ((FLAGS & F_PROD) != 0) w[(q++) * plane] = to_word(prod);
+        if constexpr ((FLAGS & F_ARG) != 0) w[(q++) * plane] = arg;
+        else if constexpr ((FLAGS & F_MAX) != 0) w[(q++) * plane] = maxk;
+        if constexpr ((FLAGS & F_MIN) != 0) w[(q++) * plane] = mink;
+        (void)q;
+    }
+    // Fold a later chunk's partial into this one.
+    __device__ __forceinline__ void merge_partial(const uint64_t *w, uint64_t plane) {
+        int q = 0;
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum += from_word<S>(w[(q++) * plane]);
+        if constexpr ((FLAGS & F_PROD) != 0) prod *= from_word<Pr>(w[(q++) * plane]);
+        if constexpr ((FLAGS & F_ARG) != 0) {
+            arg = umax64(arg, w[(q++) * plane]);
+        } else if constexpr ((FLAGS & F_MAX) != 0) {
+            const uint32_t k = (uint32_t)w[(q++) * plane];
+            maxk = maxk > k ? maxk : k;
+        }
+        if constexpr ((FLAGS & F_MIN) != 0) {
+            const uint32_t k = (uint32_t)w[(q++) * plane];
+            mink = mink < k ? mink : k;
+        }
+        (void)q;
+    }
 };
 
 // One wave per row.  VEC: unit column stride and every row start 16-byte
@@ -167,120 +210,345 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     }
 }
 
-// One thread per output; the reduced axis is walked serially, which is
-// coalesced across the wave when the outputs are adjacent in memory.
-template <typename T, bool AFFINE, int FLAGS>
-__global__ __launch_bounds__(kBlock) void cols_kernel(RowParams p) {
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
-    for (uint64_t r = (uint64_t)blockIdx.x * kBlock + threadIdx.x; r < p.rows; r += nthreads) {
-        const T *line = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
-        Stats<T, FLAGS> st;
-        for (uint64_t j = 0; j < p.cols; ++j)
-            st.visit(prologue<T, AFFINE>(line[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
-        st.write(p, r);
+// Column tiles (the reduced axis is strided, the outputs adjacent: axis-0
+// reduction of a row-major matrix).  A wave owns 64*V adjacent outputs --
+// V = 4 gives every lane one 16-byte load per line, so each load instruction
+// of a wave covers 1 KiB of one line -- and one chunk of the reduced axis,
+// kU lines in flight per lane.  Adjacent waves take adjacent output groups
+// of the same chunk.  SPLIT: the chunk's statistics go to partial planes
+// that split_fold_kernel combines in chunk order; otherwise the wave covers
+// the whole axis and writes the outputs.
+template <typename T, bool AFFINE, int FLAGS, int V, bool SPLIT>
+__global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
+                                                            uint32_t nchunks, uint64_t groups) {
+    constexpr int kU = V == 4 ? 8 : 16;
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= groups * nchunks) return;
+    const uint64_t g = w % groups, k = w / groups;
+    const uint64_t o0 = (g * kWave + (uint64_t)lane_id()) * V;
+    if (o0 >= p.rows) return;
+    const uint64_t j0 = k * chunk;
+    const uint64_t j1 = j0 + chunk < p.cols ? j0 + chunk : p.cols;
+    Stats<T, FLAGS> st[V];
+    const T *base = (const T *)p.base + ((int64_t)p.offset + (int64_t)o0 * p.row_stride);
+    uint64_t j = j0;
+    if constexpr (V == 4) {
+        using Vt = typename Vec4<T>::type;
+        auto visit = [&](const Vt &x, uint32_t jj) {
+            st[0].visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), jj);
+            st[1].visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), jj);
+            st[2].visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), jj);
+            st[3].visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), jj);
+        };
+        for (; j + kU <= j1; j += kU) {
+            Vt x[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                x[u] = __builtin_nontemporal_load((const Vt *)(base + (int64_t)(j + u) * p.col_stride));
+#pragma unroll
+            for (int u = 0; u < kU; ++u) visit(x[u], (uint32_t)(j + u));
+        }
+        for (; j < j1; ++j) visit(__builtin_nontemporal_load((const Vt *)(base + (int64_t)j * p.col_stride)), (uint32_t)j);
+    } else {
+        for (; j + kU <= j1; j += kU) {
+            T x[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) x[u] = __builtin_nontemporal_load(base + (int64_t)(j + u) * p.col_stride);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) st[0].visit(prologue<T, AFFINE>(x[u], p.a, p.b), (uint32_t)(j + u));
+        }
+        for (; j < j1; ++j)
+            st[0].visit(prologue<T, AFFINE>(__builtin_nontemporal_load(base + (int64_t)j * p.col_stride), p.a, p.b),
+                        (uint32_t)j);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        if constexpr (SPLIT)
+            st[v].store_partial(partials + k * p.rows + o0 + v, (uint64_t)nchunks * p.rows);
+        else
+            st[v].write(p, o0 + v);
     }
 }
 
-template <typename T, bool AFFINE, int FLAGS>
-hx_status launch_rows_typed(const RowParams &p, bool cols_layout, hipStream_t stream) {
-    if (p.rows == 0) return HX_OK;
-    if (cols_layout) {
-        uint64_t blocks = ceil_div(p.rows, kBlock);
-        if (blocks > (1u << 20)) blocks = 1u << 20;
-        hipLaunchKernelGGL((cols_kernel<T, AFFINE, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock),
-                           0, stream, p);
-        return check_launch("cols_kernel");
+// Few long rows (the reduced axis has unit stride but there are too few rows
+// to give every CU work): one wave per (row, chunk of 256-element multiples),
+// lanes along the chunk as in rows_kernel, partials to the planes.
+template <typename T, bool AFFINE, int FLAGS, bool VEC>
+__global__ __launch_bounds__(kBlock) void rows_split_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
+                                                            uint32_t nchunks) {
+    const int lane = lane_id();
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= p.rows * nchunks) return; // uniform across the wave
+    const uint64_t r = w / nchunks, k = w % nchunks;
+    const T *row = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
+    const uint64_t c0 = k * chunk;
+    const uint64_t c1 = c0 + chunk < p.cols ? c0 + chunk : p.cols;
+    Stats<T, FLAGS> st;
+    if constexpr (VEC) {
+        using V = typename Vec4<T>::type;
+        const V *vrow = (const V *)(row + c0);
+        const uint64_t nvec = (c1 - c0) >> 2;
+        uint64_t v = lane;
+        for (; v + 3 * kWave < nvec; v += 4 * kWave) {
+            V x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * kWave]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t j = (uint32_t)(c0 + 4 * (v + u * kWave));
+                st.visit(prologue<T, AFFINE>((T)x[u].x, p.a, p.b), j);
+                st.visit(prologue<T, AFFINE>((T)x[u].y, p.a, p.b), j + 1);
+                st.visit(prologue<T, AFFINE>((T)x[u].z, p.a, p.b), j + 2);
+                st.visit(prologue<T, AFFINE>((T)x[u].w, p.a, p.b), j + 3);
+            }
+        }
+        for (; v < nvec; v += kWave) {
+            V x = __builtin_nontemporal_load(&vrow[v]);
+            const uint32_t j = (uint32_t)(c0 + 4 * v);
+            st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
+            st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
+            st.visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), j + 2);
+            st.visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), j + 3);
+        }
+        const uint64_t j = c0 + 4 * nvec + lane;
+        if (j < c1) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), (uint32_t)j);
+    } else {
+        for (uint64_t j = c0 + lane; j < c1; j += kWave)
+            st.visit(prologue<T, AFFINE>(row[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
     }
-    const uintptr_t base = (uintptr_t)((const T *)p.base + p.offset);
-    const bool vec = p.col_stride == 1 && (base % 16) == 0 && (p.row_stride % 4) == 0;
-    uint64_t blocks = ceil_div(p.rows, kBlock / kWave);
-    if (blocks > (1u << 20)) blocks = 1u << 20;
-    if (vec)
-        hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
-    else
-        hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false>), dim3((uint32_t)blocks),
-                           dim3(kBlock), 0, stream, p);
-    return check_launch("rows_kernel");
+    st.wave_combine();
+    if (lane == 0) st.store_partial(partials + k * p.rows + r, (uint64_t)nchunks * p.rows);
+}
+
+// One thread per output: fold the chunk partials in chunk order (so f32
+// sums are deterministic) and write the statistics.
+template <typename T, int FLAGS>
+__global__ __launch_bounds__(kBlock) void split_fold_kernel(RowParams p, const uint64_t *partials, uint32_t nchunks) {
+    const uint64_t o = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (o >= p.rows) return;
+    const uint64_t plane = (uint64_t)nchunks * p.rows;
+    Stats<T, FLAGS> st;
+    for (uint32_t k = 0; k < nchunks; ++k) st.merge_partial(partials + (uint64_t)k * p.rows + o, plane);
+    st.write(p, o);
+}
+
+// Launch shape, computed identically for workspace sizing and for launch.
+constexpr uint64_t kTargetWaves = 8192;  // 32 waves per CU
+constexpr uint64_t kMinColChunk = 32;    // lines per column-tile chunk
+constexpr uint64_t kMinRowChunk = 8192;  // elements per split-row chunk
+
+struct Shape {
+    bool cols = false, vec = false;
+    int V = 1;
+    uint64_t groups = 0, chunk = 0;
+    uint32_t nchunks = 1;
+};
+
+Shape plan_shape(const RowParams &p, bool cols_layout) {
+    Shape s;
+    s.cols = cols_layout;
+    const uintptr_t base = (uintptr_t)p.base + 4u * p.offset; // every element type is 4 bytes
+    uint64_t k = 1;
+    if (cols_layout) {
+        s.vec = p.row_stride == 1 && p.rows % 4 == 0 && base % 16 == 0 && p.col_stride % 4 == 0;
+        s.V = s.vec ? 4 : 1;
+        s.groups = ceil_div(p.rows, (uint64_t)kWave * s.V);
+        if (s.groups < kTargetWaves) {
+            k = ceil_div(kTargetWaves, s.groups);
+            const uint64_t kmax = ceil_div(p.cols, kMinColChunk);
+            if (k > kmax) k = kmax;
+        }
+    } else {
+        s.vec = p.col_stride == 1 && base % 16 == 0 && (p.row_stride % 4 == 0 || p.rows == 1);
+        if (p.rows < kTargetWaves / 2 && p.cols >= 2 * kMinRowChunk) {
+            k = ceil_div(kTargetWaves, p.rows);
+            const uint64_t kmax = ceil_div(p.cols, kMinRowChunk);
+            if (k > kmax) k = kmax;
+        }
+    }
+    if (k < 1) k = 1;
+    if (k > 1) {
+        uint64_t chunk = ceil_div(p.cols, k);
+        if (!cols_layout) chunk = ceil_div(chunk, 256) * 256; // keeps 16-byte alignment of every chunk
+        s.chunk = chunk;
+        s.nchunks = (uint32_t)ceil_div(p.cols, chunk);
+    } else {
+        s.chunk = p.cols;
+        s.nchunks = 1;
+    }
+    return s;
+}
+
+int planes_of(int flags) {
+    return ((flags & (F_SUM | F_MEAN)) != 0) + ((flags & F_PROD) != 0) + ((flags & (F_ARG | F_MAX)) != 0) +
+           ((flags & F_MIN) != 0);
+}
+
+uint64_t shape_bytes(const RowParams &p, const Shape &s, int flags) {
+    if (p.rows == 0 || s.nchunks <= 1) return 0;
+    return (uint64_t)planes_of(flags) * s.nchunks * p.rows * 8u;
+}
+
+template <typename T, bool AFFINE, int FLAGS>
+hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    if (p.rows == 0) return HX_OK;
+    const Shape s = plan_shape(p, cols_layout);
+    const bool split = s.nchunks > 1;
+    uint64_t *partials = (uint64_t *)ws;
+    if (split && ws_bytes < shape_bytes(p, s, FLAGS))
+        return fail(HX_ERR_DISPATCH_FAILED, "axis reduction workspace of %llu bytes is too small",
+                    (unsigned long long)ws_bytes);
+    if (cols_layout) {
+        const uint64_t waves = s.groups * s.nchunks;
+        const uint64_t blocks = ceil_div(waves, kBlock / kWave);
+        if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");
+        const dim3 grid((uint32_t)blocks), block(kBlock);
+        if (s.vec) {
+            if (split)
+                hipLaunchKernelGGL((cols_tiles_kernel<T, AFFINE, FLAGS, 4, true>), grid, block, 0, stream, p, partials,
+                                   s.chunk, s.nchunks, s.groups);
+            else
+                hipLaunchKernelGGL((cols_tiles_kernel<T, AFFINE, FLAGS, 4, false>), grid, block, 0, stream, p, partials,
+                                   s.chunk, s.nchunks, s.groups);
+        } else {
+            if (split)
+                hipLaunchKernelGGL((cols_tiles_kernel<T, AFFINE, FLAGS, 1, true>), grid, block, 0, stream, p, partials,
+                                   s.chunk, s.nchunks, s.groups);
+            else
+                hipLaunchKernelGGL((cols_tiles_kernel<T, AFFINE, FLAGS, 1, false>), grid, block, 0, stream, p, partials,
+                                   s.chunk, s.nchunks, s.groups);
+        }
+        HX_TRY(check_launch("cols_tiles_kernel"));
+    } else if (split) {
+        const uint64_t blocks = ceil_div(p.rows * s.nchunks, kBlock / kWave);
+        if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");
+        if (s.vec)
+            hipLaunchKernelGGL((rows_split_kernel<T, AFFINE, FLAGS, true>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                               stream, p, partials, s.chunk, s.nchunks);
+        else
+            hipLaunchKernelGGL((rows_split_kernel<T, AFFINE, FLAGS, false>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                               stream, p, partials, s.chunk, s.nchunks);
+        HX_TRY(check_launch("rows_split_kernel"));
+    } else {
+        uint64_t blocks = ceil_div(p.rows, kBlock / kWave);
+        if (blocks > (1u << 20)) blocks = 1u << 20;
+        if (s.vec)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                               p);
+        else
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                               p);
+        return check_launch("rows_kernel");
+    }
+    if (!split) return HX_OK;
+    hipLaunchKernelGGL((split_fold_kernel<T, FLAGS>), dim3((uint32_t)ceil_div(p.rows, kBlock)), dim3(kBlock), 0,
+                       stream, p, (const uint64_t *)partials, s.nchunks);
+    return check_launch("split_fold_kernel");
 }
 
 template <typename T, bool AFFINE>
-hx_status launch_rows_flags(const RowParams &p, int flags, bool cols_layout, hipStream_t stream) {
+hx_status launch_rows_flags(const RowParams &p, int flags, bool cols_layout, void *ws, uint64_t ws_bytes,
+                            hipStream_t stream) {
     switch (flags) {
-    case F_SUM: return launch_rows_typed<T, AFFINE, F_SUM>(p, cols_layout, stream);
-    case F_MAX: return launch_rows_typed<T, AFFINE, F_MAX>(p, cols_layout, stream);
-    case F_ARG: return launch_rows_typed<T, AFFINE, F_ARG>(p, cols_layout, stream);
-    case F_MIN: return launch_rows_typed<T, AFFINE, F_MIN>(p, cols_layout, stream);
-    case F_PROD: return launch_rows_typed<T, AFFINE, F_PROD>(p, cols_layout, stream);
-    case F_MEAN: return launch_rows_typed<T, AFFINE, F_MEAN>(p, cols_layout, stream);
-    case F_SUM | F_MAX: return launch_rows_typed<T, AFFINE, F_SUM | F_MAX>(p, cols_layout, stream);
-    case F_SUM | F_ARG: return launch_rows_typed<T, AFFINE, F_SUM | F_ARG>(p, cols_layout, stream);
-    case F_MAX | F_ARG: return launch_rows_typed<T, AFFINE, F_MAX | F_ARG>(p, cols_layout, stream);
+    case F_SUM: return launch_rows_typed<T, AFFINE, F_SUM>(p, cols_layout, ws, ws_bytes, stream);
+    case F_MAX: return launch_rows_typed<T, AFFINE, F_MAX>(p, cols_layout, ws, ws_bytes, stream);
+    case F_ARG: return launch_rows_typed<T, AFFINE, F_ARG>(p, cols_layout, ws, ws_bytes, stream);
+    case F_MIN: return launch_rows_typed<T, AFFINE, F_MIN>(p, cols_layout, ws, ws_bytes, stream);
+    case F_PROD: return launch_rows_typed<T, AFFINE, F_PROD>(p, cols_layout, ws, ws_bytes, stream);
+    case F_MEAN: return launch_rows_typed<T, AFFINE, F_MEAN>(p, cols_layout, ws, ws_bytes, stream);
+    case F_SUM | F_MAX: return launch_rows_typed<T, AFFINE, F_SUM | F_MAX>(p, cols_layout, ws, ws_bytes, stream);
+    case F_SUM | F_ARG: return launch_rows_typed<T, AFFINE, F_SUM | F_ARG>(p, cols_layout, ws, ws_bytes, stream);
+    case F_MAX | F_ARG: return launch_rows_typed<T, AFFINE, F_MAX | F_ARG>(p, cols_layout, ws, ws_bytes, stream);
     case F_SUM | F_MAX | F_ARG:
-        return launch_rows_typed<T, AFFINE, F_SUM | F_MAX | F_ARG>(p, cols_layout, stream);
+        return launch_rows_typed<T, AFFINE, F_SUM | F_MAX | F_ARG>(p, cols_layout, ws, ws_bytes, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unsupported row statistic set %d", flags);
 }
 
-hx_status launch_rows_any(const RowParams &p, hx_dtype dtype, bool affine, int flags,
-                          bool cols_layout, hipStream_t stream) {
+hx_status launch_rows_any(const RowParams &p, hx_dtype dtype, bool affine, int flags, bool cols_layout, void *ws,
+                          uint64_t ws_bytes, hipStream_t stream) {
     switch (dtype) {
     case HX_DTYPE_F32:
-        return affine ? launch_rows_flags<float, true>(p, flags, cols_layout, stream)
-                      : launch_rows_flags<float, false>(p, flags, cols_layout, stream);
-    case HX_DTYPE_U32: return launch_rows_flags<uint32_t, false>(p, flags, cols_layout, stream);
-    case HX_DTYPE_I32: return launch_rows_flags<int32_t, false>(p, flags, cols_layout, stream);
+        return affine ? launch_rows_flags<float, true>(p, flags, cols_layout, ws, ws_bytes, stream)
+                      : launch_rows_flags<float, false>(p, flags, cols_layout, ws, ws_bytes, stream);
+    case HX_DTYPE_U32: return launch_rows_flags<uint32_t, false>(p, flags, cols_layout, ws, ws_bytes, stream);
+    case HX_DTYPE_I32: return launch_rows_flags<int32_t, false>(p, flags, cols_layout, ws, ws_bytes, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown dtype %d", (int)dtype);
 }
 
-} // namespace
-
-hx_status launch_rows(const RowsArgs &a, hipStream_t stream) {
-    RowParams p{};
-    p.base = a.base;
-    p.rows = a.rows;
-    p.cols = a.cols;
-    p.row_stride = (int64_t)a.row_stride;
-    p.col_stride = 1;
-    p.offset = a.offset;
-    p.a = a.a;
-    p.b = a.b;
-    p.out_sum = a.out_sum;
-    p.out_max = a.out_max;
-    p.out_arg = a.out_argmax;
-    p.out_stride = 1;
-    p.out_offset = 0;
-    int flags = (a.out_sum ? F_SUM : 0) | (a.out_argmax ? F_ARG : 0) | (a.out_max ? F_MAX : 0);
-    if (flags == 0) return HX_OK;
-    return launch_rows_any(p, a.dtype, a.affine, flags, false, stream);
+int rows_params(const RowsArgs &a, RowParams *p) {
+    *p = RowParams{};
+    p->base = a.base;
+    p->rows = a.rows;
+    p->cols = a.cols;
+    p->row_stride = (int64_t)a.row_stride;
+    p->col_stride = 1;
+    p->offset = a.offset;
+    p->a = a.a;
+    p->b = a.b;
+    p->out_sum = a.out_sum;
+    p->out_max = a.out_max;
+    p->out_arg = a.out_argmax;
+    p->out_stride = 1;
+    p->out_offset = 0;
+    return (a.out_sum ? F_SUM : 0) | (a.out_argmax ? F_ARG : 0) | (a.out_max ? F_MAX : 0);
 }
 
-hx_status launch_axis_reduce(const AxisArgs &a, hipStream_t stream) {
-    RowParams p{};
-    p.base = a.in;
-    p.rows = a.outer;
-    p.cols = a.axis_len;
-    p.row_stride = a.in_outer_stride;
-    p.col_stride = a.in_axis_stride;
-    p.offset = a.in_offset;
-    p.out_stride = a.out_stride;
-    p.out_offset = a.out_offset;
+int axis_params(const AxisArgs &a, RowParams *p, bool *cols_layout) {
+    *p = RowParams{};
+    p->base = a.in;
+    p->rows = a.outer;
+    p->cols = a.axis_len;
+    p->row_stride = a.in_outer_stride;
+    p->col_stride = a.in_axis_stride;
+    p->offset = a.in_offset;
+    p->out_stride = a.out_stride;
+    p->out_offset = a.out_offset;
     int flags = 0;
     switch (a.op) {
-    case HX_OP_SUM: flags = F_SUM; p.out_sum = a.out; break;
-    case HX_OP_MEAN: flags = F_MEAN; p.out_sum = a.out; break;
-    case HX_OP_PROD: flags = F_PROD; p.out_prod = a.out; break;
-    case HX_OP_MIN: flags = F_MIN; p.out_min = a.out; break;
-    case HX_OP_MAX: flags = F_MAX; p.out_max = a.out; break;
-    case HX_OP_ARGMAX: flags = F_ARG; p.out_arg = (uint32_t *)a.out; break;
+    case HX_OP_SUM: flags = F_SUM; p->out_sum = a.out; break;
+    case HX_OP_MEAN: flags = F_MEAN; p->out_sum = a.out; break;
+    case HX_OP_PROD: flags = F_PROD; p->out_prod = a.out; break;
+    case HX_OP_MIN: flags = F_MIN; p->out_min = a.out; break;
+    case HX_OP_MAX: flags = F_MAX; p->out_max = a.out; break;
+    case HX_OP_ARGMAX: flags = F_ARG; p->out_arg = (uint32_t *)a.out; break;
     }
     // Unit stride along the reduced axis -> lanes along the axis; unit
-    // stride across outputs -> threads across outputs.
+    // stride across outputs (and not along the axis) -> lanes across outputs.
     const bool axis_unit = a.in_axis_stride == 1 || a.in_axis_stride == -1;
     const bool outer_unit = a.in_outer_stride == 1 || a.in_outer_stride == -1;
-    const bool cols_layout = !axis_unit && outer_unit && a.outer >= 64;
-    return launch_rows_any(p, a.dtype, false, flags, cols_layout, stream);
+    *cols_layout = !axis_unit && outer_unit;
+    return flags;
+}
+
+} // namespace
+
+uint64_t rows_workspace_bytes(const RowsArgs &a) {
+    RowParams p;
+    const int flags = rows_params(a, &p);
+    return shape_bytes(p, plan_shape(p, false), flags);
+}
+
+hx_status launch_rows(const RowsArgs &a, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    RowParams p;
+    const int flags = rows_params(a, &p);
+    if (flags == 0) return HX_OK;
+    return launch_rows_any(p, a.dtype, a.affine, flags, false, ws, ws_bytes, stream);
+}
+
+uint64_t axis_reduce_workspace_bytes(const AxisArgs &a) {
+    RowParams p;
+    bool cols_layout;
+    const int flags = axis_params(a, &p, &cols_layout);
+    return shape_bytes(p, plan_shape(p, cols_layout), flags);
+}
+
+hx_status launch_axis_reduce(const AxisArgs &a, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    RowParams p;
+    bool cols_layout;
+    const int flags = axis_params(a, &p, &cols_layout);
+    return launch_rows_any(p, a.dtype, false, flags, cols_layout, ws, ws_bytes, stream);
 }
 
 } // namespace hx

@@ -104,6 +104,25 @@ hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t, void **w
     return HX_OK;
 }
 
+hx_status device_scratch(hx_device *dev, uint64_t bytes, void **scratch) {
+    *scratch = nullptr;
+    if (bytes == 0) return HX_OK;
+    std::lock_guard<std::mutex> lock(dev->ws_mu);
+    if (bytes > dev->scratch_bytes) {
+        if (dev->scratch) {
+            HX_HIP(hipDeviceSynchronize(), HX_ERR_DISPATCH_FAILED, "hipDeviceSynchronize");
+            HX_HIP(hipFree(dev->scratch), HX_ERR_ALLOCATION_FAILED, "scratch hipFree");
+            dev->scratch = nullptr;
+            dev->scratch_bytes = 0;
+        }
+        const uint64_t grow = bytes < (1ull << 20) ? (1ull << 20) : bytes;
+        HX_TRY(alloc_workspace(dev, grow, &dev->scratch));
+        dev->scratch_bytes = grow;
+    }
+    *scratch = dev->scratch;
+    return HX_OK;
+}
+
 hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
                                hipStream_t stream, uint32_t *tag) {
     const uint32_t t = (st.launches % 0x3FFFFFFFu) + 1u;
@@ -246,6 +265,7 @@ hx_status hx_device_close(hx_device *dev) {
         if (dev->pinned_ev[i]) (void)hipEventDestroy(dev->pinned_ev[i]);
     }
     if (dev->ws) (void)hipFree(dev->ws);
+    if (dev->scratch) (void)hipFree(dev->scratch);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return ok();
@@ -486,6 +506,17 @@ hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream) {
     if (!plan) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan");
     HX_TRY(bind_device(plan->dev));
     HX_TRY(plan->dispatch(pick_stream(plan->dev, stream)));
+    return ok();
+}
+
+hx_status hx_plan_dispatch_batch(hx_plan *const *plans, uint64_t count, hx_stream stream) {
+    if (count && !plans) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan array");
+    for (uint64_t i = 0; i < count; ++i)
+        if (!plans[i]) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan at batch index %llu", (unsigned long long)i);
+    for (uint64_t i = 0; i < count; ++i) {
+        HX_TRY(bind_device(plans[i]->dev));
+        HX_TRY(plans[i]->dispatch(pick_stream(plans[i]->dev, stream)));
+    }
     return ok();
 }
 

@@ -21,6 +21,7 @@
 
 #include <array>
 #include <cstdint>
+#include <initializer_list>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -262,10 +263,21 @@ class PreparedPlan {
         check(hx_plan_workspace_bytes(plan_, &b));
         return b;
     }
+    hx_plan *handle() const { return plan_; }
 
   private:
     hx_plan *plan_ = nullptr;
 };
+
+// submit_prepared_reduction_batch (rocm application/prepared_reduction.rs:
+// 164-174): the plans run in order on one stream, no host sync in between.
+inline void submit_prepared_reduction_batch(std::initializer_list<const PreparedPlan *> plans,
+                                            hx_stream stream = nullptr) {
+    std::vector<hx_plan *> handles;
+    handles.reserve(plans.size());
+    for (const PreparedPlan *p : plans) handles.push_back(p->handle());
+    check(hx_plan_dispatch_batch(handles.data(), handles.size(), stream));
+}
 
 namespace detail {
 inline const hx_affine *affine(const Affine *p, hx_affine &storage) {

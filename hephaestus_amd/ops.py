@@ -103,6 +103,17 @@ class PreparedPlan:
             pass
 
 
+def submit_prepared_reduction_batch(plans) -> None:
+    """Dispatch prepared plans in order on the device stream with no host
+    synchronisation between them (rocm application/prepared_reduction.rs:
+    164-174).  Accepts PreparedPlan and PreparedMapReduction handles."""
+    plans = list(plans)
+    if not plans:
+        return
+    arr = (ctypes.c_void_p * len(plans))(*[p.handle for p in plans])
+    _ffi.check(_ffi.lib().hx_plan_dispatch_batch(arr, len(plans), None))
+
+
 class RocmFullReductionOps:
     """FullReductionOps<RocmDevice, T> (rocm full_reduction_seam.rs:28-120)."""
 

@@ -405,6 +405,12 @@ hx_status hx_vector_binary(hx_device *dev, hx_vector_op op, hx_dtype dtype,
  * Allocates nothing.  Plans must not be dispatched concurrently with
  * themselves. */
 hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream);
+/* submit_prepared_reduction_batch (rocm application/prepared_reduction.rs:
+ * 164-174): dispatch `count` plans in order on `stream` with no host
+ * synchronisation between them; returns the first error.  A null entry is
+ * rejected before any plan runs. */
+hx_status hx_plan_dispatch_batch(hx_plan *const *plans, uint64_t count,
+                                 hx_stream stream);
 hx_status hx_plan_destroy(hx_plan *plan);
 /* Bytes of device workspace the plan owns. */
 hx_status hx_plan_workspace_bytes(const hx_plan *plan, uint64_t *bytes);

@@ -253,6 +253,14 @@ void rocm_reduce_contract(RocmDevice &dev) {
         CHECK(dev.download_owned(out)[0] == 0u);
         ops.reduce_full_into<MaxOp, uint32_t>(dev, {in, l}, {out, l1});
         CHECK(dev.download_owned(out)[0] == 16u);
+        // Prepared min and max submitted as one batch (prepared_reduction.rs:
+        // 164-174; cuda tests/contract.rs:717-726 holds the same clause).
+        auto out_min = dev.alloc_zeroed<uint32_t>(1), out_max = dev.alloc_zeroed<uint32_t>(1);
+        auto pmin = ops.prepare_reduce_full<MinOp, uint32_t>(dev, {in, l}, {out_min, l1});
+        auto pmax = ops.prepare_reduce_full<MaxOp, uint32_t>(dev, {in, l}, {out_max, l1});
+        submit_prepared_reduction_batch({&pmin, &pmax});
+        CHECK(dev.download_owned(out_min)[0] == 0u);
+        CHECK(dev.download_owned(out_max)[0] == 16u);
     }
     auto empty = dev.alloc_zeroed<uint32_t>(0);
     auto out = dev.upload(std::vector<uint32_t>{7});

@@ -1,0 +1,169 @@
+"""Axis reductions and axis scans on the shapes that need the split forms:
+tall matrices reduced or scanned along axis 0 (column tiles over chunks of
+the axis), few long rows reduced along axis 1 (split rows), transposed and
+negative-stride views, every op and dtype.  Each output line is checked
+against the oracle's fold of the same line: bit-exact for integers, max, min
+and argmax; f32 sums within 2*ceil(log2 n)*eps_f32*sum|y| of the oracle's
+f64 accumulation."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import hephaestus_amd as hx
+from hephaestus_amd import Layout, StridedView
+
+pytestmark = pytest.mark.gpu
+
+AXIS = hx.RocmAxisReductionOps()
+SCAN = hx.RocmScanOps()
+EPS = 2.0**-23
+OPS = {"sum": hx.SumOp, "mean": hx.MeanOp, "prod": hx.ProdOp, "min": hx.MinOp, "max": hx.MaxOp,
+       "argmax": hx.ArgMaxOp}
+
+
+def f32_bound(n, abs_sum):
+    return 2 * (int(n) - 1).bit_length() * EPS * abs_sum
+
+
+def lines_of(host, shape, strides, offset, axis):
+    """The reduced lines of a rank-2 view, in output order."""
+    idx = offset + np.indices(shape)[0] * strides[0] + np.indices(shape)[1] * strides[1]
+    sel = host[idx]
+    return np.ascontiguousarray(sel if axis == 1 else sel.T)
+
+
+def expect(oracle, op, lines):
+    if op == "sum":
+        return [oracle.full_sum(l) for l in lines]
+    if op == "mean":
+        return [oracle.full_sum(l) for l in lines]
+    if op == "prod":
+        if lines.dtype == np.float32:  # no f32 product in the oracle: numpy's f64 product, rtol below
+            return [np.prod(l.astype(np.float64)) for l in lines]
+        return [oracle.full_prod(l) for l in lines]
+    if op == "min":
+        return [oracle.full_min(l) for l in lines]
+    if op == "max":
+        return [oracle.full_max(l) for l in lines]
+    return [oracle.full_argmax(l) for l in lines]
+
+
+def run_axis(device, op, dtype, host, shape, strides, offset, axis):
+    buf = device.upload(host)
+    nout = shape[1 - axis]
+    out_dtype = np.uint32 if op == "argmax" else dtype
+    out = device.upload(np.full(nout, 7, out_dtype))
+    out_shape = [shape[0], 1] if axis == 1 else [1, shape[1]]
+    AXIS.reduce_axis_into(device, OPS[op], StridedView(buf, Layout.try_new(list(shape), list(strides), offset)),
+                          axis, StridedView(out, Layout.c_contiguous(out_shape)))
+    return device.download_owned(out)
+
+
+def check(oracle, op, dtype, got, lines):
+    want = expect(oracle, op, lines)
+    n = lines.shape[1]
+    if dtype == np.float32 and op in ("sum", "mean"):
+        for g, (ref, ab) in zip(got, want):
+            if op == "sum":
+                assert abs(float(g) - ref) <= f32_bound(n, ab)
+            else:
+                assert abs(float(g) - ref / n) <= f32_bound(n, ab) / n + EPS * abs(ref / n)
+        return
+    if dtype == np.float32 and op == "prod":
+        for g, ref in zip(got, want):
+            assert abs(float(g) - ref) <= EPS * abs(ref)
+        return
+    if op == "mean":
+        if dtype == np.int32:
+            want = [np.int32(int(np.int32(w)) // n if int(np.int32(w)) >= 0 else -((-int(np.int32(w))) // n))
+                    for w in want]
+        else:
+            want = [np.uint32(int(w) // n) for w in want]
+    assert np.array_equal(np.asarray(got), np.asarray(want, dtype=got.dtype))
+
+
+def host_for(oracle, dtype, n, seed, op):
+    if dtype == np.float32:
+        if op == "prod":
+            return oracle.uniform_real(n, seed, 0.999, 1.001)
+        return oracle.normal(n, seed)
+    if op == "argmax":
+        return (oracle.uniform_int(n, seed, 0, 50)).astype(dtype)  # many ties
+    if dtype == np.int32:
+        return oracle.uniform_int(n, seed, -1000, 1000, dtype=np.int32)
+    return oracle.uniform_int(n, seed, 0, 2**32 - 1)
+
+
+# (rows, cols), axis: tall column tiles (vector and scalar lanes), a single
+# chunk, few long rows (vector and scalar), and a [N,1] column.
+SHAPES = [((4099, 1000), 0), ((3001, 999), 0), ((20, 256), 0), ((3, 100003), 1), ((5, 65536), 1),
+          ((100000, 1), 0)]
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("shape,axis", SHAPES)
+def test_split_axis_reduce(device, oracle, shape, axis, dtype, op):
+    r, c = shape
+    host = host_for(oracle, dtype, r * c, seed=r + 3 * c + axis, op=op)
+    strides = (c, 1)
+    got = run_axis(device, op, dtype, host, shape, strides, 0, axis)
+    check(oracle, op, dtype, got, lines_of(host, shape, strides, 0, axis))
+
+
+@pytest.mark.parametrize("op", ["sum", "max", "argmax"])
+def test_axis_reduce_transposed_and_reversed_views(device, oracle, op):
+    r, c = 2000, 516
+    host = host_for(oracle, np.float32, r * c, seed=91, op=op)
+    # column-major view of a [c, r] buffer: axis 1 is strided, outputs adjacent
+    shape, strides = (c, r), (1, c)
+    got = run_axis(device, op, np.float32, host, shape, strides, 0, 1)
+    check(oracle, op, np.float32, got, lines_of(host, shape, strides, 0, 1))
+    # outputs walk backwards (stride -1) while the axis is strided
+    shape, strides, offset = (r, c), (c, -1), c - 1
+    got = run_axis(device, op, np.float32, host, shape, strides, offset, 0)
+    check(oracle, op, np.float32, got, lines_of(host, shape, strides, offset, 0))
+
+
+def test_split_f32_sums_are_deterministic(device, oracle):
+    r, c = 8192, 1024
+    host = oracle.normal(r * c, seed=5)
+    a = run_axis(device, "sum", np.float32, host, (r, c), (c, 1), 0, 0)
+    b = run_axis(device, "sum", np.float32, host, (r, c), (c, 1), 0, 0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("subset", ["sum+max+argmax", "sum", "argmax"])
+def test_fused_rows_with_few_long_rows(device, oracle, subset):
+    rows, cols = 3, (1 << 20) + 12
+    host = oracle.normal(rows * cols, seed=17)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host, rows, cols, prologue=(0.5, 0.25))
+    buf = device.upload(host)
+    want = subset.split("+")
+    s = device.upload(np.full(rows, 7.0, np.float32)) if "sum" in want else None
+    m = device.upload(np.full(rows, 7.0, np.float32)) if "max" in want else None
+    i = device.upload(np.full(rows, 7, np.uint32)) if "argmax" in want else None
+    AXIS.reduce_rows_fused(device, buf, rows, cols, out_sum=s, out_max=m, out_argmax=i, prologue=(0.5, 0.25))
+    if s is not None:
+        assert np.all(np.abs(device.download_owned(s) - s_ref) <= [f32_bound(cols, a) for a in a_ref])
+    if m is not None:
+        assert np.array_equal(device.download_owned(m), m_ref)
+    if i is not None:
+        assert np.array_equal(device.download_owned(i), i_ref)
+
+
+def test_prepared_split_axis_reduce_rebinds(device, oracle):
+    r, c = 4096, 512
+    x = oracle.uniform_int(r * c, seed=2, lo=0, hi=1000)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, c)
+    plan = AXIS.prepare_reduce_axis_into(device, hx.SumOp, StridedView(buf, Layout.c_contiguous([r, c])), 0,
+                                    StridedView(out, Layout.c_contiguous([1, c])))
+    assert plan.workspace_bytes() > 0
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), x.reshape(r, c).sum(axis=0, dtype=np.uint32))
+    y = oracle.uniform_int(r * c, seed=3, lo=0, hi=1000)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), y.reshape(r, c).sum(axis=0, dtype=np.uint32))

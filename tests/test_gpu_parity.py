@@ -6,6 +6,8 @@ sums and scans must satisfy |err| <= 2*ceil(log2 n)*eps_f32*sum|y| against
 the oracle's f64 accumulation."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -484,6 +486,51 @@ def test_prepared_plans_allocate_once_and_rebind(device, oracle):
     device.write_buffer(buf, y)
     plan.dispatch()
     assert np.array_equal(device.download_owned(out), oracle.scan_sum(y, exclusive=True))
+
+
+def test_prepared_batch_submission(device, oracle):
+    """submit_prepared_reduction_batch (prepared_reduction.rs:164-174): the
+    min/max clause of the CUDA contract (tests/contract.rs:717-726) plus a
+    map-reduction and a scan in the same batch, then a rebind."""
+    n = 1027
+    x = (np.arange(n) % 17).astype(np.uint32)
+    buf = device.upload(x)
+    one = Layout.c_contiguous([1])
+    lay = Layout.c_contiguous([n])
+    outs = [device.alloc_zeroed(np.uint32, 1) for _ in range(2)]
+    pmin = FULL.prepare_reduce_full(device, hx.MinOp, StridedView(buf, lay), StridedView(outs[0], one))
+    pmax = FULL.prepare_reduce_full(device, hx.MaxOp, StridedView(buf, lay), StridedView(outs[1], one))
+    scan_out = device.alloc_zeroed(np.uint32, n)
+    pscan = SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(buf, lay), 0, hx.ScanDirection.Forward,
+                                   StridedView(scan_out, lay), hx.ScanKind.Inclusive)
+    pl1 = hx.PreparedMapReduction(device, hx._ffi.MAP_NORM_L1, StridedView(buf, lay), None)
+    hx.submit_prepared_reduction_batch([pmin, pmax, pscan, pl1])
+    assert device.download_owned(outs[0])[0] == 0
+    assert device.download_owned(outs[1])[0] == 16
+    assert np.array_equal(device.download_owned(scan_out), oracle.scan_sum(x))
+    assert device.download_owned(pl1.output)[0] == oracle.full_sum(x)
+    y = (x + 3).astype(np.uint32)
+    device.write_buffer(buf, y)
+    hx.submit_prepared_reduction_batch([pmin, pmax, pscan, pl1])
+    assert device.download_owned(outs[0])[0] == 3
+    assert device.download_owned(outs[1])[0] == 19
+    assert np.array_equal(device.download_owned(scan_out), oracle.scan_sum(y))
+    assert device.download_owned(pl1.output)[0] == oracle.full_sum(y)
+    hx.submit_prepared_reduction_batch([])
+
+
+def test_batch_rejects_null_plan_before_running_any(device):
+    from hephaestus_amd import _ffi
+
+    n = 64
+    buf = device.upload(np.ones(n, np.uint32))
+    out = device.alloc_zeroed(np.uint32, 1)
+    plan = FULL.prepare_reduce_full(device, hx.SumOp, StridedView(buf, Layout.c_contiguous([n])),
+                                    StridedView(out, Layout.c_contiguous([1])))
+    arr = (ctypes.c_void_p * 2)(plan.handle, None)
+    with pytest.raises(hx.InvalidConfiguration, match="null plan at batch index 1"):
+        _ffi.check(_ffi.lib().hx_plan_dispatch_batch(arr, 2, None))
+    assert device.download_owned(out)[0] == 0
 
 
 # ------------------------------------------------------------ copy_buffer
