@@ -31,11 +31,12 @@ sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32",
-             "axpy_f32")
+             "axpy_f32", "colsum_f32", "colscan_u32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
              "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
-             "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1"}
+             "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
+             "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_scan_kernel"}
 
 
 def log(msg: str) -> None:
@@ -168,6 +169,36 @@ def bench_axpy_f32(hx, dev, args):
     ops = hx.RocmDenseVectorOps()
     ms = time_plan(dev, lambda: ops.axpy(dev, t, s, 0.5), args.steps, args.warmup)
     return {"n": n, "ms": ms, "bytes": 12 * n}
+
+
+def bench_colsum_f32(hx, dev, args):
+    """Axis-0 sum of a 65536 x 4096 row-major f32 matrix (4096 outputs)."""
+    from hephaestus_amd import Layout, StridedView
+
+    rows, cols = 65536, 4096
+    x = dev.alloc_uninitialized(np.float32, rows * cols)
+    dev.fill_normal(x, seed=7)
+    out = dev.alloc_uninitialized(np.float32, cols)
+    plan = hx.RocmAxisReductionOps().prepare_reduce_axis_into(
+        dev, hx.SumOp, StridedView(x, Layout.c_contiguous([rows, cols])), 0,
+        StridedView(out, Layout.c_contiguous([1, cols])))
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    return {"n": rows * cols, "ms": ms, "bytes": 4 * rows * cols + 4 * cols}
+
+
+def bench_colscan_u32(hx, dev, args):
+    """Axis-0 inclusive scan of a 65536 x 4096 row-major u32 matrix."""
+    from hephaestus_amd import Layout, StridedView
+
+    rows, cols = 65536, 4096
+    x = dev.alloc_uninitialized(np.uint32, rows * cols)
+    dev.fill_uniform_int(x, seed=8, lo=0, hi=255)
+    out = dev.alloc_uninitialized(np.uint32, rows * cols)
+    lay = Layout.c_contiguous([rows, cols])
+    plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                                              StridedView(out, lay))
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    return {"n": rows * cols, "ms": ms, "bytes": 8 * rows * cols}
 
 
 def bench_copy_u32(hx, dev, args):
@@ -364,7 +395,8 @@ def main() -> int:
         },
     }
     if args.workload == "all":
-        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32", "axpy_f32"):
+        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32",
+                     "colscan_u32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
             line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

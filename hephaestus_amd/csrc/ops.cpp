@@ -402,7 +402,13 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, scan_workspace_bytes(a), s, &ws));
+    const uint64_t bytes = scan_workspace_bytes(a);
+    if (!scan_uses_lookback(a)) {
+        HX_TRY(device_scratch(dev, bytes, &ws));
+        HX_TRY(launch_scan(a, ws, bytes, dev->ws_lookback, s));
+        return ok();
+    }
+    HX_TRY(device_workspace(dev, bytes, s, &ws));
     HX_TRY(launch_scan(a, ws, dev->ws_bytes, dev->ws_lookback, s));
     return ok();
 }

@@ -5,7 +5,7 @@
 // contiguous chunk serially, lane 0 folds the chunk totals, and a second sweep
 // re-reads and re-writes the output (core accelerator/scan.rs:56-155).  A 1-D
 // scan of 2^28 elements therefore runs on one CU.  Here every line is cut
-// into tiles of 16384 elements that all CUs process in a single pass:
+// into tiles of 32768 elements that all CUs process in a single pass:
 //
 //   * block b scans tile b.  The tile is loaded with 16-byte vectors,
 //     wave-striped: step j of wave w holds 256 contiguous elements, lane l
@@ -46,7 +46,7 @@
 namespace hx {
 namespace {
 
-constexpr int kBlock = 256;                          // serial-lines kernel
+constexpr int kBlock = 256;                          // column-scan kernels
 constexpr int kWaves = 8;                            // waves per tile block
 constexpr int kSteps = 16;                           // 16-byte vectors per lane
 constexpr int kTile = kWaves * kWave * 4 * kSteps;   // 32768 elements
@@ -481,31 +481,254 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
     }
 }
 
-// Many short strided lines whose starts are adjacent in memory (axis-0 scan
-// of a row-major matrix): one thread per line walks it serially, so each load
-// instruction of a wave covers 64 adjacent lines.  f32 sums accumulate in f64.
-template <typename T, typename Op, bool EXCL, bool REV>
-__global__ __launch_bounds__(kBlock) void scan_lines_serial_kernel(ScanParams p) {
-    using A = typename std::conditional<std::is_same<T, float>::value, double, T>::type;
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
-    const T *in = (const T *)p.in;
-    T *out = (T *)p.out;
-    for (uint64_t line = (uint64_t)blockIdx.x * kBlock + threadIdx.x; line < p.lines; line += nthreads) {
-        const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
-        const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
-        A acc = Op::template identity<A>();
-        for (uint64_t i = 0; i < p.len; ++i) {
-            const uint64_t li = REV ? (p.len - 1 - i) : i;
-            const A v = (A)in[ib + (int64_t)li * p.in_elem_stride];
+// Column scans: many strided lines whose starts are adjacent in memory
+// (axis-0 scan of a row-major matrix).  Lanes run across lines -- a wave owns
+// 64*V adjacent lines, V = 4 giving every lane one 16-byte load per step --
+// and the scan axis is cut into chunks so that thousands of waves share the
+// work however tall the matrix is:
+//   col_totals_kernel  chunk totals of every line (one read of the input);
+//   col_carry_kernel   per line, an exclusive scan of its chunk totals in
+//                      place (chunks x lines words, a thread per line);
+//   col_scan_kernel    every chunk rescanned from its carry, outputs written.
+// With one chunk only col_scan_kernel runs (carry = identity).  Each lane
+// walks its lines serially; f32 accumulates in f64, integers wrap in u32.
+template <typename T> struct ColAcc { using type = uint32_t; };
+template <> struct ColAcc<float> { using type = double; };
+
+struct ColShape {
+    int V = 1;
+    uint64_t groups = 0, chunk = 0;
+    uint32_t nchunks = 1;
+};
+
+template <typename T, int V> struct ColIO;
+template <typename T> struct ColIO<T, 1> {
+    using A = typename ColAcc<T>::type;
+    static __device__ __forceinline__ void load(const T *p, A (&x)[1]) { x[0] = (A)__builtin_nontemporal_load(p); }
+    static __device__ __forceinline__ void store(T *p, const A (&y)[1]) { __builtin_nontemporal_store((T)y[0], p); }
+};
+template <typename T> struct ColIO<T, 4> {
+    using A = typename ColAcc<T>::type;
+    using Vt = typename Vec4<T>::type;
+    static __device__ __forceinline__ void load(const T *p, A (&x)[4]) {
+        const Vt v = __builtin_nontemporal_load((const Vt *)p);
+        x[0] = (A)v.x;
+        x[1] = (A)v.y;
+        x[2] = (A)v.z;
+        x[3] = (A)v.w;
+    }
+    static __device__ __forceinline__ void store(T *p, const A (&y)[4]) {
+        Vt v;
+        v.x = (T)y[0];
+        v.y = (T)y[1];
+        v.z = (T)y[2];
+        v.w = (T)y[3];
+        __builtin_nontemporal_store(v, (Vt *)p);
+    }
+};
+
+// Wave w -> (line group g, chunk k); adjacent waves take adjacent groups of
+// the same chunk.  Returns false for lanes with no line.
+struct ColWork {
+    uint64_t line0, k, i0, i1;
+};
+__device__ __forceinline__ bool col_work(const ScanParams &p, uint64_t chunk, uint32_t nchunks, uint64_t groups,
+                                         int V, ColWork *w) {
+    const uint64_t wave = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (wave >= groups * nchunks) return false;
+    const uint64_t g = wave % groups;
+    w->k = wave / groups;
+    w->line0 = (g * kWave + (uint64_t)lane_id()) * V;
+    if (w->line0 >= p.lines) return false;
+    w->i0 = w->k * chunk;
+    w->i1 = w->i0 + chunk < p.len ? w->i0 + chunk : p.len;
+    return true;
+}
+
+template <typename T, typename Op, int V, bool REV>
+__global__ __launch_bounds__(kBlock) void col_totals_kernel(ScanParams p, typename ColAcc<T>::type *totals,
+                                                            uint64_t chunk, uint32_t nchunks, uint64_t groups) {
+    using A = typename ColAcc<T>::type;
+    constexpr int kU = V == 4 ? 8 : 16;
+    ColWork w;
+    if (!col_work(p, chunk, nchunks, groups, V, &w)) return;
+    const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)w.line0 * p.in_line_stride);
+    A acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = Op::template identity<A>();
+    uint64_t i = w.i0;
+    for (; i + kU <= w.i1; i += kU) {
+        A x[kU][V];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const uint64_t li = REV ? p.len - 1 - (i + u) : i + u;
+            ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int v = 0; v < V; ++v) acc[v] = Op::combine(acc[v], x[u][v]);
+    }
+    for (; i < w.i1; ++i) {
+        const uint64_t li = REV ? p.len - 1 - i : i;
+        A x[V];
+        ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x);
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = Op::combine(acc[v], x[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) totals[w.k * p.lines + w.line0 + v] = acc[v];
+}
+
+// Exclusive scan of each line's chunk totals, in place.  A block owns 64
+// lines (lanes) and kCarrySlices waves; wave s totals its contiguous range of
+// chunks, the slice totals are scanned through LDS, and each wave rewrites
+// its range from its slice carry.
+constexpr int kCarrySlices = 16;
+
+template <typename A, typename Op>
+__global__ __launch_bounds__(kWave *kCarrySlices) void col_carry_kernel(A *totals, uint64_t lines,
+                                                                        uint32_t nchunks) {
+    __shared__ A sh[kCarrySlices * kWave];
+    const int lane = lane_id();
+    const int s = threadIdx.x / kWave;
+    const uint64_t line = (uint64_t)blockIdx.x * kWave + lane;
+    const uint32_t per = (nchunks + kCarrySlices - 1) / kCarrySlices;
+    const uint32_t k0 = s * per < nchunks ? s * per : nchunks;
+    const uint32_t k1 = k0 + per < nchunks ? k0 + per : nchunks;
+    A t = Op::template identity<A>();
+    if (line < lines)
+        for (uint32_t k = k0; k < k1; ++k) t = Op::combine(t, totals[(uint64_t)k * lines + line]);
+    sh[s * kWave + lane] = t;
+    __syncthreads();
+    if (line >= lines) return;
+    A acc = Op::template identity<A>();
+    for (int q = 0; q < s; ++q) acc = Op::combine(acc, sh[q * kWave + lane]);
+    for (uint32_t k = k0; k < k1; ++k) {
+        const A v = totals[(uint64_t)k * lines + line];
+        totals[(uint64_t)k * lines + line] = acc;
+        acc = Op::combine(acc, v);
+    }
+}
+
+template <typename T, typename Op, int V, bool EXCL, bool REV, bool CARRY>
+__global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carries,
+                                                          uint64_t chunk, uint32_t nchunks, uint64_t groups) {
+    using A = typename ColAcc<T>::type;
+    constexpr int kU = V == 4 ? 8 : 16;
+    ColWork w;
+    if (!col_work(p, chunk, nchunks, groups, V, &w)) return;
+    const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)w.line0 * p.in_line_stride);
+    T *out = (T *)p.out + ((int64_t)p.out_offset + (int64_t)w.line0 * p.out_line_stride);
+    A acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+        acc[v] = CARRY ? carries[w.k * p.lines + w.line0 + v] : Op::template identity<A>();
+    auto step = [&](uint64_t li, const A (&x)[V]) {
+        A y[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
             if constexpr (EXCL) {
-                out[ob + (int64_t)li * p.out_elem_stride] = (T)acc;
-                acc = Op::combine(acc, v);
+                y[v] = acc[v];
+                acc[v] = Op::combine(acc[v], x[v]);
             } else {
-                acc = Op::combine(acc, v);
-                out[ob + (int64_t)li * p.out_elem_stride] = (T)acc;
+                acc[v] = Op::combine(acc[v], x[v]);
+                y[v] = acc[v];
             }
         }
+        ColIO<T, V>::store(out + (int64_t)li * p.out_elem_stride, y);
+    };
+    uint64_t i = w.i0;
+    for (; i + kU <= w.i1; i += kU) {
+        A x[kU][V];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const uint64_t li = REV ? p.len - 1 - (i + u) : i + u;
+            ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) step(REV ? p.len - 1 - (i + u) : i + u, x[u]);
     }
+    for (; i < w.i1; ++i) {
+        const uint64_t li = REV ? p.len - 1 - i : i;
+        A x[V];
+        ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x);
+        step(li, x);
+    }
+}
+
+// 16 waves per CU: on a 65536 x 4096 u32 column scan 4096 waves of 256 steps
+// took 164 + 12 + 386 us (totals, carry, rescan); 8192 waves 202 + 23 + 512.
+constexpr uint64_t kColTargetWaves = 4096;
+constexpr uint64_t kColMinChunk = 32;      // scan steps per chunk
+
+bool column_mode(const ScanArgs &a) {
+    const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
+    const bool adjacent = (a.in_line_stride == 1 || a.in_line_stride == -1) &&
+                          (a.out_line_stride == 1 || a.out_line_stride == -1);
+    return !contiguous && adjacent && a.lines >= 16;
+}
+
+ColShape column_shape(const ScanArgs &a) {
+    ColShape s;
+    const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
+    const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
+    const bool vec = a.in_line_stride == 1 && a.out_line_stride == 1 && a.lines % 4 == 0 && ibase % 16 == 0 &&
+                     obase % 16 == 0 && a.in_elem_stride % 4 == 0 && a.out_elem_stride % 4 == 0;
+    s.V = vec ? 4 : 1;
+    s.groups = ceil_div(a.lines, (uint64_t)kWave * s.V);
+    uint64_t k = 1;
+    if (s.groups < kColTargetWaves) {
+        k = ceil_div(kColTargetWaves, s.groups);
+        const uint64_t kmax = ceil_div(a.len, kColMinChunk);
+        if (k > kmax) k = kmax;
+    }
+    if (k <= 1) {
+        s.chunk = a.len;
+        s.nchunks = 1;
+    } else {
+        s.chunk = ceil_div(a.len, k);
+        s.nchunks = (uint32_t)ceil_div(a.len, s.chunk);
+    }
+    return s;
+}
+
+uint64_t column_bytes(const ScanArgs &a) {
+    const ColShape s = column_shape(a);
+    if (s.nchunks <= 1 || a.lines == 0) return 0;
+    return (uint64_t)s.nchunks * a.lines * (a.dtype == HX_DTYPE_F32 ? 8u : 4u);
+}
+
+template <typename T, typename Op, int V, bool EXCL, bool REV>
+hx_status launch_column_v(const ScanParams &p, const ColShape &s, void *ws, hipStream_t stream) {
+    using A = typename ColAcc<T>::type;
+    A *totals = (A *)ws;
+    const uint64_t blocks = ceil_div(s.groups * s.nchunks, kBlock / kWave);
+    if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "column scan exceeds the grid range");
+    const dim3 grid((uint32_t)blocks), block(kBlock);
+    if (s.nchunks <= 1) {
+        hipLaunchKernelGGL((col_scan_kernel<T, Op, V, EXCL, REV, false>), grid, block, 0, stream, p,
+                           (const A *)nullptr, s.chunk, s.nchunks, s.groups);
+        return check_launch("col_scan_kernel");
+    }
+    hipLaunchKernelGGL((col_totals_kernel<T, Op, V, REV>), grid, block, 0, stream, p, totals, s.chunk, s.nchunks,
+                       s.groups);
+    HX_TRY(check_launch("col_totals_kernel"));
+    hipLaunchKernelGGL((col_carry_kernel<A, Op>), dim3((uint32_t)ceil_div(p.lines, kWave)), dim3(kWave * kCarrySlices),
+                       0, stream, totals, p.lines, s.nchunks);
+    HX_TRY(check_launch("col_carry_kernel"));
+    hipLaunchKernelGGL((col_scan_kernel<T, Op, V, EXCL, REV, true>), grid, block, 0, stream, p, (const A *)totals,
+                       s.chunk, s.nchunks, s.groups);
+    return check_launch("col_scan_kernel");
+}
+
+template <typename T, typename Op, bool EXCL>
+hx_status launch_column(const ScanParams &p, const ColShape &s, bool rev, void *ws, hipStream_t stream) {
+    if (s.V == 4)
+        return rev ? launch_column_v<T, Op, 4, EXCL, true>(p, s, ws, stream)
+                   : launch_column_v<T, Op, 4, EXCL, false>(p, s, ws, stream);
+    return rev ? launch_column_v<T, Op, 1, EXCL, true>(p, s, ws, stream)
+               : launch_column_v<T, Op, 1, EXCL, false>(p, s, ws, stream);
 }
 
 // One 64-bit word per entry (packed u32), four per entry (split f64).
@@ -525,28 +748,8 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     return check_launch("scan_tiles_kernel");
 }
 
-template <typename T, typename Op, bool EXCL>
-hx_status launch_serial(const ScanParams &p, bool rev, hipStream_t stream) {
-    uint64_t blocks = ceil_div(p.lines, kBlock);
-    if (blocks > (1u << 20)) blocks = 1u << 20;
-    if (rev)
-        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, true>), dim3((uint32_t)blocks), dim3(kBlock), 0,
-                           stream, p);
-    else
-        hipLaunchKernelGGL((scan_lines_serial_kernel<T, Op, EXCL, false>), dim3((uint32_t)blocks), dim3(kBlock), 0,
-                           stream, p);
-    return check_launch("scan_lines_serial_kernel");
-}
-
-bool serial_mode(const ScanArgs &a) {
-    const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
-    const bool adjacent = (a.in_line_stride == 1 || a.in_line_stride == -1) &&
-                          (a.out_line_stride == 1 || a.out_line_stride == -1);
-    return !contiguous && adjacent && a.lines >= 256;
-}
-
 uint64_t scan_bytes(const ScanArgs &a) {
-    if (serial_mode(a)) return kWorkspaceHeader;
+    if (column_mode(a)) return column_bytes(a);
     const uint64_t tpl = ceil_div(a.len, kTile);
     const bool f64 = a.dtype == HX_DTYPE_F32;
     return kLookbackOffset + status_bytes(tpl * a.lines, f64) + status_bytes(ceil_div(tpl, kSuper) * a.lines, f64);
@@ -570,9 +773,13 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out_offset = a.out_offset;
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
-    if (serial_mode(a)) {
-        return a.exclusive ? launch_serial<T, Op, true>(p, a.reverse, stream)
-                           : launch_serial<T, Op, false>(p, a.reverse, stream);
+    if (column_mode(a)) {
+        const ColShape cs = column_shape(a);
+        if (cs.nchunks > 1 && ws_bytes < column_bytes(a))
+            return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small",
+                        (unsigned long long)ws_bytes);
+        return a.exclusive ? launch_column<T, Op, true>(p, cs, a.reverse, ws, stream)
+                           : launch_column<T, Op, false>(p, cs, a.reverse, ws, stream);
     }
     if (p.total_tiles > 0x7FFFFFFFull)
         return fail(HX_ERR_DISPATCH_FAILED, "scan of %llu tiles exceeds the grid range",
@@ -605,6 +812,8 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 } // namespace
 
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
+
+bool scan_uses_lookback(const ScanArgs &a) { return !column_mode(a); }
 
 hx_status launch_scan(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     const bool prod = a.op == HX_OP_PROD;

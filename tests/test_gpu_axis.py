@@ -167,3 +167,99 @@ def test_prepared_split_axis_reduce_rebinds(device, oracle):
     device.write_buffer(buf, y)
     plan.dispatch()
     assert np.array_equal(device.download_owned(out), y.reshape(r, c).sum(axis=0, dtype=np.uint32))
+
+
+# ------------------------------------------------------------ column scans
+def scan_lines_want(oracle, op, lines, exclusive, reverse):
+    """Per line: the oracle's scan (ints: bit-exact; f32 sum: (ref, |prefix|))."""
+    if op == "sum":
+        return [oracle.scan_sum(l, exclusive=exclusive, reverse=reverse) for l in lines]
+    if lines.dtype == np.float32:  # no f32 product scan in the oracle: numpy's f64 product, rtol below
+        out = []
+        for l in lines:
+            v = l.astype(np.float64)[::-1] if reverse else l.astype(np.float64)
+            c = np.cumprod(v)
+            if exclusive:
+                c = np.concatenate([[1.0], c[:-1]])
+            out.append(c[::-1] if reverse else c)
+        return out
+    return [oracle.scan_prod(l, exclusive=exclusive, reverse=reverse) for l in lines]
+
+
+def run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exclusive, reverse, seed):
+    r, c = shape
+    size = offset + 1 + sum((shape[d] - 1) * abs(strides[d]) for d in range(2))
+    if dtype == np.float32:
+        host = (oracle.uniform_real(size, seed, 0.999, 1.001) if op == "prod"
+                else oracle.uniform_real(size, seed, -1.0, 1.0))
+    elif dtype == np.int32:
+        host = oracle.uniform_int(size, seed, -1000, 1000, dtype=np.int32)
+    else:
+        host = oracle.uniform_int(size, seed, 0, 2**32 - 1)
+    buf = device.upload(host)
+    out = device.upload(np.full(size, 7, dtype))
+    lay = Layout.try_new(list(shape), list(strides), offset)  # the output mirrors the input's layout
+    SCAN.scan_axis_into(device, hx.CumSumOp if op == "sum" else hx.CumProdOp, StridedView(buf, lay), axis,
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive if exclusive else hx.ScanKind.Inclusive)
+    got_host = device.download_owned(out)
+    got_lines = lines_of(got_host, shape, strides, offset, axis)
+    touched = np.zeros(size, bool)
+    touched[offset + np.indices(shape)[0] * strides[0] + np.indices(shape)[1] * strides[1]] = True
+    assert np.all(got_host[~touched] == 7)
+    lines = lines_of(host, shape, strides, offset, axis)
+    want = scan_lines_want(oracle, op, lines, exclusive, reverse)
+    n = lines.shape[1]
+    for g, w in zip(got_lines, want):
+        if dtype == np.float32 and op == "sum":
+            bad, worst = oracle.check_f32_bound(g, w[0], w[1], n)
+            assert bad == 0, worst
+        elif dtype == np.float32:
+            assert np.all(np.abs(g.astype(np.float64) - w) <= EPS * np.abs(w))
+        else:
+            assert np.array_equal(g, w)
+
+
+# (rows, cols) scanned along axis 0: vector lanes with many chunks, scalar
+# lanes, one chunk only, 16 lines x 65536 steps (2048 chunks).
+COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256), (65536, 16)]
+
+
+@pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("op", ["sum", "prod"])
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("shape", COLUMN_SHAPES)
+def test_column_scan(device, oracle, shape, dtype, op, reverse, kind):
+    r, c = shape
+    run_column_scan(device, oracle, op, dtype, shape, (c, 1), 0, 0, kind == "exclusive", reverse,
+                    seed=r * 7 + c)
+
+
+@pytest.mark.parametrize("op", ["sum", "prod"])
+def test_column_scan_transposed_and_reversed_lines(device, oracle, op):
+    # column-major view: axis 1 strided, lines adjacent
+    run_column_scan(device, oracle, op, np.int32, (516, 2000), (1, 516), 0, 1, False, False, seed=1)
+    # lines walk backwards in memory (stride -1)
+    run_column_scan(device, oracle, op, np.int32, (2000, 516), (516, -1), 515, 0, True, True, seed=2)
+    run_column_scan(device, oracle, op, np.float32, (2000, 516), (516, -1), 515, 0, False, False, seed=3)
+
+
+def test_prepared_column_scan_rebinds(device, oracle):
+    r, c = 8192, 256
+    x = oracle.uniform_int(r * c, seed=4, lo=0, hi=1000)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, r * c)
+    lay = Layout.c_contiguous([r, c])
+    plan = SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(buf, lay), 0, hx.ScanDirection.Forward,
+                                  StridedView(out, lay), hx.ScanKind.Exclusive)
+    assert plan.workspace_bytes() > 0
+    for _ in range(2):
+        plan.dispatch()
+    want = np.cumsum(x.reshape(r, c), axis=0, dtype=np.uint32) - x.reshape(r, c)
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+    y = oracle.uniform_int(r * c, seed=5, lo=0, hi=1000)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    want = np.cumsum(y.reshape(r, c), axis=0, dtype=np.uint32) - y.reshape(r, c)
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want)
