@@ -36,9 +36,10 @@ template <int WAVES, int STEPS> struct SegTile {
     static constexpr int kWaveElems = kWave * 4 * STEPS;
     static constexpr int kElems = WAVES * kWaveElems;
 };
-// 4 x 8 measured best at 2^27 (8192-value tiles, six blocks per CU): larger
+// 4 x 8 measured best at 2^27 (8192-value tiles, seven blocks per CU): larger
 // tiles leave fewer blocks per CU to overlap one block's barriers with
-// another's loads (8 x 16: 230 us; 8 x 8: 120 us; 4 x 8: 118 us).
+// another's loads (4 x 8: 89.5 us; 2 x 8: 90.5-92; 8 x 8: 107; an earlier
+// form of the kernel: 8 x 16 230 us).
 constexpr int kSegWaves = 4, kSegSteps = 8;
 constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
 constexpr int kSlots = 2048; // segment values compacted per round
@@ -92,28 +93,6 @@ __device__ __forceinline__ void publish_if_unset(uint64_t *word, uint32_t tag, u
     if ((uint32_t)(cur >> 34) == tag) return;
     __hip_atomic_compare_exchange_strong(word, &cur, status_word(tag, flag, v), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// "Last marked value" scan across the 64 lanes: lane l ends with the (h, v)
-// of the highest lane <= l whose h is set (h = 0 when there is none).  Same
-// DPP pattern as wave_inclusive_scan with the associative operator
-// "a later entry that has a value wins".
-__device__ __forceinline__ void wave_last_scan(uint32_t &h, uint32_t &v) {
-#define HX_LAST_STEP(CTRL, MASK)                                                                           \
-    {                                                                                                      \
-        const uint32_t oh = dpp_move<CTRL, MASK>(0u, h), ov = dpp_move<CTRL, MASK>(0u, v);                 \
-        if (!h) {                                                                                          \
-            h = oh;                                                                                        \
-            v = ov;                                                                                        \
-        }                                                                                                  \
-    }
-    HX_LAST_STEP(kDppRowShr1, 0xf)
-    HX_LAST_STEP(kDppRowShr2, 0xf)
-    HX_LAST_STEP(kDppRowShr4, 0xf)
-    HX_LAST_STEP(kDppRowShr8, 0xf)
-    HX_LAST_STEP(kDppRowBcast15, 0xa)
-    HX_LAST_STEP(kDppRowBcast31, 0xc)
-#undef HX_LAST_STEP
 }
 
 // Exclusive prefix of segment sums carried in from earlier tiles: folds
@@ -170,13 +149,14 @@ template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_
 //            (q + 1 + t0 is an offset in (t0, t1]);
 //   s_wrank  per mask word, the popcount of the earlier words of its wave,
 //            so a set bit's rank among all set bits is a few LDS reads;
-//   s_val    the segment values, compacted by rank, kSlots per round.
+//   s_val    x at the set bits, compacted by rank, kSlots per round.
 // Each lane keeps its elements' tile-local inclusive prefixes x in
-// registers.  A segment ending at element q is x(q) minus x at the previous
-// set bit, found with a "last set bit" scan (lanes by DPP, steps and waves
-// by carries); with no earlier set bit the segment began at or before the
-// tile start and takes the look-back carry.  Threads assigned to the
-// offsets then read their segment's value by rank and write it.
+// registers and stores x at its set bits.  Set bits are segment ends, so
+// the bit before a segment's end bit is the end of the previous segment: the
+// thread assigned to offset k reads x at its end's rank and subtracts x at
+// the rank before (mod 2^32).  A segment that began before the tile start
+// takes its x alone plus the look-back carry; one that begins exactly at the
+// tile start takes its x alone.
 //
 // The tile's offset range comes from the map built by seg_tile_map_kernel,
 // so the offsets a block needs are loaded once, right after its values,
@@ -185,8 +165,12 @@ template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_
 // written first, and wave 0 looks back last, when the rest of the block is
 // done (polling earlier, between two barriers, held every wave of the block
 // and cost ~15% at 2^27 values).
+// Register budget: 72 VGPRs gives 7 waves per SIMD, seven 4-wave blocks per
+// CU (the compiler's own choice, 74, allows six: 92 us at 2^27 against 89.5;
+// a 64 cap spills to scratch and takes 156 us).
 template <int WAVES, int STEPS>
-__global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams p) {
+__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7, 7))) void segmented_sum_kernel(
+    SegParams p) {
     static_assert(STEPS % 8 == 0, "each lane ranks whole mask words");
     constexpr int kWaveElems = SegTile<WAVES, STEPS>::kWaveElems;
     constexpr int kTile = SegTile<WAVES, STEPS>::kElems;
@@ -196,12 +180,11 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
     constexpr int kLaneWords = kWaveWords / kWave;
     __shared__ uint32_t s_wave_tot[WAVES];
     __shared__ uint32_t s_wave_pop[WAVES];
-    __shared__ uint32_t s_wave_last[WAVES]; // x at the wave's last set bit
     __shared__ uint32_t s_hpref;
     __shared__ uint32_t s_open; // in-tile part of the open segment
     __shared__ uint32_t s_mask[kWords];
     __shared__ uint32_t s_wrank[kWords];
-    __shared__ uint32_t s_val[kSlots];
+    __shared__ uint32_t s_val[kSlots + 1]; // slot 0: the rank before the round
 
     const uint64_t tile = blockIdx.x;
     const uint32_t tag = p.tag;
@@ -327,7 +310,7 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
             st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
     }
 
-    // Per wave: popcounts for ranking, and the value at its last set bit.
+    // Per wave: popcounts for ranking.
     {
         uint32_t words[kLaneWords];
         uint32_t lane_pop = 0;
@@ -344,39 +327,15 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
             run += __builtin_popcount(words[i]);
         }
         if (lane == kWave - 1) s_wave_pop[w] = pop_incl;
-        // Highest set bit of the wave's range (wave-local position).
-        const uint64_t m = ballot(lane_pop != 0u);
-        if (m != 0ull) {
-            const int L = 63 - __builtin_clzll(m);
-            int top = -1;
-#pragma unroll
-            for (int i = 0; i < kLaneWords; ++i)
-                if (words[i]) top = (lane * kLaneWords + i) * 32 + 31 - __builtin_clz(words[i]);
-            const int qq = __builtin_amdgcn_readlane(top, L);
-            if ((qq % (kWave * 4)) / 4 == lane) {
-                const int jq = qq / (kWave * 4), cq = qq % 4;
-#pragma unroll
-                for (int j = 0; j < STEPS; ++j)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        if (j == jq && c == cq) s_wave_last[w] = x[j][c];
-            }
-        }
     }
     __syncthreads();
 
-    // The last set bit before this wave's range, and this wave's rank base.
-    uint32_t in_has = 0, in_val = 0, rank_base = 0, marks = 0;
+    // This wave's rank base.
+    uint32_t rank_base = 0, marks = 0;
 #pragma unroll
     for (int k = 0; k < WAVES; ++k) {
         const uint32_t pk = s_wave_pop[k];
-        if (k < w) {
-            rank_base += pk;
-            if (pk) {
-                in_has = 1u;
-                in_val = s_wave_last[k];
-            }
-        }
+        if (k < w) rank_base += pk;
         marks += pk;
     }
 
@@ -384,42 +343,28 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
     if (tile == 0)
         for (uint64_t k = 1 + threadIdx.x; k < k_lo && k <= p.segments; k += kThreads) p.out[k - 1] = 0u;
 
+    // Marked positions are segment ends, so the tile-local prefix at a
+    // segment's start is the value at the previous mark: a segment's sum is
+    // the difference of two consecutive ranks (mod 2^32).  Round r holds
+    // ranks [r*kSlots - 1, (r+1)*kSlots - 1) in slots 0..kSlots.
     const uint32_t rounds = marks == 0 ? 1u : (marks + kSlots - 1) / kSlots;
     for (uint32_t round = 0; round < rounds; ++round) {
         const uint32_t r0 = round * kSlots;
-        // Segment values of this wave's set bits whose rank is in the round.
-        uint32_t sc_has = in_has, sc_val = in_val; // last set bit before the step
 #pragma unroll
         for (int j = 0; j < STEPS; ++j) {
             const int word = w * kWaveWords + j * (kWave * 4 / 32) + (lane >> 3);
             const uint32_t mw = s_mask[word];
             const int sh = (lane & 7) * 4;
             const uint32_t nib = (mw >> sh) & 0xFu;
-            // This lane's last set bit in the step, scanned across lanes.
-            uint32_t lh = nib != 0u;
-            uint32_t lv = (nib & 8u) ? x[j][3] : (nib & 4u) ? x[j][2] : (nib & 2u) ? x[j][1] : x[j][0];
-            wave_last_scan(lh, lv);
-            uint32_t eh = dpp_move<kDppWaveShr1>(0u, lh), ev = dpp_move<kDppWaveShr1>(0u, lv);
-            if (!eh) {
-                eh = sc_has;
-                ev = sc_val;
-            }
             if (nib) {
                 const uint32_t rb = rank_base + s_wrank[word];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     if (nib & (1u << c)) {
-                        const uint32_t rank = rb + __builtin_popcount(mw & ((1u << (sh + c)) - 1u));
-                        if (rank >= r0 && rank - r0 < (uint32_t)kSlots) s_val[rank - r0] = x[j][c] - (eh ? ev : 0u);
-                        eh = 1u;
-                        ev = x[j][c];
+                        const uint32_t slot = rb + __builtin_popcount(mw & ((1u << (sh + c)) - 1u)) + 1u - r0;
+                        if (slot <= (uint32_t)kSlots) s_val[slot] = x[j][c];
                     }
                 }
-            }
-            const uint32_t th = read_lane(lh, kWave - 1), tv = read_lane(lv, kWave - 1);
-            if (th) {
-                sc_has = 1u;
-                sc_val = tv;
             }
         }
         __syncthreads();
@@ -439,10 +384,12 @@ __global__ __launch_bounds__(WAVES * kWave) void segmented_sum_kernel(SegParams 
             uint32_t rank = s_wrank[q >> 5] + __builtin_popcount(s_mask[q >> 5] & ((1u << (q & 31)) - 1u));
             for (int k2 = 0; k2 < qw; ++k2) rank += s_wave_pop[k2];
             if (rank < r0 || rank - r0 >= (uint32_t)kSlots) continue;
+            uint32_t v = s_val[rank - r0 + 1];
+            if (a > t0) v -= s_val[rank - r0]; // prefix at a - 1, the previous mark
             if (a < t0)
-                s_open = s_val[rank - r0]; // written after the look-back
+                s_open = v; // written after the look-back
             else
-                p.out[k - 1] = s_val[rank - r0];
+                p.out[k - 1] = v;
         }
         if (round + 1 < rounds) __syncthreads();
     }
