@@ -328,6 +328,95 @@ def cpu_baseline(dev, scan, seconds: float) -> dict:
     }
 
 
+def _cpu_rate(run, bytes_per_pass: float, seconds: float = 2.0, max_reps: int = 20):
+    """(GB/s, passes, ms per pass) of `run()` repeated for about `seconds`."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            break
+    per = el / reps
+    return bytes_per_pass / per / 1e9, reps, per * 1e3
+
+
+def cpu_secondary(name: str, seconds: float) -> dict | None:
+    """The oracle (one host core, kind "port") on a bounded host-generated
+    sample of a secondary workload; rates are per algorithmic byte like the
+    GPU figure.  None for workloads the oracle has no function for."""
+    from oracle import oracle
+
+    def line(gbs, reps, ms, sample):
+        return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{sample}; {reps} passes, {ms:.1f} ms per pass"}
+
+    if name == "sum_f32":
+        n = 1 << 26
+        x = oracle.uniform_real(n, 1, -1.0, 1.0)
+        r = _cpu_rate(lambda: oracle.full_sum(x), 4.0 * n, seconds)
+        return line(*r, "2^26 f32 (a quarter of the GPU input), oracle full_sum (f64 accumulation)")
+    if name == "rows_f32":
+        rows, cols = 4096, 4096
+        x = oracle.normal(rows * cols, 3)
+        r = _cpu_rate(lambda: oracle.rows(x, rows, cols, prologue=(0.5, 0.25)), 4.0 * rows * cols + 12.0 * rows,
+                      seconds)
+        return line(*r, "4096 x 4096 f32 (1/16 of the GPU rows), oracle rows (sum, max, argmax of fmaf(.5,x,.25))")
+    if name == "segmented_i32":
+        n = 1 << 25
+        x = oracle.uniform_int(n, 4, -1000, 1000, dtype=np.int32)
+        off = oracle.geometric_offsets(n, 300.0, seed=5)
+        s = off.size - 1
+        r = _cpu_rate(lambda: oracle.segmented_sum(x, off), 4.0 * n + 8.0 * s + 4, seconds)
+        return line(*r, f"2^25 i32 values, {s} geometric(300) segments, oracle segmented_sum")
+    if name == "scan_f32_2_30":
+        n = 1 << 23
+        x = oracle.uniform_real(n, 6, 0.0, 1.0)
+        r = _cpu_rate(lambda: oracle.scan_sum(x), 8.0 * n, seconds)
+        return line(*r, "2^23 f32 (1/128 of the GPU input), oracle scan_sum (compensated f64 prefix and |prefix|)")
+    if name == "dot_f32":
+        n = 1 << 26
+        a, b = oracle.uniform_real(n, 1, -1.0, 1.0), oracle.uniform_real(n, 2, -1.0, 1.0)
+        r = _cpu_rate(lambda: oracle.dot(a, b), 8.0 * n, seconds)
+        return line(*r, "2^26 f32 pairs, oracle dot (exact products, f64 accumulation)")
+    if name == "axpy_f32":
+        n = 1 << 24
+        a, b = oracle.uniform_real(n, 1, -1.0, 1.0), oracle.uniform_real(n, 2, -1.0, 1.0)
+        r = _cpu_rate(lambda: oracle.fma_arrays(a, b, 0.5), 12.0 * n, seconds)
+        return line(*r, "2^24 f32, oracle fma_arrays (libm fmaf per element)")
+    return None
+
+
+def device_record(dev) -> dict:
+    """CU count and architecture from the library; current and peak clocks
+    from amd-smi when the tool answers within a few seconds."""
+    import shutil
+    import subprocess
+
+    topo = dev.topology()
+    rec = {"name": topo.name, "arch": topo.arch, "compute_units": topo.compute_units}
+    tool = shutil.which("amd-smi")
+    if tool:
+        try:
+            r = subprocess.run([tool, "metric", "--clock", "--json"], capture_output=True, text=True, timeout=15)
+            if r.returncode == 0:
+                data = json.loads(r.stdout)
+                if isinstance(data, dict):
+                    data = data.get("gpu_data", [data])
+                clock = data[0].get("clock", {}) if data else {}
+                picked = {}
+                for key in ("gfx_0", "mem_0"):
+                    c = clock.get(key)
+                    if isinstance(c, dict):
+                        picked[key] = {k: (c[k] or {}).get("value") for k in ("clk", "max_clk")
+                                       if isinstance(c.get(k), dict)}
+                # sampled after the timed runs, so "clk" is usually the idle clock
+                rec["clocks_mhz"] = picked or None
+        except (OSError, ValueError, AttributeError, TypeError, IndexError, subprocess.SubprocessError):
+            rec["clocks_mhz"] = None
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -402,9 +491,15 @@ def main() -> int:
             line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
                                        "elements_per_s": round(r["n"] / (r["ms"] * 1e-3), 1),
                                        "roofline": roofline(r["bytes"], r["ms"], name)}
+            if not args.no_cpu_baseline:
+                cb = cpu_secondary(name, 2.0)
+                if cb is not None:
+                    line["secondary"][name]["cpu_baseline"] = cb
             log(f"{name}: {r['ms']:.4f} ms/launch {gbs:.1f} GB/s")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dev, scan, args.cpu_seconds)
+        line["secondary"]["f32_sum_reduce_2_28"]["cpu_baseline"] = cpu_secondary("sum_f32", 2.0)
+    line["device"] = device_record(dev)
     print(json.dumps(line))
     return 0
 
