@@ -328,6 +328,91 @@ def cpu_baseline(dev, scan, seconds: float) -> dict:
     }
 
 
+def _raw(fn_name: str, *args):
+    """A closure calling one C-ABI entry point with prebuilt ctypes arguments,
+    so that per-call host cost is one ctypes dispatch, as close as Python gets
+    to the reference's direct Rust calls."""
+    from hephaestus_amd import _ffi
+
+    fn = getattr(_ffi.lib(), fn_name)
+
+    def call():
+        status = fn(*args)
+        if status != 0:
+            _ffi.check(status)
+    return call
+
+
+def latency_suite(hx, dev, args) -> dict:
+    """The reference's only published timings for this path are small
+    problems on its WGPU backend (RTX 5080, Windows 11; benchmark_results.md:
+    151-158, harness crates/hephaestus-wgpu/benches/comparative.rs: 50
+    back-to-back calls, one device poll, wall time / 50).  The same shapes,
+    timed the same way on this path (`us_per_call`), plus the HIP-event time
+    per launch on the device stream (`gpu_us_per_launch`).  Different
+    hardware and backend: a reference point, not `vs_baseline`."""
+    import ctypes
+
+    from hephaestus_amd import Layout, _ffi
+    from hephaestus_amd.device import hx_dtype
+
+    def lay(layout):
+        return ctypes.byref(_ffi.layout_struct(layout))
+
+    def wall_us(call, iters=50, warm=5) -> float:
+        for _ in range(warm):
+            call()
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            call()
+        dev.synchronize()
+        return (time.perf_counter() - t0) / iters * 1e6
+
+    out = {}
+
+    def record(name, call, ref_us, source):
+        out[name] = {"us_per_call": round(wall_us(call), 2),
+                     "gpu_us_per_launch": round(time_plan(dev, call, 200, 20) * 1e3, 2),
+                     "reference_wgpu_rtx5080_us": ref_us, "reference_source": source}
+
+    n = 1 << 20
+    xs = dev.upload((np.arange(n) % 17).astype(np.uint32))
+    o1 = dev.alloc_zeroed(np.uint32, 1)
+    plan = hx.RocmFullReductionOps().prepare_reduce_full(
+        dev, hx.SumOp, hx.StridedView(xs, Layout.c_contiguous([n])), hx.StridedView(o1, Layout.c_contiguous([1])))
+    record("sum_u32_2_20_prepared", _raw("hx_plan_dispatch", plan.handle, None), 42.70, "benchmark_results.md:151")
+
+    m = 256
+    a = dev.upload(np.arange(m * m, dtype=np.float32) / 1000.0)
+    row = dev.alloc_zeroed(np.float32, m)
+    li, lo = Layout.c_contiguous([m, m]), Layout.c_contiguous([1, m])
+    ops = {"sum": (hx.SumOp, 22.14, 152), "min": (hx.MinOp, 20.73, 153), "max": (hx.MaxOp, 11.78, 154),
+           "mean": (hx.MeanOp, 18.05, 155)}
+    plans = []  # the reference rows are "axis-0 tiled prepared": prepared plans here too
+    for name, (op, ref, line) in ops.items():
+        plans.append(hx.RocmAxisReductionOps().prepare_reduce_axis_into(
+            dev, op, hx.StridedView(a, li), 0, hx.StridedView(row, lo)))
+        record(f"axis0_{name}_256x256", _raw("hx_plan_dispatch", plans[-1].handle, None), ref,
+               f"benchmark_results.md:{line}")
+    full = dev.alloc_zeroed(np.float32, m * m)
+    record("cumsum_axis1_256x256", _raw("hx_scan", dev.handle, hx.CumSumOp.code, hx_dtype(np.float32),
+                                        _ffi.SCAN_INCLUSIVE, _ffi.SCAN_FORWARD, a.ptr, m * m, lay(li), 1,
+                                        full.ptr, m * m, lay(li), None),
+           46.53, "benchmark_results.md:158")
+    k = 65536
+    u, v = dev.upload(np.ones(k, np.float32)), dev.upload(np.full(k, 0.5, np.float32))
+    o2 = dev.alloc_zeroed(np.float32, 1)
+    lk = Layout.c_contiguous([k])
+    record("dot_f32_65536", _raw("hx_map_reduce", dev.handle, _ffi.MAP_DOT, hx_dtype(np.float32), u.ptr, k, lay(lk),
+                                 v.ptr, k, lay(lk), o2.ptr, 1, None),
+           97.42, "benchmark_results.md:161")
+    record("trace_f32_256x256", _raw("hx_trace", dev.handle, hx_dtype(np.float32), a.ptr, m * m, lay(li), o2.ptr, 1,
+                                     None),
+           42.72, "benchmark_results.md:162")
+    return out
+
+
 def _cpu_rate(run, bytes_per_pass: float, seconds: float = 2.0, max_reps: int = 20):
     """(GB/s, passes, ms per pass) of `run()` repeated for about `seconds`."""
     reps, t0 = 0, time.perf_counter()
@@ -496,6 +581,11 @@ def main() -> int:
                 if cb is not None:
                     line["secondary"][name]["cpu_baseline"] = cb
             log(f"{name}: {r['ms']:.4f} ms/launch {gbs:.1f} GB/s")
+    if args.workload == "all":
+        line["latency"] = latency_suite(hx, dev, args)
+        for name, r in line["latency"].items():
+            log(f"{name}: {r['us_per_call']} us per call, {r['gpu_us_per_launch']} us per launch "
+                f"(reference WGPU RTX 5080: {r['reference_wgpu_rtx5080_us']} us)")
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dev, scan, args.cpu_seconds)
         line["secondary"]["f32_sum_reduce_2_28"]["cpu_baseline"] = cpu_secondary("sum_f32", 2.0)
