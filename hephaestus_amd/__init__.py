@@ -51,6 +51,7 @@ from .ops import (
     plan_axis_reduction,
     plan_axis_scan,
     reduction_pass_count,
+    submit_prepared_axis_reduction_batch,
     submit_prepared_reduction_batch,
     validate_reduction_width,
 )

@@ -278,6 +278,12 @@ inline void submit_prepared_reduction_batch(std::initializer_list<const Prepared
     for (const PreparedPlan *p : plans) handles.push_back(p->handle());
     check(hx_plan_dispatch_batch(handles.data(), handles.size(), stream));
 }
+// submit_prepared_axis_reduction_batch (rocm application/
+// prepared_axis_reduction.rs:84-92): the same for prepared axis reductions.
+inline void submit_prepared_axis_reduction_batch(RocmDevice &, std::initializer_list<const PreparedPlan *> plans,
+                                                 hx_stream stream = nullptr) {
+    submit_prepared_reduction_batch(plans, stream);
+}
 
 namespace detail {
 inline const hx_affine *affine(const Affine *p, hx_affine &storage) {

@@ -114,6 +114,16 @@ def submit_prepared_reduction_batch(plans) -> None:
     _ffi.check(_ffi.lib().hx_plan_dispatch_batch(arr, len(plans), None))
 
 
+def submit_prepared_axis_reduction_batch(device: RocmDevice, plans) -> None:
+    """Prepared axis reductions dispatched in order on the device stream
+    (rocm application/prepared_axis_reduction.rs:84-92)."""
+    plans = list(plans)
+    for p in plans:
+        if p.device is not device:
+            raise errors.DispatchFailed("prepared axis reduction belongs to a different device")
+    submit_prepared_reduction_batch(plans)
+
+
 class RocmFullReductionOps:
     """FullReductionOps<RocmDevice, T> (rocm full_reduction_seam.rs:28-120)."""
 

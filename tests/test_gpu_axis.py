@@ -263,3 +263,23 @@ def test_prepared_column_scan_rebinds(device, oracle):
     plan.dispatch()
     want = np.cumsum(y.reshape(r, c), axis=0, dtype=np.uint32) - y.reshape(r, c)
     assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+
+
+def test_prepared_axis_reduction_batch(device, oracle):
+    """submit_prepared_axis_reduction_batch (prepared_axis_reduction.rs:84-92):
+    eight prepared axis-0 sums of one input, as the reference's comparative
+    bench batches them, then a rebind."""
+    r, c = 4096, 256
+    x = oracle.uniform_int(r * c, seed=9, lo=0, hi=1000)
+    buf = device.upload(x)
+    outs = [device.alloc_zeroed(np.uint32, c) for _ in range(8)]
+    plans = [AXIS.prepare_reduce_axis_into(device, hx.SumOp, StridedView(buf, Layout.c_contiguous([r, c])), 0,
+                                           StridedView(o, Layout.c_contiguous([1, c]))) for o in outs]
+    hx.submit_prepared_axis_reduction_batch(device, plans)
+    want = x.reshape(r, c).sum(axis=0, dtype=np.uint32)
+    for o in outs:
+        assert np.array_equal(device.download_owned(o), want)
+    y = oracle.uniform_int(r * c, seed=10, lo=0, hi=1000)
+    device.write_buffer(buf, y)
+    hx.submit_prepared_axis_reduction_batch(device, plans)
+    assert np.array_equal(device.download_owned(outs[-1]), y.reshape(r, c).sum(axis=0, dtype=np.uint32))

@@ -128,3 +128,43 @@ def test_f32_inclusive_scan_2_30(device, oracle):
     note(f"f32 scan worst |err|/(eps*sum|x|) = {worst:.3f} (bound {2 * 30})")
     assert bad == 0, worst
     assert np.all(np.diff(got[:: 1 << 16]) >= 0)  # monotone for non-negative inputs
+
+
+def test_f32_column_sum_65536x4096(device, oracle):
+    """The column-tile path at the bench shape: axis-0 sum of 65536 x 4096
+    N(0,1) f32, every column against the oracle's f64 fold of that column,
+    and bitwise equal on a second dispatch (fixed fold order)."""
+    r, c = 65536, 4096
+    note("f32 axis-0 sum 65536x4096")
+    x = device.alloc_uninitialized(np.float32, r * c)
+    device.fill_normal(x, seed=7)
+    out = device.alloc_zeroed(np.float32, c)
+    plan = AXIS.prepare_reduce_axis_into(device, hx.SumOp, StridedView(x, Layout.c_contiguous([r, c])), 0,
+                                         StridedView(out, Layout.c_contiguous([1, c])))
+    plan.dispatch()
+    first = device.download_owned(out)
+    plan.dispatch()
+    assert np.array_equal(first.view(np.uint32), device.download_owned(out).view(np.uint32))
+    cols = np.ascontiguousarray(device.download_owned(x).reshape(r, c).T)
+    for j in range(c):
+        ref, ab = oracle.full_sum(cols[j])
+        assert abs(float(first[j]) - ref) <= bound(r, ab), j
+
+
+def test_u32_column_scan_65536x4096(device, oracle):
+    """The chunked column scan at the bench shape, inclusive and exclusive:
+    every element bit-exact against the wrapped cumulative sum of its
+    column."""
+    r, c = 65536, 4096
+    note("u32 axis-0 scan 65536x4096")
+    x = device.alloc_uninitialized(np.uint32, r * c)
+    device.fill_uniform_int(x, seed=8, lo=0, hi=255)
+    out = device.alloc_uninitialized(np.uint32, r * c)
+    lay = Layout.c_contiguous([r, c])
+    host = device.download_owned(x).reshape(r, c)
+    want = np.cumsum(host, axis=0, dtype=np.uint32)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward, StridedView(out, lay))
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive)
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want - host)
