@@ -174,8 +174,9 @@ struct ScanArgs {
     uint64_t out_offset;
 };
 uint64_t scan_workspace_bytes(const ScanArgs &args);
-// False for column scans, whose workspace holds chunk totals instead of
-// look-back status words (immediate calls take it from device scratch).
+// False for chunked column scans, whose workspace holds chunk totals
+// instead of look-back status words (immediate calls take it from device
+// scratch); true for every other scan.
 bool scan_uses_lookback(const ScanArgs &args);
 hx_status launch_scan(const ScanArgs &args, void *ws, uint64_t ws_bytes,
                       LookbackState &st, hipStream_t stream);

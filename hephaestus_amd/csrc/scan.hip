@@ -482,10 +482,12 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
 }
 
 // Column scans: many strided lines whose starts are adjacent in memory
-// (axis-0 scan of a row-major matrix).  Lanes run across lines -- a wave owns
-// 64*V adjacent lines, V = 4 giving every lane one 16-byte load per step --
-// and the scan axis is cut into chunks so that thousands of waves share the
-// work however tall the matrix is:
+// (axis-0 scan of a row-major matrix).  From 256 lines up they take the
+// single-pass col_lookback_kernel below; narrower matrices take this chunked
+// reduce-then-scan.  Lanes run across lines -- a wave owns 64*V adjacent
+// lines, V = 4 giving every lane one 16-byte load per step -- and the scan
+// axis is cut into chunks so that thousands of waves share the work however
+// tall the matrix is:
 //   col_totals_kernel  chunk totals of every line (one read of the input);
 //   col_carry_kernel   per line, an exclusive scan of its chunk totals in
 //                      place (chunks x lines words, a thread per line);
@@ -657,6 +659,239 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     }
 }
 
+// Single-pass column scan.  A block of kColWaves waves owns a tile of
+// kColTileRows scan steps x 64*V adjacent lines: wave w holds kColRows steps
+// of the tile in registers (lane l: lines 64*V*g + V*l .. +V-1), scans them
+// per line, and the wave totals are combined through LDS.  Wave 0 then runs a
+// decoupled look-back per line: lane l polls the statuses of its V lines in
+// the tile of the same line group one chunk earlier, folds aggregates until
+// it meets an inclusive prefix, and publishes its own.  Status entry of
+// (chunk c, line j) is c * lpad + j.  Every element is read once and written
+// once.  A predecessor that stays unpublished for kSpinLimit polls has its
+// aggregate rebuilt from the input by the waiter with the owner's arithmetic
+// (f32: per-wave f32 prefix from the identity, then f64 over the waves in
+// order), so progress never depends on dispatch order.
+constexpr int kColWaves = 8;
+constexpr int kColRows = 16;
+constexpr uint64_t kColTileRows = (uint64_t)kColWaves * kColRows;
+
+template <typename T, int V>
+__device__ __forceinline__ void col_load_t(const T *p, T (&x)[V]) {
+    if constexpr (V == 4) {
+        using Vt = typename Vec4<T>::type;
+        const Vt v = __builtin_nontemporal_load((const Vt *)p);
+        x[0] = (T)v.x;
+        x[1] = (T)v.y;
+        x[2] = (T)v.z;
+        x[3] = (T)v.w;
+    } else {
+        x[0] = __builtin_nontemporal_load(p);
+    }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void col_store_t(T *p, const T (&y)[V]) {
+    if constexpr (V == 4) {
+        using Vt = typename Vec4<T>::type;
+        Vt v;
+        v.x = y[0];
+        v.y = y[1];
+        v.z = y[2];
+        v.w = y[3];
+        __builtin_nontemporal_store(v, (Vt *)p);
+    } else {
+        __builtin_nontemporal_store(y[0], p);
+    }
+}
+
+// Aggregate of chunk c for the V lines starting at line0, exactly as the
+// owner computes it (the decoupled fallback).
+template <typename T, typename Op, int V, bool REV>
+__device__ void col_tile_aggregate(const ScanParams &p, uint64_t c, uint64_t line0,
+                                   typename ColAcc<T>::type (&agg)[V]) {
+    using A = typename ColAcc<T>::type;
+    const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)line0 * p.in_line_stride);
+#pragma unroll
+    for (int v = 0; v < V; ++v) agg[v] = Op::template identity<A>();
+    // Rolled loops: this rare path must not add register pressure to the
+    // kernel, whose tile stays live in registers across the look-back.
+#pragma unroll 1
+    for (int q = 0; q < kColWaves; ++q) {
+        T run[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) run[v] = Op::template identity<T>();
+#pragma unroll 1
+        for (int r = 0; r < kColRows; ++r) {
+            const uint64_t i = c * kColTileRows + (uint64_t)q * kColRows + r;
+            if (i >= p.len) break;
+            const uint64_t li = REV ? p.len - 1 - i : i;
+            T x[V];
+            col_load_t<T, V>(in + (int64_t)li * p.in_elem_stride, x);
+#pragma unroll
+            for (int v = 0; v < V; ++v) run[v] = Op::combine(run[v], x[v]);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) agg[v] = Op::combine(agg[v], (A)run[v]);
+    }
+}
+
+// Addressing of a line group: a wave-uniform element base (the group's
+// lowest address on every step) and one 32-bit byte offset per lane, so each
+// access is a scalar base plus a vector offset and no per-step 64-bit address
+// stays live across the look-back.
+struct ColGroupAddr {
+    int64_t base;      // element offset of the group's lowest line, step 0
+    uint32_t lane_off; // bytes from there to this lane's first line
+};
+
+template <int V, typename T>
+__device__ __forceinline__ ColGroupAddr col_group_addr(uint64_t g, int lane, int64_t line_stride, uint64_t offset) {
+    constexpr int64_t kGroup = (int64_t)kWave * V;
+    ColGroupAddr a;
+    if (line_stride > 0) {
+        a.base = (int64_t)offset + (int64_t)g * kGroup;
+        a.lane_off = (uint32_t)(lane * V) * (uint32_t)sizeof(T);
+    } else { // -1: lines run downwards in memory (one line per lane)
+        a.base = (int64_t)offset - ((int64_t)g * kGroup + kGroup - 1);
+        a.lane_off = (uint32_t)(kGroup - 1 - lane * V) * (uint32_t)sizeof(T);
+    }
+    return a;
+}
+
+template <typename T, typename Op, typename Status, int V, bool EXCL, bool REV>
+__global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanParams p, Status st, uint64_t groups,
+                                                                        uint64_t lpad) {
+    using A = typename ColAcc<T>::type;
+    constexpr int kLines = kWave * V;
+    __shared__ A s_agg[kColWaves][kLines];
+    __shared__ A s_carry[kLines];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = lane_id();
+    const uint64_t tile = blockIdx.x;
+    const uint64_t g = tile % groups, c = tile / groups;
+    const uint64_t line0 = (g * kWave + (uint64_t)lane) * V;
+    const bool active = line0 < p.lines;
+    const uint64_t i0 = c * kColTileRows + (uint64_t)w * kColRows;
+    const ColGroupAddr ia = col_group_addr<V, T>(g, lane, p.in_line_stride, p.in_offset);
+    const ColGroupAddr oa = col_group_addr<V, T>(g, lane, p.out_line_stride, p.out_offset);
+    const T tid = Op::template identity<T>();
+    const A aid = Op::template identity<A>();
+
+    // The wave's steps, scanned per line from the identity.
+    T x[kColRows][V];
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        const uint64_t i = i0 + r;
+        if (active && i < p.len) {
+            const int64_t li = (int64_t)(REV ? p.len - 1 - i : i);
+            const char *row = (const char *)((const T *)p.in + (ia.base + li * p.in_elem_stride));
+            col_load_t<T, V>((const T *)(row + ia.lane_off), x[r]);
+        } else {
+#pragma unroll
+            for (int v = 0; v < V; ++v) x[r][v] = tid;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r)
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[r][v] = Op::combine(r == 0 ? tid : x[r - 1][v], x[r][v]);
+#pragma unroll
+    for (int v = 0; v < V; ++v) s_agg[w][lane * V + v] = (A)x[kColRows - 1][v];
+    __syncthreads();
+
+    if (w == 0) {
+        A agg[V], excl[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            agg[v] = aid;
+            for (int q = 0; q < kColWaves; ++q) agg[v] = Op::combine(agg[v], s_agg[q][lane * V + v]);
+            excl[v] = aid;
+        }
+        if (active) {
+            const uint64_t e = c * lpad + line0;
+            if (c == 0) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, agg[v]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kAggregate, agg[v]);
+                bool done[V];
+#pragma unroll
+                for (int v = 0; v < V; ++v) done[v] = false;
+                uint64_t pred = c - 1;
+                for (;;) {
+                    uint32_t flag[V];
+                    A val[V];
+                    uint32_t spins = 0;
+                    for (;;) {
+                        bool all = true;
+#pragma unroll
+                        for (int v = 0; v < V; ++v) {
+                            flag[v] = kPrefix;
+                            val[v] = aid;
+                            if (!done[v]) {
+                                st.read(pred * lpad + line0 + v, p.tag, flag[v], val[v]);
+                                all = all && flag[v] != kInvalid;
+                            }
+                        }
+                        if (all) break;
+                        if (++spins >= kSpinLimit) {
+                            A fb[V];
+                            col_tile_aggregate<T, Op, V, REV>(p, pred, line0, fb);
+#pragma unroll
+                            for (int v = 0; v < V; ++v)
+                                if (!done[v] && flag[v] == kInvalid)
+                                    st.publish_if_unset(pred * lpad + line0 + v, p.tag, kAggregate, fb[v]);
+                            spins = 0;
+                            continue;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    bool all_done = true;
+#pragma unroll
+                    for (int v = 0; v < V; ++v) {
+                        if (done[v]) continue;
+                        excl[v] = Op::combine(val[v], excl[v]);
+                        if (flag[v] == kPrefix) done[v] = true;
+                        else all_done = false;
+                    }
+                    if (all_done || pred == 0) break; // chunk 0 publishes prefixes only
+                    --pred;
+                }
+#pragma unroll
+                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, Op::combine(excl[v], agg[v]));
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) s_carry[lane * V + v] = excl[v];
+    }
+    __syncthreads();
+    if (!active) return;
+
+    A carry[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        carry[v] = s_carry[lane * V + v];
+        for (int q = 0; q < w; ++q) carry[v] = Op::combine(carry[v], s_agg[q][lane * V + v]);
+    }
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        const uint64_t i = i0 + r;
+        if (i >= p.len) break;
+        T y[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            if constexpr (EXCL)
+                y[v] = r == 0 ? finalize<T, A, Op>(carry[v], tid) : finalize<T, A, Op>(carry[v], x[r - 1][v]);
+            else
+                y[v] = finalize<T, A, Op>(carry[v], x[r][v]);
+        }
+        const int64_t li = (int64_t)(REV ? p.len - 1 - i : i);
+        char *row = (char *)((T *)p.out + (oa.base + li * p.out_elem_stride));
+        col_store_t<T, V>((T *)(row + oa.lane_off), y);
+    }
+}
+
 // 16 waves per CU: on a 65536 x 4096 u32 column scan 4096 waves of 256 steps
 // took 164 + 12 + 386 us (totals, carry, rescan); 8192 waves 202 + 23 + 512.
 constexpr uint64_t kColTargetWaves = 4096;
@@ -693,6 +928,29 @@ ColShape column_shape(const ScanArgs &a) {
     return s;
 }
 
+// Single-pass column scans (col_lookback_kernel): line groups, padded line
+// count of the status array, chunks of kColTileRows steps.
+struct ColLbShape {
+    int V = 1;
+    uint64_t groups = 0, lpad = 0, chunks = 0;
+};
+
+ColLbShape col_lb_shape(const ScanArgs &a) {
+    ColLbShape s;
+    s.V = column_shape(a).V;
+    s.groups = ceil_div(a.lines, (uint64_t)kWave * s.V);
+    s.lpad = s.groups * kWave * s.V;
+    s.chunks = ceil_div(a.len, kColTileRows);
+    return s;
+}
+
+// The single pass needs whole line groups: with fewer than 256 lines every
+// tile leaves lanes idle and all tiles form one long look-back chain
+// (measured, u32: 4194304 x 64 1.63 ms single-pass against 0.75 ms chunked;
+// 1048576 x 256 0.50 against 0.71; 65536 x 4096 0.42 against 0.55).
+constexpr uint64_t kSinglePassMinLines = 256;
+bool column_single_pass(const ScanArgs &a) { return column_mode(a) && a.lines >= kSinglePassMinLines; }
+
 uint64_t column_bytes(const ScanArgs &a) {
     const ColShape s = column_shape(a);
     if (s.nchunks <= 1 || a.lines == 0) return 0;
@@ -722,6 +980,37 @@ hx_status launch_column_v(const ScanParams &p, const ColShape &s, void *ws, hipS
     return check_launch("col_scan_kernel");
 }
 
+template <typename T, typename Op, typename Status, int V, bool EXCL, bool REV>
+hx_status launch_col_lookback_v(const ScanParams &p, const ColLbShape &s, const Status &st, hipStream_t stream) {
+    hipLaunchKernelGGL((col_lookback_kernel<T, Op, Status, V, EXCL, REV>), dim3((uint32_t)(s.groups * s.chunks)),
+                       dim3(kColWaves * kWave), 0, stream, p, st, s.groups, s.lpad);
+    return check_launch("col_lookback_kernel");
+}
+
+template <typename T, typename Op, typename Status, int V>
+hx_status launch_col_lookback_s(const ScanParams &p, const ColLbShape &s, const Status &st, bool excl, bool rev,
+                                hipStream_t stream) {
+    if (excl)
+        return rev ? launch_col_lookback_v<T, Op, Status, V, true, true>(p, s, st, stream)
+                   : launch_col_lookback_v<T, Op, Status, V, true, false>(p, s, st, stream);
+    return rev ? launch_col_lookback_v<T, Op, Status, V, false, true>(p, s, st, stream)
+               : launch_col_lookback_v<T, Op, Status, V, false, false>(p, s, st, stream);
+}
+
+template <typename T, typename Op>
+hx_status launch_col_lookback(const ScanParams &p, const ColLbShape &s, bool excl, bool rev, void *status,
+                              hipStream_t stream) {
+    if constexpr (std::is_same<T, float>::value) {
+        const F64Status st{(uint64_t *)status};
+        return s.V == 4 ? launch_col_lookback_s<T, Op, F64Status, 4>(p, s, st, excl, rev, stream)
+                        : launch_col_lookback_s<T, Op, F64Status, 1>(p, s, st, excl, rev, stream);
+    } else {
+        const PackedStatus st{(uint64_t *)status};
+        return s.V == 4 ? launch_col_lookback_s<T, Op, PackedStatus, 4>(p, s, st, excl, rev, stream)
+                        : launch_col_lookback_s<T, Op, PackedStatus, 1>(p, s, st, excl, rev, stream);
+    }
+}
+
 template <typename T, typename Op, bool EXCL>
 hx_status launch_column(const ScanParams &p, const ColShape &s, bool rev, void *ws, hipStream_t stream) {
     if (s.V == 4)
@@ -749,6 +1038,10 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
 }
 
 uint64_t scan_bytes(const ScanArgs &a) {
+    if (column_mode(a) && column_single_pass(a)) {
+        const ColLbShape c = col_lb_shape(a);
+        return kLookbackOffset + status_bytes(c.chunks * c.lpad, a.dtype == HX_DTYPE_F32);
+    }
     if (column_mode(a)) return column_bytes(a);
     const uint64_t tpl = ceil_div(a.len, kTile);
     const bool f64 = a.dtype == HX_DTYPE_F32;
@@ -773,6 +1066,18 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out_offset = a.out_offset;
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
+    if (column_mode(a) && column_single_pass(a)) {
+        const ColLbShape cs = col_lb_shape(a);
+        if (cs.groups * cs.chunks > 0x7FFFFFFFull)
+            return fail(HX_ERR_DISPATCH_FAILED, "column scan exceeds the grid range");
+        if (ws_bytes < scan_bytes(a))
+            return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small",
+                        (unsigned long long)ws_bytes);
+        HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
+        hx_status s = launch_col_lookback<T, Op>(p, cs, a.exclusive, a.reverse, (char *)ws + kLookbackOffset, stream);
+        if (s == HX_OK) commit_lookback_launch(lb);
+        return s;
+    }
     if (column_mode(a)) {
         const ColShape cs = column_shape(a);
         if (cs.nchunks > 1 && ws_bytes < column_bytes(a))
@@ -813,7 +1118,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
-bool scan_uses_lookback(const ScanArgs &a) { return !column_mode(a); }
+bool scan_uses_lookback(const ScanArgs &a) { return !column_mode(a) || column_single_pass(a); }
 
 hx_status launch_scan(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     const bool prod = a.op == HX_OP_PROD;

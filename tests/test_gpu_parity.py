@@ -340,6 +340,29 @@ def test_scan_directions_kinds_and_ops(device, oracle, kind, direction, op):
     assert np.array_equal(device.download_owned(out), want)
 
 
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+@pytest.mark.parametrize("n", [5, 4097, 100003])
+def test_scan_f32_products_within_gamma(device, oracle, n, direction, kind):
+    """f32 cumprod: no oracle function, so numpy's f64 product is the check,
+    within gamma_{n-1} = (n-1)u/(1-(n-1)u) relative (u = 2^-24), the bound for
+    a product of n f32 factors in any evaluation order."""
+    x = oracle.uniform_real(n, seed=n + 21, lo=0.999, hi=1.001)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.float32, n)
+    SCAN.scan_axis_into(device, hx.CumProdOp, StridedView(buf, Layout.c_contiguous([n])), 0, direction,
+                        StridedView(out, Layout.c_contiguous([n])), kind)
+    v = x.astype(np.float64)[::-1] if direction == hx.ScanDirection.Reverse else x.astype(np.float64)
+    want = np.cumprod(v)
+    if kind == hx.ScanKind.Exclusive:
+        want = np.concatenate([[1.0], want[:-1]])
+    if direction == hx.ScanDirection.Reverse:
+        want = want[::-1]
+    k = (n - 1) * 2.0**-24
+    got = device.download_owned(out).astype(np.float64)
+    assert np.all(np.abs(got - want) <= k / (1.0 - k) * np.abs(want))
+
+
 @pytest.mark.parametrize("shape,axis", [((512, 4096), 1), ((3, 10000), 1), ((4096, 300), 0), ((40, 7), 0),
                                         ((1000, 1001), 1), ((257, 5), 1)])
 def test_scan_rank2_lines(device, oracle, shape, axis):
