@@ -659,21 +659,31 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     }
 }
 
-// Single-pass column scan.  A block of kColWaves waves owns a tile of
-// kColTileRows scan steps x 64*V adjacent lines: wave w holds kColRows steps
-// of the tile in registers (lane l: lines 64*V*g + V*l .. +V-1), scans them
-// per line, and the wave totals are combined through LDS.  Wave 0 then runs a
-// decoupled look-back per line: lane l polls the statuses of its V lines in
-// the tile of the same line group one chunk earlier, folds aggregates until
-// it meets an inclusive prefix, and publishes its own.  Status entry of
+// Single-pass column scan.  A block owns a tile of kColTileRows scan steps x
+// 64*V adjacent lines.  Its kColDataWaves data waves each hold kColRows
+// steps of the tile in registers (lane l: lines 64*V*g + V*l .. +V-1), scan
+// them per line, and combine their totals through LDS.  The block's last
+// wave holds no data: it runs the decoupled look-back, lane l for its V
+// lines, polling kColPoll earlier chunks of the same line group per round
+// trip and folding aggregates until each line meets an inclusive prefix.
+// Integer scans only (packed one-word statuses); f32 column scans take the
+// chunked path, whose f64 accumulation runs along the whole line.
+// Data and look-back waves run separate code paths (wave-uniform), so the
+// tile's registers are not live during the look-back.  Status entry of
 // (chunk c, line j) is c * lpad + j.  Every element is read once and written
-// once.  A predecessor that stays unpublished for kSpinLimit polls has its
+// once.  A predecessor that stays unpublished for kSpinLimit rounds has its
 // aggregate rebuilt from the input by the waiter with the owner's arithmetic
 // (f32: per-wave f32 prefix from the identity, then f64 over the waves in
 // order), so progress never depends on dispatch order.
-constexpr int kColWaves = 8;
+constexpr int kColWaves = 16;
+constexpr int kColDataWaves = kColWaves - 1;
 constexpr int kColRows = 16;
-constexpr uint64_t kColTileRows = (uint64_t)kColWaves * kColRows;
+constexpr uint64_t kColTileRows = (uint64_t)kColDataWaves * kColRows;
+// Predecessor chunks polled per round trip.  Status reads are device-scope
+// and uncached, and wider polls cost more than the round trips they save
+// (u32, 65536 x 4096 / 1048576 x 256: 1 chunk 0.352 / 0.462 ms; 2: 0.354 /
+// 0.491; 4: 0.361 / 0.568; 8: 0.384 / 0.762).
+constexpr int kColPoll = 1;
 
 template <typename T, int V>
 __device__ __forceinline__ void col_load_t(const T *p, T (&x)[V]) {
@@ -716,7 +726,7 @@ __device__ void col_tile_aggregate(const ScanParams &p, uint64_t c, uint64_t lin
     // Rolled loops: this rare path must not add register pressure to the
     // kernel, whose tile stays live in registers across the look-back.
 #pragma unroll 1
-    for (int q = 0; q < kColWaves; ++q) {
+    for (int q = 0; q < kColDataWaves; ++q) {
         T run[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) run[v] = Op::template identity<T>();
@@ -758,12 +768,95 @@ __device__ __forceinline__ ColGroupAddr col_group_addr(uint64_t g, int lane, int
     return a;
 }
 
+// The look-back wave: publishes the tile's aggregate, folds its
+// predecessors' statuses per line (kColPoll chunks per round trip, consumed
+// in order and in step for all of the lane's lines, so no status is counted
+// twice), publishes the inclusive prefix and leaves the carry in s_carry.
+template <typename T, typename Op, typename Status, int V, bool REV>
+__device__ void col_lookback_wave(const ScanParams &p, const Status &st, uint64_t c, uint64_t lpad, uint64_t line0,
+                                  bool active, const typename ColAcc<T>::type (&agg)[V],
+                                  typename ColAcc<T>::type (&excl)[V]) {
+    using A = typename ColAcc<T>::type;
+    constexpr int P = kColPoll;
+    const A aid = Op::template identity<A>();
+#pragma unroll
+    for (int v = 0; v < V; ++v) excl[v] = aid;
+    if (!active) return;
+    const uint64_t e = c * lpad + line0;
+    if (c == 0) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, agg[v]);
+        return;
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kAggregate, agg[v]);
+    bool done[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) done[v] = false;
+    uint64_t pos = c - 1; // next predecessor to consume
+    uint32_t spins = 0;
+    for (;;) {
+        uint32_t flag[P][V];
+        A val[P][V];
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                flag[k][v] = kInvalid;
+                val[k][v] = aid;
+                if (!done[v] && (uint64_t)k <= pos) st.read((pos - k) * lpad + line0 + v, p.tag, flag[k][v], val[k][v]);
+            }
+        int used = 0;
+        bool finished = false;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            if (finished || used < k || (uint64_t)k > pos) break;
+            bool ready = true;
+#pragma unroll
+            for (int v = 0; v < V; ++v) ready = ready && (done[v] || flag[k][v] != kInvalid);
+            if (!ready) break;
+            // Chunk 0's aggregate is its inclusive prefix: a fallback may
+            // have published it as an aggregate, and consuming it still
+            // finishes the line.
+            const bool first_chunk = (uint64_t)k == pos;
+            bool all = true;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                if (done[v]) continue;
+                excl[v] = Op::combine(val[k][v], excl[v]);
+                if (flag[k][v] == kPrefix || first_chunk) done[v] = true;
+                else all = false;
+            }
+            used = k + 1;
+            finished = all;
+        }
+        if (finished) break;
+        if (used > 0) {
+            pos -= (uint64_t)used; // > 0 remains: consuming chunk 0 finishes every line
+            spins = 0;
+            continue;
+        }
+        if (++spins >= kSpinLimit) {
+            A fb[V];
+            col_tile_aggregate<T, Op, V, REV>(p, pos, line0, fb);
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                if (!done[v] && flag[0][v] == kInvalid) st.publish_if_unset(pos * lpad + line0 + v, p.tag, kAggregate, fb[v]);
+            spins = 0;
+            continue;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, Op::combine(excl[v], agg[v]));
+}
+
 template <typename T, typename Op, typename Status, int V, bool EXCL, bool REV>
 __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanParams p, Status st, uint64_t groups,
                                                                         uint64_t lpad) {
     using A = typename ColAcc<T>::type;
     constexpr int kLines = kWave * V;
-    __shared__ A s_agg[kColWaves][kLines];
+    __shared__ A s_agg[kColDataWaves][kLines];
     __shared__ A s_carry[kLines];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = lane_id();
@@ -771,11 +864,28 @@ __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanPara
     const uint64_t g = tile % groups, c = tile / groups;
     const uint64_t line0 = (g * kWave + (uint64_t)lane) * V;
     const bool active = line0 < p.lines;
+    const A aid = Op::template identity<A>();
+
+    if (w == kColDataWaves) {
+        __syncthreads(); // the data waves' totals
+        A agg[V], excl[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) agg[v] = aid;
+#pragma unroll 1
+        for (int q = 0; q < kColDataWaves; ++q)
+#pragma unroll
+            for (int v = 0; v < V; ++v) agg[v] = Op::combine(agg[v], s_agg[q][lane * V + v]);
+        col_lookback_wave<T, Op, Status, V, REV>(p, st, c, lpad, line0, active, agg, excl);
+#pragma unroll
+        for (int v = 0; v < V; ++v) s_carry[lane * V + v] = excl[v];
+        __syncthreads(); // the carry
+        return;
+    }
+
     const uint64_t i0 = c * kColTileRows + (uint64_t)w * kColRows;
     const ColGroupAddr ia = col_group_addr<V, T>(g, lane, p.in_line_stride, p.in_offset);
     const ColGroupAddr oa = col_group_addr<V, T>(g, lane, p.out_line_stride, p.out_offset);
     const T tid = Op::template identity<T>();
-    const A aid = Op::template identity<A>();
 
     // The wave's steps, scanned per line from the identity.
     T x[kColRows][V];
@@ -797,83 +907,17 @@ __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanPara
         for (int v = 0; v < V; ++v) x[r][v] = Op::combine(r == 0 ? tid : x[r - 1][v], x[r][v]);
 #pragma unroll
     for (int v = 0; v < V; ++v) s_agg[w][lane * V + v] = (A)x[kColRows - 1][v];
-    __syncthreads();
-
-    if (w == 0) {
-        A agg[V], excl[V];
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-            agg[v] = aid;
-            for (int q = 0; q < kColWaves; ++q) agg[v] = Op::combine(agg[v], s_agg[q][lane * V + v]);
-            excl[v] = aid;
-        }
-        if (active) {
-            const uint64_t e = c * lpad + line0;
-            if (c == 0) {
-#pragma unroll
-                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, agg[v]);
-            } else {
-#pragma unroll
-                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kAggregate, agg[v]);
-                bool done[V];
-#pragma unroll
-                for (int v = 0; v < V; ++v) done[v] = false;
-                uint64_t pred = c - 1;
-                for (;;) {
-                    uint32_t flag[V];
-                    A val[V];
-                    uint32_t spins = 0;
-                    for (;;) {
-                        bool all = true;
-#pragma unroll
-                        for (int v = 0; v < V; ++v) {
-                            flag[v] = kPrefix;
-                            val[v] = aid;
-                            if (!done[v]) {
-                                st.read(pred * lpad + line0 + v, p.tag, flag[v], val[v]);
-                                all = all && flag[v] != kInvalid;
-                            }
-                        }
-                        if (all) break;
-                        if (++spins >= kSpinLimit) {
-                            A fb[V];
-                            col_tile_aggregate<T, Op, V, REV>(p, pred, line0, fb);
-#pragma unroll
-                            for (int v = 0; v < V; ++v)
-                                if (!done[v] && flag[v] == kInvalid)
-                                    st.publish_if_unset(pred * lpad + line0 + v, p.tag, kAggregate, fb[v]);
-                            spins = 0;
-                            continue;
-                        }
-                        __builtin_amdgcn_s_sleep(1);
-                    }
-                    bool all_done = true;
-#pragma unroll
-                    for (int v = 0; v < V; ++v) {
-                        if (done[v]) continue;
-                        excl[v] = Op::combine(val[v], excl[v]);
-                        if (flag[v] == kPrefix) done[v] = true;
-                        else all_done = false;
-                    }
-                    if (all_done || pred == 0) break; // chunk 0 publishes prefixes only
-                    --pred;
-                }
-#pragma unroll
-                for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, Op::combine(excl[v], agg[v]));
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < V; ++v) s_carry[lane * V + v] = excl[v];
-    }
-    __syncthreads();
+    __syncthreads(); // totals to the look-back wave
+    __syncthreads(); // its carry
     if (!active) return;
 
     A carry[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-        carry[v] = s_carry[lane * V + v];
-        for (int q = 0; q < w; ++q) carry[v] = Op::combine(carry[v], s_agg[q][lane * V + v]);
-    }
+    for (int v = 0; v < V; ++v) carry[v] = s_carry[lane * V + v];
+#pragma unroll 1
+    for (int q = 0; q < w; ++q)
+#pragma unroll
+        for (int v = 0; v < V; ++v) carry[v] = Op::combine(carry[v], s_agg[q][lane * V + v]);
 #pragma unroll
     for (int r = 0; r < kColRows; ++r) {
         const uint64_t i = i0 + r;
@@ -947,9 +991,13 @@ ColLbShape col_lb_shape(const ScanArgs &a) {
 // The single pass needs whole line groups: with fewer than 256 lines every
 // tile leaves lanes idle and all tiles form one long look-back chain
 // (measured, u32: 4194304 x 64 1.63 ms single-pass against 0.75 ms chunked;
-// 1048576 x 256 0.50 against 0.71; 65536 x 4096 0.42 against 0.55).
+// 1048576 x 256 0.46 against 0.71; 65536 x 4096 0.35 against 0.54).  f32
+// scans stay chunked: their f64 statuses take four words each, and the
+// chunked form measured faster (65536 x 4096: 0.57 against 0.64 ms).
 constexpr uint64_t kSinglePassMinLines = 256;
-bool column_single_pass(const ScanArgs &a) { return column_mode(a) && a.lines >= kSinglePassMinLines; }
+bool column_single_pass(const ScanArgs &a) {
+    return column_mode(a) && a.lines >= kSinglePassMinLines && a.dtype != HX_DTYPE_F32;
+}
 
 uint64_t column_bytes(const ScanArgs &a) {
     const ColShape s = column_shape(a);
@@ -1001,9 +1049,7 @@ template <typename T, typename Op>
 hx_status launch_col_lookback(const ScanParams &p, const ColLbShape &s, bool excl, bool rev, void *status,
                               hipStream_t stream) {
     if constexpr (std::is_same<T, float>::value) {
-        const F64Status st{(uint64_t *)status};
-        return s.V == 4 ? launch_col_lookback_s<T, Op, F64Status, 4>(p, s, st, excl, rev, stream)
-                        : launch_col_lookback_s<T, Op, F64Status, 1>(p, s, st, excl, rev, stream);
+        return fail(HX_ERR_DISPATCH_FAILED, "single-pass column scans take integer elements");
     } else {
         const PackedStatus st{(uint64_t *)status};
         return s.V == 4 ? launch_col_lookback_s<T, Op, PackedStatus, 4>(p, s, st, excl, rev, stream)
