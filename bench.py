@@ -36,7 +36,7 @@ WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30"
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
              "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
-             "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_scan_kernel"}
+             "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel"}
 
 
 def log(msg: str) -> None:
