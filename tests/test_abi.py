@@ -168,6 +168,18 @@ def test_null_device_handles_are_rejected_on_the_host():
     assert lib.hx_alloc(None, 16, 1, ctypes.byref(out)) == _ffi.INVALID_CONFIGURATION
 
 
+def test_batch_submission_checks_its_arguments_on_the_host():
+    """hx_plan_dispatch_batch rejects a null array or a null entry before any
+    plan runs; an empty batch is a no-op."""
+    lib = hx.load_native()
+    assert lib.hx_plan_dispatch_batch(None, 0, None) == _ffi.OK
+    assert lib.hx_plan_dispatch_batch(None, 2, None) == _ffi.INVALID_CONFIGURATION
+    assert _ffi.last_message() == "null plan array"
+    arr = (ctypes.c_void_p * 3)(None, None, None)
+    assert lib.hx_plan_dispatch_batch(arr, 3, None) == _ffi.INVALID_CONFIGURATION
+    assert _ffi.last_message() == "null plan at batch index 0"
+
+
 def test_entry_points_validate_before_touching_the_device():
     """Every device entry point rejects a bad operand before it needs the
     device, so these run without a GPU (and leave outputs untouched)."""
