@@ -322,13 +322,33 @@ hx_status hx_free(hx_device *dev, void *ptr) {
 
 namespace {
 
+// Both staging buffers and their events, or none: a failed set-up releases
+// what it made, and `pinned_bytes` (the chunk size the copy loops step by)
+// is set only once everything exists.
 hx_status ensure_staging(hx_device *dev) {
-    if (dev->pinned[0]) return HX_OK;
-    for (int i = 0; i < 2; ++i) {
-        HX_HIP(hipHostMalloc(&dev->pinned[i], kStagingChunk, hipHostMallocDefault),
-               HX_ERR_TRANSFER_FAILED, "pinned staging hipHostMalloc");
-        HX_HIP(hipEventCreateWithFlags(&dev->pinned_ev[i], hipEventDisableTiming),
-               HX_ERR_TRANSFER_FAILED, "staging event");
+    if (dev->pinned_bytes != 0) return HX_OK;
+    hipError_t err = hipSuccess;
+    const char *what = nullptr;
+    for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+        if (!dev->pinned[i]) {
+            err = hipHostMalloc(&dev->pinned[i], kStagingChunk, hipHostMallocDefault);
+            what = "pinned staging hipHostMalloc";
+            if (err != hipSuccess) dev->pinned[i] = nullptr;
+        }
+        if (err == hipSuccess && !dev->pinned_ev[i]) {
+            err = hipEventCreateWithFlags(&dev->pinned_ev[i], hipEventDisableTiming);
+            what = "staging event";
+            if (err != hipSuccess) dev->pinned_ev[i] = nullptr;
+        }
+    }
+    if (err != hipSuccess) {
+        for (int i = 0; i < 2; ++i) {
+            if (dev->pinned[i]) (void)hipHostFree(dev->pinned[i]);
+            if (dev->pinned_ev[i]) (void)hipEventDestroy(dev->pinned_ev[i]);
+            dev->pinned[i] = nullptr;
+            dev->pinned_ev[i] = nullptr;
+        }
+        return hip_fail(HX_ERR_TRANSFER_FAILED, err, what);
     }
     dev->pinned_bytes = kStagingChunk;
     return HX_OK;
@@ -414,6 +434,16 @@ hx_status check_elem(uint32_t elem_size) {
     return HX_OK;
 }
 
+// Byte count of `len` elements, rejecting lengths whose byte count does not
+// fit 64 bits (the transfer would otherwise wrap to a short copy).
+hx_status byte_count(uint64_t len, uint32_t elem_size, uint64_t *bytes) {
+    if (len > UINT64_MAX / elem_size)
+        return fail(HX_ERR_INVALID_CONFIGURATION, "%llu elements of %u bytes exceed the address range",
+                    (unsigned long long)len, elem_size);
+    *bytes = len * elem_size;
+    return HX_OK;
+}
+
 } // namespace
 
 extern "C" {
@@ -422,8 +452,9 @@ hx_status hx_upload(hx_device *dev, void *dst, uint64_t dst_len, const void *src
                     uint64_t src_len, uint32_t elem_size) {
     HX_TRY(check_elem(elem_size));
     if (dst_len != src_len) return length_mismatch(src_len, dst_len);
+    uint64_t bytes = 0;
+    HX_TRY(byte_count(src_len, elem_size, &bytes));
     HX_TRY(bind_device(dev));
-    uint64_t bytes = src_len * elem_size;
     if (bytes == 0) return ok();
     if (!dst || !src) return fail(HX_ERR_TRANSFER_FAILED, "null transfer pointer");
     HX_TRY(staged_h2d(dev, dst, src, bytes));
@@ -436,8 +467,10 @@ hx_status hx_write_sub(hx_device *dev, void *dst, uint64_t dst_len, uint64_t off
     // host lib.rs:157-169: overflow or end beyond the buffer -> LengthMismatch
     uint64_t end = offset + src_len;
     if (end < offset || end > dst_len) return length_mismatch(src_len, dst_len);
+    uint64_t bytes = 0, skip = 0;
+    HX_TRY(byte_count(end, elem_size, &skip)); // also bounds offset * elem_size
+    HX_TRY(byte_count(src_len, elem_size, &bytes));
     HX_TRY(bind_device(dev));
-    uint64_t bytes = src_len * elem_size;
     if (bytes == 0) return ok();
     if (!dst || !src) return fail(HX_ERR_TRANSFER_FAILED, "null transfer pointer");
     HX_TRY(staged_h2d(dev, (char *)dst + offset * elem_size, src, bytes));
@@ -448,8 +481,9 @@ hx_status hx_download(hx_device *dev, const void *src, uint64_t src_len, void *d
                       uint64_t dst_len, uint32_t elem_size) {
     HX_TRY(check_elem(elem_size));
     if (dst_len != src_len) return length_mismatch(dst_len, src_len);
+    uint64_t bytes = 0;
+    HX_TRY(byte_count(src_len, elem_size, &bytes));
     HX_TRY(bind_device(dev));
-    uint64_t bytes = src_len * elem_size;
     if (bytes == 0) return ok();
     if (!dst || !src) return fail(HX_ERR_TRANSFER_FAILED, "null transfer pointer");
     HX_TRY(staged_d2h(dev, dst, src, bytes));
@@ -461,8 +495,9 @@ hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len, void *dst,
     HX_TRY(check_elem(elem_size));
     if (src == dst && src_len == dst_len) return ok(); // host lib.rs:175-177
     if (dst_len != src_len) return length_mismatch(dst_len, src_len);
+    uint64_t bytes = 0;
+    HX_TRY(byte_count(src_len, elem_size, &bytes));
     HX_TRY(bind_device(dev));
-    uint64_t bytes = src_len * elem_size;
     if (bytes == 0) return ok();
     HX_TRY(launch_copy(src, dst, bytes, dev->stream));
     HX_HIP(hipStreamSynchronize(dev->stream), HX_ERR_TRANSFER_FAILED, "D2D synchronize");

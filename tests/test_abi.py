@@ -168,6 +168,15 @@ def test_null_device_handles_are_rejected_on_the_host():
     assert lib.hx_alloc(None, 16, 1, ctypes.byref(out)) == _ffi.INVALID_CONFIGURATION
 
 
+def test_transfer_byte_counts_that_overflow_are_rejected_on_the_host():
+    lib = hx.load_native()
+    n = 1 << 62
+    for fn in (lib.hx_upload, lib.hx_download, lib.hx_copy):
+        assert fn(None, 0x1000, n, 0x2000, n, 8) == _ffi.INVALID_CONFIGURATION
+        assert _ffi.last_message() == f"{n} elements of 8 bytes exceed the address range"
+    assert lib.hx_write_sub(None, 0x1000, n + 1, 1, 0x2000, n, 8) == _ffi.INVALID_CONFIGURATION
+
+
 def test_batch_submission_checks_its_arguments_on_the_host():
     """hx_plan_dispatch_batch rejects a null array or a null entry before any
     plan runs; an empty batch is a no-op."""
