@@ -137,6 +137,30 @@ struct F64Status {
     }
 };
 
+// f64 values for the single-pass column scan: one slot of two self-tagged
+// words (high and low halves) per entry, which the owner writes twice --
+// aggregate, then inclusive prefix.  A reader accepts the slot only when both
+// halves carry this launch's tag and the same flag; a half-updated slot reads
+// as not ready.  Every slot has exactly one writer (waiters that give up
+// compute the value themselves and do not publish it), so halves of
+// different values can only meet transiently.
+struct F64PairStatus {
+    using C = double;
+    uint64_t *words;
+    __device__ __forceinline__ void publish_tile(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        st_relaxed(&words[2 * t], status_word(tag, flag, (uint32_t)(b >> 32)));
+        st_relaxed(&words[2 * t + 1], status_word(tag, flag, (uint32_t)b));
+    }
+    __device__ __forceinline__ void publish_if_unset(uint64_t, uint32_t, uint32_t, C) const {}
+    __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
+        const uint64_t hi = ld_relaxed(&words[2 * t]), lo = ld_relaxed(&words[2 * t + 1]);
+        const uint32_t h = (uint32_t)(hi >> 32), l = (uint32_t)(lo >> 32);
+        flag = (h == l && (h >> 2) == tag) ? (h & 3u) : kInvalid;
+        v = __builtin_bit_cast(double, (hi << 32) | (lo & 0xFFFFFFFFull));
+    }
+};
+
 struct ScanParams {
     const void *in;
     void *out;
@@ -666,15 +690,16 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
 // wave holds no data: it runs the decoupled look-back, lane l for its V
 // lines, polling kColPoll earlier chunks of the same line group per round
 // trip and folding aggregates until each line meets an inclusive prefix.
-// Integer scans only (packed one-word statuses); f32 column scans take the
-// chunked path, whose f64 accumulation runs along the whole line.
+// Integer scans publish one packed word per line and chunk; f32 scans an
+// f64 carry in a two-word slot (F64PairStatus), with the tile's steps
+// scanned in f32 and the carries and outputs formed in f64.
 // Data and look-back waves run separate code paths (wave-uniform), so the
 // tile's registers are not live during the look-back.  Status entry of
 // (chunk c, line j) is c * lpad + j.  Every element is read once and written
 // once.  A predecessor that stays unpublished for kSpinLimit rounds has its
 // aggregate rebuilt from the input by the waiter with the owner's arithmetic
 // (f32: per-wave f32 prefix from the identity, then f64 over the waves in
-// order), so progress never depends on dispatch order.
+// order) and used directly, so progress never depends on dispatch order.
 constexpr int kColWaves = 16;
 constexpr int kColDataWaves = kColWaves - 1;
 constexpr int kColRows = 16;
@@ -806,6 +831,30 @@ __device__ void col_lookback_wave(const ScanParams &p, const Status &st, uint64_
                 val[k][v] = aid;
                 if (!done[v] && (uint64_t)k <= pos) st.read((pos - k) * lpad + line0 + v, p.tag, flag[k][v], val[k][v]);
             }
+        // The next predecessor not ready for some line: wait, and after
+        // kSpinLimit polls take its aggregate from the input (the owner's
+        // arithmetic) and use it directly -- so progress never depends on
+        // dispatch order.  Publishing it is only a courtesy to other
+        // waiters, and is skipped where a status slot must keep one writer.
+        bool ready0 = true;
+#pragma unroll
+        for (int v = 0; v < V; ++v) ready0 = ready0 && (done[v] || flag[0][v] != kInvalid);
+        if (!ready0) {
+            if (++spins < kSpinLimit) {
+                __builtin_amdgcn_s_sleep(1);
+                continue;
+            }
+            A fb[V];
+            col_tile_aggregate<T, Op, V, REV>(p, pos, line0, fb);
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                if (!done[v] && flag[0][v] == kInvalid) {
+                    st.publish_if_unset(pos * lpad + line0 + v, p.tag, kAggregate, fb[v]);
+                    flag[0][v] = kAggregate;
+                    val[0][v] = fb[v];
+                }
+        }
+        spins = 0;
         int used = 0;
         bool finished = false;
 #pragma unroll
@@ -831,21 +880,7 @@ __device__ void col_lookback_wave(const ScanParams &p, const Status &st, uint64_
             finished = all;
         }
         if (finished) break;
-        if (used > 0) {
-            pos -= (uint64_t)used; // > 0 remains: consuming chunk 0 finishes every line
-            spins = 0;
-            continue;
-        }
-        if (++spins >= kSpinLimit) {
-            A fb[V];
-            col_tile_aggregate<T, Op, V, REV>(p, pos, line0, fb);
-#pragma unroll
-            for (int v = 0; v < V; ++v)
-                if (!done[v] && flag[0][v] == kInvalid) st.publish_if_unset(pos * lpad + line0 + v, p.tag, kAggregate, fb[v]);
-            spins = 0;
-            continue;
-        }
-        __builtin_amdgcn_s_sleep(1);
+        pos -= (uint64_t)used; // used >= 1 (entry pos was ready); chunk 0 finishes every line
     }
 #pragma unroll
     for (int v = 0; v < V; ++v) st.publish_tile(e + v, p.tag, kPrefix, Op::combine(excl[v], agg[v]));
@@ -991,13 +1026,10 @@ ColLbShape col_lb_shape(const ScanArgs &a) {
 // The single pass needs whole line groups: with fewer than 256 lines every
 // tile leaves lanes idle and all tiles form one long look-back chain
 // (measured, u32: 4194304 x 64 1.63 ms single-pass against 0.75 ms chunked;
-// 1048576 x 256 0.46 against 0.71; 65536 x 4096 0.35 against 0.54).  f32
-// scans stay chunked: their f64 statuses take four words each, and the
-// chunked form measured faster (65536 x 4096: 0.57 against 0.64 ms).
+// 1048576 x 256 0.46 against 0.71; 65536 x 4096 0.35 against 0.54; f32
+// 65536 x 4096 0.48 against 0.56).
 constexpr uint64_t kSinglePassMinLines = 256;
-bool column_single_pass(const ScanArgs &a) {
-    return column_mode(a) && a.lines >= kSinglePassMinLines && a.dtype != HX_DTYPE_F32;
-}
+bool column_single_pass(const ScanArgs &a) { return column_mode(a) && a.lines >= kSinglePassMinLines; }
 
 uint64_t column_bytes(const ScanArgs &a) {
     const ColShape s = column_shape(a);
@@ -1049,7 +1081,9 @@ template <typename T, typename Op>
 hx_status launch_col_lookback(const ScanParams &p, const ColLbShape &s, bool excl, bool rev, void *status,
                               hipStream_t stream) {
     if constexpr (std::is_same<T, float>::value) {
-        return fail(HX_ERR_DISPATCH_FAILED, "single-pass column scans take integer elements");
+        const F64PairStatus st{(uint64_t *)status};
+        return s.V == 4 ? launch_col_lookback_s<T, Op, F64PairStatus, 4>(p, s, st, excl, rev, stream)
+                        : launch_col_lookback_s<T, Op, F64PairStatus, 1>(p, s, st, excl, rev, stream);
     } else {
         const PackedStatus st{(uint64_t *)status};
         return s.V == 4 ? launch_col_lookback_s<T, Op, PackedStatus, 4>(p, s, st, excl, rev, stream)
@@ -1086,7 +1120,7 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
 uint64_t scan_bytes(const ScanArgs &a) {
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape c = col_lb_shape(a);
-        return kLookbackOffset + status_bytes(c.chunks * c.lpad, a.dtype == HX_DTYPE_F32);
+        return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
     }
     if (column_mode(a)) return column_bytes(a);
     const uint64_t tpl = ceil_div(a.len, kTile);
