@@ -176,7 +176,7 @@ struct ScanParams {
 template <typename T, bool VEC, bool REV, bool NT>
 __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t ib, uint64_t e, T ident,
                                       T (&v)[4]) {
-    if constexpr (VEC) {
+    if constexpr (VEC && !REV) {
         if (e + 3 < p.len) {
             using V = typename Vec4<T>::type;
             const V q = load_vec<NT>((const V *)(in + ib + (int64_t)e));
@@ -359,6 +359,31 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
 // ragged last one): a block-uniform base pointer plus one 32-bit lane offset,
 // so each step is a single base + offset + immediate vector access with no
 // bounds check and no per-step 64-bit address held in registers.
+// A whole tile of a reverse scan is a mirrored block of memory: logical
+// elements e..e+3 of a lane's step are one 16-byte vector in reversed order,
+// at byte (tile_bytes - 16 - lane_off - j * 1024) from the block's lowest
+// address (always >= 0).
+// Integer tiles are held to 128 VGPRs, two 8-wave blocks per CU: the
+// inclusive forms (131 VGPRs unconstrained, one block per CU) spill a few
+// words of look-back state and still gain ~3% (2^28 u32 inclusive 0.388 ->
+// 0.378 ms).  f32 tiles, whose f64 carries need ~148, keep the compiler's
+// budget (a 128 cap spilled 88 bytes and lost 18%).
+template <typename T> struct ScanWavesPerEu { static constexpr int value = 4; };
+template <> struct ScanWavesPerEu<float> { static constexpr int value = 1; };
+
+template <typename T, bool NT, int STEPS>
+__device__ __forceinline__ void load_full_tile_rev(const T *base, uint32_t rev_off, T (&x)[STEPS][4]) {
+    using V = typename Vec4<T>::type;
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+        const V q = load_vec<NT>((const V *)((const char *)base + rev_off - (uint32_t)j * (kWave * 16)));
+        x[j][0] = (T)q.w;
+        x[j][1] = (T)q.z;
+        x[j][2] = (T)q.y;
+        x[j][3] = (T)q.x;
+    }
+}
+
 template <typename T, bool NT, int STEPS>
 __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off, T (&x)[STEPS][4]) {
     using V = typename Vec4<T>::type;
@@ -378,7 +403,8 @@ __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off,
 // vector accesses.
 template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
           bool NT = true, int WAVES = kWaves>
-__global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
+__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(ScanWavesPerEu<T>::value)))
+void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     using C = typename Status::C;
     constexpr int kWaveElems = kWave * 4 * STEPS;
     constexpr int kTileElems = WAVES * kWaveElems;
@@ -401,9 +427,15 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
     const uint32_t lane_off =
         ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * (uint32_t)sizeof(T);
     const bool full = VEC && (tin + 1) * kTileElems <= p.len;
+    // Reverse: the tile's lowest physical element, and the mirrored offset.
+    const int64_t rev_tile = REV ? (int64_t)(p.len - (tin + 1) * kTileElems) : 0;
+    const uint32_t rev_off = (uint32_t)(kTileElems - 4) * (uint32_t)sizeof(T) - lane_off;
     T x[STEPS][4];
     if (full) {
-        load_full_tile<T, NT, STEPS>(in + ib + (int64_t)(tin * kTileElems), lane_off, x);
+        if constexpr (REV)
+            load_full_tile_rev<T, NT, STEPS>(in + ib + rev_tile, rev_off, x);
+        else
+            load_full_tile<T, NT, STEPS>(in + ib + (int64_t)(tin * kTileElems), lane_off, x);
         // All STEPS loads are issued before any arithmetic is scheduled.
         __builtin_amdgcn_sched_barrier(0);
     } else {
@@ -466,15 +498,28 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
 
     if (full) {
         using V = typename Vec4<T>::type;
-        char *obase = (char *)(out + ob + (int64_t)(tin * kTileElems));
+        if constexpr (REV) {
+            char *obase = (char *)(out + ob + rev_tile);
 #pragma unroll
-        for (int j = 0; j < STEPS; ++j) {
-            V v;
-            v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
-            v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
-            v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
-            v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
-            store_vec<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
+            for (int j = 0; j < STEPS; ++j) {
+                V v;
+                v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
+                v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
+                v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
+                v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
+                store_vec<NT>(v, (V *)(obase + rev_off - (uint32_t)j * (kWave * 16)));
+            }
+        } else {
+            char *obase = (char *)(out + ob + (int64_t)(tin * kTileElems));
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                V v;
+                v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
+                v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
+                v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
+                v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
+                store_vec<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
+            }
         }
         return;
     }
@@ -484,7 +529,7 @@ __global__ __launch_bounds__(WAVES * kWave) void scan_tiles_kernel(ScanParams p,
         T r[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][c]));
-        if constexpr (VEC) {
+        if constexpr (VEC && !REV) {
             if (e + 3 < p.len) {
                 using V = typename Vec4<T>::type;
                 V v;
@@ -1107,7 +1152,9 @@ template <typename T, typename Op, typename Status, bool EXCL>
 hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
                        hipStream_t stream) {
     const dim3 grid((uint32_t)p.total_tiles), block(kWaves * kWave);
-    if (vec)
+    if (vec && rev)
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true>), grid, block, 0, stream, p, st, st1);
+    else if (vec)
         hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false>), grid, block, 0, stream, p, st, st1);
     else if (rev)
         hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true>), grid, block, 0, stream, p, st, st1);
@@ -1175,8 +1222,10 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
     const uintptr_t ibase = (uintptr_t)((const T *)a.in + a.in_offset);
     const uintptr_t obase = (uintptr_t)((T *)a.out + a.out_offset);
-    const bool vec = contiguous && !a.reverse && ibase % 16 == 0 && obase % 16 == 0 && a.in_line_stride % 4 == 0 &&
-                     a.out_line_stride % 4 == 0;
+    // Reverse scans vectorise their whole tiles as mirrored blocks, which
+    // stay 16-byte aligned when the line length is a multiple of 4.
+    const bool vec = contiguous && ibase % 16 == 0 && obase % 16 == 0 && a.in_line_stride % 4 == 0 &&
+                     a.out_line_stride % 4 == 0 && (!a.reverse || a.len % 4 == 0);
     const bool f64 = std::is_same<T, float>::value;
     uint64_t *level0 = (uint64_t *)((char *)ws + kLookbackOffset);
     uint64_t *level1 = (uint64_t *)((char *)level0 + status_bytes(p.total_tiles, f64));

@@ -298,6 +298,45 @@ def test_scan_u32_tile_and_superblock_edges(device, oracle, n, kind, direction):
     assert np.array_equal(device.download_owned(out), want)
 
 
+# Reverse scans of lengths that are multiples of 4 take the mirrored
+# 16-byte path for whole tiles and the scalar path for the ragged one.
+REV_VEC = [4, 32768, 32772, 3 * 32768 + 100, (1 << 21) + 4, 64 * 32768 * 2 + 32768 + 12]
+
+
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("n", REV_VEC)
+def test_reverse_scans_vector_path(device, oracle, n, kind):
+    excl = kind == hx.ScanKind.Exclusive
+    x = oracle.uniform_int(n, seed=n ^ 0x77, lo=0, hi=2**32 - 1)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, n)
+    lay = Layout.c_contiguous([n])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 0, hx.ScanDirection.Reverse,
+                        StridedView(out, lay), kind)
+    assert np.array_equal(device.download_owned(out), oracle.scan_sum(x, exclusive=excl, reverse=True))
+    xf = oracle.uniform_real(n, seed=n + 9, lo=-1.0, hi=1.0)
+    fb = device.upload(xf)
+    of = device.alloc_zeroed(np.float32, n)
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(fb, lay), 0, hx.ScanDirection.Reverse,
+                        StridedView(of, lay), kind)
+    ref, ab = oracle.scan_sum(xf, exclusive=excl, reverse=True)
+    bad, worst = oracle.check_f32_bound(device.download_owned(of), ref, ab, n)
+    assert bad == 0, worst
+
+
+@pytest.mark.parametrize("shape", [(3, 65540), (5, 32768), (2, 100004)])
+def test_reverse_scans_of_rank2_lines(device, oracle, shape):
+    r, c = shape
+    x = oracle.uniform_int(r * c, seed=r * c, lo=-1000, hi=1000, dtype=np.int32)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.int32, r * c)
+    lay = Layout.c_contiguous([r, c])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 1, hx.ScanDirection.Reverse,
+                        StridedView(out, lay))
+    want = np.cumsum(x.reshape(r, c)[:, ::-1], axis=1, dtype=np.int32)[:, ::-1]
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+
+
 @pytest.mark.parametrize("n", SCAN_EDGES)
 def test_scan_f32_tile_and_superblock_edges(device, oracle, n):
     x = oracle.uniform_real(n, seed=n + 3, lo=-1.0, hi=1.0)
