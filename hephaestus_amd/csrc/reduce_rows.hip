@@ -12,7 +12,9 @@
 //                      l+64, ... of the row (every load instruction covers
 //                      1 KiB of contiguous memory), keeps every requested
 //                      statistic in registers, then combines them with
-//                      xor-butterflies.  Used whenever the reduced axis has
+//                      xor-butterflies.  Rows that do not start on a 16-byte
+//                      boundary take their 0-3 leading and trailing elements
+//                      one per lane.  Used whenever the reduced axis has
 //                      unit stride (or no stride is unit).
 //   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
 //                      chunk statistics to partial planes.
@@ -163,44 +165,61 @@ template <typename T, int FLAGS> struct Stats {
     }
 };
 
-// One wave per row.  VEC: unit column stride and every row start 16-byte
-// aligned, so lanes issue global_load_dwordx4.
+// Statistics of `len` consecutive elements at `src` (unit stride, 4-byte
+// aligned), reported with global indices from `j0`.  The 0-3 elements before
+// the first 16-byte boundary go one per lane, the aligned body as 16-byte
+// vectors (lane l takes vectors l, l+64, ..., so every load instruction of
+// the wave covers 1 KiB), and the 0-3 elements after it one per lane.  Rows
+// of any length therefore stream at the aligned rate.
+template <typename T, bool AFFINE, int FLAGS>
+__device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *src, uint64_t len, uint64_t j0, int lane,
+                                                float a, float b) {
+    using V = typename Vec4<T>::type;
+    uint64_t head = (((uint64_t)0 - (uint64_t)(uintptr_t)src) & 15u) >> 2;
+    if (head > len) head = len;
+    if ((uint64_t)lane < head) st.visit(prologue<T, AFFINE>(src[lane], a, b), (uint32_t)(j0 + lane));
+    const V *vrow = (const V *)(src + head);
+    const uint64_t nvec = (len - head) >> 2;
+    const uint32_t jb = (uint32_t)(j0 + head);
+    uint64_t v = lane;
+    for (; v + 3 * kWave < nvec; v += 4 * kWave) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * kWave]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t j = jb + (uint32_t)(4 * (v + u * kWave));
+            st.visit(prologue<T, AFFINE>((T)x[u].x, a, b), j);
+            st.visit(prologue<T, AFFINE>((T)x[u].y, a, b), j + 1);
+            st.visit(prologue<T, AFFINE>((T)x[u].z, a, b), j + 2);
+            st.visit(prologue<T, AFFINE>((T)x[u].w, a, b), j + 3);
+        }
+    }
+    for (; v < nvec; v += kWave) {
+        V x = __builtin_nontemporal_load(&vrow[v]);
+        const uint32_t j = jb + (uint32_t)(4 * v);
+        st.visit(prologue<T, AFFINE>((T)x.x, a, b), j);
+        st.visit(prologue<T, AFFINE>((T)x.y, a, b), j + 1);
+        st.visit(prologue<T, AFFINE>((T)x.z, a, b), j + 2);
+        st.visit(prologue<T, AFFINE>((T)x.w, a, b), j + 3);
+    }
+    const uint64_t t = head + 4 * nvec + lane;
+    if (t < len) st.visit(prologue<T, AFFINE>(src[t], a, b), (uint32_t)(j0 + t));
+}
+
+// One wave per row.  VEC: unit column stride, so lanes issue
+// global_load_dwordx4 over each row's 16-byte-aligned body.
 template <typename T, bool AFFINE, int FLAGS, bool VEC>
 __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     const int lane = lane_id();
-    const uint64_t wave = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    const uint64_t wave =
+        (uint64_t)blockIdx.x * (kBlock / kWave) + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint64_t nwaves = (uint64_t)gridDim.x * (kBlock / kWave);
     for (uint64_t r = wave; r < p.rows; r += nwaves) {
         const T *row = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
         Stats<T, FLAGS> st;
         if constexpr (VEC) {
-            using V = typename Vec4<T>::type;
-            const V *vrow = (const V *)row;
-            const uint64_t nvec = p.cols >> 2;
-            uint64_t v = lane;
-            for (; v + 3 * kWave < nvec; v += 4 * kWave) {
-                V x[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * kWave]);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const uint32_t j = (uint32_t)(4 * (v + u * kWave));
-                    st.visit(prologue<T, AFFINE>((T)x[u].x, p.a, p.b), j);
-                    st.visit(prologue<T, AFFINE>((T)x[u].y, p.a, p.b), j + 1);
-                    st.visit(prologue<T, AFFINE>((T)x[u].z, p.a, p.b), j + 2);
-                    st.visit(prologue<T, AFFINE>((T)x[u].w, p.a, p.b), j + 3);
-                }
-            }
-            for (; v < nvec; v += kWave) {
-                V x = __builtin_nontemporal_load(&vrow[v]);
-                const uint32_t j = (uint32_t)(4 * v);
-                st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
-                st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
-                st.visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), j + 2);
-                st.visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), j + 3);
-            }
-            const uint64_t j = 4 * nvec + lane;
-            if (j < p.cols) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), (uint32_t)j);
+            visit_unit_span<T, AFFINE, FLAGS>(st, row, p.cols, 0, lane, p.a, p.b);
         } else {
             for (uint64_t j = lane; j < p.cols; j += kWave)
                 st.visit(prologue<T, AFFINE>(row[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
@@ -285,33 +304,7 @@ __global__ __launch_bounds__(kBlock) void rows_split_kernel(RowParams p, uint64_
     const uint64_t c1 = c0 + chunk < p.cols ? c0 + chunk : p.cols;
     Stats<T, FLAGS> st;
     if constexpr (VEC) {
-        using V = typename Vec4<T>::type;
-        const V *vrow = (const V *)(row + c0);
-        const uint64_t nvec = (c1 - c0) >> 2;
-        uint64_t v = lane;
-        for (; v + 3 * kWave < nvec; v += 4 * kWave) {
-            V x[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * kWave]);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t j = (uint32_t)(c0 + 4 * (v + u * kWave));
-                st.visit(prologue<T, AFFINE>((T)x[u].x, p.a, p.b), j);
-                st.visit(prologue<T, AFFINE>((T)x[u].y, p.a, p.b), j + 1);
-                st.visit(prologue<T, AFFINE>((T)x[u].z, p.a, p.b), j + 2);
-                st.visit(prologue<T, AFFINE>((T)x[u].w, p.a, p.b), j + 3);
-            }
-        }
-        for (; v < nvec; v += kWave) {
-            V x = __builtin_nontemporal_load(&vrow[v]);
-            const uint32_t j = (uint32_t)(c0 + 4 * v);
-            st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
-            st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
-            st.visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), j + 2);
-            st.visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), j + 3);
-        }
-        const uint64_t j = c0 + 4 * nvec + lane;
-        if (j < c1) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), (uint32_t)j);
+        visit_unit_span<T, AFFINE, FLAGS>(st, row + c0, c1 - c0, c0, lane, p.a, p.b);
     } else {
         for (uint64_t j = c0 + lane; j < c1; j += kWave)
             st.visit(prologue<T, AFFINE>(row[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
@@ -380,7 +373,7 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
             if (k > kmax) k = kmax;
         }
     } else {
-        s.vec = p.col_stride == 1 && base % 16 == 0 && (p.row_stride % 4 == 0 || p.rows == 1);
+        s.vec = p.col_stride == 1 && base % 4 == 0;
         if (p.rows < kRowTargetWaves / 2 && p.cols >= 2 * kMinRowChunk) {
             k = ceil_div(kRowTargetWaves, p.rows);
             const uint64_t kmax = ceil_div(p.cols, kMinRowChunk);
@@ -390,7 +383,7 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
     if (k < 1) k = 1;
     if (k > 1) {
         uint64_t chunk = ceil_div(p.cols, k);
-        if (!cols_layout) chunk = ceil_div(chunk, 256) * 256; // keeps 16-byte alignment of every chunk
+        if (!cols_layout) chunk = ceil_div(chunk, 256) * 256; // whole 1 KiB wave loads per chunk
         s.chunk = chunk;
         s.nchunks = (uint32_t)ceil_div(p.cols, chunk);
     } else {

@@ -188,7 +188,11 @@ def test_argmax_special_cases(device):
 # ------------------------------------------------------------ rows
 @pytest.mark.parametrize("rows,cols,ld,offset", [
     (1, 1, 1, 0), (3, 4, 4, 0), (7, 63, 63, 0), (5, 64, 68, 4), (33, 4096, 4096, 0),
-    (17, 4099, 4103, 1), (256, 1000, 1000, 0), (1000, 257, 260, 8), (2, 70000, 70000, 0)])
+    (17, 4099, 4103, 1), (256, 1000, 1000, 0), (1000, 257, 260, 8), (2, 70000, 70000, 0),
+    # row starts off 16-byte boundaries: 0-3 element heads and tails per row
+    (300, 4095, 4095, 0), (129, 4093, 4093, 3), (77, 4097, 4097, 2), (64, 3, 5, 1), (5, 6, 7, 3),
+    # few long rows off 16-byte boundaries (split rows)
+    (3, 70001, 70003, 1), (1, 200003, 200003, 2)])
 def test_rows_fused_f32(device, oracle, rows, cols, ld, offset):
     host = oracle.normal(offset + (rows - 1) * ld + cols + 3, seed=rows * cols)
     s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, cols, ld, prologue=(0.5, 0.25))
