@@ -180,6 +180,56 @@ template <typename A> __device__ __forceinline__ A read_lane(A v, int src) {
     return __builtin_bit_cast(A, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
 
+// Lane permutations inside each row of 16 whose sources are always in range:
+// quad xor 1 (quad_perm [1,0,3,2]), quad xor 2 ([2,3,0,1]), the 8-lane
+// mirror (l <-> 7-l) and the 16-lane mirror (l <-> 15-l).
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL, typename A> __device__ __forceinline__ A dpp_permute(A v) {
+    if constexpr (sizeof(A) == 4) {
+        return dpp_move<CTRL>(v, v);
+    } else {
+        static_assert(sizeof(A) == 8, "4- or 8-byte lanes");
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = dpp_move<CTRL>((uint32_t)b, (uint32_t)b);
+        const uint32_t hi = dpp_move<CTRL>((uint32_t)(b >> 32), (uint32_t)(b >> 32));
+        return __builtin_bit_cast(A, (uint64_t)lo | ((uint64_t)hi << 32));
+    }
+}
+template <typename A> __device__ __forceinline__ A read_lane_any(A v, int src) {
+    if constexpr (sizeof(A) == 4) {
+        return read_lane(v, src);
+    } else {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = read_lane((uint32_t)b, src), hi = read_lane((uint32_t)(b >> 32), src);
+        return __builtin_bit_cast(A, (uint64_t)lo | ((uint64_t)hi << 32));
+    }
+}
+
+// Reduction over aligned groups of G lanes (G = 4, 16 or 64) with DPP moves
+// instead of LDS shuffles: quad xor 1 and 2, then (G >= 16) the 8- and
+// 16-lane mirrors, then (G = 64) the four rows of 16 read with readlane and
+// combined as (r0 . r1) . (r2 . r3).  After each DPP step every lane of the
+// sub-group holds the same bits (f is commutative), so every lane of a group
+// ends with the group's value (wave-uniform for G = 64) and the tree is fixed:
+// floating-point results are deterministic.  Every lane of the wave must be
+// active: DPP reads of disabled lanes return the reader's own value.
+template <int G, typename A, typename F> __device__ __forceinline__ A group_reduce(A v, F f) {
+    static_assert(G == 4 || G == 16 || G == 64, "groups of 4, 16 or 64 lanes");
+    v = f(v, dpp_permute<kDppQuadXor1>(v));
+    v = f(v, dpp_permute<kDppQuadXor2>(v));
+    if constexpr (G >= 16) {
+        v = f(v, dpp_permute<kDppRowHalfMirror>(v));
+        v = f(v, dpp_permute<kDppRowMirror>(v));
+    }
+    if constexpr (G == 64)
+        v = f(f(read_lane_any(v, 0), read_lane_any(v, 16)), f(read_lane_any(v, 32), read_lane_any(v, 48)));
+    return v;
+}
+
 // Inclusive scan across the 64 lanes: Hillis-Steele inside each row of 16
 // lanes (shifts 1, 2, 4, 8), then the row totals are carried forward with
 // the two row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2

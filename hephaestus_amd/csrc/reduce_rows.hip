@@ -8,14 +8,15 @@
 // a row-major matrix reduced along axis 1, neighbouring lanes are a whole
 // row apart, so no load is coalesced, and sum and max are two full passes.
 // Here:
-//   rows_kernel        one wave64 per row: lane l reads 16-byte vectors l,
-//                      l+64, ... of the row (every load instruction covers
-//                      1 KiB of contiguous memory), keeps every requested
-//                      statistic in registers, then combines them with
-//                      xor-butterflies.  Rows that do not start on a 16-byte
-//                      boundary take their 0-3 leading and trailing elements
-//                      one per lane.  Used whenever the reduced axis has
-//                      unit stride (or no stride is unit).
+//   rows_kernel        a group of G lanes per row (4 to 256, about four
+//                      16-byte vectors per lane): lane l of the group reads
+//                      vectors l, l+G, ... of the row, keeps every requested
+//                      statistic in registers, then the group combines them
+//                      with DPP reductions (and LDS across waves).  Rows that
+//                      do not start on a 16-byte boundary take their 0-3
+//                      leading and trailing elements one per lane.  Used
+//                      whenever the reduced axis has unit stride (or no
+//                      stride is unit).
 //   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
 //                      chunk statistics to partial planes.
 //   cols_tiles_kernel  the outputs are adjacent and the reduced axis strided
@@ -93,12 +94,16 @@ template <typename T, int FLAGS> struct Stats {
             mink = mink < k ? mink : k;
         }
     }
-    __device__ __forceinline__ void wave_combine() {
-        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum = wave_sum(sum);
-        if constexpr ((FLAGS & F_PROD) != 0) prod = wave_prod(prod);
-        if constexpr ((FLAGS & F_ARG) != 0) arg = wave_umax64(arg);
-        else if constexpr ((FLAGS & F_MAX) != 0) maxk = wave_umax(maxk);
-        if constexpr ((FLAGS & F_MIN) != 0) mink = wave_umin(mink);
+    // Combine the statistics of each aligned group of G lanes (4, 16 or 64)
+    // with DPP reductions; every lane of the wave must be active.
+    template <int G> __device__ __forceinline__ void group_combine() {
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum = group_reduce<G>(sum, [](S x, S y) { return x + y; });
+        if constexpr ((FLAGS & F_PROD) != 0) prod = group_reduce<G>(prod, [](Pr x, Pr y) { return x * y; });
+        if constexpr ((FLAGS & F_ARG) != 0) arg = group_reduce<G>(arg, [](uint64_t x, uint64_t y) { return umax64(x, y); });
+        else if constexpr ((FLAGS & F_MAX) != 0)
+            maxk = group_reduce<G>(maxk, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+        if constexpr ((FLAGS & F_MIN) != 0)
+            mink = group_reduce<G>(mink, [](uint32_t x, uint32_t y) { return x < y ? x : y; });
     }
     __device__ __forceinline__ void write(const RowParams &p, uint64_t r) const {
         const int64_t o = (int64_t)p.out_offset + (int64_t)r * p.out_stride;
@@ -166,67 +171,101 @@ template <typename T, int FLAGS> struct Stats {
 };
 
 // Statistics of `len` consecutive elements at `src` (unit stride, 4-byte
-// aligned), reported with global indices from `j0`.  The 0-3 elements before
-// the first 16-byte boundary go one per lane, the aligned body as 16-byte
-// vectors (lane l takes vectors l, l+64, ..., so every load instruction of
-// the wave covers 1 KiB), and the 0-3 elements after it one per lane.  Rows
-// of any length therefore stream at the aligned rate.
-template <typename T, bool AFFINE, int FLAGS>
-__device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *src, uint64_t len, uint64_t j0, int lane,
+// aligned), read by the G lanes of a row group (`gl` = lane within the group)
+// and reported with global indices from `j0`.  The 0-3 elements before the
+// first 16-byte boundary go one per lane, the aligned body as 16-byte vectors
+// (lane gl takes vectors gl, gl+G, ..., four in flight per trip), and the
+// 0-3 elements after it one per lane.
+// Rows of any length therefore stream at the aligned rate.
+template <int G, typename T, bool AFFINE, int FLAGS>
+__device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *src, uint64_t len, uint64_t j0, int gl,
                                                 float a, float b) {
     using V = typename Vec4<T>::type;
-    uint64_t head = (((uint64_t)0 - (uint64_t)(uintptr_t)src) & 15u) >> 2;
-    if (head > len) head = len;
-    if ((uint64_t)lane < head) st.visit(prologue<T, AFFINE>(src[lane], a, b), (uint32_t)(j0 + lane));
-    const V *vrow = (const V *)(src + head);
-    const uint64_t nvec = (len - head) >> 2;
-    const uint32_t jb = (uint32_t)(j0 + head);
-    uint64_t v = lane;
-    for (; v + 3 * kWave < nvec; v += 4 * kWave) {
-        V x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * kWave]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t j = jb + (uint32_t)(4 * (v + u * kWave));
-            st.visit(prologue<T, AFFINE>((T)x[u].x, a, b), j);
-            st.visit(prologue<T, AFFINE>((T)x[u].y, a, b), j + 1);
-            st.visit(prologue<T, AFFINE>((T)x[u].z, a, b), j + 2);
-            st.visit(prologue<T, AFFINE>((T)x[u].w, a, b), j + 3);
-        }
-    }
-    for (; v < nvec; v += kWave) {
-        V x = __builtin_nontemporal_load(&vrow[v]);
-        const uint32_t j = jb + (uint32_t)(4 * v);
+    auto visit4 = [&](const V &x, uint32_t j) {
         st.visit(prologue<T, AFFINE>((T)x.x, a, b), j);
         st.visit(prologue<T, AFFINE>((T)x.y, a, b), j + 1);
         st.visit(prologue<T, AFFINE>((T)x.z, a, b), j + 2);
         st.visit(prologue<T, AFFINE>((T)x.w, a, b), j + 3);
+    };
+    uint64_t head = (((uint64_t)0 - (uint64_t)(uintptr_t)src) & 15u) >> 2;
+    if (head > len) head = len;
+    if ((uint64_t)gl < head) st.visit(prologue<T, AFFINE>(src[gl], a, b), (uint32_t)(j0 + gl));
+    const V *vrow = (const V *)(src + head);
+    const uint64_t nvec = (len - head) >> 2;
+    const uint32_t jb = (uint32_t)(j0 + head);
+    // Whole trips of 4 * G vectors, then at most one trip whose loads are
+    // predicated per lane.  The trip count is the same for every lane of the
+    // group (and of the wave: all groups of a launch share the row length),
+    // so lanes never split into a 4-load path and a remainder path.
+    const uint64_t full = nvec / (4 * G);
+    uint64_t v = gl;
+    for (uint64_t k = 0; k < full; ++k, v += 4 * G) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * G]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) visit4(x[u], jb + (uint32_t)(4 * (v + u * G)));
     }
-    const uint64_t t = head + 4 * nvec + lane;
+    if (full * 4 * G < nvec) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v + u * G < nvec) x[u] = __builtin_nontemporal_load(&vrow[v + u * G]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v + u * G < nvec) visit4(x[u], jb + (uint32_t)(4 * (v + u * G)));
+    }
+    const uint64_t t = head + 4 * nvec + gl;
     if (t < len) st.visit(prologue<T, AFFINE>(src[t], a, b), (uint32_t)(j0 + t));
 }
 
-// One wave per row.  VEC: unit column stride, so lanes issue
-// global_load_dwordx4 over each row's 16-byte-aligned body.
-template <typename T, bool AFFINE, int FLAGS, bool VEC>
+// Row groups of G lanes: G = 4 or 16 puts 16 or 4 rows in each wave, G = 64
+// a wave per row, G = 128 or 256 two or four waves of the block per row.  The
+// host picks G so that each lane holds at least three 16-byte vectors of its
+// row: fewer leaves a lane too little in flight, and the per-row combine then
+// dominates.  Multi-wave groups fold per-lane partials through LDS in wave
+// order before one group reduction, so f32 sums stay deterministic.
+// Against one wave per row (the previous form), over 2^28 f32 (sum + max +
+// argmax of fmaf(.5,x,.25)), microseconds per launch by row length:
+// 4096: 156 (162); 3072: 152 (162); 2048: 160 (162); 1000: 173 (235);
+// 768: 178 (225); 512: 162 (255); 256: 171 (360); 128: 203 (680);
+// 64: 216 (1338).
+// VEC: unit column stride, so lanes issue global_load_dwordx4 over each
+// row's 16-byte-aligned body; otherwise G = 64 with one element per lane.
+template <typename T, bool AFFINE, int FLAGS, bool VEC, int G>
 __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
-    const int lane = lane_id();
-    const uint64_t wave =
-        (uint64_t)blockIdx.x * (kBlock / kWave) + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const uint64_t nwaves = (uint64_t)gridDim.x * (kBlock / kWave);
-    for (uint64_t r = wave; r < p.rows; r += nwaves) {
+    static_assert(kBlock % G == 0, "whole row groups per block");
+    constexpr int kRowsPerBlock = kBlock / G;
+    constexpr int kParts = G > kWave ? G / kWave : 1;
+    constexpr int kMaxPlanes = 4;
+    __shared__ uint64_t sh[G > kWave ? kMaxPlanes * kBlock : 1];
+    const int t = threadIdx.x;
+    const int gl = t % G;
+    uint32_t rl = (uint32_t)(t / G);
+    if constexpr (G >= kWave) rl = (uint32_t)__builtin_amdgcn_readfirstlane(rl);
+    const uint64_t r = (uint64_t)blockIdx.x * kRowsPerBlock + rl;
+    Stats<T, FLAGS> st;
+    if (r < p.rows) {
         const T *row = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
-        Stats<T, FLAGS> st;
         if constexpr (VEC) {
-            visit_unit_span<T, AFFINE, FLAGS>(st, row, p.cols, 0, lane, p.a, p.b);
+            visit_unit_span<G, T, AFFINE, FLAGS>(st, row, p.cols, 0, gl, p.a, p.b);
         } else {
-            for (uint64_t j = lane; j < p.cols; j += kWave)
+            for (uint64_t j = gl; j < p.cols; j += G)
                 st.visit(prologue<T, AFFINE>(row[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
         }
-        st.wave_combine();
-        if (lane == 0) st.write(p, r);
     }
+    if constexpr (G > kWave) {
+        // Waves other than the row's first leave right after this barrier.
+        st.store_partial(&sh[t], kBlock);
+        __syncthreads();
+        if (gl >= kWave) return;
+#pragma unroll
+        for (int k = 1; k < kParts; ++k) st.merge_partial(&sh[t + k * kWave], kBlock);
+        st.template group_combine<kWave>();
+    } else {
+        st.template group_combine<G>();
+    }
+    if (gl == 0 && r < p.rows) st.write(p, r);
 }
 
 // Column tiles (the reduced axis is strided, the outputs adjacent: axis-0
@@ -304,12 +343,12 @@ __global__ __launch_bounds__(kBlock) void rows_split_kernel(RowParams p, uint64_
     const uint64_t c1 = c0 + chunk < p.cols ? c0 + chunk : p.cols;
     Stats<T, FLAGS> st;
     if constexpr (VEC) {
-        visit_unit_span<T, AFFINE, FLAGS>(st, row + c0, c1 - c0, c0, lane, p.a, p.b);
+        visit_unit_span<kWave, T, AFFINE, FLAGS>(st, row + c0, c1 - c0, c0, lane, p.a, p.b);
     } else {
         for (uint64_t j = c0 + lane; j < c1; j += kWave)
             st.visit(prologue<T, AFFINE>(row[(int64_t)j * p.col_stride], p.a, p.b), (uint32_t)j);
     }
-    st.wave_combine();
+    st.template group_combine<kWave>();
     if (lane == 0) st.store_partial(partials + k * p.rows + r, (uint64_t)nchunks * p.rows);
 }
 
@@ -354,9 +393,29 @@ constexpr uint64_t kRowTargetWaves = 4096; // split rows when fewer than half th
 struct Shape {
     bool cols = false, vec = false;
     int V = 1;
+    int G = kWave; // lanes per row for rows_kernel
     uint64_t groups = 0, chunk = 0;
     uint32_t nchunks = 1;
 };
+
+// Lanes per row: the largest group that still gives each lane at least
+// three 16-byte vectors of the row, except that a wave per row pays for a
+// partly filled last trip more than four rows per wave lose, so 64 lanes
+// take only rows of whole 4-vector trips.  Measured over 2^28 f32 (sum, max
+// and argmax), microseconds per launch by row length and lanes per row:
+//   768: 64 -> 181, 16 -> 162     1024: 64 -> 163, 16 -> 170
+//   1280: 64 -> 166, 16 -> 158    1536: 128 -> 159, 64 -> 164
+//   3072: 256 -> 152, 128 -> 159  256: 16 -> 167, 4 -> 185
+//   192: 16 -> 190, 4 -> 204      128: 16 -> 219, 4 -> 201
+int row_group_lanes(uint64_t cols, bool vec) {
+    if (!vec) return kWave;
+    const uint64_t nvec = cols / 4;
+    if (nvec >= 3 * 256) return 256;
+    if (nvec >= 3 * 128) return 128;
+    if (nvec >= 4 * 64 && nvec % (4 * 64) == 0) return 64;
+    if (nvec >= 3 * 16) return 16;
+    return 4;
+}
 
 Shape plan_shape(const RowParams &p, bool cols_layout) {
     Shape s;
@@ -374,6 +433,7 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         }
     } else {
         s.vec = p.col_stride == 1 && base % 4 == 0;
+        s.G = row_group_lanes(p.cols, s.vec);
         if (p.rows < kRowTargetWaves / 2 && p.cols >= 2 * kMinRowChunk) {
             k = ceil_div(kRowTargetWaves, p.rows);
             const uint64_t kmax = ceil_div(p.cols, kMinRowChunk);
@@ -444,14 +504,21 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
                                stream, p, partials, s.chunk, s.nchunks);
         HX_TRY(check_launch("rows_split_kernel"));
     } else {
-        uint64_t blocks = ceil_div(p.rows, kBlock / kWave);
-        if (blocks > (1u << 20)) blocks = 1u << 20;
-        if (s.vec)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
-                               p);
+        const uint64_t blocks = ceil_div(p.rows, (uint64_t)(kBlock / s.G));
+        if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "row reduction exceeds the grid range");
+        const dim3 grid((uint32_t)blocks), block(kBlock);
+        if (!s.vec)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false, kWave>), grid, block, 0, stream, p);
+        else if (s.G == 256)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 256>), grid, block, 0, stream, p);
+        else if (s.G == 128)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 128>), grid, block, 0, stream, p);
+        else if (s.G == 64)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 64>), grid, block, 0, stream, p);
+        else if (s.G == 16)
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 16>), grid, block, 0, stream, p);
         else
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
-                               p);
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 4>), grid, block, 0, stream, p);
         return check_launch("rows_kernel");
     }
     if (!split) return HX_OK;

@@ -208,6 +208,29 @@ def test_rows_fused_f32(device, oracle, rows, cols, ld, offset):
     assert np.all(np.abs(gs.astype(np.float64) - s_ref) <= bound)
 
 
+# Row lengths either side of every lanes-per-row threshold (4, 16, 64, 128 and
+# 256 lanes, about four 16-byte vectors per lane), with 67 rows so the last
+# block of the 4- and 16-lane forms is partly empty, and starts off 16-byte
+# boundaries (offset 1, row stride cols + 1).
+@pytest.mark.parametrize("cols", [1, 2, 3, 15, 16, 17, 63, 64, 65, 255, 256, 257, 1023, 1024, 1025,
+                                  2047, 2048, 2049, 4095, 4096, 4097, 8191])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_rows_fused_across_group_sizes(device, oracle, cols, aligned):
+    rows = 67
+    ld, offset = (cols, 0) if aligned else (cols + 1, 1)
+    host = oracle.normal(offset + (rows - 1) * ld + cols, seed=cols + 7)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, cols, ld, prologue=(0.5, 0.25))
+    buf = device.upload(host)
+    s = device.alloc_zeroed(np.float32, rows)
+    m = device.alloc_zeroed(np.float32, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    AXIS.reduce_rows_fused(device, buf, rows, cols, ld, offset, (0.5, 0.25), s, m, i)
+    assert np.array_equal(device.download_owned(i), i_ref)
+    assert np.array_equal(device.download_owned(m).view(np.uint32), m_ref.view(np.uint32))
+    bound = np.array([f32_bound(cols, a) for a in a_ref])
+    assert np.all(np.abs(device.download_owned(s).astype(np.float64) - s_ref) <= bound)
+
+
 @pytest.mark.parametrize("dtype", [np.uint32, np.int32])
 def test_rows_fused_integers(device, oracle, dtype):
     rows, cols = 300, 777
