@@ -5,7 +5,9 @@
 // contiguous chunk serially, lane 0 folds the chunk totals, and a second sweep
 // re-reads and re-writes the output (core accelerator/scan.rs:56-155).  A 1-D
 // scan of 2^28 elements therefore runs on one CU.  Here every line is cut
-// into tiles of 32768 elements that all CUs process in a single pass:
+// into tiles that all CUs process in a single pass (32768 elements for long
+// lines; a line of up to 32768 elements is one tile of the smallest shape
+// that holds it, see tile_shape):
 //
 //   * block b scans tile b.  The tile is loaded with 16-byte vectors,
 //     wave-striped: step j of wave w holds 256 contiguous elements, lane l
@@ -47,9 +49,8 @@ namespace hx {
 namespace {
 
 constexpr int kBlock = 256;                          // column-scan kernels
-constexpr int kWaves = 8;                            // waves per tile block
-constexpr int kSteps = 16;                           // 16-byte vectors per lane
-constexpr int kTile = kWaves * kWave * 4 * kSteps;   // 32768 elements
+constexpr int kWaves = 8;                            // waves per tile block (long lines)
+constexpr int kSteps = 16;                           // 16-byte vectors per lane (long lines)
 constexpr int kSuper = 64;                           // tiles per superblock
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a missing value
@@ -1148,20 +1149,57 @@ hx_status launch_column(const ScanParams &p, const ColShape &s, bool rev, void *
 // One 64-bit word per entry (packed u32), four per entry (split f64).
 uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 32 : 8); }
 
+// Tile shapes (waves x 16-byte steps per lane).  A line up to 32768
+// elements is one tile: the smallest shape that holds it, so a block never
+// carries idle waves and a row-wise scan needs no look-back.  Longer lines
+// take 8 x 16 tiles chained by the look-back.  Measured on 2^28 u32 (f32)
+// inclusive scans as 65536 x 4096: 1316 us (2329) with 8 x 16 tiles, whose
+// waves 1-7 held no elements, against 334 (333) with 4 x 4; 262144 x 1024:
+// 3404 (6047) against 331 (339) with 2 x 2; 16384 x 16384: 4 x 16 360 us,
+// 8 x 8 410.
+struct TileShape {
+    int waves, steps;
+    uint64_t elems() const { return (uint64_t)waves * kWave * 4 * steps; }
+};
+inline TileShape tile_shape(uint64_t len) {
+    if (len <= 1024) return {2, 2};
+    if (len <= 2048) return {2, 4};
+    if (len <= 4096) return {4, 4};
+    if (len <= 8192) return {4, 8};
+    if (len <= 16384) return {4, 16};
+    return {kWaves, kSteps};
+}
+
+template <typename T, typename Op, typename Status, bool EXCL, int STEPS, int WAVES>
+hx_status launch_tiles_shaped(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
+                              hipStream_t stream) {
+    const dim3 grid((uint32_t)p.total_tiles), block(WAVES * kWave);
+    if (vec && rev)
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true, STEPS, true, WAVES>), grid, block, 0,
+                           stream, p, st, st1);
+    else if (vec)
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false, STEPS, true, WAVES>), grid, block, 0,
+                           stream, p, st, st1);
+    else if (rev)
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true, STEPS, true, WAVES>), grid, block, 0,
+                           stream, p, st, st1);
+    else
+        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false, STEPS, true, WAVES>), grid, block, 0,
+                           stream, p, st, st1);
+    return check_launch("scan_tiles_kernel");
+}
+
 template <typename T, typename Op, typename Status, bool EXCL>
 hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
-                       hipStream_t stream) {
-    const dim3 grid((uint32_t)p.total_tiles), block(kWaves * kWave);
-    if (vec && rev)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true>), grid, block, 0, stream, p, st, st1);
-    else if (vec)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false>), grid, block, 0, stream, p, st, st1);
-    else if (rev)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true>), grid, block, 0, stream, p, st, st1);
-    else
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false>), grid, block, 0, stream, p, st,
-                           st1);
-    return check_launch("scan_tiles_kernel");
+                       const TileShape &shape, hipStream_t stream) {
+    switch (shape.waves * 100 + shape.steps) {
+    case 202: return launch_tiles_shaped<T, Op, Status, EXCL, 2, 2>(p, st, st1, vec, rev, stream);
+    case 204: return launch_tiles_shaped<T, Op, Status, EXCL, 4, 2>(p, st, st1, vec, rev, stream);
+    case 404: return launch_tiles_shaped<T, Op, Status, EXCL, 4, 4>(p, st, st1, vec, rev, stream);
+    case 408: return launch_tiles_shaped<T, Op, Status, EXCL, 8, 4>(p, st, st1, vec, rev, stream);
+    case 416: return launch_tiles_shaped<T, Op, Status, EXCL, 16, 4>(p, st, st1, vec, rev, stream);
+    default: return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
+    }
 }
 
 uint64_t scan_bytes(const ScanArgs &a) {
@@ -1170,7 +1208,7 @@ uint64_t scan_bytes(const ScanArgs &a) {
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
     }
     if (column_mode(a)) return column_bytes(a);
-    const uint64_t tpl = ceil_div(a.len, kTile);
+    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len).elems());
     const bool f64 = a.dtype == HX_DTYPE_F32;
     return kLookbackOffset + status_bytes(tpl * a.lines, f64) + status_bytes(ceil_div(tpl, kSuper) * a.lines, f64);
 }
@@ -1182,7 +1220,8 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out = a.out;
     p.lines = a.lines;
     p.len = a.len;
-    p.tiles_per_line = ceil_div(a.len, kTile);
+    const TileShape shape = tile_shape(a.len);
+    p.tiles_per_line = ceil_div(a.len, shape.elems());
     p.total_tiles = p.tiles_per_line * a.lines;
     p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);
     p.in_line_stride = a.in_line_stride;
@@ -1232,12 +1271,12 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     hx_status s;
     if constexpr (std::is_same<T, float>::value) {
         F64Status st{level0}, st1{level1};
-        s = a.exclusive ? launch_tiles<T, Op, F64Status, true>(p, st, st1, vec, a.reverse, stream)
-                        : launch_tiles<T, Op, F64Status, false>(p, st, st1, vec, a.reverse, stream);
+        s = a.exclusive ? launch_tiles<T, Op, F64Status, true>(p, st, st1, vec, a.reverse, shape, stream)
+                        : launch_tiles<T, Op, F64Status, false>(p, st, st1, vec, a.reverse, shape, stream);
     } else {
         PackedStatus st{level0}, st1{level1};
-        s = a.exclusive ? launch_tiles<T, Op, PackedStatus, true>(p, st, st1, vec, a.reverse, stream)
-                        : launch_tiles<T, Op, PackedStatus, false>(p, st, st1, vec, a.reverse, stream);
+        s = a.exclusive ? launch_tiles<T, Op, PackedStatus, true>(p, st, st1, vec, a.reverse, shape, stream)
+                        : launch_tiles<T, Op, PackedStatus, false>(p, st, st1, vec, a.reverse, shape, stream);
     }
     if (s == HX_OK) commit_lookback_launch(lb);
     return s;

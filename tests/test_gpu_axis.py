@@ -250,6 +250,27 @@ def test_column_scan(device, oracle, shape, dtype, op, reverse, kind):
                     seed=r * 7 + c)
 
 
+# Row-wise (axis 1) scans of many lines: a line of up to 32768 elements is one
+# tile of the smallest shape that holds it (1024, 2048, 4096, 8192, 16384 or
+# 32768 elements), longer lines chain 32768-element tiles.  Lengths either
+# side of every boundary; "misaligned" rows (stride cols + 1, offset 1) take
+# the scalar path of each shape.
+ROW_SCAN_SHAPES = [(67, 1024), (67, 1025), (33, 2048), (33, 2049), (17, 4096), (17, 4100), (9, 8192),
+                   (9, 8193), (5, 16384), (5, 16385), (3, 32769), (130, 3)]
+ROW_SCAN_VARIANTS = [("sum", False, False, True), ("sum", True, True, True), ("prod", False, False, True),
+                     ("sum", False, True, False), ("sum", True, False, False)]
+
+
+@pytest.mark.parametrize("variant", ROW_SCAN_VARIANTS, ids=lambda v: "-".join(map(str, v)))
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("shape", ROW_SCAN_SHAPES)
+def test_row_scan_tile_shapes(device, oracle, shape, dtype, variant):
+    op, exclusive, reverse, aligned = variant
+    r, c = shape
+    strides, offset = ((c, 1), 0) if aligned else ((c + 1, 1), 1)
+    run_column_scan(device, oracle, op, dtype, shape, strides, offset, 1, exclusive, reverse, seed=r * 5 + c)
+
+
 @pytest.mark.parametrize("op", ["sum", "prod"])
 def test_column_scan_transposed_and_reversed_lines(device, oracle, op):
     # column-major view: axis 1 strided, lines adjacent
