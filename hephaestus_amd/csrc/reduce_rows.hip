@@ -96,14 +96,18 @@ template <typename T, int FLAGS> struct Stats {
     }
     // Combine the statistics of each aligned group of G lanes (4, 16 or 64)
     // with DPP reductions; every lane of the wave must be active.
+    // G = 1 (a thread per row) has nothing to combine.
     template <int G> __device__ __forceinline__ void group_combine() {
-        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum = group_reduce<G>(sum, [](S x, S y) { return x + y; });
-        if constexpr ((FLAGS & F_PROD) != 0) prod = group_reduce<G>(prod, [](Pr x, Pr y) { return x * y; });
-        if constexpr ((FLAGS & F_ARG) != 0) arg = group_reduce<G>(arg, [](uint64_t x, uint64_t y) { return umax64(x, y); });
-        else if constexpr ((FLAGS & F_MAX) != 0)
-            maxk = group_reduce<G>(maxk, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
-        if constexpr ((FLAGS & F_MIN) != 0)
-            mink = group_reduce<G>(mink, [](uint32_t x, uint32_t y) { return x < y ? x : y; });
+        if constexpr (G > 1) {
+            if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum = group_reduce<G>(sum, [](S x, S y) { return x + y; });
+            if constexpr ((FLAGS & F_PROD) != 0) prod = group_reduce<G>(prod, [](Pr x, Pr y) { return x * y; });
+            if constexpr ((FLAGS & F_ARG) != 0)
+                arg = group_reduce<G>(arg, [](uint64_t x, uint64_t y) { return umax64(x, y); });
+            else if constexpr ((FLAGS & F_MAX) != 0)
+                maxk = group_reduce<G>(maxk, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+            if constexpr ((FLAGS & F_MIN) != 0)
+                mink = group_reduce<G>(mink, [](uint32_t x, uint32_t y) { return x < y ? x : y; });
+        }
     }
     __device__ __forceinline__ void write(const RowParams &p, uint64_t r) const {
         const int64_t o = (int64_t)p.out_offset + (int64_t)r * p.out_stride;
@@ -151,6 +155,25 @@ template <typename T, int FLAGS> struct Stats {
         if constexpr ((FLAGS & F_MIN) != 0) w[(q++) * plane] = mink;
         (void)q;
     }
+    // Fold another lane's (or component's) statistics into these.
+    __device__ __forceinline__ void merge(const Stats &o) {
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) sum += o.sum;
+        if constexpr ((FLAGS & F_PROD) != 0) prod *= o.prod;
+        if constexpr ((FLAGS & F_ARG) != 0) arg = umax64(arg, o.arg);
+        else if constexpr ((FLAGS & F_MAX) != 0) maxk = maxk > o.maxk ? maxk : o.maxk;
+        if constexpr ((FLAGS & F_MIN) != 0) mink = mink < o.mink ? mink : o.mink;
+    }
+    // These statistics combined with lane (lane ^ m)'s; both lanes end with
+    // the same bits (every combination is commutative).
+    __device__ __forceinline__ void merge_xor(int m) {
+        Stats o;
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) o.sum = __shfl_xor(sum, m, kWave);
+        if constexpr ((FLAGS & F_PROD) != 0) o.prod = __shfl_xor(prod, m, kWave);
+        if constexpr ((FLAGS & F_ARG) != 0) o.arg = __shfl_xor(arg, m, kWave);
+        else if constexpr ((FLAGS & F_MAX) != 0) o.maxk = __shfl_xor(maxk, m, kWave);
+        if constexpr ((FLAGS & F_MIN) != 0) o.mink = __shfl_xor(mink, m, kWave);
+        merge(o);
+    }
     // Fold a later chunk's partial into this one.
     __device__ __forceinline__ void merge_partial(const uint64_t *w, uint64_t plane) {
         int q = 0;
@@ -189,7 +212,7 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
     };
     uint64_t head = (((uint64_t)0 - (uint64_t)(uintptr_t)src) & 15u) >> 2;
     if (head > len) head = len;
-    if ((uint64_t)gl < head) st.visit(prologue<T, AFFINE>(src[gl], a, b), (uint32_t)(j0 + gl));
+    for (uint64_t h = gl; h < head; h += G) st.visit(prologue<T, AFFINE>(src[h], a, b), (uint32_t)(j0 + h));
     const V *vrow = (const V *)(src + head);
     const uint64_t nvec = (len - head) >> 2;
     const uint32_t jb = (uint32_t)(j0 + head);
@@ -215,12 +238,13 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
         for (int u = 0; u < 4; ++u)
             if (v + u * G < nvec) visit4(x[u], jb + (uint32_t)(4 * (v + u * G)));
     }
-    const uint64_t t = head + 4 * nvec + gl;
-    if (t < len) st.visit(prologue<T, AFFINE>(src[t], a, b), (uint32_t)(j0 + t));
+    for (uint64_t t = head + 4 * nvec + gl; t < len; t += G)
+        st.visit(prologue<T, AFFINE>(src[t], a, b), (uint32_t)(j0 + t));
 }
 
-// Row groups of G lanes: G = 4 or 16 puts 16 or 4 rows in each wave, G = 64
-// a wave per row, G = 128 or 256 two or four waves of the block per row.  The
+// Row groups of G lanes: G = 1 is a thread per row (rows of fewer than 16
+// elements), G = 4 or 16 puts 16 or 4 rows in each wave, G = 64 a wave per
+// row, G = 128 or 256 two or four waves of the block per row.  The
 // host picks G so that each lane holds at least three 16-byte vectors of its
 // row: fewer leaves a lane too little in flight, and the per-row combine then
 // dominates.  Multi-wave groups fold per-lane partials through LDS in wave
@@ -328,6 +352,80 @@ __global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_
     }
 }
 
+// Narrow column reductions: axis 0 of a dense row-major [R, C] matrix with
+// C a power of two from 2 to 32.  The matrix is one contiguous range; with
+// 16-byte vectors v = lane + 64 t (chunks start on multiples of 64 vectors),
+// component k of lane l's vector always lands in column (4 l + k) mod C, so
+// each lane keeps four statistics -- one per component -- and every load is a
+// coalesced 1 KiB wave access.  The column-tile form gave such matrices one
+// live lane per wave (65536^2 x 4 f32: 5.0 ms).  A wave owns a chunk of the
+// range; at its end components of the same column fold (C = 2), then lanes
+// of the same columns fold with xor butterflies from mask 32 down to C/4, and
+// lanes l < C/4 (lane 0 for C = 2) hold columns 4l..4l+3.  Chunk statistics
+// go to the partial planes that split_fold_kernel folds in chunk order.
+template <typename T, int FLAGS>
+__global__ __launch_bounds__(kBlock) void cols_narrow_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
+                                                             uint32_t nchunks) {
+    using V = typename Vec4<T>::type;
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= nchunks) return; // uniform across the wave
+    const int lane = lane_id();
+    const uint32_t C = (uint32_t)p.rows;
+    const uint32_t shift = (uint32_t)__builtin_ctz(C);
+    const V *src = (const V *)((const T *)p.base + p.offset);
+    const uint64_t nvec = (p.cols * C) >> 2;
+    const uint64_t v0 = w * chunk;
+    const uint64_t v1 = v0 + chunk < nvec ? v0 + chunk : nvec;
+    Stats<T, FLAGS> st[4];
+    auto visit4 = [&](const V &x, uint64_t vv) {
+        const uint64_t e = 4 * vv;
+        st[0].visit((T)x.x, (uint32_t)(e >> shift));
+        st[1].visit((T)x.y, (uint32_t)((e + 1) >> shift));
+        st[2].visit((T)x.z, (uint32_t)((e + 2) >> shift));
+        st[3].visit((T)x.w, (uint32_t)((e + 3) >> shift));
+    };
+    // Whole trips of 256 vectors, then one trip with per-lane predicates: the
+    // trip count is the same for every lane.
+    const uint64_t full = (v1 - v0) / (4 * kWave);
+    uint64_t v = v0 + lane;
+    for (uint64_t t = 0; t < full; ++t, v += 4 * kWave) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&src[v + u * kWave]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) visit4(x[u], v + u * kWave);
+    }
+    if (v0 + full * 4 * kWave < v1) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v + u * kWave < v1) x[u] = __builtin_nontemporal_load(&src[v + u * kWave]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v + u * kWave < v1) visit4(x[u], v + u * kWave);
+    }
+    if (C == 2) {
+        st[0].merge(st[2]);
+        st[1].merge(st[3]);
+    }
+    const int lowest = C >= 4 ? (int)(C / 4) : 1;
+    for (int m = kWave / 2; m >= lowest; m >>= 1)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) st[k].merge_xor(m);
+    const int owners = C >= 4 ? (int)(C / 4) : 1;
+    if (lane >= owners) return;
+    const int ncomp = C >= 4 ? 4 : (int)C;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k >= ncomp) break;
+        const uint64_t col = (uint64_t)(4 * lane + k);
+        if (nchunks > 1)
+            st[k].store_partial(partials + w * C + col, (uint64_t)nchunks * C);
+        else
+            st[k].write(p, col);
+    }
+}
+
 // Few long rows (the reduced axis has unit stride but there are too few rows
 // to give every CU work): one wave per (row, chunk of 256-element multiples),
 // lanes along the chunk as in rows_kernel, partials to the planes.
@@ -389,9 +487,18 @@ constexpr uint64_t kTargetWaves = 2048;
 constexpr uint64_t kMinColChunk = 32;    // lines per column-tile chunk
 constexpr uint64_t kMinRowChunk = 8192;  // elements per split-row chunk
 constexpr uint64_t kRowTargetWaves = 4096; // split rows when fewer than half this many
+constexpr uint64_t kMinNarrowChunk = 4096; // 16-byte vectors per narrow-column chunk
+
+// Axis 0 of a dense row-major matrix with 2 to 32 columns (a power of two),
+// 16-byte aligned, whole vectors: the narrow-column form.
+bool narrow_columns(const RowParams &p, uintptr_t base) {
+    const uint64_t c = p.rows;
+    return c >= 2 && c <= 32 && (c & (c - 1)) == 0 && p.row_stride == 1 && p.col_stride == (int64_t)c &&
+           base % 16 == 0 && (p.cols * c) % 4 == 0 && p.cols <= 0xFFFFFFFFull;
+}
 
 struct Shape {
-    bool cols = false, vec = false;
+    bool cols = false, vec = false, narrow = false;
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
     uint64_t groups = 0, chunk = 0;
@@ -414,7 +521,8 @@ int row_group_lanes(uint64_t cols, bool vec) {
     if (nvec >= 3 * 128) return 128;
     if (nvec >= 4 * 64 && nvec % (4 * 64) == 0) return 64;
     if (nvec >= 3 * 16) return 16;
-    return 4;
+    if (nvec >= 4) return 4;
+    return 1;
 }
 
 Shape plan_shape(const RowParams &p, bool cols_layout) {
@@ -422,6 +530,17 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
     s.cols = cols_layout;
     const uintptr_t base = (uintptr_t)p.base + 4u * p.offset; // every element type is 4 bytes
     uint64_t k = 1;
+    if (cols_layout && narrow_columns(p, base)) {
+        // Chunks of whole 256-vector trips, about kTargetWaves of them.
+        s.narrow = true;
+        const uint64_t nvec = (p.cols * p.rows) >> 2;
+        uint64_t chunk = ceil_div(nvec, kTargetWaves);
+        if (chunk < kMinNarrowChunk) chunk = kMinNarrowChunk;
+        chunk = ceil_div(chunk, 4 * kWave) * 4 * kWave;
+        s.chunk = chunk;
+        s.nchunks = (uint32_t)ceil_div(nvec, chunk);
+        return s;
+    }
     if (cols_layout) {
         s.vec = p.row_stride == 1 && p.rows % 4 == 0 && base % 16 == 0 && p.col_stride % 4 == 0;
         s.V = s.vec ? 4 : 1;
@@ -472,7 +591,12 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
     if (split && ws_bytes < shape_bytes(p, s, FLAGS))
         return fail(HX_ERR_DISPATCH_FAILED, "axis reduction workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);
-    if (cols_layout) {
+    if (s.narrow) {
+        const uint64_t blocks = ceil_div((uint64_t)s.nchunks, kBlock / kWave);
+        hipLaunchKernelGGL((cols_narrow_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
+                           s.chunk, s.nchunks);
+        HX_TRY(check_launch("cols_narrow_kernel"));
+    } else if (cols_layout) {
         const uint64_t waves = s.groups * s.nchunks;
         const uint64_t blocks = ceil_div(waves, kBlock / kWave);
         if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");
@@ -517,8 +641,10 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
             hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 64>), grid, block, 0, stream, p);
         else if (s.G == 16)
             hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 16>), grid, block, 0, stream, p);
-        else
+        else if (s.G == 4)
             hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 4>), grid, block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 1>), grid, block, 0, stream, p);
         return check_launch("rows_kernel");
     }
     if (!split) return HX_OK;

@@ -1263,8 +1263,10 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     const uintptr_t obase = (uintptr_t)((T *)a.out + a.out_offset);
     // Reverse scans vectorise their whole tiles as mirrored blocks, which
     // stay 16-byte aligned when the line length is a multiple of 4.
-    const bool vec = contiguous && ibase % 16 == 0 && obase % 16 == 0 && a.in_line_stride % 4 == 0 &&
-                     a.out_line_stride % 4 == 0 && (!a.reverse || a.len % 4 == 0);
+    // A single line's stride is never used (an [N, 1] view scanned along
+    // axis 0 is one contiguous line).
+    const bool strides4 = a.lines == 1 || (a.in_line_stride % 4 == 0 && a.out_line_stride % 4 == 0);
+    const bool vec = contiguous && ibase % 16 == 0 && obase % 16 == 0 && strides4 && (!a.reverse || a.len % 4 == 0);
     const bool f64 = std::is_same<T, float>::value;
     uint64_t *level0 = (uint64_t *)((char *)ws + kLookbackOffset);
     uint64_t *level1 = (uint64_t *)((char *)level0 + status_bytes(p.total_tiles, f64));

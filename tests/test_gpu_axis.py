@@ -106,7 +106,12 @@ def host_for(oracle, dtype, n, seed, op):
 # (rows, cols), axis: tall column tiles (vector and scalar lanes), a single
 # chunk, few long rows (vector and scalar), and a [N,1] column.
 SHAPES = [((4099, 1000), 0), ((3001, 999), 0), ((20, 256), 0), ((3, 100003), 1), ((5, 65536), 1),
-          ((100000, 1), 0)]
+          ((100000, 1), 0),
+          # narrow columns (2 to 32, powers of two): one range of whole vectors,
+          # several chunks for the tall ones; 2 columns x odd rows is not whole
+          # vectors and takes the column tiles
+          ((1048577, 4), 0), ((70001, 8), 0), ((5000, 16), 0), ((3001, 32), 0), ((4096, 2), 0), ((4097, 2), 0),
+          ((1, 4), 0)]
 
 
 @pytest.mark.parametrize("op", list(OPS))
@@ -132,6 +137,16 @@ def test_axis_reduce_transposed_and_reversed_views(device, oracle, op):
     shape, strides, offset = (r, c), (c, -1), c - 1
     got = run_axis(device, op, np.float32, host, shape, strides, offset, 0)
     check(oracle, op, np.float32, got, lines_of(host, shape, strides, offset, 0))
+
+
+@pytest.mark.parametrize("op", ["sum", "argmax", "min"])
+@pytest.mark.parametrize("offset", [4, 1])
+def test_narrow_columns_offset_views(device, oracle, op, offset):
+    # offset 4 keeps the range 16-byte aligned (narrow form), offset 1 does not
+    r, c = 30001, 8
+    host = host_for(oracle, np.float32, offset + r * c, seed=offset, op=op)
+    got = run_axis(device, op, np.float32, host, (r, c), (c, 1), offset, 0)
+    check(oracle, op, np.float32, got, lines_of(host, (r, c), (c, 1), offset, 0))
 
 
 def test_split_f32_sums_are_deterministic(device, oracle):

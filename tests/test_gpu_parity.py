@@ -430,7 +430,9 @@ def test_scan_f32_products_within_gamma(device, oracle, n, direction, kind):
 
 
 @pytest.mark.parametrize("shape,axis", [((512, 4096), 1), ((3, 10000), 1), ((4096, 300), 0), ((40, 7), 0),
-                                        ((1000, 1001), 1), ((257, 5), 1)])
+                                        ((1000, 1001), 1), ((257, 5), 1),
+                                        # one line along axis 0 (line stride 1, unused): vector path
+                                        ((100000, 1), 0), ((100003, 1), 0)])
 def test_scan_rank2_lines(device, oracle, shape, axis):
     r, c = shape
     host = oracle.uniform_int(r * c, seed=r + c, lo=-1000, hi=1000, dtype=np.int32)
