@@ -1156,12 +1156,15 @@ uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 32 :
 // inclusive scans as 65536 x 4096: 1316 us (2329) with 8 x 16 tiles, whose
 // waves 1-7 held no elements, against 334 (333) with 4 x 4; 262144 x 1024:
 // 3404 (6047) against 331 (339) with 2 x 2; 16384 x 16384: 4 x 16 360 us,
-// 8 x 8 410.
+// 8 x 8 410; 1048576 x 256: 1 x 1 351 us, 2 x 2 636; 524288 x 512: 1 x 2
+// 339, 2 x 2 434.
 struct TileShape {
     int waves, steps;
     uint64_t elems() const { return (uint64_t)waves * kWave * 4 * steps; }
 };
 inline TileShape tile_shape(uint64_t len) {
+    if (len <= 256) return {1, 1};
+    if (len <= 512) return {1, 2};
     if (len <= 1024) return {2, 2};
     if (len <= 2048) return {2, 4};
     if (len <= 4096) return {4, 4};
@@ -1193,6 +1196,8 @@ template <typename T, typename Op, typename Status, bool EXCL>
 hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
                        const TileShape &shape, hipStream_t stream) {
     switch (shape.waves * 100 + shape.steps) {
+    case 101: return launch_tiles_shaped<T, Op, Status, EXCL, 1, 1>(p, st, st1, vec, rev, stream);
+    case 102: return launch_tiles_shaped<T, Op, Status, EXCL, 2, 1>(p, st, st1, vec, rev, stream);
     case 202: return launch_tiles_shaped<T, Op, Status, EXCL, 2, 2>(p, st, st1, vec, rev, stream);
     case 204: return launch_tiles_shaped<T, Op, Status, EXCL, 4, 2>(p, st, st1, vec, rev, stream);
     case 404: return launch_tiles_shaped<T, Op, Status, EXCL, 4, 4>(p, st, st1, vec, rev, stream);

@@ -266,12 +266,13 @@ def test_column_scan(device, oracle, shape, dtype, op, reverse, kind):
 
 
 # Row-wise (axis 1) scans of many lines: a line of up to 32768 elements is one
-# tile of the smallest shape that holds it (1024, 2048, 4096, 8192, 16384 or
-# 32768 elements), longer lines chain 32768-element tiles.  Lengths either
+# tile of the smallest shape that holds it (256, 512, 1024, 2048, 4096, 8192,
+# 16384 or 32768 elements), longer lines chain 32768-element tiles.  Lengths either
 # side of every boundary; "misaligned" rows (stride cols + 1, offset 1) take
 # the scalar path of each shape.
-ROW_SCAN_SHAPES = [(67, 1024), (67, 1025), (33, 2048), (33, 2049), (17, 4096), (17, 4100), (9, 8192),
-                   (9, 8193), (5, 16384), (5, 16385), (3, 32769), (130, 3)]
+ROW_SCAN_SHAPES = [(300, 256), (300, 257), (130, 512), (130, 513), (67, 1024), (67, 1025), (33, 2048),
+                   (33, 2049), (17, 4096), (17, 4100), (9, 8192), (9, 8193), (5, 16384), (5, 16385), (3, 32769),
+                   (130, 3)]
 ROW_SCAN_VARIANTS = [("sum", False, False, True), ("sum", True, True, True), ("prod", False, False, True),
                      ("sum", False, True, False), ("sum", True, False, False)]
 
