@@ -27,25 +27,26 @@ __global__ __launch_bounds__(kTileWaves * kWave) void copy_tiles_kernel(const ch
     const uint64_t base = (uint64_t)blockIdx.x * kTileBytes;
     const uint32_t lane_off =
         ((uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave * kTileSteps + lane_id()) * 16u;
-    u32x4 v[kTileSteps];
+    u32x4_a4 v[kTileSteps];
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j)
-        v[j] = load_vec<true>((const u32x4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
+        v[j] = load_vec<true>((const u32x4_a4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j)
-        store_vec<true>(v[j], (u32x4 *)(dst + base + lane_off + (uint32_t)j * (kWave * 16)));
+        store_vec<true>(v[j], (u32x4_a4 *)(dst + base + lane_off + (uint32_t)j * (kWave * 16)));
 }
 
-// 16-byte body (both pointers 16-byte aligned), two vectors in flight per
-// lane, grid-stride; the tail (< 16 bytes) is copied bytewise.
-__global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4 *src, u32x4 *dst, uint64_t nvec,
+// 16-byte body (both pointers 4-byte aligned: the vectors need no more),
+// two vectors in flight per lane, grid-stride; the tail (< 16 bytes) is
+// copied bytewise.
+__global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4_a4 *src, u32x4_a4 *dst, uint64_t nvec,
                                                           const uint8_t *src_tail, uint8_t *dst_tail,
                                                           uint32_t tail) {
     const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
     uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
     for (; i + nthreads < nvec; i += 2 * nthreads) {
-        const u32x4 a = load_vec<true>(&src[i]);
-        const u32x4 b = load_vec<true>(&src[i + nthreads]);
+        const u32x4_a4 a = load_vec<true>(&src[i]);
+        const u32x4_a4 b = load_vec<true>(&src[i + nthreads]);
         store_vec<true>(a, &dst[i]);
         store_vec<true>(b, &dst[i + nthreads]);
     }
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4 *src, u32x
     if (blockIdx.x == 0 && threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
 
-// Unaligned pointers: bytewise, grid-stride.
+// Pointers off a 4-byte boundary: bytewise, grid-stride.
 __global__ __launch_bounds__(kBlock) void copy_bytes_kernel(const uint8_t *src, uint8_t *dst, uint64_t bytes) {
     const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
     for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < bytes; i += nthreads) dst[i] = src[i];
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(kBlock) void copy_bytes_kernel(const uint8_t *src, 
 
 hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
     if (bytes == 0) return ok();
-    const bool aligned = (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
+    const bool aligned = (((uintptr_t)src | (uintptr_t)dst) & 3u) == 0; // 16-byte vectors at 4-byte alignment
     if (aligned) {
         const uint64_t tiles = bytes / kTileBytes;
         if (tiles >= 0x80000000ull)
@@ -84,8 +85,8 @@ hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t st
         if (blocks < 1) blocks = 1;
         const char *s0 = (const char *)src + done;
         char *d0 = (char *)dst + done;
-        hipLaunchKernelGGL(copy_vec_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, (const u32x4 *)s0,
-                           (u32x4 *)d0, nvec, (const uint8_t *)s0 + nvec * 16, (uint8_t *)d0 + nvec * 16, tail);
+        hipLaunchKernelGGL(copy_vec_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, (const u32x4_a4 *)s0,
+                           (u32x4_a4 *)d0, nvec, (const uint8_t *)s0 + nvec * 16, (uint8_t *)d0 + nvec * 16, tail);
         return check_launch("copy_vec_kernel");
     }
     uint64_t blocks = ceil_div(bytes, kBlock);

@@ -60,11 +60,10 @@ hx_status plan_map(hx_map_reduction map, hx_dtype dtype, const void *a, uint64_t
     // The order of a sum does not change its value here (exact integer
     // arithmetic; f64 accumulation of exact f32 products), so dense views
     // are streamed with vector loads.  For a dot both operands must be dense
-    // row-major and agree in 16-byte phase.
+    // row-major; their vector loads need only 4-byte alignment, so the two
+    // may start at any element offsets.
     bool flat = layout_is_c_contiguous(*a_layout);
-    if (map == HX_MAP_DOT)
-        flat = flat && layout_is_c_contiguous(*b_layout) &&
-               ((((uintptr_t)a + a_layout->offset * 4) - ((uintptr_t)b + b_layout->offset * 4)) & 15u) == 0;
+    if (map == HX_MAP_DOT) flat = flat && layout_is_c_contiguous(*b_layout);
     args->flat = flat;
     args->out = out;
     return HX_OK;

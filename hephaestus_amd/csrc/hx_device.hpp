@@ -16,6 +16,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <typename T> struct Vec4 { using type = u32x4; };
 template <> struct Vec4<float> { using type = f32x4; };
+// The same 16-byte vectors at 4-byte alignment: global_load_dwordx4 and
+// global_store_dwordx4 accept any dword-aligned address (the compiler emits
+// the same instruction), so a line that starts off a 16-byte boundary still
+// moves one 16-byte vector per lane and instruction.
+typedef float f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+template <typename T> struct Vec4A4 { using type = u32x4_a4; };
+template <> struct Vec4A4<float> { using type = f32x4_a4; };
 
 // Vector loads/stores; NT marks them non-temporal (streamed through, not
 // retained in the caches).

@@ -103,12 +103,14 @@ template <typename P> __device__ __forceinline__ typename P::Acc block_reduce(ty
 }
 
 // FLAT: both operands are the contiguous ranges [a_off, +n) and [b_off, +n)
-// whose addresses agree mod 16 bytes (b is ignored for one-operand maps).
+// (b is ignored for one-operand maps).  The head peel aligns a; b's vectors
+// need only 4-byte alignment (Vec4A4), so the operands may sit at any element
+// offsets from each other.
 template <typename T, int M, bool FLAT>
 __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
     using P = MapPolicy<T, M>;
     using Acc = typename P::Acc;
-    using V = typename Vec4<T>::type;
+    using V = typename Vec4A4<T>::type;
     constexpr bool kTwo = M == kMapDot;
     __shared__ Acc lds[kBlock / kWave];
     const uint64_t n = p.n;

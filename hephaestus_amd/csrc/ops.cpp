@@ -216,8 +216,8 @@ hx_status plan_segmented(hx_op op, hx_dtype dtype, const void *values, uint64_t 
     if (segments > 0 && !out) return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce output is null");
     if (aliases(out, values) || aliases(out, offsets))
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce output must not alias its inputs");
-    if (((uintptr_t)values) % 16 != 0)
-        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 16-byte aligned");
+    if (((uintptr_t)values) % 4 != 0)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 4-byte aligned");
     *a = SegmentedArgs{};
     a->op = op;
     a->dtype = dtype;

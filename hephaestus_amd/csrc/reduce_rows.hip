@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_
     const T *base = (const T *)p.base + ((int64_t)p.offset + (int64_t)o0 * p.row_stride);
     uint64_t j = j0;
     if constexpr (V == 4) {
-        using Vt = typename Vec4<T>::type;
+        using Vt = typename Vec4A4<T>::type;
         auto visit = [&](const Vt &x, uint32_t jj) {
             st[0].visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), jj);
             st[1].visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), jj);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_
 template <typename T, int FLAGS>
 __global__ __launch_bounds__(kBlock) void cols_narrow_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
                                                              uint32_t nchunks) {
-    using V = typename Vec4<T>::type;
+    using V = typename Vec4A4<T>::type;
     const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
     if (w >= nchunks) return; // uniform across the wave
     const int lane = lane_id();
@@ -490,11 +490,12 @@ constexpr uint64_t kRowTargetWaves = 4096; // split rows when fewer than half th
 constexpr uint64_t kMinNarrowChunk = 4096; // 16-byte vectors per narrow-column chunk
 
 // Axis 0 of a dense row-major matrix with 2 to 32 columns (a power of two),
-// 16-byte aligned, whole vectors: the narrow-column form.
+// in whole 16-byte vectors (which need only 4-byte alignment): the
+// narrow-column form.
 bool narrow_columns(const RowParams &p, uintptr_t base) {
     const uint64_t c = p.rows;
     return c >= 2 && c <= 32 && (c & (c - 1)) == 0 && p.row_stride == 1 && p.col_stride == (int64_t)c &&
-           base % 16 == 0 && (p.cols * c) % 4 == 0 && p.cols <= 0xFFFFFFFFull;
+           base % 4 == 0 && (p.cols * c) % 4 == 0 && p.cols <= 0xFFFFFFFFull;
 }
 
 struct Shape {
@@ -542,7 +543,8 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         return s;
     }
     if (cols_layout) {
-        s.vec = p.row_stride == 1 && p.rows % 4 == 0 && base % 16 == 0 && p.col_stride % 4 == 0;
+        // 16-byte vectors at 4-byte alignment (Vec4A4): any line start.
+        s.vec = p.row_stride == 1 && p.rows % 4 == 0 && base % 4 == 0;
         s.V = s.vec ? 4 : 1;
         s.groups = ceil_div(p.rows, (uint64_t)kWave * s.V);
         if (s.groups < kTargetWaves) {

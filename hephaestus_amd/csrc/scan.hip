@@ -179,7 +179,7 @@ __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t 
                                       T (&v)[4]) {
     if constexpr (VEC && !REV) {
         if (e + 3 < p.len) {
-            using V = typename Vec4<T>::type;
+            using V = typename Vec4A4<T>::type;
             const V q = load_vec<NT>((const V *)(in + ib + (int64_t)e));
             v[0] = (T)q.x;
             v[1] = (T)q.y;
@@ -356,8 +356,8 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
     }
 }
 
-// Full tiles of unit-stride, 16-byte aligned lines (every tile but a line's
-// ragged last one): a block-uniform base pointer plus one 32-bit lane offset,
+// Full tiles of unit-stride lines (every tile but a line's ragged last one;
+// the vectors need only 4-byte alignment): a block-uniform base pointer plus one 32-bit lane offset,
 // so each step is a single base + offset + immediate vector access with no
 // bounds check and no per-step 64-bit address held in registers.
 // A whole tile of a reverse scan is a mirrored block of memory: logical
@@ -374,7 +374,7 @@ template <> struct ScanWavesPerEu<float> { static constexpr int value = 1; };
 
 template <typename T, bool NT, int STEPS>
 __device__ __forceinline__ void load_full_tile_rev(const T *base, uint32_t rev_off, T (&x)[STEPS][4]) {
-    using V = typename Vec4<T>::type;
+    using V = typename Vec4A4<T>::type;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
         const V q = load_vec<NT>((const V *)((const char *)base + rev_off - (uint32_t)j * (kWave * 16)));
@@ -387,7 +387,7 @@ __device__ __forceinline__ void load_full_tile_rev(const T *base, uint32_t rev_o
 
 template <typename T, bool NT, int STEPS>
 __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off, T (&x)[STEPS][4]) {
-    using V = typename Vec4<T>::type;
+    using V = typename Vec4A4<T>::type;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
         const V q = load_vec<NT>((const V *)((const char *)base + lane_off + (uint32_t)j * (kWave * 16)));
@@ -399,7 +399,8 @@ __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off,
 }
 
 // STEPS vectors per lane: a tile is 4 waves * 64 lanes * 4 * STEPS elements.
-// VEC: unit-stride, 16-byte aligned lines (vector loads and stores).  REV:
+// VEC: unit-stride lines (16-byte vector loads and stores at any 4-byte
+// aligned start).  REV:
 // suffix scan (logical element i is physical len-1-i).  NT: non-temporal
 // vector accesses.
 template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
@@ -498,7 +499,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     const C tile_excl = s_excl;
 
     if (full) {
-        using V = typename Vec4<T>::type;
+        using V = typename Vec4A4<T>::type;
         if constexpr (REV) {
             char *obase = (char *)(out + ob + rev_tile);
 #pragma unroll
@@ -532,7 +533,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][c]));
         if constexpr (VEC && !REV) {
             if (e + 3 < p.len) {
-                using V = typename Vec4<T>::type;
+                using V = typename Vec4A4<T>::type;
                 V v;
                 v.x = r[0];
                 v.y = r[1];
@@ -581,7 +582,7 @@ template <typename T> struct ColIO<T, 1> {
 };
 template <typename T> struct ColIO<T, 4> {
     using A = typename ColAcc<T>::type;
-    using Vt = typename Vec4<T>::type;
+    using Vt = typename Vec4A4<T>::type;
     static __device__ __forceinline__ void load(const T *p, A (&x)[4]) {
         const Vt v = __builtin_nontemporal_load((const Vt *)p);
         x[0] = (A)v.x;
@@ -759,7 +760,7 @@ constexpr int kColPoll = 1;
 template <typename T, int V>
 __device__ __forceinline__ void col_load_t(const T *p, T (&x)[V]) {
     if constexpr (V == 4) {
-        using Vt = typename Vec4<T>::type;
+        using Vt = typename Vec4A4<T>::type;
         const Vt v = __builtin_nontemporal_load((const Vt *)p);
         x[0] = (T)v.x;
         x[1] = (T)v.y;
@@ -773,7 +774,7 @@ __device__ __forceinline__ void col_load_t(const T *p, T (&x)[V]) {
 template <typename T, int V>
 __device__ __forceinline__ void col_store_t(T *p, const T (&y)[V]) {
     if constexpr (V == 4) {
-        using Vt = typename Vec4<T>::type;
+        using Vt = typename Vec4A4<T>::type;
         Vt v;
         v.x = y[0];
         v.y = y[1];
@@ -1033,8 +1034,11 @@ ColShape column_shape(const ScanArgs &a) {
     ColShape s;
     const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
     const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
-    const bool vec = a.in_line_stride == 1 && a.out_line_stride == 1 && a.lines % 4 == 0 && ibase % 16 == 0 &&
-                     obase % 16 == 0 && a.in_elem_stride % 4 == 0 && a.out_elem_stride % 4 == 0;
+    // A lane's four adjacent lines are one 16-byte vector per step; the
+    // vectors need only 4-byte alignment (Vec4A4), so any element stride and
+    // start qualify.
+    const bool vec = a.in_line_stride == 1 && a.out_line_stride == 1 && a.lines % 4 == 0 && ibase % 4 == 0 &&
+                     obase % 4 == 0;
     s.V = vec ? 4 : 1;
     s.groups = ceil_div(a.lines, (uint64_t)kWave * s.V);
     uint64_t k = 1;
@@ -1266,12 +1270,10 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
     const uintptr_t ibase = (uintptr_t)((const T *)a.in + a.in_offset);
     const uintptr_t obase = (uintptr_t)((T *)a.out + a.out_offset);
-    // Reverse scans vectorise their whole tiles as mirrored blocks, which
-    // stay 16-byte aligned when the line length is a multiple of 4.
-    // A single line's stride is never used (an [N, 1] view scanned along
-    // axis 0 is one contiguous line).
-    const bool strides4 = a.lines == 1 || (a.in_line_stride % 4 == 0 && a.out_line_stride % 4 == 0);
-    const bool vec = contiguous && ibase % 16 == 0 && obase % 16 == 0 && strides4 && (!a.reverse || a.len % 4 == 0);
+    // Vector accesses need only 4-byte alignment (Vec4A4), which every
+    // 4-byte element has: contiguous lines take the vector path wherever
+    // they start, forward or mirrored.
+    const bool vec = contiguous && ibase % 4 == 0 && obase % 4 == 0;
     const bool f64 = std::is_same<T, float>::value;
     uint64_t *level0 = (uint64_t *)((char *)ws + kLookbackOffset);
     uint64_t *level1 = (uint64_t *)((char *)level0 + status_bytes(p.total_tiles, f64));

@@ -215,7 +215,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
             ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * 4u;
 #pragma unroll
         for (int j = 0; j < STEPS; ++j) {
-            const u32x4 v = load_vec<true>((const u32x4 *)(base + lane_off + (uint32_t)j * (kWave * 16)));
+            const u32x4_a4 v = load_vec<true>((const u32x4_a4 *)(base + lane_off + (uint32_t)j * (kWave * 16)));
             x[j][0] = v.x;
             x[j][1] = v.y;
             x[j][2] = v.z;
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
         for (int j = 0; j < STEPS; ++j) {
             const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
             if (e + 3 < p.n) {
-                const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(p.values + e));
+                const u32x4_a4 v = __builtin_nontemporal_load((const u32x4_a4 *)(p.values + e));
                 x[j][0] = v.x;
                 x[j][1] = v.y;
                 x[j][2] = v.z;
@@ -485,8 +485,8 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     if (p.total_tiles >= 0x80000000ull)
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
-    if (((uintptr_t)a.values) % 16 != 0)
-        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 16-byte aligned");
+    if (((uintptr_t)a.values) % 4 != 0)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 4-byte aligned");
     if (ws_bytes < segmented_workspace_bytes(a))
         return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);

@@ -4,10 +4,11 @@
 // (crates/hephaestus-rocm/src/application/vector.rs:36-72):
 //   scale  t = t * f          axpy  t = fmaf(f, s, t)     xpay  t = fmaf(f, t, s)
 //   add / sub / mul / div     o = l op r
-// When every operand is 16-byte aligned, whole 4096-element tiles go to a
-// tile-per-block kernel (all loads of a lane before its stores) and the
-// remainder to a 16-byte grid-stride loop; misaligned operands take a scalar
-// grid-stride loop.
+// Whole 4096-element tiles go to a tile-per-block kernel (all loads of a
+// lane before its stores) and the remainder to a 16-byte grid-stride loop.
+// The 16-byte vectors need only 4-byte alignment, so operands at any element
+// offset take this path; only operands off a 4-byte boundary fall back to a
+// scalar grid-stride loop.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -36,14 +37,14 @@ __global__ __launch_bounds__(kBlock) void vector_kernel(const float *t, const fl
     constexpr bool kUsesS = OP != HX_VEC_SCALE;
     if constexpr (VEC) {
         const uint64_t nvec = n / 4;
-        const f32x4 *vt = (const f32x4 *)t;
-        const f32x4 *vs = (const f32x4 *)s;
-        f32x4 *vo = (f32x4 *)out;
+        const f32x4_a4 *vt = (const f32x4_a4 *)t;
+        const f32x4_a4 *vs = (const f32x4_a4 *)s;
+        f32x4_a4 *vo = (f32x4_a4 *)out;
         for (; i < nvec; i += nthreads) {
-            const f32x4 a = load_vec<true>(&vt[i]);
-            f32x4 b = a;
+            const f32x4_a4 a = load_vec<true>(&vt[i]);
+            f32x4_a4 b = a;
             if constexpr (kUsesS) b = load_vec<true>(&vs[i]);
-            f32x4 r;
+            f32x4_a4 r;
             r.x = apply<OP>(a.x, b.x, f);
             r.y = apply<OP>(a.y, b.y, f);
             r.z = apply<OP>(a.z, b.z, f);
@@ -75,27 +76,29 @@ __global__ __launch_bounds__(kTileWaves * kWave) void vector_tiles_kernel(const 
     const uint64_t base = (uint64_t)blockIdx.x * kTileElems * 4; // bytes
     const uint32_t lane_off =
         ((uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave * kTileSteps + lane_id()) * 16u;
-    f32x4 a[kTileSteps], b[kTileSteps];
+    f32x4_a4 a[kTileSteps], b[kTileSteps];
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j) {
-        a[j] = load_vec<true>((const f32x4 *)((const char *)t + base + lane_off + (uint32_t)j * (kWave * 16)));
+        a[j] = load_vec<true>((const f32x4_a4 *)((const char *)t + base + lane_off + (uint32_t)j * (kWave * 16)));
         if constexpr (kUsesS)
-            b[j] = load_vec<true>((const f32x4 *)((const char *)s + base + lane_off + (uint32_t)j * (kWave * 16)));
+            b[j] = load_vec<true>((const f32x4_a4 *)((const char *)s + base + lane_off + (uint32_t)j * (kWave * 16)));
     }
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j) {
-        f32x4 r;
-        const f32x4 y = kUsesS ? b[j] : a[j];
+        f32x4_a4 r;
+        const f32x4_a4 y = kUsesS ? b[j] : a[j];
         r.x = apply<OP>(a[j].x, y.x, f);
         r.y = apply<OP>(a[j].y, y.y, f);
         r.z = apply<OP>(a[j].z, y.z, f);
         r.w = apply<OP>(a[j].w, y.w, f);
-        store_vec<true>(r, (f32x4 *)((char *)out + base + lane_off + (uint32_t)j * (kWave * 16)));
+        store_vec<true>(r, (f32x4_a4 *)((char *)out + base + lane_off + (uint32_t)j * (kWave * 16)));
     }
 }
 
 template <int OP> hx_status launch_op(const float *t, const float *s, float *out, uint64_t n, float f, hipStream_t stream) {
-    const bool vec = ((((uintptr_t)t | (uintptr_t)out | (OP == HX_VEC_SCALE ? 0 : (uintptr_t)s)) & 15u) == 0);
+    // 16-byte vectors at 4-byte alignment (f32x4_a4): every f32 operand
+    // qualifies wherever it starts.
+    const bool vec = ((((uintptr_t)t | (uintptr_t)out | (OP == HX_VEC_SCALE ? 0 : (uintptr_t)s)) & 3u) == 0);
     if (vec && n >= kTileElems) {
         const uint64_t tiles = n / kTileElems;
         if (tiles >= 0x80000000ull)

@@ -287,6 +287,17 @@ def test_row_scan_tile_shapes(device, oracle, shape, dtype, variant):
     run_column_scan(device, oracle, op, dtype, shape, strides, offset, 1, exclusive, reverse, seed=r * 5 + c)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32])
+@pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100)])
+def test_column_scan_off_16_byte_boundaries(device, oracle, shape, dtype):
+    # offset 1: every line's vectors start 4 bytes past a 16-byte boundary
+    # (single pass for 1000 lines, chunked for 100); vectors need only 4-byte
+    # alignment, so both keep one 16-byte access per lane and step
+    r, c = shape
+    run_column_scan(device, oracle, "sum", dtype, shape, (c, 1), 1, 0, False, False, seed=r + c)
+    run_column_scan(device, oracle, "sum", dtype, shape, (c, 1), 1, 0, True, True, seed=r + c + 1)
+
+
 @pytest.mark.parametrize("op", ["sum", "prod"])
 def test_column_scan_transposed_and_reversed_lines(device, oracle, op):
     # column-major view: axis 1 strided, lines adjacent

@@ -528,6 +528,25 @@ def test_segmented_sum_16k_tile_edges(device, oracle):
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
+@pytest.mark.parametrize("skew", [1, 2, 3])
+def test_segmented_sum_values_off_16_byte_boundaries(device, oracle, skew):
+    """Values handed over as a raw pointer at an element offset: the tile loads
+    are 16-byte vectors that need only 4-byte alignment."""
+    from hephaestus_amd import _ffi
+
+    n = 3 * 8192 + 77
+    x = oracle.uniform_int(n + skew, seed=skew, lo=-1000, hi=1000, dtype=np.int32)
+    rng = np.random.default_rng(skew)
+    cuts = np.sort(rng.choice(np.arange(1, n), size=300, replace=False))
+    offsets = np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+    vb = device.upload(x)
+    ob = device.upload(offsets)
+    out = device.upload(np.full(offsets.size - 1, 0x5A5A5A5A, np.uint32).view(np.int32))
+    _ffi.check(_ffi.lib().hx_segmented_reduce(device.handle, _ffi.OP_SUM, _ffi.DTYPE_I32, vb.ptr + 4 * skew, n,
+                                              ob.ptr, offsets.size, out.ptr, offsets.size - 1, None))
+    assert np.array_equal(device.download_owned(out), oracle.segmented_sum(x[skew:], offsets))
+
+
 def test_segmented_sum_empty_values(device):
     vb = device.alloc_zeroed(np.int32, 16)  # aligned allocation, but n = 0 values
     ob = device.upload(np.zeros(4, np.uint32))

@@ -214,3 +214,31 @@ def test_vector_forms_bit_exact(device, oracle, n):
                     (OPS.divide_into, t / s)):
         fn(device, device.upload(t), ds, out)
         assert np.array_equal(device.download_owned(out), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("offsets", [(1, 2, 3), (3, 0, 1), (2, 2, 2)])
+@pytest.mark.parametrize("n", [5, 4096 * 3 + 7, 1000003])
+def test_vector_forms_at_element_offsets(device, oracle, n, offsets):
+    """Operands that start off 16-byte boundaries (raw pointers into larger
+    buffers): the 16-byte vector paths need only 4-byte alignment; the
+    elements around each range stay untouched."""
+    from hephaestus_amd import _ffi
+
+    ot, os_, oo = offsets
+    pad = 8
+    t = oracle.uniform_real(n + pad, seed=n + 11, lo=-3.0, hi=3.0)
+    s = oracle.uniform_real(n + pad, seed=n + 12, lo=0.5, hi=3.0)
+    f = np.float32(0.7)
+    dt, ds = device.upload(t), device.upload(s)
+    lib = _ffi.lib()
+    _ffi.check(lib.hx_vector_update(device.handle, 1, _ffi.DTYPE_F32, dt.ptr + 4 * ot, n, ds.ptr + 4 * os_, n,
+                                    float(f), None))  # axpy
+    want = t.copy()
+    want[ot:ot + n] = oracle.fma_arrays(s[os_:os_ + n], t[ot:ot + n], f)
+    assert np.array_equal(device.download_owned(dt), want)
+    out = device.upload(np.full(n + pad, 9.0, np.float32))
+    _ffi.check(lib.hx_vector_binary(device.handle, 5, _ffi.DTYPE_F32, ds.ptr + 4 * os_, n, ds.ptr + 4 * ot, n,
+                                    out.ptr + 4 * oo, n, None))  # mul
+    want = np.full(n + pad, 9.0, np.float32)
+    want[oo:oo + n] = s[os_:os_ + n] * s[ot:ot + n]
+    assert np.array_equal(device.download_owned(out), want)
