@@ -730,6 +730,202 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     }
 }
 
+// Narrow column scans: axis 0 of a dense row-major [R, C] matrix with C a
+// power of two from 4 to 128 (fewer lines than the single pass takes).  The
+// matrix is one contiguous range of R*C/4 16-byte vectors, and logical
+// vector g (the range mirrored, components reversed, for a suffix scan)
+// holds in component k the element of column (4g + k) mod C (reverse:
+// C-1 minus that).  Waves take chunks of whole 256-vector trips, so lane l
+// of every step sees the same columns: lanes l, l+s, l+2s, ... (s = C/4)
+// share columns, and a step's per-column scan is a strided lane scan.  The
+// column-tile forms gave such matrices one live lane in 64/C (2^28 u32 as
+// [2^26, 4]: 3.4 ms).  Three launches, as the chunked column scan:
+//   col_narrow_totals_kernel  per chunk and column, the total;
+//   col_narrow_carry_kernel   per column, an exclusive scan of its totals;
+//   col_narrow_scan_kernel    every chunk rescanned from its carries.
+// f32 steps scan in f32 and add f64 carries; integers wrap.
+template <typename T, bool REV>
+__device__ __forceinline__ void narrow_load(const T *base, uint64_t nvec, uint64_t g, T (&x)[4]) {
+    using V = typename Vec4A4<T>::type;
+    const V *src = (const V *)base;
+    if constexpr (REV) {
+        const V q = __builtin_nontemporal_load(&src[nvec - 1 - g]);
+        x[0] = (T)q.w;
+        x[1] = (T)q.z;
+        x[2] = (T)q.y;
+        x[3] = (T)q.x;
+    } else {
+        const V q = __builtin_nontemporal_load(&src[g]);
+        x[0] = (T)q.x;
+        x[1] = (T)q.y;
+        x[2] = (T)q.z;
+        x[3] = (T)q.w;
+    }
+}
+template <typename T, bool REV>
+__device__ __forceinline__ void narrow_store(T *base, uint64_t nvec, uint64_t g, const T (&y)[4]) {
+    using V = typename Vec4A4<T>::type;
+    V *dst = (V *)base;
+    V q;
+    if constexpr (REV) {
+        q.w = y[0];
+        q.z = y[1];
+        q.y = y[2];
+        q.x = y[3];
+        __builtin_nontemporal_store(q, &dst[nvec - 1 - g]);
+    } else {
+        q.x = y[0];
+        q.y = y[1];
+        q.z = y[2];
+        q.w = y[3];
+        __builtin_nontemporal_store(q, &dst[g]);
+    }
+}
+// Column of lane l's component k (C a power of two dividing 256).
+template <bool REV> __device__ __forceinline__ uint32_t narrow_col(int lane, int k, uint32_t C) {
+    const uint32_t c = (uint32_t)(4 * lane + k) & (C - 1);
+    return REV ? C - 1 - c : c;
+}
+
+template <typename T, typename Op, bool REV>
+__global__ __launch_bounds__(kBlock) void col_narrow_totals_kernel(ScanParams p, typename ColAcc<T>::type *totals,
+                                                                   uint64_t chunk, uint32_t nchunks) {
+    using A = typename ColAcc<T>::type;
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= nchunks) return; // uniform across the wave
+    const int lane = lane_id();
+    const uint32_t C = (uint32_t)p.lines;
+    const uint64_t nvec = (p.len * C) >> 2;
+    const T *in = (const T *)p.in + p.in_offset;
+    const uint64_t g0 = w * chunk;
+    const uint64_t g1 = g0 + chunk < nvec ? g0 + chunk : nvec;
+    A acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = Op::template identity<A>();
+    for (uint64_t g = g0 + lane; g < g1; g += 4 * kWave) {
+        T x[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (g + u * kWave < g1) narrow_load<T, REV>(in, nvec, g + u * kWave, x[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (g + u * kWave < g1)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] = Op::combine(acc[k], (A)x[u][k]);
+    }
+    const int s = (int)(C / 4);
+    for (int m = kWave / 2; m >= s; m >>= 1)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] = Op::combine(acc[k], __shfl_xor(acc[k], m, kWave));
+    if (lane >= s) return;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) totals[w * C + narrow_col<REV>(lane, k, C)] = acc[k];
+}
+
+// Exclusive scan of one narrow line's chunk totals, in place: a block per
+// line, thread t folding a contiguous range of chunks, the range totals
+// combined in thread order through LDS (a fixed order, so f32 carries are
+// reproducible).  col_carry_kernel runs 64 lines per block, which left a
+// handful of lanes walking thousands of chunks (4 lines x 8192 chunks:
+// 156 us).
+template <typename A, typename Op>
+__global__ __launch_bounds__(kBlock) void col_narrow_carry_kernel(A *totals, uint64_t lines, uint32_t nchunks) {
+    __shared__ A sh[kBlock];
+    const uint64_t line = blockIdx.x;
+    const uint32_t per = (nchunks + kBlock - 1) / kBlock;
+    const uint32_t k0 = threadIdx.x * per < nchunks ? threadIdx.x * per : nchunks;
+    const uint32_t k1 = k0 + per < nchunks ? k0 + per : nchunks;
+    A t = Op::template identity<A>();
+    for (uint32_t k = k0; k < k1; ++k) t = Op::combine(t, totals[(uint64_t)k * lines + line]);
+    sh[threadIdx.x] = t;
+    __syncthreads();
+    A acc = Op::template identity<A>();
+    for (uint32_t q = 0; q < threadIdx.x; ++q) acc = Op::combine(acc, sh[q]);
+    for (uint32_t k = k0; k < k1; ++k) {
+        const A v = totals[(uint64_t)k * lines + line];
+        totals[(uint64_t)k * lines + line] = acc;
+        acc = Op::combine(acc, v);
+    }
+}
+
+// A trip is 4 steps of 64 vectors.  The 16 values of a lane (4 steps x 4
+// components) are scanned across lanes together -- Hillis-Steele over lanes
+// l, l-s, l-2s, ..., one shuffle per value and distance, the 16 independent
+// shuffles of a distance in flight at once -- then each step's class totals
+// (the class's last lane) advance the running carries in step order.
+template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
+__global__ __launch_bounds__(kBlock) void col_narrow_scan_kernel(ScanParams p,
+                                                                 const typename ColAcc<T>::type *carries,
+                                                                 uint64_t chunk, uint32_t nchunks) {
+    using A = typename ColAcc<T>::type;
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= nchunks) return; // uniform across the wave
+    const int lane = lane_id();
+    const uint32_t C = (uint32_t)p.lines;
+    const int s = (int)(C / 4);
+    const uint64_t nvec = (p.len * C) >> 2;
+    const T *in = (const T *)p.in + p.in_offset;
+    T *out = (T *)p.out + p.out_offset;
+    const T tid = Op::template identity<T>();
+    const uint64_t g0 = w * chunk;
+    const uint64_t g1 = g0 + chunk < nvec ? g0 + chunk : nvec;
+    const int last = kWave - s + (lane & (s - 1)); // last lane of this lane's class
+    A carry[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        carry[k] = CARRY ? carries[w * C + narrow_col<REV>(lane, k, C)] : Op::template identity<A>();
+    // The trip count is the same for every lane (the chunk is shared), and
+    // every lane of the wave takes part in the lane scans.
+    for (uint64_t base = g0; base < g1; base += 4 * kWave) {
+        const uint64_t g = base + lane;
+        T v[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (g + u * kWave < g1) {
+                narrow_load<T, REV>(in, nvec, g + u * kWave, v[u]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[u][k] = tid;
+            }
+        }
+        for (int d = s; d < kWave; d <<= 1) {
+            T t[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) t[u][k] = __shfl_up(v[u][k], d, kWave);
+            if (lane >= d)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) v[u][k] = Op::combine(t[u][k], v[u][k]);
+        }
+        T tot[4][4], pre[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                tot[u][k] = __shfl(v[u][k], last, kWave);
+                pre[u][k] = v[u][k];
+                if constexpr (EXCL) {
+                    pre[u][k] = __shfl_up(v[u][k], s, kWave);
+                    if (lane < s) pre[u][k] = tid;
+                }
+            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            T y[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                y[k] = (T)Op::combine(carry[k], (A)pre[u][k]);
+                carry[k] = Op::combine(carry[k], (A)tot[u][k]);
+            }
+            if (g + u * kWave < g1) narrow_store<T, REV>(out, nvec, g + u * kWave, y);
+        }
+    }
+}
+
+
 // Single-pass column scan.  A block owns a tile of kColTileRows scan steps x
 // 64*V adjacent lines.  Its kColDataWaves data waves each hold kColRows
 // steps of the tile in registers (lane l: lines 64*V*g + V*l .. +V-1), scan
@@ -1211,7 +1407,75 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     }
 }
 
+// Narrow column scans (col_narrow_*): chunks of whole 256-vector trips,
+// about kNarrowTargetWaves of them.
+constexpr uint64_t kNarrowTargetWaves = 8192;
+constexpr uint64_t kNarrowMinChunk = 1024; // 16-byte vectors
+
+bool narrow_column_scan(const ScanArgs &a) {
+    const uint64_t c = a.lines;
+    const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
+    const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
+    return c >= 4 && c < kSinglePassMinLines && (c & (c - 1)) == 0 && a.in_line_stride == 1 &&
+           a.out_line_stride == 1 && a.in_elem_stride == (int64_t)c && a.out_elem_stride == (int64_t)c &&
+           ibase % 4 == 0 && obase % 4 == 0;
+}
+
+struct NarrowShape {
+    uint64_t chunk = 0; // 16-byte vectors per chunk
+    uint32_t nchunks = 1;
+};
+NarrowShape narrow_shape(const ScanArgs &a) {
+    NarrowShape s;
+    const uint64_t nvec = (a.len * a.lines) >> 2;
+    uint64_t chunk = ceil_div(nvec, kNarrowTargetWaves);
+    if (chunk < kNarrowMinChunk) chunk = kNarrowMinChunk;
+    chunk = ceil_div(chunk, 4 * kWave) * 4 * kWave;
+    s.chunk = chunk;
+    s.nchunks = (uint32_t)ceil_div(nvec, chunk);
+    return s;
+}
+uint64_t narrow_bytes(const ScanArgs &a) {
+    const NarrowShape s = narrow_shape(a);
+    if (s.nchunks <= 1) return 0;
+    return (uint64_t)s.nchunks * a.lines * (a.dtype == HX_DTYPE_F32 ? 8u : 4u);
+}
+
+template <typename T, typename Op, bool EXCL, bool REV>
+hx_status launch_narrow_dir(const ScanParams &p, const NarrowShape &s, void *ws, hipStream_t stream) {
+    using A = typename ColAcc<T>::type;
+    const dim3 grid((uint32_t)ceil_div((uint64_t)s.nchunks, (uint64_t)(kBlock / kWave))), block(kBlock);
+    A *totals = (A *)ws;
+    if (s.nchunks > 1) {
+        hipLaunchKernelGGL((col_narrow_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, totals, s.chunk,
+                           s.nchunks);
+        HX_TRY(check_launch("col_narrow_totals_kernel"));
+        hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3((uint32_t)p.lines), dim3(kBlock), 0, stream, totals,
+                           p.lines, s.nchunks);
+        HX_TRY(check_launch("col_narrow_carry_kernel"));
+        hipLaunchKernelGGL((col_narrow_scan_kernel<T, Op, EXCL, REV, true>), grid, block, 0, stream, p,
+                           (const A *)totals, s.chunk, s.nchunks);
+    } else {
+        hipLaunchKernelGGL((col_narrow_scan_kernel<T, Op, EXCL, REV, false>), grid, block, 0, stream, p,
+                           (const A *)totals, s.chunk, s.nchunks);
+    }
+    return check_launch("col_narrow_scan_kernel");
+}
+
+template <typename T, typename Op>
+hx_status launch_narrow(const ScanArgs &a, const ScanParams &p, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    const NarrowShape s = narrow_shape(a);
+    if (s.nchunks > 1 && ws_bytes < narrow_bytes(a))
+        return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
+    if (a.exclusive)
+        return a.reverse ? launch_narrow_dir<T, Op, true, true>(p, s, ws, stream)
+                         : launch_narrow_dir<T, Op, true, false>(p, s, ws, stream);
+    return a.reverse ? launch_narrow_dir<T, Op, false, true>(p, s, ws, stream)
+                     : launch_narrow_dir<T, Op, false, false>(p, s, ws, stream);
+}
+
 uint64_t scan_bytes(const ScanArgs &a) {
+    if (narrow_column_scan(a)) return narrow_bytes(a);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape c = col_lb_shape(a);
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
@@ -1241,6 +1505,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out_offset = a.out_offset;
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
+    if (narrow_column_scan(a)) return launch_narrow<T, Op>(a, p, ws, ws_bytes, stream);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape cs = col_lb_shape(a);
         if (cs.groups * cs.chunks > 0x7FFFFFFFull)
@@ -1295,7 +1560,10 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
-bool scan_uses_lookback(const ScanArgs &a) { return !column_mode(a) || column_single_pass(a); }
+bool scan_uses_lookback(const ScanArgs &a) {
+    if (narrow_column_scan(a)) return false;
+    return !column_mode(a) || column_single_pass(a);
+}
 
 hx_status launch_scan(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     const bool prod = a.op == HX_OP_PROD;

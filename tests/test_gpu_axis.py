@@ -251,7 +251,10 @@ def run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exc
 # more): vector lanes over many chunks, scalar lanes, one tile only.
 # Chunked reduce-then-scan (fewer lines): 100 lines (vector lanes), 16 lines x
 # 65536 steps.
-COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256), (3000, 100), (65536, 16)]
+COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256), (3000, 100), (65536, 16),
+                 # narrow columns (4 to 128, powers of two): the dense range
+                 # scanned with strided lane scans, one or many chunks
+                 ((1 << 20) + 3, 4), (70001, 8), (4097, 32), (1000, 64), (3001, 128), (5, 4)]
 
 
 @pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
@@ -288,10 +291,10 @@ def test_row_scan_tile_shapes(device, oracle, shape, dtype, variant):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.uint32])
-@pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100)])
+@pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100), (100003, 8)])
 def test_column_scan_off_16_byte_boundaries(device, oracle, shape, dtype):
     # offset 1: every line's vectors start 4 bytes past a 16-byte boundary
-    # (single pass for 1000 lines, chunked for 100); vectors need only 4-byte
+    # (single pass for 1000 lines, chunked for 100, narrow for 8); vectors need only 4-byte
     # alignment, so both keep one 16-byte access per lane and step
     r, c = shape
     run_column_scan(device, oracle, "sum", dtype, shape, (c, 1), 1, 0, False, False, seed=r + c)
