@@ -348,3 +348,48 @@ def test_prepared_axis_reduction_batch(device, oracle):
     device.write_buffer(buf, y)
     hx.submit_prepared_axis_reduction_batch(device, plans)
     assert np.array_equal(device.download_owned(outs[-1]), y.reshape(r, c).sum(axis=0, dtype=np.uint32))
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_prepared_narrow_column_scan_rebinds(device, oracle, reverse):
+    # narrow-column scan through a prepared plan: the workspace for the chunk
+    # carries comes with the plan; later writes to the input are observed
+    r, c = 300001, 8
+    lay = Layout.c_contiguous([r, c])
+    x = oracle.uniform_int(r * c, seed=4, lo=0, hi=1000)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.uint32, r * c)
+    direction = hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward
+    plan = SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(buf, lay), 0, direction, StridedView(out, lay))
+
+    def want(v):
+        m = v.reshape(r, c)
+        if reverse:
+            return np.cumsum(m[::-1], axis=0, dtype=np.uint32)[::-1]
+        return np.cumsum(m, axis=0, dtype=np.uint32)
+
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want(x))
+    y = oracle.uniform_int(r * c, seed=5, lo=0, hi=1000)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out).reshape(r, c), want(y))
+
+
+@pytest.mark.parametrize("shape,axis", [((500001, 8), 0), ((300001, 3), 1)])
+def test_prepared_narrow_axis_reduce_rebinds(device, oracle, shape, axis):
+    # narrow columns (axis 0) and rows of 3 elements (a thread per row, axis 1)
+    r, c = shape
+    x = oracle.uniform_int(r * c, seed=6, lo=0, hi=1000)
+    buf = device.upload(x)
+    nout = c if axis == 0 else r
+    out = device.alloc_zeroed(np.uint32, nout)
+    out_shape = [1, c] if axis == 0 else [r, 1]
+    plan = AXIS.prepare_reduce_axis_into(device, hx.SumOp, StridedView(buf, Layout.c_contiguous([r, c])), axis,
+                                         StridedView(out, Layout.c_contiguous(out_shape)))
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), x.reshape(r, c).sum(axis=axis, dtype=np.uint32))
+    y = oracle.uniform_int(r * c, seed=7, lo=0, hi=1000)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), y.reshape(r, c).sum(axis=axis, dtype=np.uint32))
