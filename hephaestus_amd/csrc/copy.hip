@@ -30,10 +30,10 @@ __global__ __launch_bounds__(kTileWaves * kWave) void copy_tiles_kernel(const ch
     u32x4_a4 v[kTileSteps];
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j)
-        v[j] = load_vec<true>((const u32x4_a4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
+        v[j] = load_a4<true>((const u32x4_a4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j)
-        store_vec<true>(v[j], (u32x4_a4 *)(dst + base + lane_off + (uint32_t)j * (kWave * 16)));
+        store_a4<true>(v[j], (u32x4_a4 *)(dst + base + lane_off + (uint32_t)j * (kWave * 16)));
 }
 
 // 16-byte body (both pointers 4-byte aligned: the vectors need no more),
@@ -45,12 +45,12 @@ __global__ __launch_bounds__(kBlock) void copy_vec_kernel(const u32x4_a4 *src, u
     const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
     uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
     for (; i + nthreads < nvec; i += 2 * nthreads) {
-        const u32x4_a4 a = load_vec<true>(&src[i]);
-        const u32x4_a4 b = load_vec<true>(&src[i + nthreads]);
-        store_vec<true>(a, &dst[i]);
-        store_vec<true>(b, &dst[i + nthreads]);
+        const u32x4_a4 a = load_a4<true>(&src[i]);
+        const u32x4_a4 b = load_a4<true>(&src[i + nthreads]);
+        store_a4<true>(a, &dst[i]);
+        store_a4<true>(b, &dst[i + nthreads]);
     }
-    if (i < nvec) store_vec<true>(load_vec<true>(&src[i]), &dst[i]);
+    if (i < nvec) store_a4<true>(load_a4<true>(&src[i]), &dst[i]);
     if (blockIdx.x == 0 && threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
 

@@ -35,6 +35,25 @@ template <bool NT, typename V> __device__ __forceinline__ void store_vec(V v, V 
     if constexpr (NT) __builtin_nontemporal_store(v, ptr);
     else *ptr = v;
 }
+// The same through dword-aligned pointers.  The parameter types name the
+// 4-byte-aligned typedefs explicitly: a template parameter deduced from the
+// pointer would be the canonical, 16-byte-aligned vector type.
+template <bool NT> __device__ __forceinline__ f32x4_a4 load_a4(const f32x4_a4 *ptr) {
+    if constexpr (NT) return __builtin_nontemporal_load(ptr);
+    else return *ptr;
+}
+template <bool NT> __device__ __forceinline__ u32x4_a4 load_a4(const u32x4_a4 *ptr) {
+    if constexpr (NT) return __builtin_nontemporal_load(ptr);
+    else return *ptr;
+}
+template <bool NT> __device__ __forceinline__ void store_a4(f32x4_a4 v, f32x4_a4 *ptr) {
+    if constexpr (NT) __builtin_nontemporal_store(v, ptr);
+    else *ptr = v;
+}
+template <bool NT> __device__ __forceinline__ void store_a4(u32x4_a4 v, u32x4_a4 *ptr) {
+    if constexpr (NT) __builtin_nontemporal_store(v, ptr);
+    else *ptr = v;
+}
 
 // ----------------------------------------------------------------- lanes
 

@@ -129,11 +129,11 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
         const V *vb = (const V *)(b + head);
         uint64_t vi = tid;
         for (; vi + nthreads < nvec; vi += 2 * nthreads) {
-            const V x0 = load_vec<true>(&va[vi]), x1 = load_vec<true>(&va[vi + nthreads]);
+            const V x0 = load_a4<true>(&va[vi]), x1 = load_a4<true>(&va[vi + nthreads]);
             V y0 = x0, y1 = x1;
             if constexpr (kTwo) {
-                y0 = load_vec<true>(&vb[vi]);
-                y1 = load_vec<true>(&vb[vi + nthreads]);
+                y0 = load_a4<true>(&vb[vi]);
+                y1 = load_a4<true>(&vb[vi + nthreads]);
             }
             acc = P::combine(acc, P::combine(P::combine(P::elem(x0.x, y0.x), P::elem(x0.y, y0.y)),
                                              P::combine(P::elem(x0.z, y0.z), P::elem(x0.w, y0.w))));
@@ -141,9 +141,9 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
                                              P::combine(P::elem(x1.z, y1.z), P::elem(x1.w, y1.w))));
         }
         if (vi < nvec) {
-            const V x0 = load_vec<true>(&va[vi]);
+            const V x0 = load_a4<true>(&va[vi]);
             V y0 = x0;
-            if constexpr (kTwo) y0 = load_vec<true>(&vb[vi]);
+            if constexpr (kTwo) y0 = load_a4<true>(&vb[vi]);
             acc = P::combine(acc, P::combine(P::combine(P::elem(x0.x, y0.x), P::elem(x0.y, y0.y)),
                                              P::combine(P::elem(x0.z, y0.z), P::elem(x0.w, y0.w))));
         }

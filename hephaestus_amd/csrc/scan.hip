@@ -180,7 +180,7 @@ __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t 
     if constexpr (VEC && !REV) {
         if (e + 3 < p.len) {
             using V = typename Vec4A4<T>::type;
-            const V q = load_vec<NT>((const V *)(in + ib + (int64_t)e));
+            const V q = load_a4<NT>((const V *)(in + ib + (int64_t)e));
             v[0] = (T)q.x;
             v[1] = (T)q.y;
             v[2] = (T)q.z;
@@ -377,7 +377,7 @@ __device__ __forceinline__ void load_full_tile_rev(const T *base, uint32_t rev_o
     using V = typename Vec4A4<T>::type;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
-        const V q = load_vec<NT>((const V *)((const char *)base + rev_off - (uint32_t)j * (kWave * 16)));
+        const V q = load_a4<NT>((const V *)((const char *)base + rev_off - (uint32_t)j * (kWave * 16)));
         x[j][0] = (T)q.w;
         x[j][1] = (T)q.z;
         x[j][2] = (T)q.y;
@@ -390,7 +390,7 @@ __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off,
     using V = typename Vec4A4<T>::type;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
-        const V q = load_vec<NT>((const V *)((const char *)base + lane_off + (uint32_t)j * (kWave * 16)));
+        const V q = load_a4<NT>((const V *)((const char *)base + lane_off + (uint32_t)j * (kWave * 16)));
         x[j][0] = (T)q.x;
         x[j][1] = (T)q.y;
         x[j][2] = (T)q.z;
@@ -509,7 +509,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
                 v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
                 v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
                 v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
-                store_vec<NT>(v, (V *)(obase + rev_off - (uint32_t)j * (kWave * 16)));
+                store_a4<NT>(v, (V *)(obase + rev_off - (uint32_t)j * (kWave * 16)));
             }
         } else {
             char *obase = (char *)(out + ob + (int64_t)(tin * kTileElems));
@@ -520,7 +520,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
                 v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
                 v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
                 v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
-                store_vec<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
+                store_a4<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
             }
         }
         return;
@@ -539,7 +539,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
                 v.y = r[1];
                 v.z = r[2];
                 v.w = r[3];
-                store_vec<NT>(v, (V *)(out + ob + (int64_t)e));
+                store_a4<NT>(v, (V *)(out + ob + (int64_t)e));
                 continue;
             }
         }

@@ -215,7 +215,7 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
             ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * 4u;
 #pragma unroll
         for (int j = 0; j < STEPS; ++j) {
-            const u32x4_a4 v = load_vec<true>((const u32x4_a4 *)(base + lane_off + (uint32_t)j * (kWave * 16)));
+            const u32x4_a4 v = load_a4<true>((const u32x4_a4 *)(base + lane_off + (uint32_t)j * (kWave * 16)));
             x[j][0] = v.x;
             x[j][1] = v.y;
             x[j][2] = v.z;

@@ -41,15 +41,15 @@ __global__ __launch_bounds__(kBlock) void vector_kernel(const float *t, const fl
         const f32x4_a4 *vs = (const f32x4_a4 *)s;
         f32x4_a4 *vo = (f32x4_a4 *)out;
         for (; i < nvec; i += nthreads) {
-            const f32x4_a4 a = load_vec<true>(&vt[i]);
+            const f32x4_a4 a = load_a4<true>(&vt[i]);
             f32x4_a4 b = a;
-            if constexpr (kUsesS) b = load_vec<true>(&vs[i]);
+            if constexpr (kUsesS) b = load_a4<true>(&vs[i]);
             f32x4_a4 r;
             r.x = apply<OP>(a.x, b.x, f);
             r.y = apply<OP>(a.y, b.y, f);
             r.z = apply<OP>(a.z, b.z, f);
             r.w = apply<OP>(a.w, b.w, f);
-            store_vec<true>(r, &vo[i]);
+            store_a4<true>(r, &vo[i]);
         }
         const uint64_t tail = nvec * 4 + (uint64_t)blockIdx.x * kBlock + threadIdx.x;
         if (blockIdx.x * (uint64_t)kBlock + threadIdx.x < n - nvec * 4)
@@ -79,9 +79,9 @@ __global__ __launch_bounds__(kTileWaves * kWave) void vector_tiles_kernel(const 
     f32x4_a4 a[kTileSteps], b[kTileSteps];
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j) {
-        a[j] = load_vec<true>((const f32x4_a4 *)((const char *)t + base + lane_off + (uint32_t)j * (kWave * 16)));
+        a[j] = load_a4<true>((const f32x4_a4 *)((const char *)t + base + lane_off + (uint32_t)j * (kWave * 16)));
         if constexpr (kUsesS)
-            b[j] = load_vec<true>((const f32x4_a4 *)((const char *)s + base + lane_off + (uint32_t)j * (kWave * 16)));
+            b[j] = load_a4<true>((const f32x4_a4 *)((const char *)s + base + lane_off + (uint32_t)j * (kWave * 16)));
     }
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j) {
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void vector_tiles_kernel(const 
         r.y = apply<OP>(a[j].y, y.y, f);
         r.z = apply<OP>(a[j].z, y.z, f);
         r.w = apply<OP>(a[j].w, y.w, f);
-        store_vec<true>(r, (f32x4_a4 *)((char *)out + base + lane_off + (uint32_t)j * (kWave * 16)));
+        store_a4<true>(r, (f32x4_a4 *)((char *)out + base + lane_off + (uint32_t)j * (kWave * 16)));
     }
 }
 
