@@ -412,24 +412,62 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
 // B_tiles = n, ub_map[t] = #{k : off(k) <= B_t} and lb_map[t] =
 // #{k : off(k) < B_t}.  With sorted offsets, the edges with ub = k are those
 // in [off(k-1), off(k)) and those with lb = k are in (off(k-1), off(k)]
-// (off(-1) = 0 resp. -1, off(S+1) = infinity), so each thread takes one k
-// and writes the few edges of its interval: one coalesced pass over the
-// offsets instead of a search per tile.
+// (off(-1) = 0 resp. -1, off(S+1) = infinity): one coalesced pass over the
+// offsets instead of a search per tile.  Lane j of a wave takes k = base + j;
+// an interval of at most kDirectEdges edges is written by its lane, and the
+// wave writes the longer ones together, one interval at a time (64 edges per
+// store), so a long segment's many edges do not fall to one thread (15
+// segments over 2^27 values: 238 us with a thread per interval).
+constexpr uint32_t kDirectEdges = 8;
+
+__device__ __forceinline__ void map_write_edges(uint32_t *map, uint32_t first, uint32_t count, uint32_t k) {
+    const int lane = lane_id();
+    const bool big = count > kDirectEdges;
+    if (!big)
+        for (uint32_t i = 0; i < count; ++i) map[first + i] = k;
+    uint64_t pending = ballot(big);
+    while (pending) { // wave-uniform
+        const int j = __ffsll((long long)pending) - 1;
+        pending &= pending - 1;
+        const uint32_t f = read_lane(first, j), c = read_lane(count, j), kj = read_lane(k, j);
+        for (uint32_t i = (uint32_t)lane; i < c; i += kWave) map[f + i] = kj;
+    }
+}
+
 template <int TILE>
 __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
     const uint64_t tiles = p.total_tiles;
     const uint64_t S = p.segments;
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
-    for (uint64_t k = (uint64_t)blockIdx.x * kBlock + threadIdx.x; k <= S + 1; k += nthreads) {
-        const uint64_t lo = k == 0 ? 0 : off_at(p, k - 1);
-        const uint64_t hi = k <= S ? off_at(p, k) : p.n + 1; // off_at clamps into [0, n]
-        // ub: edges in [lo, hi) (lo for k == 0 is 0: edges below off(0)).
-        for (uint64_t t = (lo + TILE - 1) / TILE; t < tiles && t * TILE < hi; ++t) p.ub_map[t] = (uint32_t)k;
-        if (lo <= p.n && p.n < hi) p.ub_map[tiles] = (uint32_t)k;
-        // lb: edges in (lo', hi] with lo' = off(k-1), or -1 for k == 0.
-        const uint64_t t_first = k == 0 ? 0 : lo / TILE + 1;
-        for (uint64_t t = t_first; t < tiles && t * TILE <= hi; ++t) p.lb_map[t] = (uint32_t)k;
-        if ((k == 0 || lo < p.n) && p.n <= hi) p.lb_map[tiles] = (uint32_t)k;
+    const int lane = lane_id();
+    const uint64_t wave = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    const uint64_t nwaves = (uint64_t)gridDim.x * (kBlock / kWave);
+    for (uint64_t base = wave * kWave; base <= S + 1; base += nwaves * kWave) { // wave-uniform
+        const uint64_t k = base + (uint64_t)lane;
+        uint32_t ua = 0, un = 0, la = 0, ln = 0;
+        if (k <= S + 1) {
+            const uint64_t lo = k == 0 ? 0 : off_at(p, k - 1);
+            const uint64_t hi = k <= S ? off_at(p, k) : p.n + 1; // off_at clamps into [0, n]
+            // ub: edges t with lo <= t * TILE < hi (lo for k == 0 is 0).
+            const uint64_t u0 = (lo + TILE - 1) / TILE;
+            uint64_t u1 = (hi + TILE - 1) / TILE;
+            if (u1 > tiles) u1 = tiles;
+            if (u1 > u0) {
+                ua = (uint32_t)u0;
+                un = (uint32_t)(u1 - u0);
+            }
+            if (lo <= p.n && p.n < hi) p.ub_map[tiles] = (uint32_t)k;
+            // lb: edges t with lo' < t * TILE <= hi, lo' = off(k-1) or -1 for k == 0.
+            const uint64_t l0 = k == 0 ? 0 : lo / TILE + 1;
+            uint64_t l1 = hi / TILE + 1;
+            if (l1 > tiles) l1 = tiles;
+            if (l1 > l0) {
+                la = (uint32_t)l0;
+                ln = (uint32_t)(l1 - l0);
+            }
+            if ((k == 0 || lo < p.n) && p.n <= hi) p.lb_map[tiles] = (uint32_t)k;
+        }
+        map_write_edges(p.ub_map, ua, un, (uint32_t)k);
+        map_write_edges(p.lb_map, la, ln, (uint32_t)k);
     }
 }
 
