@@ -30,11 +30,12 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32",
-             "axpy_f32", "colsum_f32", "colscan_u32")
+WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "segmented_short_i32", "scan_f32_2_30",
+             "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
-             "segmented_i32": "segmented_sum_kernel", "scan_f32_2_30": "scan_tiles_kernel",
+             "segmented_i32": "segmented_sum_kernel", "segmented_short_i32": "seg_short_kernel",
+             "scan_f32_2_30": "scan_tiles_kernel",
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
              "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel"}
 
@@ -122,6 +123,22 @@ def bench_segmented_i32(hx, dev, args):
     x = dev.alloc_uninitialized(np.int32, n)
     dev.fill_uniform_int(x, seed=4, lo=-1000, hi=1000)
     off = oracle.geometric_offsets(n, 300.0, seed=5)
+    ob = dev.upload(off)
+    out = dev.alloc_uninitialized(np.int32, off.size - 1)
+    plan = hx.RocmSegmentedReductionOps().prepare_segmented_sum(dev, x, ob, out)
+    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+    s = off.size - 1
+    return {"n": n, "ms": ms, "bytes": 4 * n + 4 * (s + 1) + 4 * s}
+
+
+def bench_segmented_short_i32(hx, dev, args):
+    """Short segments (geometric, mean 4): the segment-parallel path."""
+    from oracle import oracle
+
+    n = 1 << 27
+    x = dev.alloc_uninitialized(np.int32, n)
+    dev.fill_uniform_int(x, seed=4, lo=-1000, hi=1000)
+    off = oracle.geometric_offsets(n, 4.0, seed=5)
     ob = dev.upload(off)
     out = dev.alloc_uninitialized(np.int32, off.size - 1)
     plan = hx.RocmSegmentedReductionOps().prepare_segmented_sum(dev, x, ob, out)
@@ -454,6 +471,13 @@ def cpu_secondary(name: str, seconds: float) -> dict | None:
         s = off.size - 1
         r = _cpu_rate(lambda: oracle.segmented_sum(x, off), 4.0 * n + 8.0 * s + 4, seconds)
         return line(*r, f"2^25 i32 values, {s} geometric(300) segments, oracle segmented_sum")
+    if name == "segmented_short_i32":
+        n = 1 << 25
+        x = oracle.uniform_int(n, 4, -1000, 1000, dtype=np.int32)
+        off = oracle.geometric_offsets(n, 4.0, seed=5)
+        s = off.size - 1
+        r = _cpu_rate(lambda: oracle.segmented_sum(x, off), 4.0 * n + 8.0 * s + 4, seconds)
+        return line(*r, f"2^25 i32 values, {s} geometric(4) segments, oracle segmented_sum")
     if name == "scan_f32_2_30":
         n = 1 << 23
         x = oracle.uniform_real(n, 6, 0.0, 1.0)
@@ -569,8 +593,8 @@ def main() -> int:
         },
     }
     if args.workload == "all":
-        for name in ("rows_f32", "segmented_i32", "scan_f32_2_30", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32",
-                     "colscan_u32"):
+        for name in ("rows_f32", "segmented_i32", "segmented_short_i32", "scan_f32_2_30", "copy_u32", "dot_f32",
+                     "axpy_f32", "colsum_f32", "colscan_u32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
             line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

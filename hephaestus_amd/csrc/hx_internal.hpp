@@ -191,6 +191,9 @@ struct SegmentedArgs {
     void *out;
 };
 uint64_t segmented_workspace_bytes(const SegmentedArgs &args);
+// False when the launch writes a worklist instead of look-back status words:
+// immediate calls then take the workspace from the separate scratch buffer.
+bool segmented_uses_lookback(const SegmentedArgs &args);
 hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_bytes,
                            LookbackState &st, hipStream_t stream);
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,

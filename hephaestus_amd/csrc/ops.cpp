@@ -437,7 +437,13 @@ hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, const vo
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, segmented_workspace_bytes(a), s, &ws));
+    const uint64_t bytes = segmented_workspace_bytes(a);
+    if (!segmented_uses_lookback(a)) {
+        HX_TRY(device_scratch(dev, bytes, &ws));
+        HX_TRY(launch_segmented(a, ws, bytes, dev->ws_lookback, s));
+        return ok();
+    }
+    HX_TRY(device_workspace(dev, bytes, s, &ws));
     HX_TRY(launch_segmented(a, ws, dev->ws_bytes, dev->ws_lookback, s));
     return ok();
 }

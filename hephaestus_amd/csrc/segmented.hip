@@ -22,6 +22,9 @@
 //      prefix, so a look-back almost always stops at the nearest
 //      predecessor.
 //
+// Segments averaging at most 14.5 values take a segment-parallel path instead
+// (seg_short_kernel below), which needs no look-back.
+//
 // Integer addition mod 2^32 is associative, so every output is bit-exact.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
@@ -471,6 +474,274 @@ __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Short segments (mean length n / S of at most kShortSpan / 512).  Cut by
+// elements, a tile of 8192 values holds hundreds to thousands of segment
+// ends, and segmented_sum_kernel spends its time ranking them in rounds of
+// kSlots.  Here the work is cut by SEGMENTS instead: block b takes the
+// SB = 256 * J consecutive segments [s0, s1), whose values are the one
+// contiguous span [off(s0), off(s1)).  The block loads the span's first
+// chunk (up to 8192 values, 16-byte loads from the 4-aligned element at or
+// below off(s0)), writes the chunk's inclusive prefix sums to LDS, and
+// thread t forms out[s] = P(end - 1) - P(start - 1) for s = s0 + t + 256 j:
+// offsets are read and outputs written coalesced, and no segment needs a
+// carry from another block.  J is the largest (up to 16) whose expected
+// span, 256 J n / S values, stays within kShortSpan.
+//
+// A span longer than one chunk (a long segment among short ones) is not
+// walked by one block: the block stores the first chunk's part of each of
+// its outputs (0 for segments that start later) and appends one worklist
+// entry per further chunk -- the segment that holds the chunk's first
+// element and that element's index -- and seg_short_drain_kernel adds each
+// chunk's part to its outputs with 32-bit atomics (exact: the sum is mod
+// 2^32 in any order).
+constexpr int kShortWaves = 4, kShortSteps = 8;
+constexpr int kShortThreads = kShortWaves * kWave;
+constexpr int kShortChunk = SegTile<kShortWaves, kShortSteps>::kElems; // values per chunk
+// Most values a block's expected span may hold: 8192 less about 2.4 standard
+// deviations of 512 geometric lengths of mean 14, so spans rarely overflow.
+constexpr uint64_t kShortSpan = 7424;
+constexpr int kShortMaxJ = 16;
+constexpr uint64_t kWorkHeader = 256; // worklist count, then entries
+constexpr uint32_t kDrainBlocks = 1280; // five 32 KiB-LDS blocks per CU
+
+struct ShortParams {
+    const uint32_t *values;
+    uint64_t n;
+    const uint32_t *offsets;
+    uint64_t segments; // S
+    uint32_t *out;
+    uint64_t seg_per_block;        // SB
+    unsigned long long *work_count; // entries appended this launch
+    uint2 *work;                    // (segment holding the chunk start, chunk start)
+    uint64_t work_cap;
+};
+
+__device__ __forceinline__ uint64_t short_off(const ShortParams &p, uint64_t k) {
+    const uint64_t o = p.offsets[k];
+    return o < p.n ? o : p.n;
+}
+
+// Values [lo, hi) of the chunk that starts at element `base` (base <= lo,
+// hi <= base + kShortChunk), zero elsewhere.  Each wave writes the inclusive
+// prefix sums (mod 2^32) of its 2048 values to s_p; after the barrier the
+// last word of each wave's quarter is that wave's total, so no other LDS is
+// needed (which keeps the block at exactly 32 KiB, five blocks per CU).
+struct ChunkCarry {
+    uint32_t w1, w2, w3; // sums of the chunk before waves 1, 2, 3
+};
+constexpr int kShortWaveElems = SegTile<kShortWaves, kShortSteps>::kWaveElems;
+static_assert(kShortWaves == 4 && kShortWaveElems == 2048, "chunk_prefix_at selects among four quarters");
+
+__device__ __forceinline__ ChunkCarry short_chunk_prefix(const uint32_t *values, uint64_t base, uint64_t lo,
+                                                         uint64_t hi, uint32_t *s_p) {
+    const int w = threadIdx.x / kWave;
+    const int lane = lane_id();
+    const uint64_t e0 = base + (uint64_t)w * kShortWaveElems + (uint64_t)lane * 4;
+    uint32_t x[kShortSteps][4];
+#pragma unroll
+    for (int j = 0; j < kShortSteps; ++j) {
+        const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+        if (e >= lo && e + 4 <= hi) {
+            const u32x4_a4 v = load_a4<true>((const u32x4_a4 *)(values + e));
+            x[j][0] = v.x;
+            x[j][1] = v.y;
+            x[j][2] = v.z;
+            x[j][3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[j][c] = (e + c >= lo && e + c < hi) ? values[e + c] : 0u;
+        }
+    }
+    uint32_t carry = 0;
+#pragma unroll
+    for (int j = 0; j < kShortSteps; ++j) {
+        const uint32_t p0 = x[j][0];
+        const uint32_t p1 = p0 + x[j][1];
+        const uint32_t p2 = p1 + x[j][2];
+        const uint32_t p3 = p2 + x[j][3];
+        const uint32_t incl = wave_inclusive_scan<OpSum, uint32_t>(p3);
+        const uint32_t base_j = carry + wave_shift_right<OpSum, uint32_t>(incl);
+        u32x4 v;
+        v.x = base_j + p0;
+        v.y = base_j + p1;
+        v.z = base_j + p2;
+        v.w = base_j + p3;
+        *(u32x4 *)&s_p[w * kShortWaveElems + j * (kWave * 4) + lane * 4] = v;
+        carry += read_lane(incl, kWave - 1);
+    }
+    __syncthreads();
+    const uint32_t t0 = s_p[kShortWaveElems - 1], t1 = s_p[2 * kShortWaveElems - 1],
+                   t2 = s_p[3 * kShortWaveElems - 1];
+    return ChunkCarry{t0, t0 + t1, t0 + t1 + t2};
+}
+
+// Inclusive prefix of the chunk at local index i.
+__device__ __forceinline__ uint32_t chunk_prefix_at(const uint32_t *s_p, const ChunkCarry &c, uint32_t i) {
+    const uint32_t q = i / kShortWaveElems;
+    const uint32_t add = q == 0 ? 0u : (q == 1 ? c.w1 : (q == 2 ? c.w2 : c.w3));
+    return s_p[i] + add;
+}
+
+// Sum of chunk-local elements [l, h), 0 <= l <= h <= kShortChunk.
+__device__ __forceinline__ uint32_t chunk_range_sum(const uint32_t *s_p, const ChunkCarry &c, uint32_t l, uint32_t h) {
+    if (h <= l) return 0u;
+    uint32_t v = chunk_prefix_at(s_p, c, h - 1);
+    if (l > 0) v -= chunk_prefix_at(s_p, c, l - 1);
+    return v;
+}
+
+// Chunks [c_lo, c_lo + count) of segment s go to worklist entries
+// [slot, slot + count); chunk c starts at element base + c * kShortChunk.
+// `base` is block-uniform.  Short ranges are written by their lane; the wave
+// writes longer ones together, one range at a time.
+__device__ __forceinline__ void short_write_entries(const ShortParams &p, uint64_t slot, uint64_t base, uint32_t s,
+                                                    uint32_t c_lo, uint32_t count) {
+    const int lane = lane_id();
+    const bool big = count > kDirectEdges;
+    if (!big)
+        for (uint32_t i = 0; i < count; ++i)
+            if (slot + i < p.work_cap)
+                p.work[slot + i] = make_uint2(s, (uint32_t)(base + (uint64_t)(c_lo + i) * kShortChunk));
+    uint64_t pending = ballot(big);
+    while (pending) { // wave-uniform
+        const int j = __ffsll((long long)pending) - 1;
+        pending &= pending - 1;
+        const uint32_t lo = read_lane(c_lo, j), cnt = read_lane(count, j), sj = read_lane(s, j);
+        const uint64_t sl = ((uint64_t)read_lane((uint32_t)(slot >> 32), j) << 32) | read_lane((uint32_t)slot, j);
+        for (uint32_t i = (uint32_t)lane; i < cnt; i += kWave)
+            if (sl + i < p.work_cap)
+                p.work[sl + i] = make_uint2(sj, (uint32_t)(base + (uint64_t)(lo + i) * kShortChunk));
+    }
+}
+
+__global__ void seg_short_init_kernel(unsigned long long *work_count) { *work_count = 0ull; }
+
+// Chunks of the span [a0, a1) whose first element lies in the segment part
+// [l, h): c in [ceil((l - base) / chunk), ceil((h - base) / chunk)), from 1.
+__device__ __forceinline__ void short_chunk_range(uint64_t base, uint64_t l, uint64_t h, uint64_t chunks,
+                                                  uint32_t &c_lo, uint32_t &count) {
+    c_lo = 1;
+    count = 0;
+    if (h <= l) return;
+    uint64_t c0 = (l - base + kShortChunk - 1) / kShortChunk, c1 = (h - base + kShortChunk - 1) / kShortChunk;
+    if (c0 < 1) c0 = 1;
+    if (c1 > chunks) c1 = chunks;
+    if (c1 > c0) {
+        c_lo = (uint32_t)c0;
+        count = (uint32_t)(c1 - c0);
+    }
+}
+
+template <int J>
+__global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p) {
+    __shared__ __align__(16) uint32_t s_p[kShortChunk];
+    constexpr uint64_t SB = (uint64_t)J * kShortThreads;
+    const int lane = lane_id();
+    const uint64_t s0 = (uint64_t)blockIdx.x * SB;
+    const uint64_t s1 = s0 + SB < p.segments ? s0 + SB : p.segments;
+    const uint64_t a0 = short_off(p, s0);
+    uint64_t a1 = short_off(p, s1);
+    if (a1 < a0) a1 = a0; // only reachable with malformed offsets
+    const uint64_t base = a0 & ~3ull;
+    const uint64_t c1 = a1 < base + kShortChunk ? a1 : base + kShortChunk;
+
+    // This thread's segments s0 + t + 256 j.  Their offsets are loaded here
+    // but first used after the value loads are issued, so both arrive in one
+    // memory round trip.
+    // A segment's end is the next lane's start; the end of lane 63's segment
+    // in group j is loaded by lane j of the wave into one register.
+    uint32_t lo[J], hi[J];
+    const uint64_t wave_s = s0 + (threadIdx.x & ~(kWave - 1));
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
+        lo[j] = s <= s1 ? p.offsets[s] : 0u; // s == s1: the last segment's end
+    }
+    const uint64_t edge_k = wave_s + (uint64_t)lane * kShortThreads + kWave;
+    const uint32_t edge = (lane < J && edge_k <= s1) ? p.offsets[edge_k] : 0u;
+    const ChunkCarry cc = short_chunk_prefix(p.values, base, a0, c1, s_p);
+    // Clamped into the span (only malformed offsets are changed).
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t next = __shfl_down(lo[j], 1);
+        const uint32_t e = lane == kWave - 1 ? read_lane(edge, j) : next;
+        const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
+        const uint64_t st = lo[j] < a0 ? a0 : (lo[j] > a1 ? a1 : lo[j]);
+        const uint64_t en = (s >= s1 || e < st) ? st : (e > a1 ? a1 : e);
+        lo[j] = (uint32_t)st;
+        hi[j] = (uint32_t)en;
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
+        if (s < s1) {
+            const uint64_t h = hi[j] < c1 ? hi[j] : c1;
+            const uint64_t l = lo[j] < h ? lo[j] : h;
+            p.out[s] = chunk_range_sum(s_p, cc, (uint32_t)(l - base), (uint32_t)(h - base));
+        }
+    }
+    if (a1 <= base + kShortChunk) return; // block-uniform
+    // Chunks 1 .. chunks-1 go to the worklist: the entry of the chunk that
+    // starts at element e is written by the lane whose segment holds e, at
+    // slots each wave reserves with one atomic.
+    const uint64_t chunks = (a1 - base + kShortChunk - 1) / kShortChunk;
+    uint32_t lane_total = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        uint32_t c_lo, count;
+        short_chunk_range(base, lo[j], hi[j], chunks, c_lo, count);
+        lane_total += count;
+    }
+    const uint32_t incl = wave_inclusive_scan<OpSum, uint32_t>(lane_total);
+    const uint32_t wave_total = read_lane(incl, kWave - 1);
+    if (wave_total == 0) return; // wave-uniform
+    unsigned long long first = 0;
+    if (lane == 0) first = atomicAdd(p.work_count, (unsigned long long)wave_total);
+    first = ((uint64_t)read_lane((uint32_t)(first >> 32), 0) << 32) | read_lane((uint32_t)first, 0);
+    uint64_t slot = first + (incl - lane_total);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        uint32_t c_lo, count;
+        short_chunk_range(base, lo[j], hi[j], chunks, c_lo, count);
+        const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
+        short_write_entries(p, slot, base, (uint32_t)s, c_lo, count);
+        slot += count;
+    }
+}
+
+// Adds each deferred chunk's part to the outputs of the segments that
+// overlap it.  Grid-strided over the entries, so every block reaches the end
+// whatever the count; entries beyond the workspace (possible only with
+// malformed offsets) are dropped.
+__global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortParams p) {
+    __shared__ __align__(16) uint32_t s_p[kShortChunk];
+    uint64_t count = *p.work_count;
+    if (count > p.work_cap) count = p.work_cap;
+    for (uint64_t i = blockIdx.x; i < count; i += gridDim.x) { // block-uniform
+        const uint2 e = p.work[i];
+        if (e.x >= p.segments) continue;
+        const uint64_t sf = e.x, c0 = e.y;
+        const uint64_t s1b = (sf / p.seg_per_block + 1) * p.seg_per_block;
+        const uint64_t s1 = s1b < p.segments ? s1b : p.segments;
+        const uint64_t a1 = short_off(p, s1);
+        const uint64_t c1 = c0 + kShortChunk < a1 ? c0 + kShortChunk : a1;
+        if (c0 >= c1) continue;
+        const ChunkCarry cc = short_chunk_prefix(p.values, c0, c0, c1, s_p);
+        for (uint64_t s = sf + threadIdx.x; s < s1; s += kShortThreads) {
+            const uint64_t st = short_off(p, s);
+            if (st >= c1) break; // offsets are sorted: so do all later segments
+            const uint64_t en = short_off(p, s + 1);
+            const uint64_t l = st > c0 ? st : c0, h = en < c1 ? en : c1;
+            if (h > l) {
+                const uint32_t v = chunk_range_sum(s_p, cc, (uint32_t)(l - c0), (uint32_t)(h - c0));
+                if (v) atomicAdd(&p.out[s], v);
+            }
+        }
+        __syncthreads(); // s_p is rewritten by the next entry
+    }
+}
+
 // n == 0: every segment is empty.
 __global__ void segmented_zero_kernel(uint32_t *out, uint64_t s) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < s;
@@ -491,8 +762,76 @@ __global__ void validate_offsets_kernel(const uint32_t *offsets, uint64_t count,
 
 } // namespace
 
-// Look-back status words (8 bytes per tile), then the two tile maps.
+namespace {
+
+// Taken when a block can hold two segments per thread, mean n / S up to
+// kShortSpan / 512 = 14.5: at 2^27 values it beats the element tiles from
+// 4.5x (mean 1) to 1.4x (mean 12); at one segment per thread the two paths
+// tie (mean 16: 141 us each).
+bool short_path(const SegmentedArgs &a) {
+    return a.num_segments > 0 && a.n > 0 && 2 * (uint64_t)kShortThreads * a.n <= kShortSpan * a.num_segments;
+}
+
+// Segments per thread: the largest J up to kShortMaxJ that keeps a block's
+// expected span (256 J n / S values) within kShortSpan.
+int short_j(const SegmentedArgs &a) {
+    int j = 1;
+    while (j < kShortMaxJ && (uint64_t)(j + 1) * kShortThreads * a.n <= kShortSpan * a.num_segments) ++j;
+    return j;
+}
+
+uint64_t short_blocks(const SegmentedArgs &a) {
+    return ceil_div(a.num_segments, (uint64_t)short_j(a) * kShortThreads);
+}
+
+// Every block defers at most ceil((span + 3) / chunk) - 1 < (span + 3) / chunk
+// chunks, and the spans of sorted offsets add up to n.
+uint64_t short_work_cap(const SegmentedArgs &a) {
+    return (a.n + 3 * short_blocks(a)) / kShortChunk + 1;
+}
+
+template <int J> hx_status launch_short_j(int j, const ShortParams &p, uint64_t blocks, hipStream_t stream) {
+    if constexpr (J > kShortMaxJ) {
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce: no kernel for %d segments per thread", j);
+    } else {
+        if (j != J) return launch_short_j<J + 1>(j, p, blocks, stream);
+        hipLaunchKernelGGL((seg_short_kernel<J>), dim3((uint32_t)blocks), dim3(kShortThreads), 0, stream, p);
+        return check_launch("seg_short_kernel");
+    }
+}
+
+hx_status launch_short(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    ShortParams p{};
+    p.values = (const uint32_t *)a.values;
+    p.n = a.n;
+    p.offsets = a.offsets;
+    p.segments = a.num_segments;
+    p.out = (uint32_t *)a.out;
+    const int j = short_j(a);
+    p.seg_per_block = (uint64_t)j * kShortThreads;
+    p.work_count = (unsigned long long *)ws;
+    p.work = (uint2 *)((char *)ws + kWorkHeader);
+    p.work_cap = short_work_cap(a);
+    if (ws_bytes < kWorkHeader + p.work_cap * sizeof(uint2))
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
+                    (unsigned long long)ws_bytes);
+    const uint64_t blocks = short_blocks(a);
+    hipLaunchKernelGGL(seg_short_init_kernel, dim3(1), dim3(1), 0, stream, p.work_count);
+    HX_TRY(check_launch("seg_short_init_kernel"));
+    HX_TRY(launch_short_j<1>(j, p, blocks, stream));
+    const uint64_t drain = p.work_cap < kDrainBlocks ? p.work_cap : kDrainBlocks;
+    hipLaunchKernelGGL(seg_short_drain_kernel, dim3((uint32_t)drain), dim3(kShortThreads), 0, stream, p);
+    return check_launch("seg_short_drain_kernel");
+}
+
+} // namespace
+
+bool segmented_uses_lookback(const SegmentedArgs &a) { return !short_path(a); }
+
+// Look-back path: status words (8 bytes per tile), then the two tile maps.
+// Short path: the worklist.
 uint64_t segmented_workspace_bytes(const SegmentedArgs &a) {
+    if (short_path(a)) return kWorkHeader + short_work_cap(a) * sizeof(uint2);
     const uint64_t tiles = ceil_div(a.n, kTile);
     return kLookbackOffset + tiles * 8 + 2 * (tiles + 1) * 4;
 }
@@ -507,6 +846,12 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
                            (uint32_t *)a.out, a.num_segments);
         return check_launch("segmented_zero_kernel");
     }
+    if (a.num_segments >= 0xFFFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu segments exceeds the u32 offset range",
+                    (unsigned long long)a.num_segments);
+    if (((uintptr_t)a.values) % 4 != 0)
+        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 4-byte aligned");
+    if (short_path(a)) return launch_short(a, ws, ws_bytes, stream);
     SegParams p{};
     p.values = (const uint32_t *)a.values;
     p.n = a.n;
@@ -517,14 +862,9 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
     p.ub_map = (uint32_t *)(p.status + p.total_tiles);
     p.lb_map = p.ub_map + p.total_tiles + 1;
-    if (a.num_segments >= 0xFFFFFFFFull)
-        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu segments exceeds the u32 offset range",
-                    (unsigned long long)a.num_segments);
     if (p.total_tiles >= 0x80000000ull)
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
-    if (((uintptr_t)a.values) % 4 != 0)
-        return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce values must be 4-byte aligned");
     if (ws_bytes < segmented_workspace_bytes(a))
         return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);

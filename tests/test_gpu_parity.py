@@ -508,6 +508,102 @@ def test_segmented_sum_geometric(device, oracle, n, mean):
     assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
 
 
+# Mean segment lengths up to 14.5 take the segment-parallel path: blocks of
+# 256 * J consecutive segments (J = 16, 16, 14, 7, 3 at means 0.5 to 8), a
+# span of up to 8192 values per block, longer spans deferred to a chunk
+# worklist; means 16 and 17 take the element-tile path beside them.
+@pytest.mark.parametrize("mean", [0.5, 1.0, 2.0, 4.0, 8.0, 16.0, 17.0])
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32])
+def test_segmented_sum_short_segments(device, oracle, mean, dtype):
+    n = (1 << 20) + 13
+    x = oracle.uniform_int(n, seed=int(mean * 10), lo=0, hi=1 << 31, dtype=np.uint32).view(dtype)
+    off = oracle.geometric_offsets(n, mean, seed=int(mean * 10) + 1)
+    assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
+
+
+def _short_with_long(n, mean, longs, seed):
+    """Geometric offsets of the given mean with the cuts inside each
+    [start, start + length) of `longs` removed: long segments among short
+    ones, so a block's span exceeds one 8192-value chunk."""
+    rng = np.random.default_rng(seed)
+    cuts = np.flatnonzero(rng.random(n - 1) < 1.0 / mean) + 1
+    keep = np.ones(cuts.size, bool)
+    for start, length in longs:
+        keep &= ~((cuts > start) & (cuts < start + length))
+    extra = [v for start, length in longs for v in (start, start + length) if 0 < v < n]
+    cuts = np.unique(np.concatenate([cuts[keep], np.array(extra, np.int64)]))
+    return np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+
+
+SHORT_LONG_CASES = [
+    ((1 << 21) + 5, 2.0, [(1 << 20, 1 << 19)]),                      # one long segment mid-stream
+    ((1 << 21) + 5, 4.0, [(100, 8192 - 100), (20000, 8193), (40000, 16384 * 3 + 1)]),
+    ((1 << 20), 1.0, [(0, 8192), (8192, 8192), (16384, 1)]),         # exact chunk-sized segments at 0
+    ((1 << 20), 3.0, [(5000, 9000), (14001, 9000), (23002, 9000)]),  # several long ones in one block
+    ((1 << 20) + 1, 1.0, [(0, 1 << 19)]),                            # half of everything in one segment
+]
+
+
+@pytest.mark.parametrize("n,mean,longs", SHORT_LONG_CASES)
+def test_segmented_sum_short_with_long_segments(device, oracle, n, mean, longs):
+    x = oracle.uniform_int(n, seed=n % 1000, lo=-1 << 30, hi=1 << 30, dtype=np.int32)
+    off = _short_with_long(n, mean, longs, seed=n % 997)
+    assert 512 * n <= 7424 * (off.size - 1), "case must take the short path"
+    assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
+
+
+def test_segmented_short_path_empty_segments_around_one_long(device, oracle):
+    """All values in one segment between 2^17 empty segments on each side:
+    the mean is 8, so the short path takes it, and the one block holding
+    the long segment defers 255 chunks, written by its wave together."""
+    n = 1 << 21
+    x = oracle.uniform_int(n, seed=35, lo=0, hi=1 << 20)
+    off = np.concatenate([np.zeros(1 << 17, np.uint32), np.full(1 << 17, n, np.uint32)])
+    got = _segmented(device, x, off)
+    assert np.array_equal(got, oracle.segmented_sum(x, off))
+    assert got[(1 << 17) - 1] == np.uint32(oracle.segmented_sum(x, np.array([0, n], np.uint32))[0])
+
+
+def test_segmented_short_path_repeated_calls(device, oracle):
+    """The deferred-chunk count is cleared by every call: back-to-back calls
+    with different inputs, the second smaller, on the shared scratch."""
+    for seed, n in ((1, (1 << 21) + 5), (2, (1 << 19) + 3), (3, (1 << 21) + 5)):
+        x = oracle.uniform_int(n, seed=seed, lo=-1000, hi=1000, dtype=np.int32)
+        off = _short_with_long(n, 2.0, [(n // 3, n // 4), (n // 2, 20000)], seed=seed)
+        assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), seed
+
+
+def test_prepared_segmented_sum_short_path(device, oracle):
+    n = (1 << 20) + 7
+    x = oracle.uniform_int(n, seed=31, lo=-1000, hi=1000, dtype=np.int32)
+    off = _short_with_long(n, 4.0, [(7000, 50000)], seed=31)
+    vb, ob = device.upload(x), device.upload(off)
+    out = device.alloc_zeroed(np.int32, off.size - 1)
+    plan = SEG.prepare_segmented_sum(device, vb, ob, out)
+    assert plan.workspace_bytes() > 0
+    for _ in range(3):
+        plan.dispatch()
+    assert np.array_equal(device.download_owned(out), oracle.segmented_sum(x, off))
+    y = oracle.uniform_int(n, seed=32, lo=-1000, hi=1000, dtype=np.int32)
+    device.write_buffer(vb, y)
+    plan.dispatch()
+    assert np.array_equal(device.download_owned(out), oracle.segmented_sum(y, off))
+
+
+def test_segmented_short_path_malformed_offsets_stay_in_bounds(device, oracle):
+    """Decreasing offsets and offsets beyond n on the short path: the call
+    completes without a fault, and a well-formed call afterwards is exact."""
+    n = 100000
+    x = oracle.uniform_int(n, seed=33, lo=0, hi=10)
+    off = np.arange(0, n + 1, 2, dtype=np.uint32)
+    off[100:5000:7] = 3
+    off[6000:9000:5] = 4000000000
+    off[20000] = n + 12345
+    _segmented(device, x, off)
+    good = oracle.geometric_offsets(n, 2.0, seed=34)
+    assert np.array_equal(_segmented(device, x, good), oracle.segmented_sum(x, good))
+
+
 def test_segmented_sum_16k_tile_edges(device, oracle):
     """Segmented tiles hold 16384 values: boundaries on and beside tile
     edges, empty segments at an edge, a segment spanning several tiles (the
@@ -528,16 +624,18 @@ def test_segmented_sum_16k_tile_edges(device, oracle):
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
+@pytest.mark.parametrize("cuts_n", [300, 12000])
 @pytest.mark.parametrize("skew", [1, 2, 3])
-def test_segmented_sum_values_off_16_byte_boundaries(device, oracle, skew):
+def test_segmented_sum_values_off_16_byte_boundaries(device, oracle, skew, cuts_n):
     """Values handed over as a raw pointer at an element offset: the tile loads
-    are 16-byte vectors that need only 4-byte alignment."""
+    are 16-byte vectors that need only 4-byte alignment (300 cuts: the
+    element-tile path; 12000: the short-segment path)."""
     from hephaestus_amd import _ffi
 
     n = 3 * 8192 + 77
     x = oracle.uniform_int(n + skew, seed=skew, lo=-1000, hi=1000, dtype=np.int32)
     rng = np.random.default_rng(skew)
-    cuts = np.sort(rng.choice(np.arange(1, n), size=300, replace=False))
+    cuts = np.sort(rng.choice(np.arange(1, n), size=cuts_n, replace=False))
     offsets = np.concatenate([[0], cuts, [n]]).astype(np.uint32)
     vb = device.upload(x)
     ob = device.upload(offsets)
