@@ -190,12 +190,16 @@ struct SegmentedArgs {
     uint64_t num_segments; // S (num_offsets - 1)
     void *out;
 };
+// Immediate calls take the look-back status words from the shared look-back
+// workspace and everything else (tile maps, worklists) from the separate
+// scratch buffer, so no other data ever lands where a later launch reads
+// status words.  A prepared plan holds both in one workspace of
+// segmented_workspace_bytes and passes aux = nullptr.
+uint64_t segmented_lookback_bytes(const SegmentedArgs &args);
+uint64_t segmented_aux_bytes(const SegmentedArgs &args);
 uint64_t segmented_workspace_bytes(const SegmentedArgs &args);
-// False when the launch writes a worklist instead of look-back status words:
-// immediate calls then take the workspace from the separate scratch buffer.
-bool segmented_uses_lookback(const SegmentedArgs &args);
-hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_bytes,
-                           LookbackState &st, hipStream_t stream);
+hx_status launch_segmented(const SegmentedArgs &args, void *ws, uint64_t ws_bytes, void *aux,
+                           uint64_t aux_bytes, LookbackState &st, hipStream_t stream);
 hx_status validate_offsets_on_device(hx_device *dev, const uint32_t *offsets,
                                      uint64_t num_offsets, uint64_t n);
 

@@ -232,7 +232,7 @@ hx_status plan_segmented(hx_op op, hx_dtype dtype, const void *values, uint64_t 
 struct SegmentedPlan final : hx_plan {
     SegmentedArgs args;
     hx_status dispatch(hipStream_t stream) override {
-        return launch_segmented(args, ws, ws_bytes, lookback, stream);
+        return launch_segmented(args, ws, ws_bytes, nullptr, 0, lookback, stream);
     }
 };
 
@@ -436,15 +436,11 @@ hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, const vo
     HX_TRY(plan_segmented(op, dtype, values, n, offsets, num_offsets, out, out_len, &a));
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
-    void *ws = nullptr;
-    const uint64_t bytes = segmented_workspace_bytes(a);
-    if (!segmented_uses_lookback(a)) {
-        HX_TRY(device_scratch(dev, bytes, &ws));
-        HX_TRY(launch_segmented(a, ws, bytes, dev->ws_lookback, s));
-        return ok();
-    }
-    HX_TRY(device_workspace(dev, bytes, s, &ws));
-    HX_TRY(launch_segmented(a, ws, dev->ws_bytes, dev->ws_lookback, s));
+    void *ws = nullptr, *aux = nullptr;
+    const uint64_t lookback = segmented_lookback_bytes(a), aux_bytes = segmented_aux_bytes(a);
+    HX_TRY(device_scratch(dev, aux_bytes, &aux));
+    if (lookback) HX_TRY(device_workspace(dev, lookback, s, &ws));
+    HX_TRY(launch_segmented(a, ws, lookback ? dev->ws_bytes : 0, aux, aux_bytes, dev->ws_lookback, s));
     return ok();
 }
 

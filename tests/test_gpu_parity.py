@@ -604,6 +604,64 @@ def test_segmented_short_path_malformed_offsets_stay_in_bounds(device, oracle):
     assert np.array_equal(_segmented(device, x, good), oracle.segmented_sum(x, good))
 
 
+def _crowded(n, mean, clusters, seed):
+    """Geometric offsets of the given mean plus runs of empty segments:
+    `clusters` holds (position, count) pairs; after each run, 200 short
+    segments of 1..150 values start at the position (summed by the excess
+    kernel when the run crowds their tile)."""
+    rng = np.random.default_rng(seed)
+    cuts = list(np.flatnonzero(rng.random(n - 1) < 1.0 / mean) + 1)
+    for pos, count in clusters:
+        cuts += [pos] * count
+        cuts += list(pos + np.cumsum(rng.integers(1, 151, 200)))
+    cuts = np.sort(np.array([c for c in cuts if 0 <= c <= n], np.int64))
+    return np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+
+
+CROWDED_CASES = [
+    ("trailing empties", [((1 << 22) + 5, 1 << 17)]),
+    ("leading empties", [(0, 1 << 17)]),
+    ("mid-tile run", [(3 * 8192 + 1000, 50000)]),
+    ("runs at a tile edge and mid-tile", [(5 * 8192, 9000), (9 * 8192 + 77, 4097), (20 * 8192 + 5, 4095)]),
+]
+
+
+@pytest.mark.parametrize("name,clusters", CROWDED_CASES, ids=[c[0] for c in CROWDED_CASES])
+def test_segmented_sum_crowded_tiles(device, oracle, name, clusters):
+    """Tiles with more than 4096 segment ends (runs of empty segments) at a
+    mean above the short-path limit: the element-tile path hands the excess
+    ends to seg_excess_kernel, and empties at offset 0 are written by the
+    tile map kernel."""
+    n = (1 << 22) + 5
+    x = oracle.uniform_int(n, seed=len(name), lo=-1 << 30, hi=1 << 30, dtype=np.int32)
+    off = _crowded(n, 300.0, clusters, seed=len(name))
+    assert 512 * n > 7424 * (off.size - 1), "case must take the element-tile path"
+    assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
+
+
+def test_prepared_segmented_sum_crowded_tile(device, oracle):
+    n = (1 << 22) + 5
+    x = oracle.uniform_int(n, seed=41, lo=-1000, hi=1000, dtype=np.int32)
+    off = _crowded(n, 300.0, [(7 * 8192 + 3, 30000)], seed=41)
+    vb, ob = device.upload(x), device.upload(off)
+    out = device.alloc_zeroed(np.int32, off.size - 1)
+    plan = SEG.prepare_segmented_sum(device, vb, ob, out)
+    for _ in range(3):
+        plan.dispatch()
+    assert np.array_equal(device.download_owned(out), oracle.segmented_sum(x, off))
+
+
+def test_segmented_crowded_malformed_offsets_stay_in_bounds(device, oracle):
+    """A crowded tile whose offsets decrease: the call completes without a
+    fault, and a well-formed call afterwards is exact."""
+    n = 1 << 20
+    x = oracle.uniform_int(n, seed=42, lo=0, hi=10)
+    off = np.concatenate([[0], np.full(10000, 5000), np.full(10000, 3000), [n]]).astype(np.uint32)
+    _segmented(device, x, off)
+    good = oracle.geometric_offsets(n, 300.0, seed=43)
+    assert np.array_equal(_segmented(device, x, good), oracle.segmented_sum(x, good))
+
+
 def test_segmented_sum_16k_tile_edges(device, oracle):
     """Segmented tiles hold 16384 values: boundaries on and beside tile
     edges, empty segments at an edge, a segment spanning several tiles (the
