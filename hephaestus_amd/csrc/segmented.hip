@@ -59,16 +59,13 @@ struct SegParams {
     uint64_t *status;          // look-back words, one per tile
     uint32_t *ub_map, *lb_map; // tile edges -> offset indices (total_tiles + 1 each)
     uint32_t tag;              // this launch's status tag
-    unsigned long long *work_count; // excess-end entries appended this launch
-    uint2 *work;                    // (tile, first offset index of kEndChunk ends)
-    uint64_t work_cap;
 };
 // A tile whose segment ends number more than kEndCap (only possible with runs
-// of empty segments) handles the first kEndCap itself and hands the rest, in
-// entries of kEndChunk ends, to seg_excess_kernel.  Every excess segment lies
-// inside the tile, after the tile's first end, so its sum needs neither the
-// tile's prefixes nor its marks.
-constexpr uint64_t kEndCap = 4096, kEndChunk = 4096;
+// of empty segments) handles the first kEndCap itself; seg_tile_map_kernel
+// sums the rest beforehand.  Every such excess segment lies inside its tile,
+// after the tile's first end, so its sum needs neither the tile's prefixes
+// nor its marks.
+constexpr uint64_t kEndCap = 4096;
 
 // Offsets clamped into [0, n]: malformed offsets can never address values
 // out of bounds.
@@ -354,16 +351,6 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
         marks += pk;
     }
 
-    // Excess ends go to the worklist: wave 0 reserves the entries with one
-    // atomic and writes them together.
-    if (k_hi1 > k_end && w == 0) {
-        const uint64_t entries = (k_hi1 - k_end + kEndChunk - 1) / kEndChunk;
-        unsigned long long first = 0;
-        if (lane == 0) first = atomicAdd(p.work_count, (unsigned long long)entries);
-        first = ((uint64_t)read_lane((uint32_t)(first >> 32), 0) << 32) | read_lane((uint32_t)first, 0);
-        for (uint64_t i = (uint64_t)lane; i < entries; i += kWave)
-            if (first + i < p.work_cap) p.work[first + i] = make_uint2((uint32_t)tile, (uint32_t)(k_end + i * kEndChunk));
-    }
 
     // Marked positions are segment ends, so the tile-local prefix at a
     // segment's start is the value at the previous mark: a segment's sum is
@@ -456,6 +443,43 @@ __device__ __forceinline__ void map_write_edges(uint32_t *map, uint32_t first, u
     }
 }
 
+// Segment k - 1 = [lo, hi) ends in the tile of element hi - 1, starting at
+// t0.  It is an excess end of that tile (beyond the first kEndCap ends,
+// which the tile's block handles) exactly when off(k - kEndCap) > t0, since
+// the tile's first end is the first k' with off(k') > t0.  Such a segment
+// lies inside the tile: a lane sums up to kWave values itself, the wave sums
+// longer ones together, one at a time.  Called wave-uniformly.
+template <int TILE>
+__device__ __forceinline__ void excess_sums(const SegParams &p, uint64_t k, uint64_t lo, uint64_t hi) {
+    const int lane = lane_id();
+    uint64_t a = 0;
+    uint32_t len = 0;
+    bool mine = false;
+    if (k >= kEndCap && k <= p.segments && hi > 0) {
+        const uint64_t t0 = (hi - 1) / TILE * TILE;
+        if (off_at(p, k - kEndCap) > t0) {
+            mine = true;
+            a = lo < t0 ? t0 : (lo > hi ? hi : lo); // clamps only malformed offsets
+            len = (uint32_t)(hi - a);
+        }
+    }
+    uint32_t sum = 0;
+    if (len <= (uint32_t)kWave)
+        for (uint32_t j = 0; j < len; ++j) sum += p.values[a + j];
+    uint64_t pending = ballot(len > (uint32_t)kWave);
+    while (pending) { // wave-uniform
+        const int j = __ffsll((long long)pending) - 1;
+        pending &= pending - 1;
+        const uint64_t aj = ((uint64_t)read_lane((uint32_t)(a >> 32), j) << 32) | read_lane((uint32_t)a, j);
+        const uint32_t lj = read_lane(len, j);
+        uint32_t part = 0;
+        for (uint32_t q = (uint32_t)lane; q < lj; q += kWave) part += p.values[aj + q];
+        part = wave_sum(part);
+        if (lane == j) sum = part;
+    }
+    if (mine) p.out[k - 1] = sum;
+}
+
 template <int TILE>
 __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
     const uint64_t tiles = p.total_tiles;
@@ -463,10 +487,10 @@ __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
     const int lane = lane_id();
     const uint64_t wave = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
     const uint64_t nwaves = (uint64_t)gridDim.x * (kBlock / kWave);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *p.work_count = 0ull; // before segmented_sum_kernel runs
     for (uint64_t base = wave * kWave; base <= S + 1; base += nwaves * kWave) { // wave-uniform
         const uint64_t k = base + (uint64_t)lane;
         uint32_t ua = 0, un = 0, la = 0, ln = 0;
+        uint64_t ex_lo = 0, ex_hi = 0; // segment k - 1, for k in [1, S]
         if (k <= S + 1) {
             const uint64_t lo = k == 0 ? 0 : off_at(p, k - 1);
             const uint64_t hi = k <= S ? off_at(p, k) : p.n + 1; // off_at clamps into [0, n]
@@ -490,9 +514,14 @@ __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
             if ((k == 0 || lo < p.n) && p.n <= hi) p.lb_map[tiles] = (uint32_t)k;
             // Segments that end at offset 0 are empty and end in no tile.
             if (k >= 1 && k <= S && hi == 0) p.out[k - 1] = 0u;
+            if (k >= 1 && k <= S) {
+                ex_lo = lo;
+                ex_hi = hi;
+            }
         }
         map_write_edges(p.ub_map, ua, un, (uint32_t)k);
         map_write_edges(p.lb_map, la, ln, (uint32_t)k);
+        excess_sums<TILE>(p, k, ex_lo, ex_hi);
     }
 }
 
@@ -764,52 +793,6 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortPar
     }
 }
 
-// Sums of the excess segments of crowded tiles.  Entry (u, k0) covers ends
-// k in [k0, min(k0 + kEndChunk, ub(t1))) of tile u; segment k - 1 is
-// [off(k - 1), off(k)), inside the tile.  A lane sums a segment of up to
-// kWave values itself; the wave sums longer ones together, one at a time.
-// Grid-strided over the entries, so every block reaches the end.
-__global__ __launch_bounds__(kBlock) void seg_excess_kernel(SegParams p) {
-    const int lane = lane_id();
-    uint64_t count = *p.work_count;
-    if (count > p.work_cap) count = p.work_cap;
-    for (uint64_t i = blockIdx.x; i < count; i += gridDim.x) { // block-uniform
-        const uint2 e = p.work[i];
-        const uint64_t u = e.x < p.total_tiles ? e.x : p.total_tiles - 1;
-        const uint64_t t0 = u * kTile, t1 = t0 + kTile < p.n ? t0 + kTile : p.n;
-        uint64_t k_hi1 = p.ub_map[u + 1];
-        k_hi1 = k_hi1 < p.segments + 1 ? k_hi1 : p.segments + 1;
-        const uint64_t k_stop = (uint64_t)e.y + kEndChunk < k_hi1 ? (uint64_t)e.y + kEndChunk : k_hi1;
-        for (uint64_t kb = e.y; kb < k_stop; kb += kBlock) { // block-uniform
-            const uint64_t k = kb + threadIdx.x;
-            uint64_t a = 0, b = 0;
-            const bool mine = k < k_stop && k >= 1;
-            if (mine) {
-                b = off_at(p, k);
-                a = off_at(p, k - 1);
-                b = b < t0 ? t0 : (b > t1 ? t1 : b); // clamps only malformed offsets
-                a = a < t0 ? t0 : (a > b ? b : a);
-            }
-            const uint32_t len = (uint32_t)(b - a);
-            uint32_t sum = 0;
-            if (len <= (uint32_t)kWave)
-                for (uint32_t j = 0; j < len; ++j) sum += p.values[a + j];
-            uint64_t pending = ballot(len > (uint32_t)kWave);
-            while (pending) { // wave-uniform
-                const int j = __ffsll((long long)pending) - 1;
-                pending &= pending - 1;
-                const uint64_t aj = ((uint64_t)read_lane((uint32_t)(a >> 32), j) << 32) | read_lane((uint32_t)a, j);
-                const uint32_t lj = read_lane(len, j);
-                uint32_t part = 0;
-                for (uint32_t q = (uint32_t)lane; q < lj; q += kWave) part += p.values[aj + q];
-                part = wave_sum(part);
-                if (lane == j) sum = part;
-            }
-            if (mine) p.out[k - 1] = sum;
-        }
-    }
-}
-
 // n == 0: every segment is empty.
 __global__ void segmented_zero_kernel(uint32_t *out, uint64_t s) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < s;
@@ -896,10 +879,6 @@ hx_status launch_short(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, hipS
 
 namespace {
 uint64_t align256(uint64_t b) { return (b + 255) & ~255ull; }
-// Entries of kEndChunk ends: a tile with E > kEndCap ends appends
-// ceil((E - kEndCap) / kEndChunk) <= E / kEndChunk, and the tiles' ends add
-// up to at most S + 1 + tiles.
-uint64_t tile_work_cap(uint64_t segments, uint64_t tiles) { return (segments + 1 + tiles) / kEndChunk + 1; }
 uint64_t tile_map_bytes(uint64_t tiles) { return align256(2 * (tiles + 1) * 4); }
 } // namespace
 
@@ -911,12 +890,12 @@ uint64_t segmented_lookback_bytes(const SegmentedArgs &a) {
 }
 
 // Everything else, which must never share memory with status words: the
-// tile maps and the excess-end worklist, or the short path's chunk worklist.
+// tile maps, or the short path's chunk worklist.
 uint64_t segmented_aux_bytes(const SegmentedArgs &a) {
     if (a.n == 0 || a.num_segments == 0) return 0;
     if (short_path(a)) return kWorkHeader + short_work_cap(a) * sizeof(uint2);
     const uint64_t tiles = ceil_div(a.n, kTile);
-    return tile_map_bytes(tiles) + kWorkHeader + tile_work_cap(a.num_segments, tiles) * sizeof(uint2);
+    return tile_map_bytes(tiles);
 }
 
 // A prepared plan's one workspace: the status words, then the rest.  Its
@@ -963,9 +942,6 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
     p.ub_map = (uint32_t *)aux;
     p.lb_map = p.ub_map + p.total_tiles + 1;
-    p.work_count = (unsigned long long *)((char *)aux + tile_map_bytes(p.total_tiles));
-    p.work = (uint2 *)((char *)p.work_count + kWorkHeader);
-    p.work_cap = tile_work_cap(a.num_segments, p.total_tiles);
     if (p.total_tiles >= 0x80000000ull)
         return fail(HX_ERR_DISPATCH_FAILED, "segmented reduce of %llu tiles exceeds the grid range",
                     (unsigned long long)p.total_tiles);
@@ -981,11 +957,6 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
                        dim3(kSegWaves * kWave), 0, stream, p);
     HX_TRY(check_launch("segmented_sum_kernel"));
     commit_lookback_launch(lb);
-    if (a.num_segments + 1 > kEndCap) { // otherwise no tile can hold excess ends
-        const uint64_t blocks = p.work_cap < 512 ? p.work_cap : 512;
-        hipLaunchKernelGGL(seg_excess_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p);
-        HX_TRY(check_launch("seg_excess_kernel"));
-    }
     return HX_OK;
 }
 
