@@ -765,12 +765,39 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
 // overlap it.  Grid-strided over the entries, so every block reaches the end
 // whatever the count; entries beyond the workspace (possible only with
 // malformed offsets) are dropped.
+// Sum (mod 2^32) of this wave's share of values [c0, c1), c1 - c0 <=
+// kShortChunk, laid out as in short_chunk_prefix.
+__device__ __forceinline__ uint32_t short_chunk_wave_sum(const uint32_t *values, uint64_t c0, uint64_t c1) {
+    const int w = threadIdx.x / kWave;
+    const uint64_t e0 = c0 + (uint64_t)w * kShortWaveElems + (uint64_t)lane_id() * 4;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kShortSteps; ++j) {
+        const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
+        if (e + 4 <= c1) {
+            const u32x4_a4 v = load_a4<true>((const u32x4_a4 *)(values + e));
+            sum += v.x + v.y + v.z + v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sum += (e + c < c1) ? values[e + c] : 0u;
+        }
+    }
+    return wave_sum(sum);
+}
+
 __global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortParams p) {
     __shared__ __align__(16) uint32_t s_p[kShortChunk];
     uint64_t count = *p.work_count;
     if (count > p.work_cap) count = p.work_cap;
+    uint2 next = blockIdx.x < count ? p.work[blockIdx.x] : make_uint2(0u, 0u);
+    // Each wave accumulates its whole-chunk sums per segment and adds them
+    // once the segment changes: many chunks of one long segment would
+    // otherwise serialise on one output word.
+    uint64_t acc_s = ~0ull;
+    uint32_t acc_v = 0;
     for (uint64_t i = blockIdx.x; i < count; i += gridDim.x) { // block-uniform
-        const uint2 e = p.work[i];
+        const uint2 e = next; // the next entry is loaded while this one runs
+        if (i + gridDim.x < count) next = p.work[i + gridDim.x];
         if (e.x >= p.segments) continue;
         const uint64_t sf = e.x, c0 = e.y;
         const uint64_t s1b = (sf / p.seg_per_block + 1) * p.seg_per_block;
@@ -778,6 +805,18 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortPar
         const uint64_t a1 = short_off(p, s1);
         const uint64_t c1 = c0 + kShortChunk < a1 ? c0 + kShortChunk : a1;
         if (c0 >= c1) continue;
+        // A chunk inside one segment (the usual case: a long segment's
+        // middle) needs only its sum: no LDS and no barrier.
+        if (short_off(p, sf + 1) >= c1) {
+            const uint32_t v = short_chunk_wave_sum(p.values, c0, c1);
+            if (sf != acc_s) {
+                if (lane_id() == 0 && acc_s != ~0ull && acc_v) atomicAdd(&p.out[acc_s], acc_v);
+                acc_s = sf;
+                acc_v = 0;
+            }
+            acc_v += v;
+            continue;
+        }
         const ChunkCarry cc = short_chunk_prefix(p.values, c0, c0, c1, s_p);
         for (uint64_t s = sf + threadIdx.x; s < s1; s += kShortThreads) {
             const uint64_t st = short_off(p, s);
@@ -791,6 +830,7 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortPar
         }
         __syncthreads(); // s_p is rewritten by the next entry
     }
+    if (lane_id() == 0 && acc_s != ~0ull && acc_v) atomicAdd(&p.out[acc_s], acc_v);
 }
 
 // n == 0: every segment is empty.
