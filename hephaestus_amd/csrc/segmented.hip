@@ -694,6 +694,14 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     const uint64_t a0 = short_off(p, s0);
     uint64_t a1 = short_off(p, s1);
     if (a1 < a0) a1 = a0; // only reachable with malformed offsets
+    if (a1 == a0) { // block-uniform: every segment of the block is empty
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
+            if (s < s1) p.out[s] = 0u;
+        }
+        return;
+    }
     const uint64_t base = a0 & ~3ull;
     const uint64_t c1 = a1 < base + kShortChunk ? a1 : base + kShortChunk;
 
