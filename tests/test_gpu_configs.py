@@ -111,6 +111,25 @@ def test_i32_segmented_sum_2_27(device, oracle):
     assert np.array_equal(got, oracle.segmented_sum(host, off))
 
 
+@pytest.mark.parametrize("mean", [1.0, 4.0])
+def test_i32_segmented_sum_2_27_short_segments(device, oracle, mean):
+    """Config 4's 2^27 values with short geometric segments (mean 1 and 4):
+    the segment-parallel path at full size, bit-exact, plus the checksum
+    of checksums."""
+    n = 1 << 27
+    note(f"segmented n=2^27 mean {mean:g}")
+    x = device.alloc_uninitialized(np.int32, n)
+    device.fill_uniform_int(x, seed=4, lo=-1000, hi=1000)
+    off = oracle.geometric_offsets(n, mean, seed=5)
+    ob = device.upload(off)
+    out = device.alloc_uninitialized(np.int32, off.size - 1)
+    SEG.segmented_sum_into(device, x, ob, out)
+    got = device.download_owned(out)
+    host = device.download_owned(x)
+    assert np.sum(got, dtype=np.int32) == oracle.full_sum(host)
+    assert np.array_equal(got, oracle.segmented_sum(host, off))
+
+
 def test_f32_inclusive_scan_2_30(device, oracle):
     """Config 5: f32 inclusive scan of 2^30 uniform[0,1) values (4 GiB in,
     4 GiB out), every output within the bound."""
