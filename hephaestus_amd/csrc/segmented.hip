@@ -710,7 +710,7 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     // memory round trip.
     // A segment's end is the next lane's start; the end of lane 63's segment
     // in group j is loaded by lane j of the wave into one register.
-    uint32_t lo[J], hi[J];
+    uint32_t lo[J];
     const uint64_t wave_s = s0 + (threadIdx.x & ~(kWave - 1));
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -720,23 +720,24 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     const uint64_t edge_k = wave_s + (uint64_t)lane * kShortThreads + kWave;
     const uint32_t edge = (lane < J && edge_k <= s1) ? p.offsets[edge_k] : 0u;
     const ChunkCarry cc = short_chunk_prefix(p.values, base, a0, c1, s_p);
-    // Clamped into the span (only malformed offsets are changed).
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
+    // Segment j's bounds, clamped into the span (only malformed offsets are
+    // changed); recomputed where needed rather than held, which keeps J = 16
+    // within five waves per SIMD.
+    auto bounds = [&](int j, uint64_t &st, uint64_t &en) {
         const uint32_t next = __shfl_down(lo[j], 1);
         const uint32_t e = lane == kWave - 1 ? read_lane(edge, j) : next;
         const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
-        const uint64_t st = lo[j] < a0 ? a0 : (lo[j] > a1 ? a1 : lo[j]);
-        const uint64_t en = (s >= s1 || e < st) ? st : (e > a1 ? a1 : e);
-        lo[j] = (uint32_t)st;
-        hi[j] = (uint32_t)en;
-    }
+        st = lo[j] < a0 ? a0 : (lo[j] > a1 ? a1 : lo[j]);
+        en = (s >= s1 || e < st) ? st : (e > a1 ? a1 : e);
+    };
 #pragma unroll
     for (int j = 0; j < J; ++j) {
+        uint64_t st, en;
+        bounds(j, st, en);
         const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
         if (s < s1) {
-            const uint64_t h = hi[j] < c1 ? hi[j] : c1;
-            const uint64_t l = lo[j] < h ? lo[j] : h;
+            const uint64_t h = en < c1 ? en : c1;
+            const uint64_t l = st < h ? st : h;
             p.out[s] = chunk_range_sum(s_p, cc, (uint32_t)(l - base), (uint32_t)(h - base));
         }
     }
@@ -748,8 +749,10 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     uint32_t lane_total = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
+        uint64_t st, en;
+        bounds(j, st, en);
         uint32_t c_lo, count;
-        short_chunk_range(base, lo[j], hi[j], chunks, c_lo, count);
+        short_chunk_range(base, st, en, chunks, c_lo, count);
         lane_total += count;
     }
     const uint32_t incl = wave_inclusive_scan<OpSum, uint32_t>(lane_total);
@@ -761,18 +764,16 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     uint64_t slot = first + (incl - lane_total);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
+        uint64_t st, en;
+        bounds(j, st, en);
         uint32_t c_lo, count;
-        short_chunk_range(base, lo[j], hi[j], chunks, c_lo, count);
+        short_chunk_range(base, st, en, chunks, c_lo, count);
         const uint64_t s = s0 + threadIdx.x + (uint64_t)j * kShortThreads;
         short_write_entries(p, slot, base, (uint32_t)s, c_lo, count);
         slot += count;
     }
 }
 
-// Adds each deferred chunk's part to the outputs of the segments that
-// overlap it.  Grid-strided over the entries, so every block reaches the end
-// whatever the count; entries beyond the workspace (possible only with
-// malformed offsets) are dropped.
 // Sum (mod 2^32) of this wave's share of values [c0, c1), c1 - c0 <=
 // kShortChunk, laid out as in short_chunk_prefix.
 __device__ __forceinline__ uint32_t short_chunk_wave_sum(const uint32_t *values, uint64_t c0, uint64_t c1) {
@@ -793,6 +794,10 @@ __device__ __forceinline__ uint32_t short_chunk_wave_sum(const uint32_t *values,
     return wave_sum(sum);
 }
 
+// Adds each deferred chunk's part to the outputs of the segments that
+// overlap it.  Grid-strided over the entries, so every block reaches the end
+// whatever the count; entries beyond the workspace (possible only with
+// malformed offsets) are dropped.
 __global__ __launch_bounds__(kShortThreads) void seg_short_drain_kernel(ShortParams p) {
     __shared__ __align__(16) uint32_t s_p[kShortChunk];
     uint64_t count = *p.work_count;
