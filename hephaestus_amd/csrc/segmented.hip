@@ -45,6 +45,15 @@ template <int WAVES, int STEPS> struct SegTile {
 // form of the kernel: 8 x 16 230 us).
 constexpr int kSegWaves = 4, kSegSteps = 8;
 constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
+// Long segments (mean n / S of kLongMean or more) take 16384-value tiles,
+// 8 waves x 8 steps: half the look-backs per byte, which is what long
+// segments pay for (their tiles rarely hold a segment start).  At 2^27
+// values, us per launch with 8192- against 16384-value tiles: mean 300
+// 85.4 / 106.0, 3000 96.0 / 98.2, 10^5 119.5 / 114.7, 10^6 137.2 / 125.3,
+// 10^7 147.8 / 129.6.  (4 x 16 tiles spill: about 400 us everywhere.)
+constexpr int kLongWaves = 8;
+constexpr int kLongTile = SegTile<kLongWaves, kSegSteps>::kElems;
+constexpr uint64_t kLongMean = 16384;
 constexpr int kSlots = 2048; // segment values compacted per round
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor
@@ -932,6 +941,8 @@ hx_status launch_short(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, hipS
 
 namespace {
 uint64_t align256(uint64_t b) { return (b + 255) & ~255ull; }
+bool long_tiles(const SegmentedArgs &a) { return a.n >= kLongMean * a.num_segments; }
+uint64_t seg_tile_elems(const SegmentedArgs &a) { return long_tiles(a) ? kLongTile : kTile; }
 uint64_t tile_map_bytes(uint64_t tiles) { return align256(2 * (tiles + 1) * 4); }
 } // namespace
 
@@ -939,7 +950,7 @@ uint64_t tile_map_bytes(uint64_t tiles) { return align256(2 * (tiles + 1) * 4); 
 // the short path.
 uint64_t segmented_lookback_bytes(const SegmentedArgs &a) {
     if (a.n == 0 || a.num_segments == 0 || short_path(a)) return 0;
-    return kLookbackOffset + ceil_div(a.n, kTile) * 8;
+    return kLookbackOffset + ceil_div(a.n, seg_tile_elems(a)) * 8;
 }
 
 // Everything else, which must never share memory with status words: the
@@ -947,7 +958,7 @@ uint64_t segmented_lookback_bytes(const SegmentedArgs &a) {
 uint64_t segmented_aux_bytes(const SegmentedArgs &a) {
     if (a.n == 0 || a.num_segments == 0) return 0;
     if (short_path(a)) return kWorkHeader + short_work_cap(a) * sizeof(uint2);
-    const uint64_t tiles = ceil_div(a.n, kTile);
+    const uint64_t tiles = ceil_div(a.n, seg_tile_elems(a));
     return tile_map_bytes(tiles);
 }
 
@@ -991,7 +1002,8 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     p.offsets = a.offsets;
     p.segments = a.num_segments;
     p.out = (uint32_t *)a.out;
-    p.total_tiles = ceil_div(a.n, kTile);
+    const bool long_tile = long_tiles(a);
+    p.total_tiles = ceil_div(a.n, seg_tile_elems(a));
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
     p.ub_map = (uint32_t *)aux;
     p.lb_map = p.ub_map + p.total_tiles + 1;
@@ -1004,10 +1016,18 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     uint64_t map_blocks = ceil_div(a.num_segments + 2, kBlock);
     if (map_blocks > 2048) map_blocks = 2048;
-    hipLaunchKernelGGL((seg_tile_map_kernel<kTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream, p);
-    HX_TRY(check_launch("seg_tile_map_kernel"));
-    hipLaunchKernelGGL((segmented_sum_kernel<kSegWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
-                       dim3(kSegWaves * kWave), 0, stream, p);
+    if (long_tile) {
+        hipLaunchKernelGGL((seg_tile_map_kernel<kLongTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream,
+                           p);
+        HX_TRY(check_launch("seg_tile_map_kernel"));
+        hipLaunchKernelGGL((segmented_sum_kernel<kLongWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
+                           dim3(kLongWaves * kWave), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((seg_tile_map_kernel<kTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream, p);
+        HX_TRY(check_launch("seg_tile_map_kernel"));
+        hipLaunchKernelGGL((segmented_sum_kernel<kSegWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
+                           dim3(kSegWaves * kWave), 0, stream, p);
+    }
     HX_TRY(check_launch("segmented_sum_kernel"));
     commit_lookback_launch(lb);
     return HX_OK;

@@ -111,11 +111,11 @@ def test_i32_segmented_sum_2_27(device, oracle):
     assert np.array_equal(got, oracle.segmented_sum(host, off))
 
 
-@pytest.mark.parametrize("mean", [1.0, 4.0])
+@pytest.mark.parametrize("mean", [1.0, 4.0, 1e6])
 def test_i32_segmented_sum_2_27_short_segments(device, oracle, mean):
-    """Config 4's 2^27 values with short geometric segments (mean 1 and 4):
-    the segment-parallel path at full size, bit-exact, plus the checksum
-    of checksums."""
+    """Config 4's 2^27 values with other geometric segment lengths: means 1
+    and 4 take the segment-parallel path, mean 10^6 the 16384-value tiles;
+    bit-exact, plus the checksum of checksums."""
     n = 1 << 27
     note(f"segmented n=2^27 mean {mean:g}")
     x = device.alloc_uninitialized(np.int32, n)

@@ -682,6 +682,25 @@ def test_segmented_sum_16k_tile_edges(device, oracle):
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
+def test_segmented_sum_long_segment_tiles(device, oracle):
+    """Means of 16384 values or more take 16384-value tiles: boundaries on
+    and beside their edges, a segment spanning every tile, empties at an
+    edge and at n."""
+    t = 16384
+    n = (1 << 20) + 77
+    x = oracle.uniform_int(n, seed=44, lo=-1 << 30, hi=1 << 30, dtype=np.int32)
+    cases = [
+        [0, t - 1, t, t + 1, 3 * t, n],
+        [0, 5, n - 3, n],
+        [0, 2 * t, 2 * t, 2 * t, 40 * t + 3, n, n],
+        [0, t // 2 + 1, 17 * t - 1, 33 * t, n],
+    ]
+    for off in cases:
+        off = np.array(off, np.uint32)
+        assert n >= 16384 * (off.size - 1), "case must take the long-segment tiles"
+        assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
+
+
 @pytest.mark.parametrize("cuts_n", [300, 12000])
 @pytest.mark.parametrize("skew", [1, 2, 3])
 def test_segmented_sum_values_off_16_byte_boundaries(device, oracle, skew, cuts_n):
