@@ -14,7 +14,8 @@
 //      every tile edge, the offset indices around it (upper and lower bound),
 //      so no block searches the offsets;
 //   2. segmented_sum_kernel: block b loads tile b (4 waves x 8 vectors per
-//      lane = 8192 values) and the offsets that end in it, scans the values
+//      lane = 8192 values; 8 waves, 16384 values, when segments average
+//      16384 values or more) and the offsets that end in it, scans the values
 //      in registers, marks segment ends in an LDS bitmask and writes every
 //      segment that ends in the tile.  The segment open at the tile start
 //      takes the sum of earlier tiles from a segmented decoupled look-back:
