@@ -15,7 +15,7 @@
 //      so no block searches the offsets;
 //   2. segmented_sum_kernel: block b loads tile b (4 waves x 8 vectors per
 //      lane = 8192 values; 8 waves, 16384 values, when segments average
-//      16384 values or more) and the offsets that end in it, scans the values
+//      4096 values or more) and the offsets that end in it, scans the values
 //      in registers, marks segment ends in an LDS bitmask and writes every
 //      segment that ends in the tile.  The segment open at the tile start
 //      takes the sum of earlier tiles from a segmented decoupled look-back:
@@ -50,11 +50,12 @@ constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
 // 8 waves x 8 steps: half the look-backs per byte, which is what long
 // segments pay for (their tiles rarely hold a segment start).  At 2^27
 // values, us per launch with 8192- against 16384-value tiles: mean 300
-// 85.4 / 106.0, 3000 96.0 / 98.2, 10^5 119.5 / 114.7, 10^6 137.2 / 125.3,
-// 10^7 147.8 / 129.6.  (4 x 16 tiles spill: about 400 us everywhere.)
+// 85.4 / 106.0, 3000 96.0 / 98.2, 4000 99.8 / 99.6, 8000 106.2 / 99.0,
+// 10^5 119.5 / 114.7, 10^6 137.2 / 125.3, 10^7 147.8 / 129.6.  (4 x 16
+// tiles spill: about 400 us everywhere.)
 constexpr int kLongWaves = 8;
 constexpr int kLongTile = SegTile<kLongWaves, kSegSteps>::kElems;
-constexpr uint64_t kLongMean = 16384;
+constexpr uint64_t kLongMean = 4096;
 constexpr int kSlots = 2048; // segment values compacted per round
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor

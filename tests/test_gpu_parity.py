@@ -683,7 +683,7 @@ def test_segmented_sum_16k_tile_edges(device, oracle):
 
 
 def test_segmented_sum_long_segment_tiles(device, oracle):
-    """Means of 16384 values or more take 16384-value tiles: boundaries on
+    """Means of 4096 values or more take 16384-value tiles: boundaries on
     and beside their edges, a segment spanning every tile, empties at an
     edge and at n."""
     t = 16384
@@ -697,7 +697,7 @@ def test_segmented_sum_long_segment_tiles(device, oracle):
     ]
     for off in cases:
         off = np.array(off, np.uint32)
-        assert n >= 16384 * (off.size - 1), "case must take the long-segment tiles"
+        assert n >= 4096 * (off.size - 1), "case must take the long-segment tiles"
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
