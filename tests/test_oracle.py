@@ -367,3 +367,153 @@ def test_fma_arrays_is_single_rounding(oracle):
         assert got[i] == np.float32(float(exact)), i
     # the separately rounded form differs on the first element
     assert np.float32(f * x[0]) + y[0] != got[0]
+
+
+# ---- the streaming f32 scan checker (the only checker of the 2^30 scan) ----
+def _tol(x: np.ndarray, i: int, exclusive: bool, n_for_log: int) -> float:
+    """The north-star bound at output i from first principles:
+    2 * ceil(log2 n) * 2^-23 * (exact sum of |x| over the prefix), with the
+    prefix sum taken by math.fsum and ceil(log2 n) by integer bit length."""
+    m = i if exclusive else i + 1
+    return 2 * (n_for_log - 1).bit_length() * 2.0**-23 * math.fsum(abs(float(v)) for v in x[:m])
+
+
+@pytest.mark.parametrize("lo", [0.0, -1.0])
+@pytest.mark.parametrize("exclusive", [False, True])
+def test_streaming_scan_checker_agrees_with_the_array_checker(oracle, lo, exclusive):
+    """hxo_check_scan_f32 re-derives the prefix and the bound on the fly; on
+    the same outputs it must report what hxo_check_f32_bound reports from
+    the stored f64 prefix: same violation count, same worst ratio."""
+    n = 1 << 17
+    x = oracle.uniform_real(n, seed=21, lo=lo, hi=1.0)
+    ref, ab = oracle.scan_sum(x, exclusive=exclusive)
+    rng = np.random.default_rng(4)
+    tol = 2 * oracle.ceil_log2(n) * 2.0**-23 * ab
+    # correctly rounded, jittered inside the bound, and jittered across it
+    for scale in (0.0, 0.6, 1.8):
+        got = (ref + rng.uniform(-scale, scale, n) * tol).astype(np.float32)
+        want = oracle.check_f32_bound(got, ref, ab, n)
+        have = oracle.check_scan_f32(x, got, exclusive=exclusive)
+        assert have[0] == want[0], scale
+        assert have[1] == pytest.approx(want[1], rel=1e-12, abs=1e-12), scale
+        if scale == 0.0:
+            assert want[0] == 0 and want[1] <= 0.5
+        elif scale == 0.6:
+            assert want[0] == 0
+        else:
+            assert want[0] > n // 10
+
+
+def test_streaming_scan_checker_flags_planted_errors(oracle):
+    """Plausible scan bugs must each fail the streaming check, and outputs
+    within the bound must pass; the bound's constants are pinned against a
+    from-scratch evaluation (math.fsum, bit length)."""
+    n = 1 << 17
+    x = oracle.uniform_real(n, seed=22, lo=0.0, hi=1.0)
+    inc, _ = oracle.scan_sum(x)
+    exc, _ = oracle.scan_sum(x, exclusive=True)
+    good_inc = inc.astype(np.float32)
+    good_exc = exc.astype(np.float32)
+    assert oracle.check_scan_f32(x, good_inc)[0] == 0
+    assert oracle.check_scan_f32(x, good_exc, exclusive=True)[0] == 0
+
+    # a dropped term at i (and every later output, as a real bug would do)
+    i = 1000 + int(np.argmax(x[1000:2000] > 0.5))
+    dropped = (inc - np.where(np.arange(n) >= i, float(x[i]), 0.0)).astype(np.float32)
+    bad, worst = oracle.check_scan_f32(x, dropped)
+    assert bad >= 1 and worst > 2 * oracle.ceil_log2(n)
+    # one NaN
+    nan = good_inc.copy()
+    nan[77] = np.float32("nan")
+    assert oracle.check_scan_f32(x, nan)[0] == 1
+    # an exclusive result shifted by one position (that is, the inclusive one),
+    # and the inclusive form checked as exclusive
+    assert oracle.check_scan_f32(x, good_inc, exclusive=True)[0] > n // 2
+    assert oracle.check_scan_f32(x, good_exc)[0] > n // 2
+    # an exclusive scan one element late: out[i] = sum x[0..i-1)
+    late = np.concatenate([[0.0], exc[:-1]]).astype(np.float32)
+    assert oracle.check_scan_f32(x, late, exclusive=True)[0] > n // 2
+    # the wrong sign of one term
+    flip = (inc - 2.0 * np.where(np.arange(n) >= i, float(x[i]), 0.0)).astype(np.float32)
+    assert oracle.check_scan_f32(x, flip)[0] >= n - i - 1
+
+    # the bound itself, at three positions, from first principles
+    for k in (0, 4097, n - 1):
+        for exclusive, base in ((False, inc), (True, exc)):
+            if exclusive and k == 0:
+                continue  # exclusive out[0] = 0 with zero tolerance
+            t = _tol(x, k, exclusive, n)
+            for factor, expect in ((0.5, 0), (0.97, 0), (1.03, 1), (1.5, 1)):
+                got = (good_exc if exclusive else good_inc).copy()
+                got[k] = np.float32(base[k] + factor * t)
+                # f32 rounding of the planted value moves it by at most half
+                # an ulp, inside the 3% margins around the bound
+                assert abs(float(got[k]) - (base[k] + factor * t)) < 0.02 * t
+                assert oracle.check_scan_f32(x, got, exclusive=exclusive)[0] == expect, (k, exclusive, factor)
+    # exclusive out[0] must be exactly 0 (an empty prefix has no tolerance)
+    zero = good_exc.copy()
+    zero[0] = np.float32(1e-30)
+    assert oracle.check_scan_f32(x, zero, exclusive=True)[0] == 1
+    # n_for_log widens the bound by ceil(log2 n_for_log) / ceil(log2 n)
+    t = _tol(x, n - 1, False, n)
+    wide = good_inc.copy()
+    wide[-1] = np.float32(inc[-1] + 1.5 * t)
+    assert oracle.check_scan_f32(x, wide)[0] == 1
+    assert oracle.check_scan_f32(x, wide, n_for_log=n * n)[0] == 0
+
+
+def test_streaming_scan_checker_matches_math_fsum_prefixes(oracle):
+    """The streaming checker's prefix is exact to f64 rounding: an output set
+    to the correctly rounded math.fsum prefix has worst ratio <= 0.5 (one
+    f32 rounding), for a signed input with heavy cancellation."""
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal(3000) * 1e3).astype(np.float32)
+    x[1::2] = -x[::2][: x[1::2].size]  # pairs cancel: partial sums stay small
+    prefix = [math.fsum(map(float, x[: i + 1])) for i in range(x.size)]
+    got = np.array(prefix, dtype=np.float32)
+    bad, worst = oracle.check_scan_f32(x, got)
+    assert bad == 0 and worst <= 0.5
+
+
+def test_rows_with_padded_leading_dimension(oracle):
+    """hxo_rows_* with ld > cols read row r at r*ld: each row must match the
+    same function on that row alone, and numpy."""
+    rng = np.random.default_rng(7)
+    rows, cols, ld = 9, 37, 40
+    for dtype in (np.float32, np.int32, np.uint32):
+        if dtype == np.float32:
+            buf = rng.standard_normal(rows * ld).astype(np.float32)
+        else:
+            info = np.iinfo(dtype)
+            buf = rng.integers(info.min, info.max, rows * ld, dtype=dtype)
+        pro = (0.5, 0.25) if dtype == np.float32 else None
+        s, a, m, i = oracle.rows(buf, rows, cols, ld, prologue=pro)
+        for r in range(rows):
+            row = np.ascontiguousarray(buf[r * ld: r * ld + cols])
+            s1, a1, m1, i1 = oracle.rows(row, 1, cols, prologue=pro)
+            assert s[r] == s1[0] and m[r] == m1[0] and i[r] == i1[0], (dtype, r)
+            y = oracle.fma_arrays(row, np.full(cols, 0.25, np.float32), 0.5) if pro else row
+            assert m[r] == y.max() and i[r] == int(np.argmax(y)), (dtype, r)
+            if dtype == np.float32:
+                assert a[r] == a1[0]
+                assert s[r] == pytest.approx(math.fsum(map(float, y)), abs=1e-12)
+            else:
+                assert int(s[r]) == int(np.sum(y, dtype=dtype))  # numpy wraps mod 2^32
+        # the padding between rows is never read: poisoning it changes nothing
+        poisoned = buf.copy()
+        for r in range(rows):
+            poisoned[r * ld + cols: (r + 1) * ld] = dtype(7) if dtype != np.float32 else np.float32(1e30)
+        s2, _, m2, i2 = oracle.rows(poisoned, rows, cols, ld, prologue=pro)
+        assert np.array_equal(s2, s) and np.array_equal(m2, m) and np.array_equal(i2, i)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 16])
+def test_multithreaded_scan_baseline_equals_sequential(oracle, threads):
+    """The pthread CPU baseline computes the same exclusive scan as the
+    sequential oracle (ragged split points, wrap-around)."""
+    n = 100_003
+    x = oracle.uniform_int(n, seed=8, lo=0, hi=2**32 - 1)
+    out = np.empty_like(x)
+    oracle.scan_excl_u32_threads(x, out, threads)
+    assert np.array_equal(out, oracle.scan_sum(x, exclusive=True))
+    assert np.array_equal(out, (np.cumsum(x, dtype=np.uint32) - x))
