@@ -501,7 +501,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     if (full) {
         using V = typename Vec4A4<T>::type;
         if constexpr (REV) {
-            char *obase = (char *)(out + ob + rev_tile);
+            const auto orsrc = stream_rsrc(out + ob + rev_tile, kTileElems * (uint32_t)sizeof(T));
 #pragma unroll
             for (int j = 0; j < STEPS; ++j) {
                 V v;
@@ -509,10 +509,10 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
                 v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
                 v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
                 v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
-                store_a4<NT>(v, (V *)(obase + rev_off - (uint32_t)j * (kWave * 16)));
+                stream_store(v, orsrc, rev_off - (uint32_t)j * (kWave * 16));
             }
         } else {
-            char *obase = (char *)(out + ob + (int64_t)(tin * kTileElems));
+            const auto orsrc = stream_rsrc(out + ob + (int64_t)(tin * kTileElems), kTileElems * (uint32_t)sizeof(T));
 #pragma unroll
             for (int j = 0; j < STEPS; ++j) {
                 V v;
@@ -520,7 +520,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
                 v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
                 v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
                 v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
-                store_a4<NT>(v, (V *)(obase + lane_off + (uint32_t)j * (kWave * 16)));
+                stream_store(v, orsrc, lane_off + (uint32_t)j * (kWave * 16));
             }
         }
         return;

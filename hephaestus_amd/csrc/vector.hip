@@ -83,6 +83,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void vector_tiles_kernel(const 
         if constexpr (kUsesS)
             b[j] = load_a4<true>((const f32x4_a4 *)((const char *)s + base + lane_off + (uint32_t)j * (kWave * 16)));
     }
+    const auto orsrc = stream_rsrc((char *)out + base, (uint32_t)(kTileElems * 4));
 #pragma unroll
     for (int j = 0; j < kTileSteps; ++j) {
         f32x4_a4 r;
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kTileWaves * kWave) void vector_tiles_kernel(const 
         r.y = apply<OP>(a[j].y, y.y, f);
         r.z = apply<OP>(a[j].z, y.z, f);
         r.w = apply<OP>(a[j].w, y.w, f);
-        store_a4<true>(r, (f32x4_a4 *)((char *)out + base + lane_off + (uint32_t)j * (kWave * 16)));
+        stream_store(r, orsrc, lane_off + (uint32_t)j * (kWave * 16));
     }
 }
 
