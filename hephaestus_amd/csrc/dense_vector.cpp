@@ -75,8 +75,10 @@ struct MapPlan final : hx_plan {
 };
 
 hx_status run_map(hx_device *dev, const MapReduceArgs &a, hipStream_t stream) {
+    Immediate im;
+    HX_TRY(im.open(dev, stream));
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, map_reduce_workspace_bytes(a.n), stream, &ws));
+    HX_TRY(im.workspace(map_reduce_workspace_bytes(a.n), &ws));
     return launch_map_reduce(a, ws, stream);
 }
 

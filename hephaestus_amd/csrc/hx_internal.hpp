@@ -6,8 +6,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 
 namespace hx {
 // Host-side bookkeeping of one look-back workspace: every launch tags its
@@ -18,6 +20,24 @@ namespace hx {
 // L2) on the hot path.
 struct LookbackState {
     uint32_t launches = 0; // launches so far on this workspace
+};
+
+// The buffers the immediate (un-prepared) entry points use on ONE stream:
+//   ws       header + full-reduce partials + look-back status words;
+//   scratch  partials staged outside any look-back protocol (split axis
+//            reductions, chunked column scans, segmented tile maps and
+//            worklists), kept apart from `ws` so those writes never land on
+//            status words.
+// Each stream has its own, so launches queued on different streams never
+// share a buffer; `mu` is held from the workspace lookup until the call's
+// launches are queued (see Immediate).
+struct StreamWorkspace {
+    std::mutex mu;
+    void *ws = nullptr;
+    uint64_t ws_bytes = 0;
+    LookbackState lookback;
+    void *scratch = nullptr;
+    uint64_t scratch_bytes = 0;
 };
 } // namespace hx
 
@@ -34,17 +54,12 @@ struct hx_device {
     uint64_t pinned_bytes = 0;
     hipEvent_t pinned_ev[2] = {nullptr, nullptr};
 
-    // Workspace for the immediate (un-prepared) entry points.
-    std::mutex ws_mu;
-    void *ws = nullptr;
-    uint64_t ws_bytes = 0;
-    hx::LookbackState ws_lookback;
-
-    // Scratch for the immediate entry points that stage partials outside
-    // any look-back protocol (split axis reductions, chunked column scans).
-    // Kept apart from `ws` so those writes never land on status words.
-    void *scratch = nullptr;
-    uint64_t scratch_bytes = 0;
+    // Immediate-mode buffers, one set per stream handle the caller has used
+    // (created on first use, freed at hx_device_close).  A stream handle is
+    // only reused by the runtime after the destroyed stream's work has
+    // drained, so an entry never serves two live streams at once.
+    std::mutex streams_mu;
+    std::unordered_map<hipStream_t, std::unique_ptr<hx::StreamWorkspace>> immediate;
 };
 
 namespace hx {
@@ -99,13 +114,31 @@ constexpr uint64_t kWorkspaceHeader = 256;
 constexpr uint64_t kReduceArea = 64 * 1024;
 constexpr uint64_t kLookbackOffset = kWorkspaceHeader + kReduceArea;
 
-// Immediate-mode workspace of `dev`, grown (and zeroed) on demand; a grown
-// workspace restarts its LookbackState.
-hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t stream, void **ws);
 hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws);
-// Immediate-mode scratch of `dev` (see hx_device::scratch), grown on demand;
-// nothing is returned for 0 bytes.
-hx_status device_scratch(hx_device *dev, uint64_t bytes, void **scratch);
+
+// Exclusive use of one stream's immediate-mode buffers for the rest of an
+// entry point.  The lock is held across buffer growth, the draw of the
+// look-back tag and the launches, so calls from several host threads on one
+// stream draw distinct tags in launch order, and a buffer is never freed
+// while a launch queued on its stream may still use it (growth first waits
+// for that stream).  Calls on different streams use different buffers.
+class Immediate {
+public:
+    hx_status open(hx_device *dev, hipStream_t stream);
+    // Look-back workspace of at least `bytes` (zeroed when allocated; a new
+    // buffer restarts the tag count).
+    hx_status workspace(uint64_t bytes, void **ws);
+    // Scratch of at least `bytes`; nullptr for 0 bytes.
+    hx_status scratch(uint64_t bytes, void **scratch);
+    uint64_t workspace_bytes() const { return sw_->ws_bytes; }
+    LookbackState &lookback() { return sw_->lookback; }
+
+private:
+    hx_device *dev_ = nullptr;
+    hipStream_t stream_ = nullptr;
+    StreamWorkspace *sw_ = nullptr;
+    std::unique_lock<std::mutex> lock_;
+};
 
 // Tag for the next look-back launch on a workspace of `ws_bytes`; clears the
 // status area when the 30-bit tag space wraps.
@@ -233,11 +266,15 @@ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 // A prepared dispatch (the reference's Prepared associated types, e.g.
 // crates/hephaestus-rocm/src/application/full_reduction_seam.rs:33-43).
+// `mu` serialises dispatches of one plan from several host threads, so each
+// draws its own look-back tag; launches on different streams are ordered by
+// the caller.
 struct hx_plan {
     hx_device *dev = nullptr;
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
     hx::LookbackState lookback;
+    std::mutex mu;
     virtual ~hx_plan();
     virtual hx_status dispatch(hipStream_t stream) = 0;
 };

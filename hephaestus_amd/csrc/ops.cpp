@@ -1,8 +1,8 @@
 // Device entry points of the C ABI: validate (always before any write, so a
 // rejected call leaves its outputs untouched), then launch on the chosen
-// stream.  Immediate forms use the device-owned workspace; hx_prepare_*
-// returns a plan that owns its workspace, so hx_plan_dispatch allocates
-// nothing.
+// stream.  Immediate forms use the workspace of the stream they launch on
+// (Immediate); hx_prepare_* returns a plan that owns its workspace, so
+// hx_plan_dispatch allocates nothing.
 #include "hx_internal.hpp"
 
 #include <new>
@@ -105,8 +105,10 @@ struct FullPlan final : hx_plan {
 };
 
 hx_status run_full(hx_device *dev, const FullReduceArgs &a, hipStream_t stream) {
+    Immediate im;
+    HX_TRY(im.open(dev, stream));
     void *ws = nullptr;
-    HX_TRY(device_workspace(dev, full_reduce_workspace_bytes(a.n), stream, &ws));
+    HX_TRY(im.workspace(full_reduce_workspace_bytes(a.n), &ws));
     return launch_full_reduce(a, ws, stream);
 }
 
@@ -318,10 +320,13 @@ hx_status hx_reduce_axis(hx_device *dev, hx_op op, hx_dtype dtype, const void *i
     AxisArgs a;
     HX_TRY(plan_axis(op, dtype, in, in_buf_len, in_layout, axis, out, out_buf_len, out_layout, &a));
     HX_TRY(bind_device(dev));
+    const hipStream_t s = pick_stream(dev, stream);
+    Immediate im;
+    HX_TRY(im.open(dev, s));
     const uint64_t bytes = axis_reduce_workspace_bytes(a);
     void *scratch = nullptr;
-    HX_TRY(device_scratch(dev, bytes, &scratch));
-    HX_TRY(launch_axis_reduce(a, scratch, bytes, pick_stream(dev, stream)));
+    HX_TRY(im.scratch(bytes, &scratch));
+    HX_TRY(launch_axis_reduce(a, scratch, bytes, s));
     return ok();
 }
 
@@ -385,10 +390,13 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_
     a.out_max = out_max;
     a.out_argmax = out_argmax;
     HX_TRY(bind_device(dev));
+    const hipStream_t s = pick_stream(dev, stream);
+    Immediate im;
+    HX_TRY(im.open(dev, s));
     const uint64_t bytes = rows_workspace_bytes(a);
     void *scratch = nullptr;
-    HX_TRY(device_scratch(dev, bytes, &scratch));
-    HX_TRY(launch_rows(a, scratch, bytes, pick_stream(dev, stream)));
+    HX_TRY(im.scratch(bytes, &scratch));
+    HX_TRY(launch_rows(a, scratch, bytes, s));
     return ok();
 }
 
@@ -401,15 +409,17 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
                      out_layout, &a));
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
+    Immediate im;
+    HX_TRY(im.open(dev, s));
     void *ws = nullptr;
     const uint64_t bytes = scan_workspace_bytes(a);
     if (!scan_uses_lookback(a)) {
-        HX_TRY(device_scratch(dev, bytes, &ws));
-        HX_TRY(launch_scan(a, ws, bytes, dev->ws_lookback, s));
+        HX_TRY(im.scratch(bytes, &ws));
+        HX_TRY(launch_scan(a, ws, bytes, im.lookback(), s));
         return ok();
     }
-    HX_TRY(device_workspace(dev, bytes, s, &ws));
-    HX_TRY(launch_scan(a, ws, dev->ws_bytes, dev->ws_lookback, s));
+    HX_TRY(im.workspace(bytes, &ws));
+    HX_TRY(launch_scan(a, ws, im.workspace_bytes(), im.lookback(), s));
     return ok();
 }
 
@@ -436,11 +446,13 @@ hx_status hx_segmented_reduce(hx_device *dev, hx_op op, hx_dtype dtype, const vo
     HX_TRY(plan_segmented(op, dtype, values, n, offsets, num_offsets, out, out_len, &a));
     HX_TRY(bind_device(dev));
     hipStream_t s = pick_stream(dev, stream);
+    Immediate im;
+    HX_TRY(im.open(dev, s));
     void *ws = nullptr, *aux = nullptr;
     const uint64_t lookback = segmented_lookback_bytes(a), aux_bytes = segmented_aux_bytes(a);
-    HX_TRY(device_scratch(dev, aux_bytes, &aux));
-    if (lookback) HX_TRY(device_workspace(dev, lookback, s, &ws));
-    HX_TRY(launch_segmented(a, ws, lookback ? dev->ws_bytes : 0, aux, aux_bytes, dev->ws_lookback, s));
+    HX_TRY(im.scratch(aux_bytes, &aux));
+    if (lookback) HX_TRY(im.workspace(lookback, &ws));
+    HX_TRY(launch_segmented(a, ws, lookback ? im.workspace_bytes() : 0, aux, aux_bytes, im.lookback(), s));
     return ok();
 }
 

@@ -86,40 +86,67 @@ hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws) {
     return HX_OK;
 }
 
-hx_status device_workspace(hx_device *dev, uint64_t bytes, hipStream_t, void **ws) {
-    std::lock_guard<std::mutex> lock(dev->ws_mu);
-    if (bytes > dev->ws_bytes) {
-        if (dev->ws) {
-            HX_HIP(hipDeviceSynchronize(), HX_ERR_DISPATCH_FAILED, "hipDeviceSynchronize");
-            HX_HIP(hipFree(dev->ws), HX_ERR_ALLOCATION_FAILED, "workspace hipFree");
-            dev->ws = nullptr;
-            dev->ws_bytes = 0;
-        }
-        uint64_t grow = bytes < (1ull << 20) ? (1ull << 20) : bytes;
-        HX_TRY(alloc_workspace(dev, grow, &dev->ws));
-        dev->ws_bytes = grow;
-        dev->ws_lookback = LookbackState{};
+namespace {
+
+// Replace `buf` by a zeroed buffer of at least `need` bytes.  The old buffer
+// may still be read by launches queued on `stream` (its only user), so the
+// stream is drained before it is freed; the zero-fill is queued on `stream`
+// ahead of the launches that will use the new buffer.
+hx_status grow_stream_buffer(hipStream_t stream, void *&buf, uint64_t &have, uint64_t need, const char *what) {
+    if (need <= have) return HX_OK;
+    if (buf) {
+        HX_HIP(hipStreamSynchronize(stream), HX_ERR_DISPATCH_FAILED, "stream synchronize before buffer growth");
+        HX_HIP(hipFree(buf), HX_ERR_ALLOCATION_FAILED, what);
+        buf = nullptr;
+        have = 0;
     }
-    *ws = dev->ws;
+    const uint64_t grow = need < (1ull << 20) ? (1ull << 20) : need;
+    void *p = nullptr;
+    HX_HIP(hipMalloc(&p, grow), HX_ERR_ALLOCATION_FAILED, what);
+    hipError_t err = hipMemsetAsync(p, 0, grow, stream);
+    if (err != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(HX_ERR_ALLOCATION_FAILED, err, what);
+    }
+    buf = p;
+    have = grow;
     return HX_OK;
 }
 
-hx_status device_scratch(hx_device *dev, uint64_t bytes, void **scratch) {
+} // namespace
+
+hx_status Immediate::open(hx_device *dev, hipStream_t stream) {
+    dev_ = dev;
+    stream_ = stream;
+    {
+        std::lock_guard<std::mutex> guard(dev->streams_mu);
+        std::unique_ptr<StreamWorkspace> &slot = dev->immediate[stream];
+        if (!slot) {
+            slot.reset(new (std::nothrow) StreamWorkspace());
+            if (!slot) {
+                dev->immediate.erase(stream);
+                return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of a stream workspace failed");
+            }
+        }
+        sw_ = slot.get(); // entries are never erased before hx_device_close
+    }
+    lock_ = std::unique_lock<std::mutex>(sw_->mu);
+    return HX_OK;
+}
+
+hx_status Immediate::workspace(uint64_t bytes, void **ws) {
+    const bool grows = bytes > sw_->ws_bytes;
+    HX_TRY(grow_stream_buffer(stream_, sw_->ws, sw_->ws_bytes, bytes, "immediate workspace"));
+    if (grows) sw_->lookback = LookbackState{};
+    *ws = sw_->ws;
+    return HX_OK;
+}
+
+hx_status Immediate::scratch(uint64_t bytes, void **scratch) {
     *scratch = nullptr;
     if (bytes == 0) return HX_OK;
-    std::lock_guard<std::mutex> lock(dev->ws_mu);
-    if (bytes > dev->scratch_bytes) {
-        if (dev->scratch) {
-            HX_HIP(hipDeviceSynchronize(), HX_ERR_DISPATCH_FAILED, "hipDeviceSynchronize");
-            HX_HIP(hipFree(dev->scratch), HX_ERR_ALLOCATION_FAILED, "scratch hipFree");
-            dev->scratch = nullptr;
-            dev->scratch_bytes = 0;
-        }
-        const uint64_t grow = bytes < (1ull << 20) ? (1ull << 20) : bytes;
-        HX_TRY(alloc_workspace(dev, grow, &dev->scratch));
-        dev->scratch_bytes = grow;
-    }
-    *scratch = dev->scratch;
+    HX_TRY(grow_stream_buffer(stream_, sw_->scratch, sw_->scratch_bytes, bytes, "immediate scratch"));
+    *scratch = sw_->scratch;
     return HX_OK;
 }
 
@@ -264,8 +291,10 @@ hx_status hx_device_close(hx_device *dev) {
         if (dev->pinned[i]) (void)hipHostFree(dev->pinned[i]);
         if (dev->pinned_ev[i]) (void)hipEventDestroy(dev->pinned_ev[i]);
     }
-    if (dev->ws) (void)hipFree(dev->ws);
-    if (dev->scratch) (void)hipFree(dev->scratch);
+    for (auto &entry : dev->immediate) {
+        if (entry.second->ws) (void)hipFree(entry.second->ws);
+        if (entry.second->scratch) (void)hipFree(entry.second->scratch);
+    }
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return ok();
@@ -540,6 +569,7 @@ hx_status hx_event_elapsed_ms(hx_event start, hx_event stop, float *ms) {
 hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream) {
     if (!plan) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan");
     HX_TRY(bind_device(plan->dev));
+    std::lock_guard<std::mutex> guard(plan->mu);
     HX_TRY(plan->dispatch(pick_stream(plan->dev, stream)));
     return ok();
 }
@@ -550,6 +580,7 @@ hx_status hx_plan_dispatch_batch(hx_plan *const *plans, uint64_t count, hx_strea
         if (!plans[i]) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan at batch index %llu", (unsigned long long)i);
     for (uint64_t i = 0; i < count; ++i) {
         HX_TRY(bind_device(plans[i]->dev));
+        std::lock_guard<std::mutex> guard(plans[i]->mu);
         HX_TRY(plans[i]->dispatch(pick_stream(plans[i]->dev, stream)));
     }
     return ok();

@@ -22,6 +22,17 @@
  * hx_write_sub, hx_copy and hx_synchronize are synchronous, like the
  * reference's transfers (crates/hephaestus-rocm/src/infrastructure/
  * memory.rs:102-131,207-258).
+ *
+ * Threads: a device handle may be shared by host threads, like the
+ * reference's Send + Sync device (crates/hephaestus-rocm/src/application/
+ * pipeline.rs:101-108).  The immediate (un-prepared) entry points keep their
+ * partials and look-back state per stream, and calls on one stream from
+ * several threads are serialised from workspace lookup to launch, so
+ * immediate calls on any mix of threads and streams never share scratch
+ * memory.  A plan (hx_prepare_*) owns one workspace: dispatches of the same
+ * plan are serialised across threads, and the caller orders dispatches of
+ * one plan that go to different streams (an event, or a synchronize), as
+ * for any other work on those streams.
  */
 #ifndef HX_H
 #define HX_H
@@ -225,8 +236,8 @@ hx_status hx_plan_axis_scan(const hx_layout *in, uint64_t in_buf_len,
  * full_reduction_seam.rs:55-120).  `out` must be a 1-element view
  * (full_reduction_seam.rs:65-73).  op is SUM, PROD, MIN or MAX (MEAN divides
  * the sum by the element count).  `prologue` (may be NULL) applies
- * y = fmaf(a,x,b) to f32 inputs first.  Immediate form: uses a
- * device-owned workspace, so calls on one device must be stream-ordered. */
+ * y = fmaf(a,x,b) to f32 inputs first.  Immediate form: partials live in
+ * the workspace of the stream it launches on (see Threads above). */
 hx_status hx_reduce_full(hx_device *dev, hx_op op, hx_dtype dtype,
                          const void *in, uint64_t in_buf_len,
                          const hx_layout *in_layout, void *out,
@@ -402,8 +413,8 @@ hx_status hx_vector_binary(hx_device *dev, hx_vector_op op, hx_dtype dtype,
 
 /* dispatch_full / dispatch_prepared / dispatch_scan (core reduction.rs:
  * 222,304-308; scan.rs:259-263): re-run a prepared plan on `stream`.
- * Allocates nothing.  Plans must not be dispatched concurrently with
- * themselves. */
+ * Allocates nothing.  Concurrent calls on one plan are serialised; a plan
+ * dispatched on two streams must be ordered by the caller between them. */
 hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream);
 /* submit_prepared_reduction_batch (rocm application/prepared_reduction.rs:
  * 164-174): dispatch `count` plans in order on `stream` with no host
