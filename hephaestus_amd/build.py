@@ -30,6 +30,7 @@ SOURCES = [
     "csrc/map_reduce.hip",
     "csrc/vector.hip",
     "csrc/dense_vector.cpp",
+    "csrc/noalloc.hip",
 ]
 HEADERS = ["csrc/hx_device.hpp", "csrc/hx_internal.hpp"]
 ARCH = "gfx950"

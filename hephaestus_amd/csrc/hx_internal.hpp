@@ -60,6 +60,10 @@ struct hx_device {
     // drained, so an entry never serves two live streams at once.
     std::mutex streams_mu;
     std::unordered_map<hipStream_t, std::unique_ptr<hx::StreamWorkspace>> immediate;
+
+    // This device's copy of the no-allocation scratch array (its device
+    // address, looked up at hx_device_open with the device current).
+    void *noalloc_scratch = nullptr;
 };
 
 namespace hx {
@@ -213,6 +217,13 @@ uint64_t scan_workspace_bytes(const ScanArgs &args);
 bool scan_uses_lookback(const ScanArgs &args);
 hx_status launch_scan(const ScanArgs &args, void *ws, uint64_t ws_bytes,
                       LookbackState &st, hipStream_t stream);
+
+// The no-allocation scan (noalloc.hip): the device address of the current
+// device's scratch array, its size, and a scan whose whole workspace is that
+// array (rejected when the scan needs more).
+hx_status lookup_noalloc_scratch(void **ptr);
+uint64_t noalloc_scratch_bytes();
+hx_status launch_scan_noalloc(const ScanArgs &args, void *scratch, hipStream_t stream);
 
 struct SegmentedArgs {
     hx_op op;

@@ -423,6 +423,20 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
     return ok();
 }
 
+uint64_t hx_noalloc_scratch_bytes(void) { return noalloc_scratch_bytes(); }
+
+hx_status hx_scan_noalloc(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
+                          hx_scan_direction direction, const void *in, uint64_t in_buf_len,
+                          const hx_layout *in_layout, uint32_t axis, void *out, uint64_t out_buf_len,
+                          const hx_layout *out_layout, hx_stream stream) {
+    ScanArgs a;
+    HX_TRY(plan_scan(op, dtype, kind, direction, in, in_buf_len, in_layout, axis, out, out_buf_len,
+                     out_layout, &a));
+    HX_TRY(bind_device(dev));
+    HX_TRY(launch_scan_noalloc(a, dev->noalloc_scratch, pick_stream(dev, stream)));
+    return ok();
+}
+
 hx_status hx_prepare_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
                           hx_scan_direction direction, const void *in, uint64_t in_buf_len,
                           const hx_layout *in_layout, uint32_t axis, void *out, uint64_t out_buf_len,

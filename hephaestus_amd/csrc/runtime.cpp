@@ -258,6 +258,12 @@ hx_status hx_device_open(int32_t ordinal, hx_device **out) {
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) == hipSuccess) info.free_memory_bytes = free_b;
 
+    // This device's no-allocation scratch, looked up with the device current.
+    {
+        hx_status s = lookup_noalloc_scratch(&dev->noalloc_scratch);
+        if (s != HX_OK) return bail(s);
+    }
+
     // Default-priority stream (never a priority stream).
     err = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking);
     if (err != hipSuccess)

@@ -257,6 +257,19 @@ class RocmScanOps:
             )
         )
 
+    def scan_axis_into_noalloc(self, device: RocmDevice, op, input: StridedView, axis: int,
+                               direction: ScanDirection, output: StridedView,
+                               kind: ScanKind = ScanKind.Inclusive, stream=None) -> None:
+        """scan_axis_into through hx_scan_noalloc: no device allocation; the
+        workspace is the device's fixed scratch array."""
+        _ffi.check(
+            _ffi.lib().hx_scan_noalloc(
+                device.handle, op.code, hx_dtype(input.buffer.dtype), int(kind), int(direction),
+                input.buffer.ptr, len(input.buffer), _lp(input.layout), int(axis),
+                output.buffer.ptr, len(output.buffer), _lp(output.layout), stream,
+            )
+        )
+
     def prepare_scan_axis(self, device: RocmDevice, op, input: StridedView, axis: int,
                           direction: ScanDirection, output: StridedView,
                           kind: ScanKind = ScanKind.Inclusive) -> PreparedPlan:

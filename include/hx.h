@@ -312,6 +312,25 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
                   uint64_t in_buf_len, const hx_layout *in_layout,
                   uint32_t axis, void *out, uint64_t out_buf_len,
                   const hx_layout *out_layout, hx_stream stream);
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): hx_scan with the same arguments and
+ * results, whose whole workspace is a fixed 2 MiB device array per GPU
+ * (hx_noalloc_scratch_bytes), so it calls no hipMalloc, hipFree or
+ * allocating library routine.  A scan that needs more workspace (1-D f32
+ * scans beyond about 2^31 elements, u32 ones beyond the grid limit, large
+ * single-pass column scans) is rejected with HX_ERR_DISPATCH_FAILED before
+ * anything is launched.  Every call on a GPU shares that GPU's array: calls
+ * queued on one stream run in order, calls that overlap on one GPU (other
+ * streams, other threads) race. */
+hx_status hx_scan_noalloc(hx_device *dev, hx_op op, hx_dtype dtype,
+                          hx_scan_kind kind, hx_scan_direction direction,
+                          const void *in, uint64_t in_buf_len,
+                          const hx_layout *in_layout, uint32_t axis, void *out,
+                          uint64_t out_buf_len, const hx_layout *out_layout,
+                          hx_stream stream);
+/* Size in bytes of each GPU's no-allocation scratch array. */
+uint64_t hx_noalloc_scratch_bytes(void);
 /* ScanOps::prepare_scan_axis (core scan.rs:242-252). */
 hx_status hx_prepare_scan(hx_device *dev, hx_op op, hx_dtype dtype,
                           hx_scan_kind kind, hx_scan_direction direction,
