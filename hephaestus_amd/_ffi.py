@@ -132,6 +132,7 @@ SIGNATURES = {
     "hx_reduce_axis": (I32, [P, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_prepare_reduce_axis": (I32, [P, I32, I32, P, U64, LP, U32, P, U64, LP, POINTER(P)]),
     "hx_reduce_rows": (I32, [P, I32, P, U64, U64, U64, U64, U64, AP, P, P, P, U64, P]),
+    "hx_prepare_reduce_rows": (I32, [P, I32, P, U64, U64, U64, U64, U64, AP, P, P, P, U64, POINTER(P)]),
     "hx_scan": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_scan_noalloc": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_noalloc_scratch_bytes": (U64, []),

@@ -52,6 +52,20 @@ hx_status read_prologue(const hx_affine *pro, hx_dtype dtype, bool *affine, floa
 
 bool aliases(const void *a, const void *b) { return a != nullptr && a == b; }
 
+// Integer means divide the wrapped sum by the element count in the element
+// type, as the reference's `acc / (T)axis_len` does (rocm axis_reduction.rs:
+// 78-108); a count that the type cannot hold has no such divisor, so it is
+// rejected rather than truncated.
+hx_status check_mean_divisor(hx_dtype dtype, uint64_t n) {
+    if (dtype == HX_DTYPE_I32 && n > 0x7FFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "mean of %llu i32 elements: the count exceeds the i32 divisor range",
+                    (unsigned long long)n);
+    if (dtype == HX_DTYPE_U32 && n > 0xFFFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "mean of %llu u32 elements: the count exceeds the u32 divisor range",
+                    (unsigned long long)n);
+    return HX_OK;
+}
+
 // ---------------------------------------------------------------- full
 
 // rocm full_reduction_seam.rs:65-78: output storage, output size == 1,
@@ -96,6 +110,7 @@ hx_status plan_full(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
     a->out_index = nullptr;
     if (op == HX_OP_MEAN && n == 0)
         return fail(HX_ERR_DISPATCH_FAILED, "mean is undefined for an empty operand");
+    if (op == HX_OP_MEAN) HX_TRY(check_mean_divisor(dtype, n));
     return HX_OK;
 }
 
@@ -134,6 +149,7 @@ hx_status plan_axis(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
     if (op == HX_OP_ARGMAX && axis_len > 0xFFFFFFFFull)
         return fail(HX_ERR_DISPATCH_FAILED, "argmax axis length %llu exceeds the u32 index range",
                     (unsigned long long)axis_len);
+    if (op == HX_OP_MEAN) HX_TRY(check_mean_divisor(dtype, axis_len));
     *a = AxisArgs{};
     a->op = op;
     a->dtype = dtype;
@@ -152,6 +168,59 @@ hx_status plan_axis(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
 struct AxisPlan final : hx_plan {
     AxisArgs args;
     hx_status dispatch(hipStream_t stream) override { return launch_axis_reduce(args, ws, ws_bytes, stream); }
+};
+
+// Fused rows: validation shared by the immediate and prepared forms.
+hx_status plan_rows(hx_dtype dtype, const void *in, uint64_t in_buf_len, uint64_t rows, uint64_t cols,
+                    uint64_t row_stride, uint64_t offset, const hx_affine *prologue, void *out_sum, void *out_max,
+                    uint32_t *out_argmax, uint64_t out_len, RowsArgs *args) {
+    HX_TRY(check_dtype(dtype));
+    bool affine;
+    float pa, pb;
+    HX_TRY(read_prologue(prologue, dtype, &affine, &pa, &pb));
+    if (!out_sum && !out_max && !out_argmax)
+        return fail(HX_ERR_DISPATCH_FAILED, "row reduction needs at least one output");
+    if (out_len != rows) return length_mismatch(out_len, rows);
+    if ((out_max || out_argmax) && cols == 0 && rows > 0)
+        return fail(HX_ERR_DISPATCH_FAILED, "%s_axis is undefined for empty axis 1",
+                    out_argmax ? "argmax" : "max");
+    if (out_argmax && cols > 0xFFFFFFFFull)
+        return fail(HX_ERR_DISPATCH_FAILED, "argmax row length %llu exceeds the u32 index range",
+                    (unsigned long long)cols);
+    if (rows > 1 && row_stride < cols)
+        return fail(HX_ERR_DISPATCH_FAILED, "row stride %llu is shorter than the row length %llu",
+                    (unsigned long long)row_stride, (unsigned long long)cols);
+    if (rows > 0 && cols > 0) {
+        const unsigned __int128 last =
+            (unsigned __int128)offset + (unsigned __int128)(rows - 1) * row_stride + (cols - 1);
+        if (last >= in_buf_len)
+            return fail(HX_ERR_DISPATCH_FAILED,
+                        "layout rejected: rows need %llu elements but the buffer holds %llu",
+                        (unsigned long long)(last + 1), (unsigned long long)in_buf_len);
+        if (!in) return fail(HX_ERR_DISPATCH_FAILED, "row reduction input is null");
+    }
+    if (aliases(in, out_sum) || aliases(in, out_max) || aliases(in, out_argmax))
+        return fail(HX_ERR_DISPATCH_FAILED, "axis reduction output buffer must not alias input buffer");
+    RowsArgs &a = *args;
+    a = RowsArgs{};
+    a.dtype = dtype;
+    a.base = in;
+    a.rows = rows;
+    a.cols = cols;
+    a.row_stride = row_stride;
+    a.offset = offset;
+    a.affine = affine;
+    a.a = pa;
+    a.b = pb;
+    a.out_sum = out_sum;
+    a.out_max = out_max;
+    a.out_argmax = out_argmax;
+    return HX_OK;
+}
+
+struct RowsPlan final : hx_plan {
+    RowsArgs args;
+    hx_status dispatch(hipStream_t stream) override { return launch_rows(args, ws, ws_bytes, stream); }
 };
 
 // ---------------------------------------------------------------- scan
@@ -349,46 +418,9 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_
                          uint64_t rows, uint64_t cols, uint64_t row_stride, uint64_t offset,
                          const hx_affine *prologue, void *out_sum, void *out_max,
                          uint32_t *out_argmax, uint64_t out_len, hx_stream stream) {
-    HX_TRY(check_dtype(dtype));
-    bool affine;
-    float pa, pb;
-    HX_TRY(read_prologue(prologue, dtype, &affine, &pa, &pb));
-    if (!out_sum && !out_max && !out_argmax)
-        return fail(HX_ERR_DISPATCH_FAILED, "row reduction needs at least one output");
-    if (out_len != rows) return length_mismatch(out_len, rows);
-    if ((out_max || out_argmax) && cols == 0 && rows > 0)
-        return fail(HX_ERR_DISPATCH_FAILED, "%s_axis is undefined for empty axis 1",
-                    out_argmax ? "argmax" : "max");
-    if (out_argmax && cols > 0xFFFFFFFFull)
-        return fail(HX_ERR_DISPATCH_FAILED, "argmax row length %llu exceeds the u32 index range",
-                    (unsigned long long)cols);
-    if (rows > 1 && row_stride < cols)
-        return fail(HX_ERR_DISPATCH_FAILED, "row stride %llu is shorter than the row length %llu",
-                    (unsigned long long)row_stride, (unsigned long long)cols);
-    if (rows > 0 && cols > 0) {
-        const unsigned __int128 last =
-            (unsigned __int128)offset + (unsigned __int128)(rows - 1) * row_stride + (cols - 1);
-        if (last >= in_buf_len)
-            return fail(HX_ERR_DISPATCH_FAILED,
-                        "layout rejected: rows need %llu elements but the buffer holds %llu",
-                        (unsigned long long)(last + 1), (unsigned long long)in_buf_len);
-        if (!in) return fail(HX_ERR_DISPATCH_FAILED, "row reduction input is null");
-    }
-    if (aliases(in, out_sum) || aliases(in, out_max) || aliases(in, out_argmax))
-        return fail(HX_ERR_DISPATCH_FAILED, "axis reduction output buffer must not alias input buffer");
-    RowsArgs a{};
-    a.dtype = dtype;
-    a.base = in;
-    a.rows = rows;
-    a.cols = cols;
-    a.row_stride = row_stride;
-    a.offset = offset;
-    a.affine = affine;
-    a.a = pa;
-    a.b = pb;
-    a.out_sum = out_sum;
-    a.out_max = out_max;
-    a.out_argmax = out_argmax;
+    RowsArgs a;
+    HX_TRY(plan_rows(dtype, in, in_buf_len, rows, cols, row_stride, offset, prologue, out_sum, out_max, out_argmax,
+                     out_len, &a));
     HX_TRY(bind_device(dev));
     const hipStream_t s = pick_stream(dev, stream);
     Immediate im;
@@ -398,6 +430,22 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_
     HX_TRY(im.scratch(bytes, &scratch));
     HX_TRY(launch_rows(a, scratch, bytes, s));
     return ok();
+}
+
+hx_status hx_prepare_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in, uint64_t in_buf_len,
+                                 uint64_t rows, uint64_t cols, uint64_t row_stride, uint64_t offset,
+                                 const hx_affine *prologue, void *out_sum, void *out_max,
+                                 uint32_t *out_argmax, uint64_t out_len, hx_plan **plan) {
+    if (!plan) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan out-pointer");
+    *plan = nullptr;
+    RowsArgs a;
+    HX_TRY(plan_rows(dtype, in, in_buf_len, rows, cols, row_stride, offset, prologue, out_sum, out_max, out_argmax,
+                     out_len, &a));
+    HX_TRY(bind_device(dev));
+    RowsPlan *p = new (std::nothrow) RowsPlan();
+    if (!p) return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of plan failed");
+    p->args = a;
+    return finish_plan(dev, p, rows_workspace_bytes(a), plan);
 }
 
 hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,

@@ -150,8 +150,10 @@ __device__ __forceinline__ void write_result_impl(const FullParams &p, typename 
         if constexpr (std::is_same<T, float>::value) {
             *(float *)p.out_value = (float)(r / (double)p.n);
         } else if constexpr (std::is_same<T, int32_t>::value) {
+            // n <= INT32_MAX here (the host rejects larger integer means)
             *(int32_t *)p.out_value = (int32_t)r / (int32_t)p.n;
         } else {
+            // n <= UINT32_MAX here
             *(uint32_t *)p.out_value = (uint32_t)r / (uint32_t)p.n;
         }
     } else if constexpr (K == kMax || K == kMin) {

@@ -381,6 +381,26 @@ class RocmAxisReductionOps {
                              out_max ? out_max->device_ptr() : nullptr,
                              out_argmax ? out_argmax->device_ptr() : nullptr, out_len, stream));
     }
+    // The prepared form (prepared_axis_reduction.rs:20-222): dispatch
+    // re-reads the bound input and allocates nothing.
+    template <typename T>
+    PreparedPlan prepare_reduce_rows_fused(RocmDevice &dev, const RocmBuffer<T> &input, uint64_t rows,
+                                           uint64_t cols, uint64_t row_stride, const Affine *prologue,
+                                           RocmBuffer<T> *out_sum, RocmBuffer<T> *out_max,
+                                           RocmBuffer<uint32_t> *out_argmax) const {
+        uint64_t out_len = rows;
+        if (out_sum) out_len = out_sum->len();
+        else if (out_max) out_len = out_max->len();
+        else if (out_argmax) out_len = out_argmax->len();
+        hx_affine a;
+        hx_plan *p = nullptr;
+        check(hx_prepare_reduce_rows(dev.raw(), Scalar<T>::dtype, input.device_ptr(), input.len(), rows, cols,
+                                     row_stride, 0, detail::affine(prologue, a),
+                                     out_sum ? out_sum->device_ptr() : nullptr,
+                                     out_max ? out_max->device_ptr() : nullptr,
+                                     out_argmax ? out_argmax->device_ptr() : nullptr, out_len, &p));
+        return PreparedPlan(p);
+    }
 };
 
 // ------------------------------------------------------------------ ScanOps

@@ -215,11 +215,8 @@ class RocmAxisReductionOps:
     def dispatch_prepared(self, device: RocmDevice, prepared: PreparedPlan, stream=None) -> None:
         prepared.dispatch(stream)
 
-    def reduce_rows_fused(self, device: RocmDevice, input: RocmBuffer, rows: int, cols: int,
-                          row_stride: int | None = None, offset: int = 0, prologue=None,
-                          out_sum: RocmBuffer | None = None, out_max: RocmBuffer | None = None,
-                          out_argmax: RocmBuffer | None = None, stream=None) -> None:
-        """Sum, max and argmax of y = fmaf(a, x, b) per row, from one read."""
+    @staticmethod
+    def _rows_args(input, rows, cols, row_stride, offset, prologue, out_sum, out_max, out_argmax):
         row_stride = cols if row_stride is None else row_stride
         outs = [b for b in (out_sum, out_max, out_argmax) if b is not None]
         out_len = len(outs[0]) if outs else rows
@@ -232,15 +229,29 @@ class RocmAxisReductionOps:
             if b is not None and b.dtype != input.dtype:
                 raise errors.DispatchFailed("sum/max outputs must have the input dtype")
         aff = _ffi.affine_struct(prologue)
-        _ffi.check(
-            _ffi.lib().hx_reduce_rows(
-                device.handle, hx_dtype(input.dtype), input.ptr, len(input), int(rows), int(cols),
-                int(row_stride), int(offset), ctypes.byref(aff) if aff else None,
-                out_sum.ptr if out_sum is not None else None,
+        return (hx_dtype(input.dtype), input.ptr, len(input), int(rows), int(cols), int(row_stride), int(offset),
+                ctypes.byref(aff) if aff else None, out_sum.ptr if out_sum is not None else None,
                 out_max.ptr if out_max is not None else None,
-                out_argmax.ptr if out_argmax is not None else None, out_len, stream,
-            )
-        )
+                out_argmax.ptr if out_argmax is not None else None, out_len)
+
+    def reduce_rows_fused(self, device: RocmDevice, input: RocmBuffer, rows: int, cols: int,
+                          row_stride: int | None = None, offset: int = 0, prologue=None,
+                          out_sum: RocmBuffer | None = None, out_max: RocmBuffer | None = None,
+                          out_argmax: RocmBuffer | None = None, stream=None) -> None:
+        """Sum, max and argmax of y = fmaf(a, x, b) per row, from one read."""
+        args = self._rows_args(input, rows, cols, row_stride, offset, prologue, out_sum, out_max, out_argmax)
+        _ffi.check(_ffi.lib().hx_reduce_rows(device.handle, *args, stream))
+
+    def prepare_reduce_rows_fused(self, device: RocmDevice, input: RocmBuffer, rows: int, cols: int,
+                                  row_stride: int | None = None, offset: int = 0, prologue=None,
+                                  out_sum: RocmBuffer | None = None, out_max: RocmBuffer | None = None,
+                                  out_argmax: RocmBuffer | None = None) -> PreparedPlan:
+        """Prepared reduce_rows_fused (hx_prepare_reduce_rows): validated
+        once, dispatched without allocation, batchable."""
+        args = self._rows_args(input, rows, cols, row_stride, offset, prologue, out_sum, out_max, out_argmax)
+        plan = ctypes.c_void_p()
+        _ffi.check(_ffi.lib().hx_prepare_reduce_rows(device.handle, *args, ctypes.byref(plan)))
+        return PreparedPlan(device, plan.value, (input, out_sum, out_max, out_argmax))
 
 
 class RocmScanOps:

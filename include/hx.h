@@ -300,6 +300,21 @@ hx_status hx_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in,
                          void *out_max, uint32_t *out_argmax,
                          uint64_t out_len, hx_stream stream);
 
+/* Prepared form of hx_reduce_rows, as prepare_reduce_axis_into is of
+ * reduce_axis_into (crates/hephaestus-rocm/src/application/
+ * prepared_axis_reduction.rs:20-222): binds the operands, validates once and
+ * owns the workspace of the split forms, so hx_plan_dispatch allocates
+ * nothing, re-reads the bound input on every dispatch, and the plan can go
+ * to hx_plan_dispatch_batch (submit_prepared_axis_reduction_batch,
+ * prepared_axis_reduction.rs:84-92). */
+hx_status hx_prepare_reduce_rows(hx_device *dev, hx_dtype dtype, const void *in,
+                                 uint64_t in_buf_len, uint64_t rows,
+                                 uint64_t cols, uint64_t row_stride,
+                                 uint64_t offset, const hx_affine *prologue,
+                                 void *out_sum, void *out_max,
+                                 uint32_t *out_argmax, uint64_t out_len,
+                                 hx_plan **plan);
+
 /* ---------------------------------------------------------------- ScanOps */
 
 /* ScanOps::scan_axis_into (core scan.rs:219-233) over rank-1 or rank-2

@@ -220,3 +220,29 @@ def test_entry_points_validate_before_touching_the_device():
     st = lib.hx_reduce_full(None, _ffi.OP_SUM, _ffi.DTYPE_U32, 0x1000, 12, ctypes.byref(lay),
                             0x2000, 1, ctypes.byref(_ffi.layout_struct(L([1]))), ctypes.byref(aff), None)
     assert st == _ffi.INVALID_CONFIGURATION and "f32" in _ffi.last_message()
+
+
+def test_integer_mean_counts_beyond_the_divisor_type_are_rejected():
+    """An integer mean divides in the element type (the reference's
+    `acc / (T)axis_len`); counts the type cannot hold are rejected on the
+    host, before the device is touched, instead of being truncated.  Counts
+    that fit reach the device step (here: the null device handle)."""
+    lib = hx.load_native()
+    one = ctypes.byref(_ffi.layout_struct(L([1])))
+    cases = [(_ffi.DTYPE_I32, 2**31, "i32 divisor"), (_ffi.DTYPE_U32, 2**32, "u32 divisor")]
+    for dtype, n, text in cases:
+        lay = ctypes.byref(_ffi.layout_struct(L([n])))
+        st = lib.hx_reduce_full(None, _ffi.OP_MEAN, dtype, 0x1000, n, lay, 0x2000, 1, one, None, None)
+        assert st == _ffi.DISPATCH_FAILED and text in _ffi.last_message(), _ffi.last_message()
+        fits = ctypes.byref(_ffi.layout_struct(L([n - 1])))
+        st = lib.hx_reduce_full(None, _ffi.OP_MEAN, dtype, 0x1000, n - 1, fits, 0x2000, 1, one, None, None)
+        assert st == _ffi.INVALID_CONFIGURATION and _ffi.last_message() == "null device handle"
+        # axis form: 2 rows of n elements reduced along axis 1
+        rows = ctypes.byref(_ffi.layout_struct(L([2, n])))
+        out = ctypes.byref(_ffi.layout_struct(L([2, 1])))
+        st = lib.hx_reduce_axis(None, _ffi.OP_MEAN, dtype, 0x1000, 2 * n, rows, 1, 0x2000, 2, out, None)
+        assert st == _ffi.DISPATCH_FAILED and text in _ffi.last_message(), _ffi.last_message()
+    # f32 means divide in f64: no such limit
+    lay = ctypes.byref(_ffi.layout_struct(L([2**33])))
+    st = lib.hx_reduce_full(None, _ffi.OP_MEAN, _ffi.DTYPE_F32, 0x1000, 2**33, lay, 0x2000, 1, one, None, None)
+    assert st == _ffi.INVALID_CONFIGURATION and _ffi.last_message() == "null device handle"

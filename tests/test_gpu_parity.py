@@ -132,6 +132,39 @@ def test_full_reduce_output_offset(device):
     assert list(device.download_owned(out)) == [99, 99, 45, 99]
 
 
+def test_integer_mean_at_the_largest_counts(device):
+    """Integer means at counts beyond 2^31: the wrapped sum divided by the
+    count in the element type.  A constant input gives the sum in closed
+    form (c*n mod 2^32); an i32 count of 2^31 is rejected before launch and
+    leaves the output untouched."""
+    n_u = (1 << 31) + 3  # 8 GiB of u32
+    print(f"[mean] u32 mean over {n_u} elements, i32 over {2**31 - 1}", flush=True)
+    buf = device.alloc_uninitialized(np.uint32, n_u)
+    out = device.upload(np.full(1, 99, np.uint32))
+    one = Layout.c_contiguous([1])
+    for c in (1, 3, 0xFFFFFFFF):
+        device.fill_uniform_int(buf, seed=1, lo=c, hi=c)
+        FULL.reduce_full_into(device, hx.MeanOp, StridedView(buf, Layout.c_contiguous([n_u])), StridedView(out, one))
+        assert int(device.download_owned(out)[0]) == ((c * n_u) % 2**32) // n_u, c
+    ibuf = hx.RocmBuffer(device, buf.ptr, n_u, np.int32)  # the same memory viewed as i32
+    try:
+        iout = device.upload(np.full(1, 99, np.int32))
+        n_i = (1 << 31) - 1
+        for c in (1, -1, 3):
+            device.fill_uniform_int(ibuf, seed=1, lo=c, hi=c)
+            FULL.reduce_full_into(device, hx.MeanOp, StridedView(ibuf, Layout.c_contiguous([n_i])),
+                                  StridedView(iout, one))
+            wrapped = ((c * n_i + 2**31) % 2**32) - 2**31
+            assert int(device.download_owned(iout)[0]) == int(wrapped / n_i), c  # C division truncates
+        device.write_buffer(iout, np.full(1, 99, np.int32))
+        with pytest.raises(hx.DispatchFailed, match="i32 divisor range"):
+            FULL.reduce_full_into(device, hx.MeanOp, StridedView(ibuf, Layout.c_contiguous([1 << 31])),
+                                  StridedView(iout, one))
+        assert int(device.download_owned(iout)[0]) == 99
+    finally:
+        ibuf.ptr = None  # the memory belongs to `buf`
+
+
 def test_full_sum_with_prologue(device, oracle):
     x = oracle.uniform_real((1 << 20) + 5, seed=2, lo=-1.0, hi=1.0)
     ref, ab = oracle.full_sum(x, prologue=(0.5, 0.25))
@@ -802,6 +835,83 @@ def test_prepared_batch_submission(device, oracle):
     assert np.array_equal(device.download_owned(scan_out), oracle.scan_sum(y))
     assert device.download_owned(pl1.output)[0] == oracle.full_sum(y)
     hx.submit_prepared_reduction_batch([])
+
+
+def _check_rows(device, oracle, host, rows, cols, ld, offset, pro, s, m, i):
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, cols, ld, prologue=pro)
+    assert np.array_equal(device.download_owned(i), i_ref)
+    assert np.array_equal(device.download_owned(m), m_ref)
+    got = device.download_owned(s).astype(np.float64)
+    if host.dtype == np.float32:
+        assert np.all(np.abs(got - s_ref) <= f32_bound(cols, a_ref))
+    else:
+        assert np.array_equal(device.download_owned(s), s_ref)
+
+
+@pytest.mark.parametrize("rows,cols,ld,offset", [(4096, 1000, 1000, 0), (300, 4099, 4101, 3), (8, 1 << 20, 1 << 20, 0)])
+def test_prepared_rows_allocate_once_and_rebind(device, oracle, rows, cols, ld, offset):
+    """hx_prepare_reduce_rows (prepared_axis_reduction.rs:20-222): dispatches
+    re-read the bound input (rebind contract), and the few-long-rows split
+    form keeps its partials in the plan's own workspace."""
+    n = offset + (rows - 1) * ld + cols
+    pro = (0.5, 0.25)
+    x = oracle.normal(n, seed=31)
+    buf = device.upload(x)
+    s, m = device.alloc_zeroed(np.float32, rows), device.alloc_zeroed(np.float32, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    plan = AXIS.prepare_reduce_rows_fused(device, buf, rows, cols, row_stride=ld, offset=offset, prologue=pro,
+                                          out_sum=s, out_max=m, out_argmax=i)
+    if cols >= 1 << 20:
+        assert plan.workspace_bytes() > 0  # split rows stage chunk partials in the plan
+    for _ in range(2):
+        plan.dispatch()
+    _check_rows(device, oracle, x, rows, cols, ld, offset, pro, s, m, i)
+    y = oracle.normal(n, seed=32)
+    device.write_buffer(buf, y)
+    plan.dispatch()
+    _check_rows(device, oracle, y, rows, cols, ld, offset, pro, s, m, i)
+
+
+def test_prepared_rows_batch_submission(device, oracle):
+    """Prepared fused-rows plans go through submit_prepared_axis_reduction_batch
+    (prepared_axis_reduction.rs:84-92) with an axis plan, then rebind."""
+    rows, cols = 1000, 777
+    xf = oracle.normal(rows * cols, seed=33)
+    xi = oracle.uniform_int(rows * cols, seed=34, lo=-1000, hi=1000, dtype=np.int32)
+    bf, bi = device.upload(xf), device.upload(xi)
+    sf, mf, af = (device.alloc_zeroed(np.float32, rows), device.alloc_zeroed(np.float32, rows),
+                  device.alloc_zeroed(np.uint32, rows))
+    si, mi, ai = (device.alloc_zeroed(np.int32, rows), device.alloc_zeroed(np.int32, rows),
+                  device.alloc_zeroed(np.uint32, rows))
+    colsum = device.alloc_zeroed(np.int32, cols)
+    pf = AXIS.prepare_reduce_rows_fused(device, bf, rows, cols, prologue=(0.5, 0.25), out_sum=sf, out_max=mf,
+                                        out_argmax=af)
+    pi = AXIS.prepare_reduce_rows_fused(device, bi, rows, cols, out_sum=si, out_max=mi, out_argmax=ai)
+    pc = AXIS.prepare_reduce_axis_into(device, hx.SumOp, StridedView(bi, Layout.c_contiguous([rows, cols])), 0,
+                                       StridedView(colsum, Layout.c_contiguous([1, cols])))
+    for _ in range(2):
+        hx.submit_prepared_axis_reduction_batch(device, [pf, pi, pc])
+        _check_rows(device, oracle, xf, rows, cols, cols, 0, (0.5, 0.25), sf, mf, af)
+        _check_rows(device, oracle, xi, rows, cols, cols, 0, None, si, mi, ai)
+        want = xi.reshape(rows, cols).astype(np.int64).sum(axis=0).astype(np.int32)
+        assert np.array_equal(device.download_owned(colsum), want)
+        xf = oracle.normal(rows * cols, seed=35)
+        xi = oracle.uniform_int(rows * cols, seed=36, lo=-1000, hi=1000, dtype=np.int32)
+        device.write_buffer(bf, xf)
+        device.write_buffer(bi, xi)
+
+
+def test_prepared_rows_validate_at_prepare(device):
+    """Invalid operands are rejected when the plan is prepared, with the
+    immediate form's messages, and no plan is returned."""
+    buf = device.alloc_zeroed(np.float32, 100)
+    m = device.alloc_zeroed(np.float32, 10)
+    with pytest.raises(hx.DispatchFailed, match="layout rejected"):
+        AXIS.prepare_reduce_rows_fused(device, buf, 10, 11, out_max=m)
+    with pytest.raises(hx.DispatchFailed, match="max_axis is undefined for empty axis 1"):
+        AXIS.prepare_reduce_rows_fused(device, buf, 10, 0, out_max=m)
+    with pytest.raises(hx.DispatchFailed, match="row stride 9 is shorter"):
+        AXIS.prepare_reduce_rows_fused(device, buf, 10, 10, row_stride=9, out_max=m)
 
 
 def test_batch_rejects_null_plan_before_running_any(device):
