@@ -1,25 +1,41 @@
 #!/usr/bin/env python3
 """Throughput of the reduction / scan hot path on one MI355X.
 
-Metric: achieved HBM GB/s (and fraction of the 8 TB/s peak)
-for the u32 exclusive scan and the f32 sum-reduce at 2^28 elements.  A step
-is one exclusive scan of the 2^28-element u32 operand (the headline configuration); inputs
-are generated in HBM before timing, and every step is one launch of the
-single-pass look-back scan kernel.  The f32 sum-reduce at 2^28 is timed the
-same way and reported under "secondary".
+Metric: achieved HBM GB/s (and fraction of the 8 TB/s peak) for the u32
+exclusive scan and the f32 sum-reduce at 2^28 elements.  A step is one
+exclusive scan of the 2^28-element u32 operand (the
+headline); inputs are generated in HBM before timing and every step is one
+launch of the single-pass look-back scan kernel.
 
-`value` and `roofline.achieved` are algorithmic bytes (read 4n + write 4n
-for the scan) divided by the mean launch time, measured with HIP events on
-the stream the kernels run on.  `cpu_baseline` times the CPU oracle (a
-sequential port of the same semantics) on this host over the same input.
+The default run also times, the same way, every other BASELINE.json
+configuration and the f32 sum-reduce at 2^28 (the metric's second half),
+under "secondary":
+  cfg1  f32 full sum, n = 2^20 (the CPU reference device's plumbing case;
+        cache-resident on the GPU)
+  cfg3  f32 row-wise sum, max, argmax of fmaf(0.5, x, 0.25), 65536 x 4096
+  cfg4  i32 segmented sum, n = 2^27, geometric(300) segment lengths
+  cfg5  f32 inclusive scan, n = 2^30
+Each line carries its roofline, the mean, median and minimum time per launch,
+a CPU baseline (the oracle on this host over a bounded sample) and the check
+of the GPU output.  "ceiling" times the best read+write streams on the same
+device in the same run: the library's copy kernel and the runtime's
+hipMemcpyAsync device-to-device blit, 1 GiB each way.
+
+Timing: HIP events on the device stream, which every launch here uses.  The
+mean comes from one pair of events around `steps` back-to-back launches;
+median and minimum from five further batches of steps/5 back-to-back
+launches, each between its own pair of events.  GB/s = algorithmic bytes per
+launch / mean time per launch.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload NAME]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -30,12 +46,12 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ("scan_u32", "sum_f32", "rows_f32", "segmented_i32", "segmented_short_i32", "scan_f32_2_30",
-             "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32")
+WORKLOADS = ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30",
+             "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
-KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "rows_f32": "rows_kernel",
-             "segmented_i32": "segmented_sum_kernel", "segmented_short_i32": "seg_short_kernel",
-             "scan_f32_2_30": "scan_tiles_kernel",
+KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "sum_f32_2_20": "full_reduce_kernel<",
+             "rows_f32": "rows_kernel", "segmented_i32": "segmented_sum_kernel",
+             "segmented_short_i32": "seg_short_kernel", "scan_f32_2_30": "scan_tiles_kernel",
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
              "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel"}
 
@@ -44,8 +60,37 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def time_launches(dev, run, steps: int, warmup: int, batches: int = 5) -> dict:
+    """Milliseconds per launch of `run`: the mean over one pair of events
+    around `steps` back-to-back launches, then the median and minimum over
+    `batches` further batches of steps/batches back-to-back launches, each
+    between a pair of events.  (An event between every two launches would
+    add its own fence to each launch.)"""
+    for _ in range(warmup):
+        run()
+    dev.synchronize()
+    start, stop = dev.event(), dev.event()
+    start.record()
+    for _ in range(steps):
+        run()
+    stop.record()
+    stop.synchronize()
+    mean = start.elapsed_ms(stop) / steps
+    per_batch = max(1, steps // batches)
+    evs = [dev.event() for _ in range(batches + 1)]
+    evs[0].record()
+    for b in range(batches):
+        for _ in range(per_batch):
+            run()
+        evs[b + 1].record()
+    evs[-1].synchronize()
+    per = [evs[b].elapsed_ms(evs[b + 1]) / per_batch for b in range(batches)]
+    dev.synchronize()
+    return {"mean_ms": mean, "median_ms": statistics.median(per), "min_ms": min(per)}
+
+
 def time_plan(dev, run, steps: int, warmup: int) -> float:
-    """Mean milliseconds per launch of `run` over `steps` back-to-back launches."""
+    """Mean milliseconds per launch (time_launches' first pass only)."""
     for _ in range(warmup):
         run()
     dev.synchronize()
@@ -64,8 +109,7 @@ def traffic_for(name: str):
     f = REPO / "profiles" / "pmc_traffic.json"
     if not f.exists():
         return None
-    data = json.loads(f.read_text())
-    entry = data.get(name)
+    entry = json.loads(f.read_text()).get(name)
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
@@ -75,7 +119,36 @@ def roofline(bytes_per_launch: float, ms: float, name: str) -> dict:
             "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_for(name)}
 
 
-def bench_scan_u32(hx, dev, args):
+def gbs(nbytes: float, ms: float) -> float:
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def _cpu_rate(run, bytes_per_pass: float, seconds: float = 2.0, max_reps: int = 50):
+    """(GB/s, passes, ms per pass) of `run()` repeated for about `seconds`."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            break
+    per = el / reps
+    return bytes_per_pass / per / 1e9, reps, per * 1e3
+
+
+def _cpu_line(gbs_, reps, ms, sample):
+    out = {"value": round(gbs_, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{sample}; {reps} passes, {ms:.1f} ms per pass"}
+    return out
+
+
+# ------------------------------------------------------------- workloads
+# Each returns {"n", "bytes", "run", "verify"}: `run` is one step on the
+# device stream, `verify()` checks the output of the last step against the
+# oracle and returns a short record, `cpu(seconds)` times the oracle.
+
+def wl_scan_u32(hx, dev):
+    """cfg 2 (headline): u32 exclusive scan, n = 2^28, uniform ints in [0, 256)."""
     from hephaestus_amd import Layout, StridedView
 
     n = 1 << 28
@@ -85,38 +158,125 @@ def bench_scan_u32(hx, dev, args):
     lay = Layout.c_contiguous([n])
     plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
                                               StridedView(out, lay), hx.ScanKind.Exclusive)
-    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
-    nbytes = 2 * 4 * n
-    return {"n": n, "ms": ms, "bytes": nbytes, "x": x, "out": out}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        host = dev.download_owned(x)
+        got = dev.download_owned(out)
+        ref = np.empty_like(host)
+        gb, reps, ms = _cpu_rate(lambda: oracle.lib().hxo_scan_sum_u32(host.ctypes.data, n, 1, 0, ref.ctypes.data),
+                                 8.0 * n, seconds)
+        cores = os.cpu_count() or 1
+        mt = np.empty_like(host)
+        t1 = time.perf_counter()
+        oracle.scan_excl_u32_threads(host, mt, cores)
+        tt = time.perf_counter() - t1
+        line = _cpu_line(gb, reps, ms, "the full 2^28-element u32 exclusive scan, sequential C oracle "
+                                       "(oracle/hx_oracle.c hxo_scan_sum_u32)")
+        line["multithread"] = {"value": round(8.0 * n / tt / 1e9, 3), "unit": "GB/s", "cores": cores,
+                               "sample": "one pass of the two-pass pthread scan hxo_scan_excl_u32_threads on "
+                                         "every host core", "equals_sequential": bool(np.array_equal(mt, ref))}
+        line["gpu_output_verified"] = bool(np.array_equal(got, ref))
+        return line
+
+    return {"n": n, "bytes": 8 * n, "run": plan.dispatch, "cpu": cpu, "verify": None,
+            "keep": (x, out, plan), "dtype": "u32",
+            "workload": "u32 exclusive prefix scan, n=2^28 (BASELINE configs[1], the headline)"}
 
 
-def bench_sum_f32(hx, dev, args):
+def _sum_f32(hx, dev, n, seed):
     from hephaestus_amd import Layout, StridedView
 
-    n = 1 << 28
     x = dev.alloc_uninitialized(np.float32, n)
-    dev.fill_uniform_real(x, seed=1, lo=-1.0, hi=1.0)
+    dev.fill_uniform_real(x, seed=seed, lo=-1.0, hi=1.0)
     out = dev.alloc_zeroed(np.float32, 1)
     plan = hx.RocmFullReductionOps().prepare_reduce_full(dev, hx.SumOp, StridedView(x, Layout.c_contiguous([n])),
                                                          StridedView(out, Layout.c_contiguous([1])))
-    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
-    return {"n": n, "ms": ms, "bytes": 4 * n + 4, "x": x, "out": out}
+
+    def verify():
+        from oracle import oracle
+
+        ref, ab = oracle.full_sum(dev.download_owned(x))
+        got = float(dev.download_owned(out)[0])
+        tol = 2 * oracle.ceil_log2(n) * 2.0**-23 * ab
+        return {"ok": abs(got - ref) <= tol, "check": "|gpu - f64 sum| <= 2*ceil(log2 n)*eps*sum|x|",
+                "err_over_eps_abs": abs(got - ref) / (2.0**-23 * ab)}
+
+    return plan, x, out, verify
 
 
-def bench_rows_f32(hx, dev, args):
+def wl_sum_f32(hx, dev):
+    """The metric's second half: f32 full sum, n = 2^28, uniform[-1, 1)."""
+    n = 1 << 28
+    plan, x, out, verify = _sum_f32(hx, dev, n, 1)
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        m = 1 << 26
+        h = oracle.uniform_real(m, 1, -1.0, 1.0)
+        return _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * m, seconds),
+                         "2^26 f32 (a quarter of the GPU input), oracle full_sum (f64 accumulation)")
+
+    return {"n": n, "bytes": 4 * n + 4, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (plan, x, out),
+            "dtype": "f32", "workload": "f32 full sum-reduce, n=2^28, uniform[-1,1)"}
+
+
+def wl_sum_f32_2_20(hx, dev):
+    """cfg 1: f32 full sum, n = 2^20 (cache-resident on the GPU)."""
+    n = 1 << 20
+    plan, x, out, verify = _sum_f32(hx, dev, n, 1)
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        h = oracle.uniform_real(n, 1, -1.0, 1.0)
+        return _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * n, seconds, max_reps=2000),
+                         "the full 2^20 f32 input, oracle full_sum (the CPU reference device's role)")
+
+    return {"n": n, "bytes": 4 * n + 4, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (plan, x, out),
+            "dtype": "f32", "workload": "f32 full sum-reduce, n=2^20 (BASELINE configs[0]; 4 MiB, cache-resident)"}
+
+
+def wl_rows_f32(hx, dev):
+    """cfg 3: per-row sum, max, argmax of fmaf(0.5, x, 0.25), 65536 x 4096
+    N(0,1) f32, one prepared launch."""
     rows, cols = 65536, 4096
     x = dev.alloc_uninitialized(np.float32, rows * cols)
     dev.fill_normal(x, seed=3)
     s = dev.alloc_uninitialized(np.float32, rows)
     m = dev.alloc_uninitialized(np.float32, rows)
     i = dev.alloc_uninitialized(np.uint32, rows)
-    ops = hx.RocmAxisReductionOps()
-    run = lambda: ops.reduce_rows_fused(dev, x, rows, cols, prologue=(0.5, 0.25), out_sum=s, out_max=m, out_argmax=i)
-    ms = time_plan(dev, run, args.steps, args.warmup)
-    return {"n": rows * cols, "ms": ms, "bytes": 4 * rows * cols + 12 * rows}
+    plan = hx.RocmAxisReductionOps().prepare_reduce_rows_fused(dev, x, rows, cols, prologue=(0.5, 0.25),
+                                                               out_sum=s, out_max=m, out_argmax=i)
+
+    def verify():
+        from oracle import oracle
+
+        s_ref, a_ref, m_ref, i_ref = oracle.rows(dev.download_owned(x), rows, cols, prologue=(0.5, 0.25))
+        got = dev.download_owned(s).astype(np.float64)
+        tol = 2 * oracle.ceil_log2(cols) * 2.0**-23 * a_ref
+        ok = (np.array_equal(dev.download_owned(m), m_ref) and np.array_equal(dev.download_owned(i), i_ref)
+              and bool(np.all(np.abs(got - s_ref) <= tol)))
+        return {"ok": ok, "check": "max and argmax bit-exact, sums within 2*ceil(log2 cols)*eps*sum|y|"}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        r = 4096
+        h = oracle.normal(r * cols, 3)
+        return _cpu_line(*_cpu_rate(lambda: oracle.rows(h, r, cols, prologue=(0.5, 0.25)), 4.0 * r * cols + 12.0 * r,
+                                    seconds),
+                         "4096 x 4096 f32 (1/16 of the GPU rows), oracle rows (sum, max, argmax of fmaf(.5,x,.25))")
+
+    return {"n": rows * cols, "bytes": 4 * rows * cols + 12 * rows, "run": plan.dispatch, "cpu": cpu,
+            "verify": verify, "keep": (x, s, m, i, plan), "dtype": "f32",
+            "workload": "f32 row-wise sum+max+argmax of fmaf(0.5,x,0.25), 65536 x 4096 (BASELINE configs[2])"}
 
 
-def bench_segmented_i32(hx, dev, args):
+def wl_segmented_i32(hx, dev):
+    """cfg 4: i32 segmented sum, n = 2^27, geometric(300) lengths."""
     from oracle import oracle  # geometric offsets are generated on the host
 
     n = 1 << 27
@@ -126,11 +286,93 @@ def bench_segmented_i32(hx, dev, args):
     ob = dev.upload(off)
     out = dev.alloc_uninitialized(np.int32, off.size - 1)
     plan = hx.RocmSegmentedReductionOps().prepare_segmented_sum(dev, x, ob, out)
-    ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
-    s = off.size - 1
-    return {"n": n, "ms": ms, "bytes": 4 * n + 4 * (s + 1) + 4 * s}
+    segs = off.size - 1
+
+    def verify():
+        ok = np.array_equal(dev.download_owned(out), oracle.segmented_sum(dev.download_owned(x), off))
+        return {"ok": bool(ok), "check": "bit-exact", "segments": int(segs)}
+
+    def cpu(seconds):
+        m = 1 << 25
+        h = oracle.uniform_int(m, 4, -1000, 1000, dtype=np.int32)
+        o = oracle.geometric_offsets(m, 300.0, seed=5)
+        return _cpu_line(*_cpu_rate(lambda: oracle.segmented_sum(h, o), 4.0 * m + 8.0 * (o.size - 1) + 4, seconds),
+                         f"2^25 i32 values, {o.size - 1} geometric(300) segments, oracle segmented_sum")
+
+    return {"n": n, "bytes": 4 * n + 4 * (segs + 1) + 4 * segs, "run": plan.dispatch, "cpu": cpu, "verify": verify,
+            "keep": (x, ob, out, plan), "dtype": "i32",
+            "workload": f"i32 segmented sum, n=2^27, {segs} geometric(300) segments (BASELINE configs[3])"}
 
 
+def wl_scan_f32_2_30(hx, dev):
+    """cfg 5: f32 inclusive scan, n = 2^30, uniform[0, 1)."""
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 30
+    x = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(x, seed=6, lo=0.0, hi=1.0)
+    out = dev.alloc_uninitialized(np.float32, n)
+    lay = Layout.c_contiguous([n])
+    plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                                              StridedView(out, lay))
+    head = 1 << 24
+
+    def verify():
+        # A prefix of a scan depends on nothing after it: the first 2^24
+        # outputs are checked in full (the tests check all 2^30).
+        from oracle import oracle
+
+        hx_ = hx.RocmBuffer(dev, x.ptr, head, np.float32)
+        ho = hx.RocmBuffer(dev, out.ptr, head, np.float32)
+        try:
+            xi, go = dev.download_owned(hx_), dev.download_owned(ho)
+        finally:
+            hx_.ptr = ho.ptr = None  # views of x and out
+        bad, worst = oracle.check_scan_f32(xi, go, n_for_log=n)
+        return {"ok": bad == 0, "check": f"first 2^24 outputs within 2*ceil(log2 2^30)*eps*sum|x|",
+                "worst_err_over_eps_abs": worst}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        m = 1 << 23
+        h = oracle.uniform_real(m, 6, 0.0, 1.0)
+        return _cpu_line(*_cpu_rate(lambda: oracle.scan_sum(h), 8.0 * m, seconds),
+                         "2^23 f32 (1/128 of the GPU input), oracle scan_sum (compensated f64 prefix and |prefix|)")
+
+    return {"n": n, "bytes": 8 * n, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (x, out, plan),
+            "dtype": "f32", "workload": "f32 inclusive prefix scan, n=2^30 (BASELINE configs[4])"}
+
+
+def ceiling(hx, dev, steps: int, warmup: int) -> dict:
+    """The best read+write streams on this device: the library's copy
+    kernel (nt loads, nt|sc1 stores, 256 KiB tiles) and the runtime's
+    hipMemcpyAsync device-to-device, each 1 GiB in and 1 GiB out."""
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.uint32, n)
+    dev.fill_uniform_int(x, seed=7, lo=0, hi=255)
+    y = dev.alloc_uninitialized(np.uint32, n)
+    out = {}
+    t = time_launches(dev, lambda: dev.copy_buffer_async(x, y), steps, warmup)
+    out["copy_kernel"] = {"GB/s": round(gbs(8.0 * n, t["mean_ms"]), 1), **{k: round(v, 5) for k, v in t.items()}}
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+
+    def blit():
+        err = hip.hipMemcpyAsync(y.ptr, x.ptr, 4 * n, 3, dev.stream)  # hipMemcpyDeviceToDevice
+        if err != 0:
+            raise RuntimeError(f"hipMemcpyAsync failed: {err}")
+
+    t = time_launches(dev, blit, steps, warmup)
+    out["runtime_blit_hipMemcpyAsync"] = {"GB/s": round(gbs(8.0 * n, t["mean_ms"]), 1),
+                                          **{k: round(v, 5) for k, v in t.items()}}
+    out["bytes_per_launch"] = 8 * n
+    x.free()
+    y.free()
+    return out
+
+
+# ----------------------------------------------- extra workloads (--workload)
 def bench_segmented_short_i32(hx, dev, args):
     """Short segments (geometric, mean 4): the segment-parallel path."""
     from oracle import oracle
@@ -145,20 +387,6 @@ def bench_segmented_short_i32(hx, dev, args):
     ms = time_plan(dev, plan.dispatch, args.steps, args.warmup)
     s = off.size - 1
     return {"n": n, "ms": ms, "bytes": 4 * n + 4 * (s + 1) + 4 * s}
-
-
-def bench_scan_f32_2_30(hx, dev, args):
-    from hephaestus_amd import Layout, StridedView
-
-    n = 1 << 30
-    x = dev.alloc_uninitialized(np.float32, n)
-    dev.fill_uniform_real(x, seed=6, lo=0.0, hi=1.0)
-    out = dev.alloc_uninitialized(np.float32, n)
-    lay = Layout.c_contiguous([n])
-    plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
-                                              StridedView(out, lay))
-    ms = time_plan(dev, plan.dispatch, max(1, args.steps // 4), max(1, args.warmup // 2))
-    return {"n": n, "ms": ms, "bytes": 8 * n}
 
 
 def bench_dot_f32(hx, dev, args):
@@ -219,13 +447,14 @@ def bench_colscan_u32(hx, dev, args):
 
 
 def bench_copy_u32(hx, dev, args):
-    """The device copy kernel behind copy_buffer over 2^28 u32: the yardstick
-    (read B + write B) for the HBM byte counters, and the streaming ceiling."""
+    """The copy kernel behind copy_buffer over 2^28 u32, queued back to back
+    (hx_copy_async): the yardstick (read B + write B) for the HBM byte
+    counters, and the read+write stream ceiling."""
     n = 1 << 28
     x = dev.alloc_uninitialized(np.uint32, n)
     dev.fill_uniform_int(x, seed=7, lo=0, hi=255)
     y = dev.alloc_uninitialized(np.uint32, n)
-    ms = time_plan(dev, lambda: dev.copy_buffer(x, y), args.steps, args.warmup)
+    ms = time_plan(dev, lambda: dev.copy_buffer_async(x, y), args.steps, args.warmup)
     return {"n": n, "ms": ms, "bytes": 8 * n}
 
 
@@ -310,39 +539,80 @@ def pmc_summary(root: Path) -> int:
     return 0
 
 
-def cpu_baseline(dev, scan, seconds: float) -> dict:
-    """Time the oracle's sequential exclusive scan on this host's cores over
-    the same 2^28-element input; verify the GPU output against it."""
-    from oracle import oracle
+# Kernels of each default configuration, as (name substring, launch grid
+# in threads) pairs of the kernel trace; one step runs each once.
+TRACE_CONFIGS = [
+    ("scan_u32", "u32 exclusive scan 2^28 (headline)", [("scan_tiles_kernel<unsigned int", 8192 * 512)], 8 << 28),
+    ("sum_f32", "f32 sum 2^28", [("full_reduce_kernel<float", 768 * 256), ("full_reduce_final_kernel<float", 256)],
+     (4 << 28) + 4),
+    ("sum_f32_2_20", "f32 sum 2^20 (cfg1)", [("full_reduce_kernel<float", 512 * 256),
+                                            ("full_reduce_final_kernel<float", 256)], (4 << 20) + 4),
+    ("rows_f32", "rows 65536 x 4096 (cfg3)", [("rows_kernel<float", 65536 * 256)], (4 << 28) + 12 * 65536),
+    ("segmented_i32", "segmented 2^27 (cfg4)", [("seg_tile_map_kernel", None), ("segmented_sum_kernel", None)], None),
+    ("scan_f32_2_30", "f32 inclusive scan 2^30 (cfg5)", [("scan_tiles_kernel<float", 32768 * 512)], 8 << 30),
+    ("copy_u32", "copy 1 GiB (ceiling yardstick)", [("copy_tiles_kernel", 4096 * 512)], 8 << 28),
+    ("blit", "hipMemcpyAsync 1 GiB (ceiling)", [("__amd_rocclr_copyBuffer", 131072)], 8 << 28),
+]
 
-    x = dev.download_owned(scan["x"])
-    got = dev.download_owned(scan["out"])
-    n = x.size
-    out = np.empty_like(x)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.lib().hxo_scan_sum_u32(x.ctypes.data, n, 1, 0, out.ctypes.data)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 50:
-            break
-    per = el / reps
-    verified = bool(np.array_equal(got, out))
-    threads = min(16, os.cpu_count() or 1)
-    t1 = time.perf_counter()
-    oracle.scan_excl_u32_threads(x, out, threads)
-    tt = time.perf_counter() - t1
-    return {
-        "value": round(8 * n / per / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"the full 2^28-element u32 exclusive scan, {reps} sequential passes of the C oracle "
-                  f"(oracle/hx_oracle.c hxo_scan_sum_u32), {per * 1e3:.1f} ms per pass",
-        "multithread": {"value": round(8 * n / tt / 1e9, 3), "cores": threads,
-                        "sample": "one pass of the two-pass pthread scan hxo_scan_excl_u32_threads"},
-        "gpu_output_verified": verified,
-    }
+
+def trace_summary(root: Path, bench_json: Path | None) -> int:
+    """Markdown summary of a `rocprofv3 --kernel-trace --stats` run of the
+    default bench: per kernel and launch grid, calls and the mean, median,
+    minimum and maximum duration, then per configuration the step time (its
+    kernels' means added) beside the bench's own event-timed mean."""
+    import csv
+
+    files = sorted(root.rglob("*kernel_trace.csv"))
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {root}")
+    groups: dict = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    bench = json.loads(bench_json.read_text()) if bench_json else None
+    sec = (bench or {}).get("secondary", {})
+    bench_ms = {"scan_u32": (bench or {}).get("ms_per_step"),
+                "sum_f32": sec.get("f32_sum_reduce_2_28", {}).get("ms_per_launch"),
+                "sum_f32_2_20": sec.get("cfg1_f32_sum_2_20", {}).get("ms_per_launch"),
+                "rows_f32": sec.get("cfg3_rows_f32_65536x4096", {}).get("ms_per_launch"),
+                "segmented_i32": sec.get("cfg4_segmented_i32_2_27", {}).get("ms_per_launch"),
+                "scan_f32_2_30": sec.get("cfg5_scan_f32_2_30", {}).get("ms_per_launch"),
+                "copy_u32": (bench or {}).get("ceiling", {}).get("copy_kernel", {}).get("mean_ms"),
+                "blit": (bench or {}).get("ceiling", {}).get("runtime_blit_hipMemcpyAsync", {}).get("mean_ms")}
+    seg_bytes = (sec.get("cfg4_segmented_i32_2_27") or {}).get("algorithmic_bytes_per_launch")
+    lines = ["| kernel | grid (threads) | calls | mean us | median us | min us | max us |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        short = name.replace("hx::(anonymous namespace)::", "").replace("hx::", "").replace("|", "\\|")
+        short = short if len(short) <= 110 else short[:110] + "..."
+        lines.append(f"| `{short}` | {grid} | {len(d)} | {statistics.mean(d):.1f} | {statistics.median(d):.1f} | "
+                     f"{min(d):.1f} | {max(d):.1f} |")
+    lines += ["", "| configuration | kernels per step | trace: step us (means added) | trace: step us (medians added) "
+                  "| bench: event-timed us per step | trace frac | bench frac |",
+              "|---|---|---:|---:|---:|---:|---:|"]
+    for key, label, kernels, nbytes in TRACE_CONFIGS:
+        nbytes = seg_bytes if key == "segmented_i32" else nbytes
+        mean_sum = med_sum = 0.0
+        found = True
+        for sub, grid in kernels:
+            ds = [d for (name, g), d in groups.items() if sub in name and (grid is None or g == grid)]
+            if not ds:
+                found = False
+                break
+            d = [x for lst in ds for x in lst]
+            mean_sum += statistics.mean(d)
+            med_sum += statistics.median(d)
+        if not found:
+            continue
+        b = bench_ms.get(key)
+        tf = f"{nbytes / (mean_sum * 1e-6) / 8e12:.4f}" if nbytes else "-"
+        bf = f"{nbytes / (b * 1e-3) / 8e12:.4f}" if (nbytes and b) else "-"
+        lines.append(f"| {label} | {len(kernels)} | {mean_sum:.1f} | {med_sum:.1f} | "
+                     f"{b * 1e3 if b else float('nan'):.1f} | {tf} | {bf} |")
+    print("\n".join(lines))
+    return 0
 
 
 def _raw(fn_name: str, *args):
@@ -430,72 +700,6 @@ def latency_suite(hx, dev, args) -> dict:
     return out
 
 
-def _cpu_rate(run, bytes_per_pass: float, seconds: float = 2.0, max_reps: int = 20):
-    """(GB/s, passes, ms per pass) of `run()` repeated for about `seconds`."""
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        run()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= max_reps:
-            break
-    per = el / reps
-    return bytes_per_pass / per / 1e9, reps, per * 1e3
-
-
-def cpu_secondary(name: str, seconds: float) -> dict | None:
-    """The oracle (one host core, kind "port") on a bounded host-generated
-    sample of a secondary workload; rates are per algorithmic byte like the
-    GPU figure.  None for workloads the oracle has no function for."""
-    from oracle import oracle
-
-    def line(gbs, reps, ms, sample):
-        return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"{sample}; {reps} passes, {ms:.1f} ms per pass"}
-
-    if name == "sum_f32":
-        n = 1 << 26
-        x = oracle.uniform_real(n, 1, -1.0, 1.0)
-        r = _cpu_rate(lambda: oracle.full_sum(x), 4.0 * n, seconds)
-        return line(*r, "2^26 f32 (a quarter of the GPU input), oracle full_sum (f64 accumulation)")
-    if name == "rows_f32":
-        rows, cols = 4096, 4096
-        x = oracle.normal(rows * cols, 3)
-        r = _cpu_rate(lambda: oracle.rows(x, rows, cols, prologue=(0.5, 0.25)), 4.0 * rows * cols + 12.0 * rows,
-                      seconds)
-        return line(*r, "4096 x 4096 f32 (1/16 of the GPU rows), oracle rows (sum, max, argmax of fmaf(.5,x,.25))")
-    if name == "segmented_i32":
-        n = 1 << 25
-        x = oracle.uniform_int(n, 4, -1000, 1000, dtype=np.int32)
-        off = oracle.geometric_offsets(n, 300.0, seed=5)
-        s = off.size - 1
-        r = _cpu_rate(lambda: oracle.segmented_sum(x, off), 4.0 * n + 8.0 * s + 4, seconds)
-        return line(*r, f"2^25 i32 values, {s} geometric(300) segments, oracle segmented_sum")
-    if name == "segmented_short_i32":
-        n = 1 << 25
-        x = oracle.uniform_int(n, 4, -1000, 1000, dtype=np.int32)
-        off = oracle.geometric_offsets(n, 4.0, seed=5)
-        s = off.size - 1
-        r = _cpu_rate(lambda: oracle.segmented_sum(x, off), 4.0 * n + 8.0 * s + 4, seconds)
-        return line(*r, f"2^25 i32 values, {s} geometric(4) segments, oracle segmented_sum")
-    if name == "scan_f32_2_30":
-        n = 1 << 23
-        x = oracle.uniform_real(n, 6, 0.0, 1.0)
-        r = _cpu_rate(lambda: oracle.scan_sum(x), 8.0 * n, seconds)
-        return line(*r, "2^23 f32 (1/128 of the GPU input), oracle scan_sum (compensated f64 prefix and |prefix|)")
-    if name == "dot_f32":
-        n = 1 << 26
-        a, b = oracle.uniform_real(n, 1, -1.0, 1.0), oracle.uniform_real(n, 2, -1.0, 1.0)
-        r = _cpu_rate(lambda: oracle.dot(a, b), 8.0 * n, seconds)
-        return line(*r, "2^26 f32 pairs, oracle dot (exact products, f64 accumulation)")
-    if name == "axpy_f32":
-        n = 1 << 24
-        a, b = oracle.uniform_real(n, 1, -1.0, 1.0), oracle.uniform_real(n, 2, -1.0, 1.0)
-        r = _cpu_rate(lambda: oracle.fma_arrays(a, b, 0.5), 12.0 * n, seconds)
-        return line(*r, "2^24 f32, oracle fma_arrays (libm fmaf per element)")
-    return None
-
-
 def device_record(dev) -> dict:
     """CU count and architecture from the library; current and peak clocks
     from amd-smi when the tool answers within a few seconds."""
@@ -526,18 +730,43 @@ def device_record(dev) -> dict:
     return rec
 
 
+def run_config(name, hx, dev, args, cpu_seconds):
+    """Time one configuration; returns (record, workload dict)."""
+    w = globals()[f"wl_{name}"](hx, dev)
+    steps = args.steps if name != "scan_f32_2_30" else max(5, args.steps // 4)
+    t = time_launches(dev, w["run"], steps, args.warmup)
+    rec = {"value": round(gbs(w["bytes"], t["mean_ms"]), 1), "unit": "GB/s", "dtype": w["dtype"],
+           "workload": w["workload"], "n": w["n"], "algorithmic_bytes_per_launch": w["bytes"], "steps": steps,
+           "ms_per_launch": round(t["mean_ms"], 5), "median_ms": round(t["median_ms"], 5),
+           "min_ms": round(t["min_ms"], 5), "elements_per_s": round(w["n"] / (t["mean_ms"] * 1e-3), 1),
+           "roofline": roofline(w["bytes"], t["mean_ms"], name)}
+    if w["verify"] is not None:
+        rec["gpu_output_check"] = w["verify"]()
+    if cpu_seconds > 0:
+        rec["cpu_baseline"] = w["cpu"](cpu_seconds)
+    log(f"{name}: {t['mean_ms']:.4f} ms/launch (median {t['median_ms']:.4f}, min {t['min_ms']:.4f}) "
+        f"{rec['value']:.1f} GB/s")
+    return rec, w
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=("default", "all") + WORKLOADS, default="default")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="CPU time for the headline's baseline (each other configuration gets a third)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 --pmc runs under DIR and exit")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="summarise a rocprofv3 --kernel-trace run of the default bench under DIR and exit")
+    ap.add_argument("--bench-json", metavar="FILE", help="with --trace-summary: that run's bench JSON line")
     args = ap.parse_args()
     if args.pmc_summary:
         return pmc_summary(Path(args.pmc_summary))
+    if args.trace_summary:
+        return trace_summary(Path(args.trace_summary), Path(args.bench_json) if args.bench_json else None)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -549,70 +778,73 @@ def main() -> int:
 
     dev = hx.RocmDevice.try_default()
     topo = dev.topology()
-    log(f"device {topo.name} {topo.arch} CUs={topo.compute_units} lib={hx.native_library_path()}")
+    log(f"device {topo.name} {topo.arch} CUs={topo.compute_units} lib={hx.native_library_path()} "
+        f"host cores={os.cpu_count()}")
 
     if args.workload not in ("default", "all"):
-        fn = globals()[f"bench_{args.workload}"]
-        r = fn(hx, dev, args)
-        gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
-        print(json.dumps({"workload": args.workload, "n": r["n"], "ms": round(r["ms"], 5),
-                          "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
-                          "elements_per_s": round(r["n"] / (r["ms"] * 1e-3), 1)}))
+        if args.workload in ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30"):
+            w = globals()[f"wl_{args.workload}"](hx, dev)
+            ms = time_plan(dev, w["run"], args.steps, args.warmup)
+            n, nbytes = w["n"], w["bytes"]
+        else:
+            r = globals()[f"bench_{args.workload}"](hx, dev, args)
+            ms, n, nbytes = r["ms"], r["n"], r["bytes"]
+        g = gbs(nbytes, ms)
+        print(json.dumps({"workload": args.workload, "n": n, "ms": round(ms, 5), "GB/s": round(g, 1),
+                          "frac": round(g / PEAK_GBS, 4), "elements_per_s": round(n / (ms * 1e-3), 1)}))
         return 0
 
-    scan = bench_scan_u32(hx, dev, args)
-    log(f"scan u32 2^28: {scan['ms']:.4f} ms/launch")
-    ssum = bench_sum_f32(hx, dev, args)
-    log(f"sum f32 2^28: {ssum['ms']:.4f} ms/launch")
+    cpu_head = 0.0 if args.no_cpu_baseline else args.cpu_seconds
+    cpu_other = cpu_head / 3.0
+    head, w = run_config("scan_u32", hx, dev, args, cpu_head)
+    del w
+    secondary = {}
+    for key, name in (("f32_sum_reduce_2_28", "sum_f32"), ("cfg1_f32_sum_2_20", "sum_f32_2_20"),
+                      ("cfg3_rows_f32_65536x4096", "rows_f32"), ("cfg4_segmented_i32_2_27", "segmented_i32"),
+                      ("cfg5_scan_f32_2_30", "scan_f32_2_30")):
+        secondary[key], w = run_config(name, hx, dev, args, cpu_other)
+        del w
+    ceil = ceiling(hx, dev, args.steps, args.warmup)
+    best = max(ceil["copy_kernel"]["GB/s"], ceil["runtime_blit_hipMemcpyAsync"]["GB/s"])
+    ceil["best_GB/s"] = best
+    ceil["headline_scan_over_best"] = round(head["value"] / best, 4)
+    log(f"ceiling: copy kernel {ceil['copy_kernel']['GB/s']} GB/s, runtime blit "
+        f"{ceil['runtime_blit_hipMemcpyAsync']['GB/s']} GB/s; scan at {ceil['headline_scan_over_best']:.3f} of best")
 
-    value = scan["bytes"] / (scan["ms"] * 1e-3) / 1e9
     line = {
         "metric": "achieved HBM GB/s (% of peak) for f32 sum-reduce and u32 scan at 2^28 elems",
-        "value": round(value, 1),
+        "value": head["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(scan["ms"], 5),
+        "ms_per_step": head["ms_per_launch"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u32",
-        "data": "synthetic (SplitMix64 seed 2, uniform integers in [0,256), generated in HBM)",
-        "config": {"workload": "u32 exclusive prefix scan, n=2^28 (the headline configuration)",
-                   "n": scan["n"], "algorithmic_bytes_per_step": scan["bytes"],
-                   "elements_per_s": round(scan["n"] / (scan["ms"] * 1e-3), 1)},
-        "roofline": roofline(scan["bytes"], scan["ms"], "scan_u32"),
-        "secondary": {
-            "f32_sum_reduce_2_28": {
-                "value": round(ssum["bytes"] / (ssum["ms"] * 1e-3) / 1e9, 1), "unit": "GB/s",
-                "ms_per_launch": round(ssum["ms"], 5),
-                "elements_per_s": round(ssum["n"] / (ssum["ms"] * 1e-3), 1),
-                "roofline": roofline(ssum["bytes"], ssum["ms"], "sum_f32"),
-            }
-        },
+        "data": "synthetic (SplitMix64 seeds, generated in HBM; the BASELINE.json distributions)",
+        "config": {"workload": head["workload"], "n": head["n"],
+                   "algorithmic_bytes_per_step": head["algorithmic_bytes_per_launch"],
+                   "elements_per_s": head["elements_per_s"]},
+        "timing": {"mean_ms": head["ms_per_launch"], "median_ms": head["median_ms"], "min_ms": head["min_ms"]},
+        "roofline": head["roofline"],
     }
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+    line["secondary"] = secondary
+    line["ceiling"] = ceil
     if args.workload == "all":
-        for name in ("rows_f32", "segmented_i32", "segmented_short_i32", "scan_f32_2_30", "copy_u32", "dot_f32",
-                     "axpy_f32", "colsum_f32", "colscan_u32"):
+        extra = {}
+        for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
-            gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
-            line["secondary"][name] = {"value": round(gbs, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
-                                       "elements_per_s": round(r["n"] / (r["ms"] * 1e-3), 1),
-                                       "roofline": roofline(r["bytes"], r["ms"], name)}
-            if not args.no_cpu_baseline:
-                cb = cpu_secondary(name, 2.0)
-                if cb is not None:
-                    line["secondary"][name]["cpu_baseline"] = cb
-            log(f"{name}: {r['ms']:.4f} ms/launch {gbs:.1f} GB/s")
-    if args.workload == "all":
+            g = gbs(r["bytes"], r["ms"])
+            extra[name] = {"value": round(g, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
+                           "roofline": roofline(r["bytes"], r["ms"], name)}
+            log(f"{name}: {r['ms']:.4f} ms/launch {g:.1f} GB/s")
+        line["extra"] = extra
         line["latency"] = latency_suite(hx, dev, args)
-        for name, r in line["latency"].items():
-            log(f"{name}: {r['us_per_call']} us per call, {r['gpu_us_per_launch']} us per launch "
-                f"(reference WGPU RTX 5080: {r['reference_wgpu_rtx5080_us']} us)")
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(dev, scan, args.cpu_seconds)
-        line["secondary"]["f32_sum_reduce_2_28"]["cpu_baseline"] = cpu_secondary("sum_f32", 2.0)
+    line["host"] = {"cpu_count": os.cpu_count()}
     line["device"] = device_record(dev)
     print(json.dumps(line))
     return 0

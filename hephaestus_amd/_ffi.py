@@ -114,6 +114,7 @@ SIGNATURES = {
     "hx_write_sub": (I32, [P, P, U64, U64, P, U64, U32]),
     "hx_download": (I32, [P, P, U64, P, U64, U32]),
     "hx_copy": (I32, [P, P, U64, P, U64, U32]),
+    "hx_copy_async": (I32, [P, P, U64, P, U64, U32, P]),
     "hx_event_create": (I32, [P, POINTER(P)]),
     "hx_event_destroy": (I32, [P]),
     "hx_event_record": (I32, [P, P, P]),

@@ -539,6 +539,19 @@ hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len, void *dst,
     return ok();
 }
 
+hx_status hx_copy_async(hx_device *dev, const void *src, uint64_t src_len, void *dst, uint64_t dst_len,
+                        uint32_t elem_size, hx_stream stream) {
+    HX_TRY(check_elem(elem_size));
+    if (src == dst && src_len == dst_len) return ok();
+    if (dst_len != src_len) return length_mismatch(dst_len, src_len);
+    uint64_t bytes = 0;
+    HX_TRY(byte_count(src_len, elem_size, &bytes));
+    HX_TRY(bind_device(dev));
+    if (bytes == 0) return ok();
+    HX_TRY(launch_copy(src, dst, bytes, pick_stream(dev, stream)));
+    return ok();
+}
+
 hx_status hx_event_create(hx_device *dev, hx_event *out) {
     if (!out) return fail(HX_ERR_INVALID_CONFIGURATION, "null event out-pointer");
     HX_TRY(bind_device(dev));

@@ -202,6 +202,14 @@ class RocmDevice:
             _ffi.lib().hx_copy(self.handle, src.ptr, len(src), dst.ptr, len(dst), src.itemsize)
         )
 
+    def copy_buffer_async(self, src: RocmBuffer, dst: RocmBuffer, stream=None) -> None:
+        """copy_buffer queued on `stream` without waiting (hx_copy_async)."""
+        if src.dtype != dst.dtype:
+            raise errors.InvalidConfiguration("copy_buffer between different element types")
+        _ffi.check(
+            _ffi.lib().hx_copy_async(self.handle, src.ptr, len(src), dst.ptr, len(dst), src.itemsize, stream)
+        )
+
     # -- synthetic inputs (RandomInitOps analog) -----------------------
     def fill_uniform_int(self, buffer: RocmBuffer, seed: int, lo: int, hi: int, stream=None) -> None:
         _ffi.check(

@@ -189,6 +189,14 @@ hx_status hx_download(hx_device *dev, const void *src, uint64_t src_len,
 hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len,
                   void *dst, uint64_t dst_len, uint32_t elem_size);
 
+/* Stream-ordered form of hx_copy (no reference counterpart; copy_buffer is
+ * synchronous): the same streaming copy kernel queued on `stream`, returning
+ * without waiting.  It is also the read+write bandwidth yardstick that the
+ * bench times back to back. */
+hx_status hx_copy_async(hx_device *dev, const void *src, uint64_t src_len,
+                        void *dst, uint64_t dst_len, uint32_t elem_size,
+                        hx_stream stream);
+
 /* ------------------------------------------------------------- timing */
 
 hx_status hx_event_create(hx_device *dev, hx_event *out);

@@ -938,6 +938,9 @@ def test_copy_buffer_bit_exact(device, oracle, n):
     dst = device.alloc_zeroed(np.uint32, n)
     device.copy_buffer(src, dst)
     assert np.array_equal(device.download_owned(dst), x)
+    again = device.alloc_zeroed(np.uint32, n)
+    device.copy_buffer_async(dst, again)  # stream-ordered before the download
+    assert np.array_equal(device.download_owned(again), x)
 
 
 @pytest.mark.parametrize("skew,nbytes", [(1, 1), (1, 17), (3, 4099), (4, 262144 + 20), (8, 3 * 262144), (0, 262144 + 15)])
