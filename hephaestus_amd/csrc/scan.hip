@@ -1362,7 +1362,10 @@ struct TileShape {
     int waves, steps;
     uint64_t elems() const { return (uint64_t)waves * kWave * 4 * steps; }
 };
-inline TileShape tile_shape(uint64_t len) {
+// Lines longer than one 8 x 16 tile: the tiles chained by the look-back.
+constexpr int kLongWaves = 8, kLongSteps = 16;   // integer
+constexpr int kF32Waves = 12, kF32Steps = 16;    // f32
+inline TileShape tile_shape(uint64_t len, bool f32) {
     if (len <= 256) return {1, 1};
     if (len <= 512) return {1, 2};
     if (len <= 1024) return {2, 2};
@@ -1370,7 +1373,8 @@ inline TileShape tile_shape(uint64_t len) {
     if (len <= 4096) return {4, 4};
     if (len <= 8192) return {4, 8};
     if (len <= 16384) return {4, 16};
-    return {kWaves, kSteps};
+    if (len <= 32768) return {kWaves, kSteps};
+    return f32 ? TileShape{kF32Waves, kF32Steps} : TileShape{kLongWaves, kLongSteps};
 }
 
 template <typename T, typename Op, typename Status, bool EXCL, int STEPS, int WAVES>
@@ -1403,8 +1407,16 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     case 404: return launch_tiles_shaped<T, Op, Status, EXCL, 4, 4>(p, st, st1, vec, rev, stream);
     case 408: return launch_tiles_shaped<T, Op, Status, EXCL, 8, 4>(p, st, st1, vec, rev, stream);
     case 416: return launch_tiles_shaped<T, Op, Status, EXCL, 16, 4>(p, st, st1, vec, rev, stream);
-    default: return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
+    default: break;
     }
+    if constexpr (std::is_same<T, float>::value) {
+        if (shape.waves == kF32Waves && shape.steps == kF32Steps)
+            return launch_tiles_shaped<T, Op, Status, EXCL, kF32Steps, kF32Waves>(p, st, st1, vec, rev, stream);
+    } else {
+        if (shape.waves == kLongWaves && shape.steps == kLongSteps)
+            return launch_tiles_shaped<T, Op, Status, EXCL, kLongSteps, kLongWaves>(p, st, st1, vec, rev, stream);
+    }
+    return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
 }
 
 // Narrow column scans (col_narrow_*): chunks of whole 256-vector trips,
@@ -1481,7 +1493,7 @@ uint64_t scan_bytes(const ScanArgs &a) {
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
     }
     if (column_mode(a)) return column_bytes(a);
-    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len).elems());
+    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len, a.dtype == HX_DTYPE_F32).elems());
     const bool f64 = a.dtype == HX_DTYPE_F32;
     return kLookbackOffset + status_bytes(tpl * a.lines, f64) + status_bytes(ceil_div(tpl, kSuper) * a.lines, f64);
 }
@@ -1493,7 +1505,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out = a.out;
     p.lines = a.lines;
     p.len = a.len;
-    const TileShape shape = tile_shape(a.len);
+    const TileShape shape = tile_shape(a.len, std::is_same<T, float>::value);
     p.tiles_per_line = ceil_div(a.len, shape.elems());
     p.total_tiles = p.tiles_per_line * a.lines;
     p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);

@@ -409,6 +409,45 @@ def test_scan_f32_tile_and_superblock_edges(device, oracle, n):
     assert bad == 0, worst
 
 
+# f32 lines longer than 32768 elements take 12-wave x 16-step tiles of
+# 49152 elements: lengths either side of one, two and 64 tiles (a
+# superblock), and the mirrored reverse path.
+F32_LONG = [32769, 49151, 49152, 49153, 2 * 49152 - 1, 2 * 49152 + 4, 64 * 49152, 64 * 49152 + 49152 + 12,
+            65 * 49152 + 3]
+
+
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+@pytest.mark.parametrize("n", F32_LONG)
+def test_scan_f32_long_tile_edges(device, oracle, n, direction, kind):
+    rev = direction == hx.ScanDirection.Reverse
+    excl = kind == hx.ScanKind.Exclusive
+    x = oracle.uniform_real(n, seed=n + 21, lo=-1.0, hi=1.0)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.float32, n)
+    lay = Layout.c_contiguous([n])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 0, direction, StridedView(out, lay), kind)
+    ref, ab = oracle.scan_sum(x, exclusive=excl, reverse=rev)
+    bad, worst = oracle.check_f32_bound(device.download_owned(out), ref, ab, n)
+    assert bad == 0, worst
+
+
+@pytest.mark.parametrize("shape", [(3, 49153), (2, 64 * 49152 + 5)])
+def test_scan_f32_long_rank2_lines(device, oracle, shape):
+    """Several long f32 lines in one launch: tiles and superblocks per line."""
+    r, c = shape
+    x = oracle.uniform_real(r * c, seed=r + c, lo=0.0, hi=1.0)
+    buf = device.upload(x)
+    out = device.alloc_zeroed(np.float32, r * c)
+    lay = Layout.c_contiguous([r, c])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 1, hx.ScanDirection.Forward,
+                        StridedView(out, lay))
+    got = device.download_owned(out).reshape(r, c)
+    for i in range(r):
+        ref, ab = oracle.scan_sum(x[i * c:(i + 1) * c])
+        assert oracle.check_f32_bound(got[i], ref, ab, c)[0] == 0, i
+
+
 @pytest.mark.parametrize("exclusive", [False, True])
 @pytest.mark.parametrize("n", [1, 2, 5, 4096, 4097, 65536 + 17, (1 << 20) + 3])
 def test_scan_f32_within_bound(device, oracle, n, exclusive):
