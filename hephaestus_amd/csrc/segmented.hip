@@ -185,9 +185,12 @@ template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_
 // written first, and wave 0 looks back last, when the rest of the block is
 // done (polling earlier, between two barriers, held every wave of the block
 // and cost ~15% at 2^27 values).
-// Register budget: 72 VGPRs gives 7 waves per SIMD, seven 4-wave blocks per
-// CU (the compiler's own choice, 74, allows six: 92 us at 2^27 against 89.5;
-// a 64 cap spills to scratch and takes 156 us).
+// Register budget: 72 VGPRs gives 7 waves per SIMD.  For the 4 x 8 tiles
+// (one wave per SIMD per block) that is seven blocks per CU (the compiler's
+// own choice, 74, allows six: 92 us at 2^27 against 89.5; a 64 cap spills to
+// scratch and takes 156 us).  The 8 x 8 long-segment tiles take two waves
+// per SIMD per block, so the same budget fits three of them per CU (six
+// waves per SIMD).
 template <int WAVES, int STEPS>
 __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7, 7))) void segmented_sum_kernel(
     SegParams p) {
@@ -732,8 +735,9 @@ __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p)
     const uint32_t edge = (lane < J && edge_k <= s1) ? p.offsets[edge_k] : 0u;
     const ChunkCarry cc = short_chunk_prefix(p.values, base, a0, c1, s_p);
     // Segment j's bounds, clamped into the span (only malformed offsets are
-    // changed); recomputed where needed rather than held, which keeps J = 16
-    // within five waves per SIMD.
+    // changed); recomputed where needed rather than held, which took J = 16
+    // from 115 to 102 VGPRs (J = 15 and 16 run four waves per SIMD; J <= 14,
+    // at 94, five).
     auto bounds = [&](int j, uint64_t &st, uint64_t &en) {
         const uint32_t next = __shfl_down(lo[j], 1);
         const uint32_t e = lane == kWave - 1 ? read_lane(edge, j) : next;

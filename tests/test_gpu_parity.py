@@ -773,6 +773,43 @@ def test_segmented_sum_long_segment_tiles(device, oracle):
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
+def _crowded_long(n, seed):
+    """Geometric(20000) segments plus: 5000 empty segments mid-tile, 4097 at
+    a 16384-value tile edge, and 3000 segments of 1..4 values packed into one
+    tile -- crowded tiles (more than 2048 and more than 4096 ends) on the
+    16384-value tile route."""
+    rng = np.random.default_rng(seed)
+    t = 16384
+    cuts = list(np.flatnonzero(rng.random(n - 1) < 1.0 / 20000.0) + 1)
+    cuts += [37 * t + 5000] * 5000
+    cuts += [90 * t] * 4097
+    cuts += list(150 * t + 11 + np.cumsum(rng.integers(1, 5, 3000)))
+    cuts = np.sort(np.array([c for c in cuts if 0 <= c <= n], np.int64))
+    return np.concatenate([[0], cuts, [n]]).astype(np.uint32)
+
+
+def test_segmented_crowded_long_segment_tiles(device, oracle):
+    """Crowded tiles on the long-segment route (mean n/S >= 4096 selects
+    16384-value tiles): several mask rounds, and ends beyond the tile's
+    first 4096 summed by the map kernel; immediate and prepared forms."""
+    n = 1 << 26
+    x = oracle.uniform_int(n, seed=45, lo=-1 << 30, hi=1 << 30, dtype=np.int32)
+    off = _crowded_long(n, seed=45)
+    s = off.size - 1
+    assert n >= 4096 * s, "case must take the long-segment tiles"
+    t = 16384
+    ends_per_tile = np.bincount(np.minimum((off[1:].astype(np.int64) - 1) // t, n // t - 1), minlength=n // t)
+    assert ends_per_tile.max() > 4096 and ((ends_per_tile > 2048) & (ends_per_tile <= 4096)).any()
+    want = oracle.segmented_sum(x, off)
+    assert np.array_equal(_segmented(device, x, off), want)
+    vb, ob = device.upload(x), device.upload(off)
+    out = device.alloc_zeroed(np.int32, s)
+    plan = SEG.prepare_segmented_sum(device, vb, ob, out)
+    for _ in range(2):
+        plan.dispatch()
+    assert np.array_equal(device.download_owned(out), want)
+
+
 @pytest.mark.parametrize("cuts_n", [300, 12000])
 @pytest.mark.parametrize("skew", [1, 2, 3])
 def test_segmented_sum_values_off_16_byte_boundaries(device, oracle, skew, cuts_n):
