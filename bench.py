@@ -549,7 +549,7 @@ TRACE_CONFIGS = [
                                             ("full_reduce_final_kernel<float", 256)], (4 << 20) + 4),
     ("rows_f32", "rows 65536 x 4096 (cfg3)", [("rows_kernel<float", 65536 * 256)], (4 << 28) + 12 * 65536),
     ("segmented_i32", "segmented 2^27 (cfg4)", [("seg_tile_map_kernel", None), ("segmented_sum_kernel", None)], None),
-    ("scan_f32_2_30", "f32 inclusive scan 2^30 (cfg5)", [("scan_tiles_kernel<float", 32768 * 512)], 8 << 30),
+    ("scan_f32_2_30", "f32 inclusive scan 2^30 (cfg5)", [("scan_tiles_kernel<float", None)], 8 << 30),
     ("copy_u32", "copy 1 GiB (ceiling yardstick)", [("copy_tiles_kernel", 4096 * 512)], 8 << 28),
     ("blit", "hipMemcpyAsync 1 GiB (ceiling)", [("__amd_rocclr_copyBuffer", 131072)], 8 << 28),
 ]
