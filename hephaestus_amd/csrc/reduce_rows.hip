@@ -94,6 +94,103 @@ template <typename T, int FLAGS> struct Stats {
             mink = mink < k ? mink : k;
         }
     }
+    // Sixteen elements of one lane's trip through a unit-stride row: y[e]
+    // has index jt + 4*(e/4)*G + e%4, so e ascends with the index.
+    //  - f32 sums: each vector's four values are added pairwise in f32 (two
+    //    roundings, at most 2*eps_f32 of their magnitudes) and the four
+    //    vector sums are added in f64.  A trip whose total is not finite is
+    //    redone element by element in f64, so f32 overflow inside a pair
+    //    never changes a result.
+    //  - f32 max/argmax: signed keys (one shift and one bit-op per element)
+    //    and a max over the trip, then one equality search for the first
+    //    index holding it.  Per element that is about half the VALU work of
+    //    a 64-bit (key, index) compare per element.  With the per-element
+    //    form, 65536 x 4096 rows started at 155 us per launch and rose to
+    //    about 195 us a few milliseconds into a sustained run (the clocks
+    //    backing off under the extra VALU power) before settling near 160;
+    //    this form holds 151-158 us throughout.
+    template <int G> __device__ __forceinline__ void visit_trip(const T (&y)[16], uint32_t jt) {
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) {
+            if constexpr (std::is_same<T, float>::value) {
+                double q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) q[u] = (double)((y[4 * u] + y[4 * u + 1]) + (y[4 * u + 2] + y[4 * u + 3]));
+                double t = (q[0] + q[1]) + (q[2] + q[3]);
+                if (!__builtin_isfinite(t)) {
+                    // An f32 pair sum overflowed (or the trip holds inf or
+                    // NaN): redo the trip in f64, as the per-element path.
+                    t = 0.0;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) t += (double)y[e];
+                }
+                sum += t;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) sum += (S)(typename Wrap<T>::type)y[e];
+            }
+        }
+        if constexpr ((FLAGS & F_PROD) != 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) prod *= (Pr)(typename Wrap<T>::type)y[e];
+        }
+        if constexpr ((FLAGS & (F_ARG | F_MAX)) != 0) {
+            if constexpr (std::is_same<T, float>::value) {
+                int32_t ks[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) ks[e] = signed_key(y[e]);
+                int32_t tk = ks[0];
+#pragma unroll
+                for (int e = 1; e < 16; ++e) tk = tk > ks[e] ? tk : ks[e];
+                if (tk > kSignedPosInf) {
+                    // A NaN with the sign bit clear: the max of the rest.
+                    tk = INT32_MIN;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int32_t k = ks[e] > kSignedPosInf ? INT32_MIN : ks[e];
+                        tk = tk > k ? tk : k;
+                    }
+                }
+                // Below -inf: only NaNs with the sign bit set (or none).
+                if (tk >= kSignedNegInf) {
+                    const uint32_t k = (uint32_t)tk ^ 0x80000000u;  // max_key of that value
+                    if constexpr ((FLAGS & F_ARG) != 0) {
+                        uint32_t tl = (uint32_t)(4 * 3 * G + 3);
+#pragma unroll
+                        for (int e = 14; e >= 0; --e) tl = ks[e] == tk ? (uint32_t)(4 * (e / 4) * G + e % 4) : tl;
+                        arg = umax64(arg, pack_arg(k, jt + tl));
+                    } else {
+                        maxk = maxk > k ? maxk : k;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    if constexpr ((FLAGS & F_ARG) != 0) {
+                        arg = umax64(arg, pack_arg(Key<T>::max_key(y[e]), jt + (uint32_t)(4 * (e / 4) * G + e % 4)));
+                    } else {
+                        const uint32_t k = Key<T>::max_key(y[e]);
+                        maxk = maxk > k ? maxk : k;
+                    }
+                }
+            }
+        }
+        if constexpr ((FLAGS & F_MIN) != 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t k = Key<T>::min_key(y[e]);
+                mink = mink < k ? mink : k;
+            }
+        }
+    }
+    // f32 bits ^ (sign ? 0x7FFFFFFF : 0): as int32 this orders like the
+    // value (-0 < +0), with NaNs above +inf (sign clear) or below -inf (sign
+    // set); XOR 0x80000000 turns it into max_key of the same value.
+    static constexpr int32_t kSignedPosInf = 0x7F800000;
+    static constexpr int32_t kSignedNegInf = (int32_t)0x807FFFFF;
+    static __device__ __forceinline__ int32_t signed_key(float y) {
+        const int32_t b = __float_as_int(y);
+        return b ^ ((b >> 31) & 0x7FFFFFFF);
+    }
     // Combine the statistics of each aligned group of G lanes (4, 16 or 64)
     // with DPP reductions; every lane of the wave must be active.
     // G = 1 (a thread per row) has nothing to combine.
@@ -226,8 +323,17 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
         V x[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&vrow[v + u * G]);
+        // All four loads issue before any arithmetic waits on the first.
+        __builtin_amdgcn_sched_barrier(0);
+        T y[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) visit4(x[u], jb + (uint32_t)(4 * (v + u * G)));
+        for (int u = 0; u < 4; ++u) {
+            y[4 * u] = prologue<T, AFFINE>((T)x[u].x, a, b);
+            y[4 * u + 1] = prologue<T, AFFINE>((T)x[u].y, a, b);
+            y[4 * u + 2] = prologue<T, AFFINE>((T)x[u].z, a, b);
+            y[4 * u + 3] = prologue<T, AFFINE>((T)x[u].w, a, b);
+        }
+        st.template visit_trip<G>(y, jb + (uint32_t)(4 * v));
     }
     if (full * 4 * G < nvec) {
         V x[4];

@@ -298,6 +298,57 @@ def test_rows_output_subsets(device, oracle, subset):
         assert np.array_equal(device.download_owned(i), i_ref)
 
 
+def _special_rows(rng, rows, cols):
+    """Rows drawn from small pools of special values, so NaNs of both signs,
+    signed zeros, infinities, f32 extremes and ties fall inside every 16-value
+    stretch a lane reads: each row family stresses one rule of the max/argmax
+    order (NaN ignored, -0 < +0, the first of equal maxima)."""
+    qnan, nqnan, snan = (np.array([b], np.uint32).view(np.float32) for b in (0x7FC00000, 0xFFC00000, 0x7F800001))
+    inf, fmax = np.float32(np.inf), np.float32(3.4028235e38)
+    pools = [
+        np.concatenate([qnan, nqnan, snan, np.float32([-0.0, 0.0, 1.0, -1.0])]),  # max 1, ties
+        np.concatenate([qnan, nqnan, np.float32([-0.0, -0.0, -0.0, 0.0])]),       # zeros only
+        np.concatenate([qnan, nqnan, snan]),                                       # NaN only: no max
+        np.concatenate([nqnan, np.float32([-inf, -inf])]),                         # below f32::MIN
+        np.concatenate([qnan, np.float32([inf, -inf, fmax, -fmax, 2.0])]),         # infinities
+        np.float32([fmax, -fmax, 1.0, -1.0]),                                      # extremes, sums overflow f32
+    ]
+    x = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        pool = pools[r % len(pools)]
+        x[r] = pool[rng.integers(0, pool.size, cols)]
+        if r % 7 == 3:  # a single winner placed late in the row
+            x[r, (r * 131) % cols] = np.float32(8.0) if r % len(pools) in (0, 4, 5) else x[r, 0]
+    return x
+
+
+@pytest.mark.parametrize("rows,cols", [(96, 4096), (48, 16384), (60, 1000), (64, 64), (6, 70001)])
+@pytest.mark.parametrize("prologue", [None, (0.5, 0.25)])
+def test_rows_special_values(device, oracle, rows, cols, prologue):
+    """Max and argmax bit-exact with the oracle on NaNs, signed zeros,
+    infinities and ties; sums equal in NaN/inf pattern and within the bound
+    where finite (including rows whose partial sums pass f32's range)."""
+    x = _special_rows(np.random.default_rng(rows * 10 + cols), rows, cols)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(x.ravel(), rows, cols, prologue=prologue)
+    buf = device.upload(x.ravel())
+    s = device.alloc_zeroed(np.float32, rows)
+    m = device.alloc_zeroed(np.float32, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    AXIS.reduce_rows_fused(device, buf, rows, cols, prologue=prologue, out_sum=s, out_max=m, out_argmax=i)
+    gi, gm = device.download_owned(i), device.download_owned(m)
+    bad = np.nonzero(gi != i_ref)[0]
+    assert bad.size == 0, f"argmax rows {bad[:8]}: got {gi[bad[:8]]}, want {i_ref[bad[:8]]}"
+    assert np.array_equal(gm.view(np.uint32), m_ref.view(np.uint32))
+    gs = device.download_owned(s).astype(np.float64)
+    ref32 = s_ref.astype(np.float32).astype(np.float64)  # the f32 the row sum rounds to
+    nonfinite = ~np.isfinite(ref32)
+    assert np.array_equal(np.isnan(gs), np.isnan(ref32))
+    assert np.array_equal(gs[nonfinite & ~np.isnan(ref32)], ref32[nonfinite & ~np.isnan(ref32)])
+    fin = ~nonfinite
+    bound = np.array([f32_bound(cols, a) for a in a_ref])
+    assert np.all(np.abs(gs[fin] - s_ref[fin]) <= bound[fin])
+
+
 @pytest.mark.parametrize("axis", [0, 1])
 @pytest.mark.parametrize("op", ["sum", "max", "min", "prod", "argmax"])
 def test_axis_reduce_matches_oracle(device, oracle, axis, op):
