@@ -354,7 +354,8 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
 // host picks G so that each lane holds at least three 16-byte vectors of its
 // row: fewer leaves a lane too little in flight, and the per-row combine then
 // dominates.  Multi-wave groups fold per-lane partials through LDS in wave
-// order before one group reduction, so f32 sums stay deterministic.
+// order before one group reduction, so f32 sums stay deterministic.  Blocks
+// take their rows in XCD-contiguous order (xcd_contiguous).
 // Against one wave per row (the previous form), over 2^28 f32 (sum + max +
 // argmax of fmaf(.5,x,.25)), microseconds per launch by row length:
 // 4096: 156 (162); 3072: 152 (162); 2048: 160 (162); 1000: 173 (235);
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     const int gl = t % G;
     uint32_t rl = (uint32_t)(t / G);
     if constexpr (G >= kWave) rl = (uint32_t)__builtin_amdgcn_readfirstlane(rl);
-    const uint64_t r = (uint64_t)blockIdx.x * kRowsPerBlock + rl;
+    const uint64_t r = (uint64_t)xcd_contiguous(blockIdx.x, gridDim.x) * kRowsPerBlock + rl;
     Stats<T, FLAGS> st;
     if (r < p.rows) {
         const T *row = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
