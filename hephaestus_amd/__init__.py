@@ -10,6 +10,7 @@ it raises ImportError.
 """
 from . import _ffi, errors
 from .device import Event, RocmBuffer, RocmDevice, Topology
+from .device_api import LaunchGeometry, RocmCompiledKernel
 from .errors import (
     AdapterUnavailable,
     AllocationFailed,

@@ -96,6 +96,9 @@ I32 = c_int32
 LP = POINTER(HxLayout)
 AP = POINTER(HxAffine)
 
+# hx_kernel_source_fn: returns the address of NUL-terminated source text.
+SOURCE_FN = ctypes.CFUNCTYPE(c_void_p, c_void_p)
+
 # name -> (restype, argtypes); one entry per declaration in include/hx.h.
 SIGNATURES = {
     "hx_abi_version": (U32, []),
@@ -151,6 +154,9 @@ SIGNATURES = {
     "hx_plan_destroy": (I32, [P]),
     "hx_plan_workspace_bytes": (I32, [P, POINTER(U64)]),
     "hx_fill_random": (I32, [P, P, U64, I32, I32, U64, c_double, c_double, P]),
+    "hx_kernel_compile_cached": (I32, [P, P, U64, c_char_p, SOURCE_FN, P, POINTER(P)]),
+    "hx_kernel_launch": (I32, [P, P, U32, U32, U32, P, U64, POINTER(P), U64, P]),
+    "hx_buffers_alias": (I32, [P, U64, P, U64]),
 }
 
 _lib = None

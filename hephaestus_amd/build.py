@@ -31,6 +31,7 @@ SOURCES = [
     "csrc/vector.hip",
     "csrc/dense_vector.cpp",
     "csrc/noalloc.hip",
+    "csrc/device_api.cpp",
 ]
 HEADERS = ["csrc/hx_device.hpp", "csrc/hx_internal.hpp"]
 ARCH = "gfx950"
@@ -78,7 +79,7 @@ def build(jobs: int = 8) -> Path:
         for fut in [pool.submit(_run, c) for c in cmds]:
             fut.result()
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-lhiprtc", "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

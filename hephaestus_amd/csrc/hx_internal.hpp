@@ -43,6 +43,13 @@ struct StreamWorkspace {
 
 // The device handle behind hx_device* (RocmDevice analog:
 // crates/hephaestus-rocm/src/infrastructure/device.rs:109-165).
+// A run-time compiled kernel (hx_kernel_compile_cached): its module and
+// entry point.
+struct hx_kernel {
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+};
+
 struct hx_device {
     int32_t ordinal = -1;
     hipStream_t stream = nullptr;
@@ -64,6 +71,11 @@ struct hx_device {
     // This device's copy of the no-allocation scratch array (its device
     // address, looked up at hx_device_open with the device current).
     void *noalloc_scratch = nullptr;
+
+    // Run-time compiled kernels (hx_kernel_compile_cached), by cache key;
+    // their modules are unloaded at hx_device_close.
+    std::mutex kernels_mu;
+    std::unordered_map<std::string, std::unique_ptr<hx_kernel>> kernels;
 };
 
 namespace hx {
@@ -94,6 +106,8 @@ hx_status bind_device(const hx_device *dev);
 hipStream_t pick_stream(const hx_device *dev, hx_stream stream);
 // Map the status of a kernel launch (hipGetLastError) to DispatchFailed.
 hx_status check_launch(const char *kernel);
+// Unload every run-time compiled kernel of the device (hx_device_close).
+void release_kernels(hx_device *dev);
 
 // ------------------------------------------------------------- layouts
 

@@ -51,6 +51,9 @@ hx_status length_mismatch(uint64_t host_len, uint64_t device_len) {
 }
 
 hx_status hip_fail(hx_status status, hipError_t err, const char *what) {
+    // The runtime also keeps this error as the thread's last error; clear it,
+    // or the next launch's check_launch would report it again.
+    (void)hipGetLastError();
     return fail(status, "%s: %s (%d)", what, hipGetErrorString(err), (int)err);
 }
 
@@ -301,6 +304,7 @@ hx_status hx_device_close(hx_device *dev) {
         if (entry.second->ws) (void)hipFree(entry.second->ws);
         if (entry.second->scratch) (void)hipFree(entry.second->scratch);
     }
+    release_kernels(dev);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return ok();

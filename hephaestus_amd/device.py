@@ -235,6 +235,30 @@ class RocmDevice:
             )
         )
 
+    # -- DeviceApi (core accelerator/device_api.rs:69-133) --------------
+    def compile_cached(self, key, entry: str, source):
+        """Run-time compiled kernel cached under `key` (device_api.py)."""
+        from . import device_api
+
+        return device_api.compile_cached(self, key, entry, source)
+
+    def launch(self, kernel, geometry, params=None, operands=(), stream=None) -> None:
+        from . import device_api
+
+        device_api.launch(self, kernel, geometry, params, operands, stream)
+
+    @staticmethod
+    def device_ptr(buffer) -> int:
+        from . import device_api
+
+        return device_api.device_ptr(buffer)
+
+    @staticmethod
+    def buffers_alias(lhs, rhs) -> bool:
+        from . import device_api
+
+        return device_api.buffers_alias(lhs, rhs)
+
     # -- events ---------------------------------------------------------
     def event(self) -> "Event":
         return Event(self)

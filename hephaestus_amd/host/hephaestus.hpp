@@ -10,6 +10,7 @@
 //   ScanOps / ScanDirection                   crates/hephaestus-core/src/domain/scan.rs:36-264
 //   DenseVectorOps                            crates/hephaestus-core/src/domain/vector.rs:57-200
 //   dot / trace / norms                       crates/hephaestus-rocm/src/application/linalg/norms.rs:394-490
+//   DeviceApi / LaunchGeometry                crates/hephaestus-core/src/domain/accelerator/device_api.rs:10-133
 //   HephaestusError                           crates/hephaestus-core/src/domain/error.rs:8-58
 // Errors are thrown as hephaestus::Error carrying the variant and the
 // native message; every entry point validates before it writes, so a
@@ -21,6 +22,7 @@
 
 #include <array>
 #include <cstdint>
+#include <functional>
 #include <initializer_list>
 #include <memory>
 #include <stdexcept>
@@ -179,6 +181,16 @@ struct Topology {
 };
 
 // ------------------------------------------------------------------ device
+// LaunchGeometry (device_api.rs:10-47): `groups` blocks of `width` lanes
+// with `shared_bytes` of dynamic LDS.
+struct LaunchGeometry {
+    uint32_t groups, width, shared_bytes;
+    static LaunchGeometry linear(uint32_t groups, uint32_t width) { return {groups, width, 0}; }
+    static LaunchGeometry linear_shared(uint32_t groups, uint32_t width, uint32_t shared_bytes) {
+        return {groups, width, shared_bytes};
+    }
+};
+
 class RocmDevice {
   public:
     // ComputeDeviceAcquisition: the first device / a given ordinal.
@@ -234,6 +246,41 @@ class RocmDevice {
     }
     template <typename T> void copy_buffer(const RocmBuffer<T> &src, RocmBuffer<T> &dst) {
         check(hx_copy(dev_, src.device_ptr(), src.len(), dst.device_ptr(), dst.len(), sizeof(T)));
+    }
+
+    // -- DeviceApi (device_api.rs:69-133) -------------------------------
+    using Kernel = const hx_kernel *;
+    using DevicePtr = void *;
+    // compile_cached: `source` runs only on a cache miss.
+    Kernel compile_cached(const std::string &key, const std::string &entry,
+                          const std::function<std::string()> &source) {
+        struct Ctx {
+            const std::function<std::string()> *source;
+            std::string text;
+        } ctx{&source, {}};
+        hx_kernel *k = nullptr;
+        check(hx_kernel_compile_cached(
+            dev_, key.data(), key.size(), entry.c_str(),
+            [](void *c) -> const char * {
+                Ctx *x = static_cast<Ctx *>(c);
+                x->text = (*x->source)();
+                return x->text.c_str();
+            },
+            &ctx, &k));
+        return k;
+    }
+    template <typename T> static DevicePtr device_ptr(const RocmBuffer<T> &b) { return b.device_ptr(); }
+    template <typename T> static bool buffers_alias(const RocmBuffer<T> &a, const RocmBuffer<T> &b) {
+        return hx_buffers_alias(a.device_ptr(), a.len() * sizeof(T), b.device_ptr(), b.len() * sizeof(T)) != 0;
+    }
+    // launch: `params` by value as the kernel's first argument, then each
+    // operand's address.
+    template <typename P>
+    void launch(Kernel kernel, const LaunchGeometry &g, const P &params, std::initializer_list<DevicePtr> operands) {
+        static_assert(std::is_trivially_copyable<P>::value, "the parameter block is copied bytewise");
+        std::vector<void *> ops(operands);
+        check(hx_kernel_launch(dev_, kernel, g.groups, g.width, g.shared_bytes, &params, sizeof(P), ops.data(),
+                               ops.size(), nullptr));
     }
 
   private:

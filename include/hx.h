@@ -468,6 +468,53 @@ hx_status hx_plan_destroy(hx_plan *plan);
 /* Bytes of device workspace the plan owns. */
 hx_status hx_plan_workspace_bytes(const hx_plan *plan, uint64_t *bytes);
 
+/* ------------------------------------------------------------ DeviceApi */
+/* The vendor seam beneath the reference's generic accelerator layer
+ * (DeviceApi, core accelerator/device_api.rs:69-133; ROCm impl
+ * crates/hephaestus-rocm/src/application/device_api.rs:49-103 over
+ * pipeline.rs:175-349): kernel source compiled at run time with hipRTC for
+ * this device's architecture, cached per device under a caller key, and
+ * launched with a parameter block and an ordered operand list.  Consumers
+ * run their own kernels through it next to the library's. */
+
+typedef struct hx_kernel hx_kernel; /* owned by the device; valid until
+                                       hx_device_close */
+
+/* Returns the NUL-terminated source to compile, or NULL to fail the call.
+ * Called only on a cache miss (compile_cached's `source: impl FnOnce`);
+ * the text is copied before hx_kernel_compile_cached returns. */
+typedef const char *(*hx_kernel_source_fn)(void *ctx);
+
+/* compile_cached (device_api.rs:83-99, pipeline.rs:259-322): the kernel
+ * cached under `key` (key_len bytes, compared bytewise), else source(ctx)
+ * compiled (-O3, no packed FP32 instructions, the device's
+ * --offload-arch), loaded as a module, and `entry` looked up.  Compile,
+ * load and lookup failures are HX_ERR_DISPATCH_FAILED (a compile failure
+ * carries the hipRTC log) and are not cached. */
+hx_status hx_kernel_compile_cached(hx_device *dev, const void *key,
+                                   uint64_t key_len, const char *entry,
+                                   hx_kernel_source_fn source, void *ctx,
+                                   hx_kernel **kernel);
+
+/* launch (device_api.rs:116-132; ROCm device_api.rs:75-102): `groups`
+ * blocks of `width` lanes (LaunchGeometry, device_api.rs:16-24) with
+ * `shared_bytes` of dynamic LDS.  The argument list is the parameter block
+ * (params_bytes at `params`, passed by value as the kernel's first
+ * argument; omitted when params_bytes is 0) followed by each operand's
+ * device address.  width 0 is HX_ERR_INVALID_CONFIGURATION; the runtime's
+ * launch errors are HX_ERR_DISPATCH_FAILED.  Stream-ordered on `stream`. */
+hx_status hx_kernel_launch(hx_device *dev, const hx_kernel *kernel,
+                           uint32_t groups, uint32_t width,
+                           uint32_t shared_bytes, const void *params,
+                           uint64_t params_bytes, void *const *operands,
+                           uint64_t operand_count, hx_stream stream);
+
+/* buffers_alias (device_api.rs:105-110; ROCm buffer.rs:47-49): 1 when both
+ * addresses are non-null and equal (the reference's rule) or the byte
+ * ranges [a, a + a_bytes) and [b, b + b_bytes) overlap, else 0. */
+int32_t hx_buffers_alias(const void *a, uint64_t a_bytes, const void *b,
+                         uint64_t b_bytes);
+
 /* --------------------------------------------------- synthetic inputs */
 
 /* RandomInitOps analog (core random.rs), counter-based so every element is

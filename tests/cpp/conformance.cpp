@@ -440,6 +440,45 @@ void additions_at_size(RocmDevice &dev) {
     CHECK(same(dev.download_owned(sout), swant));
 }
 
+// ------------------------------------------- accelerator/device_api.rs
+// A consumer kernel through the DeviceApi seam: compiled once per key (the
+// source callback runs only on a miss), launched with a parameter block
+// followed by operand addresses; a broken source is DispatchFailed.
+void device_api_contract(RocmDevice &dev) {
+    static const char *kSrc = R"(
+struct Params { unsigned int n; unsigned int k; };
+extern "C" __global__ void add_k(Params p, const unsigned int *x, unsigned int *y) {
+    unsigned int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < p.n) y[i] = x[i] + p.k;
+}
+)";
+    int calls = 0;
+    auto source = [&]() {
+        ++calls;
+        return std::string(kSrc);
+    };
+    RocmDevice::Kernel k1 = dev.compile_cached("cpp-add-k", "add_k", source);
+    RocmDevice::Kernel k2 = dev.compile_cached("cpp-add-k", "add_k", source);
+    CHECK(k1 == k2 && calls == 1);
+    struct Params {
+        uint32_t n, k;
+    };
+    const uint32_t n = 1000;
+    std::vector<uint32_t> x(n);
+    for (uint32_t i = 0; i < n; ++i) x[i] = i * 7u;
+    RocmBuffer<uint32_t> xb = dev.upload(x);
+    RocmBuffer<uint32_t> yb = dev.alloc_zeroed<uint32_t>(n);
+    dev.launch(k1, LaunchGeometry::linear((n + 127) / 128, 128), Params{n, 42u},
+               {RocmDevice::device_ptr(xb), RocmDevice::device_ptr(yb)});
+    dev.synchronize();
+    std::vector<uint32_t> want(n);
+    for (uint32_t i = 0; i < n; ++i) want[i] = i * 7u + 42u;
+    CHECK(same(dev.download_owned(yb), want));
+    CHECK(RocmDevice::buffers_alias(xb, xb) && !RocmDevice::buffers_alias(xb, yb));
+    expect_error(ErrorKind::DispatchFailed, "hiprtcCompileProgram",
+                 [&] { dev.compile_cached("cpp-broken", "broken", [] { return std::string("not c++ {"); }); });
+}
+
 } // namespace
 
 int main() {
@@ -462,6 +501,7 @@ int main() {
         {"dense_vector", dense_vector_contract},
         {"rocm_map_reduction", map_reduction_contract},
         {"additions_at_size", additions_at_size},
+        {"device_api", device_api_contract},
     };
     for (const auto &c : clauses) {
         const int before = g_failures;

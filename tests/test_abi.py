@@ -246,3 +246,39 @@ def test_integer_mean_counts_beyond_the_divisor_type_are_rejected():
     lay = ctypes.byref(_ffi.layout_struct(L([2**33])))
     st = lib.hx_reduce_full(None, _ffi.OP_MEAN, _ffi.DTYPE_F32, 0x1000, 2**33, lay, 0x2000, 1, one, None, None)
     assert st == _ffi.INVALID_CONFIGURATION and _ffi.last_message() == "null device handle"
+
+
+def test_buffers_alias_rule():
+    """hx_buffers_alias: one non-null base (the reference's rule, rocm
+    buffer.rs:47-49) or overlapping byte ranges; null never aliases."""
+    lib = hx.load_native()
+    assert lib.hx_buffers_alias(0x1000, 64, 0x1000, 64) == 1
+    assert lib.hx_buffers_alias(0x1000, 0, 0x1000, 0) == 1
+    assert lib.hx_buffers_alias(0x1000, 64, 0x1040, 64) == 0  # adjacent
+    assert lib.hx_buffers_alias(0x1000, 65, 0x1040, 64) == 1  # one byte of overlap
+    assert lib.hx_buffers_alias(0x1040, 64, 0x1000, 65) == 1
+    assert lib.hx_buffers_alias(None, 64, None, 64) == 0
+    assert lib.hx_buffers_alias(None, 64, 0x1000, 64) == 0
+
+
+def test_device_api_rejects_null_handles_before_the_device():
+    """The DeviceApi entry points check their handles before any HIP call,
+    so these run without a GPU; the source callback is never reached."""
+    lib = hx.load_native()
+    calls = []
+
+    def provide(_ctx):
+        calls.append(1)
+        return None
+
+    cb = _ffi.SOURCE_FN(provide)
+    out = ctypes.c_void_p(1)
+    st = lib.hx_kernel_compile_cached(None, b"k", 1, b"entry", cb, None, ctypes.byref(out))
+    assert st == _ffi.INVALID_CONFIGURATION and _ffi.last_message() == "null device handle"
+    assert out.value is None and not calls
+    st = lib.hx_kernel_launch(None, None, 1, 64, 0, None, 0, None, 0, None)
+    assert st == _ffi.INVALID_CONFIGURATION and _ffi.last_message() == "null kernel handle"
+    with pytest.raises(hx.InvalidConfiguration):
+        hx.LaunchGeometry.linear(4, 0)
+    g = hx.LaunchGeometry.linear_shared(4, 64, 256)
+    assert (g.groups, g.width, g.shared_bytes) == (4, 64, 256)
