@@ -796,15 +796,20 @@ def main() -> int:
 
     cpu_head = 0.0 if args.no_cpu_baseline else args.cpu_seconds
     cpu_other = cpu_head / 3.0
+    # Every configuration's buffers stay resident until the end, as a
+    # caller's would: a 1 GiB input allocated into memory that an earlier
+    # configuration had freed streamed 4% slower (the f32 sum at 2^28: 154.5
+    # us in a fresh process, 161 after the scan's buffers were freed).
     head, w = run_config("scan_u32", hx, dev, args, cpu_head)
-    del w
+    resident = [w]
     secondary = {}
     for key, name in (("f32_sum_reduce_2_28", "sum_f32"), ("cfg1_f32_sum_2_20", "sum_f32_2_20"),
                       ("cfg3_rows_f32_65536x4096", "rows_f32"), ("cfg4_segmented_i32_2_27", "segmented_i32"),
                       ("cfg5_scan_f32_2_30", "scan_f32_2_30")):
         secondary[key], w = run_config(name, hx, dev, args, cpu_other)
-        del w
+        resident.append(w)
     ceil = ceiling(hx, dev, args.steps, args.warmup)
+    del resident
     best = max(ceil["copy_kernel"]["GB/s"], ceil["runtime_blit_hipMemcpyAsync"]["GB/s"])
     ceil["best_GB/s"] = best
     ceil["headline_scan_over_best"] = round(head["value"] / best, 4)
