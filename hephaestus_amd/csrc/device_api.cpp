@@ -115,6 +115,7 @@ hx_status hx_kernel_compile_cached(hx_device *dev, const void *key, uint64_t key
     std::vector<char> code;
     HX_TRY(compile_to_code(dev, src, code));
     auto compiled = std::make_unique<hx_kernel>();
+    compiled->owner = dev;
     HX_HIP(hipModuleLoadData(&compiled->module, code.data()), HX_ERR_DISPATCH_FAILED, "hipModuleLoadData");
     hipError_t err = hipModuleGetFunction(&compiled->function, compiled->module, entry);
     if (err != hipSuccess) {
@@ -140,6 +141,8 @@ hx_status hx_kernel_launch(hx_device *dev, const hx_kernel *kernel, uint32_t gro
     if (kernel == nullptr || kernel->function == nullptr)
         return fail(HX_ERR_INVALID_CONFIGURATION, "null kernel handle");
     if (width == 0) return fail(HX_ERR_INVALID_CONFIGURATION, "block width must be non-zero");
+    if (kernel->owner != dev)
+        return fail(HX_ERR_INVALID_CONFIGURATION, "kernel was compiled for another device");
     if (params == nullptr && params_bytes != 0) return fail(HX_ERR_INVALID_CONFIGURATION, "null parameter block");
     if (operands == nullptr && operand_count != 0) return fail(HX_ERR_INVALID_CONFIGURATION, "null operand list");
     HX_TRY(bind_device(dev));

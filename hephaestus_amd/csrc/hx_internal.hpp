@@ -48,6 +48,7 @@ struct StreamWorkspace {
 struct hx_kernel {
     hipModule_t module = nullptr;
     hipFunction_t function = nullptr;
+    const hx_device *owner = nullptr; // the device whose cache holds it
 };
 
 struct hx_device {

@@ -501,8 +501,9 @@ hx_status hx_kernel_compile_cached(hx_device *dev, const void *key,
  * `shared_bytes` of dynamic LDS.  The argument list is the parameter block
  * (params_bytes at `params`, passed by value as the kernel's first
  * argument; omitted when params_bytes is 0) followed by each operand's
- * device address.  width 0 is HX_ERR_INVALID_CONFIGURATION; the runtime's
- * launch errors are HX_ERR_DISPATCH_FAILED.  Stream-ordered on `stream`. */
+ * device address.  width 0, or a kernel compiled for another device, is
+ * HX_ERR_INVALID_CONFIGURATION; the runtime's launch errors are
+ * HX_ERR_DISPATCH_FAILED.  Stream-ordered on `stream`. */
 hx_status hx_kernel_launch(hx_device *dev, const hx_kernel *kernel,
                            uint32_t groups, uint32_t width,
                            uint32_t shared_bytes, const void *params,

@@ -230,3 +230,35 @@ def test_buffers_alias(device):
     assert hx.RocmDevice.buffers_alias(a, a)
     assert not hx.RocmDevice.buffers_alias(a, b)
     assert hx.RocmDevice.device_ptr(a) == a.ptr
+
+
+def test_concurrent_compiles_of_one_key_share_one_kernel(device):
+    """Threads racing to compile the same key all get the one cached kernel
+    (the loser of the race unloads its own module)."""
+    import threading
+
+    start = threading.Barrier(4)
+    handles, errors_seen = [], []
+
+    def work():
+        try:
+            start.wait()
+            handles.append(device.compile_cached(b"test-race", "affine_u32", lambda: AFFINE_SRC).handle)
+        except Exception as exc:
+            errors_seen.append(exc)
+
+    threads = [threading.Thread(target=work) for _ in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors_seen, errors_seen
+    assert len(handles) == 4 and len(set(handles)) == 1
+    # and the kernel works
+    n = 4096
+    x = np.arange(n, dtype=np.uint32)
+    xb, yb = device.upload(x), device.alloc_zeroed(np.uint32, n)
+    device.launch(hx.RocmCompiledKernel(device, handles[0], b"test-race", "affine_u32"),
+                  LaunchGeometry.linear(n // 256, 256), AffineParams(n, 2, 1, 0), [xb, yb])
+    device.synchronize()
+    assert np.array_equal(device.download_owned(yb), x * np.uint32(2) + np.uint32(1))
