@@ -69,6 +69,18 @@ class HxAffine(Structure):
     _fields_ = [("a", c_float), ("b", c_float), ("enabled", c_uint32), ("reserved", c_uint32)]
 
 
+class HxDeviceLimits(Structure):
+    _fields_ = [
+        ("max_buffer_size", c_uint64),
+        ("max_compute_workgroup_size_x", c_uint32),
+        ("max_compute_workgroup_size_y", c_uint32),
+        ("max_compute_workgroup_size_z", c_uint32),
+        ("max_compute_invocations_per_workgroup", c_uint32),
+        ("max_compute_workgroup_storage_size", c_uint32),
+        ("max_immediate_size", c_uint32),
+    ]
+
+
 class HxDeviceInfo(Structure):
     _fields_ = [
         ("name", c_char * 96),
@@ -110,6 +122,9 @@ SIGNATURES = {
     "hx_device_close": (I32, [P]),
     "hx_device_get_info": (I32, [P, POINTER(HxDeviceInfo)]),
     "hx_device_stream": (I32, [P, POINTER(P)]),
+    "hx_device_get_limits": (I32, [P, POINTER(HxDeviceLimits)]),
+    "hx_device_supports_feature": (I32, [P, I32]),
+    "hx_require_limits": (I32, [POINTER(HxDeviceLimits), POINTER(HxDeviceLimits)]),
     "hx_synchronize": (I32, [P]),
     "hx_alloc": (I32, [P, U64, U32, POINTER(P)]),
     "hx_free": (I32, [P, P]),

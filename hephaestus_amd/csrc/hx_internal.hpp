@@ -55,6 +55,7 @@ struct hx_device {
     int32_t ordinal = -1;
     hipStream_t stream = nullptr;
     hx_device_info info{};
+    hx_device_limits limits{};
 
     // Pinned double-buffered staging for host<->device transfers.
     std::mutex staging_mu;

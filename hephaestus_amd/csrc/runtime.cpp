@@ -260,6 +260,33 @@ hx_status hx_device_open(int32_t ordinal, hx_device **out) {
     info.total_memory_bytes = (uint64_t)prop.totalGlobalMem;
     size_t free_b = 0, total_b = 0;
     if (hipMemGetInfo(&free_b, &total_b) == hipSuccess) info.free_memory_bytes = free_b;
+    // Device limits (ROCm query.rs:28-90).
+    {
+        hx_device_limits &lim = dev->limits;
+        lim.max_buffer_size = info.free_memory_bytes;
+        struct {
+            hipDeviceAttribute_t attr;
+            uint32_t *dst;
+            const char *name;
+        } q[] = {
+            {hipDeviceAttributeMaxBlockDimX, &lim.max_compute_workgroup_size_x, "max_block_dim_x"},
+            {hipDeviceAttributeMaxBlockDimY, &lim.max_compute_workgroup_size_y, "max_block_dim_y"},
+            {hipDeviceAttributeMaxBlockDimZ, &lim.max_compute_workgroup_size_z, "max_block_dim_z"},
+            {hipDeviceAttributeMaxThreadsPerBlock, &lim.max_compute_invocations_per_workgroup,
+             "max_threads_per_block"},
+            {hipDeviceAttributeMaxSharedMemoryPerBlock, &lim.max_compute_workgroup_storage_size,
+             "max_shared_memory_per_block"},
+        };
+        for (auto &e : q) {
+            int v = 0;
+            err = hipDeviceGetAttribute(&v, e.attr, ordinal);
+            if (err != hipSuccess) return bail(hip_fail(HX_ERR_DEVICE_UNAVAILABLE, err, e.name));
+            if (v < 0)
+                return bail(fail(HX_ERR_DEVICE_UNAVAILABLE, "ROCm attribute %s returned negative value %d", e.name, v));
+            *e.dst = (uint32_t)v;
+        }
+        lim.max_immediate_size = 0;
+    }
 
     // This device's no-allocation scratch, looked up with the device current.
     {
@@ -313,6 +340,41 @@ hx_status hx_device_close(hx_device *dev) {
 hx_status hx_device_get_info(const hx_device *dev, hx_device_info *out) {
     if (!dev || !out) return fail(HX_ERR_INVALID_CONFIGURATION, "null argument");
     *out = dev->info;
+    return ok();
+}
+
+hx_status hx_device_get_limits(const hx_device *dev, hx_device_limits *out) {
+    if (!dev || !out) return fail(HX_ERR_INVALID_CONFIGURATION, "null argument");
+    *out = dev->limits;
+    return ok();
+}
+
+int32_t hx_device_supports_feature(const hx_device *dev, hx_device_feature feature) {
+    (void)dev;
+    (void)feature;
+    return 0;
+}
+
+hx_status hx_require_limits(const hx_device_limits *actual, const hx_device_limits *required) {
+    if (!actual || !required) return fail(HX_ERR_INVALID_CONFIGURATION, "null argument");
+    const struct {
+        const char *name;
+        uint64_t available, needed;
+    } rows[] = {
+        {"max_buffer_size", actual->max_buffer_size, required->max_buffer_size},
+        {"max_compute_workgroup_size_x", actual->max_compute_workgroup_size_x, required->max_compute_workgroup_size_x},
+        {"max_compute_workgroup_size_y", actual->max_compute_workgroup_size_y, required->max_compute_workgroup_size_y},
+        {"max_compute_workgroup_size_z", actual->max_compute_workgroup_size_z, required->max_compute_workgroup_size_z},
+        {"max_compute_invocations_per_workgroup", actual->max_compute_invocations_per_workgroup,
+         required->max_compute_invocations_per_workgroup},
+        {"max_compute_workgroup_storage_size", actual->max_compute_workgroup_storage_size,
+         required->max_compute_workgroup_storage_size},
+        {"max_immediate_size", actual->max_immediate_size, required->max_immediate_size},
+    };
+    for (const auto &r : rows)
+        if (r.available < r.needed)
+            return fail(HX_ERR_DEVICE_UNAVAILABLE, "ROCm device limit %s %llu is below required %llu", r.name,
+                        (unsigned long long)r.available, (unsigned long long)r.needed);
     return ok();
 }
 

@@ -8,6 +8,7 @@ infrastructure/buffer.rs:16-80).
 from __future__ import annotations
 
 import ctypes
+import enum
 from dataclasses import dataclass
 
 import numpy as np
@@ -45,6 +46,49 @@ class Topology:
     clock_khz: int
     memory_clock_khz: int
     memory_bus_width_bits: int
+
+
+class DevicePreference(enum.Enum):
+    """DevicePreference (core device.rs:10-17)."""
+
+    HighPerformance = 0
+    LowPower = 1
+
+
+class DeviceFeature(enum.IntEnum):
+    """DeviceFeature (core device.rs:19-36), hx_device_feature values."""
+
+    TimestampQuery = 0
+    ShaderF64 = 1
+    ShaderF16 = 2
+    MappablePrimaryBuffers = 3
+    ImmediateData = 4
+
+
+@dataclass(frozen=True)
+class DeviceLimits:
+    """DeviceLimits (core device.rs:38-80); the optional per-stage binding
+    limits are None on ROCm (query.rs:85-86)."""
+
+    max_buffer_size: int = 0
+    max_compute_workgroup_size_x: int = 0
+    max_compute_workgroup_size_y: int = 0
+    max_compute_workgroup_size_z: int = 0
+    max_compute_invocations_per_workgroup: int = 0
+    max_compute_workgroup_storage_size: int = 0
+    max_immediate_size: int = 0
+    max_storage_buffers_per_shader_stage: int | None = None
+    max_buffers_and_acceleration_structures_per_shader_stage: int | None = None
+
+    def _struct(self) -> _ffi.HxDeviceLimits:
+        s = _ffi.HxDeviceLimits()
+        for name, _ in _ffi.HxDeviceLimits._fields_:
+            setattr(s, name, int(getattr(self, name)))
+        return s
+
+    @classmethod
+    def _from(cls, s: _ffi.HxDeviceLimits) -> "DeviceLimits":
+        return cls(**{name: getattr(s, name) for name, _ in _ffi.HxDeviceLimits._fields_})
 
 
 class RocmBuffer:
@@ -126,6 +170,52 @@ class RocmDevice:
     @classmethod
     def try_default(cls) -> "RocmDevice":
         return cls.try_with_ordinal(0)
+
+    # -- ComputeDeviceAcquisition (ROCm acquisition.rs:8-35) -------------
+    @classmethod
+    def try_acquire_device(cls, label: str = "", device_preference=DevicePreference.HighPerformance,
+                           optional_features=(), required_limits: DeviceLimits = DeviceLimits()) -> "RocmDevice":
+        """The first device, if it meets `required_limits` (label,
+        preference and optional features do not select among AMD devices)."""
+        device = cls.try_default()
+        try:
+            cls.require_limits(device.device_limits(), required_limits)
+        except BaseException:
+            device.close()
+            raise
+        return device
+
+    @classmethod
+    def try_acquire_devices(cls, label_prefix: str = "", max_devices: int = 1,
+                            device_preference=DevicePreference.HighPerformance, optional_features=(),
+                            required_limits: DeviceLimits = DeviceLimits()) -> list:
+        devices = []
+        try:
+            for ordinal in range(min(cls.device_count(), int(max_devices))):
+                device = cls.try_with_ordinal(ordinal)
+                devices.append(device)
+                cls.require_limits(device.device_limits(), required_limits)
+        except BaseException:
+            for d in devices:
+                d.close()
+            raise
+        return devices
+
+    @staticmethod
+    def require_limits(actual: DeviceLimits, required: DeviceLimits) -> None:
+        """DeviceUnavailable for the first limit below the required one
+        (ROCm device.rs:187-238)."""
+        a, r = actual._struct(), required._struct()
+        _ffi.check(_ffi.lib().hx_require_limits(ctypes.byref(a), ctypes.byref(r)))
+
+    # -- ComputeDeviceCapabilities (ROCm capabilities.rs:5-21) -----------
+    def device_limits(self) -> DeviceLimits:
+        s = _ffi.HxDeviceLimits()
+        _ffi.check(_ffi.lib().hx_device_get_limits(self.handle, ctypes.byref(s)))
+        return DeviceLimits._from(s)
+
+    def supports_device_feature(self, feature: DeviceFeature) -> bool:
+        return bool(_ffi.lib().hx_device_supports_feature(self.handle, int(feature)))
 
     def close(self) -> None:
         if self.handle:

@@ -11,6 +11,7 @@
 //   DenseVectorOps                            crates/hephaestus-core/src/domain/vector.rs:57-200
 //   dot / trace / norms                       crates/hephaestus-rocm/src/application/linalg/norms.rs:394-490
 //   DeviceApi / LaunchGeometry                crates/hephaestus-core/src/domain/accelerator/device_api.rs:10-133
+//   ComputeDeviceCapabilities / limits        crates/hephaestus-core/src/domain/device.rs:38-80,225-238
 //   HephaestusError                           crates/hephaestus-core/src/domain/error.rs:8-58
 // Errors are thrown as hephaestus::Error carrying the variant and the
 // native message; every entry point validates before it writes, so a
@@ -205,6 +206,15 @@ class RocmDevice {
         check(hx_device_count(&n));
         return n;
     }
+    // ComputeDeviceAcquisition::try_acquire_device (ROCm acquisition.rs:9-18).
+    static RocmDevice try_acquire_device(const hx_device_limits &required) {
+        RocmDevice d = try_default();
+        require_limits(d.device_limits(), required);
+        return d;
+    }
+    static void require_limits(const hx_device_limits &actual, const hx_device_limits &required) {
+        check(hx_require_limits(&actual, &required));
+    }
 
     RocmDevice(RocmDevice &&o) noexcept : dev_(o.dev_) { o.dev_ = nullptr; }
     RocmDevice(const RocmDevice &) = delete;
@@ -221,6 +231,13 @@ class RocmDevice {
         return Topology{i.name, i.arch, i.compute_units, i.warp_size, i.total_memory_bytes};
     }
     void synchronize() { check(hx_synchronize(dev_)); }
+    // ComputeDeviceCapabilities (ROCm capabilities.rs:5-21).
+    hx_device_limits device_limits() const {
+        hx_device_limits l{};
+        check(hx_device_get_limits(dev_, &l));
+        return l;
+    }
+    bool supports_device_feature(hx_device_feature f) const { return hx_device_supports_feature(dev_, f) != 0; }
 
     template <typename T> RocmBuffer<T> alloc_zeroed(uint64_t len) { return alloc<T>(len, true); }
     template <typename T> RocmBuffer<T> alloc_uninitialized(uint64_t len) { return alloc<T>(len, false); }

@@ -161,6 +161,41 @@ hx_status hx_device_close(hx_device *dev);
 hx_status hx_device_get_info(const hx_device *dev, hx_device_info *out);
 /* The device's own stream (what a NULL hx_stream selects). */
 hx_status hx_device_stream(const hx_device *dev, hx_stream *out);
+
+/* ComputeDeviceCapabilities (core device.rs:225-238; ROCm
+ * infrastructure/capabilities.rs:5-21 over query.rs:28-101).  The limits
+ * are queried at hx_device_open: max_buffer_size is the free device memory
+ * then (query.rs:39), the workgroup limits are the HIP device attributes,
+ * max_immediate_size is 0. */
+typedef struct hx_device_limits {
+    uint64_t max_buffer_size;
+    uint32_t max_compute_workgroup_size_x;
+    uint32_t max_compute_workgroup_size_y;
+    uint32_t max_compute_workgroup_size_z;
+    uint32_t max_compute_invocations_per_workgroup;
+    uint32_t max_compute_workgroup_storage_size;
+    uint32_t max_immediate_size;
+} hx_device_limits;
+/* DeviceFeature (core device.rs:19-36). */
+typedef enum hx_device_feature {
+    HX_FEATURE_TIMESTAMP_QUERY = 0,
+    HX_FEATURE_SHADER_F64 = 1,
+    HX_FEATURE_SHADER_F16 = 2,
+    HX_FEATURE_MAPPABLE_PRIMARY_BUFFERS = 3,
+    HX_FEATURE_IMMEDIATE_DATA = 4
+} hx_device_feature;
+hx_status hx_device_get_limits(const hx_device *dev, hx_device_limits *out);
+/* supports_device_feature: 0 for every feature, as the reference's ROCm
+ * device reports (capabilities.rs:12-20: hipMalloc memory is not
+ * host-mappable). */
+int32_t hx_device_supports_feature(const hx_device *dev,
+                                   hx_device_feature feature);
+/* require_limits (ROCm device.rs:187-238), used by try_acquire_device(s)
+ * (ROCm acquisition.rs:8-35): HX_ERR_DEVICE_UNAVAILABLE "ROCm device limit
+ * <name> <available> is below required <needed>" for the first field of
+ * `actual` below `required`, in the order of the struct. */
+hx_status hx_require_limits(const hx_device_limits *actual,
+                            const hx_device_limits *required);
 /* ComputeDevice::synchronize (core device.rs:218-223). */
 hx_status hx_synchronize(hx_device *dev);
 

@@ -477,6 +477,14 @@ extern "C" __global__ void add_k(Params p, const unsigned int *x, unsigned int *
     CHECK(RocmDevice::buffers_alias(xb, xb) && !RocmDevice::buffers_alias(xb, yb));
     expect_error(ErrorKind::DispatchFailed, "hiprtcCompileProgram",
                  [&] { dev.compile_cached("cpp-broken", "broken", [] { return std::string("not c++ {"); }); });
+    // ComputeDeviceCapabilities / require_limits
+    const hx_device_limits lim = dev.device_limits();
+    CHECK(lim.max_compute_invocations_per_workgroup == 1024 && lim.max_immediate_size == 0);
+    CHECK(!dev.supports_device_feature(HX_FEATURE_SHADER_F64));
+    hx_device_limits need = lim;
+    need.max_compute_workgroup_storage_size = lim.max_compute_workgroup_storage_size + 1;
+    expect_error(ErrorKind::DeviceUnavailable, "ROCm device limit max_compute_workgroup_storage_size",
+                 [&] { RocmDevice::require_limits(lim, need); });
 }
 
 } // namespace

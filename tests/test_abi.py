@@ -282,3 +282,24 @@ def test_device_api_rejects_null_handles_before_the_device():
         hx.LaunchGeometry.linear(4, 0)
     g = hx.LaunchGeometry.linear_shared(4, 64, 256)
     assert (g.groups, g.width, g.shared_bytes) == (4, 64, 256)
+
+
+def test_require_limits_messages():
+    """require_limits (ROCm device.rs:187-238): the first field short of the
+    requirement, in DeviceLimits order, is DeviceUnavailable with the
+    reference's message; equal values satisfy."""
+    have = hx.DeviceLimits(max_buffer_size=100, max_compute_workgroup_size_x=1024, max_compute_workgroup_size_y=1024,
+                           max_compute_workgroup_size_z=1024, max_compute_invocations_per_workgroup=1024,
+                           max_compute_workgroup_storage_size=65536, max_immediate_size=0)
+    hx.RocmDevice.require_limits(have, have)
+    hx.RocmDevice.require_limits(have, hx.DeviceLimits())
+    with pytest.raises(hx.DeviceUnavailable) as info:
+        hx.RocmDevice.require_limits(have, hx.DeviceLimits(max_buffer_size=200, max_immediate_size=4))
+    assert _ffi.last_message() == "ROCm device limit max_buffer_size 100 is below required 200"
+    with pytest.raises(hx.DeviceUnavailable):
+        hx.RocmDevice.require_limits(have, hx.DeviceLimits(max_compute_invocations_per_workgroup=2048))
+    assert _ffi.last_message() == "ROCm device limit max_compute_invocations_per_workgroup 1024 is below required 2048"
+    with pytest.raises(hx.DeviceUnavailable):
+        hx.RocmDevice.require_limits(have, hx.DeviceLimits(max_immediate_size=1))
+    assert _ffi.last_message() == "ROCm device limit max_immediate_size 0 is below required 1"
+    assert "below required" in str(info.value)

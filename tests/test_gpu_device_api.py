@@ -262,3 +262,29 @@ def test_concurrent_compiles_of_one_key_share_one_kernel(device):
                   LaunchGeometry.linear(n // 256, 256), AffineParams(n, 2, 1, 0), [xb, yb])
     device.synchronize()
     assert np.array_equal(device.download_owned(yb), x * np.uint32(2) + np.uint32(1))
+
+
+def test_capabilities_and_acquisition(device):
+    """ComputeDeviceCapabilities and ComputeDeviceAcquisition (ROCm
+    capabilities.rs:5-21, acquisition.rs:8-35, query.rs:28-101)."""
+    lim = device.device_limits()
+    topo = device.topology()
+    assert lim.max_compute_invocations_per_workgroup == topo.max_threads_per_block == 1024
+    assert lim.max_compute_workgroup_size_x == 1024
+    assert lim.max_compute_workgroup_size_y >= 1 and lim.max_compute_workgroup_size_z >= 1
+    assert lim.max_compute_workgroup_storage_size >= 65536
+    assert 0 < lim.max_buffer_size <= topo.total_memory_bytes
+    assert lim.max_immediate_size == 0
+    assert lim.max_storage_buffers_per_shader_stage is None
+    for f in hx.DeviceFeature:
+        assert device.supports_device_feature(f) is False
+    d2 = hx.RocmDevice.try_acquire_device("test", hx.DevicePreference.HighPerformance, [],
+                                          hx.DeviceLimits(max_compute_invocations_per_workgroup=1024))
+    d2.close()
+    with pytest.raises(hx.DeviceUnavailable, match="max_compute_invocations_per_workgroup 1024 is below required 2048"):
+        hx.RocmDevice.try_acquire_device("test", hx.DevicePreference.LowPower, [hx.DeviceFeature.ShaderF64],
+                                         hx.DeviceLimits(max_compute_invocations_per_workgroup=2048))
+    devices = hx.RocmDevice.try_acquire_devices("test", 8)
+    assert 1 <= len(devices) <= hx.RocmDevice.device_count()
+    for d in devices:
+        d.close()
