@@ -9,7 +9,16 @@ been built (`python -m hephaestus_amd.build`); importing an operation without
 it raises ImportError.
 """
 from . import _ffi, errors
-from .device import DeviceFeature, DeviceLimits, DevicePreference, Event, RocmBuffer, RocmDevice, Topology
+from .device import (
+    DeviceFeature,
+    DeviceLimits,
+    DevicePreference,
+    Event,
+    PlacementHint,
+    RocmBuffer,
+    RocmDevice,
+    Topology,
+)
 from .device_api import LaunchGeometry, RocmCompiledKernel
 from .errors import (
     AdapterUnavailable,

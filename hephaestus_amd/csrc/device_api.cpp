@@ -144,6 +144,9 @@ hx_status hx_kernel_launch(hx_device *dev, const hx_kernel *kernel, uint32_t gro
     if (kernel->owner != dev)
         return fail(HX_ERR_INVALID_CONFIGURATION, "kernel was compiled for another device");
     if (params == nullptr && params_bytes != 0) return fail(HX_ERR_INVALID_CONFIGURATION, "null parameter block");
+    if (params_bytes > kMaxKernargBytes)
+        return fail(HX_ERR_INVALID_CONFIGURATION, "parameter block of %llu bytes exceeds the %llu-byte argument segment",
+                    (unsigned long long)params_bytes, (unsigned long long)kMaxKernargBytes);
     if (operands == nullptr && operand_count != 0) return fail(HX_ERR_INVALID_CONFIGURATION, "null operand list");
     HX_TRY(bind_device(dev));
     // HIP reads each argument through a pointer to the slot holding it: the

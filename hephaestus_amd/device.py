@@ -91,6 +91,45 @@ class DeviceLimits:
         return cls(**{name: getattr(s, name) for name, _ in _ffi.HxDeviceLimits._fields_})
 
 
+@dataclass(frozen=True)
+class PlacementHint:
+    """A placement request (themis PlacementHint, as the reference's devices
+    read it: Current, Any, Numa(node), Domain(id) or Tier(tier)).  `tier` is
+    the memory tier's name and `host_allocatable` whether it can hold a
+    primary buffer; budget-only tiers cannot."""
+
+    kind: str = "Current"
+    value: object = None
+    host_allocatable: bool = True
+
+    @classmethod
+    def current(cls) -> "PlacementHint":
+        return cls("Current")
+
+    @classmethod
+    def any(cls) -> "PlacementHint":
+        return cls("Any")
+
+    @classmethod
+    def numa(cls, node: int) -> "PlacementHint":
+        return cls("Numa", int(node))
+
+    @classmethod
+    def domain(cls, domain) -> "PlacementHint":
+        return cls("Domain", domain)
+
+    @classmethod
+    def tier(cls, tier: str, host_allocatable: bool = True) -> "PlacementHint":
+        return cls("Tier", tier, bool(host_allocatable))
+
+    @staticmethod
+    def check_primary(hint: "PlacementHint") -> None:
+        """allocation_tier (ROCm device.rs:167-185)."""
+        if hint.kind == "Tier" and not hint.host_allocatable:
+            raise errors.AllocationFailed(
+                f"ROCm primary buffers cannot be allocated from budget-only tier {hint.value}")
+
+
 class RocmBuffer:
     """A typed, device-resident linear buffer of `len` elements."""
 
@@ -253,6 +292,21 @@ class RocmDevice:
         buf = self.alloc_uninitialized(host.dtype, host.size)
         self.write_buffer(buf, host)
         return buf
+
+    # The *_with_hint forms (core device.rs:103-143): every hint places a
+    # primary buffer in device memory, except a tier that cannot hold
+    # primary buffers (ROCm device.rs:167-185).
+    def alloc_zeroed_with_hint(self, dtype, length: int, hint: "PlacementHint") -> RocmBuffer:
+        PlacementHint.check_primary(hint)
+        return self._alloc(dtype, length, True)
+
+    def alloc_uninitialized_with_hint(self, dtype, length: int, hint: "PlacementHint") -> RocmBuffer:
+        PlacementHint.check_primary(hint)
+        return self._alloc(dtype, length, False)
+
+    def upload_with_hint(self, host, hint: "PlacementHint") -> RocmBuffer:
+        PlacementHint.check_primary(hint)
+        return self.upload(host)
 
     def write_buffer(self, buffer: RocmBuffer, host) -> None:
         host = np.ascontiguousarray(host, dtype=buffer.dtype)

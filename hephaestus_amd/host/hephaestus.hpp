@@ -23,6 +23,7 @@
 
 #include <array>
 #include <cstdint>
+#include <exception>
 #include <functional>
 #include <initializer_list>
 #include <memory>
@@ -268,22 +269,31 @@ class RocmDevice {
     // -- DeviceApi (device_api.rs:69-133) -------------------------------
     using Kernel = const hx_kernel *;
     using DevicePtr = void *;
-    // compile_cached: `source` runs only on a cache miss.
+    // compile_cached: `source` runs only on a cache miss.  An exception it
+    // throws is caught before the C ABI and rethrown here.
     Kernel compile_cached(const std::string &key, const std::string &entry,
                           const std::function<std::string()> &source) {
         struct Ctx {
             const std::function<std::string()> *source;
             std::string text;
-        } ctx{&source, {}};
+            std::exception_ptr error;
+        } ctx{&source, {}, nullptr};
         hx_kernel *k = nullptr;
-        check(hx_kernel_compile_cached(
+        const hx_status s = hx_kernel_compile_cached(
             dev_, key.data(), key.size(), entry.c_str(),
             [](void *c) -> const char * {
                 Ctx *x = static_cast<Ctx *>(c);
-                x->text = (*x->source)();
+                try {
+                    x->text = (*x->source)();
+                } catch (...) {
+                    x->error = std::current_exception();
+                    return nullptr;
+                }
                 return x->text.c_str();
             },
-            &ctx, &k));
+            &ctx, &k);
+        if (ctx.error) std::rethrow_exception(ctx.error);
+        check(s);
         return k;
     }
     template <typename T> static DevicePtr device_ptr(const RocmBuffer<T> &b) { return b.device_ptr(); }

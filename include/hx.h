@@ -517,7 +517,8 @@ typedef struct hx_kernel hx_kernel; /* owned by the device; valid until
 
 /* Returns the NUL-terminated source to compile, or NULL to fail the call.
  * Called only on a cache miss (compile_cached's `source: impl FnOnce`);
- * the text is copied before hx_kernel_compile_cached returns. */
+ * the text is copied before hx_kernel_compile_cached returns.  It must not
+ * unwind (throw or longjmp) through the library. */
 typedef const char *(*hx_kernel_source_fn)(void *ctx);
 
 /* compile_cached (device_api.rs:83-99, pipeline.rs:259-322): the kernel
@@ -536,9 +537,10 @@ hx_status hx_kernel_compile_cached(hx_device *dev, const void *key,
  * `shared_bytes` of dynamic LDS.  The argument list is the parameter block
  * (params_bytes at `params`, passed by value as the kernel's first
  * argument; omitted when params_bytes is 0) followed by each operand's
- * device address.  width 0, or a kernel compiled for another device, is
- * HX_ERR_INVALID_CONFIGURATION; the runtime's launch errors are
- * HX_ERR_DISPATCH_FAILED.  Stream-ordered on `stream`. */
+ * device address.  width 0, a parameter block over 4 KiB, or a kernel
+ * compiled for another device is HX_ERR_INVALID_CONFIGURATION; the
+ * runtime's launch errors are HX_ERR_DISPATCH_FAILED.  Stream-ordered on
+ * `stream`. */
 hx_status hx_kernel_launch(hx_device *dev, const hx_kernel *kernel,
                            uint32_t groups, uint32_t width,
                            uint32_t shared_bytes, const void *params,

@@ -222,6 +222,8 @@ def test_launch_validation(device):
     assert status == hx._ffi.INVALID_CONFIGURATION
     status = lib.hx_kernel_launch(device.handle, None, 1, 64, 0, None, 0, None, 0, None)
     assert status == hx._ffi.INVALID_CONFIGURATION
+    with pytest.raises(hx.InvalidConfiguration, match="argument segment"):
+        device.launch(k, LaunchGeometry.linear(1, 64), bytes(8192), [])
 
 
 def test_buffers_alias(device):
@@ -288,3 +290,18 @@ def test_capabilities_and_acquisition(device):
     assert 1 <= len(devices) <= hx.RocmDevice.device_count()
     for d in devices:
         d.close()
+
+
+def test_allocation_with_placement_hints(device):
+    """alloc_*_with_hint / upload_with_hint (core device.rs:103-143): every
+    hint gives device memory, a budget-only tier is AllocationFailed (ROCm
+    device.rs:167-185)."""
+    for hint in (hx.PlacementHint.current(), hx.PlacementHint.any(), hx.PlacementHint.numa(0),
+                 hx.PlacementHint.domain("gpu0"), hx.PlacementHint.tier("Device")):
+        b = device.alloc_zeroed_with_hint(np.uint32, 17, hint)
+        assert np.array_equal(device.download_owned(b), np.zeros(17, np.uint32))
+        u = device.upload_with_hint(np.arange(5, dtype=np.float32), hint)
+        assert np.array_equal(device.download_owned(u), np.arange(5, dtype=np.float32))
+        assert len(device.alloc_uninitialized_with_hint(np.int32, 3, hint)) == 3
+    with pytest.raises(hx.AllocationFailed, match="budget-only tier Pooled"):
+        device.alloc_zeroed_with_hint(np.uint32, 4, hx.PlacementHint.tier("Pooled", host_allocatable=False))
