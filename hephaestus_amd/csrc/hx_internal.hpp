@@ -182,8 +182,10 @@ struct FullReduceArgs {
     uint32_t *out_index; // u32[1] (argmax only)
 };
 uint64_t full_reduce_workspace_bytes(uint64_t n);
-hx_status launch_full_reduce(const FullReduceArgs &args, void *ws,
-                             hipStream_t stream);
+// One launch; its partials are tagged status words of `ws` (tag drawn
+// from `lb`).
+hx_status launch_full_reduce(const FullReduceArgs &args, void *ws, uint64_t ws_bytes,
+                             LookbackState &lb, hipStream_t stream);
 
 struct RowsArgs {
     hx_dtype dtype;

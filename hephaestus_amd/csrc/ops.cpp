@@ -116,7 +116,9 @@ hx_status plan_full(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
 
 struct FullPlan final : hx_plan {
     FullReduceArgs args;
-    hx_status dispatch(hipStream_t stream) override { return launch_full_reduce(args, ws, stream); }
+    hx_status dispatch(hipStream_t stream) override {
+        return launch_full_reduce(args, ws, ws_bytes, lookback, stream);
+    }
 };
 
 hx_status run_full(hx_device *dev, const FullReduceArgs &a, hipStream_t stream) {
@@ -124,7 +126,7 @@ hx_status run_full(hx_device *dev, const FullReduceArgs &a, hipStream_t stream) 
     HX_TRY(im.open(dev, stream));
     void *ws = nullptr;
     HX_TRY(im.workspace(full_reduce_workspace_bytes(a.n), &ws));
-    return launch_full_reduce(a, ws, stream);
+    return launch_full_reduce(a, ws, im.workspace_bytes(), im.lookback(), stream);
 }
 
 // ---------------------------------------------------------------- axis

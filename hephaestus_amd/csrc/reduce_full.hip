@@ -4,16 +4,22 @@
 // The reference runs a 256-lane LDS halving tree with one element per thread
 // and one launch per tree pass (crates/hephaestus-rocm/src/application/
 // reduction.rs:16-52, prepared_reduction.rs:39-132), after a strided staging
-// copy (full_reduction_seam.rs:102-120).  Here two launches do the whole
-// job and read the operand exactly once:
-//   pass 1  every block grid-strides over the operand with 16-byte loads,
-//           folds into registers (f32 sums in f64), reduces its 4 waves with
-//           xor-butterflies and writes one partial;
-//   pass 2  a one-block launch folds the partials in index order and writes
-//           the result.  (A "last block folds" single launch needs a
-//           device-scope acq_rel per block, which on multi-XCD CDNA writes
-//           back and invalidates the L2 each time: measured 2.5x slower at
-//           8192 blocks.)
+// copy (full_reduction_seam.rs:102-120).  Here ONE launch does the whole job
+// and reads the operand exactly once:
+//   * every block grid-strides over the operand with 16-byte loads, folds
+//     into registers (f32 sums in f64), reduces its 4 waves with
+//     xor-butterflies and publishes one partial;
+//   * the last block (dispatched last) gathers the partials, folds them in
+//     index order and writes the result.
+// A partial is published as self-tagged 64-bit words -- (launch tag, 32-bit
+// half of the value) -- with relaxed agent-scope stores, and the gathering
+// block accepts a partial only when every half carries this launch's tag.
+// No release/acquire pair is needed: a "last block done" counter would need
+// a device-scope acq_rel per block, which on multi-XCD CDNA writes back and
+// invalidates the L2 each time (measured 2.5x slower at 8192 blocks).  A
+// partial still missing after a long bounded wait is recomputed by the
+// gathering block from the operand, bit-identically, so the launch finishes
+// whatever the dispatch order.
 // The grid size is a function of n only, so the combination order and the
 // result bits do not depend on the GPU's CU count.
 #include "hx_device.hpp"
@@ -25,9 +31,9 @@ namespace hx {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxBlocks = 768; // 8-byte partials: 6 KiB of the 64 KiB reduce area
+constexpr int kMaxBlocks = 768; // 16-byte partial slots: 12 KiB of status words
 
-// Pass-1 grid: a function of n only (so is the combination tree), one
+// The grid: a function of n only (so is the combination tree), one
 // trip's worth (2048 elements) per block up to 768 blocks, three per CU on
 // 256 CUs.  At 2^28 f32 a sweep over 512..4096 blocks and 1/2/4 loads in
 // flight per lane put 768 blocks with two 16-byte non-temporal loads per
@@ -107,9 +113,43 @@ struct FullParams {
     float a, b;
     void *out_value;
     uint32_t *out_index;
-    WorkspaceHeader *hdr;
-    void *partials;
+    uint64_t *slots; // partial slots, PartialSlot<Acc>::kWords words per block
+    uint32_t tag;    // this launch's tag
 };
+
+// One block's partial as self-tagged words: word h = (tag << 32) | 32-bit
+// half h of the value.  Slot words start zeroed and tags are never 0, so a
+// word left by an earlier launch never reads as current.
+template <typename Acc> struct PartialSlot {
+    static_assert(sizeof(Acc) == 4 || sizeof(Acc) == 8, "partials are 32- or 64-bit");
+    static constexpr uint32_t kWords = sizeof(Acc) / 4;
+    __device__ __forceinline__ static void publish(uint64_t *w, uint32_t tag, Acc v) {
+        const uint64_t t = (uint64_t)tag << 32;
+        if constexpr (kWords == 1) {
+            st_relaxed(w, t | __builtin_bit_cast(uint32_t, v));
+        } else {
+            const uint64_t b = __builtin_bit_cast(uint64_t, v);
+            st_relaxed(&w[0], t | (b & 0xFFFFFFFFull));
+            st_relaxed(&w[1], t | (b >> 32));
+        }
+    }
+    __device__ __forceinline__ static bool read(const uint64_t *w, uint32_t tag, Acc &v) {
+        if constexpr (kWords == 1) {
+            const uint64_t a = ld_relaxed(w);
+            v = __builtin_bit_cast(Acc, (uint32_t)a);
+            return (uint32_t)(a >> 32) == tag;
+        } else {
+            const uint64_t a = ld_relaxed(&w[0]), b = ld_relaxed(&w[1]);
+            v = __builtin_bit_cast(Acc, (a & 0xFFFFFFFFull) | (b << 32));
+            return (uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag;
+        }
+    }
+};
+
+// Polls of one partial slot before the gathering block recomputes that
+// partial itself (each poll is a memory round trip plus a short sleep, so
+// this is milliseconds; partials normally land within microseconds).
+constexpr uint32_t kPollLimit = 1u << 14;
 
 template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
 template <> __device__ __forceinline__ float prologue<float, true>(float x, float a, float b) {
@@ -181,18 +221,18 @@ __device__ __forceinline__ typename P::Acc fold4(const V &v, uint64_t e, float a
     return P::combine(P::combine(a0, a1), P::combine(a2, a3));
 }
 
+// The fold of "block" vb of a G-block grid, per thread (the thread's
+// grid-stride share), before the block reduction.  The gathering block
+// calls it with another block's index to recompute a missing partial.
 // FLAT: the view is the contiguous element range [offset, offset + n).
 // UNROLL independent 16-byte loads are in flight per thread per trip; NT
 // marks them non-temporal (streamed, not kept in the caches).
-template <typename T, int K, bool AFFINE, bool FLAT, int UNROLL = 2, bool NT = true>
-__global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
-    using P = Policy<T, K>;
+template <typename P, typename T, bool AFFINE, bool FLAT, int UNROLL, bool NT>
+__device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint32_t vb, uint32_t G) {
     using Acc = typename P::Acc;
-    __shared__ Acc lds[kBlock / kWave];
-
     const uint64_t n = p.n;
-    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
+    const uint64_t tid = (uint64_t)vb * kBlock + threadIdx.x;
+    const uint64_t nthreads = (uint64_t)G * kBlock;
     Acc acc = P::identity();
 
     if constexpr (FLAT) {
@@ -226,22 +266,70 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
         for (uint64_t i = tid; i < n; i += nthreads)
             acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[strided_offset(p, i)], p.a, p.b), i));
     }
-
-    Acc part = block_reduce<P>(acc, lds);
-    if (threadIdx.x == 0) ((Acc *)p.partials)[blockIdx.x] = part;
+    return acc;
 }
 
-// Pass 2: one block folds the G partials in index order (a fixed tree, so
-// the result bits depend only on n) and writes the result.  The kernel
-// boundary orders it after pass 1; no device-scope fences are needed.
-template <typename T, int K>
-__global__ __launch_bounds__(kBlock) void full_reduce_final_kernel(FullParams p, uint32_t parts) {
+template <typename T, int K, bool AFFINE, bool FLAT, int UNROLL = 2, bool NT = true>
+__global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
     using P = Policy<T, K>;
     using Acc = typename P::Acc;
+    using Slot = PartialSlot<Acc>;
     __shared__ Acc lds[kBlock / kWave];
-    const Acc *partials = (const Acc *)p.partials;
+    __shared__ Acc vals[kMaxBlocks];
+    __shared__ uint32_t missing[kMaxBlocks / 32];
+
+    const uint32_t G = gridDim.x;
+    const uint32_t last = G - 1;
+    const Acc part = block_reduce<P>(thread_fold<P, T, AFFINE, FLAT, UNROLL, NT>(p, blockIdx.x, G), lds);
+    if (blockIdx.x != last) {
+        if (threadIdx.x == 0) Slot::publish(p.slots + (uint64_t)blockIdx.x * Slot::kWords, p.tag, part);
+        return;
+    }
+
+    // The last block gathers every partial into LDS: one round of loads for
+    // all of a thread's slots (one memory round trip in the common case),
+    // then polls only the slots still unpublished ...
+    for (uint32_t k = threadIdx.x; k < kMaxBlocks / 32; k += kBlock) missing[k] = 0u;
+    __syncthreads();
+    constexpr int kPer = kMaxBlocks / kBlock;
+    static_assert(kMaxBlocks % kBlock == 0, "whole slots per thread");
+    Acc v[kPer];
+    bool ok[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t k = threadIdx.x + (uint32_t)i * kBlock;
+        ok[i] = k >= last || Slot::read(p.slots + (uint64_t)k * Slot::kWords, p.tag, v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t k = threadIdx.x + (uint32_t)i * kBlock;
+        if (k >= last) continue;
+        uint32_t polls = 0;
+        while (!ok[i] && polls++ < kPollLimit) {
+            __builtin_amdgcn_s_sleep(2);
+            ok[i] = Slot::read(p.slots + (uint64_t)k * Slot::kWords, p.tag, v[i]);
+        }
+        if (ok[i])
+            vals[k] = v[i];
+        else
+            atomicOr(&missing[k / 32], 1u << (k % 32));
+    }
+    if (threadIdx.x == 0) vals[last] = part;
+    __syncthreads();
+    // ... recomputes any that never arrived (block-uniform loop) ...
+    for (uint32_t wd = 0; wd * 32 < last; ++wd) {
+        uint32_t m = missing[wd];
+        while (m != 0u) {
+            const uint32_t k = wd * 32 + (uint32_t)(__builtin_ctz(m));
+            m &= m - 1u;
+            const Acc v = block_reduce<P>(thread_fold<P, T, AFFINE, FLAT, UNROLL, NT>(p, k, G), lds);
+            if (threadIdx.x == 0) vals[k] = v;
+        }
+    }
+    __syncthreads();
+    // ... and folds them in index order: thread t takes t, t + 256, ...
     Acc r = P::identity();
-    for (uint32_t k = threadIdx.x; k < parts; k += kBlock) r = P::combine(r, partials[k]);
+    for (uint32_t k = threadIdx.x; k < G; k += kBlock) r = P::combine(r, vals[k]);
     r = block_reduce<P>(r, lds);
     if (threadIdx.x == 0) write_result_impl<T, K>(p, r);
 }
@@ -254,7 +342,7 @@ template <typename T, int K> __global__ void full_reduce_empty_kernel(FullParams
 }
 
 template <typename T, int K, bool AFFINE>
-hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_typed(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     FullParams p{};
     p.base = a.base;
     p.n = a.n;
@@ -268,8 +356,7 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
     p.b = a.b;
     p.out_value = a.out_value;
     p.out_index = a.out_index;
-    p.hdr = (WorkspaceHeader *)ws;
-    p.partials = (char *)ws + kWorkspaceHeader;
+    p.slots = (uint64_t *)((char *)ws + kLookbackOffset);
     if (a.n == 0) {
         if constexpr (K == kMean) {
             return fail(HX_ERR_DISPATCH_FAILED, "mean is undefined for an empty operand");
@@ -279,6 +366,10 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
         }
     }
     const uint32_t blocks = full_reduce_blocks(a.n);
+    if (ws_bytes < full_reduce_workspace_bytes(a.n))
+        return fail(HX_ERR_DISPATCH_FAILED, "full-reduction workspace of %llu bytes is below %llu",
+                    (unsigned long long)ws_bytes, (unsigned long long)full_reduce_workspace_bytes(a.n));
+    HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     if (a.flat)
         hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, true>), dim3(blocks), dim3(kBlock), 0,
                            stream, p);
@@ -286,34 +377,39 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, hipStream_t stream) {
         hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, false>), dim3(blocks), dim3(kBlock), 0,
                            stream, p);
     HX_TRY(check_launch("full_reduce_kernel"));
-    hipLaunchKernelGGL((full_reduce_final_kernel<T, K>), dim3(1), dim3(kBlock), 0, stream, p, blocks);
-    return check_launch("full_reduce_final_kernel");
+    commit_lookback_launch(lb);
+    return HX_OK;
 }
 
 template <typename T, bool AFFINE>
-hx_status launch_kind(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_kind(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     switch (a.op) {
-    case HX_OP_SUM: return launch_typed<T, kSum, AFFINE>(a, ws, stream);
-    case HX_OP_PROD: return launch_typed<T, kProd, AFFINE>(a, ws, stream);
-    case HX_OP_MIN: return launch_typed<T, kMin, AFFINE>(a, ws, stream);
-    case HX_OP_MAX: return launch_typed<T, kMax, AFFINE>(a, ws, stream);
-    case HX_OP_ARGMAX: return launch_typed<T, kArgmax, AFFINE>(a, ws, stream);
-    case HX_OP_MEAN: return launch_typed<T, kMean, AFFINE>(a, ws, stream);
+    case HX_OP_SUM: return launch_typed<T, kSum, AFFINE>(a, ws, ws_bytes, lb, stream);
+    case HX_OP_PROD: return launch_typed<T, kProd, AFFINE>(a, ws, ws_bytes, lb, stream);
+    case HX_OP_MIN: return launch_typed<T, kMin, AFFINE>(a, ws, ws_bytes, lb, stream);
+    case HX_OP_MAX: return launch_typed<T, kMax, AFFINE>(a, ws, ws_bytes, lb, stream);
+    case HX_OP_ARGMAX: return launch_typed<T, kArgmax, AFFINE>(a, ws, ws_bytes, lb, stream);
+    case HX_OP_MEAN: return launch_typed<T, kMean, AFFINE>(a, ws, ws_bytes, lb, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown reduction operator %d", (int)a.op);
 }
 
 } // namespace
 
-uint64_t full_reduce_workspace_bytes(uint64_t) { return kWorkspaceHeader + kReduceArea; }
+// Two 64-bit slot words per block (the widest partial) after the header
+// and reduce area, where every tagged status word of a workspace lives.
+uint64_t full_reduce_workspace_bytes(uint64_t n) {
+    return kLookbackOffset + (uint64_t)full_reduce_blocks(n) * 16;
+}
 
-hx_status launch_full_reduce(const FullReduceArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_full_reduce(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb,
+                             hipStream_t stream) {
     switch (a.dtype) {
     case HX_DTYPE_F32:
-        return a.affine ? launch_kind<float, true>(a, ws, stream)
-                        : launch_kind<float, false>(a, ws, stream);
-    case HX_DTYPE_U32: return launch_kind<uint32_t, false>(a, ws, stream);
-    case HX_DTYPE_I32: return launch_kind<int32_t, false>(a, ws, stream);
+        return a.affine ? launch_kind<float, true>(a, ws, ws_bytes, lb, stream)
+                        : launch_kind<float, false>(a, ws, ws_bytes, lb, stream);
+    case HX_DTYPE_U32: return launch_kind<uint32_t, false>(a, ws, ws_bytes, lb, stream);
+    case HX_DTYPE_I32: return launch_kind<int32_t, false>(a, ws, ws_bytes, lb, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown dtype %d", (int)a.dtype);
 }
