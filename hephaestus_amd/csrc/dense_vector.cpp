@@ -71,7 +71,9 @@ hx_status plan_map(hx_map_reduction map, hx_dtype dtype, const void *a, uint64_t
 
 struct MapPlan final : hx_plan {
     MapReduceArgs args;
-    hx_status dispatch(hipStream_t stream) override { return launch_map_reduce(args, ws, stream); }
+    hx_status dispatch(hipStream_t stream) override {
+        return launch_map_reduce(args, ws, ws_bytes, lookback, stream);
+    }
 };
 
 hx_status run_map(hx_device *dev, const MapReduceArgs &a, hipStream_t stream) {
@@ -79,7 +81,7 @@ hx_status run_map(hx_device *dev, const MapReduceArgs &a, hipStream_t stream) {
     HX_TRY(im.open(dev, stream));
     void *ws = nullptr;
     HX_TRY(im.workspace(map_reduce_workspace_bytes(a.n), &ws));
-    return launch_map_reduce(a, ws, stream);
+    return launch_map_reduce(a, ws, im.workspace_bytes(), im.lookback(), stream);
 }
 
 hx_status check_f32_vector(hx_dtype dtype) {

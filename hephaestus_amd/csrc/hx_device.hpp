@@ -366,6 +366,98 @@ __device__ __forceinline__ double ld_relaxed_f64(const double *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ----------------------------------------------- single-launch grid folds
+// A grid reduction in one launch: every block but the last publishes its
+// partial as self-tagged words (word h = (tag << 32) | 32-bit half h of the
+// value) with relaxed agent-scope stores; the last block -- dispatched last
+// -- gathers them.  A reader accepts a partial only when every half carries
+// this launch's tag, so no release/acquire pair (which on multi-XCD CDNA
+// writes back and invalidates the L2) is needed.  Slot words start zeroed
+// and tags are never 0.
+template <typename Acc> struct PartialSlot {
+    static_assert(sizeof(Acc) == 4 || sizeof(Acc) == 8, "partials are 32- or 64-bit");
+    static constexpr uint32_t kWords = sizeof(Acc) / 4;
+    __device__ __forceinline__ static void publish(uint64_t *w, uint32_t tag, Acc v) {
+        const uint64_t t = (uint64_t)tag << 32;
+        if constexpr (kWords == 1) {
+            st_relaxed(w, t | __builtin_bit_cast(uint32_t, v));
+        } else {
+            const uint64_t b = __builtin_bit_cast(uint64_t, v);
+            st_relaxed(&w[0], t | (b & 0xFFFFFFFFull));
+            st_relaxed(&w[1], t | (b >> 32));
+        }
+    }
+    __device__ __forceinline__ static bool read(const uint64_t *w, uint32_t tag, Acc &v) {
+        if constexpr (kWords == 1) {
+            const uint64_t a = ld_relaxed(w);
+            v = __builtin_bit_cast(Acc, (uint32_t)a);
+            return (uint32_t)(a >> 32) == tag;
+        } else {
+            const uint64_t a = ld_relaxed(&w[0]), b = ld_relaxed(&w[1]);
+            v = __builtin_bit_cast(Acc, (a & 0xFFFFFFFFull) | (b << 32));
+            return (uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag;
+        }
+    }
+};
+
+// Polls of one slot before the gathering block recomputes that partial
+// itself (each poll is a memory round trip plus a short sleep, so this is
+// milliseconds; partials normally land within microseconds).
+constexpr uint32_t kGatherPollLimit = 1u << 14;
+
+// Run by every thread of the last block of a G-block grid (G <= MAXP) once
+// its own partial `own` is known: leaves partial k of every block in
+// vals[k] (LDS).  Each thread loads its slots (t, t + BLOCK, ...) in one
+// round -- one memory round trip in the common case -- then polls those
+// still unpublished.  A partial missing after kGatherPollLimit polls is
+// recomputed by `recompute(k)`, a block-uniform call that returns block k's
+// partial with the streaming code, so the value is bit-identical and the
+// launch finishes whatever the dispatch order.  `missing` is MAXP / 32
+// words of LDS.
+template <int BLOCK, int MAXP, typename Acc, typename Recompute>
+__device__ __forceinline__ void gather_partials(const uint64_t *slots, uint32_t tag, uint32_t G, Acc own,
+                                                Acc *vals, uint32_t *missing, Recompute &&recompute) {
+    using Slot = PartialSlot<Acc>;
+    constexpr int kPer = MAXP / BLOCK;
+    static_assert(MAXP % BLOCK == 0 && MAXP % 32 == 0, "whole slots per thread");
+    const uint32_t last = G - 1;
+    for (uint32_t k = threadIdx.x; k < MAXP / 32; k += BLOCK) missing[k] = 0u;
+    __syncthreads();
+    Acc v[kPer];
+    bool ok[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t k = threadIdx.x + (uint32_t)i * BLOCK;
+        ok[i] = k >= last || Slot::read(slots + (uint64_t)k * Slot::kWords, tag, v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t k = threadIdx.x + (uint32_t)i * BLOCK;
+        if (k >= last) continue;
+        uint32_t polls = 0;
+        while (!ok[i] && polls++ < kGatherPollLimit) {
+            __builtin_amdgcn_s_sleep(2);
+            ok[i] = Slot::read(slots + (uint64_t)k * Slot::kWords, tag, v[i]);
+        }
+        if (ok[i])
+            vals[k] = v[i];
+        else
+            atomicOr(&missing[k / 32], 1u << (k % 32));
+    }
+    if (threadIdx.x == 0) vals[last] = own;
+    __syncthreads();
+    for (uint32_t wd = 0; wd * 32 < last; ++wd) {
+        uint32_t m = missing[wd];
+        while (m != 0u) {
+            const uint32_t k = wd * 32 + (uint32_t)__builtin_ctz(m);
+            m &= m - 1u;
+            const Acc r = recompute(k);
+            if (threadIdx.x == 0) vals[k] = r;
+        }
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------ generator
 // SplitMix64 (Steele, Lea, Flood, "Fast splittable pseudorandom number
 // generators", OOPSLA 2014): output i for seed s is mix(s + (i+1)*gamma).

@@ -123,16 +123,12 @@ bool layout_is_permuted_dense(const hx_layout &l);
 hx_status layout_basic_check(const hx_layout *l, const char *what);
 
 // ----------------------------------------------------------- workspace
-// Header of every workspace (256 bytes), followed by the full-reduce
-// partials area (64 KiB) and then the look-back status words.
-struct WorkspaceHeader {
-    uint32_t reserved[4]; // unused
-    uint32_t pad1[60];
-};
-static_assert(sizeof(WorkspaceHeader) == 256, "workspace header is 256 bytes");
+// Every workspace: a reserved 256-byte header, then the tagged status words
+// (look-back statuses of the scans and the segmented sum, partial slots of
+// the single-launch grid folds), all tagged from the workspace's one
+// LookbackState.
 constexpr uint64_t kWorkspaceHeader = 256;
-constexpr uint64_t kReduceArea = 64 * 1024;
-constexpr uint64_t kLookbackOffset = kWorkspaceHeader + kReduceArea;
+constexpr uint64_t kLookbackOffset = kWorkspaceHeader;
 
 hx_status alloc_workspace(hx_device *dev, uint64_t bytes, void **ws);
 
@@ -275,7 +271,10 @@ struct MapReduceArgs {
     void *out;
 };
 uint64_t map_reduce_workspace_bytes(uint64_t n);
-hx_status launch_map_reduce(const MapReduceArgs &args, void *ws, hipStream_t stream);
+// One launch; its partials are tagged status words of `ws` (tag drawn
+// from `lb`).
+hx_status launch_map_reduce(const MapReduceArgs &args, void *ws, uint64_t ws_bytes, LookbackState &lb,
+                            hipStream_t stream);
 
 // Elementwise f32 vector forms: out[i] = op(t[i], s[i], factor).
 hx_status launch_vector_op(hx_vector_op op, const float *t, const float *s, float *out, uint64_t n,

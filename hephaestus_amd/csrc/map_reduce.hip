@@ -5,13 +5,15 @@
 // The reference maps and reduces one element per thread in a 256-wide LDS
 // halving tree, one launch per tree pass, and takes the L2 square root in a
 // further elementwise launch (norms.rs:466-477).  Here the map is fused into
-// the same two-launch grid reduction as the full reduce:
-//   pass 1  every block grid-strides over the operand(s) with 16-byte loads
-//           (both operands of a dot when their alignment agrees), maps each
-//           element, accumulates (f32 sums in f64: products and squares of
-//           f32 values are exact in f64) and writes one partial;
-//   pass 2  one block folds the partials in index order and writes the
-//           scalar, taking the square root of an L2 norm in the same launch.
+// the same single-launch grid reduction as the full reduce:
+//   * every block grid-strides over the operand(s) with 16-byte loads
+//     (both operands of a dot when their alignment agrees), maps each
+//     element, accumulates (f32 sums in f64: products and squares of f32
+//     values are exact in f64) and publishes one partial as tagged slot
+//     words (PartialSlot);
+//   * the last block gathers the partials (gather_partials), folds them in
+//     index order and writes the scalar, taking the square root of an L2
+//     norm in the same launch.
 // Integer sums and products wrap mod 2^32; |INT_MIN| is INT_MIN, as abs()
 // on a two's-complement int.
 #include "hx_device.hpp"
@@ -76,7 +78,8 @@ struct MapParams {
     uint64_t shape[4];
     int64_t a_strides[4], b_strides[4];
     void *out;
-    void *partials;
+    uint64_t *slots; // partial slots (PartialSlot), 16 bytes per block
+    uint32_t tag;    // this launch's tag
 };
 
 __device__ __forceinline__ void strided_pair(const MapParams &p, uint64_t i, int64_t &oa, int64_t &ob) {
@@ -99,6 +102,7 @@ template <typename P> __device__ __forceinline__ typename P::Acc block_reduce(ty
     typename P::Acc r = lds[0];
 #pragma unroll
     for (int k = 1; k < kBlock / kWave; ++k) r = P::combine(r, lds[k]);
+    __syncthreads(); // lds is reused by the next reduction
     return r;
 }
 
@@ -106,16 +110,18 @@ template <typename P> __device__ __forceinline__ typename P::Acc block_reduce(ty
 // (b is ignored for one-operand maps).  The head peel aligns a; b's vectors
 // need only 4-byte alignment (Vec4A4), so the operands may sit at any element
 // offsets from each other.
+// map_thread_fold: the fold of thread threadIdx.x of "block" vb of a
+// G-block grid (the last block calls it with another block's index to
+// recompute a missing partial).
 template <typename T, int M, bool FLAT>
-__global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
+__device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const MapParams &p, uint32_t vb, uint32_t G) {
     using P = MapPolicy<T, M>;
     using Acc = typename P::Acc;
     using V = typename Vec4A4<T>::type;
     constexpr bool kTwo = M == kMapDot;
-    __shared__ Acc lds[kBlock / kWave];
     const uint64_t n = p.n;
-    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
+    const uint64_t tid = (uint64_t)vb * kBlock + threadIdx.x;
+    const uint64_t nthreads = (uint64_t)G * kBlock;
     Acc acc = P::identity();
     if constexpr (FLAT) {
         const T *a = (const T *)p.a + p.a_off;
@@ -158,8 +164,7 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
             acc = P::combine(acc, P::elem(a[oa], kTwo ? b[ob] : a[oa]));
         }
     }
-    const Acc part = block_reduce<P>(acc, lds);
-    if (threadIdx.x == 0) ((Acc *)p.partials)[blockIdx.x] = part;
+    return acc;
 }
 
 template <typename T, int M> __device__ __forceinline__ void write_map_result(const MapParams &p, typename MapPolicy<T, M>::Acc r) {
@@ -172,14 +177,25 @@ template <typename T, int M> __device__ __forceinline__ void write_map_result(co
     }
 }
 
-template <typename T, int M>
-__global__ __launch_bounds__(kBlock) void map_reduce_final_kernel(MapParams p, uint32_t parts) {
+template <typename T, int M, bool FLAT>
+__global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
     using P = MapPolicy<T, M>;
     using Acc = typename P::Acc;
+    using Slot = PartialSlot<Acc>;
     __shared__ Acc lds[kBlock / kWave];
-    const Acc *partials = (const Acc *)p.partials;
+    __shared__ Acc vals[kMaxBlocks];
+    __shared__ uint32_t missing[kMaxBlocks / 32];
+    const uint32_t G = gridDim.x;
+    const Acc part = block_reduce<P>(map_thread_fold<T, M, FLAT>(p, blockIdx.x, G), lds);
+    if (blockIdx.x + 1 != G) {
+        if (threadIdx.x == 0) Slot::publish(p.slots + (uint64_t)blockIdx.x * Slot::kWords, p.tag, part);
+        return;
+    }
+    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, G, part, vals, missing, [&](uint32_t k) {
+        return block_reduce<P>(map_thread_fold<T, M, FLAT>(p, k, G), lds);
+    });
     Acc r = P::identity();
-    for (uint32_t k = threadIdx.x; k < parts; k += kBlock) r = P::combine(r, partials[k]);
+    for (uint32_t k = threadIdx.x; k < G; k += kBlock) r = P::combine(r, vals[k]);
     r = block_reduce<P>(r, lds);
     if (threadIdx.x == 0) write_map_result<T, M>(p, r);
 }
@@ -194,7 +210,8 @@ uint32_t map_blocks(uint64_t n) {
     return blocks < 1 ? 1u : (uint32_t)blocks;
 }
 
-template <typename T, int M> hx_status launch_typed(const MapReduceArgs &a, void *ws, hipStream_t stream) {
+template <typename T, int M>
+hx_status launch_typed(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     MapParams p{};
     p.a = a.a;
     p.b = a.b;
@@ -208,41 +225,49 @@ template <typename T, int M> hx_status launch_typed(const MapReduceArgs &a, void
         p.b_strides[d] = d < a.b_layout.rank ? a.b_layout.strides[d] : 0;
     }
     p.out = a.out;
-    p.partials = (char *)ws + kWorkspaceHeader;
+    p.slots = (uint64_t *)((char *)ws + kLookbackOffset);
     if (a.n == 0) {
         hipLaunchKernelGGL((map_reduce_empty_kernel<T, M>), dim3(1), dim3(64), 0, stream, p);
         return check_launch("map_reduce_empty_kernel");
     }
     const uint32_t blocks = map_blocks(a.n);
+    if (ws_bytes < map_reduce_workspace_bytes(a.n))
+        return fail(HX_ERR_DISPATCH_FAILED, "map-reduction workspace of %llu bytes is below %llu",
+                    (unsigned long long)ws_bytes, (unsigned long long)map_reduce_workspace_bytes(a.n));
+    HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     if (a.flat)
         hipLaunchKernelGGL((map_reduce_kernel<T, M, true>), dim3(blocks), dim3(kBlock), 0, stream, p);
     else
         hipLaunchKernelGGL((map_reduce_kernel<T, M, false>), dim3(blocks), dim3(kBlock), 0, stream, p);
     HX_TRY(check_launch("map_reduce_kernel"));
-    hipLaunchKernelGGL((map_reduce_final_kernel<T, M>), dim3(1), dim3(kBlock), 0, stream, p, blocks);
-    return check_launch("map_reduce_final_kernel");
+    commit_lookback_launch(lb);
+    return HX_OK;
 }
 
-template <typename T> hx_status launch_kind(const MapReduceArgs &a, void *ws, hipStream_t stream) {
+template <typename T>
+hx_status launch_kind(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb, hipStream_t stream) {
     switch (a.map) {
-    case HX_MAP_SUM: return launch_typed<T, kMapSum>(a, ws, stream);
-    case HX_MAP_DOT: return launch_typed<T, kMapDot>(a, ws, stream);
-    case HX_MAP_NORM_L1: return launch_typed<T, kMapAbsSum>(a, ws, stream);
-    case HX_MAP_NORM_L2: return launch_typed<T, kMapSquareSum>(a, ws, stream);
-    case HX_MAP_NORM_MAX: return launch_typed<T, kMapAbsMax>(a, ws, stream);
+    case HX_MAP_SUM: return launch_typed<T, kMapSum>(a, ws, ws_bytes, lb, stream);
+    case HX_MAP_DOT: return launch_typed<T, kMapDot>(a, ws, ws_bytes, lb, stream);
+    case HX_MAP_NORM_L1: return launch_typed<T, kMapAbsSum>(a, ws, ws_bytes, lb, stream);
+    case HX_MAP_NORM_L2: return launch_typed<T, kMapSquareSum>(a, ws, ws_bytes, lb, stream);
+    case HX_MAP_NORM_MAX: return launch_typed<T, kMapAbsMax>(a, ws, ws_bytes, lb, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown map-reduction %d", (int)a.map);
 }
 
 } // namespace
 
-uint64_t map_reduce_workspace_bytes(uint64_t) { return kWorkspaceHeader + (uint64_t)kMaxBlocks * 8; }
+// Two 64-bit slot words per block after the header, where every tagged
+// status word of a workspace lives.
+uint64_t map_reduce_workspace_bytes(uint64_t n) { return kLookbackOffset + (uint64_t)map_blocks(n) * 16; }
 
-hx_status launch_map_reduce(const MapReduceArgs &a, void *ws, hipStream_t stream) {
+hx_status launch_map_reduce(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb,
+                            hipStream_t stream) {
     switch (a.dtype) {
-    case HX_DTYPE_F32: return launch_kind<float>(a, ws, stream);
-    case HX_DTYPE_U32: return launch_kind<uint32_t>(a, ws, stream);
-    case HX_DTYPE_I32: return launch_kind<int32_t>(a, ws, stream);
+    case HX_DTYPE_F32: return launch_kind<float>(a, ws, ws_bytes, lb, stream);
+    case HX_DTYPE_U32: return launch_kind<uint32_t>(a, ws, ws_bytes, lb, stream);
+    case HX_DTYPE_I32: return launch_kind<int32_t>(a, ws, ws_bytes, lb, stream);
     }
     return fail(HX_ERR_INVALID_CONFIGURATION, "unknown dtype %d", (int)a.dtype);
 }

@@ -113,43 +113,9 @@ struct FullParams {
     float a, b;
     void *out_value;
     uint32_t *out_index;
-    uint64_t *slots; // partial slots, PartialSlot<Acc>::kWords words per block
+    uint64_t *slots; // partial slots (PartialSlot), 16 bytes per block
     uint32_t tag;    // this launch's tag
 };
-
-// One block's partial as self-tagged words: word h = (tag << 32) | 32-bit
-// half h of the value.  Slot words start zeroed and tags are never 0, so a
-// word left by an earlier launch never reads as current.
-template <typename Acc> struct PartialSlot {
-    static_assert(sizeof(Acc) == 4 || sizeof(Acc) == 8, "partials are 32- or 64-bit");
-    static constexpr uint32_t kWords = sizeof(Acc) / 4;
-    __device__ __forceinline__ static void publish(uint64_t *w, uint32_t tag, Acc v) {
-        const uint64_t t = (uint64_t)tag << 32;
-        if constexpr (kWords == 1) {
-            st_relaxed(w, t | __builtin_bit_cast(uint32_t, v));
-        } else {
-            const uint64_t b = __builtin_bit_cast(uint64_t, v);
-            st_relaxed(&w[0], t | (b & 0xFFFFFFFFull));
-            st_relaxed(&w[1], t | (b >> 32));
-        }
-    }
-    __device__ __forceinline__ static bool read(const uint64_t *w, uint32_t tag, Acc &v) {
-        if constexpr (kWords == 1) {
-            const uint64_t a = ld_relaxed(w);
-            v = __builtin_bit_cast(Acc, (uint32_t)a);
-            return (uint32_t)(a >> 32) == tag;
-        } else {
-            const uint64_t a = ld_relaxed(&w[0]), b = ld_relaxed(&w[1]);
-            v = __builtin_bit_cast(Acc, (a & 0xFFFFFFFFull) | (b << 32));
-            return (uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag;
-        }
-    }
-};
-
-// Polls of one partial slot before the gathering block recomputes that
-// partial itself (each poll is a memory round trip plus a short sleep, so
-// this is milliseconds; partials normally land within microseconds).
-constexpr uint32_t kPollLimit = 1u << 14;
 
 template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
 template <> __device__ __forceinline__ float prologue<float, true>(float x, float a, float b) {
@@ -286,47 +252,10 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
         return;
     }
 
-    // The last block gathers every partial into LDS: one round of loads for
-    // all of a thread's slots (one memory round trip in the common case),
-    // then polls only the slots still unpublished ...
-    for (uint32_t k = threadIdx.x; k < kMaxBlocks / 32; k += kBlock) missing[k] = 0u;
-    __syncthreads();
-    constexpr int kPer = kMaxBlocks / kBlock;
-    static_assert(kMaxBlocks % kBlock == 0, "whole slots per thread");
-    Acc v[kPer];
-    bool ok[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const uint32_t k = threadIdx.x + (uint32_t)i * kBlock;
-        ok[i] = k >= last || Slot::read(p.slots + (uint64_t)k * Slot::kWords, p.tag, v[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const uint32_t k = threadIdx.x + (uint32_t)i * kBlock;
-        if (k >= last) continue;
-        uint32_t polls = 0;
-        while (!ok[i] && polls++ < kPollLimit) {
-            __builtin_amdgcn_s_sleep(2);
-            ok[i] = Slot::read(p.slots + (uint64_t)k * Slot::kWords, p.tag, v[i]);
-        }
-        if (ok[i])
-            vals[k] = v[i];
-        else
-            atomicOr(&missing[k / 32], 1u << (k % 32));
-    }
-    if (threadIdx.x == 0) vals[last] = part;
-    __syncthreads();
-    // ... recomputes any that never arrived (block-uniform loop) ...
-    for (uint32_t wd = 0; wd * 32 < last; ++wd) {
-        uint32_t m = missing[wd];
-        while (m != 0u) {
-            const uint32_t k = wd * 32 + (uint32_t)(__builtin_ctz(m));
-            m &= m - 1u;
-            const Acc v = block_reduce<P>(thread_fold<P, T, AFFINE, FLAT, UNROLL, NT>(p, k, G), lds);
-            if (threadIdx.x == 0) vals[k] = v;
-        }
-    }
-    __syncthreads();
+    // The last block gathers every partial into LDS ...
+    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, G, part, vals, missing, [&](uint32_t k) {
+        return block_reduce<P>(thread_fold<P, T, AFFINE, FLAT, UNROLL, NT>(p, k, G), lds);
+    });
     // ... and folds them in index order: thread t takes t, t + 256, ...
     Acc r = P::identity();
     for (uint32_t k = threadIdx.x; k < G; k += kBlock) r = P::combine(r, vals[k]);
@@ -396,8 +325,8 @@ hx_status launch_kind(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Look
 
 } // namespace
 
-// Two 64-bit slot words per block (the widest partial) after the header
-// and reduce area, where every tagged status word of a workspace lives.
+// Two 64-bit slot words per block (the widest partial) after the header,
+// where every tagged status word of a workspace lives.
 uint64_t full_reduce_workspace_bytes(uint64_t n) {
     return kLookbackOffset + (uint64_t)full_reduce_blocks(n) * 16;
 }
