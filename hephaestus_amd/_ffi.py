@@ -155,6 +155,7 @@ SIGNATURES = {
     "hx_scan": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_scan_noalloc": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_noalloc_scratch_bytes": (U64, []),
+    "hx_debug_set_wait_limits": (I32, [U32, U32]),
     "hx_prepare_scan": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, POINTER(P)]),
     "hx_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),
     "hx_prepare_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, POINTER(P)]),

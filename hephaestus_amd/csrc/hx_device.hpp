@@ -400,23 +400,21 @@ template <typename Acc> struct PartialSlot {
     }
 };
 
-// Polls of one slot before the gathering block recomputes that partial
-// itself (each poll is a memory round trip plus a short sleep, so this is
-// milliseconds; partials normally land within microseconds).
-constexpr uint32_t kGatherPollLimit = 1u << 14;
-
 // Run by every thread of the last block of a G-block grid (G <= MAXP) once
 // its own partial `own` is known: leaves partial k of every block in
 // vals[k] (LDS).  Each thread loads its slots (t, t + BLOCK, ...) in one
 // round -- one memory round trip in the common case -- then polls those
-// still unpublished.  A partial missing after kGatherPollLimit polls is
+// still unpublished.  A partial missing after `poll_limit` polls (16384 by
+// default: each poll is a memory round trip plus a short sleep, so that is
+// milliseconds, while partials normally land within microseconds) is
 // recomputed by `recompute(k)`, a block-uniform call that returns block k's
 // partial with the streaming code, so the value is bit-identical and the
-// launch finishes whatever the dispatch order.  `missing` is MAXP / 32
-// words of LDS.
+// launch finishes whatever the dispatch order.  poll_limit 0 skips the
+// slots and recomputes every partial (a test of that path).  `missing` is
+// MAXP / 32 words of LDS.
 template <int BLOCK, int MAXP, typename Acc, typename Recompute>
-__device__ __forceinline__ void gather_partials(const uint64_t *slots, uint32_t tag, uint32_t G, Acc own,
-                                                Acc *vals, uint32_t *missing, Recompute &&recompute) {
+__device__ __forceinline__ void gather_partials(const uint64_t *slots, uint32_t tag, uint32_t poll_limit, uint32_t G,
+                                                Acc own, Acc *vals, uint32_t *missing, Recompute &&recompute) {
     using Slot = PartialSlot<Acc>;
     constexpr int kPer = MAXP / BLOCK;
     static_assert(MAXP % BLOCK == 0 && MAXP % 32 == 0, "whole slots per thread");
@@ -428,14 +426,14 @@ __device__ __forceinline__ void gather_partials(const uint64_t *slots, uint32_t 
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const uint32_t k = threadIdx.x + (uint32_t)i * BLOCK;
-        ok[i] = k >= last || Slot::read(slots + (uint64_t)k * Slot::kWords, tag, v[i]);
+        ok[i] = k >= last || (poll_limit != 0 && Slot::read(slots + (uint64_t)k * Slot::kWords, tag, v[i]));
     }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const uint32_t k = threadIdx.x + (uint32_t)i * BLOCK;
         if (k >= last) continue;
         uint32_t polls = 0;
-        while (!ok[i] && polls++ < kGatherPollLimit) {
+        while (!ok[i] && polls++ < poll_limit) {
             __builtin_amdgcn_s_sleep(2);
             ok[i] = Slot::read(slots + (uint64_t)k * Slot::kWords, tag, v[i]);
         }

@@ -158,6 +158,12 @@ private:
 
 // Tag for the next look-back launch on a workspace of `ws_bytes`; clears the
 // status area when the 30-bit tag space wraps.
+// Poll limits of the bounded waits (hx_debug_set_wait_limits): look-back
+// polls before a waiter computes a missing predecessor, and gather polls per
+// partial before the gathering block recomputes it (0: recompute all).
+uint32_t lookback_poll_limit();
+uint32_t gather_poll_limit();
+
 hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
                                hipStream_t stream, uint32_t *tag);
 void commit_lookback_launch(LookbackState &st);

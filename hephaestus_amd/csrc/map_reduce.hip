@@ -79,7 +79,8 @@ struct MapParams {
     int64_t a_strides[4], b_strides[4];
     void *out;
     uint64_t *slots; // partial slots (PartialSlot), 16 bytes per block
-    uint32_t tag;    // this launch's tag
+    uint32_t tag;        // this launch's tag
+    uint32_t poll_limit; // gather polls per partial before recomputing it
 };
 
 __device__ __forceinline__ void strided_pair(const MapParams &p, uint64_t i, int64_t &oa, int64_t &ob) {
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
         if (threadIdx.x == 0) Slot::publish(p.slots + (uint64_t)blockIdx.x * Slot::kWords, p.tag, part);
         return;
     }
-    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, G, part, vals, missing, [&](uint32_t k) {
+    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, p.poll_limit, G, part, vals, missing, [&](uint32_t k) {
         return block_reduce<P>(map_thread_fold<T, M, FLAT>(p, k, G), lds);
     });
     Acc r = P::identity();
@@ -226,6 +227,7 @@ hx_status launch_typed(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, Look
     }
     p.out = a.out;
     p.slots = (uint64_t *)((char *)ws + kLookbackOffset);
+    p.poll_limit = gather_poll_limit();
     if (a.n == 0) {
         hipLaunchKernelGGL((map_reduce_empty_kernel<T, M>), dim3(1), dim3(64), 0, stream, p);
         return check_launch("map_reduce_empty_kernel");

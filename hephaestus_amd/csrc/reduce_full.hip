@@ -114,7 +114,8 @@ struct FullParams {
     void *out_value;
     uint32_t *out_index;
     uint64_t *slots; // partial slots (PartialSlot), 16 bytes per block
-    uint32_t tag;    // this launch's tag
+    uint32_t tag;        // this launch's tag
+    uint32_t poll_limit; // gather polls per partial before recomputing it
 };
 
 template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
     }
 
     // The last block gathers every partial into LDS ...
-    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, G, part, vals, missing, [&](uint32_t k) {
+    gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, p.poll_limit, G, part, vals, missing, [&](uint32_t k) {
         return block_reduce<P>(thread_fold<P, T, AFFINE, FLAT, UNROLL, NT>(p, k, G), lds);
     });
     // ... and folds them in index order: thread t takes t, t + 256, ...
@@ -286,6 +287,7 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Loo
     p.out_value = a.out_value;
     p.out_index = a.out_index;
     p.slots = (uint64_t *)((char *)ws + kLookbackOffset);
+    p.poll_limit = gather_poll_limit();
     if (a.n == 0) {
         if constexpr (K == kMean) {
             return fail(HX_ERR_DISPATCH_FAILED, "mean is undefined for an empty operand");

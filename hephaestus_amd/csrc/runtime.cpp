@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <new>
 
@@ -168,6 +169,14 @@ hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
 
 void commit_lookback_launch(LookbackState &st) { st.launches += 1u; }
 
+namespace {
+std::atomic<uint32_t> g_lookback_polls{64};
+std::atomic<uint32_t> g_gather_polls{1u << 14};
+} // namespace
+
+uint32_t lookback_poll_limit() { return g_lookback_polls.load(std::memory_order_relaxed); }
+uint32_t gather_poll_limit() { return g_gather_polls.load(std::memory_order_relaxed); }
+
 } // namespace hx
 
 hx_plan::~hx_plan() {
@@ -182,6 +191,12 @@ using namespace hx;
 extern "C" {
 
 uint32_t hx_abi_version(void) { return HX_ABI_VERSION; }
+
+hx_status hx_debug_set_wait_limits(uint32_t lookback_polls, uint32_t gather_polls) {
+    g_lookback_polls.store(lookback_polls, std::memory_order_relaxed);
+    g_gather_polls.store(gather_polls, std::memory_order_relaxed);
+    return ok();
+}
 
 const char *hx_status_name(hx_status status) {
     switch (status) {

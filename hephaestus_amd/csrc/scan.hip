@@ -26,7 +26,7 @@
 // reach a published prefix; the two levels need about two.
 //
 // Forward progress does not depend on the order in which the hardware
-// dispatches blocks: when a status stays unpublished for kSpinLimit polls
+// dispatches blocks: when a status stays unpublished for p.spin_limit polls
 // (its block may not be running yet), the waiting wave computes the missing
 // value itself -- a tile aggregate from the input with the owner's
 // arithmetic, a superblock value from its tiles' statuses -- and publishes
@@ -53,7 +53,6 @@ constexpr int kWaves = 8;                            // waves per tile block (lo
 constexpr int kSteps = 16;                           // 16-byte vectors per lane (long lines)
 constexpr int kSuper = 64;                           // tiles per superblock
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
-constexpr uint32_t kSpinLimit = 64; // polls before computing a missing value
 
 __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
     return ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v;
@@ -169,7 +168,8 @@ struct ScanParams {
     int64_t in_line_stride, in_elem_stride;
     int64_t out_line_stride, out_elem_stride;
     uint64_t in_offset, out_offset;
-    uint32_t tag; // this launch's status tag
+    uint32_t tag;        // this launch's status tag
+    uint32_t spin_limit; // polls before a waiter computes a missing value (64)
 };
 
 // The four elements of one lane and step (logical index e..e+3 of the
@@ -268,7 +268,7 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
         const uint64_t missing = im & need;
         if (missing == 0ull) break;
         hook.poll();
-        if (++spins >= kSpinLimit) {
+        if (++spins >= p.spin_limit) {
             const uint64_t u = tile_end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
             const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS, WAVES>(p, u);
             if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
@@ -325,7 +325,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
             const uint64_t missing = im & need;
             if (missing == 0ull) break;
             hook.poll();
-            if (++spins >= kSpinLimit) {
+            if (++spins >= p.spin_limit) {
                 // Rebuild the missing superblock's value from its 64 tiles:
                 // an inclusive prefix if one of them has one, else the sum.
                 const uint64_t s = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
@@ -939,7 +939,7 @@ __global__ __launch_bounds__(kBlock) void col_narrow_scan_kernel(ScanParams p,
 // Data and look-back waves run separate code paths (wave-uniform), so the
 // tile's registers are not live during the look-back.  Status entry of
 // (chunk c, line j) is c * lpad + j.  Every element is read once and written
-// once.  A predecessor that stays unpublished for kSpinLimit rounds has its
+// once.  A predecessor that stays unpublished for p.spin_limit rounds has its
 // aggregate rebuilt from the input by the waiter with the owner's arithmetic
 // (f32: per-wave f32 prefix from the identity, then f64 over the waves in
 // order) and used directly, so progress never depends on dispatch order.
@@ -1075,7 +1075,7 @@ __device__ void col_lookback_wave(const ScanParams &p, const Status &st, uint64_
                 if (!done[v] && (uint64_t)k <= pos) st.read((pos - k) * lpad + line0 + v, p.tag, flag[k][v], val[k][v]);
             }
         // The next predecessor not ready for some line: wait, and after
-        // kSpinLimit polls take its aggregate from the input (the owner's
+        // p.spin_limit polls take its aggregate from the input (the owner's
         // arithmetic) and use it directly -- so progress never depends on
         // dispatch order.  Publishing it is only a courtesy to other
         // waiters, and is skipped where a status slot must keep one writer.
@@ -1083,7 +1083,7 @@ __device__ void col_lookback_wave(const ScanParams &p, const Status &st, uint64_
 #pragma unroll
         for (int v = 0; v < V; ++v) ready0 = ready0 && (done[v] || flag[0][v] != kInvalid);
         if (!ready0) {
-            if (++spins < kSpinLimit) {
+            if (++spins < p.spin_limit) {
                 __builtin_amdgcn_s_sleep(1);
                 continue;
             }
@@ -1515,6 +1515,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out_elem_stride = a.out_elem_stride;
     p.in_offset = a.in_offset;
     p.out_offset = a.out_offset;
+    p.spin_limit = lookback_poll_limit();
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
     if (narrow_column_scan(a)) return launch_narrow<T, Op>(a, p, ws, ws_bytes, stream);

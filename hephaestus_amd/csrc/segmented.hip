@@ -58,7 +58,6 @@ constexpr int kLongTile = SegTile<kLongWaves, kSegSteps>::kElems;
 constexpr uint64_t kLongMean = 4096;
 constexpr int kSlots = 2048; // segment values compacted per round
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
-constexpr uint32_t kSpinLimit = 64; // polls before computing a predecessor
 
 struct SegParams {
     const uint32_t *values;
@@ -70,6 +69,7 @@ struct SegParams {
     uint64_t *status;          // look-back words, one per tile
     uint32_t *ub_map, *lb_map; // tile edges -> offset indices (total_tiles + 1 each)
     uint32_t tag;              // this launch's status tag
+    uint32_t spin_limit;       // polls before computing a predecessor (64)
 };
 // A tile whose segment ends number more than kEndCap (only possible with runs
 // of empty segments) handles the first kEndCap itself; seg_tile_map_kernel
@@ -141,7 +141,7 @@ template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_
             const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
             const uint64_t missing = im & need;
             if (missing == 0ull) break;
-            if (++spins >= kSpinLimit) {
+            if (++spins >= p.spin_limit) {
                 const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
                 uint32_t fflag, fval;
                 seg_tile_status<TILE>(p, u, fflag, fval);
@@ -1020,6 +1020,7 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
         return fail(HX_ERR_DISPATCH_FAILED, "segmented workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
+    p.spin_limit = lookback_poll_limit();
     uint64_t map_blocks = ceil_div(a.num_segments + 2, kBlock);
     if (map_blocks > 2048) map_blocks = 2048;
     if (long_tile) {

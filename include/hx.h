@@ -572,6 +572,21 @@ hx_status hx_fill_random(hx_device *dev, void *dst, uint64_t n, hx_dtype dtype,
                          hx_distribution dist, uint64_t seed, double p0,
                          double p1, hx_stream stream);
 
+/* ------------------------------------------------------------ diagnostics */
+
+/* No counterpart in the reference.  For tests of the forward-progress
+ * fallbacks: sets, for launches queued afterwards by this process, how many
+ * polls a look-back (scans, segmented sums) makes before it computes a
+ * missing predecessor itself (default 64), and how many polls the gathering
+ * block of a one-launch reduction (full reduce, map-reductions) makes per
+ * partial before it recomputes that partial from the operand (default
+ * 16384).  0 takes every fallback at once; for the gather, 0 skips the
+ * partials entirely, so the gathering block recomputes every one.  Results
+ * are the same at every setting (integer results bit-identical, f32
+ * reductions bit-identical, f32 scans within their bound); only time
+ * changes.  Not for production use: a small limit makes large inputs slow. */
+hx_status hx_debug_set_wait_limits(uint32_t lookback_polls, uint32_t gather_polls);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif
