@@ -120,6 +120,20 @@ bool layout_is_c_contiguous(const hx_layout &l);
 // Strides are a permutation of a dense row-major stride set (all positive):
 // the view covers exactly [offset, offset + size) in some order.
 bool layout_is_permuted_dense(const hx_layout &l);
+// A view as rows in logical (row-major) order: `rows` rows of `cols`
+// elements, element c of a row at c * cstride, the row index split over up
+// to three outer dimensions (innermost first) from the view's offset.
+// Built by dropping unit dimensions and merging dimension pairs that are
+// row-major adjacent (stride[d] == stride[d+1] * shape[d+1]), so logical
+// element index row * cols + c is the original one.
+struct RowsView {
+    uint64_t rows = 1, cols = 1;
+    int64_t cstride = 1;
+    uint32_t orank = 0;
+    uint64_t oshape[HX_MAX_RANK - 1] = {1, 1, 1};
+    int64_t ostride[HX_MAX_RANK - 1] = {0, 0, 0};
+};
+RowsView layout_rows(const hx_layout &l);
 hx_status layout_basic_check(const hx_layout *l, const char *what);
 
 // ----------------------------------------------------------- workspace

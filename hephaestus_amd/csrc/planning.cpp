@@ -51,6 +51,34 @@ bool layout_is_c_contiguous(const hx_layout &l) {
     return true;
 }
 
+RowsView layout_rows(const hx_layout &l) {
+    uint64_t ext[HX_MAX_RANK];
+    int64_t str[HX_MAX_RANK];
+    int m = 0;
+    for (uint32_t d = 0; d < l.rank; ++d) {
+        if (l.shape[d] == 1) continue;
+        if (m > 0 && str[m - 1] == l.strides[d] * (int64_t)l.shape[d]) {
+            ext[m - 1] *= l.shape[d]; // row-major adjacent: one dimension
+            str[m - 1] = l.strides[d];
+            continue;
+        }
+        ext[m] = l.shape[d];
+        str[m] = l.strides[d];
+        ++m;
+    }
+    RowsView v;
+    if (m == 0) return v; // one element
+    v.cols = ext[m - 1];
+    v.cstride = str[m - 1];
+    v.orank = (uint32_t)(m - 1);
+    for (int k = 0; k < m - 1; ++k) {
+        v.oshape[k] = ext[m - 2 - k];
+        v.ostride[k] = str[m - 2 - k];
+        v.rows *= ext[m - 2 - k];
+    }
+    return v;
+}
+
 bool layout_is_permuted_dense(const hx_layout &l) {
     uint64_t ext[HX_MAX_RANK];
     int64_t str[HX_MAX_RANK];

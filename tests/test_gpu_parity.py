@@ -124,6 +124,101 @@ def test_full_reduce_strided_views(device, oracle):
         assert device.download_owned(out)[0] == oracle.full_max(np.ascontiguousarray(sel))
 
 
+# Non-dense views walked as rows: contiguous rows of every length either side
+# of the 4-element vector (16-byte loads at 4-byte alignment), row starts off
+# 16-byte boundaries, merged row-major dimensions, rank 3 and 4 outer walks,
+# negative outer strides, and element walks (inner stride != 1, transposes).
+ROW_VIEWS = [
+    ([300, 1], [7, 1], 0),                     # one column: element walk
+    ([300, 3], [7, 1], 1),                     # rows of 3: element walk
+    ([300, 4], [7, 1], 2),                     # one vector per row
+    ([300, 5], [7, 1], 3),                     # vector + 1-element tail
+    ([123, 9], [11, 1], 1),
+    ([64, 1000], [1003, 1], 5),                # a slice of wider rows
+    ([7, 9, 13], [200, 20, 1], 3),             # rank 3, two outer digits
+    ([3, 4, 5, 6], [400, 90, 15, 1], 2),       # rank 4, three outer digits
+    ([3, 4, 5, 6], [360, 90, 18, 1], 0),       # dims 1 and 2 merge (90 = 18 * 5)
+    ([40, 33], [-40, 1], 1560 + 3),            # rows in reverse order
+    ([500], [3], 4),                           # stride 3
+    ([50, 40], [1, 50], 0),                    # transposed (dense, permuted)
+    ([20, 30], [2, 60], 1),                    # inner stride 60
+    ([33, 17], [-1, 40], 32),                  # negative inner stride
+]
+
+
+def _view_elems(host, shape, strides, offset):
+    idx = offset + sum(np.indices(shape)[d] * strides[d] for d in range(len(shape)))
+    return np.ascontiguousarray(host[idx.ravel()])
+
+
+@pytest.mark.parametrize("view", ROW_VIEWS, ids=lambda v: "x".join(map(str, v[0])) + "_" + "_".join(map(str, v[1])))
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+def test_full_reduce_row_walks(device, oracle, view, dtype):
+    shape, strides, offset = view
+    span = offset + 1 + sum((e - 1) * st for e, st in zip(shape, strides) if st > 0)
+    host = inputs(oracle, dtype, span + 3, seed=sum(shape) + 7)
+    if dtype != np.float32:
+        host = (host % 977).astype(dtype)  # ties for argmax
+    lay = Layout.try_new(shape, strides, offset)
+    sel = _view_elems(host, shape, strides, offset)
+    buf = device.upload(host)
+    one = Layout.c_contiguous([1])
+    out = device.alloc_zeroed(dtype, 1)
+
+    def run(op):
+        FULL.reduce_full_into(device, op, StridedView(buf, lay), StridedView(out, one))
+        return device.download_owned(out)[0]
+
+    if dtype == np.float32:
+        ref, ab = oracle.full_sum(sel)
+        assert abs(float(run(hx.SumOp)) - ref) <= f32_bound(sel.size, ab)
+    else:
+        assert run(hx.SumOp) == oracle.full_sum(sel)
+        assert run(hx.ProdOp) == oracle.full_prod(sel)
+    assert run(hx.MaxOp) == oracle.full_max(sel)
+    assert run(hx.MinOp) == oracle.full_min(sel)
+    idx = device.alloc_zeroed(np.uint32, 1)
+    val = device.alloc_zeroed(dtype, 1)
+    FULL.argmax_full_into(device, StridedView(buf, lay), idx, val)
+    want = oracle.full_argmax(sel)
+    assert int(device.download_owned(idx)[0]) == want
+    assert device.download_owned(val)[0] == sel[want]
+
+
+def test_full_reduce_row_walk_with_prologue(device, oracle):
+    host = inputs(oracle, np.float32, 70000, seed=3)
+    shape, strides, offset = [250, 255], [257, 1], 2
+    lay = Layout.try_new(shape, strides, offset)
+    sel = _view_elems(host, shape, strides, offset)
+    buf = device.upload(host)
+    one = Layout.c_contiguous([1])
+    out = device.alloc_zeroed(np.float32, 1)
+    FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, lay), StridedView(out, one), prologue=(0.5, 0.25))
+    ref, ab = oracle.full_sum(sel, prologue=(0.5, 0.25))
+    assert abs(float(device.download_owned(out)[0]) - ref) <= f32_bound(sel.size, ab)
+    idx = device.alloc_zeroed(np.uint32, 1)
+    FULL.argmax_full_into(device, StridedView(buf, lay), idx, None, prologue=(-0.5, 0.25))
+    assert int(device.download_owned(idx)[0]) == oracle.full_argmax(sel, prologue=(-0.5, 0.25))
+
+
+def test_full_reduce_row_walk_at_scale(device, oracle):
+    """A 4096 x 4000 slice of 4096-wide rows (the walker's multi-row steps,
+    the fallback-free path at full grid) and its stride-2 columns."""
+    rows, cols, ld = 4096, 4000, 4096
+    host = inputs(oracle, np.uint32, rows * ld, seed=21)
+    buf = device.upload(host)
+    one = Layout.c_contiguous([1])
+    out = device.alloc_zeroed(np.uint32, 1)
+    for shape, strides in (([rows, cols], [ld, 1]), ([rows, cols // 2], [ld, 2])):
+        lay = Layout.try_new(shape, strides, 0)
+        sel = _view_elems(host, shape, strides, 0)
+        FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, lay), StridedView(out, one))
+        assert device.download_owned(out)[0] == oracle.full_sum(sel)
+        idx = device.alloc_zeroed(np.uint32, 1)
+        FULL.argmax_full_into(device, StridedView(buf, lay), idx, None)
+        assert int(device.download_owned(idx)[0]) == oracle.full_argmax(sel)
+
+
 def test_full_reduce_output_offset(device):
     buf = device.upload(np.arange(10, dtype=np.uint32))
     out = device.upload(np.full(4, 99, np.uint32))
