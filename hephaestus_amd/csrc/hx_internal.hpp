@@ -120,20 +120,27 @@ bool layout_is_c_contiguous(const hx_layout &l);
 // Strides are a permutation of a dense row-major stride set (all positive):
 // the view covers exactly [offset, offset + size) in some order.
 bool layout_is_permuted_dense(const hx_layout &l);
-// A view as rows in logical (row-major) order: `rows` rows of `cols`
-// elements, element c of a row at c * cstride, the row index split over up
-// to three outer dimensions (innermost first) from the view's offset.
-// Built by dropping unit dimensions and merging dimension pairs that are
-// row-major adjacent (stride[d] == stride[d+1] * shape[d+1]), so logical
-// element index row * cols + c is the original one.
+// A view as rows: `rows` rows of `cols` elements, element c of a row at
+// c * cstride, the row index split over up to three outer dimensions
+// (innermost first) from the view's offset.  Each dimension also carries
+// its logical (row-major) stride, so an element's logical index is the
+// same linear form over the digits.  Built by dropping unit dimensions and
+// merging dimension pairs that are adjacent both in memory (stride[d] ==
+// stride[d+1] * shape[d+1]) and logically.
 struct RowsView {
     uint64_t rows = 1, cols = 1;
-    int64_t cstride = 1;
+    int64_t cstride = 1, clstride = 1;
     uint32_t orank = 0;
     uint64_t oshape[HX_MAX_RANK - 1] = {1, 1, 1};
     int64_t ostride[HX_MAX_RANK - 1] = {0, 0, 0};
+    int64_t olstride[HX_MAX_RANK - 1] = {0, 0, 0};
 };
+// Rows in logical (row-major) order.
 RowsView layout_rows(const hx_layout &l);
+// Rows in memory order (dimensions by decreasing stride) of a view whose
+// strides are all positive (layout_is_permuted_dense): for order-free
+// folds that still need logical indices (argmax of a transposed view).
+RowsView layout_rows_memory_order(const hx_layout &l);
 hx_status layout_basic_check(const hx_layout *l, const char *what);
 
 // ----------------------------------------------------------- workspace
@@ -191,6 +198,7 @@ struct FullReduceArgs {
     hx_layout layout;    // logical view
     uint64_t n;          // logical size
     bool flat;           // view is the flat range [flat_offset, +n)
+    bool memory_order;   // not flat: walk rows in memory order (argmax of a permuted dense view)
     uint64_t flat_offset;
     bool affine;
     float a, b;

@@ -373,7 +373,11 @@ hx_status hx_argmax_full(hx_device *dev, hx_dtype dtype, const void *in, uint64_
     a.base = in;
     a.layout = *in_layout;
     a.n = n;
-    a.flat = layout_is_c_contiguous(*in_layout); // indices follow logical order
+    // Indices follow logical order: only a row-major view is the flat range;
+    // a permuted dense one (a transpose) is read in memory order with each
+    // element's logical index carried along.
+    a.flat = layout_is_c_contiguous(*in_layout);
+    a.memory_order = !a.flat && layout_is_permuted_dense(*in_layout);
     a.flat_offset = in_layout->offset;
     a.affine = affine;
     a.a = pa;

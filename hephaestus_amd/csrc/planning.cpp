@@ -51,32 +51,75 @@ bool layout_is_c_contiguous(const hx_layout &l) {
     return true;
 }
 
-RowsView layout_rows(const hx_layout &l) {
+namespace {
+// Rows from dimensions listed outermost first (extent, memory stride,
+// logical stride), merging neighbours adjacent in both senses.
+RowsView rows_from_dims(const uint64_t *shape, const int64_t *stride, const int64_t *lstride, int n) {
     uint64_t ext[HX_MAX_RANK];
-    int64_t str[HX_MAX_RANK];
+    int64_t str[HX_MAX_RANK], lst[HX_MAX_RANK];
     int m = 0;
-    for (uint32_t d = 0; d < l.rank; ++d) {
-        if (l.shape[d] == 1) continue;
-        if (m > 0 && str[m - 1] == l.strides[d] * (int64_t)l.shape[d]) {
-            ext[m - 1] *= l.shape[d]; // row-major adjacent: one dimension
-            str[m - 1] = l.strides[d];
+    for (int d = 0; d < n; ++d) {
+        if (shape[d] == 1) continue;
+        if (m > 0 && str[m - 1] == stride[d] * (int64_t)shape[d] && lst[m - 1] == lstride[d] * (int64_t)shape[d]) {
+            ext[m - 1] *= shape[d];
+            str[m - 1] = stride[d];
+            lst[m - 1] = lstride[d];
             continue;
         }
-        ext[m] = l.shape[d];
-        str[m] = l.strides[d];
+        ext[m] = shape[d];
+        str[m] = stride[d];
+        lst[m] = lstride[d];
         ++m;
     }
     RowsView v;
     if (m == 0) return v; // one element
     v.cols = ext[m - 1];
     v.cstride = str[m - 1];
+    v.clstride = lst[m - 1];
     v.orank = (uint32_t)(m - 1);
     for (int k = 0; k < m - 1; ++k) {
         v.oshape[k] = ext[m - 2 - k];
         v.ostride[k] = str[m - 2 - k];
+        v.olstride[k] = lst[m - 2 - k];
         v.rows *= ext[m - 2 - k];
     }
     return v;
+}
+
+void logical_strides(const hx_layout &l, int64_t *lstride) {
+    int64_t s = 1;
+    for (int d = (int)l.rank - 1; d >= 0; --d) {
+        lstride[d] = s;
+        s *= (int64_t)(l.shape[d] ? l.shape[d] : 1);
+    }
+}
+} // namespace
+
+RowsView layout_rows(const hx_layout &l) {
+    int64_t lstride[HX_MAX_RANK];
+    logical_strides(l, lstride);
+    return rows_from_dims(l.shape, l.strides, lstride, (int)l.rank);
+}
+
+RowsView layout_rows_memory_order(const hx_layout &l) {
+    int64_t lstride[HX_MAX_RANK];
+    logical_strides(l, lstride);
+    uint64_t shape[HX_MAX_RANK];
+    int64_t stride[HX_MAX_RANK], lst[HX_MAX_RANK];
+    const int n = (int)l.rank;
+    for (int d = 0; d < n; ++d) {
+        shape[d] = l.shape[d];
+        stride[d] = l.strides[d];
+        lst[d] = lstride[d];
+    }
+    // Decreasing stride: memory order, outermost first (ties keep logical order).
+    for (int i = 1; i < n; ++i)
+        for (int j = i; j > 0 && stride[j - 1] < stride[j]; --j) {
+            std::swap(shape[j - 1], shape[j]);
+            std::swap(stride[j - 1], stride[j]);
+            std::swap(lst[j - 1], lst[j]);
+        }
+    return rows_from_dims(shape, stride, lst, n);
 }
 
 bool layout_is_permuted_dense(const hx_layout &l) {

@@ -105,20 +105,21 @@ template <typename T> struct Policy<T, kArgmax> {
 
 // A non-flat view walked as rows (RowsView): `units` work units per row --
 // 16-byte vectors of 4 elements when the row is contiguous (cstride 1),
-// single elements otherwise -- unit u of a row at element u * ustride.  The
-// walker's step of `step` units is split on the host into whole rows (as
-// outer digits, innermost first, and their element offset step_off) and
-// leftover units (step_units, element offset step_uoff), so a step is adds
-// and compares only.  ospan[k] = oshape[k] * ostride[k].
+// single elements otherwise -- unit u of a row at element u * ustride and
+// logical index u * lustride.  The walker's step of `step` units is split
+// on the host into whole rows (as outer digits, innermost first, with
+// their element offset step_off and logical step step_loff) and leftover
+// units (step_units, step_uoff, step_luoff), so a step is adds and
+// compares only.  ospan / olspan[k] = oshape[k] * ostride / olstride[k].
 struct RowsGeom {
     uint64_t rows, cols, units;
-    int64_t ustride, units_span;
+    int64_t ustride, units_span, clstride, lustride, lunits_span;
     uint32_t orank;
     uint64_t oshape[3];
-    int64_t ostride[3], ospan[3];
+    int64_t ostride[3], ospan[3], olstride[3], olspan[3];
     uint64_t step_units, step_rows;
     uint64_t step_digits[3];
-    int64_t step_uoff, step_off;
+    int64_t step_uoff, step_off, step_luoff, step_loff;
 };
 
 struct FullParams {
@@ -142,15 +143,17 @@ template <> __device__ __forceinline__ float prologue<float, true>(float x, floa
 // Walks a thread's units of a RowsGeom view: unit `item` is unit
 // item % units of row item / units.  Divisions only at the start; each
 // advance adds the precomputed step with carries.  `off` is the element
-// offset of the walker's unit.
+// offset of the walker's unit, `lidx` the logical index of its first
+// element.
 struct RowWalker {
-    uint64_t row, unit;
-    uint64_t dig[3]; // outer digits of `row`, innermost first (the outermost unwrapped)
-    int64_t off;
+    uint64_t unit;
+    uint64_t dig[3]; // outer digits of the row, innermost first (the outermost unwrapped)
+    int64_t off, lidx;
     __device__ __forceinline__ void init(const RowsGeom &g, int64_t base, uint64_t item) {
-        row = item / g.units;
+        const uint64_t row = item / g.units;
         unit = item - row * g.units;
         off = base + (int64_t)unit * g.ustride;
+        lidx = (int64_t)unit * g.lustride;
         uint64_t r = row;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
@@ -162,28 +165,36 @@ struct RowWalker {
                 dig[k] = r;
                 r = 0;
             }
-            if ((uint32_t)k < g.orank) off += (int64_t)dig[k] * g.ostride[k];
+            if ((uint32_t)k < g.orank) {
+                off += (int64_t)dig[k] * g.ostride[k];
+                lidx += (int64_t)dig[k] * g.olstride[k];
+            }
         }
     }
     __device__ __forceinline__ void advance(const RowsGeom &g) {
         unit += g.step_units;
         off += g.step_uoff + g.step_off;
+        lidx += g.step_luoff + g.step_loff;
         uint64_t carry = 0;
         if (unit >= g.units) {
             unit -= g.units;
             off -= g.units_span;
+            lidx -= g.lunits_span;
             carry = 1;
         }
-        row += g.step_rows + carry;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
             if ((uint32_t)k < g.orank) {
                 dig[k] += g.step_digits[k] + carry;
-                if (carry) off += g.ostride[k];
+                if (carry) {
+                    off += g.ostride[k];
+                    lidx += g.olstride[k];
+                }
                 carry = 0;
                 if ((uint32_t)k + 1 < g.orank && dig[k] >= g.oshape[k]) {
                     dig[k] -= g.oshape[k];
                     off -= g.ospan[k];
+                    lidx -= g.olspan[k];
                     carry = 1;
                 }
             }
@@ -278,19 +289,22 @@ __device__ __forceinline__ uint32_t load_unit(const RowsGeom &g, const T *src, c
     }
 }
 
-// Fold of `cnt` elements whose logical indices start at e0.
+// Fold of `cnt` elements whose logical indices are e0, e0 + es, ...
 template <typename P, typename T, bool AFFINE>
-__device__ __forceinline__ typename P::Acc fold_n(const T (&x)[4], uint32_t cnt, uint64_t e0, float a, float b) {
+__device__ __forceinline__ typename P::Acc fold_n(const T (&x)[4], uint32_t cnt, uint64_t e0, uint64_t es, float a,
+                                                  float b) {
     using Acc = typename P::Acc;
     if (cnt == 4) {
         const Acc a0 = P::lift(prologue<T, AFFINE>(x[0], a, b), e0);
-        const Acc a1 = P::lift(prologue<T, AFFINE>(x[1], a, b), e0 + 1);
-        const Acc a2 = P::lift(prologue<T, AFFINE>(x[2], a, b), e0 + 2);
-        const Acc a3 = P::lift(prologue<T, AFFINE>(x[3], a, b), e0 + 3);
+        const Acc a1 = P::lift(prologue<T, AFFINE>(x[1], a, b), e0 + es);
+        const Acc a2 = P::lift(prologue<T, AFFINE>(x[2], a, b), e0 + 2 * es);
+        const Acc a3 = P::lift(prologue<T, AFFINE>(x[3], a, b), e0 + 3 * es);
         return P::combine(P::combine(a0, a1), P::combine(a2, a3));
     }
     Acc r = P::identity();
-    for (uint32_t c = 0; c < cnt; ++c) r = P::combine(r, P::lift(prologue<T, AFFINE>(x[c], a, b), e0 + c));
+#pragma unroll
+    for (uint32_t c = 0; c < 3; ++c)
+        if (c < cnt) r = P::combine(r, P::lift(prologue<T, AFFINE>(x[c], a, b), e0 + c * es));
     return r;
 }
 
@@ -339,7 +353,6 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
         }
     } else {
         constexpr int W = Walkers<MODE>::value;
-        constexpr uint64_t kUnitElems = MODE == kRowsVec ? 4 : 1;
         const RowsGeom &g = p.g;
         const T *src = (const T *)p.base;
         const uint64_t items = g.rows * g.units;
@@ -355,7 +368,7 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
 #pragma unroll
             for (int k = 0; k < W; ++k) {
                 if (cnt[k] != 0u)
-                    acc = P::combine(acc, fold_n<P, T, AFFINE>(x[k], cnt[k], w[k].row * g.cols + kUnitElems * w[k].unit,
+                    acc = P::combine(acc, fold_n<P, T, AFFINE>(x[k], cnt[k], (uint64_t)w[k].lidx, (uint64_t)g.clstride,
                                                                p.a, p.b));
                 w[k].advance(g);
             }
@@ -410,15 +423,21 @@ RowsGeom rows_geom(const RowsView &v, bool vec, uint64_t step) {
     g.units = vec ? ceil_div(v.cols, 4) : v.cols;
     g.ustride = vec ? 4 : v.cstride;
     g.units_span = (int64_t)g.units * g.ustride;
+    g.clstride = v.clstride;
+    g.lustride = vec ? 4 * v.clstride : v.clstride;
+    g.lunits_span = (int64_t)g.units * g.lustride;
     g.orank = v.orank;
     for (int k = 0; k < 3; ++k) {
         g.oshape[k] = v.oshape[k];
         g.ostride[k] = v.ostride[k];
         g.ospan[k] = (int64_t)v.oshape[k] * v.ostride[k];
+        g.olstride[k] = v.olstride[k];
+        g.olspan[k] = (int64_t)v.oshape[k] * v.olstride[k];
     }
     g.step_units = step % g.units;
     g.step_rows = step / g.units;
     g.step_uoff = (int64_t)g.step_units * g.ustride;
+    g.step_luoff = (int64_t)g.step_units * g.lustride;
     uint64_t r = g.step_rows;
     for (uint32_t k = 0; k < 3; ++k) {
         if (k + 1 < g.orank) {
@@ -430,7 +449,10 @@ RowsGeom rows_geom(const RowsView &v, bool vec, uint64_t step) {
         } else {
             g.step_digits[k] = 0;
         }
-        if (k < g.orank) g.step_off += (int64_t)g.step_digits[k] * g.ostride[k];
+        if (k < g.orank) {
+            g.step_off += (int64_t)g.step_digits[k] * g.ostride[k];
+            g.step_loff += (int64_t)g.step_digits[k] * g.olstride[k];
+        }
     }
     return g;
 }
@@ -463,7 +485,7 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Loo
     if (a.flat) {
         hipLaunchKernelGGL((full_reduce_kernel<T, K, AFFINE, kFlat>), dim3(blocks), dim3(kBlock), 0, stream, p);
     } else {
-        const RowsView rv = layout_rows(a.layout);
+        const RowsView rv = a.memory_order ? layout_rows_memory_order(a.layout) : layout_rows(a.layout);
         const bool vec = rv.cstride == 1 && rv.cols >= 4;
         p.g = rows_geom(rv, vec, (uint64_t)(vec ? Walkers<kRowsVec>::value : Walkers<kRowsScalar>::value) *
                                      blocks * kBlock);

@@ -140,7 +140,9 @@ ROW_VIEWS = [
     ([3, 4, 5, 6], [360, 90, 18, 1], 0),       # dims 1 and 2 merge (90 = 18 * 5)
     ([40, 33], [-40, 1], 1560 + 3),            # rows in reverse order
     ([500], [3], 4),                           # stride 3
-    ([50, 40], [1, 50], 0),                    # transposed (dense, permuted)
+    ([50, 40], [1, 50], 0),                    # transposed (dense, permuted: argmax in memory order)
+    ([6, 7, 8], [1, 48, 6], 0),                # rank-3 permutation
+    ([9, 5, 4], [20, 1, 5], 3),                # rank-3 permutation, offset
     ([20, 30], [2, 60], 1),                    # inner stride 60
     ([33, 17], [-1, 40], 32),                  # negative inner stride
 ]
