@@ -1,0 +1,105 @@
+"""Maximum sizes: full reductions, argmax and a scan over 2^32 elements and
+more (16 GiB operands), where element counts, offsets and logical indices
+no longer fit in 32 bits. Inputs are generated on the device with constant
+or planted values, so every result has a closed form. The reference checks
+no size this large; the oracle would take minutes here, and the closed
+forms pin the same arithmetic (u32 sums and products wrap mod 2^32, f32
+sums accumulate in f64, argmax ties go to the lowest index)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import hephaestus_amd as hx
+from hephaestus_amd import Layout, StridedView, _ffi
+
+pytestmark = pytest.mark.gpu
+
+FULL = hx.RocmFullReductionOps()
+SCAN = hx.RocmScanOps()
+N = (1 << 32) + 1029  # past 2^32, not a multiple of any tile or vector width
+ONE = Layout.c_contiguous([1])
+
+
+def _slice(device, buf, start, count):
+    out = device.alloc_zeroed(buf.dtype, count)
+    _ffi.check(_ffi.lib().hx_copy(device.handle, buf.ptr + start * buf.itemsize, count, out.ptr, count,
+                                  buf.itemsize))
+    return device.download_owned(out)
+
+
+def _full(device, op, buf, n, dtype):
+    out = device.alloc_zeroed(dtype, 1)
+    FULL.reduce_full_into(device, op, StridedView(buf, Layout.c_contiguous([n])), StridedView(out, ONE))
+    return device.download_owned(out)[0]
+
+
+def test_u32_full_reductions_past_2_32_elements(device):
+    buf = device.alloc_uninitialized(np.uint32, N)
+    device.fill_uniform_int(buf, seed=1, lo=3, hi=3)
+    assert _slice(device, buf, N - 4, 4).tolist() == [3, 3, 3, 3]
+    assert _full(device, hx.SumOp, buf, N, np.uint32) == (3 * N) % 2**32
+    assert _full(device, hx.ProdOp, buf, N, np.uint32) == pow(3, N, 2**32)
+    assert _full(device, hx.MaxOp, buf, N, np.uint32) == 3
+    assert _full(device, hx.MinOp, buf, N, np.uint32) == 3
+    # A view of the last 2^32 + 5 elements starting past element 2^10: the
+    # head peel and the 64-bit offset arithmetic of the flat path.
+    n2 = (1 << 32) + 5
+    out = device.alloc_zeroed(np.uint32, 1)
+    FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, Layout.try_new([n2], [1], N - n2)),
+                          StridedView(out, ONE))
+    assert device.download_owned(out)[0] == (3 * n2) % 2**32
+    buf.free()
+
+
+def test_f32_sum_and_mean_past_2_32_elements(device):
+    buf = device.alloc_uninitialized(np.float32, N)
+    device.fill_uniform_real(buf, seed=2, lo=1.0, hi=1.0)  # fmaf(0, u, 1) = 1 everywhere
+    assert _slice(device, buf, 0, 2).tolist() == [1.0, 1.0]
+    # The f64 sum is exact (N < 2^53); one rounding to f32.
+    assert _full(device, hx.SumOp, buf, N, np.float32) == np.float32(float(N))
+    assert _full(device, hx.MeanOp, buf, N, np.float32) == np.float32(1.0)
+    # Rows of a 65537-wide matrix: the row walker with offsets past 2^32.
+    rows, ld, cols = (N - 1029) // 65537, 65537, 65530
+    out = device.alloc_zeroed(np.float32, 1)
+    FULL.reduce_full_into(device, hx.SumOp, StridedView(buf, Layout.try_new([rows, cols], [ld, 1], 1029)),
+                          StridedView(out, ONE))
+    assert device.download_owned(out)[0] == np.float32(float(rows * cols))
+    buf.free()
+
+
+def test_argmax_at_the_largest_count(device):
+    """The largest argmax operand (2^32 - 2 elements: index 0xFFFFFFFF is the
+    no-index sentinel): a planted maximum past 2^31 wins over an equal one at
+    the last index, and after it is removed the last index wins."""
+    n = (1 << 32) - 2
+    buf = device.alloc_uninitialized(np.uint32, n)
+    device.fill_uniform_int(buf, seed=3, lo=5, hi=5)
+    device.write_sub_buffer(buf, n - 1, np.array([7], np.uint32))
+    device.write_sub_buffer(buf, (1 << 31) + 3, np.array([7], np.uint32))
+    idx = device.alloc_zeroed(np.uint32, 1)
+    val = device.alloc_zeroed(np.uint32, 1)
+    lay = Layout.c_contiguous([n])
+    FULL.argmax_full_into(device, StridedView(buf, lay), idx, val)
+    assert int(device.download_owned(idx)[0]) == (1 << 31) + 3
+    assert int(device.download_owned(val)[0]) == 7
+    device.write_sub_buffer(buf, (1 << 31) + 3, np.array([5], np.uint32))
+    FULL.argmax_full_into(device, StridedView(buf, lay), idx, val)
+    assert int(device.download_owned(idx)[0]) == n - 1
+    buf.free()
+
+
+def test_exclusive_scan_past_2_32_elements(device):
+    """All-ones u32: out[i] = i mod 2^32, so the prefix wraps once (at
+    element 2^32) and the last tile is ragged."""
+    x = device.alloc_uninitialized(np.uint32, N)
+    device.fill_uniform_int(x, seed=4, lo=1, hi=1)
+    out = device.alloc_uninitialized(np.uint32, N)
+    lay = Layout.c_contiguous([N])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                        StridedView(out, lay), hx.ScanKind.Exclusive)
+    for start in (0, (1 << 31) - 4, (1 << 32) - 4, N - 8):
+        want = [(start + i) % 2**32 for i in range(8)]
+        assert _slice(device, out, start, 8).tolist() == want, start
+    x.free()
+    out.free()
