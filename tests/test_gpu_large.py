@@ -1,6 +1,7 @@
 """Maximum sizes: full reductions, argmax and a scan over 2^32 elements and
-more (16 GiB operands), where element counts, offsets and logical indices
-no longer fit in 32 bits. Inputs are generated on the device with constant
+more, and segmented sums over 2^32 - 1 values (the most u32 offsets
+address) -- 16 GiB operands, where element counts, offsets and logical
+indices no longer fit in 31 or 32 bits. Inputs are generated on the device with constant
 or planted values, so every result has a closed form. The reference checks
 no size this large; the oracle would take minutes here, and the closed
 forms pin the same arithmetic (u32 sums and products wrap mod 2^32, f32
@@ -103,3 +104,33 @@ def test_exclusive_scan_past_2_32_elements(device):
         assert _slice(device, out, start, 8).tolist() == want, start
     x.free()
     out.free()
+
+
+SEG = hx.RocmSegmentedReductionOps()
+
+
+@pytest.mark.parametrize("case", ["geometric-300", "geometric-50000", "extremes"])
+def test_segmented_sum_at_the_largest_count(device, case):
+    """n = 2^32 - 1 values (the most u32 offsets address), all ones, so
+    every segment's sum is its length. Element tiles of 8192 values (mean
+    300, about 14.3 million segments) and of 16384 values (mean 50000),
+    and hand-placed segments: empty ones at both ends, one of a single
+    value, one ending at 2^31 and one spanning past 2^31 to the end."""
+    n = 2**32 - 1
+    if case == "extremes":
+        offsets = np.array([0, 0, 1, 2**31, 2**32 - 2, n, n], np.uint64)
+    else:
+        mean = 300.0 if case == "geometric-300" else 50000.0
+        rng = np.random.default_rng(7)
+        lengths = rng.geometric(1.0 / mean, size=int(n / mean * 1.05) + 64).astype(np.uint64)
+        ends = np.cumsum(lengths)
+        offsets = np.concatenate([[0], ends[ends < n], [n]]).astype(np.uint64)
+    values = device.alloc_uninitialized(np.int32, n)
+    device.fill_uniform_int(values, seed=8, lo=1, hi=1)
+    off = device.upload(offsets.astype(np.uint32))
+    out = device.upload(np.full(offsets.size - 1, -7, np.int32))
+    SEG.segmented_sum_into(device, values, off, out)
+    want = np.diff(offsets.astype(np.int64))
+    got = device.download_owned(out).view(np.uint32).astype(np.int64)
+    assert np.array_equal(got, want)
+    values.free()
