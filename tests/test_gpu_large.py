@@ -134,3 +134,46 @@ def test_segmented_sum_at_the_largest_count(device, case):
     got = device.download_owned(out).view(np.uint32).astype(np.int64)
     assert np.array_equal(got, want)
     values.free()
+
+
+def test_f32_scan_past_2_32_elements(device):
+    """All-ones f32, inclusive: within a tile the f32 prefixes are exact
+    integers (< 2^24) and the inter-tile carry is f64, so out[i] is the
+    f32 rounding of i + 1 exactly, far inside the 2*ceil(log2 n)*eps*i
+    bound, across the 2^24, 2^31 and 2^32 boundaries."""
+    x = device.alloc_uninitialized(np.float32, N)
+    device.fill_uniform_real(x, seed=5, lo=1.0, hi=1.0)
+    out = device.alloc_uninitialized(np.float32, N)
+    lay = Layout.c_contiguous([N])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0, hx.ScanDirection.Forward,
+                        StridedView(out, lay), hx.ScanKind.Inclusive)
+    for start in (0, (1 << 24) - 4, (1 << 31) - 4, (1 << 32) - 4, N - 8):
+        want = np.array([float(start + i + 1) for i in range(8)], np.float64).astype(np.float32)
+        assert np.array_equal(_slice(device, out, start, 8), want), start
+    x.free()
+    out.free()
+
+
+def test_rows_past_2_31_rows(device):
+    """2^31 + 3 rows of 2 f32 (one thread per row): row indices past 2^31
+    and outputs of 2^31 + 3 entries. Every row is (1, 1) except planted
+    rows whose second element is 5."""
+    rows, cols = (1 << 31) + 3, 2
+    x = device.alloc_uninitialized(np.float32, rows * cols)
+    device.fill_uniform_real(x, seed=6, lo=1.0, hi=1.0)
+    planted = [0, (1 << 31) - 1, 1 << 31, rows - 1]
+    for r in planted:
+        device.write_sub_buffer(x, r * cols + 1, np.array([5.0], np.float32))
+    s = device.alloc_zeroed(np.float32, rows)
+    m = device.alloc_zeroed(np.float32, rows)
+    a = device.alloc_zeroed(np.uint32, rows)
+    hx.RocmAxisReductionOps().reduce_rows_fused(device, x, rows, cols, out_sum=s, out_max=m, out_argmax=a)
+    for start in (0, (1 << 31) - 2, rows - 4):
+        want_s = [6.0 if start + i in planted else 2.0 for i in range(4)]
+        want_m = [5.0 if start + i in planted else 1.0 for i in range(4)]
+        want_a = [1 if start + i in planted else 0 for i in range(4)]
+        assert _slice(device, s, start, 4).tolist() == want_s, start
+        assert _slice(device, m, start, 4).tolist() == want_m, start
+        assert _slice(device, a, start, 4).tolist() == want_a, start
+    for b in (x, s, m, a):
+        b.free()
