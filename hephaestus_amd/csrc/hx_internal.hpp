@@ -122,25 +122,30 @@ bool layout_is_c_contiguous(const hx_layout &l);
 bool layout_is_permuted_dense(const hx_layout &l);
 // A view as rows: `rows` rows of `cols` elements, element c of a row at
 // c * cstride, the row index split over up to three outer dimensions
-// (innermost first) from the view's offset.  Each dimension also carries
-// its logical (row-major) stride, so an element's logical index is the
-// same linear form over the digits.  Built by dropping unit dimensions and
-// merging dimension pairs that are adjacent both in memory (stride[d] ==
-// stride[d+1] * shape[d+1]) and logically.
+// (innermost first) from the view's offset.  Each dimension also carries a
+// second stride (cstride2, ostride2): the logical (row-major) stride for
+// one operand, or a second operand's stride, so a second linear form over
+// the same digits follows the walk.  Built by dropping unit dimensions and
+// merging dimension pairs adjacent under both strides (stride[d] ==
+// stride[d+1] * shape[d+1]).
 struct RowsView {
     uint64_t rows = 1, cols = 1;
-    int64_t cstride = 1, clstride = 1;
+    int64_t cstride = 1, cstride2 = 1;
     uint32_t orank = 0;
     uint64_t oshape[HX_MAX_RANK - 1] = {1, 1, 1};
     int64_t ostride[HX_MAX_RANK - 1] = {0, 0, 0};
-    int64_t olstride[HX_MAX_RANK - 1] = {0, 0, 0};
+    int64_t ostride2[HX_MAX_RANK - 1] = {0, 0, 0};
 };
-// Rows in logical (row-major) order.
+// Rows in logical (row-major) order; the second form is the logical index.
 RowsView layout_rows(const hx_layout &l);
 // Rows in memory order (dimensions by decreasing stride) of a view whose
-// strides are all positive (layout_is_permuted_dense): for order-free
-// folds that still need logical indices (argmax of a transposed view).
+// strides are all positive (layout_is_permuted_dense), the second form the
+// logical index: for order-free folds that still need logical indices
+// (argmax of a transposed view).
 RowsView layout_rows_memory_order(const hx_layout &l);
+// Rows of two same-shape views in logical order: the first form walks `a`,
+// the second `b`'s strides.
+RowsView layout_rows_pair(const hx_layout &a, const hx_layout &b);
 hx_status layout_basic_check(const hx_layout *l, const char *what);
 
 // ----------------------------------------------------------- workspace

@@ -52,8 +52,8 @@ bool layout_is_c_contiguous(const hx_layout &l) {
 }
 
 namespace {
-// Rows from dimensions listed outermost first (extent, memory stride,
-// logical stride), merging neighbours adjacent in both senses.
+// Rows from dimensions listed outermost first (extent, stride, second
+// stride), merging neighbours adjacent under both strides.
 RowsView rows_from_dims(const uint64_t *shape, const int64_t *stride, const int64_t *lstride, int n) {
     uint64_t ext[HX_MAX_RANK];
     int64_t str[HX_MAX_RANK], lst[HX_MAX_RANK];
@@ -75,12 +75,12 @@ RowsView rows_from_dims(const uint64_t *shape, const int64_t *stride, const int6
     if (m == 0) return v; // one element
     v.cols = ext[m - 1];
     v.cstride = str[m - 1];
-    v.clstride = lst[m - 1];
+    v.cstride2 = lst[m - 1];
     v.orank = (uint32_t)(m - 1);
     for (int k = 0; k < m - 1; ++k) {
         v.oshape[k] = ext[m - 2 - k];
         v.ostride[k] = str[m - 2 - k];
-        v.olstride[k] = lst[m - 2 - k];
+        v.ostride2[k] = lst[m - 2 - k];
         v.rows *= ext[m - 2 - k];
     }
     return v;
@@ -99,6 +99,10 @@ RowsView layout_rows(const hx_layout &l) {
     int64_t lstride[HX_MAX_RANK];
     logical_strides(l, lstride);
     return rows_from_dims(l.shape, l.strides, lstride, (int)l.rank);
+}
+
+RowsView layout_rows_pair(const hx_layout &a, const hx_layout &b) {
+    return rows_from_dims(a.shape, a.strides, b.strides, (int)a.rank);
 }
 
 RowsView layout_rows_memory_order(const hx_layout &l) {

@@ -24,6 +24,7 @@
 // result bits do not depend on the GPU's CU count.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
+#include "rows_walk.hpp"
 
 #include <type_traits>
 
@@ -103,25 +104,6 @@ template <typename T> struct Policy<T, kArgmax> {
     __device__ static Acc wave(Acc a) { return wave_umax64(a); }
 };
 
-// A non-flat view walked as rows (RowsView): `units` work units per row --
-// 16-byte vectors of 4 elements when the row is contiguous (cstride 1),
-// single elements otherwise -- unit u of a row at element u * ustride and
-// logical index u * lustride.  The walker's step of `step` units is split
-// on the host into whole rows (as outer digits, innermost first, with
-// their element offset step_off and logical step step_loff) and leftover
-// units (step_units, step_uoff, step_luoff), so a step is adds and
-// compares only.  ospan / olspan[k] = oshape[k] * ostride / olstride[k].
-struct RowsGeom {
-    uint64_t rows, cols, units;
-    int64_t ustride, units_span, clstride, lustride, lunits_span;
-    uint32_t orank;
-    uint64_t oshape[3];
-    int64_t ostride[3], ospan[3], olstride[3], olspan[3];
-    uint64_t step_units, step_rows;
-    uint64_t step_digits[3];
-    int64_t step_uoff, step_off, step_luoff, step_loff;
-};
-
 struct FullParams {
     const void *base;
     uint64_t n;
@@ -139,68 +121,6 @@ template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, fl
 template <> __device__ __forceinline__ float prologue<float, true>(float x, float a, float b) {
     return __builtin_fmaf(a, x, b);
 }
-
-// Walks a thread's units of a RowsGeom view: unit `item` is unit
-// item % units of row item / units.  Divisions only at the start; each
-// advance adds the precomputed step with carries.  `off` is the element
-// offset of the walker's unit, `lidx` the logical index of its first
-// element.
-struct RowWalker {
-    uint64_t unit;
-    uint64_t dig[3]; // outer digits of the row, innermost first (the outermost unwrapped)
-    int64_t off, lidx;
-    __device__ __forceinline__ void init(const RowsGeom &g, int64_t base, uint64_t item) {
-        const uint64_t row = item / g.units;
-        unit = item - row * g.units;
-        off = base + (int64_t)unit * g.ustride;
-        lidx = (int64_t)unit * g.lustride;
-        uint64_t r = row;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            if ((uint32_t)k + 1 < g.orank) {
-                const uint64_t q = r / g.oshape[k];
-                dig[k] = r - q * g.oshape[k];
-                r = q;
-            } else {
-                dig[k] = r;
-                r = 0;
-            }
-            if ((uint32_t)k < g.orank) {
-                off += (int64_t)dig[k] * g.ostride[k];
-                lidx += (int64_t)dig[k] * g.olstride[k];
-            }
-        }
-    }
-    __device__ __forceinline__ void advance(const RowsGeom &g) {
-        unit += g.step_units;
-        off += g.step_uoff + g.step_off;
-        lidx += g.step_luoff + g.step_loff;
-        uint64_t carry = 0;
-        if (unit >= g.units) {
-            unit -= g.units;
-            off -= g.units_span;
-            lidx -= g.lunits_span;
-            carry = 1;
-        }
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            if ((uint32_t)k < g.orank) {
-                dig[k] += g.step_digits[k] + carry;
-                if (carry) {
-                    off += g.ostride[k];
-                    lidx += g.olstride[k];
-                }
-                carry = 0;
-                if ((uint32_t)k + 1 < g.orank && dig[k] >= g.oshape[k]) {
-                    dig[k] -= g.oshape[k];
-                    off -= g.ospan[k];
-                    lidx -= g.olspan[k];
-                    carry = 1;
-                }
-            }
-        }
-    }
-};
 
 template <typename P>
 __device__ __forceinline__ typename P::Acc block_reduce(typename P::Acc v,
@@ -358,7 +278,7 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
         const uint64_t items = g.rows * g.units;
         RowWalker w[W];
 #pragma unroll
-        for (int k = 0; k < W; ++k) w[k].init(g, (int64_t)p.offset, tid + (uint64_t)k * nthreads);
+        for (int k = 0; k < W; ++k) w[k].init(g, (int64_t)p.offset, 0, tid + (uint64_t)k * nthreads);
         for (uint64_t j = tid; j < items; j += (uint64_t)W * nthreads) {
             T x[W][4];
             uint32_t cnt[W];
@@ -368,7 +288,7 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
 #pragma unroll
             for (int k = 0; k < W; ++k) {
                 if (cnt[k] != 0u)
-                    acc = P::combine(acc, fold_n<P, T, AFFINE>(x[k], cnt[k], (uint64_t)w[k].lidx, (uint64_t)g.clstride,
+                    acc = P::combine(acc, fold_n<P, T, AFFINE>(x[k], cnt[k], (uint64_t)w[k].off2, (uint64_t)g.cstride2,
                                                                p.a, p.b));
                 w[k].advance(g);
             }
@@ -410,51 +330,6 @@ __global__ __launch_bounds__(kBlock) void full_reduce_kernel(FullParams p) {
 template <typename T, int K> __global__ void full_reduce_empty_kernel(FullParams p) {
     using P = Policy<T, K>;
     if (threadIdx.x == 0 && blockIdx.x == 0) write_result_impl<T, K>(p, P::identity());
-}
-
-// The walker geometry of a row view: units per row (vectors of 4 elements
-// or single elements) and a step of `step` units as whole rows, outer
-// digits of those rows (innermost first; the outermost unwrapped) and
-// leftover units.
-RowsGeom rows_geom(const RowsView &v, bool vec, uint64_t step) {
-    RowsGeom g{};
-    g.rows = v.rows;
-    g.cols = v.cols;
-    g.units = vec ? ceil_div(v.cols, 4) : v.cols;
-    g.ustride = vec ? 4 : v.cstride;
-    g.units_span = (int64_t)g.units * g.ustride;
-    g.clstride = v.clstride;
-    g.lustride = vec ? 4 * v.clstride : v.clstride;
-    g.lunits_span = (int64_t)g.units * g.lustride;
-    g.orank = v.orank;
-    for (int k = 0; k < 3; ++k) {
-        g.oshape[k] = v.oshape[k];
-        g.ostride[k] = v.ostride[k];
-        g.ospan[k] = (int64_t)v.oshape[k] * v.ostride[k];
-        g.olstride[k] = v.olstride[k];
-        g.olspan[k] = (int64_t)v.oshape[k] * v.olstride[k];
-    }
-    g.step_units = step % g.units;
-    g.step_rows = step / g.units;
-    g.step_uoff = (int64_t)g.step_units * g.ustride;
-    g.step_luoff = (int64_t)g.step_units * g.lustride;
-    uint64_t r = g.step_rows;
-    for (uint32_t k = 0; k < 3; ++k) {
-        if (k + 1 < g.orank) {
-            g.step_digits[k] = r % g.oshape[k];
-            r /= g.oshape[k];
-        } else if (k + 1 == g.orank) {
-            g.step_digits[k] = r;
-            r = 0;
-        } else {
-            g.step_digits[k] = 0;
-        }
-        if (k < g.orank) {
-            g.step_off += (int64_t)g.step_digits[k] * g.ostride[k];
-            g.step_loff += (int64_t)g.step_digits[k] * g.olstride[k];
-        }
-    }
-    return g;
 }
 
 template <typename T, int K, bool AFFINE>

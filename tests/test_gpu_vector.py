@@ -242,3 +242,52 @@ def test_vector_forms_at_element_offsets(device, oracle, n, offsets):
     want = np.full(n + pad, 9.0, np.float32)
     want[oo:oo + n] = s[os_:os_ + n] * s[ot:ot + n]
     assert np.array_equal(device.download_owned(out), want)
+
+
+# Pairs of same-shape views walked as rows (layout_rows_pair): dimensions
+# merge only where both operands allow it; 16-byte units only where both
+# have contiguous rows.  (a layout, b layout) as (shape, a strides, a offset,
+# b strides, b offset).
+PAIR_VIEWS = [
+    ([64, 1000], [1003, 1], 5, [1000, 1], 0),        # slice . dense: vector units
+    ([64, 1001], [1003, 1], 1, [1001, 1], 2),        # ragged rows, both contiguous
+    ([7, 9, 13], [200, 20, 1], 3, [117, 13, 1], 0),  # rank 3: a slice, b dense (merges for b only)
+    ([3, 4, 5, 6], [400, 90, 15, 1], 2, [360, 90, 18, 1], 1),
+    ([50, 40], [1, 50], 0, [40, 1], 0),              # transposed . dense: element walk
+    ([40, 33], [-40, 1], 1563, [33, 1], 0),          # reversed rows
+    ([500], [3], 4, [-2, ], 1200),                   # stride 3 . stride -2
+    ([300, 3], [7, 1], 1, [3, 1], 0),                # rows of 3
+]
+
+
+def _elems(host, shape, strides, offset):
+    idx = offset + sum(np.indices(shape)[d] * strides[d] for d in range(len(shape)))
+    return np.ascontiguousarray(host[idx.ravel()])
+
+
+@pytest.mark.parametrize("view", PAIR_VIEWS, ids=lambda v: "x".join(map(str, v[0])) + f"_{v[1]}_{v[3]}")
+@pytest.mark.parametrize("dtype", [np.float32, np.int32])
+def test_map_reductions_of_strided_views(device, oracle, view, dtype):
+    shape, sa, oa, sb, ob = view
+    size = 70000
+    if dtype == np.float32:
+        host = oracle.uniform_real(size, seed=sum(shape), lo=-2.0, hi=2.0)
+    else:
+        host = oracle.uniform_int(size, seed=sum(shape), lo=-1000, hi=1000, dtype=np.int32)
+    buf = device.upload(host)
+    la, lb = Layout.try_new(shape, sa, oa), Layout.try_new(shape, sb, ob)
+    xa, xb = _elems(host, shape, sa, oa), _elems(host, shape, sb, ob)
+    n = xa.size
+    va, vb = StridedView(buf, la), StridedView(buf, lb)
+    if dtype == np.float32:
+        want, mags = oracle.dot(xa, xb)
+        got = float(one(device, hx.dot(device, va, vb)))
+        assert abs(got - want) <= f32_bound(n, mags) + abs(want) * EPS / 2, (got, want)
+        l1 = oracle.norm_l1(xa)
+        assert abs(float(one(device, hx.norm_l1(device, va))) - l1) <= f32_bound(n, l1) + l1 * EPS
+        l2 = oracle.norm_l2(xa)
+        assert abs(float(one(device, hx.norm_l2(device, va))) - l2) <= l2 * 2 * EPS + 1e-30
+    else:
+        assert one(device, hx.dot(device, va, vb)) == oracle.dot(xa, xb)
+        assert one(device, hx.norm_l1(device, va)) == oracle.norm_l1(xa)
+    assert one(device, hx.norm_max(device, va)) == oracle.norm_max(xa)
