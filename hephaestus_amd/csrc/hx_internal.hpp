@@ -23,7 +23,8 @@ struct LookbackState {
 };
 
 // The buffers the immediate (un-prepared) entry points use on ONE stream:
-//   ws       header + full-reduce partials + look-back status words;
+//   ws       header + tagged status words (look-back statuses and the
+//            partial slots of the one-launch grid folds);
 //   scratch  partials staged outside any look-back protocol (split axis
 //            reductions, chunked column scans, segmented tile maps and
 //            worklists), kept apart from `ws` so those writes never land on

@@ -9,8 +9,8 @@
 // device is opened (hx_device_open calls lookup_noalloc_scratch) and kept in
 // the device handle; kernels and the clear kernel receive that pointer.
 //
-// The layout is that of a scan workspace: 256-byte header, 64 KiB partials
-// area, look-back status words (or, for chunked column scans, chunk totals).
+// The layout is that of a scan workspace: 256-byte header, then look-back
+// status words (or, for chunked column scans, chunk totals).
 // The array keeps the last call's contents, so every look-back call first
 // clears the status words it will use with a fill kernel (no
 // hipMemsetAsync, which a captured graph may replay wrongly) and then runs
