@@ -21,8 +21,10 @@ of the GPU output.  "ceiling" times the best read+write streams on the same
 device in the same run: the library's copy kernel and the runtime's
 hipMemcpyAsync device-to-device blit, 1 GiB each way.
 
-Timing: HIP events on the device stream, which every launch here uses.  The
-mean comes from one pair of events around `steps` back-to-back launches;
+Timing: HIP events on the device stream, which every launch here uses.  Each
+configuration first runs untimed for --settle-ms of device time (100 ms by
+default; its first launches after set-up run slow), then `warmup` untimed
+launches.  The mean comes from one pair of events around `steps` back-to-back launches;
 median and minimum from five further batches of steps/5 back-to-back
 launches, each between its own pair of events.  GB/s = algorithmic bytes per
 launch / mean time per launch.
@@ -60,12 +62,44 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# Untimed device time spent on each configuration before its warm-up steps.
+# A configuration's first launches after its set-up run slow, and the timed
+# region must see the steady state: measured on MI355X in batches of 10
+# launches, the first batch of each ran 2-5x its steady time (segmented sum
+# 185.8 us per launch against 85.0, the scan 1684 against 355), and the f32
+# sum at 2^28 took 158 us per launch for its first ~60 ms before settling at
+# 151.  With 10 warm-up launches alone, the segmented sum's mean over 100
+# timed launches came out at 91.8 us against a median of 85.5.
+SETTLE_MS = 100.0
+
+
+def settle(dev, run, ms: float, chunk: int = 10, max_launches: int = 100000) -> int:
+    """Launches `run` untimed, `chunk` at a time, until `ms` of device time
+    has passed; returns the number of launches."""
+    if ms <= 0:
+        return 0
+    start, stop = dev.event(), dev.event()
+    start.record()
+    n = 0
+    while n < max_launches:
+        for _ in range(chunk):
+            run()
+        n += chunk
+        stop.record()
+        stop.synchronize()
+        if start.elapsed_ms(stop) >= ms:
+            break
+    return n
+
+
 def time_launches(dev, run, steps: int, warmup: int, batches: int = 5) -> dict:
     """Milliseconds per launch of `run`: the mean over one pair of events
     around `steps` back-to-back launches, then the median and minimum over
     `batches` further batches of steps/batches back-to-back launches, each
     between a pair of events.  (An event between every two launches would
-    add its own fence to each launch.)"""
+    add its own fence to each launch.)  The settle launches and the
+    `warmup` launches before them are untimed."""
+    settled = settle(dev, run, SETTLE_MS)
     for _ in range(warmup):
         run()
     dev.synchronize()
@@ -86,11 +120,12 @@ def time_launches(dev, run, steps: int, warmup: int, batches: int = 5) -> dict:
     evs[-1].synchronize()
     per = [evs[b].elapsed_ms(evs[b + 1]) / per_batch for b in range(batches)]
     dev.synchronize()
-    return {"mean_ms": mean, "median_ms": statistics.median(per), "min_ms": min(per)}
+    return {"mean_ms": mean, "median_ms": statistics.median(per), "min_ms": min(per), "settle_launches": settled}
 
 
 def time_plan(dev, run, steps: int, warmup: int) -> float:
     """Mean milliseconds per launch (time_launches' first pass only)."""
+    settle(dev, run, SETTLE_MS)
     for _ in range(warmup):
         run()
     dev.synchronize()
@@ -557,20 +592,38 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
     """Markdown summary of a `rocprofv3 --kernel-trace --stats` run of the
     default bench: per kernel and launch grid, calls and the mean, median,
     minimum and maximum duration, then per configuration the step time (its
-    kernels' means added) beside the bench's own event-timed mean."""
+    kernels' means added, over the launches the bench timed) beside the
+    bench's own event-timed mean."""
     import csv
 
     files = sorted(root.rglob("*kernel_trace.csv"))
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {root}")
-    groups: dict = {}
+    starts: dict = {}
     for f in files:
         with open(f, newline="") as fh:
             for r in csv.DictReader(fh):
                 key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
-                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+                starts.setdefault(key, []).append((t0, (t1 - t0) / 1e3))
+    # Every group's durations in launch order.
+    groups = {k: [d for _, d in sorted(v)] for k, v in starts.items()}
     bench = json.loads(bench_json.read_text()) if bench_json else None
     sec = (bench or {}).get("secondary", {})
+    ceil = (bench or {}).get("ceiling", {})
+    warm = int((bench or {}).get("warmup", 0))
+    # Untimed launches at the start of each configuration (settle, then
+    # warm-up): the step times below skip them, so they cover the launches
+    # the bench's events timed.
+    untimed = {"scan_u32": (bench or {}).get("timing", {}).get("settle_launches", 0),
+               "sum_f32": sec.get("f32_sum_reduce_2_28", {}).get("settle_launches", 0),
+               "sum_f32_2_20": sec.get("cfg1_f32_sum_2_20", {}).get("settle_launches", 0),
+               "rows_f32": sec.get("cfg3_rows_f32_65536x4096", {}).get("settle_launches", 0),
+               "segmented_i32": sec.get("cfg4_segmented_i32_2_27", {}).get("settle_launches", 0),
+               "scan_f32_2_30": sec.get("cfg5_scan_f32_2_30", {}).get("settle_launches", 0),
+               "copy_u32": ceil.get("copy_kernel", {}).get("settle_launches", 0),
+               "blit": ceil.get("runtime_blit_hipMemcpyAsync", {}).get("settle_launches", 0)}
+    untimed = {k: int(v or 0) + warm for k, v in untimed.items()} if bench else {}
     bench_ms = {"scan_u32": (bench or {}).get("ms_per_step"),
                 "sum_f32": sec.get("f32_sum_reduce_2_28", {}).get("ms_per_launch"),
                 "sum_f32_2_20": sec.get("cfg1_f32_sum_2_20", {}).get("ms_per_launch"),
@@ -587,9 +640,9 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
         short = short if len(short) <= 110 else short[:110] + "..."
         lines.append(f"| `{short}` | {grid} | {len(d)} | {statistics.mean(d):.1f} | {statistics.median(d):.1f} | "
                      f"{min(d):.1f} | {max(d):.1f} |")
-    lines += ["", "| configuration | kernels per step | trace: step us (means added) | trace: step us (medians added) "
-                  "| bench: event-timed us per step | trace frac | bench frac |",
-              "|---|---|---:|---:|---:|---:|---:|"]
+    lines += ["", "| configuration | kernels per step | untimed launches skipped | trace: step us (means added) "
+                  "| trace: step us (medians added) | bench: event-timed us per step | trace frac | bench frac |",
+              "|---|---|---:|---:|---:|---:|---:|---:|"]
     for key, label, kernels, nbytes in TRACE_CONFIGS:
         nbytes = seg_bytes if key == "segmented_i32" else nbytes
         mean_sum = med_sum = 0.0
@@ -599,7 +652,11 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
             if not ds:
                 found = False
                 break
-            d = [x for lst in ds for x in lst]
+            skip = untimed.get(key, 0)
+            d = [x for lst in ds for x in lst[skip:]]
+            if not d:
+                found = False
+                break
             mean_sum += statistics.mean(d)
             med_sum += statistics.median(d)
         if not found:
@@ -607,7 +664,7 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
         b = bench_ms.get(key)
         tf = f"{nbytes / (mean_sum * 1e-6) / 8e12:.4f}" if nbytes else "-"
         bf = f"{nbytes / (b * 1e-3) / 8e12:.4f}" if (nbytes and b) else "-"
-        lines.append(f"| {label} | {len(kernels)} | {mean_sum:.1f} | {med_sum:.1f} | "
+        lines.append(f"| {label} | {len(kernels)} | {untimed.get(key, 0)} | {mean_sum:.1f} | {med_sum:.1f} | "
                      f"{b * 1e3 if b else float('nan'):.1f} | {tf} | {bf} |")
     print("\n".join(lines))
     return 0
@@ -736,7 +793,8 @@ def run_config(name, hx, dev, args, cpu_seconds):
     rec = {"value": round(gbs(w["bytes"], t["mean_ms"]), 1), "unit": "GB/s", "dtype": w["dtype"],
            "workload": w["workload"], "n": w["n"], "algorithmic_bytes_per_launch": w["bytes"], "steps": steps,
            "ms_per_launch": round(t["mean_ms"], 5), "median_ms": round(t["median_ms"], 5),
-           "min_ms": round(t["min_ms"], 5), "elements_per_s": round(w["n"] / (t["mean_ms"] * 1e-3), 1),
+           "min_ms": round(t["min_ms"], 5), "settle_launches": t["settle_launches"],
+           "elements_per_s": round(w["n"] / (t["mean_ms"] * 1e-3), 1),
            "roofline": roofline(w["bytes"], t["mean_ms"], name)}
     if w["verify"] is not None:
         rec["gpu_output_check"] = w["verify"]()
@@ -760,7 +818,10 @@ def main() -> int:
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="summarise a rocprofv3 --kernel-trace run of the default bench under DIR and exit")
     ap.add_argument("--bench-json", metavar="FILE", help="with --trace-summary: that run's bench JSON line")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed device time per configuration before its warm-up steps")
     args = ap.parse_args()
+    globals()["SETTLE_MS"] = args.settle_ms
     if args.pmc_summary:
         return pmc_summary(Path(args.pmc_summary))
     if args.trace_summary:
@@ -830,7 +891,8 @@ def main() -> int:
         "config": {"workload": head["workload"], "n": head["n"],
                    "algorithmic_bytes_per_step": head["algorithmic_bytes_per_launch"],
                    "elements_per_s": head["elements_per_s"]},
-        "timing": {"mean_ms": head["ms_per_launch"], "median_ms": head["median_ms"], "min_ms": head["min_ms"]},
+        "timing": {"mean_ms": head["ms_per_launch"], "median_ms": head["median_ms"], "min_ms": head["min_ms"],
+                   "settle_ms": SETTLE_MS, "settle_launches": head["settle_launches"]},
         "roofline": head["roofline"],
     }
     if "cpu_baseline" in head:
