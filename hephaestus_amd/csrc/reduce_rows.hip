@@ -45,6 +45,12 @@ enum Flag : int {
     F_MEAN = 32,
 };
 
+// Waves per fold block (split_fold_kernel, cols_block_kernel), and the most
+// statistic planes a reduction keeps (sum or mean, product, max or argmax,
+// min).
+constexpr int kFoldSlices = 16;
+constexpr int kMaxPlanes = 4;
+
 struct RowParams {
     const void *base;
     uint64_t rows, cols;
@@ -368,7 +374,6 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     static_assert(kBlock % G == 0, "whole row groups per block");
     constexpr int kRowsPerBlock = kBlock / G;
     constexpr int kParts = G > kWave ? G / kWave : 1;
-    constexpr int kMaxPlanes = 4;
     __shared__ uint64_t sh[G > kWave ? kMaxPlanes * kBlock : 1];
     const int t = threadIdx.x;
     const int gl = t % G;
@@ -399,26 +404,14 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     if (gl == 0 && r < p.rows) st.write(p, r);
 }
 
-// Column tiles (the reduced axis is strided, the outputs adjacent: axis-0
-// reduction of a row-major matrix).  A wave owns 64*V adjacent outputs --
-// V = 4 gives every lane one 16-byte load per line, so each load instruction
-// of a wave covers 1 KiB of one line -- and one chunk of the reduced axis,
-// kU lines in flight per lane.  Adjacent waves take adjacent output groups
-// of the same chunk.  SPLIT: the chunk's statistics go to partial planes
-// that split_fold_kernel combines in chunk order; otherwise the wave covers
-// the whole axis and writes the outputs.
-template <typename T, bool AFFINE, int FLAGS, int V, bool SPLIT>
-__global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
-                                                            uint32_t nchunks, uint64_t groups) {
+// Statistics of lines [j0, j1) of the 64*V adjacent outputs from o0 (V per
+// lane) of a column tile, kU lines in flight per lane: V = 4 gives every
+// lane one 16-byte load per line, so each load instruction of a wave covers
+// 1 KiB of one line.
+template <typename T, bool AFFINE, int FLAGS, int V>
+__device__ __forceinline__ void cols_walk(const RowParams &p, uint64_t o0, uint64_t j0, uint64_t j1,
+                                          Stats<T, FLAGS> (&st)[V]) {
     constexpr int kU = V == 4 ? 8 : 16;
-    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
-    if (w >= groups * nchunks) return;
-    const uint64_t g = w % groups, k = w / groups;
-    const uint64_t o0 = (g * kWave + (uint64_t)lane_id()) * V;
-    if (o0 >= p.rows) return;
-    const uint64_t j0 = k * chunk;
-    const uint64_t j1 = j0 + chunk < p.cols ? j0 + chunk : p.cols;
-    Stats<T, FLAGS> st[V];
     const T *base = (const T *)p.base + ((int64_t)p.offset + (int64_t)o0 * p.row_stride);
     uint64_t j = j0;
     if constexpr (V == 4) {
@@ -450,12 +443,66 @@ __global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_
             st[0].visit(prologue<T, AFFINE>(__builtin_nontemporal_load(base + (int64_t)j * p.col_stride), p.a, p.b),
                         (uint32_t)j);
     }
+}
+
+// Column tiles (the reduced axis is strided, the outputs adjacent: axis-0
+// reduction of a row-major matrix).  A wave owns 64*V adjacent outputs and
+// one chunk of the reduced axis (cols_walk).  Adjacent waves take adjacent
+// output groups of the same chunk.  SPLIT: the chunk's statistics go to
+// partial planes that split_fold_kernel combines in chunk order; otherwise
+// the wave covers the whole axis and writes the outputs.
+template <typename T, bool AFFINE, int FLAGS, int V, bool SPLIT>
+__global__ __launch_bounds__(kBlock) void cols_tiles_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
+                                                            uint32_t nchunks, uint64_t groups) {
+    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
+    if (w >= groups * nchunks) return;
+    const uint64_t g = w % groups, k = w / groups;
+    const uint64_t o0 = (g * kWave + (uint64_t)lane_id()) * V;
+    if (o0 >= p.rows) return;
+    const uint64_t j0 = k * chunk;
+    const uint64_t j1 = j0 + chunk < p.cols ? j0 + chunk : p.cols;
+    Stats<T, FLAGS> st[V];
+    cols_walk<T, AFFINE, FLAGS, V>(p, o0, j0, j1, st);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         if constexpr (SPLIT)
             st[v].store_partial(partials + k * p.rows + o0 + v, (uint64_t)nchunks * p.rows);
         else
             st[v].write(p, o0 + v);
+    }
+}
+
+// Small column reductions in one launch, with no workspace: a block of
+// kFoldSlices waves per output group, wave s walking slice s of the reduced
+// axis (`chunk` lines), then lane o of wave 0 folding the slices' statistics
+// through LDS in slice order, one component at a time, and writing the
+// outputs.  The order depends only on the shape, so f32 sums are bitwise
+// reproducible.  The split form (column tiles into partial planes, then
+// split_fold_kernel) takes two launches; on a 256 x 256 f32 axis-0 sum that
+// is about 6 us per call, each launch costing a few microseconds of host and
+// device time whatever its size.
+template <typename T, bool AFFINE, int FLAGS, int V>
+__global__ __launch_bounds__(kWave *kFoldSlices) void cols_block_kernel(RowParams p, uint64_t chunk) {
+    __shared__ uint64_t sh[kMaxPlanes * kFoldSlices * kWave];
+    const int lane = lane_id();
+    const int s = threadIdx.x / kWave;
+    const uint64_t o0 = ((uint64_t)blockIdx.x * kWave + (uint64_t)lane) * V;
+    const bool live = o0 < p.rows; // V = 4 only when rows % 4 == 0: all four outputs exist
+    const uint64_t j0 = (uint64_t)s * chunk < p.cols ? (uint64_t)s * chunk : p.cols;
+    const uint64_t j1 = j0 + chunk < p.cols ? j0 + chunk : p.cols;
+    Stats<T, FLAGS> st[V];
+    if (live) cols_walk<T, AFFINE, FLAGS, V>(p, o0, j0, j1, st);
+    constexpr uint64_t kPlane = (uint64_t)kFoldSlices * kWave;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        st[v].store_partial(&sh[s * kWave + lane], kPlane);
+        __syncthreads();
+        if (s == 0 && live) {
+            Stats<T, FLAGS> total;
+            for (int q = 0; q < kFoldSlices; ++q) total.merge_partial(&sh[q * kWave + lane], kPlane);
+            total.write(p, o0 + v);
+        }
+        __syncthreads();
     }
 }
 
@@ -561,8 +608,6 @@ __global__ __launch_bounds__(kBlock) void rows_split_kernel(RowParams p, uint64_
 // waves; wave s folds its contiguous range of chunks in order, then lane o of
 // wave 0 folds the slice results in slice order.  The order depends only on
 // the chunk count, so f32 sums do not depend on scheduling.
-constexpr int kFoldSlices = 16;
-constexpr int kMaxPlanes = 4;
 
 template <typename T, int FLAGS>
 __global__ __launch_bounds__(kWave *kFoldSlices) void split_fold_kernel(RowParams p, const uint64_t *partials,
@@ -605,8 +650,15 @@ bool narrow_columns(const RowParams &p, uintptr_t base) {
            base % 4 == 0 && (p.cols * c) % 4 == 0 && p.cols <= 0xFFFFFFFFull;
 }
 
+// Column reductions that would split their axis take one launch
+// (cols_block_kernel) when the matrix is small: at most kBlockFoldLines lines
+// (64 per wave) and kBlockFoldElems elements.
+constexpr uint64_t kBlockFoldLines = 64 * kFoldSlices;
+constexpr uint64_t kBlockFoldElems = 1ull << 20;
+
 struct Shape {
     bool cols = false, vec = false, narrow = false;
+    bool block = false; // cols_block_kernel: one launch, no partials
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
     uint64_t groups = 0, chunk = 0;
@@ -669,6 +721,12 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         }
     }
     if (k < 1) k = 1;
+    if (cols_layout && k > 1 && p.cols <= kBlockFoldLines && p.rows * p.cols <= kBlockFoldElems) {
+        s.block = true;
+        s.chunk = ceil_div(p.cols, (uint64_t)kFoldSlices);
+        s.nchunks = 1;
+        return s;
+    }
     if (k > 1) {
         uint64_t chunk = ceil_div(p.cols, k);
         if (!cols_layout) chunk = ceil_div(chunk, 256) * 256; // whole 1 KiB wave loads per chunk
@@ -705,6 +763,14 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
         hipLaunchKernelGGL((cols_narrow_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
                            s.chunk, s.nchunks);
         HX_TRY(check_launch("cols_narrow_kernel"));
+    } else if (s.block) {
+        if (s.groups > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");
+        const dim3 grid((uint32_t)s.groups), block(kWave * kFoldSlices);
+        if (s.vec)
+            hipLaunchKernelGGL((cols_block_kernel<T, AFFINE, FLAGS, 4>), grid, block, 0, stream, p, s.chunk);
+        else
+            hipLaunchKernelGGL((cols_block_kernel<T, AFFINE, FLAGS, 1>), grid, block, 0, stream, p, s.chunk);
+        return check_launch("cols_block_kernel");
     } else if (cols_layout) {
         const uint64_t waves = s.groups * s.nchunks;
         const uint64_t blocks = ceil_div(waves, kBlock / kWave);

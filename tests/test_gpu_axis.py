@@ -139,6 +139,46 @@ def test_axis_reduce_transposed_and_reversed_views(device, oracle, op):
     check(oracle, op, np.float32, got, lines_of(host, shape, strides, offset, 0))
 
 
+# Axis-0 reductions of small matrices (at most 1024 lines and 2^20 elements,
+# more than 32 lines) take one launch: a block of 16 waves per group of
+# outputs, each wave walking a slice of the axis, the slices folded in LDS.
+# [1000, 300] and [1024, 1024] have 16-byte lanes (outputs a multiple of 4),
+# [999, 1049] and [77, 5] one output per lane; [1025, 1000] is past the line
+# limit and takes the two-launch split.
+SMALL_COLUMN_SHAPES = [(256, 256), (1000, 300), (1024, 1024), (999, 1049), (77, 5), (33, 64), (1025, 1000)]
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("shape", SMALL_COLUMN_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_small_column_reductions(device, oracle, shape, dtype, op):
+    r, c = shape
+    host = host_for(oracle, dtype, r * c, seed=7 * r + c, op=op)
+    got = run_axis(device, op, dtype, host, shape, (c, 1), 0, 0)
+    check(oracle, op, dtype, got, lines_of(host, shape, (c, 1), 0, 0))
+
+
+@pytest.mark.parametrize("op", ["sum", "max", "argmax", "min"])
+def test_small_column_reductions_of_strided_views(device, oracle, op):
+    r, c = 200, 516
+    host = host_for(oracle, np.float32, r * c + 3, seed=17, op=op)
+    # axis 1 of a column-major view: the outputs are adjacent, the axis strided
+    shape, strides = (c, r), (1, c)
+    got = run_axis(device, op, np.float32, host, shape, strides, 0, 1)
+    check(oracle, op, np.float32, got, lines_of(host, shape, strides, 0, 1))
+    # outputs walking backwards, and a view that starts 3 elements in
+    for shape, strides, offset in (((r, c), (c, -1), c - 1), ((r, c), (c, 1), 3)):
+        got = run_axis(device, op, np.float32, host, shape, strides, offset, 0)
+        check(oracle, op, np.float32, got, lines_of(host, shape, strides, offset, 0))
+
+
+def test_small_column_f32_sums_are_deterministic(device, oracle):
+    host = oracle.normal(1000 * 300, seed=23)
+    a = run_axis(device, "sum", np.float32, host, (1000, 300), (300, 1), 0, 0)
+    b = run_axis(device, "sum", np.float32, host, (1000, 300), (300, 1), 0, 0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("op", ["sum", "argmax", "min"])
 @pytest.mark.parametrize("offset", [4, 1])
 def test_narrow_columns_offset_views(device, oracle, op, offset):
