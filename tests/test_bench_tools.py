@@ -70,7 +70,7 @@ class _FakeEvent:
         self.t = self.clock["ms"]
 
     def synchronize(self):
-        pass
+        self.clock["syncs"] += 1
 
     def elapsed_ms(self, other):
         return other.t - self.t
@@ -80,9 +80,13 @@ class _FakeDevice:
     """Each launch advances a fake device clock by `ms_per_launch`."""
 
     def __init__(self, ms_per_launch):
-        self.clock = {"ms": 0.0}
+        self.clock = {"ms": 0.0, "syncs": 0}
         self.ms = ms_per_launch
         self.launches = 0
+
+    @property
+    def syncs(self):
+        return self.clock["syncs"]
 
     def event(self):
         return _FakeEvent(self.clock)
@@ -99,7 +103,10 @@ def test_settle_runs_until_its_device_time_has_passed():
     dev = _FakeDevice(0.35)
     n = bench.settle(dev, dev.launch, 100.0)
     assert n == dev.launches
-    assert n % 10 == 0 and (n - 10) * 0.35 < 100.0 <= n * 0.35
+    # just past 100 ms of device time, in two batches: the 10-launch
+    # calibration, then the rest back to back
+    assert 100.0 <= n * 0.35 <= 100.0 + 2 * 0.35
+    assert dev.syncs == 2
     assert bench.settle(dev, dev.launch, 0.0) == 0
 
 
