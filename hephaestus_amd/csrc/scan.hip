@@ -744,184 +744,363 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
 //   col_narrow_carry_kernel   per column, an exclusive scan of its totals;
 //   col_narrow_scan_kernel    every chunk rescanned from its carries.
 // f32 steps scan in f32 and add f64 carries; integers wrap.
-template <typename T, bool REV>
-__device__ __forceinline__ void narrow_load(const T *base, uint64_t nvec, uint64_t g, T (&x)[4]) {
-    using V = typename Vec4A4<T>::type;
-    const V *src = (const V *)base;
-    if constexpr (REV) {
-        const V q = __builtin_nontemporal_load(&src[nvec - 1 - g]);
-        x[0] = (T)q.w;
-        x[1] = (T)q.z;
-        x[2] = (T)q.y;
-        x[3] = (T)q.x;
-    } else {
-        const V q = __builtin_nontemporal_load(&src[g]);
-        x[0] = (T)q.x;
-        x[1] = (T)q.y;
-        x[2] = (T)q.z;
-        x[3] = (T)q.w;
-    }
-}
-template <typename T, bool REV>
-__device__ __forceinline__ void narrow_store(T *base, uint64_t nvec, uint64_t g, const T (&y)[4]) {
-    using V = typename Vec4A4<T>::type;
-    V *dst = (V *)base;
-    V q;
-    if constexpr (REV) {
-        q.w = y[0];
-        q.z = y[1];
-        q.y = y[2];
-        q.x = y[3];
-        __builtin_nontemporal_store(q, &dst[nvec - 1 - g]);
-    } else {
-        q.x = y[0];
-        q.y = y[1];
-        q.z = y[2];
-        q.w = y[3];
-        __builtin_nontemporal_store(q, &dst[g]);
-    }
-}
-// Column of lane l's component k (C a power of two dividing 256).
-template <bool REV> __device__ __forceinline__ uint32_t narrow_col(int lane, int k, uint32_t C) {
-    const uint32_t c = (uint32_t)(4 * lane + k) & (C - 1);
-    return REV ? C - 1 - c : c;
+// Narrow column scans: axis 0 of a dense row-major [R, C] matrix, C a power
+// of two from 4 to 128, read as the one contiguous range of 16-byte vectors
+// it is.  Component k of vector g holds column (4g + k) mod C, and since C
+// divides 256 that is column (4l + k) mod C for lane l of every step: a lane
+// always holds the same four columns, and the lanes of one column in a step
+// are l, l + s, l + 2s, ... with s = C / 4 (a "class").  A reverse scan
+// mirrors the range (logical vector g is physical vector nvec - 1 - g, its
+// components reversed), so every pass works in logical order and logical
+// columns.  Tiles are 12 waves x 16 steps of 64 vectors (192 KiB, one block
+// per CU at up to 168 VGPRs), each wave streaming its own 16 KiB run with all
+// 16 loads in flight.  Three passes: tile totals per column (one read), an exclusive
+// scan of the tile totals per column, and the rescan (one read, one write).
+constexpr int kNarrowWaves = 12, kNarrowSteps = 16;
+constexpr uint64_t kNarrowTileVecs = (uint64_t)kNarrowWaves * kNarrowSteps * kWave;
+
+// Lane permutes for the class scans: lane l reads lane src(l), src given as
+// a byte address (4 * lane), 32-bit values.
+template <typename A> __device__ __forceinline__ A lane_permute(A v, int addr) {
+    static_assert(sizeof(A) == 4, "32-bit lanes");
+    return __builtin_bit_cast(A, __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v)));
 }
 
+// Byte addresses of the lanes a class scan reads, per lane (S = C / 4 >= 2):
+// its class's last lane in the row below and in row 1 (S <= 16) or the lane
+// 32 below (S = 32), its class's last lane in the wave, and the lane S below.
+struct ClassLanes {
+    int below, row1, last, prev;
+    template <int S> __device__ __forceinline__ void init(int lane) {
+        const int c = lane & (S - 1);
+        if constexpr (S <= 16) {
+            below = 4 * (((lane & ~15) - S + c) & (kWave - 1));
+            row1 = 4 * (32 - S + c);
+        } else {
+            below = 4 * (lane & 31);
+            row1 = 0;
+        }
+        last = 4 * (kWave - S + c);
+        prev = 4 * ((lane - S) & (kWave - 1));
+    }
+};
+
+// Inclusive scan over the lanes of each class l mod S (S = 1, 2, 4, ..., 32):
+// lane l ends with the combination, in lane order, of the lanes l' <= l with
+// l' = l (mod S).  Distances S..8 inside each row of 16 lanes are DPP row
+// shifts; the class totals of lower rows then come in with two lane permutes
+// (rows 1 and 3 take their class's last lane of the row below; rows 2 and 3
+// then take its last lane of row 1).  S = 1 is the plain wave scan.  32-bit
+// values.
+template <int S, typename Op, typename A>
+__device__ __forceinline__ A class_inclusive_scan(A v, int lane, const ClassLanes &cl) {
+    if constexpr (S == 1) {
+        return wave_inclusive_scan<Op, A>(v);
+    } else {
+        const A id = Op::template identity<A>();
+        if constexpr (S <= 2) v = Op::combine(dpp_move<kDppRowShr2>(id, v), v);
+        if constexpr (S <= 4) v = Op::combine(dpp_move<kDppRowShr4>(id, v), v);
+        if constexpr (S <= 8) v = Op::combine(dpp_move<kDppRowShr8>(id, v), v);
+        if constexpr (S <= 16) {
+            const A below = lane_permute(v, cl.below);
+            v = (lane & 16) ? Op::combine(below, v) : v;
+            const A row1 = lane_permute(v, cl.row1);
+            v = lane >= 32 ? Op::combine(row1, v) : v;
+        } else {
+            const A half = lane_permute(v, cl.below);
+            v = lane >= 32 ? Op::combine(half, v) : v;
+        }
+        return v;
+    }
+}
+// The class total (the inclusive value of the class's last lane).
+template <int S, typename A> __device__ __forceinline__ A class_total(A incl, const ClassLanes &cl) {
+    if constexpr (S == 1) return read_lane(incl, kWave - 1);
+    else return lane_permute(incl, cl.last);
+}
+// Exclusive form: lane l takes lane l - S's inclusive value, the first S
+// lanes the identity.
+template <int S, typename Op, typename A>
+__device__ __forceinline__ A class_shift(A incl, int lane, const ClassLanes &cl) {
+    if constexpr (S == 1) {
+        return wave_shift_right<Op, A>(incl);
+    } else {
+        const A t = lane_permute(incl, cl.prev);
+        return lane >= S ? t : Op::template identity<A>();
+    }
+}
+
+// The rescan's in-wave part for class stride S: each step's components
+// scanned over their classes, x[j][k] replaced by the lane's running class
+// total before the step combined with its (inclusive or exclusive) class
+// prefix; run[k] ends with the wave's total of the lane's column k.  All in
+// T: an f32 wave prefix covers at most 16 steps of 64 values, and the
+// carries into the wave are added in f64 afterwards.
+template <int S, typename T, typename Op, bool EXCL>
+__device__ __forceinline__ void narrow_wave_scan(T (&x)[16][4], T (&run)[4], int lane) {
+    ClassLanes cl;
+    if constexpr (S > 1) cl.template init<S>(lane);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const T incl = class_inclusive_scan<S, Op, T>(x[j][k], lane, cl);
+            const T tot = class_total<S, T>(incl, cl);
+            const T pre = EXCL ? class_shift<S, Op, T>(incl, lane, cl) : incl;
+            x[j][k] = Op::combine(run[k], pre);
+            run[k] = Op::combine(run[k], tot);
+        }
+        // One step's four class scans at a time, to bound live registers.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Lane `lane`, wave `w` of tile `t`: its 16 logical vectors (steps j), whole
+// tiles through one block-uniform base and a 32-bit lane offset, the last
+// tile checked (identity past the end).
+template <typename T, bool REV>
+__device__ __forceinline__ void narrow_tile_load(const T *in, uint64_t nvec, uint64_t t, int w, int lane, T ident,
+                                                 T (&x)[kNarrowSteps][4]) {
+    using V = typename Vec4A4<T>::type;
+    const uint64_t g0 = t * kNarrowTileVecs + (uint64_t)w * (kNarrowSteps * kWave) + (uint64_t)lane;
+    if ((t + 1) * kNarrowTileVecs <= nvec) {
+        const uint32_t lane_off = ((uint32_t)__builtin_amdgcn_readfirstlane(w) * (kNarrowSteps * kWave) +
+                                   (uint32_t)lane) * 16u;
+        if constexpr (REV) {
+            const char *base = (const char *)(in + 4 * (nvec - (t + 1) * kNarrowTileVecs));
+            const uint32_t rev_off = (uint32_t)(kNarrowTileVecs * 16 - 16) - lane_off;
+#pragma unroll
+            for (int j = 0; j < kNarrowSteps; ++j) {
+                const V q = load_a4<true>((const V *)(base + rev_off - (uint32_t)j * (kWave * 16)));
+                x[j][0] = (T)q.w;
+                x[j][1] = (T)q.z;
+                x[j][2] = (T)q.y;
+                x[j][3] = (T)q.x;
+            }
+        } else {
+            const char *base = (const char *)(in + 4 * t * kNarrowTileVecs);
+#pragma unroll
+            for (int j = 0; j < kNarrowSteps; ++j) {
+                const V q = load_a4<true>((const V *)(base + lane_off + (uint32_t)j * (kWave * 16)));
+                x[j][0] = (T)q.x;
+                x[j][1] = (T)q.y;
+                x[j][2] = (T)q.z;
+                x[j][3] = (T)q.w;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < kNarrowSteps; ++j) {
+        const uint64_t g = g0 + (uint64_t)j * kWave;
+        if (g < nvec) {
+            const V q = load_a4<true>((const V *)(in + 4 * (REV ? nvec - 1 - g : g)));
+            x[j][0] = (T)(REV ? q.w : q.x);
+            x[j][1] = (T)(REV ? q.z : q.y);
+            x[j][2] = (T)(REV ? q.y : q.z);
+            x[j][3] = (T)(REV ? q.x : q.w);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[j][k] = ident;
+        }
+    }
+}
+
+// Pass 1: the totals of tile t, one per logical column, at totals[t * C + c].
+// Each lane folds its 16 steps per component, the lanes of a class fold with
+// xor butterflies from 32 down to s, and the waves' totals fold in wave
+// order: a fixed order, so f32 totals (accumulated in f64) are reproducible.
 template <typename T, typename Op, bool REV>
-__global__ __launch_bounds__(kBlock) void col_narrow_totals_kernel(ScanParams p, typename ColAcc<T>::type *totals,
-                                                                   uint64_t chunk, uint32_t nchunks) {
+__global__ __launch_bounds__(kNarrowWaves *kWave) void col_narrow_totals_kernel(ScanParams p,
+                                                                                typename ColAcc<T>::type *totals) {
     using A = typename ColAcc<T>::type;
-    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
-    if (w >= nchunks) return; // uniform across the wave
+    __shared__ A sh[kNarrowWaves][kBlock / 2]; // C <= 128 columns
     const int lane = lane_id();
+    const int w = threadIdx.x / kWave;
     const uint32_t C = (uint32_t)p.lines;
+    const uint32_t s = C / 4;
     const uint64_t nvec = (p.len * C) >> 2;
-    const T *in = (const T *)p.in + p.in_offset;
-    const uint64_t g0 = w * chunk;
-    const uint64_t g1 = g0 + chunk < nvec ? g0 + chunk : nvec;
+    const uint64_t t = blockIdx.x;
+    T x[kNarrowSteps][4];
+    narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, Op::template identity<T>(), x);
     A acc[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] = Op::template identity<A>();
-    for (uint64_t g = g0 + lane; g < g1; g += 4 * kWave) {
-        T x[4][4];
+    for (int k = 0; k < 4; ++k) {
+        acc[k] = Op::template identity<A>();
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (g + u * kWave < g1) narrow_load<T, REV>(in, nvec, g + u * kWave, x[u]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (g + u * kWave < g1)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] = Op::combine(acc[k], (A)x[u][k]);
+        for (int j = 0; j < kNarrowSteps; ++j) acc[k] = Op::combine(acc[k], (A)x[j][k]);
     }
-    const int s = (int)(C / 4);
-    for (int m = kWave / 2; m >= s; m >>= 1)
+    for (int m = kWave / 2; m >= (int)s; m >>= 1)
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[k] = Op::combine(acc[k], __shfl_xor(acc[k], m, kWave));
-    if (lane >= s) return;
+    if (lane < (int)s)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) totals[w * C + narrow_col<REV>(lane, k, C)] = acc[k];
-}
-
-// Exclusive scan of one narrow line's chunk totals, in place: a block per
-// line, thread t folding a contiguous range of chunks, the range totals
-// combined in thread order through LDS (a fixed order, so f32 carries are
-// reproducible).  col_carry_kernel runs 64 lines per block, which left a
-// handful of lanes walking thousands of chunks (4 lines x 8192 chunks:
-// 156 us).
-template <typename A, typename Op>
-__global__ __launch_bounds__(kBlock) void col_narrow_carry_kernel(A *totals, uint64_t lines, uint32_t nchunks) {
-    __shared__ A sh[kBlock];
-    const uint64_t line = blockIdx.x;
-    const uint32_t per = (nchunks + kBlock - 1) / kBlock;
-    const uint32_t k0 = threadIdx.x * per < nchunks ? threadIdx.x * per : nchunks;
-    const uint32_t k1 = k0 + per < nchunks ? k0 + per : nchunks;
-    A t = Op::template identity<A>();
-    for (uint32_t k = k0; k < k1; ++k) t = Op::combine(t, totals[(uint64_t)k * lines + line]);
-    sh[threadIdx.x] = t;
+        for (int k = 0; k < 4; ++k) sh[w][4 * lane + k] = acc[k];
     __syncthreads();
-    A acc = Op::template identity<A>();
-    for (uint32_t q = 0; q < threadIdx.x; ++q) acc = Op::combine(acc, sh[q]);
-    for (uint32_t k = k0; k < k1; ++k) {
-        const A v = totals[(uint64_t)k * lines + line];
-        totals[(uint64_t)k * lines + line] = acc;
-        acc = Op::combine(acc, v);
+    for (uint32_t c = threadIdx.x; c < C; c += kNarrowWaves * kWave) {
+        A tot = Op::template identity<A>();
+#pragma unroll
+        for (int q = 0; q < kNarrowWaves; ++q) tot = Op::combine(tot, sh[q][c]);
+        totals[t * C + c] = tot;
     }
 }
 
-// A trip is 4 steps of 64 vectors.  The 16 values of a lane (4 steps x 4
-// components) are scanned across lanes together -- Hillis-Steele over lanes
-// l, l-s, l-2s, ..., one shuffle per value and distance, the 16 independent
-// shuffles of a distance in flight at once -- then each step's class totals
-// (the class's last lane) advance the running carries in step order.
-template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
-__global__ __launch_bounds__(kBlock) void col_narrow_scan_kernel(ScanParams p,
-                                                                 const typename ColAcc<T>::type *carries,
-                                                                 uint64_t chunk, uint32_t nchunks) {
-    using A = typename ColAcc<T>::type;
-    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
-    if (w >= nchunks) return; // uniform across the wave
+// Pass 2: per column, the exclusive scan of the tile totals in place.  A
+// block per column; thread i owns a contiguous range of tiles, loaded 8 at a
+// time with the loads of a batch in flight together (one batch, held in
+// registers, for up to 8192 tiles), its range total scanned across the block
+// in thread order, and its range rewritten.  The order depends only on the
+// tile count, so f32 carries are reproducible.  (Re-reading each value in the
+// rewrite loop made every iteration a dependent memory round trip: 17-25 us
+// per launch.)
+constexpr int kNarrowCarryThreads = 1024;
+constexpr int kNarrowCarryBatch = 8;
+template <typename A, typename Op>
+__global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A *totals, uint32_t C,
+                                                                               uint64_t ntiles) {
+    __shared__ A sh[kNarrowCarryThreads / kWave];
+    const uint64_t c = blockIdx.x;
     const int lane = lane_id();
+    const int w = threadIdx.x / kWave;
+    const uint64_t per = (ntiles + kNarrowCarryThreads - 1) / kNarrowCarryThreads;
+    const uint64_t k0 = (uint64_t)threadIdx.x * per < ntiles ? (uint64_t)threadIdx.x * per : ntiles;
+    const uint64_t k1 = k0 + per < ntiles ? k0 + per : ntiles;
+    const A id = Op::template identity<A>();
+    A v[kNarrowCarryBatch];
+    A sum = id;
+    for (uint64_t k = k0; k < k1; k += kNarrowCarryBatch) {
+#pragma unroll
+        for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? totals[(k + u) * C + c] : id;
+#pragma unroll
+        for (int u = 0; u < kNarrowCarryBatch; ++u) sum = Op::combine(sum, v[u]);
+    }
+    // Exclusive scan of the range totals in thread order: within each wave,
+    // then the wave totals through LDS.
+    A incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const A t = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl = Op::combine(t, incl);
+    }
+    if (lane == kWave - 1) sh[w] = incl;
+    __syncthreads();
+    A acc = id;
+    for (int q = 0; q < w; ++q) acc = Op::combine(acc, sh[q]);
+    const A prev = __shfl_up(incl, 1, kWave);
+    if (lane > 0) acc = Op::combine(acc, prev);
+    for (uint64_t k = k0; k < k1; k += kNarrowCarryBatch) {
+        if (per > kNarrowCarryBatch) { // the range spans several batches: reload this one
+#pragma unroll
+            for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? totals[(k + u) * C + c] : id;
+        }
+#pragma unroll
+        for (int u = 0; u < kNarrowCarryBatch; ++u) {
+            if (k + u < k1) totals[(k + u) * C + c] = acc;
+            acc = Op::combine(acc, v[u]);
+        }
+    }
+}
+
+// Pass 3: tile t rescanned from its columns' carries (pass 2), or from the
+// identity for a single tile.  Per step each component is scanned over its
+// class (class_inclusive_scan, in T), and the lane's running class totals
+// (in ColAcc: f64 for f32) advance in step order; the waves' column totals
+// combine through LDS in wave order; outputs are carry + wave prefix + local
+// prefix, stored through the stream-store path (whole tiles) or element
+// checked (the last tile).
+template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
+__global__ __launch_bounds__(kNarrowWaves *kWave) __attribute__((amdgpu_waves_per_eu(3)))
+void col_narrow_scan_kernel(
+    ScanParams p, const typename ColAcc<T>::type *carries) {
+    using A = typename ColAcc<T>::type;
+    using V = typename Vec4A4<T>::type;
+    __shared__ A sh[kNarrowWaves][kBlock / 2]; // C <= 128 columns
+    const int lane = lane_id();
+    const int w = threadIdx.x / kWave;
     const uint32_t C = (uint32_t)p.lines;
-    const int s = (int)(C / 4);
+    const uint32_t s = C / 4;
     const uint64_t nvec = (p.len * C) >> 2;
-    const T *in = (const T *)p.in + p.in_offset;
-    T *out = (T *)p.out + p.out_offset;
+    const uint64_t t = blockIdx.x;
     const T tid = Op::template identity<T>();
-    const uint64_t g0 = w * chunk;
-    const uint64_t g1 = g0 + chunk < nvec ? g0 + chunk : nvec;
-    const int last = kWave - s + (lane & (s - 1)); // last lane of this lane's class
-    A carry[4];
+    T x[kNarrowSteps][4];
+    narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, tid, x);
+
+    T run[4]; // this lane's class totals so far, per component
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        carry[k] = CARRY ? carries[w * C + narrow_col<REV>(lane, k, C)] : Op::template identity<A>();
-    // The trip count is the same for every lane (the chunk is shared), and
-    // every lane of the wave takes part in the lane scans.
-    for (uint64_t base = g0; base < g1; base += 4 * kWave) {
-        const uint64_t g = base + lane;
-        T v[4][4];
+    for (int k = 0; k < 4; ++k) run[k] = tid;
+    switch (s) { // wave-uniform: C is a launch parameter
+    case 1: narrow_wave_scan<1, T, Op, EXCL>(x, run, lane); break;
+    case 2: narrow_wave_scan<2, T, Op, EXCL>(x, run, lane); break;
+    case 4: narrow_wave_scan<4, T, Op, EXCL>(x, run, lane); break;
+    case 8: narrow_wave_scan<8, T, Op, EXCL>(x, run, lane); break;
+    case 16: narrow_wave_scan<16, T, Op, EXCL>(x, run, lane); break;
+    default: narrow_wave_scan<32, T, Op, EXCL>(x, run, lane); break;
+    }
+    if (lane < (int)s)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (g + u * kWave < g1) {
-                narrow_load<T, REV>(in, nvec, g + u * kWave, v[u]);
-            } else {
+        for (int k = 0; k < 4; ++k) sh[w][4 * lane + k] = (A)run[k];
+    __syncthreads();
+    // Per column, the carry into each wave, in place: the tile's column carry,
+    // then the lower waves' totals in wave order.
+    if (threadIdx.x < C) {
+        A acc = CARRY ? carries[t * C + threadIdx.x] : Op::template identity<A>();
 #pragma unroll
-                for (int k = 0; k < 4; ++k) v[u][k] = tid;
+        for (int q = 0; q < kNarrowWaves; ++q) {
+            const A v = sh[q][threadIdx.x];
+            sh[q][threadIdx.x] = acc;
+            acc = Op::combine(acc, v);
+        }
+    }
+    __syncthreads();
+    A outer[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) outer[k] = sh[w][(uint32_t)(4 * lane + k) & (C - 1)];
+    T *out = (T *)p.out + p.out_offset;
+    if ((t + 1) * kNarrowTileVecs <= nvec) {
+        const uint32_t lane_off = ((uint32_t)__builtin_amdgcn_readfirstlane(w) * (kNarrowSteps * kWave) +
+                                   (uint32_t)lane) * 16u;
+        if constexpr (REV) {
+            const auto orsrc = stream_rsrc(out + 4 * (nvec - (t + 1) * kNarrowTileVecs),
+                                           (uint32_t)(kNarrowTileVecs * 16));
+            const uint32_t rev_off = (uint32_t)(kNarrowTileVecs * 16 - 16) - lane_off;
+#pragma unroll
+            for (int j = 0; j < kNarrowSteps; ++j) {
+                V v;
+                v.w = (T)Op::combine(outer[0], (A)x[j][0]);
+                v.z = (T)Op::combine(outer[1], (A)x[j][1]);
+                v.y = (T)Op::combine(outer[2], (A)x[j][2]);
+                v.x = (T)Op::combine(outer[3], (A)x[j][3]);
+                stream_store(v, orsrc, rev_off - (uint32_t)j * (kWave * 16));
+            }
+        } else {
+            const auto orsrc = stream_rsrc(out + 4 * t * kNarrowTileVecs, (uint32_t)(kNarrowTileVecs * 16));
+#pragma unroll
+            for (int j = 0; j < kNarrowSteps; ++j) {
+                V v;
+                v.x = (T)Op::combine(outer[0], (A)x[j][0]);
+                v.y = (T)Op::combine(outer[1], (A)x[j][1]);
+                v.z = (T)Op::combine(outer[2], (A)x[j][2]);
+                v.w = (T)Op::combine(outer[3], (A)x[j][3]);
+                stream_store(v, orsrc, lane_off + (uint32_t)j * (kWave * 16));
             }
         }
-        for (int d = s; d < kWave; d <<= 1) {
-            T t[4][4];
+        return;
+    }
+    const uint64_t g0 = t * kNarrowTileVecs + (uint64_t)w * (kNarrowSteps * kWave) + (uint64_t)lane;
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+    for (int j = 0; j < kNarrowSteps; ++j) {
+        const uint64_t g = g0 + (uint64_t)j * kWave;
+        if (g >= nvec) continue;
+        T y[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) t[u][k] = __shfl_up(v[u][k], d, kWave);
-            if (lane >= d)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) v[u][k] = Op::combine(t[u][k], v[u][k]);
-        }
-        T tot[4][4], pre[4][4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                tot[u][k] = __shfl(v[u][k], last, kWave);
-                pre[u][k] = v[u][k];
-                if constexpr (EXCL) {
-                    pre[u][k] = __shfl_up(v[u][k], s, kWave);
-                    if (lane < s) pre[u][k] = tid;
-                }
-            }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            T y[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                y[k] = (T)Op::combine(carry[k], (A)pre[u][k]);
-                carry[k] = Op::combine(carry[k], (A)tot[u][k]);
-            }
-            if (g + u * kWave < g1) narrow_store<T, REV>(out, nvec, g + u * kWave, y);
-        }
+        for (int k = 0; k < 4; ++k) y[k] = (T)Op::combine(outer[k], (A)x[j][k]);
+        V v;
+        v.x = REV ? y[3] : y[0];
+        v.y = REV ? y[2] : y[1];
+        v.z = REV ? y[1] : y[2];
+        v.w = REV ? y[0] : y[3];
+        store_a4<true>(v, (V *)(out + 4 * (REV ? nvec - 1 - g : g)));
     }
 }
 
@@ -1419,11 +1598,7 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
 }
 
-// Narrow column scans (col_narrow_*): chunks of whole 256-vector trips,
-// about kNarrowTargetWaves of them.
-constexpr uint64_t kNarrowTargetWaves = 8192;
-constexpr uint64_t kNarrowMinChunk = 1024; // 16-byte vectors
-
+// Narrow column scans (col_narrow_*): see the kernels' comment.
 bool narrow_column_scan(const ScanArgs &a) {
     const uint64_t c = a.lines;
     const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
@@ -1433,57 +1608,44 @@ bool narrow_column_scan(const ScanArgs &a) {
            ibase % 4 == 0 && obase % 4 == 0;
 }
 
-struct NarrowShape {
-    uint64_t chunk = 0; // 16-byte vectors per chunk
-    uint32_t nchunks = 1;
-};
-NarrowShape narrow_shape(const ScanArgs &a) {
-    NarrowShape s;
-    const uint64_t nvec = (a.len * a.lines) >> 2;
-    uint64_t chunk = ceil_div(nvec, kNarrowTargetWaves);
-    if (chunk < kNarrowMinChunk) chunk = kNarrowMinChunk;
-    chunk = ceil_div(chunk, 4 * kWave) * 4 * kWave;
-    s.chunk = chunk;
-    s.nchunks = (uint32_t)ceil_div(nvec, chunk);
-    return s;
-}
+uint64_t narrow_tiles(const ScanArgs &a) { return ceil_div((a.len * a.lines) >> 2, kNarrowTileVecs); }
 uint64_t narrow_bytes(const ScanArgs &a) {
-    const NarrowShape s = narrow_shape(a);
-    if (s.nchunks <= 1) return 0;
-    return (uint64_t)s.nchunks * a.lines * (a.dtype == HX_DTYPE_F32 ? 8u : 4u);
+    const uint64_t tiles = narrow_tiles(a);
+    if (tiles <= 1) return 0;
+    return tiles * a.lines * (a.dtype == HX_DTYPE_F32 ? 8u : 4u);
 }
 
 template <typename T, typename Op, bool EXCL, bool REV>
-hx_status launch_narrow_dir(const ScanParams &p, const NarrowShape &s, void *ws, hipStream_t stream) {
+hx_status launch_narrow_dir(const ScanParams &p, uint64_t tiles, void *ws, hipStream_t stream) {
     using A = typename ColAcc<T>::type;
-    const dim3 grid((uint32_t)ceil_div((uint64_t)s.nchunks, (uint64_t)(kBlock / kWave))), block(kBlock);
+    if (tiles > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "column scan exceeds the grid range");
+    const dim3 grid((uint32_t)tiles), block(kNarrowWaves * kWave);
     A *totals = (A *)ws;
-    if (s.nchunks > 1) {
-        hipLaunchKernelGGL((col_narrow_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, totals, s.chunk,
-                           s.nchunks);
+    if (tiles > 1) {
+        hipLaunchKernelGGL((col_narrow_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, totals);
         HX_TRY(check_launch("col_narrow_totals_kernel"));
-        hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3((uint32_t)p.lines), dim3(kBlock), 0, stream, totals,
-                           p.lines, s.nchunks);
+        hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3((uint32_t)p.lines), dim3(kNarrowCarryThreads), 0,
+                           stream, totals, (uint32_t)p.lines, tiles);
         HX_TRY(check_launch("col_narrow_carry_kernel"));
         hipLaunchKernelGGL((col_narrow_scan_kernel<T, Op, EXCL, REV, true>), grid, block, 0, stream, p,
-                           (const A *)totals, s.chunk, s.nchunks);
+                           (const A *)totals);
     } else {
         hipLaunchKernelGGL((col_narrow_scan_kernel<T, Op, EXCL, REV, false>), grid, block, 0, stream, p,
-                           (const A *)totals, s.chunk, s.nchunks);
+                           (const A *)totals);
     }
     return check_launch("col_narrow_scan_kernel");
 }
 
 template <typename T, typename Op>
 hx_status launch_narrow(const ScanArgs &a, const ScanParams &p, void *ws, uint64_t ws_bytes, hipStream_t stream) {
-    const NarrowShape s = narrow_shape(a);
-    if (s.nchunks > 1 && ws_bytes < narrow_bytes(a))
+    const uint64_t tiles = narrow_tiles(a);
+    if (tiles > 1 && ws_bytes < narrow_bytes(a))
         return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
     if (a.exclusive)
-        return a.reverse ? launch_narrow_dir<T, Op, true, true>(p, s, ws, stream)
-                         : launch_narrow_dir<T, Op, true, false>(p, s, ws, stream);
-    return a.reverse ? launch_narrow_dir<T, Op, false, true>(p, s, ws, stream)
-                     : launch_narrow_dir<T, Op, false, false>(p, s, ws, stream);
+        return a.reverse ? launch_narrow_dir<T, Op, true, true>(p, tiles, ws, stream)
+                         : launch_narrow_dir<T, Op, true, false>(p, tiles, ws, stream);
+    return a.reverse ? launch_narrow_dir<T, Op, false, true>(p, tiles, ws, stream)
+                     : launch_narrow_dir<T, Op, false, false>(p, tiles, ws, stream);
 }
 
 uint64_t scan_bytes(const ScanArgs &a) {

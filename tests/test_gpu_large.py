@@ -177,3 +177,30 @@ def test_rows_past_2_31_rows(device):
         assert _slice(device, a, start, 4).tolist() == want_a, start
     for b in (x, s, m, a):
         b.free()
+
+
+@pytest.mark.parametrize("kind,reverse", [("inclusive", False), ("exclusive", True)])
+def test_narrow_column_scan_with_many_tiles(device, kind, reverse):
+    """[2^23 + 5, 64] u32 along axis 0: 10923 tiles of 12288 vectors, so
+    each thread of the carry pass owns 11 tiles (past its one-batch case).
+    Every element is 1 except x[r0][c0] = 1000, so column c gets out[r][c] =
+    r + 1 (inclusive forward) or R - 1 - r (exclusive reverse), plus 999 in
+    column c0 from row r0 on (forward) or before row r0 (reverse)."""
+    R, C = (1 << 23) + 5, 64
+    r0, c0 = (1 << 22) + 7, 37
+    x = device.alloc_uninitialized(np.uint32, R * C)
+    device.fill_uniform_int(x, seed=9, lo=1, hi=1)
+    device.write_sub_buffer(x, r0 * C + c0, np.array([1000], np.uint32))
+    out = device.alloc_uninitialized(np.uint32, R * C)
+    lay = Layout.c_contiguous([R, C])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0,
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive if kind == "exclusive" else hx.ScanKind.Inclusive)
+    for r in (0, 1, 767, 768, r0 - 1, r0, r0 + 1, (1 << 23) - 1, R - 1):  # 768 rows per tile
+        got = _slice(device, out, r * C, C)
+        want = np.full(C, (R - 1 - r) if reverse else (r + 1), np.uint64)
+        if (r < r0) if reverse else (r >= r0):
+            want[c0] += 999
+        assert np.array_equal(got, want.astype(np.uint32)), r
+    x.free()
+    out.free()
