@@ -56,6 +56,10 @@ constexpr int kTile = SegTile<kSegWaves, kSegSteps>::kElems;
 constexpr int kLongWaves = 8;
 constexpr int kLongTile = SegTile<kLongWaves, kSegSteps>::kElems;
 constexpr uint64_t kLongMean = 4096;
+// Mean segment length from which look-backs walk tiles only (one level):
+// segments of thousands of tiles leave few superblocks resolved when a
+// look-back reaches them (see seg_lookback).
+constexpr uint64_t kTwoLevelMaxMean = 1ull << 18;
 constexpr int kSlots = 2048; // segment values compacted per round
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 
@@ -67,6 +71,7 @@ struct SegParams {
     uint32_t *out;
     uint64_t total_tiles;
     uint64_t *status;          // look-back words, one per tile
+    uint64_t *sstatus;         // then one per 64-tile superblock
     uint32_t *ub_map, *lb_map; // tile edges -> offset indices (total_tiles + 1 each)
     uint32_t tag;              // this launch's status tag
     uint32_t spin_limit;       // polls before computing a predecessor (64)
@@ -115,49 +120,117 @@ __device__ __forceinline__ void publish_if_unset(uint64_t *word, uint32_t tag, u
                                          __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tiles per superblock.  The last tile of each superblock also publishes
+// the superblock's carry out, as a prefix, when the tile holds a segment
+// start (at once) or once its own look-back resolves.  A two-level look-back
+// folds the tiles of its own superblock, then whole superblocks (scan.hip has
+// the same two levels), so where superblocks have resolved it skips 64 tiles
+// a step.  The superblock statuses are published in both forms.
+constexpr int kSegSuper = 64;
+
+// Fold of the statuses of the `count` (<= 64) tiles just before tile `end`,
+// nearest first, stopping at the first prefix; `found` tells whether one was
+// met.  Lane l reads the tile at distance l.  A status that stays
+// unpublished is computed by the waiter (decoupled fallback).  One wave.
+template <int TILE>
+__device__ uint32_t seg_fold_tiles(const SegParams &p, uint64_t end, int count, uint32_t tag, bool &found) {
+    const int lane = lane_id();
+    uint32_t flag, val;
+    uint32_t spins = 0;
+    for (;;) {
+        flag = kAggregate; // lanes past `count`: valid, not a prefix, 0
+        val = 0;
+        if (lane < count) {
+            const uint64_t wd = ld_relaxed(&p.status[end - 1 - (uint64_t)lane]);
+            const uint32_t hi = (uint32_t)(wd >> 32);
+            flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
+            val = (uint32_t)wd;
+        }
+        const uint64_t pm = ballot(flag == kPrefix);
+        const uint64_t im = ballot(flag == kInvalid);
+        // Every status up to and including the nearest prefix is needed.
+        const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
+        const uint64_t missing = im & need;
+        if (missing == 0ull) break;
+        if (++spins >= p.spin_limit) {
+            const uint64_t u = end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
+            uint32_t fflag, fval;
+            seg_tile_status<TILE>(p, u, fflag, fval);
+            if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
+            spins = 0;
+            continue;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    const uint64_t pm = ballot(flag == kPrefix);
+    const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
+    found = pm != 0ull;
+    return wave_sum((lane <= first) ? val : 0u);
+}
+
 // Exclusive prefix of segment sums carried in from earlier tiles: folds
 // predecessor statuses until one is a prefix (a tile that holds a segment
-// start, or that already resolved its own carry), computing any status that
-// stays unpublished (decoupled fallback).  One wave.
-template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_t tile, uint32_t tag) {
+// start, or that already resolved its own carry).  TWO_LEVEL: the tiles of
+// the tile's superblock, then whole superblocks; otherwise tiles only, 64
+// per round trip.  One wave.
+//
+// Measured at 2^27 values, geometric segment lengths (us per launch, one
+// level / two levels): mean 300 85 / 84.4, 3000 96 / 86.4, 10^5 114 /
+// 102.9, 10^6 125 / 138, 10^7 130 / 188.  When segments span thousands of
+// tiles, few superblocks have resolved when a look-back reaches them, and
+// the second level only adds round trips; the host picks the form by mean
+// segment length (kTwoLevelMaxMean).
+template <int TILE, bool TWO_LEVEL> __device__ uint32_t seg_lookback(const SegParams &p, uint64_t tile, uint32_t tag) {
     const int lane = lane_id();
-    uint32_t c_in = 0;
-    int64_t pred = (int64_t)tile - 1;
-    for (;;) {
-        const int64_t idx = pred - lane;
-        uint32_t flag, val;
-        uint32_t spins = 0;
+    if constexpr (!TWO_LEVEL) {
+        uint32_t c_in = 0;
+        for (uint64_t end = tile;; end -= kWave) {
+            const int count = end < (uint64_t)kWave ? (int)end : kWave;
+            bool found = false;
+            c_in += seg_fold_tiles<TILE>(p, end, count, tag, found);
+            if (found || end <= (uint64_t)kWave) return c_in; // tile 0 always holds a segment start
+        }
+    } else {
+        const int pos = (int)(tile % kSegSuper);
+        const uint64_t sb = tile / kSegSuper;
+        bool found = false;
+        uint32_t c_in = pos > 0 ? seg_fold_tiles<TILE>(p, tile, pos, tag, found) : 0u;
+        if (found) return c_in;
+        // Level 1: windows of 64 superblocks, nearest first.  A superblock
+        // status is only ever a prefix (its carry out), published by its last
+        // tile once that tile's carry is known, or by a waiter that found a
+        // prefix among its tiles; a superblock without one is folded from its
+        // 64 tiles (one round trip).  Publishing aggregates as well made
+        // look-backs skip tiles that had resolved since and walk further
+        // back (10^6: 186 us, 10^7: 279).
+        int64_t pred = (int64_t)sb - 1;
         for (;;) {
-            flag = kPrefix;
-            val = 0;
+            const int64_t idx = pred - lane;
+            uint32_t flag = kPrefix, val = 0; // before superblock 0: the identity
             if (idx >= 0) {
-                const uint64_t wd = ld_relaxed(&p.status[idx]);
+                const uint64_t wd = ld_relaxed(&p.sstatus[idx]);
                 const uint32_t hi = (uint32_t)(wd >> 32);
                 flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
                 val = (uint32_t)wd;
             }
             const uint64_t pm = ballot(flag == kPrefix);
-            const uint64_t im = ballot(flag == kInvalid);
-            const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
-            const uint64_t missing = im & need;
-            if (missing == 0ull) break;
-            if (++spins >= p.spin_limit) {
-                const uint64_t u = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
-                uint32_t fflag, fval;
-                seg_tile_status<TILE>(p, u, fflag, fval);
-                if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
-                spins = 0;
-                continue;
+            const int stop = pm ? (__ffsll((long long)pm) - 1) : kWave;
+            // Superblocks nearer than the nearest published prefix, from their
+            // tiles, nearest first.
+            for (int q = 0; q < stop; ++q) {
+                const uint64_t s = (uint64_t)(pred - q);
+                bool f = false;
+                const uint32_t v = seg_fold_tiles<TILE>(p, (s + 1) * kSegSuper, kSegSuper, tag, f);
+                c_in += v;
+                if (f) {
+                    if (lane == 0) publish_if_unset(&p.sstatus[s], tag, kPrefix, v);
+                    return c_in;
+                }
             }
-            __builtin_amdgcn_s_sleep(1);
+            if (pm) return c_in + read_lane(val, stop);
+            pred -= kWave;
         }
-        const uint64_t pm = ballot(flag == kPrefix);
-        const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
-        c_in += wave_sum((lane <= first) ? val : 0u);
-        if (pm) break;
-        pred -= kWave;
     }
-    return c_in;
 }
 
 // Block b processes tile b; see scan.hip for why there is no ticket counter
@@ -191,7 +264,7 @@ template <int TILE> __device__ uint32_t seg_lookback(const SegParams &p, uint64_
 // scratch and takes 156 us).  The 8 x 8 long-segment tiles take two waves
 // per SIMD per block, so the same budget fits three of them per CU (six
 // waves per SIMD).
-template <int WAVES, int STEPS>
+template <int WAVES, int STEPS, bool TWO_LEVEL = true>
 __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7, 7))) void segmented_sum_kernel(
     SegParams p) {
     static_assert(STEPS % 8 == 0, "each lane ranks whole mask words");
@@ -329,11 +402,15 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
 
     const bool has_head = h >= t0;
     const bool needs_carry = tile > 0 && first_start < t0;
+    const bool last_in_super = tile % kSegSuper == kSegSuper - 1;
     if (w == 0 && lane == 0) {
-        if (has_head)
-            st_relaxed(&p.status[tile], status_word(tag, kPrefix, total - (h > t0 ? s_hpref : 0u)));
-        else if (tile > 0)
+        if (has_head) {
+            const uint32_t carry_out = total - (h > t0 ? s_hpref : 0u);
+            st_relaxed(&p.status[tile], status_word(tag, kPrefix, carry_out));
+            if (last_in_super) st_relaxed(&p.sstatus[tile / kSegSuper], status_word(tag, kPrefix, carry_out));
+        } else if (tile > 0) {
             st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
+        }
     }
 
     // Per wave: popcounts for ranking.
@@ -422,9 +499,11 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
     if (needs_carry || (!has_head && tile > 0)) {
         __syncthreads(); // s_open
         if (w == 0) {
-            const uint32_t c_in = seg_lookback<kTile>(p, tile, tag);
+            const bool publish_super = last_in_super && !has_head;
+            const uint32_t c_in = seg_lookback<kTile, TWO_LEVEL>(p, tile, tag);
             if (lane == 0) {
                 if (!has_head) st_relaxed(&p.status[tile], status_word(tag, kPrefix, c_in + total));
+                if (publish_super) st_relaxed(&p.sstatus[tile / kSegSuper], status_word(tag, kPrefix, c_in + total));
                 if (needs_carry && k_lo < k_hi1 && k_lo >= 1 && k_lo <= p.segments) p.out[k_lo - 1] = s_open + c_in;
             }
         }
@@ -952,11 +1031,12 @@ uint64_t seg_tile_elems(const SegmentedArgs &a) { return long_tiles(a) ? kLongTi
 uint64_t tile_map_bytes(uint64_t tiles) { return align256(2 * (tiles + 1) * 4); }
 } // namespace
 
-// Look-back status words: 8 bytes per tile on the element-tile path, none on
-// the short path.
+// Look-back status words: 8 bytes per tile and per 64-tile superblock on the
+// element-tile path, none on the short path.
 uint64_t segmented_lookback_bytes(const SegmentedArgs &a) {
     if (a.n == 0 || a.num_segments == 0 || short_path(a)) return 0;
-    return kLookbackOffset + ceil_div(a.n, seg_tile_elems(a)) * 8;
+    const uint64_t tiles = ceil_div(a.n, seg_tile_elems(a));
+    return kLookbackOffset + (tiles + ceil_div(tiles, kSegSuper)) * 8;
 }
 
 // Everything else, which must never share memory with status words: the
@@ -1011,6 +1091,7 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     const bool long_tile = long_tiles(a);
     p.total_tiles = ceil_div(a.n, seg_tile_elems(a));
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
+    p.sstatus = p.status + p.total_tiles;
     p.ub_map = (uint32_t *)aux;
     p.lb_map = p.ub_map + p.total_tiles + 1;
     if (p.total_tiles >= 0x80000000ull)
@@ -1027,8 +1108,12 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
         hipLaunchKernelGGL((seg_tile_map_kernel<kLongTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream,
                            p);
         HX_TRY(check_launch("seg_tile_map_kernel"));
-        hipLaunchKernelGGL((segmented_sum_kernel<kLongWaves, kSegSteps>), dim3((uint32_t)p.total_tiles),
-                           dim3(kLongWaves * kWave), 0, stream, p);
+        if (a.n < kTwoLevelMaxMean * a.num_segments)
+            hipLaunchKernelGGL((segmented_sum_kernel<kLongWaves, kSegSteps, true>), dim3((uint32_t)p.total_tiles),
+                               dim3(kLongWaves * kWave), 0, stream, p);
+        else
+            hipLaunchKernelGGL((segmented_sum_kernel<kLongWaves, kSegSteps, false>), dim3((uint32_t)p.total_tiles),
+                               dim3(kLongWaves * kWave), 0, stream, p);
     } else {
         hipLaunchKernelGGL((seg_tile_map_kernel<kTile>), dim3((uint32_t)map_blocks), dim3(kBlock), 0, stream, p);
         HX_TRY(check_launch("seg_tile_map_kernel"));

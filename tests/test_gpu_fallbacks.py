@@ -133,11 +133,13 @@ def _segmented(device, values, offsets):
 
 
 # Element tiles of 8192 values (mean 300) and 16384 values (mean 50000,
-# where nearly no tile holds a segment start, so look-backs chain far).
+# where nearly no tile holds a segment start, so look-backs chain far).  At
+# 2^24 values (1024 tiles, 16 superblocks) mean 50000 takes the two-level
+# look-back, which folds missing superblocks from their tiles, and mean 10^6
+# the one-level walk over tiles.
 @pytest.mark.parametrize("limits", FORCED)
-@pytest.mark.parametrize("mean", [300.0, 50000.0])
-def test_segmented_sums_under_forced_fallbacks(device, oracle, limits, mean):
-    n = 1 << 21
+@pytest.mark.parametrize("n,mean", [(1 << 21, 300.0), (1 << 21, 50000.0), (1 << 24, 50000.0), (1 << 24, 1e6)])
+def test_segmented_sums_under_forced_fallbacks(device, oracle, limits, n, mean):
     x = oracle.uniform_int(n, seed=23, lo=-1000, hi=1000, dtype=np.int32)
     off = oracle.geometric_offsets(n, mean, seed=29)
     normal = _segmented(device, x, off)
