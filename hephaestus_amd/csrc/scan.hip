@@ -752,11 +752,12 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
 // are l, l + s, l + 2s, ... with s = C / 4 (a "class").  A reverse scan
 // mirrors the range (logical vector g is physical vector nvec - 1 - g, its
 // components reversed), so every pass works in logical order and logical
-// columns.  Tiles are 12 waves x 16 steps of 64 vectors (192 KiB, one block
-// per CU at up to 168 VGPRs), each wave streaming its own 16 KiB run with all
-// 16 loads in flight.  Three passes: tile totals per column (one read), an exclusive
+// columns.  Tiles are the scan's own: 8 waves x 16 steps of 64 vectors
+// (128 KiB, two blocks per CU), each wave streaming its own 16 KiB run with
+// all 16 loads in flight.  Three passes: tile totals per column (one read), an exclusive
 // scan of the tile totals per column, and the rescan (one read, one write).
-constexpr int kNarrowWaves = 12, kNarrowSteps = 16;
+constexpr int kNarrowWaves = 8, kNarrowSteps = 16;
+constexpr int kNarrowWavesPerEu = 4; // two 8-wave blocks per CU: at most 128 VGPRs
 constexpr uint64_t kNarrowTileVecs = (uint64_t)kNarrowWaves * kNarrowSteps * kWave;
 
 // Lane permutes for the class scans: lane l reads lane src(l), src given as
@@ -830,28 +831,34 @@ __device__ __forceinline__ A class_shift(A incl, int lane, const ClassLanes &cl)
     }
 }
 
-// The rescan's in-wave part for class stride S: each step's components
-// scanned over their classes, x[j][k] replaced by the lane's running class
-// total before the step combined with its (inclusive or exclusive) class
-// prefix; run[k] ends with the wave's total of the lane's column k.  All in
-// T: an f32 wave prefix covers at most 16 steps of 64 values, and the
-// carries into the wave are added in f64 afterwards.
-template <int S, typename T, typename Op, bool EXCL>
-__device__ __forceinline__ void narrow_wave_scan(T (&x)[16][4], T (&run)[4], int lane) {
+// The rescan's in-wave part for class stride S, once the carries into the
+// wave are known (`outer`, per component): each step's components scanned
+// over their classes, and each output -- the carry, then the lane's running
+// class total before the step, then its (inclusive or exclusive) class
+// prefix -- handed to store(j, y) as soon as the step is scanned, so no
+// output is held in registers.  The running totals are in T: an f32 wave
+// prefix covers at most 16 steps of 64 values, and the carry is f64.
+template <int S, typename T, typename Op, bool EXCL, typename Store>
+__device__ __forceinline__ void narrow_wave_scan(const T (&x)[16][4], const typename ColAcc<T>::type (&outer)[4],
+                                                 int lane, Store &&store) {
+    using A = typename ColAcc<T>::type;
     ClassLanes cl;
     if constexpr (S > 1) cl.template init<S>(lane);
+    T run[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) run[k] = Op::template identity<T>();
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
+        T y[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const T incl = class_inclusive_scan<S, Op, T>(x[j][k], lane, cl);
             const T tot = class_total<S, T>(incl, cl);
             const T pre = EXCL ? class_shift<S, Op, T>(incl, lane, cl) : incl;
-            x[j][k] = Op::combine(run[k], pre);
+            y[k] = (T)Op::combine(outer[k], (A)Op::combine(run[k], pre));
             run[k] = Op::combine(run[k], tot);
         }
-        // One step's four class scans at a time, to bound live registers.
-        __builtin_amdgcn_sched_barrier(0);
+        store(j, y);
     }
 }
 
@@ -1003,16 +1010,16 @@ __global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A
 }
 
 // Pass 3: tile t rescanned from its columns' carries (pass 2), or from the
-// identity for a single tile.  Per step each component is scanned over its
-// class (class_inclusive_scan, in T), and the lane's running class totals
-// (in ColAcc: f64 for f32) advance in step order; the waves' column totals
-// combine through LDS in wave order; outputs are carry + wave prefix + local
-// prefix, stored through the stream-store path (whole tiles) or element
-// checked (the last tile).
+// identity for a single tile.  Each wave first folds its column totals (per
+// lane over its 16 steps, then across the lanes of a class), the waves'
+// totals combine with the tile's carries through LDS in wave order, and only
+// then are the steps scanned (narrow_wave_scan), every step stored as soon as
+// it is scanned: holding the outputs until the carries were known took
+// 140-145 VGPRs, one block per CU.  Whole tiles store through the
+// stream-store path, the last tile element by element.
 template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
-__global__ __launch_bounds__(kNarrowWaves *kWave) __attribute__((amdgpu_waves_per_eu(3)))
-void col_narrow_scan_kernel(
-    ScanParams p, const typename ColAcc<T>::type *carries) {
+__global__ __launch_bounds__(kNarrowWaves *kWave) __attribute__((amdgpu_waves_per_eu(kNarrowWavesPerEu)))
+void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carries) {
     using A = typename ColAcc<T>::type;
     using V = typename Vec4A4<T>::type;
     __shared__ A sh[kNarrowWaves][kBlock / 2]; // C <= 128 columns
@@ -1022,85 +1029,67 @@ void col_narrow_scan_kernel(
     const uint32_t s = C / 4;
     const uint64_t nvec = (p.len * C) >> 2;
     const uint64_t t = blockIdx.x;
-    const T tid = Op::template identity<T>();
     T x[kNarrowSteps][4];
-    narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, tid, x);
+    narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, Op::template identity<T>(), x);
 
-    T run[4]; // this lane's class totals so far, per component
+    // The wave's column totals, then per column the carry into each wave.
+    A acc[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) run[k] = tid;
-    switch (s) { // wave-uniform: C is a launch parameter
-    case 1: narrow_wave_scan<1, T, Op, EXCL>(x, run, lane); break;
-    case 2: narrow_wave_scan<2, T, Op, EXCL>(x, run, lane); break;
-    case 4: narrow_wave_scan<4, T, Op, EXCL>(x, run, lane); break;
-    case 8: narrow_wave_scan<8, T, Op, EXCL>(x, run, lane); break;
-    case 16: narrow_wave_scan<16, T, Op, EXCL>(x, run, lane); break;
-    default: narrow_wave_scan<32, T, Op, EXCL>(x, run, lane); break;
+    for (int k = 0; k < 4; ++k) {
+        acc[k] = Op::template identity<A>();
+#pragma unroll
+        for (int j = 0; j < kNarrowSteps; ++j) acc[k] = Op::combine(acc[k], (A)x[j][k]);
     }
+    for (int m = kWave / 2; m >= (int)s; m >>= 1)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] = Op::combine(acc[k], __shfl_xor(acc[k], m, kWave));
     if (lane < (int)s)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) sh[w][4 * lane + k] = (A)run[k];
+        for (int k = 0; k < 4; ++k) sh[w][4 * lane + k] = acc[k];
     __syncthreads();
-    // Per column, the carry into each wave, in place: the tile's column carry,
-    // then the lower waves' totals in wave order.
     if (threadIdx.x < C) {
-        A acc = CARRY ? carries[t * C + threadIdx.x] : Op::template identity<A>();
+        A c = CARRY ? carries[t * C + threadIdx.x] : Op::template identity<A>();
 #pragma unroll
         for (int q = 0; q < kNarrowWaves; ++q) {
             const A v = sh[q][threadIdx.x];
-            sh[q][threadIdx.x] = acc;
-            acc = Op::combine(acc, v);
+            sh[q][threadIdx.x] = c;
+            c = Op::combine(c, v);
         }
     }
     __syncthreads();
     A outer[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) outer[k] = sh[w][(uint32_t)(4 * lane + k) & (C - 1)];
+
     T *out = (T *)p.out + p.out_offset;
-    if ((t + 1) * kNarrowTileVecs <= nvec) {
-        const uint32_t lane_off = ((uint32_t)__builtin_amdgcn_readfirstlane(w) * (kNarrowSteps * kWave) +
-                                   (uint32_t)lane) * 16u;
-        if constexpr (REV) {
-            const auto orsrc = stream_rsrc(out + 4 * (nvec - (t + 1) * kNarrowTileVecs),
-                                           (uint32_t)(kNarrowTileVecs * 16));
-            const uint32_t rev_off = (uint32_t)(kNarrowTileVecs * 16 - 16) - lane_off;
-#pragma unroll
-            for (int j = 0; j < kNarrowSteps; ++j) {
-                V v;
-                v.w = (T)Op::combine(outer[0], (A)x[j][0]);
-                v.z = (T)Op::combine(outer[1], (A)x[j][1]);
-                v.y = (T)Op::combine(outer[2], (A)x[j][2]);
-                v.x = (T)Op::combine(outer[3], (A)x[j][3]);
-                stream_store(v, orsrc, rev_off - (uint32_t)j * (kWave * 16));
-            }
-        } else {
-            const auto orsrc = stream_rsrc(out + 4 * t * kNarrowTileVecs, (uint32_t)(kNarrowTileVecs * 16));
-#pragma unroll
-            for (int j = 0; j < kNarrowSteps; ++j) {
-                V v;
-                v.x = (T)Op::combine(outer[0], (A)x[j][0]);
-                v.y = (T)Op::combine(outer[1], (A)x[j][1]);
-                v.z = (T)Op::combine(outer[2], (A)x[j][2]);
-                v.w = (T)Op::combine(outer[3], (A)x[j][3]);
-                stream_store(v, orsrc, lane_off + (uint32_t)j * (kWave * 16));
-            }
-        }
-        return;
-    }
+    const bool full = (t + 1) * kNarrowTileVecs <= nvec;
+    const uint32_t lane_off =
+        ((uint32_t)__builtin_amdgcn_readfirstlane(w) * (kNarrowSteps * kWave) + (uint32_t)lane) * 16u;
+    const uint32_t rev_off = (uint32_t)(kNarrowTileVecs * 16 - 16) - lane_off;
+    const auto orsrc = stream_rsrc(out + 4 * (REV ? (full ? nvec - (t + 1) * kNarrowTileVecs : 0)
+                                                   : t * kNarrowTileVecs),
+                                   (uint32_t)(kNarrowTileVecs * 16));
     const uint64_t g0 = t * kNarrowTileVecs + (uint64_t)w * (kNarrowSteps * kWave) + (uint64_t)lane;
-#pragma unroll
-    for (int j = 0; j < kNarrowSteps; ++j) {
-        const uint64_t g = g0 + (uint64_t)j * kWave;
-        if (g >= nvec) continue;
-        T y[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) y[k] = (T)Op::combine(outer[k], (A)x[j][k]);
+    auto store = [&](int j, const T (&y)[4]) {
         V v;
         v.x = REV ? y[3] : y[0];
         v.y = REV ? y[2] : y[1];
         v.z = REV ? y[1] : y[2];
         v.w = REV ? y[0] : y[3];
-        store_a4<true>(v, (V *)(out + 4 * (REV ? nvec - 1 - g : g)));
+        if (full) {
+            stream_store(v, orsrc, REV ? rev_off - (uint32_t)j * (kWave * 16) : lane_off + (uint32_t)j * (kWave * 16));
+        } else {
+            const uint64_t g = g0 + (uint64_t)j * kWave;
+            if (g < nvec) store_a4<true>(v, (V *)(out + 4 * (REV ? nvec - 1 - g : g)));
+        }
+    };
+    switch (s) { // wave-uniform: C is a launch parameter
+    case 1: narrow_wave_scan<1, T, Op, EXCL>(x, outer, lane, store); break;
+    case 2: narrow_wave_scan<2, T, Op, EXCL>(x, outer, lane, store); break;
+    case 4: narrow_wave_scan<4, T, Op, EXCL>(x, outer, lane, store); break;
+    case 8: narrow_wave_scan<8, T, Op, EXCL>(x, outer, lane, store); break;
+    case 16: narrow_wave_scan<16, T, Op, EXCL>(x, outer, lane, store); break;
+    default: narrow_wave_scan<32, T, Op, EXCL>(x, outer, lane, store); break;
     }
 }
 
