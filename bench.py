@@ -49,13 +49,15 @@ sys.path.insert(0, str(REPO))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30",
-             "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32")
+             "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
+             "colscan_narrow_u32", "segmented_long_i32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "sum_f32_2_20": "full_reduce_kernel<",
              "rows_f32": "rows_kernel", "segmented_i32": "segmented_sum_kernel",
              "segmented_short_i32": "seg_short_kernel", "scan_f32_2_30": "scan_tiles_kernel",
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
-             "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel"}
+             "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel",
+             "colscan_narrow_u32": "col_narrow_scan_kernel", "segmented_long_i32": "segmented_sum_kernel"}
 
 
 def log(msg: str) -> None:
@@ -487,6 +489,46 @@ def bench_colscan_u32(hx, dev, args):
     return {"n": rows * cols, "ms": ms, "bytes": 8 * rows * cols}
 
 
+def bench_colscan_narrow_u32(hx, dev, args):
+    """Axis-0 inclusive scans of 2^28-element row-major u32 matrices with 4,
+    16, 64 and 128 columns (the narrow-column form); "ms" is their mean."""
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.uint32, n)
+    dev.fill_uniform_int(x, seed=3, lo=0, hi=255)
+    out = dev.alloc_uninitialized(np.uint32, n)
+    per = {}
+    for c in (4, 16, 64, 128):
+        lay = Layout.c_contiguous([n // c, c])
+        plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0,
+                                                  hx.ScanDirection.Forward, StridedView(out, lay))
+        per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+        log(f"colscan_narrow_u32: {c} columns {per[c]:.4f} ms/launch")
+    return {"n": n, "ms": statistics.mean(per.values()), "bytes": 8 * n}
+
+
+def bench_segmented_long_i32(hx, dev, args):
+    """Segmented sums of 2^27 i32 values with geometric segment lengths of
+    mean 3000, 10^5, 10^6 and 10^7 (long segments: tiles without a segment
+    start, whose carries come from look-backs); "ms" is their mean."""
+    from oracle import oracle  # geometric offsets are generated on the host
+
+    n = 1 << 27
+    x = dev.alloc_uninitialized(np.int32, n)
+    dev.fill_uniform_int(x, seed=4, lo=-1000, hi=1000)
+    per, nbytes = {}, []
+    for mean in (3000.0, 1e5, 1e6, 1e7):
+        off = oracle.geometric_offsets(n, mean, seed=5)
+        ob = dev.upload(off)
+        out = dev.alloc_uninitialized(np.int32, off.size - 1)
+        plan = hx.RocmSegmentedReductionOps().prepare_segmented_sum(dev, x, ob, out)
+        per[mean] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+        nbytes.append(4 * n + 4 * off.size + 4 * (off.size - 1))
+        log(f"segmented_long_i32: mean {mean:g}, {off.size - 1} segments, {per[mean]:.4f} ms/launch")
+    return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
+
+
 def bench_copy_u32(hx, dev, args):
     """The copy kernel behind copy_buffer over 2^28 u32, queued back to back
     (hx_copy_async): the yardstick (read B + write B) for the HBM byte
@@ -912,7 +954,8 @@ def main() -> int:
     line["ceiling"] = ceil
     if args.workload == "all":
         extra = {}
-        for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32"):
+        for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
+                     "colscan_narrow_u32", "segmented_long_i32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             g = gbs(r["bytes"], r["ms"])
             extra[name] = {"value": round(g, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),
