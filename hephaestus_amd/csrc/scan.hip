@@ -928,7 +928,7 @@ __global__ __launch_bounds__(kNarrowWaves *kWave) void col_narrow_totals_kernel(
     const uint32_t C = (uint32_t)p.lines;
     const uint32_t s = C / 4;
     const uint64_t nvec = (p.len * C) >> 2;
-    const uint64_t t = blockIdx.x;
+    const uint64_t t = xcd_contiguous(blockIdx.x, gridDim.x); // no look-back: any tile order
     T x[kNarrowSteps][4];
     narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, Op::template identity<T>(), x);
     A acc[4];
@@ -1028,7 +1028,7 @@ void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carrie
     const uint32_t C = (uint32_t)p.lines;
     const uint32_t s = C / 4;
     const uint64_t nvec = (p.len * C) >> 2;
-    const uint64_t t = blockIdx.x;
+    const uint64_t t = xcd_contiguous(blockIdx.x, gridDim.x); // no look-back: any tile order
     T x[kNarrowSteps][4];
     narrow_tile_load<T, REV>((const T *)p.in + p.in_offset, nvec, t, w, lane, Op::template identity<T>(), x);
 
