@@ -922,6 +922,25 @@ def test_segmented_sum_long_segment_tiles(device, oracle):
         assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off)), off[:8]
 
 
+# 2^25 + 13 values: 4097 tiles of 8192 values (mean 3000) or 2049 of 16384
+# (the rest), i.e. 32 to 64 superblocks of 64 tiles.  Means below 2^18 take
+# the two-level look-back (superblock prefixes, missing superblocks folded
+# from their tiles), the others the walk over tiles; "spanning" puts one
+# segment of 2.1e7 values (20 superblocks of 16384-value tiles) among
+# mean-3000 ones.
+@pytest.mark.parametrize("mean", [3000.0, 50000.0, 200000.0, 300000.0, 1e7, "spanning"])
+def test_segmented_sum_many_superblocks(device, oracle, mean):
+    n = (1 << 25) + 13
+    x = oracle.uniform_int(n, seed=51, lo=-1000, hi=1000, dtype=np.int32)
+    if mean == "spanning":
+        off = oracle.geometric_offsets(n, 3000.0, seed=52).astype(np.int64)
+        a, b = 100 * 8192 + 7, 2660 * 8192 + 3
+        off = np.concatenate([off[off < a], [a, b], off[off > b]]).astype(np.uint32)
+    else:
+        off = oracle.geometric_offsets(n, mean, seed=53)
+    assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
+
+
 def _crowded_long(n, seed):
     """Geometric(20000) segments plus: 5000 empty segments mid-tile, 4097 at
     a 16384-value tile edge, and 3000 segments of 1..4 values packed into one
