@@ -257,8 +257,9 @@ template <typename T, int M> __global__ void map_reduce_empty_kernel(MapParams p
     if (threadIdx.x == 0 && blockIdx.x == 0) write_map_result<T, M>(p, MapPolicy<T, M>::identity());
 }
 
+// One block per 4096 elements up to 768 (the full reduction's grid rule).
 uint32_t map_blocks(uint64_t n) {
-    uint64_t blocks = ceil_div(n, 2048);
+    uint64_t blocks = ceil_div(n, 4096);
     if (blocks > kMaxBlocks) blocks = kMaxBlocks;
     return blocks < 1 ? 1u : (uint32_t)blocks;
 }

@@ -34,13 +34,17 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 768; // 16-byte partial slots: 12 KiB of status words
 
-// The grid: a function of n only (so is the combination tree), one
-// trip's worth (2048 elements) per block up to 768 blocks, three per CU on
-// 256 CUs.  At 2^28 f32 a sweep over 512..4096 blocks and 1/2/4 loads in
-// flight per lane put 768 blocks with two 16-byte non-temporal loads per
-// lane at 7.08 TB/s (151.6 us), ahead of 1024 blocks (6.9) and 8192 (3.9).
+// The grid: a function of n only (so is the combination tree), one block
+// per 4096 elements (two trips) up to 768 blocks, three per CU on 256 CUs.
+// At 2^28 f32 a sweep over 512..4096 blocks and 1/2/4 loads in flight per
+// lane put 768 blocks with two 16-byte non-temporal loads per lane at 7.08
+// TB/s (151.6 us), ahead of 1024 blocks (6.9) and 8192 (3.9).  Small,
+// launch-bound operands gain from fewer blocks (fewer partials to gather):
+// 2^20 elements, per-launch median, 512 / 256 / 128 / 64 blocks: f32 4.96 /
+// 4.12 / 3.88 / 4.31 us, u32 4.51 / 3.72 / 4.06 / 4.36.
+constexpr uint64_t kElemsPerBlock = 4096;
 inline uint32_t full_reduce_blocks(uint64_t n) {
-    uint64_t blocks = ceil_div(n, 2048);
+    uint64_t blocks = ceil_div(n, kElemsPerBlock);
     if (blocks > kMaxBlocks) blocks = kMaxBlocks;
     return blocks < 1 ? 1u : (uint32_t)blocks;
 }
