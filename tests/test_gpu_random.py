@@ -1,0 +1,300 @@
+"""Seeded random sweep of rank-2 axis reductions and axis scans.
+
+The other axis tests pick shapes at each planning boundary by hand; this one
+draws 120 cases from a fixed seed -- shapes from 1 to 4096 per side (narrow,
+tall, wide and square), every layout the view type allows (row-major,
+column-major, padded lines, either axis walking backwards, offsets), every op,
+dtype, direction and kind -- and checks each against the oracle line by line
+to the same bar as the hand-picked tests: bit-exact for integers, min, max
+and argmax; f32 sums within 2*ceil(log2 n)*eps*sum|x|; f32 products within
+gamma_{n-1} (any evaluation order).  Scans write through the input's own
+layout, so every element outside the view must keep its fill value.
+"""
+from __future__ import annotations
+
+import contextlib
+
+import numpy as np
+import pytest
+
+import hephaestus_amd as hx
+from hephaestus_amd import Layout, StridedView
+
+from test_gpu_axis import OPS, check, host_for, lines_of, prod_bound, run_column_scan
+
+AXIS = hx.RocmAxisReductionOps()
+DTYPES = [np.float32, np.uint32, np.int32]
+LAYOUTS = ["row", "col", "padded", "rev_cols", "rev_rows", "rev_both"]
+
+
+def _side(rng):
+    """1 to 4096, log-uniform, with the narrow widths 1-8 and powers of two
+    (and their neighbours) drawn more often than chance would."""
+    pick = rng.integers(0, 4)
+    if pick == 0:
+        return int(rng.integers(1, 9))
+    if pick == 1:
+        p = 1 << int(rng.integers(2, 13))
+        return max(1, p + int(rng.integers(-1, 2)))
+    return int(np.exp(rng.uniform(0.0, np.log(4096.0))))
+
+
+def _shape(rng):
+    r, c = _side(rng), _side(rng)
+    if rng.integers(0, 4) == 0:  # tall: many rows of few columns
+        r = int(rng.integers(4096, 70000))
+        c = int(rng.integers(1, 33))
+    while r * c > (1 << 21):
+        r = max(1, r // 2)
+    return r, c
+
+
+def _layout(rng, shape, kind):
+    """(strides, offset) for a view of `shape`; offsets keep every index
+    non-negative."""
+    r, c = shape
+    pad = int(rng.integers(1, 4))
+    extra = int(rng.integers(0, 5))
+    if kind == "row":
+        strides = (c, 1)
+    elif kind == "col":
+        strides = (1, r)
+    elif kind == "padded":
+        strides = (c + pad, 1)
+    elif kind == "rev_cols":
+        strides = (c + pad, -1)
+    elif kind == "rev_rows":
+        strides = (-(c + pad), 1)
+    else:
+        strides = (-(c + pad), -1)
+    offset = extra + sum((shape[d] - 1) * -strides[d] for d in range(2) if strides[d] < 0)
+    return strides, offset
+
+
+def _cases(seed, count, scan):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        shape = _shape(rng)
+        layout = LAYOUTS[int(rng.integers(0, len(LAYOUTS)))]
+        strides, offset = _layout(rng, shape, layout)
+        axis = int(rng.integers(0, 2))
+        dtype = DTYPES[int(rng.integers(0, 3))]
+        if scan:
+            op = ["sum", "prod"][int(rng.integers(0, 2))]
+            extra = (bool(rng.integers(0, 2)), bool(rng.integers(0, 2)))  # exclusive, reverse
+        else:
+            op = list(OPS)[int(rng.integers(0, len(OPS)))]
+            extra = ()
+        out.append(pytest.param(shape, strides, offset, axis, dtype, op, extra, 1000 * seed + i,
+                                id=f"{i}-{shape[0]}x{shape[1]}-{layout}-ax{axis}-{np.dtype(dtype).name}-{op}"))
+    return out
+
+
+def _buffer_size(shape, strides, offset):
+    return offset + 1 + sum((shape[d] - 1) * max(strides[d], 0) for d in range(2))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,strides,offset,axis,dtype,op,extra,seed", _cases(11, 60, scan=False))
+def test_random_axis_reduce(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed):
+    size = _buffer_size(shape, strides, offset)
+    host = host_for(oracle, dtype, size, seed=seed, op=op)
+    buf = device.upload(host)
+    nout = shape[1 - axis]
+    out_dtype = np.uint32 if op == "argmax" else dtype
+    out = device.upload(np.full(nout + 1, 7, out_dtype))  # one element past the outputs
+    out_shape = [shape[0], 1] if axis == 1 else [1, shape[1]]
+    AXIS.reduce_axis_into(device, OPS[op], StridedView(buf, Layout.try_new(list(shape), list(strides), offset)),
+                          axis, StridedView(out, Layout.c_contiguous(out_shape)))
+    got = device.download_owned(out)
+    assert got[nout] == 7
+    lines = lines_of(host, shape, strides, offset, axis)
+    if dtype == np.float32 and op == "prod":
+        n = lines.shape[1]
+        want = [np.prod(l.astype(np.float64)) for l in lines]
+        assert np.all(np.abs(got[:nout].astype(np.float64) - want) <= prod_bound(n) * np.abs(want))
+        return
+    check(oracle, op, dtype, got[:nout], lines)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,strides,offset,axis,dtype,op,extra,seed", _cases(12, 60, scan=True))
+def test_random_axis_scan(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed):
+    exclusive, reverse = extra
+    run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exclusive, reverse, seed)
+
+
+def test_case_lists_cover_the_layouts_and_paths():
+    """The fixed seeds reach every layout, both axes, narrow (at most 8
+    columns) and tall (more than 4096 rows) shapes (CPU only)."""
+    for scan, seed in ((False, 11), (True, 12)):
+        cases = [p.values for p in _cases(seed, 60, scan)]
+        ids = [p.id for p in _cases(seed, 60, scan)]
+        assert {i.split("-")[2] for i in ids} == set(LAYOUTS)
+        assert {c[3] for c in cases} == {0, 1}
+        assert any(c[0][1] <= 8 for c in cases) and any(c[0][0] > 4096 for c in cases)
+        assert all(c[0][0] * c[0][1] <= (1 << 21) for c in cases)
+
+
+# ------------------------------------------------------------ 1-D forms
+FULL = hx.RocmFullReductionOps()
+SCAN = hx.RocmScanOps()
+SEG = hx.RocmSegmentedReductionOps()
+
+
+@contextlib.contextmanager
+def _prefix(device, buf, count):
+    """The first `count` elements of `buf` as a buffer of their own; the
+    memory stays `buf`'s (the alias never frees it)."""
+    alias = hx.RocmBuffer(device, buf.ptr, count, buf.dtype)
+    try:
+        yield alias
+    finally:
+        alias.ptr = None
+
+
+def _length(rng, top):
+    """1 to 2^top, log-uniform, with powers of two and their neighbours
+    drawn more often than chance would."""
+    if rng.integers(0, 3) == 0:
+        return max(1, (1 << int(rng.integers(0, top + 1))) + int(rng.integers(-1, 2)))
+    return int(np.exp(rng.uniform(0.0, top * np.log(2.0))))
+
+
+def _cases_1d(seed, count, scan):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n = _length(rng, 24)
+        stride = [1, 1, 1, 2, 3, -1, -2][int(rng.integers(0, 7))]
+        offset = int(rng.integers(0, 5)) + (n - 1) * max(-stride, 0)
+        dtype = DTYPES[int(rng.integers(0, 3))]
+        if scan:
+            op = ["sum", "sum", "prod"][int(rng.integers(0, 3))]
+            extra = (bool(rng.integers(0, 2)), bool(rng.integers(0, 2)))  # exclusive, reverse
+        else:
+            op = list(OPS)[int(rng.integers(0, len(OPS)))]
+            extra = ()
+        out.append(pytest.param(n, stride, offset, dtype, op, extra, 1000 * seed + i,
+                                id=f"{i}-n{n}-s{stride}-o{offset}-{np.dtype(dtype).name}-{op}"))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,stride,offset,dtype,op,extra,seed", _cases_1d(13, 60, scan=False))
+def test_random_full_reduce(device, oracle, n, stride, offset, dtype, op, extra, seed):
+    size = offset + 1 + (n - 1) * max(stride, 0)
+    host = host_for(oracle, dtype, size, seed=seed, op=op)
+    sel = np.ascontiguousarray(host[offset + np.arange(n, dtype=np.int64) * stride])
+    buf = device.upload(host)
+    view = StridedView(buf, Layout.try_new([n], [stride], offset))
+    if op == "argmax":
+        idx = device.upload(np.full(2, 7, np.uint32))
+        with _prefix(device, idx, 1) as first:
+            FULL.argmax_full_into(device, view, first, None)
+        got = device.download_owned(idx)
+        assert got[1] == 7
+        assert int(got[0]) == oracle.full_argmax(sel)
+        return
+    out = device.upload(np.full(2, 7, dtype))
+    FULL.reduce_full_into(device, OPS[op], view, StridedView(out, Layout.c_contiguous([1])))
+    got = device.download_owned(out)
+    assert got[1] == 7
+    if dtype == np.float32 and op == "prod":
+        want = np.prod(sel.astype(np.float64))
+        assert abs(float(got[0]) - want) <= prod_bound(n) * abs(want)
+        return
+    check(oracle, op, dtype, got[:1], sel[None, :])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,stride,offset,dtype,op,extra,seed", _cases_1d(14, 60, scan=True))
+def test_random_scan(device, oracle, n, stride, offset, dtype, op, extra, seed):
+    """Scans of 1-D views, written through the input's own layout."""
+    exclusive, reverse = extra
+    size = offset + 1 + (n - 1) * max(stride, 0)
+    if dtype == np.float32:
+        host = (oracle.uniform_real(size, seed, 0.999, 1.001) if op == "prod"
+                else oracle.uniform_real(size, seed, -1.0, 1.0))
+    else:
+        host = oracle.uniform_int(size, seed, -1000, 1000, dtype=np.int32).view(dtype)
+    where = offset + np.arange(n, dtype=np.int64) * stride
+    sel = np.ascontiguousarray(host[where])
+    buf = device.upload(host)
+    out = device.upload(np.full(size, 7, dtype))
+    lay = Layout.try_new([n], [stride], offset)
+    SCAN.scan_axis_into(device, hx.CumSumOp if op == "sum" else hx.CumProdOp, StridedView(buf, lay), 0,
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive if exclusive else hx.ScanKind.Inclusive)
+    got_host = device.download_owned(out)
+    touched = np.zeros(size, bool)
+    touched[where] = True
+    assert np.all(got_host[~touched] == 7)
+    got = got_host[where]
+    if op == "sum":
+        want = oracle.scan_sum(sel, exclusive=exclusive, reverse=reverse)
+        if dtype == np.float32:
+            bad, worst = oracle.check_f32_bound(got, want[0], want[1], n)
+            assert bad == 0, worst
+        else:
+            assert np.array_equal(got, want)
+    elif dtype == np.float32:
+        v = sel.astype(np.float64)[::-1] if reverse else sel.astype(np.float64)
+        c = np.cumprod(v)
+        if exclusive:
+            c = np.concatenate([[1.0], c[:-1]])
+        want = c[::-1] if reverse else c
+        assert np.all(np.abs(got.astype(np.float64) - want) <= prod_bound(n) * np.abs(want))
+    else:
+        assert np.array_equal(got, oracle.scan_prod(sel, exclusive=exclusive, reverse=reverse))
+
+
+def _random_offsets(rng, n):
+    """CSR offsets over n values mixing segment regimes: geometric lengths of
+    a per-run mean from 0.5 to 70000, runs of empty segments, one long
+    segment; the first offset is 0 and the last n."""
+    lengths = []
+    total = 0
+    while total < n:
+        kind = int(rng.integers(0, 10))
+        if kind == 0:
+            run = [0] * int(rng.integers(1, 6000))  # empty segments
+        elif kind == 1:
+            run = [int(rng.integers(1, max(2, n // 2 + 1)))]  # one long segment
+        else:
+            mean = [0.5, 2.0, 8.0, 15.0, 40.0, 300.0, 5000.0, 70000.0][int(rng.integers(0, 8))]
+            count = int(rng.integers(1, 4000))
+            run = list(rng.geometric(1.0 / (mean + 1.0), size=count) - 1)
+        lengths += run
+        total += int(sum(run))
+    off = np.concatenate([[0], np.minimum(np.cumsum(lengths, dtype=np.int64), n)]).astype(np.uint32)
+    if rng.integers(0, 4) == 0:  # trailing empty segments
+        off = np.concatenate([off, np.full(int(rng.integers(1, 3000)), n, np.uint32)])
+    return off
+
+
+def _cases_segmented(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n = _length(rng, 22)
+        off = _random_offsets(rng, n)
+        dtype = [np.int32, np.uint32][int(rng.integers(0, 2))]
+        out.append(pytest.param(n, off, dtype, 1000 * seed + i,
+                                id=f"{i}-n{n}-S{off.size - 1}-{np.dtype(dtype).name}"))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,offsets,dtype,seed", _cases_segmented(15, 40))
+def test_random_segmented_sum(device, oracle, n, offsets, dtype, seed):
+    x = oracle.uniform_int(n, seed, lo=0, hi=1 << 31, dtype=np.uint32).view(dtype)
+    vb = device.upload(x)
+    ob = device.upload(offsets)
+    out = device.upload(np.full(offsets.size, 0x5A5A5A5A, np.uint32).view(dtype))  # one past the outputs
+    with _prefix(device, out, offsets.size - 1) as outputs:
+        SEG.segmented_sum_into(device, vb, ob, outputs)
+    got = device.download_owned(out)
+    assert got.view(np.uint32)[-1] == 0x5A5A5A5A
+    assert np.array_equal(got[:-1], oracle.segmented_sum(x, offsets))
