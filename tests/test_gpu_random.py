@@ -20,7 +20,7 @@ import pytest
 import hephaestus_amd as hx
 from hephaestus_amd import Layout, StridedView
 
-from test_gpu_axis import OPS, check, host_for, lines_of, prod_bound, run_column_scan
+from test_gpu_axis import OPS, check, f32_bound, host_for, lines_of, prod_bound, run_column_scan
 
 AXIS = hx.RocmAxisReductionOps()
 DTYPES = [np.float32, np.uint32, np.int32]
@@ -298,3 +298,72 @@ def test_random_segmented_sum(device, oracle, n, offsets, dtype, seed):
     got = device.download_owned(out)
     assert got.view(np.uint32)[-1] == 0x5A5A5A5A
     assert np.array_equal(got[:-1], oracle.segmented_sum(x, offsets))
+
+
+# ------------------------------------------------------------ fused rows
+AXIS_ROWS = hx.RocmAxisReductionOps()
+
+
+def _cases_rows(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        if rng.integers(0, 4) == 0:  # few long rows (split rows)
+            rows, cols = int(rng.integers(1, 6)), _length(rng, 18)
+        else:
+            rows, cols = _side(rng), _length(rng, 13)
+        pad = [0, 0, 1, 3, 4][int(rng.integers(0, 5))]
+        offset = int(rng.integers(0, 5))
+        dtype = DTYPES[int(rng.integers(0, 3))]
+        prologue = None
+        if dtype == np.float32 and rng.integers(0, 3) > 0:
+            prologue = ([0.5, -0.5, 1.0, -2.0][int(rng.integers(0, 4))], float(rng.uniform(-1.0, 1.0)))
+        wanted = int(rng.integers(1, 8))  # bits: sum, max, argmax
+        prepared = bool(rng.integers(0, 2))
+        out.append(pytest.param(rows, cols, cols + pad, offset, dtype, prologue, wanted, prepared, 1000 * seed + i,
+                                id=f"{i}-{rows}x{cols}-ld{cols + pad}-o{offset}-{np.dtype(dtype).name}"
+                                   f"-{'aff' if prologue else 'id'}-w{wanted}-{'prep' if prepared else 'imm'}"))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,ld,offset,dtype,prologue,wanted,prepared,seed", _cases_rows(16, 60))
+def test_random_rows_fused(device, oracle, rows, cols, ld, offset, dtype, prologue, wanted, prepared, seed):
+    """Sum, max and argmax of fmaf(a, x, b) per row (any subset of the three
+    outputs), immediate or prepared, against the oracle's row fold."""
+    size = offset + (rows - 1) * ld + cols + 2
+    if dtype == np.float32:
+        host = oracle.normal(size, seed=seed)
+    else:
+        host = (oracle.uniform_int(size, seed, 0, 50)).astype(dtype)  # ties for argmax
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, cols, ld, prologue=prologue)
+    buf = device.upload(host)
+    bufs = [device.upload(np.full(rows + 1, 7, dt)) for dt in (dtype, dtype, np.uint32)]
+    with contextlib.ExitStack() as stack:
+        views = [stack.enter_context(_prefix(device, b, rows)) if wanted >> k & 1 else None
+                 for k, b in enumerate(bufs)]
+        if prepared:
+            plan = AXIS_ROWS.prepare_reduce_rows_fused(device, buf, rows, cols, ld, offset, prologue, *views)
+            try:
+                plan.dispatch()
+                plan.dispatch()  # a second dispatch rewrites the same outputs
+            finally:
+                plan.destroy()
+        else:
+            AXIS_ROWS.reduce_rows_fused(device, buf, rows, cols, ld, offset, prologue, *views)
+    got = [device.download_owned(b) for b in bufs]
+    for k, g in enumerate(got):
+        if not wanted >> k & 1:
+            assert np.all(g == 7)
+            continue
+        assert g[rows] == 7
+        g = g[:rows]
+        if k == 2:
+            assert np.array_equal(g, i_ref)
+        elif k == 1:
+            assert np.array_equal(g.view(np.uint32), m_ref.view(np.uint32))
+        elif dtype == np.float32:
+            bound = np.array([f32_bound(cols, a) for a in a_ref])
+            assert np.all(np.abs(g.astype(np.float64) - s_ref) <= bound)
+        else:
+            assert np.array_equal(g, s_ref)
