@@ -20,7 +20,7 @@ import pytest
 import hephaestus_amd as hx
 from hephaestus_amd import Layout, StridedView
 
-from test_gpu_axis import OPS, check, f32_bound, host_for, lines_of, prod_bound, run_column_scan
+from test_gpu_axis import EPS, OPS, check, f32_bound, host_for, lines_of, prod_bound, run_column_scan
 
 AXIS = hx.RocmAxisReductionOps()
 DTYPES = [np.float32, np.uint32, np.int32]
@@ -367,3 +367,53 @@ def test_random_rows_fused(device, oracle, rows, cols, ld, offset, dtype, prolog
             assert np.all(np.abs(g.astype(np.float64) - s_ref) <= bound)
         else:
             assert np.array_equal(g, s_ref)
+
+
+# ------------------------------------------------------------ dot and norms
+def _cases_vector(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n = _length(rng, 22) if rng.integers(0, 10) else 0
+        views = []
+        for _ in range(2):
+            stride = [1, 1, 1, 2, 3, -1, -2][int(rng.integers(0, 7))]
+            views.append((stride, int(rng.integers(0, 5)) + max(n - 1, 0) * max(-stride, 0)))
+        dtype = DTYPES[int(rng.integers(0, 3))]
+        out.append(pytest.param(n, views, dtype, 1000 * seed + i,
+                                id=f"{i}-n{n}-a{views[0][0]}o{views[0][1]}-b{views[1][0]}o{views[1][1]}"
+                                   f"-{np.dtype(dtype).name}"))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,views,dtype,seed", _cases_vector(17, 40))
+def test_random_dot_and_norms(device, oracle, n, views, dtype, seed):
+    """dot(a, b) of two independently strided and offset views, and the L1,
+    L2 and max norms of the first."""
+    from test_gpu_vector import one
+
+    hosts, sels, svs = [], [], []
+    for k, (stride, offset) in enumerate(views):
+        size = offset + 1 + max(n - 1, 0) * max(stride, 0)
+        if dtype == np.float32:
+            host = oracle.uniform_real(size, seed + k, -2.0, 2.0)
+        else:
+            host = oracle.uniform_int(size, seed + k, 0, 2**32 - 1).view(dtype)
+        sels.append(np.ascontiguousarray(host[offset + np.arange(n, dtype=np.int64) * stride]))
+        svs.append(StridedView(device.upload(host), Layout.try_new([n], [stride], offset)))
+        hosts.append(host)
+    a, b = sels
+    got_dot = one(device, hx.dot(device, svs[0], svs[1]))
+    got_l1 = one(device, hx.norm_l1(device, svs[0]))
+    assert one(device, hx.norm_max(device, svs[0])) == oracle.norm_max(a)
+    if dtype != np.float32:
+        assert got_dot == oracle.dot(a, b)
+        assert got_l1 == oracle.norm_l1(a)
+        return
+    want, mags = oracle.dot(a, b)
+    assert abs(float(got_dot) - want) <= f32_bound(max(n, 1), mags) + abs(want) * EPS / 2
+    l1 = oracle.norm_l1(a)
+    assert abs(float(got_l1) - l1) <= f32_bound(max(n, 1), l1) + l1 * EPS
+    l2 = oracle.norm_l2(a)
+    assert abs(float(one(device, hx.norm_l2(device, svs[0]))) - l2) <= l2 * 2 * EPS
