@@ -20,6 +20,7 @@ import pytest
 import hephaestus_amd as hx
 from hephaestus_amd import Layout, StridedView
 
+import test_gpu_axis
 from test_gpu_axis import EPS, OPS, check, f32_bound, host_for, lines_of, prod_bound, run_column_scan
 
 AXIS = hx.RocmAxisReductionOps()
@@ -91,6 +92,18 @@ def _cases(seed, count, scan):
     return out
 
 
+class _PreparedScan:
+    """scan_axis_into through hx_prepare_scan: one plan, two dispatches."""
+
+    def scan_axis_into(self, device, op, input, axis, direction, output, kind):
+        plan = hx.RocmScanOps().prepare_scan_axis(device, op, input, axis, direction, output, kind)
+        try:
+            plan.dispatch()
+            plan.dispatch()
+        finally:
+            plan.destroy()
+
+
 def _buffer_size(shape, strides, offset):
     return offset + 1 + sum((shape[d] - 1) * max(strides[d], 0) for d in range(2))
 
@@ -105,8 +118,17 @@ def test_random_axis_reduce(device, oracle, shape, strides, offset, axis, dtype,
     out_dtype = np.uint32 if op == "argmax" else dtype
     out = device.upload(np.full(nout + 1, 7, out_dtype))  # one element past the outputs
     out_shape = [shape[0], 1] if axis == 1 else [1, shape[1]]
-    AXIS.reduce_axis_into(device, OPS[op], StridedView(buf, Layout.try_new(list(shape), list(strides), offset)),
-                          axis, StridedView(out, Layout.c_contiguous(out_shape)))
+    view = StridedView(buf, Layout.try_new(list(shape), list(strides), offset))
+    outputs = StridedView(out, Layout.c_contiguous(out_shape))
+    if seed % 2:  # odd seeds: the prepared plan, dispatched twice
+        plan = AXIS.prepare_reduce_axis_into(device, OPS[op], view, axis, outputs)
+        try:
+            plan.dispatch()
+            plan.dispatch()
+        finally:
+            plan.destroy()
+    else:
+        AXIS.reduce_axis_into(device, OPS[op], view, axis, outputs)
     got = device.download_owned(out)
     assert got[nout] == 7
     lines = lines_of(host, shape, strides, offset, axis)
@@ -120,8 +142,10 @@ def test_random_axis_reduce(device, oracle, shape, strides, offset, axis, dtype,
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape,strides,offset,axis,dtype,op,extra,seed", _cases(12, 60, scan=True))
-def test_random_axis_scan(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed):
+def test_random_axis_scan(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed, monkeypatch):
     exclusive, reverse = extra
+    if seed % 2:  # odd seeds: the prepared plan, dispatched twice
+        monkeypatch.setattr(test_gpu_axis, "SCAN", _PreparedScan())
     run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exclusive, reverse, seed)
 
 
