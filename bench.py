@@ -148,18 +148,33 @@ def time_plan(dev, run, steps: int, warmup: int) -> float:
 
 
 def traffic_for(name: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    """(HBM bytes per launch, where that figure comes from) from the
+    committed rocprofv3 PMC summary; (None, None) when it has no entry.
+    The counters cannot be read in this run (rocprofv3 --pmc needs a run of
+    its own), so the figure is the one committed under profiles/, with the
+    command and run that measured it."""
     f = REPO / "profiles" / "pmc_traffic.json"
     if not f.exists():
-        return None
-    entry = json.loads(f.read_text()).get(name)
-    return None if entry is None else entry.get("hbm_bytes_per_launch")
+        return None, None
+    data = json.loads(f.read_text())
+    entry = data.get(name)
+    if entry is None:
+        return None, None
+    prov = data.get("_provenance", {})
+    src = (f"profiles/pmc_traffic.json, not measured in this run: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each "
+           f"in its own run of `{prov.get('command', 'bench.py --workload ' + name)}`, scaled by the copy-kernel "
+           f"calibration; measured {prov.get('measured', 'on an earlier lease')}")
+    return entry.get("hbm_bytes_per_launch"), src
 
 
 def roofline(bytes_per_launch: float, ms: float, name: str) -> dict:
     achieved = bytes_per_launch / (ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_for(name)}
+    traffic, source = traffic_for(name)
+    out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic}
+    if source:
+        out["traffic_source"] = source
+    return out
 
 
 def gbs(nbytes: float, ms: float) -> float:
@@ -183,6 +198,24 @@ def _cpu_line(gbs_, reps, ms, sample):
     out = {"value": round(gbs_, 3), "unit": "GB/s", "cores": 1, "kind": "port",
            "sample": f"{sample}; {reps} passes, {ms:.1f} ms per pass"}
     return out
+
+
+def host_cores() -> int:
+    """Threads for the all-core CPU baselines: the cores this process may
+    run on, at most 16 (one GPU's share of a GPU box's host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _multithread(run, bytes_per_pass: float, seconds: float, sample: str, max_reps: int = 50) -> dict:
+    """The all-core figure: `run(cores)` repeated for about `seconds`."""
+    cores = host_cores()
+    gb, reps, ms = _cpu_rate(lambda: run(cores), bytes_per_pass, seconds, max_reps)
+    return {"value": round(gb, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{sample}; {reps} passes, {ms:.1f} ms per pass"}
 
 
 # ------------------------------------------------------------- workloads
@@ -210,16 +243,13 @@ def wl_scan_u32(hx, dev):
         ref = np.empty_like(host)
         gb, reps, ms = _cpu_rate(lambda: oracle.lib().hxo_scan_sum_u32(host.ctypes.data, n, 1, 0, ref.ctypes.data),
                                  8.0 * n, seconds)
-        cores = os.cpu_count() or 1
         mt = np.empty_like(host)
-        t1 = time.perf_counter()
-        oracle.scan_excl_u32_threads(host, mt, cores)
-        tt = time.perf_counter() - t1
         line = _cpu_line(gb, reps, ms, "the full 2^28-element u32 exclusive scan, sequential C oracle "
                                        "(oracle/hx_oracle.c hxo_scan_sum_u32)")
-        line["multithread"] = {"value": round(8.0 * n / tt / 1e9, 3), "unit": "GB/s", "cores": cores,
-                               "sample": "one pass of the two-pass pthread scan hxo_scan_excl_u32_threads on "
-                                         "every host core", "equals_sequential": bool(np.array_equal(mt, ref))}
+        line["multithread"] = _multithread(lambda c: oracle.scan_excl_u32_threads(host, mt, c), 8.0 * n, seconds / 2,
+                                           "the full 2^28-element input, two-pass pthread scan "
+                                           "hxo_scan_excl_u32_threads")
+        line["multithread"]["equals_sequential"] = bool(np.array_equal(mt, ref))
         line["gpu_output_verified"] = bool(np.array_equal(got, ref))
         return line
 
@@ -259,8 +289,13 @@ def wl_sum_f32(hx, dev):
 
         m = 1 << 26
         h = oracle.uniform_real(m, 1, -1.0, 1.0)
-        return _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * m, seconds),
-                         "2^26 f32 (a quarter of the GPU input), oracle full_sum (f64 accumulation)")
+        line = _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * m, seconds),
+                         "2^26 f32 (a quarter of the GPU input), oracle full_sum (compensated f64 accumulation)")
+        full = dev.download_owned(x)
+        line["multithread"] = _multithread(lambda c: oracle.sum_f32_threads(full, c), 4.0 * n, seconds,
+                                           "the full 2^28-element GPU input, pthread f64 partial sums "
+                                           "hxo_sum_f32_threads")
+        return line
 
     return {"n": n, "bytes": 4 * n + 4, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (plan, x, out),
             "dtype": "f32", "workload": "f32 full sum-reduce, n=2^28, uniform[-1,1)"}
@@ -275,8 +310,12 @@ def wl_sum_f32_2_20(hx, dev):
         from oracle import oracle
 
         h = oracle.uniform_real(n, 1, -1.0, 1.0)
-        return _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * n, seconds, max_reps=2000),
+        line = _cpu_line(*_cpu_rate(lambda: oracle.full_sum(h), 4.0 * n, seconds, max_reps=2000),
                          "the full 2^20 f32 input, oracle full_sum (the CPU reference device's role)")
+        line["multithread"] = _multithread(lambda c: oracle.sum_f32_threads(h, c), 4.0 * n, seconds,
+                                           "the full 2^20 f32 input, pthread f64 partial sums hxo_sum_f32_threads",
+                                           max_reps=2000)
+        return line
 
     return {"n": n, "bytes": 4 * n + 4, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (plan, x, out),
             "dtype": "f32", "workload": "f32 full sum-reduce, n=2^20 (BASELINE configs[0]; 4 MiB, cache-resident)"}
@@ -309,9 +348,14 @@ def wl_rows_f32(hx, dev):
 
         r = 4096
         h = oracle.normal(r * cols, 3)
-        return _cpu_line(*_cpu_rate(lambda: oracle.rows(h, r, cols, prologue=(0.5, 0.25)), 4.0 * r * cols + 12.0 * r,
+        line = _cpu_line(*_cpu_rate(lambda: oracle.rows(h, r, cols, prologue=(0.5, 0.25)), 4.0 * r * cols + 12.0 * r,
                                     seconds),
                          "4096 x 4096 f32 (1/16 of the GPU rows), oracle rows (sum, max, argmax of fmaf(.5,x,.25))")
+        full = dev.download_owned(x)
+        line["multithread"] = _multithread(
+            lambda c: oracle.rows_threads(full, rows, cols, c, prologue=(0.5, 0.25)), 4.0 * rows * cols + 12.0 * rows,
+            seconds, "the full 65536 x 4096 GPU input, oracle rows on pthread row ranges (hxo_rows_f32_threads)")
+        return line
 
     return {"n": rows * cols, "bytes": 4 * rows * cols + 12 * rows, "run": plan.dispatch, "cpu": cpu,
             "verify": verify, "keep": (x, s, m, i, plan), "dtype": "f32",
@@ -339,8 +383,14 @@ def wl_segmented_i32(hx, dev):
         m = 1 << 25
         h = oracle.uniform_int(m, 4, -1000, 1000, dtype=np.int32)
         o = oracle.geometric_offsets(m, 300.0, seed=5)
-        return _cpu_line(*_cpu_rate(lambda: oracle.segmented_sum(h, o), 4.0 * m + 8.0 * (o.size - 1) + 4, seconds),
+        line = _cpu_line(*_cpu_rate(lambda: oracle.segmented_sum(h, o), 4.0 * m + 8.0 * (o.size - 1) + 4, seconds),
                          f"2^25 i32 values, {o.size - 1} geometric(300) segments, oracle segmented_sum")
+        full = dev.download_owned(x)
+        line["multithread"] = _multithread(
+            lambda c: oracle.segmented_sum_threads(full, off, c), 4.0 * n + 4.0 * (segs + 1) + 4.0 * segs, seconds,
+            f"the full 2^27-value GPU input and its {segs} segments, oracle segmented_sum on pthread segment ranges "
+            "(hxo_segmented_sum_u32_threads)")
+        return line
 
     return {"n": n, "bytes": 4 * n + 4 * (segs + 1) + 4 * segs, "run": plan.dispatch, "cpu": cpu, "verify": verify,
             "keep": (x, ob, out, plan), "dtype": "i32",
@@ -380,8 +430,16 @@ def wl_scan_f32_2_30(hx, dev):
 
         m = 1 << 23
         h = oracle.uniform_real(m, 6, 0.0, 1.0)
-        return _cpu_line(*_cpu_rate(lambda: oracle.scan_sum(h), 8.0 * m, seconds),
+        line = _cpu_line(*_cpu_rate(lambda: oracle.scan_sum(h), 8.0 * m, seconds),
                          "2^23 f32 (1/128 of the GPU input), oracle scan_sum (compensated f64 prefix and |prefix|)")
+        full = dev.download_owned(x)
+        res = np.empty_like(full)
+        line["multithread"] = _multithread(
+            lambda c: oracle.scan_incl_f32_threads(full, res, c), 8.0 * n, seconds,
+            "the full 2^30-element GPU input to an f32 output, pthread reduce-then-scan with f64 carries "
+            "(hxo_scan_incl_f32_threads)")
+        del full, res
+        return line
 
     return {"n": n, "bytes": 8 * n, "run": plan.dispatch, "cpu": cpu, "verify": verify, "keep": (x, out, plan),
             "dtype": "f32", "workload": "f32 inclusive prefix scan, n=2^30 (BASELINE configs[4])"}
@@ -409,7 +467,38 @@ def ceiling(hx, dev, steps: int, warmup: int) -> dict:
     t = time_launches(dev, blit, steps, warmup)
     out["runtime_blit_hipMemcpyAsync"] = {"GB/s": round(gbs(8.0 * n, t["mean_ms"]), 1),
                                           **{k: round(v, 5) for k, v in t.items()}}
+    # The two yardsticks a single-pass look-back scan is actually held to.
+    # (1) The copy in the integer scan's own tile shape and order: block b
+    # moves 128 KiB tile b, each wave a contiguous 16 KiB run; a look-back
+    # needs every tile's predecessors dispatched first, so it cannot take
+    # the XCD-contiguous order of the copy above.
+    t = time_launches(dev, _raw("hx_debug_copy_scan_shape", dev.handle, x.ptr, y.ptr, 4 * n, None), steps, warmup)
+    out["copy_scan_shape_block_order"] = {"GB/s": round(gbs(8.0 * n, t["mean_ms"]), 1),
+                                          **{k: round(v, 5) for k, v in t.items()}}
+    # (2) The headline's own kernel with no look-back: the same 2^28 u32
+    # exclusive scan cut into 8192 lines of 32768 elements scanned along
+    # axis 1, so every line is one 8 x 16 tile of the same kernel
+    # instantiation and no tile has a predecessor to wait for.  A real,
+    # checked workload (row-wise scans), not a switch in the kernel.
+    from hephaestus_amd import Layout, StridedView
+
+    lines, width = 8192, 32768
+    lay = Layout.c_contiguous([lines, width])
+    rows_plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 1,
+                                                   hx.ScanDirection.Forward, StridedView(y, lay),
+                                                   hx.ScanKind.Exclusive)
+    t = time_launches(dev, rows_plan.dispatch, steps, warmup)
+    from oracle import oracle
+
+    host_x, host_y = dev.download_owned(x).reshape(lines, width), dev.download_owned(y).reshape(lines, width)
+    sample = range(0, lines, 257)
+    ok = all(np.array_equal(host_y[r], oracle.scan_sum(host_x[r], exclusive=True)) for r in sample)
+    out["scan_rows_one_tile_no_lookback"] = {
+        "GB/s": round(gbs(8.0 * n, t["mean_ms"]), 1), **{k: round(v, 5) for k, v in t.items()},
+        "workload": "u32 exclusive scan of [8192, 32768] along axis 1: scan_tiles_kernel 8 x 16, one tile per line",
+        "gpu_output_check": {"ok": bool(ok), "check": f"{len(sample)} sampled lines bit-exact against the oracle"}}
     out["bytes_per_launch"] = 8 * n
+    rows_plan.destroy()
     x.free()
     y.free()
     return out
@@ -926,8 +1015,15 @@ def main() -> int:
     best = max(ceil["copy_kernel"]["GB/s"], ceil["runtime_blit_hipMemcpyAsync"]["GB/s"])
     ceil["best_GB/s"] = best
     ceil["headline_scan_over_best"] = round(head["value"] / best, 4)
+    ceil["headline_scan_over_in_order_copy"] = round(head["value"] / ceil["copy_scan_shape_block_order"]["GB/s"], 4)
+    ceil["headline_scan_over_lookback_free"] = round(
+        head["value"] / ceil["scan_rows_one_tile_no_lookback"]["GB/s"], 4)
     log(f"ceiling: copy kernel {ceil['copy_kernel']['GB/s']} GB/s, runtime blit "
-        f"{ceil['runtime_blit_hipMemcpyAsync']['GB/s']} GB/s; scan at {ceil['headline_scan_over_best']:.3f} of best")
+        f"{ceil['runtime_blit_hipMemcpyAsync']['GB/s']} GB/s, scan-shaped copy in block order "
+        f"{ceil['copy_scan_shape_block_order']['GB/s']} GB/s, same scan kernel without look-back "
+        f"{ceil['scan_rows_one_tile_no_lookback']['GB/s']} GB/s; scan at {ceil['headline_scan_over_best']:.3f} "
+        f"of best, {ceil['headline_scan_over_in_order_copy']:.3f} of the in-order copy, "
+        f"{ceil['headline_scan_over_lookback_free']:.3f} of itself without look-back")
 
     line = {
         "metric": "achieved HBM GB/s (% of peak) for f32 sum-reduce and u32 scan at 2^28 elems",

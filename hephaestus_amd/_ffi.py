@@ -120,6 +120,7 @@ SIGNATURES = {
     "hx_device_count": (I32, [POINTER(I32)]),
     "hx_device_open": (I32, [I32, POINTER(P)]),
     "hx_device_close": (I32, [P]),
+    "hx_stream_release": (I32, [P, P]),
     "hx_device_get_info": (I32, [P, POINTER(HxDeviceInfo)]),
     "hx_device_stream": (I32, [P, POINTER(P)]),
     "hx_device_get_limits": (I32, [P, POINTER(HxDeviceLimits)]),
@@ -156,6 +157,9 @@ SIGNATURES = {
     "hx_scan_noalloc": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, P]),
     "hx_noalloc_scratch_bytes": (U64, []),
     "hx_debug_set_wait_limits": (I32, [U32, U32]),
+    "hx_debug_set_launch_count": (I32, [P, P, P, U64]),
+    "hx_debug_tagged_word_hi": (U32, [U32, U32, U32]),
+    "hx_debug_copy_scan_shape": (I32, [P, P, P, U64, P]),
     "hx_prepare_scan": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, POINTER(P)]),
     "hx_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),
     "hx_prepare_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, POINTER(P)]),

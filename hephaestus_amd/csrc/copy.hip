@@ -62,7 +62,62 @@ __global__ __launch_bounds__(kBlock) void copy_bytes_kernel(const uint8_t *src, 
     for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < bytes; i += nthreads) dst[i] = src[i];
 }
 
+// Copy in the access pattern of the integer scan's look-back tiles: block b
+// moves tile b (no XCD reordering, since a look-back needs every tile's
+// predecessors dispatched first), 8 waves x 16 steps = 128 KiB, each wave
+// its own contiguous 16 KiB run, every load issued before the first store.
+// The best a single-pass scan in that order and shape could stream; the
+// bench reports it beside the library copy (copy_tiles_kernel).
+constexpr int kScanShapeWaves = 8;
+constexpr int kScanShapeSteps = 16;
+constexpr uint64_t kScanShapeBytes = (uint64_t)kScanShapeWaves * kWave * 16 * kScanShapeSteps;
+
+__global__ __launch_bounds__(kScanShapeWaves * kWave) void copy_scan_shape_kernel(const char *src, char *dst) {
+    const uint64_t base = (uint64_t)blockIdx.x * kScanShapeBytes;
+    const uint32_t lane_off =
+        ((uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave * kScanShapeSteps + lane_id()) * 16u;
+    u32x4_a4 v[kScanShapeSteps];
+#pragma unroll
+    for (int j = 0; j < kScanShapeSteps; ++j)
+        v[j] = load_a4<true>((const u32x4_a4 *)(src + base + lane_off + (uint32_t)j * (kWave * 16)));
+    __builtin_amdgcn_sched_barrier(0);
+    const auto orsrc = stream_rsrc(dst + base, (uint32_t)kScanShapeBytes);
+#pragma unroll
+    for (int j = 0; j < kScanShapeSteps; ++j) stream_store(v[j], orsrc, lane_off + (uint32_t)j * (kWave * 16));
+}
+
+// Zero `count` 64-bit words.  Used where status words must be cleared on a
+// stream that a caller may capture into a HIP graph (a kernel node replays
+// correctly where a captured memset node may not).
+__global__ __launch_bounds__(kBlock) void clear_words_kernel(uint64_t *words, uint64_t count) {
+    const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < count; i += stride) words[i] = 0;
+}
+
 } // namespace
+
+hx_status launch_clear_words(void *words, uint64_t count, hipStream_t stream) {
+    if (count == 0) return HX_OK;
+    uint64_t blocks = ceil_div(count, kBlock);
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(clear_words_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, (uint64_t *)words,
+                       count);
+    return check_launch("clear_words_kernel");
+}
+
+hx_status launch_copy_scan_shape(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
+    if (bytes % kScanShapeBytes != 0 || (((uintptr_t)src | (uintptr_t)dst) & 3u) != 0)
+        return fail(HX_ERR_DISPATCH_FAILED,
+                    "the scan-shaped copy moves whole %llu-byte tiles between 4-byte aligned buffers",
+                    (unsigned long long)kScanShapeBytes);
+    const uint64_t tiles = bytes / kScanShapeBytes;
+    if (tiles >= 0x80000000ull)
+        return fail(HX_ERR_DISPATCH_FAILED, "copy of %llu bytes exceeds the grid range", (unsigned long long)bytes);
+    if (tiles == 0) return HX_OK;
+    hipLaunchKernelGGL(copy_scan_shape_kernel, dim3((uint32_t)tiles), dim3(kScanShapeWaves * kWave), 0, stream,
+                       (const char *)src, (char *)dst);
+    return check_launch("copy_scan_shape_kernel");
+}
 
 hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t stream) {
     if (bytes == 0) return ok();

@@ -71,6 +71,7 @@ hx_status plan_map(hx_map_reduction map, hx_dtype dtype, const void *a, uint64_t
 
 struct MapPlan final : hx_plan {
     MapReduceArgs args;
+    bool tagged() const override { return true; }
     hx_status dispatch(hipStream_t stream) override {
         return launch_map_reduce(args, ws, ws_bytes, lookback, stream);
     }

@@ -368,17 +368,28 @@ __device__ __forceinline__ double ld_relaxed_f64(const double *p) {
 
 // ----------------------------------------------- single-launch grid folds
 // A grid reduction in one launch: every block but the last publishes its
-// partial as self-tagged words (word h = (tag << 32) | 32-bit half h of the
-// value) with relaxed agent-scope stores; the last block -- dispatched last
-// -- gathers them.  A reader accepts a partial only when every half carries
-// this launch's tag, so no release/acquire pair (which on multi-XCD CDNA
-// writes back and invalidates the L2) is needed.  Slot words start zeroed
-// and tags are never 0.
+// partial as self-tagged words with relaxed agent-scope stores; the last
+// block -- dispatched last -- gathers them.  A reader accepts a partial only
+// when every half carries this launch's tag, so no release/acquire pair
+// (which on multi-XCD CDNA writes back and invalidates the L2) is needed.
+// Slot words start zeroed and tags are never 0.
+//
+// A slot word has the layout of a look-back status word -- high half
+// (tag << 2) | flag, low half 32 bits of the value -- with flag 3
+// (kSlotFlag), which no look-back status uses (they use 1 and 2).  Slots
+// and statuses share one workspace region and one tag counter, so a slot
+// never reads a status word left by another kernel as a current partial,
+// whatever the two launches' tags.
+// The look-back statuses (scan.hip, segmented.hip) build their high halves
+// with status_word_hi as well.
+constexpr uint32_t kSlotFlag = 3;
+__host__ __device__ __forceinline__ uint32_t status_word_hi(uint32_t tag, uint32_t flag) { return (tag << 2) | flag; }
+__host__ __device__ __forceinline__ uint32_t slot_word_hi(uint32_t tag) { return status_word_hi(tag, kSlotFlag); }
 template <typename Acc> struct PartialSlot {
     static_assert(sizeof(Acc) == 4 || sizeof(Acc) == 8, "partials are 32- or 64-bit");
     static constexpr uint32_t kWords = sizeof(Acc) / 4;
     __device__ __forceinline__ static void publish(uint64_t *w, uint32_t tag, Acc v) {
-        const uint64_t t = (uint64_t)tag << 32;
+        const uint64_t t = (uint64_t)slot_word_hi(tag) << 32;
         if constexpr (kWords == 1) {
             st_relaxed(w, t | __builtin_bit_cast(uint32_t, v));
         } else {
@@ -388,14 +399,15 @@ template <typename Acc> struct PartialSlot {
         }
     }
     __device__ __forceinline__ static bool read(const uint64_t *w, uint32_t tag, Acc &v) {
+        const uint32_t want = slot_word_hi(tag);
         if constexpr (kWords == 1) {
             const uint64_t a = ld_relaxed(w);
             v = __builtin_bit_cast(Acc, (uint32_t)a);
-            return (uint32_t)(a >> 32) == tag;
+            return (uint32_t)(a >> 32) == want;
         } else {
             const uint64_t a = ld_relaxed(&w[0]), b = ld_relaxed(&w[1]);
             v = __builtin_bit_cast(Acc, (a & 0xFFFFFFFFull) | (b << 32));
-            return (uint32_t)(a >> 32) == tag && (uint32_t)(b >> 32) == tag;
+            return (uint32_t)(a >> 32) == want && (uint32_t)(b >> 32) == want;
         }
     }
 };

@@ -18,8 +18,16 @@ namespace hx {
 // end-of-launch bookkeeping is needed, and therefore no device-scope
 // release/acquire (which on multi-XCD CDNA writes back and invalidates the
 // L2) on the hot path.
+//
+// A dispatch recorded into a HIP graph (stream capture) is replayed with the
+// tag it was recorded with, so captured dispatches use the one reserved tag
+// kCapturedTag, which eager launches never draw, and record a clear of the
+// status words in front of the kernel: every replay starts from zeroed words,
+// and eager launches never read a replay's words as current.
+constexpr uint32_t kCapturedTag = 0x3FFFFFFFu;
 struct LookbackState {
-    uint32_t launches = 0; // launches so far on this workspace
+    uint64_t launches = 0;  // eager launches so far on this workspace
+    bool captured = false;  // the launch being queued is under stream capture
 };
 
 // The buffers the immediate (un-prepared) entry points use on ONE stream:
@@ -65,15 +73,20 @@ struct hx_device {
     hipEvent_t pinned_ev[2] = {nullptr, nullptr};
 
     // Immediate-mode buffers, one set per stream handle the caller has used
-    // (created on first use, freed at hx_device_close).  A stream handle is
-    // only reused by the runtime after the destroyed stream's work has
-    // drained, so an entry never serves two live streams at once.
+    // (created on first use, freed by hx_stream_release or at
+    // hx_device_close).  A stream handle is only reused by the runtime after
+    // the destroyed stream's work has drained, so an entry never serves two
+    // live streams at once.
     std::mutex streams_mu;
     std::unordered_map<hipStream_t, std::unique_ptr<hx::StreamWorkspace>> immediate;
 
     // This device's copy of the no-allocation scratch array (its device
-    // address, looked up at hx_device_open with the device current).
+    // address, looked up at hx_device_open with the device current), and the
+    // lock held by hx_scan_noalloc from its clear kernel to its scan launch,
+    // so calls from several host threads on one stream queue as whole
+    // clear + scan pairs.
     void *noalloc_scratch = nullptr;
+    std::mutex noalloc_mu;
 
     // Run-time compiled kernels (hx_kernel_compile_cached), by cache key;
     // their modules are unloaded at hx_device_close.
@@ -107,6 +120,9 @@ hx_status hip_fail(hx_status status, hipError_t err, const char *what);
 
 hx_status bind_device(const hx_device *dev);
 hipStream_t pick_stream(const hx_device *dev, hx_stream stream);
+// Whether `stream` is being captured into a HIP graph (any capture status
+// other than none, an invalidated capture included).
+hx_status stream_capturing(hipStream_t stream, bool *capturing);
 // Map the status of a kernel launch (hipGetLastError) to DispatchFailed.
 hx_status check_launch(const char *kernel);
 // Unload every run-time compiled kernel of the device (hx_device_close).
@@ -183,14 +199,16 @@ private:
     std::unique_lock<std::mutex> lock_;
 };
 
-// Tag for the next look-back launch on a workspace of `ws_bytes`; clears the
-// status area when the 30-bit tag space wraps.
 // Poll limits of the bounded waits (hx_debug_set_wait_limits): look-back
 // polls before a waiter computes a missing predecessor, and gather polls per
 // partial before the gathering block recomputes it (0: recompute all).
 uint32_t lookback_poll_limit();
 uint32_t gather_poll_limit();
 
+// Tag for the next look-back launch on a workspace of `ws_bytes`: a fresh
+// eager tag in [1, kCapturedTag), with the status area cleared (by a fill
+// kernel) when that range wraps; kCapturedTag under capture (the caller has
+// cleared the words in front of the launch).
 hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
                                hipStream_t stream, uint32_t *tag);
 void commit_lookback_launch(LookbackState &st);
@@ -316,6 +334,11 @@ hx_status launch_vector_op(hx_vector_op op, const float *t, const float *s, floa
 
 // Stream-ordered device-to-device copy of `bytes` bytes (a streaming kernel).
 hx_status launch_copy(const void *src, void *dst, uint64_t bytes, hipStream_t stream);
+// The copy in the integer scan's tile shape and order (a bench yardstick):
+// whole 128 KiB tiles, block b -> tile b.
+hx_status launch_copy_scan_shape(const void *src, void *dst, uint64_t bytes, hipStream_t stream);
+// Zero `count` 64-bit words with a fill kernel (safe under graph capture).
+hx_status launch_clear_words(void *words, uint64_t count, hipStream_t stream);
 
 hx_status launch_fill_random(void *dst, uint64_t n, hx_dtype dtype,
                              hx_distribution dist, uint64_t seed, double p0,
@@ -331,6 +354,11 @@ inline uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 // `mu` serialises dispatches of one plan from several host threads, so each
 // draws its own look-back tag; launches on different streams are ordered by
 // the caller.
+//
+// Under stream capture (hx_plan_dispatch checks), a plan whose launches are
+// tagged (tagged()) records a fill kernel over its status words and then its
+// launch with kCapturedTag, so the graph can be replayed any number of
+// times; plans without tagged words are captured as they are.
 struct hx_plan {
     hx_device *dev = nullptr;
     void *ws = nullptr;
@@ -339,4 +367,6 @@ struct hx_plan {
     std::mutex mu;
     virtual ~hx_plan();
     virtual hx_status dispatch(hipStream_t stream) = 0;
+    // Whether dispatch() draws a look-back tag for words in ws.
+    virtual bool tagged() const { return false; }
 };

@@ -25,15 +25,6 @@ constexpr uint64_t kNoAllocBytes = 2ull << 20;
 
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 
-namespace {
-
-__global__ __launch_bounds__(256) void clear_words_kernel(uint64_t *words, uint64_t count) {
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) words[i] = 0;
-}
-
-} // namespace
-
 uint64_t noalloc_scratch_bytes() { return kNoAllocBytes; }
 
 hx_status lookup_noalloc_scratch(void **ptr) {
@@ -57,14 +48,8 @@ hx_status launch_scan_noalloc(const ScanArgs &a, void *scratch_ptr, hipStream_t 
                     (unsigned long long)bytes, (unsigned long long)kNoAllocBytes);
     if (scratch_ptr == nullptr)
         return fail(HX_ERR_DEVICE_UNAVAILABLE, "the no-allocation scratch was not set up for this device");
-    if (scan_uses_lookback(a) && bytes > kLookbackOffset) {
-        const uint64_t words = (bytes - kLookbackOffset) / 8;
-        uint64_t blocks = ceil_div(words, 256);
-        if (blocks > 1024) blocks = 1024;
-        hipLaunchKernelGGL(clear_words_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
-                           (uint64_t *)((char *)scratch_ptr + kLookbackOffset), words);
-        HX_TRY(check_launch("clear_words_kernel"));
-    }
+    if (scan_uses_lookback(a) && bytes > kLookbackOffset)
+        HX_TRY(launch_clear_words((char *)scratch_ptr + kLookbackOffset, (bytes - kLookbackOffset) / 8, stream));
     // The status words were just cleared, so the first tag is fresh.
     LookbackState fresh;
     return launch_scan(a, scratch_ptr, bytes, fresh, stream);

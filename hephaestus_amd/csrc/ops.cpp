@@ -116,6 +116,7 @@ hx_status plan_full(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
 
 struct FullPlan final : hx_plan {
     FullReduceArgs args;
+    bool tagged() const override { return true; }
     hx_status dispatch(hipStream_t stream) override {
         return launch_full_reduce(args, ws, ws_bytes, lookback, stream);
     }
@@ -261,6 +262,7 @@ hx_status plan_scan(hx_op op, hx_dtype dtype, hx_scan_kind kind, hx_scan_directi
 
 struct ScanPlan final : hx_plan {
     ScanArgs args;
+    bool tagged() const override { return scan_uses_lookback(args); }
     hx_status dispatch(hipStream_t stream) override {
         return launch_scan(args, ws, ws_bytes, lookback, stream);
     }
@@ -304,6 +306,7 @@ hx_status plan_segmented(hx_op op, hx_dtype dtype, const void *values, uint64_t 
 
 struct SegmentedPlan final : hx_plan {
     SegmentedArgs args;
+    bool tagged() const override { return true; }
     hx_status dispatch(hipStream_t stream) override {
         return launch_segmented(args, ws, ws_bytes, nullptr, 0, lookback, stream);
     }
@@ -487,6 +490,7 @@ hx_status hx_scan_noalloc(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind
     HX_TRY(plan_scan(op, dtype, kind, direction, in, in_buf_len, in_layout, axis, out, out_buf_len,
                      out_layout, &a));
     HX_TRY(bind_device(dev));
+    std::lock_guard<std::mutex> guard(dev->noalloc_mu);
     HX_TRY(launch_scan_noalloc(a, dev->noalloc_scratch, pick_stream(dev, stream)));
     return ok();
 }

@@ -11,8 +11,9 @@
 //     xor-butterflies and publishes one partial;
 //   * the last block (dispatched last) gathers the partials, folds them in
 //     index order and writes the result.
-// A partial is published as self-tagged 64-bit words -- (launch tag, 32-bit
-// half of the value) -- with relaxed agent-scope stores, and the gathering
+// A partial is published as self-tagged 64-bit words -- high half the launch
+// tag in the look-back layout with the slot flag (slot_word_hi), low half 32
+// bits of the value -- with relaxed agent-scope stores, and the gathering
 // block accepts a partial only when every half carries this launch's tag.
 // No release/acquire pair is needed: a "last block done" counter would need
 // a device-scope acq_rel per block, which on multi-XCD CDNA writes back and
@@ -401,6 +402,13 @@ uint64_t full_reduce_workspace_bytes(uint64_t n) {
     return kLookbackOffset + (uint64_t)full_reduce_blocks(n) * 16;
 }
 
+// High half of a tagged word as the kernels build it (the host-side copy of
+// the same inline functions): kind 0 a look-back status with `flag`, kind 1
+// a partial slot.
+uint32_t tagged_word_hi(uint32_t kind, uint32_t tag, uint32_t flag) {
+    return kind == 0 ? status_word_hi(tag, flag) : slot_word_hi(tag);
+}
+
 hx_status launch_full_reduce(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, LookbackState &lb,
                              hipStream_t stream) {
     switch (a.dtype) {
@@ -414,3 +422,7 @@ hx_status launch_full_reduce(const FullReduceArgs &a, void *ws, uint64_t ws_byte
 }
 
 } // namespace hx
+
+extern "C" uint32_t hx_debug_tagged_word_hi(uint32_t kind, uint32_t tag, uint32_t flag) {
+    return hx::tagged_word_hi(kind, tag, flag);
+}

@@ -69,6 +69,13 @@ hipStream_t pick_stream(const hx_device *dev, hx_stream stream) {
     return stream ? (hipStream_t)stream : dev->stream;
 }
 
+hx_status stream_capturing(hipStream_t stream, bool *capturing) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    HX_HIP(hipStreamIsCapturing(stream, &status), HX_ERR_DISPATCH_FAILED, "hipStreamIsCapturing");
+    *capturing = status != hipStreamCaptureStatusNone;
+    return HX_OK;
+}
+
 hx_status check_launch(const char *kernel) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(HX_ERR_DISPATCH_FAILED, err, kernel);
@@ -122,6 +129,15 @@ hx_status grow_stream_buffer(hipStream_t stream, void *&buf, uint64_t &have, uin
 hx_status Immediate::open(hx_device *dev, hipStream_t stream) {
     dev_ = dev;
     stream_ = stream;
+    // An immediate call draws a fresh look-back tag per call and may grow
+    // (allocate, zero-fill, synchronize) its stream's buffers: none of that
+    // can be recorded into a graph and replayed.
+    bool capturing = false;
+    HX_TRY(stream_capturing(stream, &capturing));
+    if (capturing)
+        return fail(HX_ERR_DISPATCH_FAILED,
+                    "immediate calls cannot be recorded into a HIP graph (the stream is capturing): capture "
+                    "hx_plan_dispatch of a prepared plan, or hx_scan_noalloc, instead");
     {
         std::lock_guard<std::mutex> guard(dev->streams_mu);
         std::unique_ptr<StreamWorkspace> &slot = dev->immediate[stream];
@@ -132,7 +148,9 @@ hx_status Immediate::open(hx_device *dev, hipStream_t stream) {
                 return fail(HX_ERR_ALLOCATION_FAILED, "host allocation of a stream workspace failed");
             }
         }
-        sw_ = slot.get(); // entries are never erased before hx_device_close
+        // Entries are erased only by hx_stream_release, whose caller
+        // guarantees that no other call uses that stream meanwhile.
+        sw_ = slot.get();
     }
     lock_ = std::unique_lock<std::mutex>(sw_->mu);
     return HX_OK;
@@ -156,18 +174,25 @@ hx_status Immediate::scratch(uint64_t bytes, void **scratch) {
 
 hx_status next_lookback_launch(LookbackState &st, void *ws, uint64_t ws_bytes,
                                hipStream_t stream, uint32_t *tag) {
-    const uint32_t t = (st.launches % 0x3FFFFFFFu) + 1u;
+    if (st.captured) {
+        *tag = kCapturedTag;
+        return HX_OK;
+    }
+    // Eager tags cycle through [1, kCapturedTag).
+    const uint32_t t = (uint32_t)(st.launches % (kCapturedTag - 1u)) + 1u;
     if (t == 1u && st.launches != 0u && ws_bytes > kLookbackOffset) {
-        // The tag space wrapped: words from 2^30 - 1 launches ago would read
-        // as current, so clear them once.
-        HX_HIP(hipMemsetAsync((char *)ws + kLookbackOffset, 0, ws_bytes - kLookbackOffset, stream),
-               HX_ERR_DISPATCH_FAILED, "look-back status clear");
+        // The tag range wrapped: words from kCapturedTag - 1 launches ago
+        // would read as current, so clear them once (a fill kernel, which a
+        // graph replays correctly).
+        HX_TRY(launch_clear_words((char *)ws + kLookbackOffset, (ws_bytes - kLookbackOffset) / 8, stream));
     }
     *tag = t;
     return HX_OK;
 }
 
-void commit_lookback_launch(LookbackState &st) { st.launches += 1u; }
+void commit_lookback_launch(LookbackState &st) {
+    if (!st.captured) st.launches += 1u;
+}
 
 namespace {
 std::atomic<uint32_t> g_lookback_polls{64};
@@ -197,6 +222,28 @@ hx_status hx_debug_set_wait_limits(uint32_t lookback_polls, uint32_t gather_poll
     g_gather_polls.store(gather_polls, std::memory_order_relaxed);
     return ok();
 }
+
+hx_status hx_debug_set_launch_count(hx_device *dev, hx_plan *plan, hx_stream stream, uint64_t launches) {
+    if (plan) {
+        std::lock_guard<std::mutex> guard(plan->mu);
+        plan->lookback.launches = launches;
+        return ok();
+    }
+    if (!dev) return fail(HX_ERR_INVALID_CONFIGURATION, "null device handle");
+    const hipStream_t s = pick_stream(dev, stream);
+    StreamWorkspace *sw = nullptr;
+    {
+        std::lock_guard<std::mutex> guard(dev->streams_mu);
+        auto it = dev->immediate.find(s);
+        if (it == dev->immediate.end())
+            return fail(HX_ERR_INVALID_CONFIGURATION, "no immediate workspace has been used on this stream");
+        sw = it->second.get();
+    }
+    std::lock_guard<std::mutex> guard(sw->mu);
+    sw->lookback.launches = launches;
+    return ok();
+}
+
 
 const char *hx_status_name(hx_status status) {
     switch (status) {
@@ -331,6 +378,26 @@ hx_status hx_device_open(int32_t ordinal, hx_device **out) {
         return bail(fail(HX_ERR_ADAPTER_UNAVAILABLE, "ROCm sanity transfer mismatch: [%u] != [%u]",
                          back, host));
     *out = dev;
+    return ok();
+}
+
+hx_status hx_stream_release(hx_device *dev, hx_stream stream) {
+    if (!stream) return ok(); // the device's own stream keeps its buffers until hx_device_close
+    HX_TRY(bind_device(dev));
+    std::unique_ptr<StreamWorkspace> sw;
+    {
+        std::lock_guard<std::mutex> guard(dev->streams_mu);
+        auto it = dev->immediate.find((hipStream_t)stream);
+        if (it == dev->immediate.end()) return ok();
+        sw = std::move(it->second);
+        dev->immediate.erase(it);
+    }
+    std::lock_guard<std::mutex> guard(sw->mu);
+    // Launches queued on the stream may still read the buffers.
+    const hipError_t err = hipStreamSynchronize((hipStream_t)stream);
+    if (sw->ws) (void)hipFree(sw->ws);
+    if (sw->scratch) (void)hipFree(sw->scratch);
+    if (err != hipSuccess) return hip_fail(HX_ERR_DISPATCH_FAILED, err, "stream synchronize before release");
     return ok();
 }
 
@@ -620,6 +687,13 @@ hx_status hx_copy(hx_device *dev, const void *src, uint64_t src_len, void *dst,
     return ok();
 }
 
+hx_status hx_debug_copy_scan_shape(hx_device *dev, const void *src, void *dst, uint64_t bytes, hx_stream stream) {
+    HX_TRY(bind_device(dev));
+    if (bytes > 0 && (!src || !dst)) return fail(HX_ERR_DISPATCH_FAILED, "null copy pointer");
+    HX_TRY(launch_copy_scan_shape(src, dst, bytes, pick_stream(dev, stream)));
+    return ok();
+}
+
 hx_status hx_copy_async(hx_device *dev, const void *src, uint64_t src_len, void *dst, uint64_t dst_len,
                         uint32_t elem_size, hx_stream stream) {
     HX_TRY(check_elem(elem_size));
@@ -666,11 +740,34 @@ hx_status hx_event_elapsed_ms(hx_event start, hx_event stop, float *ms) {
     return ok();
 }
 
+} // extern "C"
+
+namespace {
+
+// One dispatch of `plan` on `s` (plan->mu held).  Under stream capture a
+// tagged plan records a clear of its status words and runs with the reserved
+// captured tag, so every replay of the graph starts from zeroed words.
+hx_status dispatch_locked(hx_plan *plan, hipStream_t s) {
+    bool capturing = false;
+    HX_TRY(stream_capturing(s, &capturing));
+    if (!capturing || !plan->tagged()) return plan->dispatch(s);
+    if (plan->ws_bytes > kLookbackOffset)
+        HX_TRY(launch_clear_words((char *)plan->ws + kLookbackOffset, (plan->ws_bytes - kLookbackOffset) / 8, s));
+    plan->lookback.captured = true;
+    const hx_status st = plan->dispatch(s);
+    plan->lookback.captured = false;
+    return st;
+}
+
+} // namespace
+
+extern "C" {
+
 hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream) {
     if (!plan) return fail(HX_ERR_INVALID_CONFIGURATION, "null plan");
     HX_TRY(bind_device(plan->dev));
     std::lock_guard<std::mutex> guard(plan->mu);
-    HX_TRY(plan->dispatch(pick_stream(plan->dev, stream)));
+    HX_TRY(dispatch_locked(plan, pick_stream(plan->dev, stream)));
     return ok();
 }
 
@@ -681,7 +778,7 @@ hx_status hx_plan_dispatch_batch(hx_plan *const *plans, uint64_t count, hx_strea
     for (uint64_t i = 0; i < count; ++i) {
         HX_TRY(bind_device(plans[i]->dev));
         std::lock_guard<std::mutex> guard(plans[i]->mu);
-        HX_TRY(plans[i]->dispatch(pick_stream(plans[i]->dev, stream)));
+        HX_TRY(dispatch_locked(plans[i], pick_stream(plans[i]->dev, stream)));
     }
     return ok();
 }

@@ -55,7 +55,7 @@ constexpr int kSuper = 64;                           // tiles per superblock
 constexpr uint32_t kInvalid = 0, kAggregate = 1, kPrefix = 2;
 
 __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
-    return ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v;
+    return ((uint64_t)status_word_hi(tag, flag) << 32) | (uint64_t)v;
 }
 
 // (tag, flag, value) in one 64-bit word: [63:34] tag, [33:32] flag, [31:0] value.

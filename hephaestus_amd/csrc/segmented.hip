@@ -91,7 +91,7 @@ __device__ __forceinline__ uint64_t off_at(const SegParams &p, uint64_t k) {
 }
 
 __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
-    return ((uint64_t)((tag << 2) | flag) << 32) | (uint64_t)v;
+    return ((uint64_t)status_word_hi(tag, flag) << 32) | (uint64_t)v;
 }
 
 // The status tile u's owner publishes, computed by ONE wave (fallback path):

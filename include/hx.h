@@ -33,6 +33,22 @@
  * plan are serialised across threads, and the caller orders dispatches of
  * one plan that go to different streams (an event, or a synchronize), as
  * for any other work on those streams.
+ *
+ * Graph capture: hx_plan_dispatch and hx_plan_dispatch_batch may be called
+ * on a stream that is being captured into a HIP graph.  A captured dispatch
+ * of a plan with look-back statuses or partial slots (scan, full reduce,
+ * map-reduction, segmented plans) records a fill kernel that zeroes the
+ * plan's status words, then its launches with one tag reserved for captured
+ * work, so the graph may be replayed any number of times and reads the
+ * plan's bound buffers afresh on each replay.  A replay uses the plan's
+ * workspace: replays and eager dispatches of the same plan must be ordered
+ * like any two dispatches of it.  The immediate entry points (hx_scan,
+ * hx_reduce_full, hx_argmax_full, hx_reduce_axis, hx_reduce_rows,
+ * hx_segmented_reduce, hx_map_reduce, hx_trace) draw a fresh tag per call
+ * and may grow their stream's buffers, so on a capturing stream they fail
+ * with HX_ERR_DISPATCH_FAILED before anything is queued; hx_scan_noalloc,
+ * the vector forms, hx_copy_async and hx_fill_random queue plain kernels and
+ * may be captured.
  */
 #ifndef HX_H
 #define HX_H
@@ -158,6 +174,15 @@ hx_status hx_device_count(int32_t *count);
  * No device / bad ordinal -> HX_ERR_ADAPTER_UNAVAILABLE. */
 hx_status hx_device_open(int32_t ordinal, hx_device **out);
 hx_status hx_device_close(hx_device *dev);
+/* No counterpart in the reference (its launches all go to the null stream).
+ * Frees the buffers that immediate calls keep for `stream` (created on its
+ * first use, at least 1 MiB of workspace and 1 MiB of scratch) after waiting
+ * for the work queued on it.  Call it before destroying a stream that
+ * immediate calls have used; otherwise those buffers stay allocated until
+ * hx_device_close.  The caller guarantees that no other call uses `stream`
+ * meanwhile, as for destroying it.  NULL (the device's own stream) and
+ * streams without buffers are no-ops. */
+hx_status hx_stream_release(hx_device *dev, hx_stream stream);
 hx_status hx_device_get_info(const hx_device *dev, hx_device_info *out);
 /* The device's own stream (what a NULL hx_stream selects). */
 hx_status hx_device_stream(const hx_device *dev, hx_stream *out);
@@ -491,7 +516,8 @@ hx_status hx_vector_binary(hx_device *dev, hx_vector_op op, hx_dtype dtype,
 /* dispatch_full / dispatch_prepared / dispatch_scan (core reduction.rs:
  * 222,304-308; scan.rs:259-263): re-run a prepared plan on `stream`.
  * Allocates nothing.  Concurrent calls on one plan are serialised; a plan
- * dispatched on two streams must be ordered by the caller between them. */
+ * dispatched on two streams must be ordered by the caller between them.
+ * May be captured into a HIP graph (see Graph capture above). */
 hx_status hx_plan_dispatch(hx_plan *plan, hx_stream stream);
 /* submit_prepared_reduction_batch (rocm application/prepared_reduction.rs:
  * 164-174): dispatch `count` plans in order on `stream` with no host
@@ -586,6 +612,29 @@ hx_status hx_fill_random(hx_device *dev, void *dst, uint64_t n, hx_dtype dtype,
  * reductions bit-identical, f32 scans within their bound); only time
  * changes.  Not for production use: a small limit makes large inputs slow. */
 hx_status hx_debug_set_wait_limits(uint32_t lookback_polls, uint32_t gather_polls);
+/* No counterpart in the reference.  For tests of the look-back tag range:
+ * sets how many launches the library counts as already made on a
+ * workspace -- `plan`'s when it is not NULL, else the immediate workspace of
+ * `stream` on `dev` (HX_ERR_INVALID_CONFIGURATION if that stream has none
+ * yet).  Eager tags cycle through [1, 2^30 - 1); the launch that wraps the
+ * range back to tag 1 first clears the workspace's status words, so
+ * presetting the count to 2^30 - 2 makes the next launch the wrap. */
+hx_status hx_debug_set_launch_count(hx_device *dev, hx_plan *plan,
+                                    hx_stream stream, uint64_t launches);
+/* No counterpart in the reference.  The high 32 bits of a tagged word as the
+ * kernels build it: kind 0 a look-back status word with `flag` (1 aggregate,
+ * 2 inclusive prefix), kind 1 a partial slot of a one-launch reduction
+ * (`flag` ignored).  Both kinds share a workspace region and one tag
+ * counter; a test checks that no slot word equals any status word. */
+uint32_t hx_debug_tagged_word_hi(uint32_t kind, uint32_t tag, uint32_t flag);
+/* No counterpart in the reference.  A bench yardstick: copies `bytes` (a
+ * multiple of 131072) from src to dst in the access pattern of the integer
+ * scan's look-back tiles -- block b moves 128 KiB tile b, each of 8 waves a
+ * contiguous 16 KiB run, every load issued before the first store -- the
+ * order and shape a single-pass scan is held to, unlike hx_copy_async's
+ * 256 KiB tiles in XCD-contiguous order. */
+hx_status hx_debug_copy_scan_shape(hx_device *dev, const void *src, void *dst,
+                                   uint64_t bytes, hx_stream stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

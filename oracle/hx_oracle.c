@@ -497,3 +497,120 @@ void hxo_scan_excl_u32_threads(const uint32_t *x, uint64_t n, uint32_t *out, int
     free(jobs);
     free(tid);
 }
+
+/* All-core forms of the remaining baselines: the same per-element
+ * arithmetic as the sequential functions above, split over `threads`
+ * pthreads by contiguous ranges. */
+
+typedef struct {
+    const float *x;
+    uint64_t rows, cols, ld;
+    const hxo_affine *pro;
+    double *sum, *abs_sum;
+    float *max;
+    uint32_t *argmax;
+    uint64_t lo, hi;
+} rows_job_t;
+
+static void *rows_job(void *arg) {
+    rows_job_t *j = (rows_job_t *)arg;
+    hxo_rows_f32(j->x + j->lo * j->ld, j->hi - j->lo, j->cols, j->ld, j->pro, j->sum ? j->sum + j->lo : NULL,
+                 j->abs_sum ? j->abs_sum + j->lo : NULL, j->max ? j->max + j->lo : NULL,
+                 j->argmax ? j->argmax + j->lo : NULL);
+    return NULL;
+}
+
+void hxo_rows_f32_threads(const float *x, uint64_t rows, uint64_t cols, uint64_t ld, const hxo_affine *pro,
+                          double *sum, double *abs_sum, float *max, uint32_t *argmax, int threads) {
+    if (threads < 1) threads = 1;
+    rows_job_t *jobs = calloc((size_t)threads, sizeof(rows_job_t));
+    pthread_t *tid = calloc((size_t)threads, sizeof(pthread_t));
+    for (int t = 0; t < threads; ++t) {
+        jobs[t] = (rows_job_t){x, rows, cols, ld, pro, sum, abs_sum, max, argmax,
+                               rows * (uint64_t)t / (uint64_t)threads, rows * (uint64_t)(t + 1) / (uint64_t)threads};
+        pthread_create(&tid[t], NULL, rows_job, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    free(jobs);
+    free(tid);
+}
+
+typedef struct {
+    const uint32_t *x;
+    uint64_t n;
+    const uint32_t *offsets;
+    uint32_t *out;
+    uint64_t lo, hi; /* segment range */
+} seg_job_t;
+
+static void *seg_job(void *arg) {
+    seg_job_t *j = (seg_job_t *)arg;
+    hxo_segmented_sum_u32(j->x, j->n, j->offsets + j->lo, j->hi - j->lo, j->out + j->lo);
+    return NULL;
+}
+
+void hxo_segmented_sum_u32_threads(const uint32_t *x, uint64_t n, const uint32_t *offsets, uint64_t segments,
+                                   uint32_t *out, int threads) {
+    if (threads < 1) threads = 1;
+    seg_job_t *jobs = calloc((size_t)threads, sizeof(seg_job_t));
+    pthread_t *tid = calloc((size_t)threads, sizeof(pthread_t));
+    for (int t = 0; t < threads; ++t) {
+        jobs[t] = (seg_job_t){x, n, offsets, out, segments * (uint64_t)t / (uint64_t)threads,
+                              segments * (uint64_t)(t + 1) / (uint64_t)threads};
+        pthread_create(&tid[t], NULL, seg_job, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    free(jobs);
+    free(tid);
+}
+
+typedef struct {
+    const float *x;
+    float *out;
+    uint64_t lo, hi;
+    double total, carry;
+} fscan_job_t;
+
+static void *fsum_job(void *arg) {
+    fscan_job_t *j = (fscan_job_t *)arg;
+    double s = 0.0;
+    for (uint64_t i = j->lo; i < j->hi; ++i) s += (double)j->x[i];
+    j->total = s;
+    return NULL;
+}
+
+static void *fscan_job(void *arg) {
+    fscan_job_t *j = (fscan_job_t *)arg;
+    double run = j->carry;
+    for (uint64_t i = j->lo; i < j->hi; ++i) {
+        run += (double)j->x[i];
+        j->out[i] = (float)run;
+    }
+    return NULL;
+}
+
+/* Forward inclusive f32 scan on all cores: chunk totals in f64, their
+ * exclusive prefix as each chunk's carry, then each chunk's running f64 sum
+ * rounded to f32 per element (a reduce-then-scan, the usual CPU form). */
+void hxo_scan_incl_f32_threads(const float *x, uint64_t n, float *out, int threads) {
+    if (threads < 1) threads = 1;
+    fscan_job_t *jobs = calloc((size_t)threads, sizeof(fscan_job_t));
+    pthread_t *tid = calloc((size_t)threads, sizeof(pthread_t));
+    for (int t = 0; t < threads; ++t) {
+        jobs[t].x = x;
+        jobs[t].out = out;
+        jobs[t].lo = n * (uint64_t)t / (uint64_t)threads;
+        jobs[t].hi = n * (uint64_t)(t + 1) / (uint64_t)threads;
+        pthread_create(&tid[t], NULL, fsum_job, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    double run = 0.0;
+    for (int t = 0; t < threads; ++t) {
+        jobs[t].carry = run;
+        run += jobs[t].total;
+    }
+    for (int t = 0; t < threads; ++t) pthread_create(&tid[t], NULL, fscan_job, &jobs[t]);
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    free(jobs);
+    free(tid);
+}

@@ -108,9 +108,21 @@ int32_t hxo_norm_max_i32(const int32_t *x, uint64_t n);
 float hxo_norm_max_f32(const float *x, uint64_t n);
 void hxo_fma_arrays(const float *x, const float *y, float f, uint64_t n, float *out);
 
-/* ---- CPU baselines (timed, not checkers) ---- */
+/* ---- CPU baselines on all cores (timed, not checkers; each pinned against
+ * the sequential functions above by tests/test_oracle.py) ----
+ * f32 sum: plain f64 partial per thread, partials added in thread order. */
 double hxo_sum_f32_threads(const float *x, uint64_t n, int threads);
+/* u32 exclusive scan: chunk totals, then each chunk rescanned from its carry. */
 void hxo_scan_excl_u32_threads(const uint32_t *x, uint64_t n, uint32_t *out, int threads);
+/* hxo_rows_f32 over contiguous row ranges (bit-identical to it). */
+void hxo_rows_f32_threads(const float *x, uint64_t rows, uint64_t cols, uint64_t ld, const hxo_affine *pro,
+                          double *sum, double *abs_sum, float *max, uint32_t *argmax, int threads);
+/* hxo_segmented_sum_u32 over contiguous segment ranges (bit-identical). */
+void hxo_segmented_sum_u32_threads(const uint32_t *x, uint64_t n, const uint32_t *offsets, uint64_t segments,
+                                   uint32_t *out, int threads);
+/* Forward inclusive f32 scan: f64 chunk totals and carries, f64 running sum
+ * rounded to f32 per element. */
+void hxo_scan_incl_f32_threads(const float *x, uint64_t n, float *out, int threads);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,10 @@ _SIG = {
     "hxo_fma_arrays": (None, [c_void_p, c_void_p, c_float, c_uint64, c_void_p]),
     "hxo_sum_f32_threads": (c_double, [c_void_p, c_uint64, c_int]),
     "hxo_scan_excl_u32_threads": (None, [c_void_p, c_uint64, c_void_p, c_int]),
+    "hxo_rows_f32_threads": (None, [c_void_p, c_uint64, c_uint64, c_uint64, POINTER(Affine), c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_int]),
+    "hxo_segmented_sum_u32_threads": (None, [c_void_p, c_uint64, c_void_p, c_uint64, c_void_p, c_int]),
+    "hxo_scan_incl_f32_threads": (None, [c_void_p, c_uint64, c_void_p, c_int]),
 }
 
 _lib = None
@@ -303,3 +307,27 @@ def sum_f32_threads(x: np.ndarray, threads: int) -> float:
 
 def scan_excl_u32_threads(x: np.ndarray, out: np.ndarray, threads: int) -> None:
     lib().hxo_scan_excl_u32_threads(_ptr(x), x.size, _ptr(out), threads)
+
+
+def rows_threads(x: np.ndarray, nrows: int, cols: int, threads: int, ld: int | None = None, prologue=None):
+    """rows() on `threads` pthreads: (sum f64, abs sum f64, max f32, argmax u32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ld = cols if ld is None else ld
+    s, a = np.empty(nrows, np.float64), np.empty(nrows, np.float64)
+    m, i = np.empty(nrows, np.float32), np.empty(nrows, np.uint32)
+    lib().hxo_rows_f32_threads(_ptr(x), nrows, cols, ld, _aff(prologue), _ptr(s), _ptr(a), _ptr(m), _ptr(i),
+                               threads)
+    return s, a, m, i
+
+
+def segmented_sum_threads(x: np.ndarray, offsets: np.ndarray, threads: int) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    offsets = np.ascontiguousarray(offsets, dtype=np.uint32)
+    s = offsets.size - 1
+    out = np.empty(max(s, 0), dtype=np.uint32)
+    lib().hxo_segmented_sum_u32_threads(_ptr(x.view(np.uint32)), x.size, _ptr(offsets), s, _ptr(out), threads)
+    return out.view(x.dtype)
+
+
+def scan_incl_f32_threads(x: np.ndarray, out: np.ndarray, threads: int) -> None:
+    lib().hxo_scan_incl_f32_threads(_ptr(x), x.size, _ptr(out), threads)

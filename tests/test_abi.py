@@ -303,3 +303,44 @@ def test_require_limits_messages():
         hx.RocmDevice.require_limits(have, hx.DeviceLimits(max_immediate_size=1))
     assert _ffi.last_message() == "ROCm device limit max_immediate_size 0 is below required 1"
     assert "below required" in str(info.value)
+
+
+def test_partial_slots_never_match_lookback_status_words():
+    """Look-back statuses (flag 1 aggregate, 2 inclusive prefix) and the
+    partial slots of the one-launch reductions share a workspace region and
+    one tag counter.  Through the library's own encoders: a slot word of any
+    tag never equals a status word of any tag (the slot layout carries flag
+    3), and within each kind distinct tags give distinct words.  Checked for
+    every tag below 2^14, around powers of two and at the ends of the eager
+    range and the reserved captured tag (2^30 - 1)."""
+    lib = hx.load_native()
+    tags = set(range(1, 1 << 14))
+    for k in range(14, 30):
+        tags |= {(1 << k) - 1, 1 << k, (1 << k) + 1, (1 << k) + 2}
+    tags |= {(1 << 30) - 3, (1 << 30) - 2, (1 << 30) - 1}
+    tags = sorted(t for t in tags if 1 <= t < (1 << 30))
+    slot = {lib.hx_debug_tagged_word_hi(1, t, 0): t for t in tags}
+    agg = {lib.hx_debug_tagged_word_hi(0, t, 1): t for t in tags}
+    pre = {lib.hx_debug_tagged_word_hi(0, t, 2): t for t in tags}
+    for words in (slot, agg, pre):
+        assert len(words) == len(tags)          # injective in the tag
+        assert 0 not in words                   # zeroed memory is never current
+    assert not (set(slot) & set(agg)), "a slot word equals an aggregate status word"
+    assert not (set(slot) & set(pre)), "a slot word equals a prefix status word"
+    assert not (set(agg) & set(pre))
+    # The collision the old slot layout had: a slot of tag 4t + f read a
+    # status word of tag t with flag f.
+    for t in (1, 2, 1000, (1 << 28) - 1):
+        for f in (1, 2):
+            assert lib.hx_debug_tagged_word_hi(1, 4 * t + f, 0) != lib.hx_debug_tagged_word_hi(0, t, f)
+
+
+def test_captured_and_eager_tags_are_disjoint_in_status_words():
+    """The tag reserved for captured dispatches (2^30 - 1) encodes to words
+    that no eager tag in [1, 2^30 - 1) produces."""
+    lib = hx.load_native()
+    cap = 0x3FFFFFFF
+    captured = {lib.hx_debug_tagged_word_hi(0, cap, f) for f in (1, 2)} | {lib.hx_debug_tagged_word_hi(1, cap, 0)}
+    for t in (1, 2, 3, (1 << 29), cap - 2, cap - 1):
+        eager = {lib.hx_debug_tagged_word_hi(0, t, f) for f in (1, 2)} | {lib.hx_debug_tagged_word_hi(1, t, 0)}
+        assert not (eager & captured)

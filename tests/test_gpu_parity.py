@@ -1202,3 +1202,20 @@ def test_copy_unaligned_ranges(device, oracle, skew, nbytes):
     want = np.zeros(total, np.uint8)
     want[skew:skew + nbytes] = x[skew:skew + nbytes]
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("tiles", [1, 3, 257])
+def test_copy_in_scan_shape_bit_exact(device, oracle, tiles):
+    """hx_debug_copy_scan_shape (the bench's in-order yardstick) moves whole
+    128 KiB tiles bit-exactly and rejects partial tiles."""
+    from hephaestus_amd import _ffi
+
+    n = tiles * 32768
+    x = oracle.uniform_int(n, seed=tiles, lo=0, hi=2**32 - 1)
+    src = device.upload(x)
+    dst = device.alloc_zeroed(np.uint32, n + 1)
+    _ffi.check(_ffi.lib().hx_debug_copy_scan_shape(device.handle, src.ptr, dst.ptr, 4 * n, None))
+    got = device.download_owned(dst)
+    assert np.array_equal(got[:n], x) and got[n] == 0
+    with pytest.raises(hx.DispatchFailed, match="whole 131072-byte tiles"):
+        _ffi.check(_ffi.lib().hx_debug_copy_scan_shape(device.handle, src.ptr, dst.ptr, 4 * n - 16, None))

@@ -517,3 +517,62 @@ def test_multithreaded_scan_baseline_equals_sequential(oracle, threads):
     oracle.scan_excl_u32_threads(x, out, threads)
     assert np.array_equal(out, oracle.scan_sum(x, exclusive=True))
     assert np.array_equal(out, (np.cumsum(x, dtype=np.uint32) - x))
+
+
+@pytest.mark.parametrize("threads", [1, 3, 16])
+def test_multithreaded_sum_baseline(oracle, threads):
+    """The all-core f32 sum baseline (plain f64 partials in thread order):
+    exact on integer-valued inputs (every partial and total below 2^53), and
+    within the f32 bound of the compensated oracle on random inputs.  A
+    dropped or doubled chunk fails the exact case."""
+    n = 1_000_003
+    xi = (oracle.uniform_int(n, seed=21, lo=0, hi=1000).astype(np.float32) - np.float32(500))
+    exact = int(np.sum(xi.astype(np.int64)))
+    assert oracle.sum_f32_threads(xi, threads) == float(exact)
+    x = oracle.uniform_real(n, seed=22, lo=-1.0, hi=1.0)
+    ref, ab = oracle.full_sum(x)
+    assert abs(oracle.sum_f32_threads(x, threads) - ref) <= 2 * oracle.ceil_log2(n) * 2.0**-23 * ab
+
+
+@pytest.mark.parametrize("threads", [1, 5, 16])
+def test_multithreaded_rows_baseline_equals_sequential(oracle, threads):
+    """The all-core rows baseline is the sequential rows fold per row range:
+    bit-identical sums, maxima and argmaxes (ragged row split, padded rows,
+    with and without the prologue)."""
+    rows, cols, ld = 101, 333, 340
+    x = oracle.normal(rows * ld, seed=23)
+    for pro in (None, (0.5, 0.25)):
+        want = oracle.rows(x, rows, cols, ld, prologue=pro)
+        got = oracle.rows_threads(x, rows, cols, threads, ld=ld, prologue=pro)
+        for g, w in zip(got, want):
+            assert np.array_equal(g, w)
+
+
+@pytest.mark.parametrize("threads", [1, 7, 16])
+def test_multithreaded_segmented_baseline_equals_sequential(oracle, threads):
+    """All-core segmented sum == the sequential oracle, bit-exact, including
+    empty segments and fewer segments than threads."""
+    n = 200_003
+    x = oracle.uniform_int(n, seed=24, lo=-1000, hi=1000, dtype=np.int32)
+    for mean in (3.0, 300.0, 1e6):
+        off = oracle.geometric_offsets(n, mean, seed=25)
+        assert np.array_equal(oracle.segmented_sum_threads(x, off, threads), oracle.segmented_sum(x, off))
+    off = np.array([0, 0, 5, 5, n], np.uint32)
+    assert np.array_equal(oracle.segmented_sum_threads(x, off, threads), oracle.segmented_sum(x, off))
+
+
+@pytest.mark.parametrize("threads", [1, 4, 16])
+def test_multithreaded_f32_scan_baseline(oracle, threads):
+    """All-core inclusive f32 scan: exact on integer-valued inputs whose
+    prefixes stay below 2^24 (a wrong chunk carry or a shifted index fails
+    it), and within 2*ceil(log2 n)*eps*sum|x| of the compensated oracle on
+    uniform[0, 1) inputs."""
+    n = 500_009
+    xi = oracle.uniform_int(n, seed=26, lo=0, hi=31).astype(np.float32)
+    out = np.empty_like(xi)
+    oracle.scan_incl_f32_threads(xi, out, threads)
+    assert np.array_equal(out, np.cumsum(xi.astype(np.int64)).astype(np.float32))
+    x = oracle.uniform_real(n, seed=27, lo=0.0, hi=1.0)
+    oracle.scan_incl_f32_threads(x, out, threads)
+    bad, _ = oracle.check_scan_f32(x, out)
+    assert bad == 0
