@@ -159,6 +159,8 @@ SIGNATURES = {
     "hx_debug_set_wait_limits": (I32, [U32, U32]),
     "hx_debug_set_launch_count": (I32, [P, P, P, U64]),
     "hx_debug_tagged_word_hi": (U32, [U32, U32, U32]),
+    "hx_debug_slot16_encode": (None, [U32, U32, U64, P]),
+    "hx_debug_slot16_decode": (U32, [U32, P, P]),
     "hx_debug_copy_scan_shape": (I32, [P, P, P, U64, P]),
     "hx_prepare_scan": (I32, [P, I32, I32, I32, I32, P, U64, LP, U32, P, U64, LP, POINTER(P)]),
     "hx_segmented_reduce": (I32, [P, I32, I32, P, U64, P, U64, P, U64, P]),

@@ -385,6 +385,28 @@ __device__ __forceinline__ double ld_relaxed_f64(const double *p) {
 constexpr uint32_t kSlotFlag = 3;
 __host__ __device__ __forceinline__ uint32_t status_word_hi(uint32_t tag, uint32_t flag) { return (tag << 2) | flag; }
 __host__ __device__ __forceinline__ uint32_t slot_word_hi(uint32_t tag) { return status_word_hi(tag, kSlotFlag); }
+
+// The 16-byte f64 status slot of the f32 tile scans (scan.hip
+// F64QuadStatus): dword i = (check << 16) | bits [63-16i : 48-16i] of the
+// value, check = status_word_hi(tag, flag) with tag < 2^14.  decode gives
+// flag 0 unless all four checks are equal and carry `tag`, so a read that
+// mixes dwords of two writes, or meets words of the 64-bit formats above
+// (whose high halves are below 2^16, while a check dword is >= 2^18), reads
+// as not ready.
+__host__ __device__ __forceinline__ void slot16_encode(uint32_t tag, uint32_t flag, uint64_t b, uint32_t (&q)[4]) {
+    const uint32_t c = status_word_hi(tag, flag) << 16;
+    q[0] = c | (uint32_t)(b >> 48);
+    q[1] = c | ((uint32_t)(b >> 32) & 0xFFFFu);
+    q[2] = c | ((uint32_t)(b >> 16) & 0xFFFFu);
+    q[3] = c | ((uint32_t)b & 0xFFFFu);
+}
+__host__ __device__ __forceinline__ uint32_t slot16_decode(uint32_t tag, const uint32_t (&q)[4], uint64_t &b) {
+    const uint32_t c = q[0] >> 16;
+    const bool same = (((q[0] ^ q[1]) | (q[0] ^ q[2]) | (q[0] ^ q[3])) >> 16) == 0u;
+    b = ((uint64_t)(q[0] & 0xFFFFu) << 48) | ((uint64_t)(q[1] & 0xFFFFu) << 32) | ((uint64_t)(q[2] & 0xFFFFu) << 16) |
+        (uint64_t)(q[3] & 0xFFFFu);
+    return (same && (c >> 2) == tag) ? (c & 3u) : 0u;
+}
 template <typename Acc> struct PartialSlot {
     static_assert(sizeof(Acc) == 4 || sizeof(Acc) == 8, "partials are 32- or 64-bit");
     static constexpr uint32_t kWords = sizeof(Acc) / 4;

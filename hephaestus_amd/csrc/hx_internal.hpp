@@ -13,7 +13,7 @@
 
 namespace hx {
 // Host-side bookkeeping of one look-back workspace: every launch tags its
-// status words with a fresh 30-bit tag, so words left by earlier launches
+// status words with a fresh 14-bit tag, so words left by earlier launches
 // (of any look-back kernel) read as "not yet published".  No device-side
 // end-of-launch bookkeeping is needed, and therefore no device-scope
 // release/acquire (which on multi-XCD CDNA writes back and invalidates the
@@ -24,7 +24,11 @@ namespace hx {
 // kCapturedTag, which eager launches never draw, and record a clear of the
 // status words in front of the kernel: every replay starts from zeroed words,
 // and eager launches never read a replay's words as current.
-constexpr uint32_t kCapturedTag = 0x3FFFFFFFu;
+// Tags stay below 2^14 because the f32 scan slots carry (tag << 2) | flag
+// in 16 bits of each dword; eager tags cycle through [1, kCapturedTag) and
+// the wrapping launch clears the status words (one fill kernel per 16382
+// launches).
+constexpr uint32_t kCapturedTag = 0x3FFFu;
 struct LookbackState {
     uint64_t launches = 0;  // eager launches so far on this workspace
     bool captured = false;  // the launch being queued is under stream capture

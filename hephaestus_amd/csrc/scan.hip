@@ -34,12 +34,13 @@
 // tile-ticket counter: one same-address device-scope atomic per tile
 // serialises at ~11 ns on MI355X, which alone cost 745 us for 65536 tiles.
 //
-// Status words carry a 30-bit per-launch tag (set by the host), so a launch
+// Status words carry a 14-bit per-launch tag (set by the host), so a launch
 // never clears the status array and needs no end-of-launch bookkeeping.
 // Integer scans publish (tag, flag, value) in ONE 64-bit word.  f32 scans
-// carry the inter-tile prefix in f64, split into two self-tagged words,
-// which keeps every output within a few ulp of the f32-rounded exact prefix
-// at 2^30 elements.
+// carry the inter-tile prefix in f64 (every output stays within a few ulp of
+// the f32-rounded exact prefix at 2^30 elements) in ONE 16-byte slot, read
+// and written with one 16-byte access; each of its four dwords carries the
+// tag and flag next to 16 bits of the value.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -85,55 +86,49 @@ struct PackedStatus {
     }
 };
 
-// f64 carries: each 64-bit status word holds (tag, flag, one 32-bit half of
-// the f64).  Entry t's aggregate lives in words [4t, 4t+1] and its inclusive
-// prefix in [4t+2, 4t+3]; a reader accepts a value only when both halves
-// carry the current tag, so no release/acquire ordering is needed.  A
-// superblock slot can have writers whose values differ in the last bits (its
-// owner, and fallbacks that rebuild it from its tiles in another order):
-// whoever moves the high word from an old tag to this launch's tag with a
-// CAS also writes the low word, and everyone else leaves the slot alone, so
-// halves of different writers never mix (publish).  Tile slots need no CAS
-// (publish_tile).
-struct F64Status {
+// f64 carries of the tile scans: one 16-byte slot per entry, overwritten by
+// its single writer (aggregate, then inclusive prefix) and read with ONE
+// 16-byte load per lane.  Dword i of the slot is (check << 16) | bits
+// [63-16i : 48-16i] of the f64, with check = (tag << 2) | flag (tags below
+// 2^14; slot16_encode / slot16_decode).  A reader accepts the slot only when the four checks agree with
+// each other and carry this launch's tag, so only 32-bit single-copy
+// atomicity is assumed: a read that mixes dwords of two writes (aggregate
+// and prefix, or an earlier launch's words) never has four equal checks.
+// Words of the packed and partial-slot formats left in the same area read as
+// not ready: their high halves are below 2^16, a check dword is at least
+// 2^18.  Measured against two self-tagged 8-byte words read with two loads,
+// 2^30 f32 inclusive scan on MI355X: 1360 -> 1315 us; the number of loads
+// per poll, not their cache scope, set the difference (agent and system
+// scope both 1360 us).
+struct F64QuadStatus {
     using C = double;
+    typedef uint32_t slot_t __attribute__((ext_vector_type(4)));
     uint64_t *words;
-    __device__ __forceinline__ void publish(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
-        const uint64_t b = __builtin_bit_cast(uint64_t, v);
-        uint64_t *w = words + 4 * t + (flag == kPrefix ? 2 : 0);
-        uint64_t cur = ld_relaxed(&w[0]);
-        if ((uint32_t)(cur >> 34) == tag) return;
-        if (__hip_atomic_compare_exchange_strong(&w[0], &cur, status_word(tag, flag, (uint32_t)(b >> 32)),
-                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            st_relaxed(&w[1], status_word(tag, flag, (uint32_t)b));
+    __device__ __forceinline__ volatile __attribute__((address_space(1))) slot_t *slot(uint64_t t) const {
+        return (volatile __attribute__((address_space(1))) slot_t *)(words + 2 * t);
     }
-    __device__ __forceinline__ void publish_if_unset(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+    __device__ __forceinline__ void publish(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
+        uint32_t w[4];
+        slot16_encode(tag, flag, __builtin_bit_cast(uint64_t, v), w);
+        slot_t q;
+        q.x = w[0];
+        q.y = w[1];
+        q.z = w[2];
+        q.w = w[3];
+        *slot(t) = q;
+    }
+    __device__ __forceinline__ void publish_tile(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
         publish(t, tag, flag, v);
     }
-    // Tile-level owner publication, two plain stores and no CAS round trip.
-    // Safe without the CAS: a tile's inclusive prefix has one writer (its
-    // owner), and every writer of a tile's aggregate (owner or fallback)
-    // computes bit-identical values, so halves of different writers agree.
-    __device__ __forceinline__ void publish_tile(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
-        const uint64_t b = __builtin_bit_cast(uint64_t, v);
-        uint64_t *w = words + 4 * t + (flag == kPrefix ? 2 : 0);
-        st_relaxed(&w[0], status_word(tag, flag, (uint32_t)(b >> 32)));
-        st_relaxed(&w[1], status_word(tag, flag, (uint32_t)b));
-    }
+    // Slots have one writer: waiters that compute a missing value keep it
+    // to themselves (SharedFallback).
+    __device__ __forceinline__ void publish_if_unset(uint64_t, uint32_t, uint32_t, C) const {}
     __device__ __forceinline__ void read(uint64_t t, uint32_t tag, uint32_t &flag, C &v) const {
-        const uint64_t *w = words + 4 * t;
-        const uint64_t a0 = ld_relaxed(&w[0]), a1 = ld_relaxed(&w[1]);
-        const uint64_t p0 = ld_relaxed(&w[2]), p1 = ld_relaxed(&w[3]);
-        const uint32_t want_a = (tag << 2) | kAggregate, want_p = (tag << 2) | kPrefix;
-        if ((uint32_t)(p0 >> 32) == want_p && (uint32_t)(p1 >> 32) == want_p) {
-            flag = kPrefix;
-            v = __builtin_bit_cast(double, (p0 << 32) | (p1 & 0xFFFFFFFFull));
-        } else if ((uint32_t)(a0 >> 32) == want_a && (uint32_t)(a1 >> 32) == want_a) {
-            flag = kAggregate;
-            v = __builtin_bit_cast(double, (a0 << 32) | (a1 & 0xFFFFFFFFull));
-        } else {
-            flag = kInvalid;
-        }
+        const slot_t q = *slot(t);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        uint64_t b;
+        flag = slot16_decode(tag, w, b);
+        v = __builtin_bit_cast(double, b);
     }
 };
 
@@ -160,6 +155,11 @@ struct F64PairStatus {
         v = __builtin_bit_cast(double, (hi << 32) | (lo & 0xFFFFFFFFull));
     }
 };
+
+// Whether waiters that compute a missing status publish it for others
+// (publish_if_unset, a CAS on a single word) or keep it to themselves.
+template <typename S> struct SharedFallback { static constexpr bool value = true; };
+template <> struct SharedFallback<F64QuadStatus> { static constexpr bool value = false; };
 
 struct ScanParams {
     const void *in;
@@ -243,10 +243,22 @@ template <typename C> struct KnownAgg {
     __device__ __forceinline__ C agg() { return a; }
 };
 
+// Wave-wide fold of the look-back values.  f64 carries fold with DPP moves
+// (no lane-address registers, which the shuffle form keeps live across the
+// whole look-back); 32-bit values keep the shuffle butterfly.
+template <typename Op, typename C> __device__ __forceinline__ C lookback_reduce(C v) {
+    if constexpr (sizeof(C) == 8)
+        return group_reduce<64>(v, [](C a, C b) { return Op::combine(a, b); });
+    else
+        return wave_reduce<Op, C>(v);
+}
+
 // Fold of the statuses of the `count` (<= 64) tiles just before tile
 // `tile_end`, nearest first, stopping at the first inclusive prefix; `found`
 // tells whether one was met.  Lane l reads the tile at distance l.  A tile
-// that stays unpublished is computed by tile_aggregate.
+// that stays unpublished is computed by tile_aggregate: published for every
+// waiter where the status takes shared fallbacks, else kept in the lane that
+// reads that tile.
 template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES,
           typename Hook>
 __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, uint64_t tile_end, int count,
@@ -257,10 +269,19 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
     uint32_t flag;
     C val;
     uint32_t spins = 0;
+    constexpr bool kShared = SharedFallback<Status>::value;
+    bool own = false; // this lane's tile aggregate, computed by this wave
+    C own_val = ident;
     for (;;) {
         flag = kAggregate; // lanes past `count`: valid, not a prefix, identity
         val = ident;
         if (lane < count) st.read(tile_end - 1 - lane, p.tag, flag, val);
+        if constexpr (!kShared) {
+            if (own && flag == kInvalid) {
+                flag = kAggregate;
+                val = own_val;
+            }
+        }
         const uint64_t pm = ballot(flag == kPrefix);
         const uint64_t im = ballot(flag == kInvalid);
         // Every status up to and including the nearest prefix is needed.
@@ -269,9 +290,15 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
         if (missing == 0ull) break;
         hook.poll();
         if (++spins >= p.spin_limit) {
-            const uint64_t u = tile_end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
+            const int k = __ffsll((long long)missing) - 1;
+            const uint64_t u = tile_end - 1 - (uint64_t)k;
             const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS, WAVES>(p, u);
-            if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
+            if constexpr (kShared) {
+                if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
+            } else if (lane == k) {
+                own = true;
+                own_val = (C)a;
+            }
             spins = 0;
             continue;
         }
@@ -280,7 +307,7 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
     const uint64_t pm = ballot(flag == kPrefix);
     const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
     found = pm != 0ull;
-    return wave_reduce<Op, C>((lane <= first) ? val : ident);
+    return lookback_reduce<Op, C>((lane <= first) ? val : ident);
 }
 
 // Exclusive prefix of tile `tile` (position `tin` in its line), computed by
@@ -315,10 +342,19 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
         uint32_t flag;
         C val;
         uint32_t spins = 0;
+        constexpr bool kShared = SharedFallback<Status>::value;
+        uint32_t own_flag = kInvalid; // this lane's superblock, rebuilt by this wave
+        C own_val = ident;
         for (;;) {
             flag = kPrefix; // before the line's first superblock: identity
             val = ident;
             if (in_line) st1.read((uint64_t)idx, p.tag, flag, val);
+            if constexpr (!kShared) {
+                if (flag == kInvalid && own_flag != kInvalid) {
+                    flag = own_flag;
+                    val = own_val;
+                }
+            }
             const uint64_t pm = ballot(flag == kPrefix);
             const uint64_t im = ballot(flag == kInvalid);
             const uint64_t need = pm ? (((pm & (~pm + 1ull)) << 1) - 1ull) : ~0ull;
@@ -328,11 +364,17 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
             if (++spins >= p.spin_limit) {
                 // Rebuild the missing superblock's value from its 64 tiles:
                 // an inclusive prefix if one of them has one, else the sum.
-                const uint64_t s = (uint64_t)(pred - (__ffsll((long long)missing) - 1));
+                const int k = __ffsll((long long)missing) - 1;
+                const uint64_t s = (uint64_t)(pred - k);
                 const uint64_t s_end = line * p.tiles_per_line + (s - line_super + 1) * kSuper;
                 bool f = false;
                 const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, s_end, kSuper, f, hook);
-                if (lane == 0) st1.publish_if_unset(s, p.tag, f ? kPrefix : kAggregate, v);
+                if constexpr (kShared) {
+                    if (lane == 0) st1.publish_if_unset(s, p.tag, f ? kPrefix : kAggregate, v);
+                } else if (lane == k) {
+                    own_flag = f ? kPrefix : kAggregate;
+                    own_val = v;
+                }
                 spins = 0;
                 continue;
             }
@@ -340,7 +382,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
         }
         const uint64_t pm = ballot(flag == kPrefix);
         const int first = pm ? (__ffsll((long long)pm) - 1) : kWave;
-        excl = Op::combine(excl, wave_reduce<Op, C>((lane <= first) ? val : ident));
+        excl = Op::combine(excl, lookback_reduce<Op, C>((lane <= first) ? val : ident));
         if (pm) break;
         pred -= kWave;
     }
@@ -356,6 +398,35 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
     }
 }
 
+// The tile's exclusive prefix applied to an element's in-tile prefix.
+// Integers: one combine.  f32 with an f64 carry: the carry is split once per
+// tile into f32 hi + lo (lo = the f32 rounding of carry - hi, exact to
+// ~2^-48 relative) and each output is hi + (within + lo) (sums) or
+// fma(hi, within, lo * within) (products), about one ulp from the f64
+// combine rounded to f32 and far inside 2 ceil(log2 n) eps sum|x|.  The f64
+// form converts every element to f64: the compiler hoists those conversions
+// above the store branch and holds 96 extra registers, which kept f32 tiles
+// at one block per CU.  A non-finite hi takes lo = 0 (hi + w then gives the
+// f64 form's inf or NaN).
+template <typename T, typename C, typename Op> struct TileCarry {
+    T c;
+    __device__ __forceinline__ explicit TileCarry(C v) : c((T)v) {}
+    __device__ __forceinline__ T apply(T within) const { return Op::combine(c, within); }
+};
+template <typename Op> struct TileCarry<float, double, Op> {
+    float hi, lo;
+    __device__ __forceinline__ explicit TileCarry(double v) {
+        hi = (float)v;
+        lo = __builtin_isfinite(hi) ? (float)(v - (double)hi) : 0.0f;
+    }
+    __device__ __forceinline__ float apply(float w) const {
+        if constexpr (std::is_same<Op, OpSum>::value)
+            return hi + (w + lo);
+        else
+            return __builtin_fmaf(hi, w, lo * w);
+    }
+};
+
 // Full tiles of unit-stride lines (every tile but a line's ragged last one;
 // the vectors need only 4-byte alignment): a block-uniform base pointer plus one 32-bit lane offset,
 // so each step is a single base + offset + immediate vector access with no
@@ -364,13 +435,21 @@ __device__ __forceinline__ T finalize(C tile_excl, T within) {
 // elements e..e+3 of a lane's step are one 16-byte vector in reversed order,
 // at byte (tile_bytes - 16 - lane_off - j * 1024) from the block's lowest
 // address (always >= 0).
-// Integer tiles are held to 128 VGPRs, two 8-wave blocks per CU: the
+// Tiles are held to 128 VGPRs, two 8-wave blocks per CU: the integer
 // inclusive forms (131 VGPRs unconstrained, one block per CU) spill a few
 // words of look-back state and still gain ~3% (2^28 u32 inclusive 0.388 ->
-// 0.378 ms).  f32 tiles, whose f64 carries need ~148, keep the compiler's
-// budget (a 128 cap spilled 88 bytes and lost 18%).
+// 0.378 ms).  f32 tiles fit in 121 with no spill through three changes: the
+// split carry (TileCarry), the DPP look-back fold (lookback_reduce), and wave
+// 0's 64 data registers parked in LDS while it looks back (ParkTile), with
+// the wave's exclusive offset read only after the look-back.  Before them
+// f32 tiles needed ~150 and ran one 12-wave block per CU.
 template <typename T> struct ScanWavesPerEu { static constexpr int value = 4; };
-template <> struct ScanWavesPerEu<float> { static constexpr int value = 1; };
+
+// f32 tiles park wave 0's data in LDS during the look-back (16 KiB per
+// block).  Integer tiles fit without it (116 VGPRs); parking measured 0.4%
+// slower there.
+template <typename T> struct ParkTile { static constexpr bool value = false; };
+template <> struct ParkTile<float> { static constexpr bool value = true; };
 
 // Paced tiles (integer scans).  Two blocks share each CU, and the memory
 // instructions of all their waves queue through the CU's one vector-memory
@@ -390,11 +469,9 @@ template <> struct ScanWavesPerEu<float> { static constexpr int value = 1; };
 // the look-back: 338.6).  At 2^30: 1405.5 -> 1323.2 us.  Lines of one tile
 // (row-wise scans) never look back; for them the gaps alone pay (the same
 // kernel without look-back: burst 363.9 us, gaps 341.1; with the priority as
-// well 349.5), so they keep the default priority.  f32 tiles run one 12-wave
-// block per CU, with no second block to let ahead (2^30 f32: 1374.8 us
-// as is, 1375.1 with the priority, 1385.4 with gaps), and are not paced.
-template <typename T> struct ScanPaced { static constexpr bool value = true; };
-template <> struct ScanPaced<float> { static constexpr bool value = false; };
+// well 349.5), so they keep the default priority.  f32 tiles, two blocks
+// per CU as well, gain the same way (2^30 f32: 1382.8 us unpaced, 1315.6
+// paced).
 
 __device__ __forceinline__ void store_gap() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
@@ -438,16 +515,16 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     constexpr int kTileElems = WAVES * kWaveElems;
     __shared__ T s_wave_tot[WAVES];
     __shared__ C s_excl;
+    constexpr bool kPark = ParkTile<T>::value;
+    __shared__ T s_park[kPark ? STEPS * 4 * kWave : 1];
 
-    constexpr bool kPaced = ScanPaced<T>::value;
     const bool looks_back = p.tiles_per_line > 1;
-    if constexpr (kPaced)
-        if (looks_back) __builtin_amdgcn_s_setprio(3);
+    if (looks_back) __builtin_amdgcn_s_setprio(3);
 
     const uint64_t tile = blockIdx.x;
     const uint64_t line = tile / p.tiles_per_line;
     const uint64_t tin = tile - line * p.tiles_per_line;
-    const int w = threadIdx.x / kWave;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = lane_id();
     const int64_t ib = (int64_t)p.in_offset + (int64_t)line * p.in_line_stride;
     const int64_t ob = (int64_t)p.out_offset + (int64_t)line * p.out_line_stride;
@@ -503,15 +580,37 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     }
     if (lane == 0) s_wave_tot[w] = carry;
     __syncthreads();
+    // Wave totals are combined in wave order for the tile aggregate and each
+    // wave's exclusive offset.  f32 tiles read the offset after the look-back
+    // (nothing of it is held across the look-back) and park wave 0's data in
+    // LDS meanwhile, so its registers are free for the look-back; the empty
+    // asm statements keep the compiler from forwarding the parked values.
     T wave_excl = ident;
     T tile_agg = ident;
+    if constexpr (!kPark) {
 #pragma unroll
-    for (int k = 0; k < WAVES; ++k) {
-        if (k < w) wave_excl = Op::combine(wave_excl, s_wave_tot[k]);
-        tile_agg = Op::combine(tile_agg, s_wave_tot[k]);
+        for (int k = 0; k < WAVES; ++k) {
+            if (k < w) wave_excl = Op::combine(wave_excl, s_wave_tot[k]);
+            tile_agg = Op::combine(tile_agg, s_wave_tot[k]);
+        }
     }
 
     if (w == 0) {
+        if constexpr (kPark) {
+#pragma unroll
+            for (int k = 0; k < WAVES; ++k) tile_agg = Op::combine(tile_agg, s_wave_tot[k]);
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                using V = typename Vec4A4<T>::type;
+                V v;
+                v.x = x[j][0];
+                v.y = x[j][1];
+                v.z = x[j][2];
+                v.w = x[j][3];
+                *(V *)&s_park[(j * kWave + lane) * 4] = v;
+            }
+            asm volatile("" ::: "memory");
+        }
         const C agg = (C)tile_agg;
         C excl = Op::template identity<C>();
         if (tin == 0) {
@@ -525,11 +624,27 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
             st1.publish(line * p.supers_per_line + tin / kSuper, p.tag, kPrefix, Op::combine(excl, agg));
         if (lane == 0) s_excl = excl;
+        if constexpr (kPark) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                using V = typename Vec4A4<T>::type;
+                const V v = *(const V *)&s_park[(j * kWave + lane) * 4];
+                x[j][0] = v.x;
+                x[j][1] = v.y;
+                x[j][2] = v.z;
+                x[j][3] = v.w;
+            }
+        }
     }
     __syncthreads();
-    const C tile_excl = s_excl;
-    if constexpr (kPaced)
-        if (looks_back) __builtin_amdgcn_s_setprio(0);
+    const TileCarry<T, C, Op> tile_carry(s_excl);
+    if constexpr (kPark) {
+#pragma unroll
+        for (int k = 0; k < WAVES; ++k)
+            if (k < w) wave_excl = Op::combine(wave_excl, s_wave_tot[k]);
+    }
+    if (looks_back) __builtin_amdgcn_s_setprio(0);
 
     if (full) {
         using V = typename Vec4A4<T>::type;
@@ -538,24 +653,24 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
 #pragma unroll
             for (int j = 0; j < STEPS; ++j) {
                 V v;
-                v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
-                v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
-                v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
-                v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
+                v.w = tile_carry.apply(Op::combine(wave_excl, x[j][0]));
+                v.z = tile_carry.apply(Op::combine(wave_excl, x[j][1]));
+                v.y = tile_carry.apply(Op::combine(wave_excl, x[j][2]));
+                v.x = tile_carry.apply(Op::combine(wave_excl, x[j][3]));
                 stream_store(v, orsrc, rev_off - (uint32_t)j * (kWave * 16));
-                if constexpr (kPaced) store_gap();
+                store_gap();
             }
         } else {
             const auto orsrc = stream_rsrc(out + ob + (int64_t)(tin * kTileElems), kTileElems * (uint32_t)sizeof(T));
 #pragma unroll
             for (int j = 0; j < STEPS; ++j) {
                 V v;
-                v.x = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][0]));
-                v.y = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][1]));
-                v.z = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][2]));
-                v.w = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][3]));
+                v.x = tile_carry.apply(Op::combine(wave_excl, x[j][0]));
+                v.y = tile_carry.apply(Op::combine(wave_excl, x[j][1]));
+                v.z = tile_carry.apply(Op::combine(wave_excl, x[j][2]));
+                v.w = tile_carry.apply(Op::combine(wave_excl, x[j][3]));
                 stream_store(v, orsrc, lane_off + (uint32_t)j * (kWave * 16));
-                if constexpr (kPaced) store_gap();
+                store_gap();
             }
         }
         return;
@@ -565,7 +680,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
         T r[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) r[c] = finalize<T, C, Op>(tile_excl, Op::combine(wave_excl, x[j][c]));
+        for (int c = 0; c < 4; ++c) r[c] = tile_carry.apply(Op::combine(wave_excl, x[j][c]));
         if constexpr (VEC && !REV) {
             if (e + 3 < p.len) {
                 using V = typename Vec4A4<T>::type;
@@ -1549,8 +1664,8 @@ hx_status launch_column(const ScanParams &p, const ColShape &s, bool rev, void *
                : launch_column_v<T, Op, 1, EXCL, false>(p, s, ws, stream);
 }
 
-// One 64-bit word per entry (packed u32), four per entry (split f64).
-uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 32 : 8); }
+// One 64-bit word per entry (packed u32), one 16-byte slot (f64 carries).
+uint64_t status_bytes(uint64_t entries, bool f64) { return entries * (f64 ? 16 : 8); }
 
 // Tile shapes (waves x 16-byte steps per lane).  A line up to 32768
 // elements is one tile: the smallest shape that holds it, so a block never
@@ -1566,9 +1681,10 @@ struct TileShape {
     uint64_t elems() const { return (uint64_t)waves * kWave * 4 * steps; }
 };
 // Lines longer than one 8 x 16 tile: the tiles chained by the look-back.
-constexpr int kLongWaves = 8, kLongSteps = 16;   // integer
-constexpr int kF32Waves = 12, kF32Steps = 16;    // f32
-inline TileShape tile_shape(uint64_t len, bool f32) {
+// f32 lines took 12 x 16 tiles (one block per CU) before f32 tiles fit in
+// 128 VGPRs; 8 x 16 at two blocks per CU: 2^30 f32 1373.1 -> 1315.6 us.
+constexpr int kLongWaves = 8, kLongSteps = 16;
+inline TileShape tile_shape(uint64_t len) {
     if (len <= 256) return {1, 1};
     if (len <= 512) return {1, 2};
     if (len <= 1024) return {2, 2};
@@ -1577,7 +1693,7 @@ inline TileShape tile_shape(uint64_t len, bool f32) {
     if (len <= 8192) return {4, 8};
     if (len <= 16384) return {4, 16};
     if (len <= 32768) return {kWaves, kSteps};
-    return f32 ? TileShape{kF32Waves, kF32Steps} : TileShape{kLongWaves, kLongSteps};
+    return TileShape{kLongWaves, kLongSteps};
 }
 
 template <typename T, typename Op, typename Status, bool EXCL, int STEPS, int WAVES>
@@ -1612,13 +1728,7 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     case 416: return launch_tiles_shaped<T, Op, Status, EXCL, 16, 4>(p, st, st1, vec, rev, stream);
     default: break;
     }
-    if constexpr (std::is_same<T, float>::value) {
-        if (shape.waves == kF32Waves && shape.steps == kF32Steps)
-            return launch_tiles_shaped<T, Op, Status, EXCL, kF32Steps, kF32Waves>(p, st, st1, vec, rev, stream);
-    } else {
-        if (shape.waves == kLongWaves && shape.steps == kLongSteps)
-            return launch_tiles_shaped<T, Op, Status, EXCL, kLongSteps, kLongWaves>(p, st, st1, vec, rev, stream);
-    }
+    static_assert(kLongWaves == kWaves && kLongSteps == kSteps, "long lines take the 32768-element tile");
     return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
 }
 
@@ -1679,7 +1789,7 @@ uint64_t scan_bytes(const ScanArgs &a) {
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
     }
     if (column_mode(a)) return column_bytes(a);
-    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len, a.dtype == HX_DTYPE_F32).elems());
+    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len).elems());
     const bool f64 = a.dtype == HX_DTYPE_F32;
     return kLookbackOffset + status_bytes(tpl * a.lines, f64) + status_bytes(ceil_div(tpl, kSuper) * a.lines, f64);
 }
@@ -1691,7 +1801,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.out = a.out;
     p.lines = a.lines;
     p.len = a.len;
-    const TileShape shape = tile_shape(a.len, std::is_same<T, float>::value);
+    const TileShape shape = tile_shape(a.len);
     p.tiles_per_line = ceil_div(a.len, shape.elems());
     p.total_tiles = p.tiles_per_line * a.lines;
     p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);
@@ -1743,9 +1853,9 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     uint64_t *level1 = (uint64_t *)((char *)level0 + status_bytes(p.total_tiles, f64));
     hx_status s;
     if constexpr (std::is_same<T, float>::value) {
-        F64Status st{level0}, st1{level1};
-        s = a.exclusive ? launch_tiles<T, Op, F64Status, true>(p, st, st1, vec, a.reverse, shape, stream)
-                        : launch_tiles<T, Op, F64Status, false>(p, st, st1, vec, a.reverse, shape, stream);
+        F64QuadStatus st{level0}, st1{level1};
+        s = a.exclusive ? launch_tiles<T, Op, F64QuadStatus, true>(p, st, st1, vec, a.reverse, shape, stream)
+                        : launch_tiles<T, Op, F64QuadStatus, false>(p, st, st1, vec, a.reverse, shape, stream);
     } else {
         PackedStatus st{level0}, st1{level1};
         s = a.exclusive ? launch_tiles<T, Op, PackedStatus, true>(p, st, st1, vec, a.reverse, shape, stream)
@@ -1780,3 +1890,18 @@ hx_status launch_scan(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackSt
 }
 
 } // namespace hx
+
+// Host-side checks of the f32 scan slot codec (the device code uses the same
+// inline functions).
+extern "C" void hx_debug_slot16_encode(uint32_t tag, uint32_t flag, uint64_t bits, uint32_t *dwords) {
+    uint32_t q[4];
+    hx::slot16_encode(tag, flag, bits, q);
+    for (int i = 0; i < 4; ++i) dwords[i] = q[i];
+}
+extern "C" uint32_t hx_debug_slot16_decode(uint32_t tag, const uint32_t *dwords, uint64_t *bits) {
+    const uint32_t q[4] = {dwords[0], dwords[1], dwords[2], dwords[3]};
+    uint64_t b = 0;
+    const uint32_t flag = hx::slot16_decode(tag, q, b);
+    *bits = b;
+    return flag;
+}

@@ -616,9 +616,9 @@ hx_status hx_debug_set_wait_limits(uint32_t lookback_polls, uint32_t gather_poll
  * sets how many launches the library counts as already made on a
  * workspace -- `plan`'s when it is not NULL, else the immediate workspace of
  * `stream` on `dev` (HX_ERR_INVALID_CONFIGURATION if that stream has none
- * yet).  Eager tags cycle through [1, 2^30 - 1); the launch that wraps the
+ * yet).  Eager tags cycle through [1, 2^14 - 1); the launch that wraps the
  * range back to tag 1 first clears the workspace's status words, so
- * presetting the count to 2^30 - 2 makes the next launch the wrap. */
+ * presetting the count to 2^14 - 2 makes the next launch the wrap. */
 hx_status hx_debug_set_launch_count(hx_device *dev, hx_plan *plan,
                                     hx_stream stream, uint64_t launches);
 /* No counterpart in the reference.  The high 32 bits of a tagged word as the
@@ -627,6 +627,14 @@ hx_status hx_debug_set_launch_count(hx_device *dev, hx_plan *plan,
  * (`flag` ignored).  Both kinds share a workspace region and one tag
  * counter; a test checks that no slot word equals any status word. */
 uint32_t hx_debug_tagged_word_hi(uint32_t kind, uint32_t tag, uint32_t flag);
+/* No counterpart in the reference.  The 16-byte status slot of the f32 scans
+ * (f64 carries), as the kernels encode and decode it: four dwords, each
+ * ((tag << 2 | flag) << 16) | 16 bits of `bits` (tags below 2^14).  decode
+ * returns the flag (1 aggregate, 2 inclusive prefix) and the value when all
+ * four dwords carry `tag` and one flag, else 0 ("not ready"), so a read that
+ * mixes dwords of two writes is never accepted.  Host-only, for tests. */
+void hx_debug_slot16_encode(uint32_t tag, uint32_t flag, uint64_t bits, uint32_t *dwords);
+uint32_t hx_debug_slot16_decode(uint32_t tag, const uint32_t *dwords, uint64_t *bits);
 /* No counterpart in the reference.  A bench yardstick: copies `bytes` (a
  * multiple of 131072) from src to dst in the access pattern of the integer
  * scan's look-back tiles -- block b moves 128 KiB tile b, each of 8 waves a

@@ -34,7 +34,7 @@ SCAN = hx.RocmScanOps()
 SEG = hx.RocmSegmentedReductionOps()
 EPS = 2.0 ** -23
 CAPTURE_MODE_GLOBAL = 0
-LAST_EAGER_TAG = (1 << 30) - 2  # eager tags cycle through [1, 2^30 - 1)
+LAST_EAGER_TAG = (1 << 14) - 2  # eager tags cycle through [1, 2^14 - 1)
 
 
 def _hip():
