@@ -21,7 +21,7 @@
 
 namespace hx {
 
-constexpr uint64_t kNoAllocBytes = 2ull << 20;
+constexpr uint64_t kNoAllocBytes = 8ull << 20;
 
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 

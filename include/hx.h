@@ -398,12 +398,11 @@ hx_status hx_scan(hx_device *dev, hx_op op, hx_dtype dtype, hx_scan_kind kind,
 /* No counterpart in the reference.  For callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): hx_scan with the same arguments and
- * results, whose whole workspace is a fixed 2 MiB device array per GPU
+ * results, whose whole workspace is a fixed 8 MiB device array per GPU
  * (hx_noalloc_scratch_bytes), so it calls no hipMalloc, hipFree or
- * allocating library routine.  A scan that needs more workspace (1-D f32
- * scans beyond about 2^31 elements, u32 ones beyond the grid limit, large
- * single-pass column scans) is rejected with HX_ERR_DISPATCH_FAILED before
- * anything is launched.  Every call on a GPU shares that GPU's array: calls
+ * allocating library routine.  A scan that needs more workspace (1-D scans
+ * beyond about 2^31 elements, large single-pass column scans) is rejected
+ * with HX_ERR_DISPATCH_FAILED before anything is launched.  Every call on a GPU shares that GPU's array: calls
  * queued on one stream run in order, calls that overlap on one GPU (other
  * streams, other threads) race. */
 hx_status hx_scan_noalloc(hx_device *dev, hx_op op, hx_dtype dtype,

@@ -83,12 +83,12 @@ def test_noalloc_scan_rejects_oversized_workspace(device):
     import hephaestus_amd as hx
     from hephaestus_amd import Layout, StridedView, _ffi
 
-    assert _ffi.lib().hx_noalloc_scratch_bytes() == 2 << 20
+    assert _ffi.lib().hx_noalloc_scratch_bytes() == 8 << 20
     rows, cols = 65536, 4096
     lay = Layout.c_contiguous([rows, cols])
     x = device.alloc_zeroed(np.uint32, rows * cols)
     out = device.upload(np.full(rows * cols, 7, np.uint32))
-    with pytest.raises(hx.DispatchFailed, match="no-allocation scratch holds 2097152"):
+    with pytest.raises(hx.DispatchFailed, match="no-allocation scratch holds 8388608"):
         hx.RocmScanOps().scan_axis_into_noalloc(device, hx.CumSumOp, StridedView(x, lay), 0,
                                                 hx.ScanDirection.Forward, StridedView(out, lay))
     device.synchronize()
