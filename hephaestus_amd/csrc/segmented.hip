@@ -70,7 +70,7 @@ struct SegParams {
     uint64_t segments; // S
     uint32_t *out;
     uint64_t total_tiles;
-    uint64_t *status;          // look-back words, one per tile
+    uint64_t *status;          // look-back words, one per tile (16 bytes apart)
     uint64_t *sstatus;         // then one per 64-tile superblock
     uint32_t *ub_map, *lb_map; // tile edges -> offset indices (total_tiles + 1 each)
     uint32_t tag;              // this launch's status tag
@@ -93,6 +93,16 @@ __device__ __forceinline__ uint64_t off_at(const SegParams &p, uint64_t k) {
 __device__ __forceinline__ uint64_t status_word(uint32_t tag, uint32_t flag, uint32_t v) {
     return ((uint64_t)status_word_hi(tag, flag) << 32) | (uint64_t)v;
 }
+
+// Status words 16 bytes apart (tile and superblock statuses alike): tiles
+// publish at about the same moment from CUs all over the chip, and dense
+// words put 16 publishers on one 128-byte line.  The scans, whose tiles are
+// four times larger, take a whole line per status; here a 64-lane poll
+// over 64 lines costs more than it saves.  Measured at 2^27 values, us per
+// launch with 8 / 16 / 32 / 128-byte strides: mean 300 84.6 / 84.4 / 85.0 /
+// 88.3; segmented_long workload 111.2 / 105.9 / 105.2 / 107.1.
+constexpr uint64_t kSegStatusStride = 2; // 64-bit words
+__device__ __forceinline__ uint64_t *seg_word(uint64_t *base, uint64_t i) { return base + i * kSegStatusStride; }
 
 // The status tile u's owner publishes, computed by ONE wave (fallback path):
 // a prefix (the sum from the last segment start in the tile to its end) when
@@ -141,7 +151,7 @@ __device__ uint32_t seg_fold_tiles(const SegParams &p, uint64_t end, int count, 
         flag = kAggregate; // lanes past `count`: valid, not a prefix, 0
         val = 0;
         if (lane < count) {
-            const uint64_t wd = ld_relaxed(&p.status[end - 1 - (uint64_t)lane]);
+            const uint64_t wd = ld_relaxed(seg_word(p.status, end - 1 - (uint64_t)lane));
             const uint32_t hi = (uint32_t)(wd >> 32);
             flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
             val = (uint32_t)wd;
@@ -156,7 +166,7 @@ __device__ uint32_t seg_fold_tiles(const SegParams &p, uint64_t end, int count, 
             const uint64_t u = end - 1 - (uint64_t)(__ffsll((long long)missing) - 1);
             uint32_t fflag, fval;
             seg_tile_status<TILE>(p, u, fflag, fval);
-            if (lane == 0) publish_if_unset(&p.status[u], tag, fflag, fval);
+            if (lane == 0) publish_if_unset(seg_word(p.status, u), tag, fflag, fval);
             spins = 0;
             continue;
         }
@@ -208,7 +218,7 @@ template <int TILE, bool TWO_LEVEL> __device__ uint32_t seg_lookback(const SegPa
             const int64_t idx = pred - lane;
             uint32_t flag = kPrefix, val = 0; // before superblock 0: the identity
             if (idx >= 0) {
-                const uint64_t wd = ld_relaxed(&p.sstatus[idx]);
+                const uint64_t wd = ld_relaxed(seg_word(p.sstatus, (uint64_t)idx));
                 const uint32_t hi = (uint32_t)(wd >> 32);
                 flag = ((hi >> 2) == tag) ? (hi & 3u) : kInvalid;
                 val = (uint32_t)wd;
@@ -223,7 +233,7 @@ template <int TILE, bool TWO_LEVEL> __device__ uint32_t seg_lookback(const SegPa
                 const uint32_t v = seg_fold_tiles<TILE>(p, (s + 1) * kSegSuper, kSegSuper, tag, f);
                 c_in += v;
                 if (f) {
-                    if (lane == 0) publish_if_unset(&p.sstatus[s], tag, kPrefix, v);
+                    if (lane == 0) publish_if_unset(seg_word(p.sstatus, s), tag, kPrefix, v);
                     return c_in;
                 }
             }
@@ -406,10 +416,10 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
     if (w == 0 && lane == 0) {
         if (has_head) {
             const uint32_t carry_out = total - (h > t0 ? s_hpref : 0u);
-            st_relaxed(&p.status[tile], status_word(tag, kPrefix, carry_out));
-            if (last_in_super) st_relaxed(&p.sstatus[tile / kSegSuper], status_word(tag, kPrefix, carry_out));
+            st_relaxed(seg_word(p.status, tile), status_word(tag, kPrefix, carry_out));
+            if (last_in_super) st_relaxed(seg_word(p.sstatus, tile / kSegSuper), status_word(tag, kPrefix, carry_out));
         } else if (tile > 0) {
-            st_relaxed(&p.status[tile], status_word(tag, kAggregate, total));
+            st_relaxed(seg_word(p.status, tile), status_word(tag, kAggregate, total));
         }
     }
 
@@ -502,8 +512,8 @@ __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(7
             const bool publish_super = last_in_super && !has_head;
             const uint32_t c_in = seg_lookback<kTile, TWO_LEVEL>(p, tile, tag);
             if (lane == 0) {
-                if (!has_head) st_relaxed(&p.status[tile], status_word(tag, kPrefix, c_in + total));
-                if (publish_super) st_relaxed(&p.sstatus[tile / kSegSuper], status_word(tag, kPrefix, c_in + total));
+                if (!has_head) st_relaxed(seg_word(p.status, tile), status_word(tag, kPrefix, c_in + total));
+                if (publish_super) st_relaxed(seg_word(p.sstatus, tile / kSegSuper), status_word(tag, kPrefix, c_in + total));
                 if (needs_carry && k_lo < k_hi1 && k_lo >= 1 && k_lo <= p.segments) p.out[k_lo - 1] = s_open + c_in;
             }
         }
@@ -1036,7 +1046,7 @@ uint64_t tile_map_bytes(uint64_t tiles) { return align256(2 * (tiles + 1) * 4); 
 uint64_t segmented_lookback_bytes(const SegmentedArgs &a) {
     if (a.n == 0 || a.num_segments == 0 || short_path(a)) return 0;
     const uint64_t tiles = ceil_div(a.n, seg_tile_elems(a));
-    return kLookbackOffset + (tiles + ceil_div(tiles, kSegSuper)) * 8;
+    return kLookbackOffset + (tiles + ceil_div(tiles, kSegSuper)) * 8 * kSegStatusStride;
 }
 
 // Everything else, which must never share memory with status words: the
@@ -1091,7 +1101,7 @@ hx_status launch_segmented(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, 
     const bool long_tile = long_tiles(a);
     p.total_tiles = ceil_div(a.n, seg_tile_elems(a));
     p.status = (uint64_t *)((char *)ws + kLookbackOffset);
-    p.sstatus = p.status + p.total_tiles;
+    p.sstatus = p.status + p.total_tiles * kSegStatusStride;
     p.ub_map = (uint32_t *)aux;
     p.lb_map = p.ub_map + p.total_tiles + 1;
     if (p.total_tiles >= 0x80000000ull)
