@@ -762,6 +762,18 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
                "copy_u32": ceil.get("copy_kernel", {}).get("settle_launches", 0),
                "blit": ceil.get("runtime_blit_hipMemcpyAsync", {}).get("settle_launches", 0)}
     untimed = {k: int(v or 0) + warm for k, v in untimed.items()} if bench else {}
+    # The launches each configuration's event-timed mean covers, right after
+    # its untimed ones.  A kernel+grid group can hold later launches of
+    # another leg (the ceiling's one-tile-per-row scan runs the headline's
+    # kernel on the headline's grid), so only this window is taken.
+    top_steps = int((bench or {}).get("steps", 0))
+    timed = {"scan_u32": top_steps,
+             "sum_f32": sec.get("f32_sum_reduce_2_28", {}).get("steps", 0),
+             "sum_f32_2_20": sec.get("cfg1_f32_sum_2_20", {}).get("steps", 0),
+             "rows_f32": sec.get("cfg3_rows_f32_65536x4096", {}).get("steps", 0),
+             "segmented_i32": sec.get("cfg4_segmented_i32_2_27", {}).get("steps", 0),
+             "scan_f32_2_30": sec.get("cfg5_scan_f32_2_30", {}).get("steps", 0),
+             "copy_u32": top_steps, "blit": top_steps}
     bench_ms = {"scan_u32": (bench or {}).get("ms_per_step"),
                 "sum_f32": sec.get("f32_sum_reduce_2_28", {}).get("ms_per_launch"),
                 "sum_f32_2_20": sec.get("cfg1_f32_sum_2_20", {}).get("ms_per_launch"),
@@ -778,9 +790,10 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
         short = short if len(short) <= 110 else short[:110] + "..."
         lines.append(f"| `{short}` | {grid} | {len(d)} | {statistics.mean(d):.1f} | {statistics.median(d):.1f} | "
                      f"{min(d):.1f} | {max(d):.1f} |")
-    lines += ["", "| configuration | kernels per step | untimed launches skipped | trace: step us (means added) "
-                  "| trace: step us (medians added) | bench: event-timed us per step | trace frac | bench frac |",
-              "|---|---|---:|---:|---:|---:|---:|---:|"]
+    lines += ["", "| configuration | kernels per step | untimed launches skipped | timed launches taken "
+                  "| trace: step us (means added) | trace: step us (medians added) "
+                  "| bench: event-timed us per step | trace frac | bench frac |",
+              "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
     for key, label, kernels, nbytes in TRACE_CONFIGS:
         nbytes = seg_bytes if key == "segmented_i32" else nbytes
         mean_sum = med_sum = 0.0
@@ -791,7 +804,8 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
                 found = False
                 break
             skip = untimed.get(key, 0)
-            d = [x for lst in ds for x in lst[skip:]]
+            take = int(timed.get(key) or 0) if bench else 0
+            d = [x for lst in ds for x in (lst[skip:skip + take] if take else lst[skip:])]
             if not d:
                 found = False
                 break
@@ -802,7 +816,8 @@ def trace_summary(root: Path, bench_json: Path | None) -> int:
         b = bench_ms.get(key)
         tf = f"{nbytes / (mean_sum * 1e-6) / 8e12:.4f}" if nbytes else "-"
         bf = f"{nbytes / (b * 1e-3) / 8e12:.4f}" if (nbytes and b) else "-"
-        lines.append(f"| {label} | {len(kernels)} | {untimed.get(key, 0)} | {mean_sum:.1f} | {med_sum:.1f} | "
+        lines.append(f"| {label} | {len(kernels)} | {untimed.get(key, 0)} | {timed.get(key, 0) if bench else '-'} | "
+                     f"{mean_sum:.1f} | {med_sum:.1f} | "
                      f"{b * 1e3 if b else float('nan'):.1f} | {tf} | {bf} |")
     print("\n".join(lines))
     return 0
