@@ -434,10 +434,15 @@ template <typename Op> struct TileCarry<float, double, Op> {
         lo = __builtin_isfinite(hi) ? (float)(v - (double)hi) : 0.0f;
     }
     __device__ __forceinline__ float apply(float w) const {
-        if constexpr (std::is_same<Op, OpSum>::value)
+        if constexpr (std::is_same<Op, OpSum>::value) {
             return hi + (w + lo);
-        else
-            return __builtin_fmaf(hi, w, lo * w);
+        } else {
+            // lo * w is not finite only where w is infinite or NaN, or the
+            // product overflows; hi * w then gives the f64 form's inf, NaN
+            // or sign (fma(hi, w, -inf) would turn +inf into NaN or -inf).
+            const float lw = lo * w;
+            return __builtin_isfinite(lw) ? __builtin_fmaf(hi, w, lw) : hi * w;
+        }
     }
 };
 
@@ -694,7 +699,14 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         const uint64_t e = e0 + (uint64_t)j * (kWave * 4);
         T r[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) r[c] = tile_carry.apply(Op::combine(wave_excl, x[j][c]));
+        for (int c = 0; c < 4; ++c) {
+            // Opaque to the optimizer: the ragged tile's outputs are not
+            // merged with the whole-tile path's and hoisted above the branch
+            // (which kept every output of the tile live at once).
+            T xv = x[j][c];
+            asm volatile("" : "+v"(xv));
+            r[c] = tile_carry.apply(Op::combine(wave_excl, xv));
+        }
         if constexpr (VEC && !REV) {
             if (e + 3 < p.len) {
                 using V = typename Vec4A4<T>::type;

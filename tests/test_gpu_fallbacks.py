@@ -95,7 +95,7 @@ def _scan(device, x, exclusive, reverse):
 
 
 # 2^21 + 5 u32: 65 tiles of 32768, so both look-back levels (superblocks of
-# 64 tiles) and the ragged last tile run; f32 lines take 49152-element tiles.
+# 64 tiles) and the ragged last tile run; f32 lines take the same tiles.
 @pytest.mark.parametrize("limits", FORCED)
 @pytest.mark.parametrize("exclusive,reverse", [(True, False), (False, True)])
 def test_scans_under_forced_fallbacks(device, oracle, limits, exclusive, reverse):

@@ -558,11 +558,11 @@ def test_scan_f32_tile_and_superblock_edges(device, oracle, n):
     assert bad == 0, worst
 
 
-# f32 lines longer than 32768 elements take 12-wave x 16-step tiles of
-# 49152 elements: lengths either side of one, two and 64 tiles (a
-# superblock), and the mirrored reverse path.
-F32_LONG = [32769, 49151, 49152, 49153, 2 * 49152 - 1, 2 * 49152 + 4, 64 * 49152, 64 * 49152 + 49152 + 12,
-            65 * 49152 + 3]
+# f32 lines longer than 32768 elements take 8-wave x 16-step tiles of 32768
+# elements: lengths either side of one, two and 64 tiles (a superblock), the
+# mirrored reverse path, and lengths of the former 49152-element f32 tiles.
+F32_LONG = [32769, 65535, 65536, 65537, 2 * 32768 + 4, 49152, 49153, 64 * 32768, 64 * 32768 + 32768 + 12,
+            65 * 32768 + 3, 65 * 49152 + 3]
 
 
 @pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
@@ -579,6 +579,69 @@ def test_scan_f32_long_tile_edges(device, oracle, n, direction, kind):
     ref, ab = oracle.scan_sum(x, exclusive=excl, reverse=rev)
     bad, worst = oracle.check_f32_bound(device.download_owned(out), ref, ab, n)
     assert bad == 0, worst
+
+
+# Special values in early tiles reach later tiles through the f64 tile carry
+# (applied as an f32 hi + lo pair): infinities, NaN and, for products, zeros.
+# Lines of five 32768-element tiles and a ragged sixth, one launch for all
+# lines.  Non-finite and zero outputs must match numpy's f64 scan in kind;
+# finite ones stay within the bound (sums) or gamma_{n-1} relative
+# (products).  A carry beyond f32's range gives +-inf, as the reference's
+# f32 accumulation does (crates/hephaestus-core/src/domain/accelerator/
+# scan.rs:90-150), so the values stay far from it.
+SPECIAL_LEN = 5 * 32768 + 77
+
+
+def _special_lines(op):
+    rng = np.random.default_rng(4242 if op == "sum" else 4343)
+    lo, hi = (0.0, 1.0) if op == "sum" else (0.999, 1.001)
+    x = rng.uniform(lo, hi, (6, SPECIAL_LEN)).astype(np.float32)
+    inf, nan = np.float32(np.inf), np.float32(np.nan)
+    x[0, 40000] = inf                           # +inf from tile 1 on
+    x[1, 70000] = nan                           # NaN from tile 2 on
+    x[2, 100] = 0.0 if op == "prod" else inf    # prod: 0, then 0 * inf = NaN; sum: inf, then inf - inf
+    x[2, 100000] = inf if op == "prod" else -inf
+    x[3, 32768] = -inf                          # first element of tile 1
+    x[5, 50000] = 0.0 if op == "prod" else x[5, 50000]  # prod: exact zeros from tile 1 on
+    x[5, SPECIAL_LEN - 1] = nan                 # the ragged last tile
+    return x
+
+
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("op", ["sum", "prod"])
+def test_scan_f32_special_values_across_tiles(device, oracle, op, kind, direction):
+    x = _special_lines(op)
+    rows, cols = x.shape
+    buf = device.upload(x.reshape(-1))
+    out = device.alloc_zeroed(np.float32, rows * cols)
+    lay = Layout.c_contiguous([rows, cols])
+    SCAN.scan_axis_into(device, hx.CumSumOp if op == "sum" else hx.CumProdOp, StridedView(buf, lay), 1,
+                        direction, StridedView(out, lay), kind)
+    got = device.download_owned(out).reshape(rows, cols).astype(np.float64)
+    rev = direction == hx.ScanDirection.Reverse
+    k = 2 * oracle.ceil_log2(cols) * 2.0**-23
+    g = (cols - 1) * 2.0**-24
+    for r in range(rows):
+        v = x[r].astype(np.float64)[::-1] if rev else x[r].astype(np.float64)
+        with np.errstate(invalid="ignore"):
+            want = np.cumsum(v) if op == "sum" else np.cumprod(v)
+            ab = np.cumsum(np.abs(v))
+        if kind == hx.ScanKind.Exclusive:
+            want = np.concatenate([[0.0 if op == "sum" else 1.0], want[:-1]])
+            ab = np.concatenate([[0.0], ab[:-1]])
+        if rev:
+            want, ab = want[::-1], ab[::-1]
+        g_r = got[r]
+        assert np.array_equal(np.isnan(g_r), np.isnan(want)), (r, "NaN pattern")
+        assert np.array_equal(np.isposinf(g_r), np.isposinf(want)), (r, "+inf pattern")
+        assert np.array_equal(np.isneginf(g_r), np.isneginf(want)), (r, "-inf pattern")
+        fin = np.isfinite(want)
+        if op == "sum":
+            assert np.all(np.abs(g_r[fin] - want[fin]) <= k * ab[fin]), r
+        else:
+            assert np.array_equal(g_r[fin] == 0.0, want[fin] == 0.0), (r, "zeros")
+            assert np.all(np.abs(g_r[fin] - want[fin]) <= g / (1.0 - g) * np.abs(want[fin])), r
 
 
 @pytest.mark.parametrize("shape", [(3, 49153), (2, 64 * 49152 + 5)])
