@@ -24,28 +24,30 @@ def _write_trace(path, rows):
 def test_trace_summary_skips_untimed_launches(tmp_path, capsys):
     scan = "void scan_tiles_kernel<unsigned int, OpSum, PackedStatus, true, true, false, 16, true, 8>(ScanParams)"
     grid = 8192 * 512
-    # 2 settle + 1 warm-up launches at 1000 us, then 5 timed at 350 us; the
-    # rows are written out of order to check the sort by start time.
-    durations = [1000.0, 1000.0, 1000.0] + [350.0] * 5
+    # 2 settle + 1 warm-up launches at 1000 us, then 5 timed at 350 us, then
+    # 4 launches of a later leg on the same kernel and grid (the ceiling's
+    # one-tile-per-row scan) at 341 us; the rows are written out of order to
+    # check the sort by start time.
+    durations = [1000.0, 1000.0, 1000.0] + [350.0] * 5 + [341.0] * 4
     rows = [(scan, grid, 1_000_000 * (i + 1), d) for i, d in enumerate(durations)]
     trace_dir = tmp_path / "stats"
     trace_dir.mkdir()
     _write_trace(trace_dir / "x_kernel_trace.csv", list(reversed(rows)))
     bj = tmp_path / "bench.json"
-    bj.write_text(json.dumps({"warmup": 1, "ms_per_step": 0.35,
+    bj.write_text(json.dumps({"warmup": 1, "steps": 5, "ms_per_step": 0.35,
                               "timing": {"settle_launches": 2}, "secondary": {}, "ceiling": {}}))
     assert bench.trace_summary(trace_dir, bj) == 0
     out = capsys.readouterr().out
     line = next(ln for ln in out.splitlines() if ln.startswith("| u32 exclusive scan 2^28"))
     cells = [c.strip() for c in line.strip("|").split("|")]
-    # label, kernels, skipped, mean sum, median sum, bench us, trace frac, bench frac
-    assert cells[2] == "3"
-    assert cells[3] == "350.0" and cells[4] == "350.0"
-    assert cells[5] == "350.0"
-    assert abs(float(cells[6]) - (8 << 28) / 350e-6 / 8e12) < 1e-4
+    # label, kernels, skipped, taken, mean sum, median sum, bench us, trace frac, bench frac
+    assert cells[2] == "3" and cells[3] == "5"
+    assert cells[4] == "350.0" and cells[5] == "350.0"
+    assert cells[6] == "350.0"
+    assert abs(float(cells[7]) - (8 << 28) / 350e-6 / 8e12) < 1e-4
     # The per-kernel table still lists every dispatch.
     kline = next(ln for ln in out.splitlines() if ln.startswith("| `void scan_tiles_kernel"))
-    assert f"| {grid} | 8 |" in kline
+    assert f"| {grid} | 12 |" in kline
 
 
 def test_trace_summary_without_bench_json_keeps_every_launch(tmp_path, capsys):
@@ -58,7 +60,7 @@ def test_trace_summary_without_bench_json_keeps_every_launch(tmp_path, capsys):
     out = capsys.readouterr().out
     line = next(ln for ln in out.splitlines() if ln.startswith("| u32 exclusive scan 2^28"))
     cells = [c.strip() for c in line.strip("|").split("|")]
-    assert cells[2] == "0" and cells[3] == "200.0"
+    assert cells[2] == "0" and cells[3] == "-" and cells[4] == "200.0"
 
 
 class _FakeEvent:
