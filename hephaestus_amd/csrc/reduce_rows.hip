@@ -29,6 +29,7 @@
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace hx {
@@ -64,6 +65,7 @@ struct RowParams {
     void *out_prod;
     int64_t out_stride;
     uint64_t out_offset;
+    uint64_t row0 = 0; // rows_kernel: row of block 0's first group (launched in batches)
 };
 
 template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
@@ -379,7 +381,7 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     const int gl = t % G;
     uint32_t rl = (uint32_t)(t / G);
     if constexpr (G >= kWave) rl = (uint32_t)__builtin_amdgcn_readfirstlane(rl);
-    const uint64_t r = (uint64_t)xcd_contiguous(blockIdx.x, gridDim.x) * kRowsPerBlock + rl;
+    const uint64_t r = p.row0 + (uint64_t)xcd_contiguous(blockIdx.x, gridDim.x) * kRowsPerBlock + rl;
     Stats<T, FLAGS> st;
     if (r < p.rows) {
         const T *row = (const T *)p.base + ((int64_t)p.offset + (int64_t)r * p.row_stride);
@@ -803,24 +805,32 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
                                stream, p, partials, s.chunk, s.nchunks);
         HX_TRY(check_launch("rows_split_kernel"));
     } else {
-        const uint64_t blocks = ceil_div(p.rows, (uint64_t)(kBlock / s.G));
-        if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "row reduction exceeds the grid range");
-        const dim3 grid((uint32_t)blocks), block(kBlock);
-        if (!s.vec)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false, kWave>), grid, block, 0, stream, p);
-        else if (s.G == 256)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 256>), grid, block, 0, stream, p);
-        else if (s.G == 128)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 128>), grid, block, 0, stream, p);
-        else if (s.G == 64)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 64>), grid, block, 0, stream, p);
-        else if (s.G == 16)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 16>), grid, block, 0, stream, p);
-        else if (s.G == 4)
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 4>), grid, block, 0, stream, p);
-        else
-            hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 1>), grid, block, 0, stream, p);
-        return check_launch("rows_kernel");
+        // A launch's work-items must stay below 2^32: 2^26 rows of 64 lanes
+        // (strided rows) or 2^30 of 4 take several launches of whole blocks.
+        const uint64_t rows_per_block = kBlock / s.G;
+        const uint64_t max_blocks = 0xFFFFFFFFull / kBlock;
+        const uint64_t blocks = ceil_div(p.rows, rows_per_block);
+        RowParams q = p;
+        for (uint64_t b0 = 0; b0 < blocks; b0 += max_blocks) {
+            q.row0 = b0 * rows_per_block;
+            const dim3 grid((uint32_t)std::min<uint64_t>(max_blocks, blocks - b0)), block(kBlock);
+            if (!s.vec)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, false, kWave>), grid, block, 0, stream, q);
+            else if (s.G == 256)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 256>), grid, block, 0, stream, q);
+            else if (s.G == 128)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 128>), grid, block, 0, stream, q);
+            else if (s.G == 64)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 64>), grid, block, 0, stream, q);
+            else if (s.G == 16)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 16>), grid, block, 0, stream, q);
+            else if (s.G == 4)
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 4>), grid, block, 0, stream, q);
+            else
+                hipLaunchKernelGGL((rows_kernel<T, AFFINE, FLAGS, true, 1>), grid, block, 0, stream, q);
+            HX_TRY(check_launch("rows_kernel"));
+        }
+        return HX_OK;
     }
     if (!split) return HX_OK;
     hipLaunchKernelGGL((split_fold_kernel<T, FLAGS>), dim3((uint32_t)ceil_div(p.rows, kWave)),

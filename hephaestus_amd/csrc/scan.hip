@@ -44,6 +44,7 @@
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace hx {
@@ -184,6 +185,7 @@ struct ScanParams {
     uint64_t in_offset, out_offset;
     uint32_t tag;        // this launch's status tag
     uint32_t spin_limit; // polls before a waiter computes a missing value (64)
+    uint64_t tile0;      // tile of block 0 (tile kernels launched in batches)
 };
 
 // The four elements of one lane and step (logical index e..e+3 of the
@@ -540,7 +542,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     const bool looks_back = p.tiles_per_line > 1;
     if (looks_back) __builtin_amdgcn_s_setprio(3);
 
-    const uint64_t tile = blockIdx.x;
+    const uint64_t tile = p.tile0 + blockIdx.x;
     const uint64_t line = tile / p.tiles_per_line;
     const uint64_t tin = tile - line * p.tiles_per_line;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -633,7 +635,9 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         const C agg = (C)tile_agg;
         C excl = Op::template identity<C>();
         if (tin == 0) {
-            if (lane == 0) st.publish_tile(tile, p.tag, kPrefix, agg);
+            // A line of one tile has no successor to read it (its status
+            // area is not even allocated: scan_bytes).
+            if (lane == 0 && looks_back) st.publish_tile(tile, p.tag, kPrefix, agg);
         } else {
             if (lane == 0) st.publish_tile(tile, p.tag, kAggregate, agg);
             KnownAgg<C> hook{agg};
@@ -1723,23 +1727,34 @@ inline TileShape tile_shape(uint64_t len) {
     return TileShape{kLongWaves, kLongSteps};
 }
 
+// A launch's work-items (blocks x block size) must stay below 2^32, so many
+// short lines (2^26 lines of at most 512 elements, 2^24 of at most 8192)
+// take several launches of consecutive tiles, in order.  A later batch's
+// look-back reads an earlier batch's statuses, published under the same tag
+// before that launch ended; lines of one tile publish none.
 template <typename T, typename Op, typename Status, bool EXCL, int STEPS, int WAVES>
-hx_status launch_tiles_shaped(const ScanParams &p, const Status &st, const Status &st1, bool vec, bool rev,
+hx_status launch_tiles_shaped(ScanParams p, const Status &st, const Status &st1, bool vec, bool rev,
                               hipStream_t stream) {
-    const dim3 grid((uint32_t)p.total_tiles), block(WAVES * kWave);
-    if (vec && rev)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true, STEPS, true, WAVES>), grid, block, 0,
-                           stream, p, st, st1);
-    else if (vec)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false, STEPS, true, WAVES>), grid, block, 0,
-                           stream, p, st, st1);
-    else if (rev)
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true, STEPS, true, WAVES>), grid, block, 0,
-                           stream, p, st, st1);
-    else
-        hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false, STEPS, true, WAVES>), grid, block, 0,
-                           stream, p, st, st1);
-    return check_launch("scan_tiles_kernel");
+    const uint64_t max_blocks = std::min<uint64_t>(0x7FFFFFFFull, 0xFFFFFFFFull / (WAVES * kWave));
+    const uint64_t total = p.total_tiles;
+    for (uint64_t t0 = 0; t0 < total; t0 += max_blocks) {
+        p.tile0 = t0;
+        const dim3 grid((uint32_t)std::min<uint64_t>(max_blocks, total - t0)), block(WAVES * kWave);
+        if (vec && rev)
+            hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true, STEPS, true, WAVES>), grid, block,
+                               0, stream, p, st, st1);
+        else if (vec)
+            hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false, STEPS, true, WAVES>), grid, block,
+                               0, stream, p, st, st1);
+        else if (rev)
+            hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, true, STEPS, true, WAVES>), grid, block,
+                               0, stream, p, st, st1);
+        else
+            hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, false, false, STEPS, true, WAVES>), grid, block,
+                               0, stream, p, st, st1);
+        HX_TRY(check_launch("scan_tiles_kernel"));
+    }
+    return HX_OK;
 }
 
 template <typename T, typename Op, typename Status, bool EXCL>
@@ -1817,6 +1832,8 @@ uint64_t scan_bytes(const ScanArgs &a) {
     }
     if (column_mode(a)) return column_bytes(a);
     const uint64_t tpl = ceil_div(a.len, tile_shape(a.len).elems());
+    // Lines of one tile never look back and publish no status.
+    if (tpl <= 1) return kLookbackOffset;
     return kLookbackOffset + status_bytes(tpl * a.lines) + status_bytes(ceil_div(tpl, kSuper) * a.lines);
 }
 
@@ -1861,9 +1878,6 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
         return a.exclusive ? launch_column<T, Op, true>(p, cs, a.reverse, ws, stream)
                            : launch_column<T, Op, false>(p, cs, a.reverse, ws, stream);
     }
-    if (p.total_tiles > 0x7FFFFFFFull)
-        return fail(HX_ERR_DISPATCH_FAILED, "scan of %llu tiles exceeds the grid range",
-                    (unsigned long long)p.total_tiles);
     if (ws_bytes < scan_bytes(a))
         return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));

@@ -204,3 +204,54 @@ def test_narrow_column_scan_with_many_tiles(device, kind, reverse):
         assert np.array_equal(got, want.astype(np.uint32)), r
     x.free()
     out.free()
+
+
+def test_row_scans_of_2_26_lines(device):
+    """[2^26 + 5, 4] u32 scanned along axis 1: every line is one 64-lane
+    tile, so one launch would need 2^32 + 320 work-items, past the 32-bit
+    grid size; the tiles go out in several launches.  Lines of one tile
+    never look back and publish no status, so the plan's workspace is the
+    256-byte header alone (not a status line per tile).  Every element is 1
+    except planted x[r][2] = 7, so out[r] = (1, 2, 9, 10) there and
+    (1, 2, 3, 4) elsewhere."""
+    R, C = (1 << 26) + 5, 4
+    x = device.alloc_uninitialized(np.uint32, R * C)
+    device.fill_uniform_int(x, seed=11, lo=1, hi=1)
+    planted = [0, (1 << 26) - 1, 1 << 26, R - 1]
+    for r in planted:
+        device.write_sub_buffer(x, r * C + 2, np.array([7], np.uint32))
+    out = device.alloc_zeroed(np.uint32, R * C)
+    lay = Layout.c_contiguous([R, C])
+    plan = SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(x, lay), 1, hx.ScanDirection.Forward,
+                                  StridedView(out, lay), hx.ScanKind.Inclusive)
+    assert plan.workspace_bytes() <= 256
+    plan.dispatch()
+    for r in (0, 1, (1 << 26) - 2, (1 << 26) - 1, 1 << 26, (1 << 26) + 1, R - 1):
+        want = [1, 2, 9, 10] if r in planted else [1, 2, 3, 4]
+        assert _slice(device, out, r * C, C).tolist() == want, r
+    plan.destroy()
+    x.free()
+    out.free()
+
+
+def test_strided_row_sums_of_2_26_rows(device):
+    """Sums along axis 1 of the [2^26 + 3, 2] view with strides (4, 2) of a
+    u32 buffer: neither stride is 1, so each row gets a 64-lane group and
+    one launch would need 2^32 + 192 work-items; the rows go out in several
+    launches.  Every element is 1 except planted x[4 r + 2] = 9 (the second
+    element of row r), so out[r] = 10 there and 2 elsewhere."""
+    R = (1 << 26) + 3
+    x = device.alloc_uninitialized(np.uint32, 4 * R)
+    device.fill_uniform_int(x, seed=12, lo=1, hi=1)
+    planted = [0, (1 << 26) - 1, 1 << 26, R - 1]
+    for r in planted:
+        device.write_sub_buffer(x, 4 * r + 2, np.array([9], np.uint32))
+    out = device.alloc_zeroed(np.uint32, R)
+    view = StridedView(x, Layout.try_new([R, 2], [4, 2], 0))
+    hx.RocmAxisReductionOps().reduce_axis_into(device, hx.SumOp, view, 1,
+                                               StridedView(out, Layout.c_contiguous([R, 1])))
+    for start in (0, (1 << 26) - 2, R - 4):
+        want = [10 if start + i in planted else 2 for i in range(4)]
+        assert _slice(device, out, start, 4).tolist() == want, start
+    x.free()
+    out.free()
