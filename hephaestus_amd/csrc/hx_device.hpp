@@ -218,6 +218,7 @@ template <> __device__ __forceinline__ uint32_t wave_reduce<OpSum, uint32_t>(uin
 template <> __device__ __forceinline__ float wave_reduce<OpSum, float>(float v) { return wave_sum(v); }
 template <> __device__ __forceinline__ double wave_reduce<OpProd, double>(double v) { return wave_prod(v); }
 template <> __device__ __forceinline__ uint32_t wave_reduce<OpProd, uint32_t>(uint32_t v) { return wave_prod(v); }
+template <> __device__ __forceinline__ float wave_reduce<OpProd, float>(float v) { return wave_prod(v); }
 
 // ------------------------------------------------------- DPP lane moves
 // GFX9 data-parallel-primitive controls.  A DPP move reads another lane's

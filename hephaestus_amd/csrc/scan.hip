@@ -732,6 +732,246 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     }
 }
 
+// Short dense lines: a scan along lines of fewer than 256 elements packed
+// back to back (line stride = length, element stride 1, input and output).
+// One tile per line (scan_tiles_kernel) left most of a block idle and made
+// the launch block-bound: [2^24, 4] u32 along axis 1 took 4.0 ms.  Here the
+// operand is one flat range of lines x len elements, cut into tiles of
+// WAVES x 64 x 4 x STEPS elements in logical order (a reverse scan mirrors
+// the range), loaded and stored as 16-byte vectors exactly like a 1-D scan,
+// and scanned with a segmented scan that restarts at every line start
+// (logical index k with k % len == 0):
+//
+//   * per lane, the four elements' running values restart at a line start;
+//   * across the wave, (flag, value) pairs -- flag: a line starts in the
+//     span -- take a six-step DPP scan under the segmented combine
+//     (f1, v1) . (f2, v2) = (f1 | f2, f2 ? v2 : v1 + v2), which is
+//     associative; across steps a register carry, across waves LDS;
+//   * the line open at the tile start takes the fold of its elements in the
+//     previous tile (at most len - 1 < 255 of them), which wave 0 re-reads,
+//     so no tile waits for another: no look-back and no status words.
+//
+// Line starts are tracked with an incremental remainder, no division per
+// element.  f32 lines scan in f32 (a line holds fewer than 256 elements).
+// Tiles of 8 waves x 16 steps with gaps between stores (as the paced
+// integer tiles): 2^28 u32 along lines of 4 / 100 / 255 elements, 357.9 /
+// 355.5 / 365.6 us without gaps, 354.9 / 357.2 / 358.9 with; 8 steps
+// 406.7 / 417.0 / 419.6 (one tile per line took 16 ms at 4 elements).  f32
+// lines at 16 steps spill a few registers under the 128-VGPR cap and still
+// beat 12 steps, which fit (355.3 / 359.1 / 362.6 against 368.9 / 366.8 /
+// 368.4 us) and 8 steps (395.7 / 404.4 / 410.5).
+struct ShortParams {
+    const void *in;
+    void *out;
+    uint64_t n;      // lines * len
+    uint64_t in_offset, out_offset;
+    uint64_t tile0;  // tile of block 0 (launched in batches)
+    uint32_t len;    // elements per line, 1..255
+};
+
+// The segmented combine on (flag, value) pairs.
+template <typename Op, typename T>
+__device__ __forceinline__ void seg_combine(uint32_t fa, T va, uint32_t &fb, T &vb) {
+    vb = fb ? vb : Op::combine(va, vb);
+    fb |= fa;
+}
+
+// Inclusive segmented scan across the 64 lanes (Hillis-Steele on DPP moves,
+// as wave_inclusive_scan; lanes with no source take (0, identity)).
+template <typename Op, typename T> __device__ __forceinline__ void wave_seg_scan(uint32_t &f, T &v) {
+    const T id = Op::template identity<T>();
+#define HX_SEG_STEP(CTRL, MASK)                                                                                      \
+    {                                                                                                                \
+        const T vs = dpp_move<CTRL, MASK>(id, v);                                                                    \
+        const uint32_t fs = dpp_move<CTRL, MASK>(0u, f);                                                             \
+        seg_combine<Op, T>(fs, vs, f, v);                                                                            \
+    }
+    HX_SEG_STEP(kDppRowShr1, 0xf)
+    HX_SEG_STEP(kDppRowShr2, 0xf)
+    HX_SEG_STEP(kDppRowShr4, 0xf)
+    HX_SEG_STEP(kDppRowShr8, 0xf)
+    HX_SEG_STEP(kDppRowBcast15, 0xa)
+    HX_SEG_STEP(kDppRowBcast31, 0xc)
+#undef HX_SEG_STEP
+}
+
+template <typename T, typename Op, bool EXCL, bool REV, int STEPS, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(4)))
+void scan_short_lines_kernel(ShortParams p) {
+    constexpr uint32_t kWaveElems = kWave * 4 * STEPS;
+    constexpr uint32_t kTileElems = WAVES * kWaveElems;
+    __shared__ uint32_t s_wf[WAVES];
+    __shared__ T s_wv[WAVES];
+    __shared__ T s_carry;
+
+    const T ident = Op::template identity<T>();
+    const uint64_t tile = p.tile0 + blockIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = lane_id();
+    const uint32_t L = p.len;
+    const T *in = (const T *)p.in + p.in_offset;
+    T *out = (T *)p.out + p.out_offset;
+    const uint64_t k0 = tile * kTileElems;                                // tile's first logical element
+    const uint64_t wbase = k0 + (uint64_t)w * kWaveElems;
+    const bool full = k0 + kTileElems <= p.n;
+    // Logical element k lives at in[k] (forward) or in[n - 1 - k] (reverse).
+    const uint32_t lane_off = ((uint32_t)w * kWaveElems + (uint32_t)lane * 4) * (uint32_t)sizeof(T);
+
+    T x[STEPS][4];
+    if (full) {
+        using V = typename Vec4A4<T>::type;
+        if constexpr (REV) {
+            const char *base = (const char *)(in + (p.n - k0 - kTileElems));
+            const uint32_t rev = (kTileElems - 4) * (uint32_t)sizeof(T) - lane_off;
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                const V q = load_a4<true>((const V *)(base + rev - (uint32_t)j * (kWave * 16)));
+                x[j][0] = (T)q.w;
+                x[j][1] = (T)q.z;
+                x[j][2] = (T)q.y;
+                x[j][3] = (T)q.x;
+            }
+        } else {
+            const char *base = (const char *)(in + k0);
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+                const V q = load_a4<true>((const V *)(base + lane_off + (uint32_t)j * (kWave * 16)));
+                x[j][0] = (T)q.x;
+                x[j][1] = (T)q.y;
+                x[j][2] = (T)q.z;
+                x[j][3] = (T)q.w;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint64_t k = wbase + (uint64_t)j * (kWave * 4) + (uint64_t)lane * 4 + c;
+                x[j][c] = k < p.n ? in[REV ? p.n - 1 - k : k] : ident;
+            }
+    }
+
+    // The line open at the tile start: the fold of its elements before k0.
+    const uint32_t m = (uint32_t)(k0 % L);
+    if (w == 0) {
+        T a = ident;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t i = (uint32_t)lane + 64u * q;
+            if (i < m) {
+                const uint64_t k = k0 - m + i;
+                a = Op::combine(a, in[REV ? p.n - 1 - k : k]);
+            }
+        }
+        a = wave_reduce<Op, T>(a);
+        if (lane == 0) s_carry = a;
+    }
+
+    // Remainder of this lane's first element modulo L, then per step.
+    const uint32_t wrem = (uint32_t)(wbase % L);
+    uint32_t r = (wrem + (uint32_t)lane * 4u) % L;
+    const uint32_t step_inc = (kWave * 4u) % L;
+    uint32_t fs = 0u; // step carry: (flag, value)
+    T vs = ident;
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+        // flags of the four elements: remainder 0 marks a line start
+        uint32_t rc = r, f[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            f[c] = rc == 0u;
+            rc += 1u;
+            rc = rc >= L ? rc - L : rc;
+        }
+        T pl[4];
+        pl[0] = x[j][0];
+#pragma unroll
+        for (int c = 1; c < 4; ++c) pl[c] = f[c] ? x[j][c] : Op::combine(pl[c - 1], x[j][c]);
+        uint32_t fl = f[0] | f[1] | f[2] | f[3];
+        T vl = pl[3];
+        wave_seg_scan<Op, T>(fl, vl); // lane inclusive over the wave's step
+        // lane exclusive: the previous lane's inclusive value
+        uint32_t fe = dpp_move<kDppWaveShr1>(0u, fl);
+        T ve = dpp_move<kDppWaveShr1>(ident, vl);
+        // this lane's incoming value within the wave: step carry, then lanes before
+        const T vin = fe ? ve : Op::combine(vs, ve);
+        uint32_t seen = 0u; // a line start at or before element c in this lane
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            seen |= f[c];
+            x[j][c] = seen ? pl[c] : Op::combine(vin, pl[c]);
+        }
+        if constexpr (EXCL) {
+            // exclusive: identity at a line start, else the inclusive value
+            // of the element before (the lane's incoming value for c = 0)
+#pragma unroll
+            for (int c = 3; c >= 1; --c) x[j][c] = f[c] ? ident : x[j][c - 1];
+            x[j][0] = f[0] ? ident : vin;
+        }
+        // carry to the next step: the wave's inclusive (flag, value) at lane 63
+        const uint32_t f63 = read_lane(fl, kWave - 1);
+        const T v63 = read_lane(vl, kWave - 1);
+        vs = f63 ? v63 : Op::combine(vs, v63);
+        fs |= f63;
+        r += step_inc;
+        r = r >= L ? r - L : r;
+        // One step at a time: interleaving steps' scans (the scheduler's
+        // choice) spilled the f32 forms at 16 steps.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (lane == 0) {
+        s_wf[w] = fs;
+        s_wv[w] = vs;
+    }
+    __syncthreads();
+    // This wave's incoming value: the open line's carry, then waves before.
+    T win = s_carry;
+    for (int q = 0; q < w; ++q) win = s_wf[q] ? s_wv[q] : Op::combine(win, s_wv[q]);
+    // Elements before the wave's first line start take win.
+    const uint64_t first_start = wbase + (uint64_t)((L - wrem) % L);
+
+    if (full) {
+        using V = typename Vec4A4<T>::type;
+        const auto orsrc = stream_rsrc(REV ? (void *)(out + (p.n - k0 - kTileElems)) : (void *)(out + k0),
+                                       kTileElems * (uint32_t)sizeof(T));
+        const uint32_t rev = (kTileElems - 4) * (uint32_t)sizeof(T) - lane_off;
+#pragma unroll
+        for (int j = 0; j < STEPS; ++j) {
+            const uint64_t k = wbase + (uint64_t)j * (kWave * 4) + (uint64_t)lane * 4;
+            T y[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[c] = k + c >= first_start ? x[j][c] : Op::combine(win, x[j][c]);
+            V v;
+            if constexpr (REV) {
+                v.w = y[0];
+                v.z = y[1];
+                v.y = y[2];
+                v.x = y[3];
+                stream_store(v, orsrc, rev - (uint32_t)j * (kWave * 16));
+            } else {
+                v.x = y[0];
+                v.y = y[1];
+                v.z = y[2];
+                v.w = y[3];
+                stream_store(v, orsrc, lane_off + (uint32_t)j * (kWave * 16));
+            }
+            store_gap();
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint64_t k = wbase + (uint64_t)j * (kWave * 4) + (uint64_t)lane * 4 + c;
+            T xv = x[j][c];
+            asm volatile("" : "+v"(xv)); // not merged with the whole-tile stores (see scan_tiles_kernel)
+            if (k < p.n) out[REV ? p.n - 1 - k : k] = k >= first_start ? xv : Op::combine(win, xv);
+        }
+}
+
 // Column scans: many strided lines whose starts are adjacent in memory
 // (axis-0 scan of a row-major matrix).  From 256 lines up they take the
 // single-pass col_lookback_kernel below; narrower matrices take this chunked
@@ -1774,6 +2014,44 @@ hx_status launch_tiles(const ScanParams &p, const Status &st, const Status &st1,
     return launch_tiles_shaped<T, Op, Status, EXCL, kSteps, kWaves>(p, st, st1, vec, rev, stream);
 }
 
+// Short dense lines (scan_short_lines_kernel): fewer than 256 elements per
+// line, lines packed back to back in input and output.
+constexpr uint64_t kShortLineMax = 256;
+constexpr int kShortWaves = 8, kShortSteps = 16;
+bool short_line_scan(const ScanArgs &a) {
+    return a.len >= 1 && a.len < kShortLineMax && a.lines >= 2 && a.in_elem_stride == 1 &&
+           a.out_elem_stride == 1 && a.in_line_stride == (int64_t)a.len && a.out_line_stride == (int64_t)a.len;
+}
+
+template <typename T, typename Op, bool EXCL, bool REV>
+hx_status launch_short_dir(ShortParams p, hipStream_t stream) {
+    constexpr uint64_t kTile = (uint64_t)kShortWaves * kWave * 4 * kShortSteps;
+    const uint64_t tiles = ceil_div(p.n, kTile);
+    const uint64_t max_blocks = std::min<uint64_t>(0x7FFFFFFFull, 0xFFFFFFFFull / (kShortWaves * kWave));
+    for (uint64_t t0 = 0; t0 < tiles; t0 += max_blocks) {
+        p.tile0 = t0;
+        hipLaunchKernelGGL((scan_short_lines_kernel<T, Op, EXCL, REV, kShortSteps, kShortWaves>),
+                           dim3((uint32_t)std::min<uint64_t>(max_blocks, tiles - t0)), dim3(kShortWaves * kWave), 0,
+                           stream, p);
+        HX_TRY(check_launch("scan_short_lines_kernel"));
+    }
+    return HX_OK;
+}
+
+template <typename T, typename Op>
+hx_status launch_short(const ScanArgs &a, hipStream_t stream) {
+    ShortParams p{};
+    p.in = a.in;
+    p.out = a.out;
+    p.n = a.lines * a.len;
+    p.in_offset = a.in_offset;
+    p.out_offset = a.out_offset;
+    p.len = (uint32_t)a.len;
+    if (a.exclusive)
+        return a.reverse ? launch_short_dir<T, Op, true, true>(p, stream) : launch_short_dir<T, Op, true, false>(p, stream);
+    return a.reverse ? launch_short_dir<T, Op, false, true>(p, stream) : launch_short_dir<T, Op, false, false>(p, stream);
+}
+
 // Narrow column scans (col_narrow_*): see the kernels' comment.
 bool narrow_column_scan(const ScanArgs &a) {
     const uint64_t c = a.lines;
@@ -1825,6 +2103,7 @@ hx_status launch_narrow(const ScanArgs &a, const ScanParams &p, void *ws, uint64
 }
 
 uint64_t scan_bytes(const ScanArgs &a) {
+    if (short_line_scan(a)) return 0;
     if (narrow_column_scan(a)) return narrow_bytes(a);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape c = col_lb_shape(a);
@@ -1857,6 +2136,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     p.spin_limit = lookback_poll_limit();
     if (a.lines == 0 || a.len == 0) return HX_OK;
 
+    if (short_line_scan(a)) return launch_short<T, Op>(a, stream);
     if (narrow_column_scan(a)) return launch_narrow<T, Op>(a, p, ws, ws_bytes, stream);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape cs = col_lb_shape(a);
@@ -1909,7 +2189,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
 bool scan_uses_lookback(const ScanArgs &a) {
-    if (narrow_column_scan(a)) return false;
+    if (short_line_scan(a) || narrow_column_scan(a)) return false;
     return !column_mode(a) || column_single_pass(a);
 }
 
