@@ -50,14 +50,15 @@ sys.path.insert(0, str(REPO))
 PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30",
              "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
-             "colscan_narrow_u32", "segmented_long_i32")
+             "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colsum_period_f32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "sum_f32_2_20": "full_reduce_kernel<",
              "rows_f32": "rows_kernel", "segmented_i32": "segmented_sum_kernel",
              "segmented_short_i32": "seg_short_kernel", "scan_f32_2_30": "scan_tiles_kernel",
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
              "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel",
-             "colscan_narrow_u32": "col_narrow_scan_kernel", "segmented_long_i32": "segmented_sum_kernel"}
+             "colscan_narrow_u32": "col_narrow_scan_kernel", "segmented_long_i32": "segmented_sum_kernel",
+             "colscan_rowtile_u32": "col_rowtile_scan_kernel", "colsum_period_f32": "cols_period_kernel"}
 
 
 def log(msg: str) -> None:
@@ -597,6 +598,48 @@ def bench_colscan_narrow_u32(hx, dev, args):
     return {"n": n, "ms": statistics.mean(per.values()), "bytes": 8 * n}
 
 
+def bench_colscan_rowtile_u32(hx, dev, args):
+    """Axis-0 inclusive scans of 2^28-element row-major u32 matrices with 3,
+    12, 100 and 255 columns (the row-tile form); "ms" is their mean."""
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.uint32, n)
+    dev.fill_uniform_int(x, seed=3, lo=0, hi=255)
+    out = dev.alloc_uninitialized(np.uint32, n)
+    per, nbytes = {}, []
+    for c in (3, 12, 100, 255):
+        m = (n // c) * c
+        lay = Layout.c_contiguous([n // c, c])
+        plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0,
+                                                  hx.ScanDirection.Forward, StridedView(out, lay))
+        per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+        nbytes.append(8 * m)
+        log(f"colscan_rowtile_u32: {c} columns {per[c]:.4f} ms/launch")
+    return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
+
+
+def bench_colsum_period_f32(hx, dev, args):
+    """Axis-0 sums of 2^28-element row-major f32 matrices with 3, 5, 12 and
+    24 columns (the period form); "ms" is their mean."""
+    from hephaestus_amd import Layout, StridedView
+
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(x, seed=6, lo=-1.0, hi=1.0)
+    out = dev.alloc_uninitialized(np.float32, 32)
+    per, nbytes = {}, []
+    for c in (3, 5, 12, 24):
+        m = (n // c) * c
+        plan = hx.RocmAxisReductionOps().prepare_reduce_axis_into(
+            dev, hx.SumOp, StridedView(x, Layout.c_contiguous([n // c, c])), 0,
+            StridedView(out, Layout.c_contiguous([1, c])))
+        per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+        nbytes.append(4 * m + 4 * c)
+        log(f"colsum_period_f32: {c} columns {per[c]:.4f} ms/launch")
+    return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
+
+
 def bench_segmented_long_i32(hx, dev, args):
     """Segmented sums of 2^27 i32 values with geometric segment lengths of
     mean 3000, 10^5, 10^6 and 10^7 (long segments: tiles without a segment
@@ -1067,7 +1110,7 @@ def main() -> int:
     if args.workload == "all":
         extra = {}
         for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
-                     "colscan_narrow_u32", "segmented_long_i32"):
+                     "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colsum_period_f32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             g = gbs(r["bytes"], r["ms"])
             extra[name] = {"value": round(g, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

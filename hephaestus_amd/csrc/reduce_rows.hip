@@ -24,6 +24,11 @@
 //                      256 adjacent outputs (one 16-byte load per lane per
 //                      line) and a chunk of the axis, so the chip gets
 //                      thousands of waves however tall the matrix is.
+//   cols_block_kernel  small column reductions in one launch (slices of the
+//                      axis folded through LDS).
+//   cols_narrow_kernel / cols_period_kernel
+//                      axis 0 of dense matrices with fewer than 96 columns,
+//                      read as one contiguous range of 1 KiB wave loads.
 //   split_fold_kernel  folds the chunk partials of either split form in a
 //                      fixed order, so f32 sums do not depend on scheduling.
 #include "hx_device.hpp"
@@ -582,6 +587,99 @@ __global__ __launch_bounds__(kBlock) void cols_narrow_kernel(RowParams p, uint64
     }
 }
 
+// Statistic planes a flag set keeps (sum or mean, product, max or argmax, min).
+template <int FLAGS> constexpr int kPlanes = ((FLAGS & (F_SUM | F_MEAN)) != 0) + ((FLAGS & F_PROD) != 0) +
+                                             ((FLAGS & (F_ARG | F_MAX)) != 0) + ((FLAGS & F_MIN) != 0);
+
+// Narrow column reductions for other C below 96: axis 0 of a dense
+// row-major [R, C] matrix.  The matrix is one contiguous range of 1 KiB
+// blocks (256 elements); component k of lane l's vector in block b holds
+// element 256 b + 4 l + k, in column (256 b + 4 l + k) mod C.  Blocks b and
+// b + P, P = C / gcd(C, 256), give every lane-component the same column, so
+// wave w takes the blocks rho + P m of one residue rho = w mod P for m in
+// its chunk (w / P): each lane keeps four statistics and every load is a
+// coalesced 1 KiB wave access, as in cols_narrow_kernel.  Lane-components
+// that share a column fold through the wave's LDS in ascending lane-component
+// order, and lane c (c + 64, ...) stores column c's statistics to plane w,
+// which split_fold_kernel folds in wave order, so f32 sums depend only on
+// the shape (a single wave writes the outputs).  Column tiles gave such matrices C live lanes per wave
+// (2^28 f32 with C = 3: 2.9 ms against 0.19 ms at C = 4).
+template <typename T, int FLAGS>
+__global__ __launch_bounds__(kBlock) void cols_period_kernel(RowParams p, uint64_t *partials, uint32_t period,
+                                                             uint64_t chunk, uint32_t nwaves) {
+    using V = typename Vec4A4<T>::type;
+    constexpr int kBlockWaves = kBlock / kWave;
+    __shared__ uint64_t sh[kBlockWaves][kPlanes<FLAGS> * 4 * kWave];
+    const int lane = lane_id();
+    const int wv = threadIdx.x / kWave;
+    const uint64_t w = (uint64_t)blockIdx.x * kBlockWaves + wv;
+    const bool live = w < nwaves; // uniform across the wave
+    const uint32_t C = (uint32_t)p.rows;
+    const uint64_t n = p.cols * C;
+    const uint64_t nblk = (n + 4 * kWave - 1) / (4 * kWave);
+    const uint64_t full_blk = n / (4 * kWave); // blocks whose 256 elements all exist
+    const uint32_t rho = (uint32_t)(w % period);
+    const uint64_t mcount = nblk > rho ? (nblk - rho + period - 1) / period : 0;
+    const uint64_t m0 = w / period * chunk;
+    const uint64_t m1 = live ? (m0 + chunk < mcount ? m0 + chunk : mcount) : m0;
+    // Column of lane 0's component 0, the same in every block of the
+    // residue, and the rows of this lane's four components in block
+    // rho + P m0, which advance by 256 P / C = rstep per block of the residue.
+    const uint32_t col0 = (uint32_t)(((uint64_t)rho * (4 * kWave)) % C);
+    const uint32_t rstep = (uint32_t)((uint64_t)period * (4 * kWave) / C);
+    uint32_t row[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) row[k] = (uint32_t)(((rho + (uint64_t)period * m0) * (4 * kWave) + 4 * lane + k) / C);
+    const V *src = (const V *)((const T *)p.base + p.offset);
+    Stats<T, FLAGS> st[4];
+    auto visit4 = [&](const V &x, uint32_t dr) {
+        st[0].visit((T)x.x, row[0] + dr);
+        st[1].visit((T)x.y, row[1] + dr);
+        st[2].visit((T)x.z, row[2] + dr);
+        st[3].visit((T)x.w, row[3] + dr);
+    };
+    // Trips of four whole blocks, then the rest one block at a time with
+    // per-element bounds (the range's last block may be partial).
+    uint64_t m = m0;
+    for (; m + 4 <= m1 && rho + (uint64_t)period * (m + 3) < full_blk; m += 4) {
+        V x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            x[u] = __builtin_nontemporal_load(&src[(rho + (uint64_t)period * (m + u)) * kWave + lane]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) visit4(x[u], u * rstep);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) row[k] += 4 * rstep;
+    }
+    for (; m < m1; ++m) {
+        const uint64_t v = (rho + (uint64_t)period * m) * kWave + lane;
+        if (4 * v + 4 <= n) {
+            visit4(__builtin_nontemporal_load(&src[v]), 0);
+        } else {
+            const T *s1 = (const T *)src + 4 * v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (4 * v + k < n) st[k].visit(__builtin_nontemporal_load(&s1[k]), row[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) row[k] += rstep;
+    }
+    constexpr uint64_t kPlane = 4 * kWave;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st[k].store_partial(&sh[wv][4 * lane + k], kPlane);
+    __syncthreads();
+    if (!live) return;
+    for (uint32_t c = lane; c < C; c += kWave) {
+        // Lane-components i = 4 l + k in column c: i = c - col0 (mod C).
+        Stats<T, FLAGS> total;
+        for (uint32_t i = (c + C - col0) % C; i < 4 * kWave; i += C) total.merge_partial(&sh[wv][i], kPlane);
+        if (nwaves > 1)
+            total.store_partial(partials + w * C + c, (uint64_t)nwaves * C);
+        else
+            total.write(p, c);
+    }
+}
+
 // Few long rows (the reduced axis has unit stride but there are too few rows
 // to give every CU work): one wave per (row, chunk of 256-element multiples),
 // lanes along the chunk as in rows_kernel, partials to the planes.
@@ -658,8 +756,24 @@ bool narrow_columns(const RowParams &p, uintptr_t base) {
 constexpr uint64_t kBlockFoldLines = 64 * kFoldSlices;
 constexpr uint64_t kBlockFoldElems = 1ull << 20;
 
+// Axis 0 of a dense row-major matrix with any other column count below 96,
+// more than kBlockFoldLines lines (fewer take the one-launch block form) and
+// row indices within 32 bits: the period form, cols_period_kernel.  From 96
+// columns the column tiles keep enough lanes busy (2^28 f32 sums, period
+// form against column tiles: C = 65 212 / 227 us, 80 199 / 212, 96 200 /
+// 198, 100 200 / 196, 255 201 / 172).
+constexpr uint64_t kPeriodMaxCols = 95;
+constexpr uint64_t kMinPeriodChunk = 64; // 1 KiB blocks per period-form wave
+bool period_columns(const RowParams &p, uintptr_t base) {
+    const uint64_t c = p.rows;
+    return c >= 2 && c <= kPeriodMaxCols && p.row_stride == 1 && p.col_stride == (int64_t)c && base % 4 == 0 &&
+           p.cols > kBlockFoldLines && p.cols <= 0xFFFFFFFFull;
+}
+
 struct Shape {
     bool cols = false, vec = false, narrow = false;
+    bool period = false; // cols_period_kernel over residues mod P of 1 KiB blocks
+    uint32_t P = 1;
     bool block = false; // cols_block_kernel: one launch, no partials
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
@@ -701,6 +815,24 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         chunk = ceil_div(chunk, 4 * kWave) * 4 * kWave;
         s.chunk = chunk;
         s.nchunks = (uint32_t)ceil_div(nvec, chunk);
+        return s;
+    }
+    if (cols_layout && period_columns(p, base)) {
+        // Chunks of whole 4-block trips, about kTargetWaves waves in all;
+        // nchunks counts waves (one partial plane each).
+        s.period = true;
+        uint64_t g = 4 * kWave;
+        for (uint64_t a = p.rows; a != 0;) {
+            const uint64_t t = g % a;
+            g = a;
+            a = t;
+        }
+        s.P = (uint32_t)(p.rows / g);
+        const uint64_t nblk = ceil_div(p.cols * p.rows, 4 * kWave);
+        uint64_t chunk = ceil_div(nblk, kTargetWaves);
+        if (chunk < kMinPeriodChunk) chunk = kMinPeriodChunk;
+        s.chunk = ceil_div(chunk, 4) * 4;
+        s.nchunks = s.P * (uint32_t)ceil_div(ceil_div(nblk, s.P), s.chunk);
         return s;
     }
     if (cols_layout) {
@@ -765,6 +897,11 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
         hipLaunchKernelGGL((cols_narrow_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
                            s.chunk, s.nchunks);
         HX_TRY(check_launch("cols_narrow_kernel"));
+    } else if (s.period) {
+        const uint64_t blocks = ceil_div((uint64_t)s.nchunks, kBlock / kWave);
+        hipLaunchKernelGGL((cols_period_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
+                           s.P, s.chunk, s.nchunks);
+        HX_TRY(check_launch("cols_period_kernel"));
     } else if (s.block) {
         if (s.groups > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");
         const dim3 grid((uint32_t)s.groups), block(kWave * kFoldSlices);

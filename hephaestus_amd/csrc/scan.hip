@@ -1513,6 +1513,192 @@ void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carrie
     }
 }
 
+// Row-tile column scans: axis 0 of a dense row-major [R, C] matrix for the
+// other column counts below 256 (C = 2, or C not a power of two), where
+// the 16-byte lanes of the narrow form would not see fixed columns.  A tile
+// of `rows` whole rows (a multiple of 4, at most kRowTileElems elements)
+// moves between HBM and LDS as coalesced 16-byte vectors.  In LDS, thread j
+// owns column j mod C over row group j / C, one of G = 256 / C contiguous
+// groups of `rpg` rows: pass 1 (col_rowtile_totals_kernel) folds each group
+// and then the groups in order into the tile's column totals; pass 2 is
+// col_narrow_carry_kernel; pass 3 (col_rowtile_scan_kernel) folds the
+// groups again, then rescans each group's rows in place from the tile's
+// carry and the earlier groups' totals before the tile is stored.  Every
+// combination runs in ColAcc (f64 for f32) in an order fixed by the shape,
+// so f32 results are reproducible.  Mirrored scans take tiles from row R - 1
+// down and walk each tile's rows upwards in LDS.  The strided per-line path
+// gave these shapes one lane per line (2^28 u32, C = 3: 2.3 ms; C = 12:
+// 10 ms).  Tiles of 16384 elements and 512 threads (two blocks per CU by
+// LDS) measured best: 2^28 u32 at C = 3 / 12 / 100 / 255 took 597 / 586 /
+// 592 / 638 us, against 614 / 594 / 656 / 712 with 8192 elements and 256
+// threads and 651 / 682 / 820 / 906 with 4096.
+constexpr int kRowTileThreads = 512;
+constexpr uint32_t kRowTileElems = 16384;
+constexpr int kRowTileVecsPerThread = (int)(kRowTileElems / 4 / kRowTileThreads);
+
+struct RowTileShape {
+    uint64_t R = 0, tiles = 0;
+    uint32_t C = 0;
+    uint32_t rows = 0;   // rows per tile
+    uint32_t groups = 0; // row groups (threads) per column
+    uint32_t rpg = 0;    // rows per group
+};
+
+RowTileShape row_tile_shape(uint64_t C, uint64_t R) {
+    RowTileShape s;
+    s.R = R;
+    s.C = (uint32_t)C;
+    s.rows = (uint32_t)(kRowTileElems / C) & ~3u; // C < 256: at least 64
+    s.groups = (uint32_t)(kRowTileThreads / C);
+    // An odd group length keeps the lanes of one wave (64 / C groups, C * rpg
+    // elements apart in LDS) off a common bank: with C = 2 and 32 rows per
+    // group every lane of a wave hit one bank (2^28 u32: 1081 us).
+    s.rpg = ((s.rows + s.groups - 1) / s.groups) | 1u;
+    s.tiles = ceil_div(R, (uint64_t)s.rows);
+    return s;
+}
+
+// Tile t's physical rows [r0, r0 + n).
+template <bool REV>
+__device__ __forceinline__ void row_tile_span(const RowTileShape &s, uint64_t t, uint64_t &r0, uint32_t &n) {
+    const uint64_t a = t * s.rows;
+    const uint64_t b = a + s.rows < s.R ? a + s.rows : s.R;
+    n = (uint32_t)(b - a);
+    r0 = REV ? s.R - b : a;
+}
+
+// ne elements from src (4-byte aligned) into the 16-byte aligned LDS tile:
+// every vector load of the thread in flight before the LDS writes.  Loads
+// past the tile's last vector re-read that vector (no predicated loads, whose
+// merges into the register array cost over 200 VGPRs) and are not written.
+template <typename T> __device__ __forceinline__ void row_tile_load(const T *src, uint32_t ne, T *tile) {
+    using VA = typename Vec4A4<T>::type;
+    using VL = typename Vec4<T>::type;
+    const uint32_t nv = ne / 4;
+    if (nv > 0) {
+        VA x[kRowTileVecsPerThread];
+#pragma unroll
+        for (int u = 0; u < kRowTileVecsPerThread; ++u) {
+            const uint32_t v = threadIdx.x + (uint32_t)u * kRowTileThreads;
+            x[u] = load_a4<true>((const VA *)(src + 4 * (v < nv ? v : nv - 1)));
+        }
+#pragma unroll
+        for (int u = 0; u < kRowTileVecsPerThread; ++u) {
+            const uint32_t v = threadIdx.x + (uint32_t)u * kRowTileThreads;
+            if (v < nv) *(VL *)(tile + 4 * v) = x[u];
+        }
+    }
+    const uint32_t e = 4 * nv + threadIdx.x;
+    if (e < ne) tile[e] = __builtin_nontemporal_load(src + e);
+}
+
+template <typename T> __device__ __forceinline__ void row_tile_store(const T *tile, uint32_t ne, T *dst) {
+    using VA = typename Vec4A4<T>::type;
+    using VL = typename Vec4<T>::type;
+    const uint32_t nv = ne / 4;
+#pragma unroll
+    for (int u = 0; u < kRowTileVecsPerThread; ++u) {
+        const uint32_t v = threadIdx.x + (uint32_t)u * kRowTileThreads;
+        if (v < nv) store_a4<true>((VA)(*(const VL *)(tile + 4 * v)), (VA *)(dst + 4 * v));
+    }
+    const uint32_t e = 4 * nv + threadIdx.x;
+    if (e < ne) __builtin_nontemporal_store(tile[e], dst + e);
+}
+
+// Fold of column c over logical rows [lo, hi) of a tile of n rows (logical
+// row i is physical row n - 1 - i when mirrored), eight LDS reads in flight.
+template <typename T, typename Op, bool REV>
+__device__ __forceinline__ typename ColAcc<T>::type row_group_fold(const T *tile, uint32_t n, uint32_t C, uint32_t c,
+                                                                  uint32_t lo, uint32_t hi) {
+    using A = typename ColAcc<T>::type;
+    A acc = Op::template identity<A>();
+    uint32_t i = lo;
+    for (; i + 8 <= hi; i += 8) {
+        T x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = tile[(REV ? n - 1 - (i + u) : i + u) * C + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = Op::combine(acc, (A)x[u]);
+    }
+    for (; i < hi; ++i) acc = Op::combine(acc, (A)tile[(REV ? n - 1 - i : i) * C + c]);
+    return acc;
+}
+
+template <typename T, typename Op, bool REV>
+__global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void col_rowtile_totals_kernel(ScanParams p, RowTileShape s,
+                                                                             typename ColAcc<T>::type *totals) {
+    using A = typename ColAcc<T>::type;
+    __shared__ __attribute__((aligned(16))) T tile[kRowTileElems];
+    __shared__ A gtot[kRowTileThreads];
+    const uint64_t t = xcd_contiguous(blockIdx.x, gridDim.x); // no look-back: any tile order
+    const uint32_t C = s.C;
+    uint64_t r0;
+    uint32_t n;
+    row_tile_span<REV>(s, t, r0, n);
+    row_tile_load<T>((const T *)p.in + p.in_offset + r0 * C, n * C, tile);
+    __syncthreads();
+    const uint32_t j = threadIdx.x, g = j / C, c = j - g * C;
+    if (g < s.groups) {
+        const uint32_t lo = g * s.rpg < n ? g * s.rpg : n;
+        const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
+        gtot[j] = row_group_fold<T, Op, REV>(tile, n, C, c, lo, hi);
+    }
+    __syncthreads();
+    if (j < C) {
+        A tot = Op::template identity<A>();
+        for (uint32_t q = 0; q < s.groups; ++q) tot = Op::combine(tot, gtot[q * C + j]);
+        totals[t * C + j] = tot;
+    }
+}
+
+template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
+__global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void col_rowtile_scan_kernel(ScanParams p, RowTileShape s,
+                                                                           const typename ColAcc<T>::type *carries) {
+    using A = typename ColAcc<T>::type;
+    __shared__ __attribute__((aligned(16))) T tile[kRowTileElems];
+    __shared__ A gtot[kRowTileThreads];
+    const uint64_t t = xcd_contiguous(blockIdx.x, gridDim.x); // no look-back: any tile order
+    const uint32_t C = s.C;
+    uint64_t r0;
+    uint32_t n;
+    row_tile_span<REV>(s, t, r0, n);
+    row_tile_load<T>((const T *)p.in + p.in_offset + r0 * C, n * C, tile);
+    __syncthreads();
+    const uint32_t j = threadIdx.x, g = j / C, c = j - g * C;
+    const bool owner = g < s.groups;
+    const uint32_t lo = g * s.rpg < n ? g * s.rpg : n;
+    const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
+    if (owner) gtot[j] = row_group_fold<T, Op, REV>(tile, n, C, c, lo, hi);
+    __syncthreads();
+    if (owner) {
+        A pre = CARRY ? carries[t * C + c] : Op::template identity<A>();
+        for (uint32_t q = 0; q < g; ++q) pre = Op::combine(pre, gtot[q * C + c]);
+        // Eight rows read, then rescanned and written (distinct slots).
+        auto step = [&](T &slot, T x) {
+            if constexpr (EXCL) {
+                slot = (T)pre;
+                pre = Op::combine(pre, (A)x);
+            } else {
+                pre = Op::combine(pre, (A)x);
+                slot = (T)pre;
+            }
+        };
+        uint32_t i = lo;
+        for (; i + 8 <= hi; i += 8) {
+            T x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = tile[(REV ? n - 1 - (i + u) : i + u) * C + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) step(tile[(REV ? n - 1 - (i + u) : i + u) * C + c], x[u]);
+        }
+        for (; i < hi; ++i) {
+            T &slot = tile[(REV ? n - 1 - i : i) * C + c];
+            step(slot, slot);
+        }
+    }
+    __syncthreads();
+    row_tile_store<T>(tile, n * C, (T *)p.out + p.out_offset + r0 * C);
+}
 
 // Single-pass column scan.  A block owns a tile of kColTileRows scan steps x
 // 64*V adjacent lines.  Its kColDataWaves data waves each hold kColRows
@@ -2102,9 +2288,59 @@ hx_status launch_narrow(const ScanArgs &a, const ScanParams &p, void *ws, uint64
                      : launch_narrow_dir<T, Op, false, false>(p, tiles, ws, stream);
 }
 
+// Row-tile column scans (col_rowtile_*): see the kernels' comment.
+bool rowtile_column_scan(const ScanArgs &a) {
+    const uint64_t c = a.lines;
+    const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
+    const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
+    return c >= 2 && c < kSinglePassMinLines && !narrow_column_scan(a) && a.in_line_stride == 1 &&
+           a.out_line_stride == 1 && a.in_elem_stride == (int64_t)c && a.out_elem_stride == (int64_t)c &&
+           ibase % 4 == 0 && obase % 4 == 0;
+}
+
+uint64_t rowtile_bytes(const ScanArgs &a) {
+    const RowTileShape s = row_tile_shape(a.lines, a.len);
+    if (s.tiles <= 1) return 0;
+    return s.tiles * a.lines * (a.dtype == HX_DTYPE_F32 ? 8u : 4u);
+}
+
+template <typename T, typename Op, bool EXCL, bool REV>
+hx_status launch_rowtile_dir(const ScanParams &p, const RowTileShape &s, void *ws, hipStream_t stream) {
+    using A = typename ColAcc<T>::type;
+    if (s.tiles > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "column scan exceeds the grid range");
+    const dim3 grid((uint32_t)s.tiles), block(kRowTileThreads);
+    A *totals = (A *)ws;
+    if (s.tiles > 1) {
+        hipLaunchKernelGGL((col_rowtile_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, s, totals);
+        HX_TRY(check_launch("col_rowtile_totals_kernel"));
+        hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3(s.C), dim3(kNarrowCarryThreads), 0, stream, totals,
+                           s.C, s.tiles);
+        HX_TRY(check_launch("col_narrow_carry_kernel"));
+        hipLaunchKernelGGL((col_rowtile_scan_kernel<T, Op, EXCL, REV, true>), grid, block, 0, stream, p, s,
+                           (const A *)totals);
+    } else {
+        hipLaunchKernelGGL((col_rowtile_scan_kernel<T, Op, EXCL, REV, false>), grid, block, 0, stream, p, s,
+                           (const A *)totals);
+    }
+    return check_launch("col_rowtile_scan_kernel");
+}
+
+template <typename T, typename Op>
+hx_status launch_rowtile(const ScanArgs &a, const ScanParams &p, void *ws, uint64_t ws_bytes, hipStream_t stream) {
+    const RowTileShape s = row_tile_shape(a.lines, a.len);
+    if (s.tiles > 1 && ws_bytes < rowtile_bytes(a))
+        return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
+    if (a.exclusive)
+        return a.reverse ? launch_rowtile_dir<T, Op, true, true>(p, s, ws, stream)
+                         : launch_rowtile_dir<T, Op, true, false>(p, s, ws, stream);
+    return a.reverse ? launch_rowtile_dir<T, Op, false, true>(p, s, ws, stream)
+                     : launch_rowtile_dir<T, Op, false, false>(p, s, ws, stream);
+}
+
 uint64_t scan_bytes(const ScanArgs &a) {
     if (short_line_scan(a)) return 0;
     if (narrow_column_scan(a)) return narrow_bytes(a);
+    if (rowtile_column_scan(a)) return rowtile_bytes(a);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape c = col_lb_shape(a);
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
@@ -2138,6 +2374,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 
     if (short_line_scan(a)) return launch_short<T, Op>(a, stream);
     if (narrow_column_scan(a)) return launch_narrow<T, Op>(a, p, ws, ws_bytes, stream);
+    if (rowtile_column_scan(a)) return launch_rowtile<T, Op>(a, p, ws, ws_bytes, stream);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape cs = col_lb_shape(a);
         if (cs.groups * cs.chunks > 0x7FFFFFFFull)
@@ -2189,7 +2426,7 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
 bool scan_uses_lookback(const ScanArgs &a) {
-    if (short_line_scan(a) || narrow_column_scan(a)) return false;
+    if (short_line_scan(a) || narrow_column_scan(a) || rowtile_column_scan(a)) return false;
     return !column_mode(a) || column_single_pass(a);
 }
 

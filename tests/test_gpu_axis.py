@@ -111,7 +111,14 @@ SHAPES = [((4099, 1000), 0), ((3001, 999), 0), ((20, 256), 0), ((3, 100003), 1),
           # several chunks for the tall ones; 2 columns x odd rows is not whole
           # vectors and takes the column tiles
           ((1048577, 4), 0), ((70001, 8), 0), ((5000, 16), 0), ((3001, 32), 0), ((4096, 2), 0), ((4097, 2), 0),
-          ((1, 4), 0)]
+          ((1, 4), 0),
+          # other column counts below 96 past 1024 lines (the period form:
+          # every P-th 1 KiB block per wave, P = C / gcd(C, 256)): ranges that
+          # end inside a vector or a block, many waves per residue, C = 95
+          # (P = 95), a power of two above 32 (P = 1), 1025 lines; from 96
+          # columns the column tiles again
+          ((1048577, 3), 0), ((70001, 5), 0), ((30001, 6), 0), ((20000, 90), 0), ((4099, 95), 0),
+          ((9000, 64), 0), ((1025, 7), 0), ((20000, 100), 0), ((4099, 255), 0)]
 
 
 @pytest.mark.parametrize("op", list(OPS))
@@ -181,16 +188,18 @@ def test_small_column_f32_sums_are_deterministic(device, oracle):
 
 @pytest.mark.parametrize("op", ["sum", "argmax", "min"])
 @pytest.mark.parametrize("offset", [4, 1])
-def test_narrow_columns_offset_views(device, oracle, op, offset):
-    # offset 4 keeps the range 16-byte aligned (narrow form), offset 1 does not
-    r, c = 30001, 8
+@pytest.mark.parametrize("c", [8, 3, 90])
+def test_narrow_columns_offset_views(device, oracle, op, offset, c):
+    # offset 4 keeps the range 16-byte aligned, offset 1 does not (both forms
+    # load 16-byte vectors at 4-byte alignment)
+    r = 30001
     host = host_for(oracle, np.float32, offset + r * c, seed=offset, op=op)
     got = run_axis(device, op, np.float32, host, (r, c), (c, 1), offset, 0)
     check(oracle, op, np.float32, got, lines_of(host, (r, c), (c, 1), offset, 0))
 
 
-def test_split_f32_sums_are_deterministic(device, oracle):
-    r, c = 8192, 1024
+@pytest.mark.parametrize("r,c", [(8192, 1024), (1 << 20, 3), (40000, 95)])
+def test_split_f32_sums_are_deterministic(device, oracle, r, c):
     host = oracle.normal(r * c, seed=5)
     a = run_axis(device, "sum", np.float32, host, (r, c), (c, 1), 0, 0)
     b = run_axis(device, "sum", np.float32, host, (r, c), (c, 1), 0, 0)
@@ -294,7 +303,12 @@ def run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exc
 COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256), (3000, 100), (65536, 16),
                  # narrow columns (4 to 128, powers of two): the dense range
                  # scanned with strided lane scans, one or many chunks
-                 ((1 << 20) + 3, 4), (70001, 8), (4097, 32), (1000, 64), (3001, 128), (5, 4)]
+                 ((1 << 20) + 3, 4), (70001, 8), (4097, 32), (1000, 64), (3001, 128), (5, 4),
+                 # other columns below 256 (row tiles of about 8192 elements
+                 # staged through LDS, a thread per column and row group): many
+                 # tiles with a partial last one, a single tile, one row
+                 ((1 << 20) + 1, 2), (70001, 3), (30001, 5), (4099, 7), (20001, 12), (5000, 24), (1000, 200),
+                 (3001, 255), (5, 3), (1, 6)]
 
 
 @pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
@@ -331,7 +345,7 @@ def test_row_scan_tile_shapes(device, oracle, shape, dtype, variant):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.uint32])
-@pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100), (100003, 8)])
+@pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100), (100003, 8), (100003, 3), (30001, 6)])
 def test_column_scan_off_16_byte_boundaries(device, oracle, shape, dtype):
     # offset 1: every line's vectors start 4 bytes past a 16-byte boundary
     # (single pass for 1000 lines, chunked for 100, narrow for 8); vectors need only 4-byte

@@ -206,6 +206,32 @@ def test_narrow_column_scan_with_many_tiles(device, kind, reverse):
     out.free()
 
 
+@pytest.mark.parametrize("kind,reverse", [("inclusive", False), ("exclusive", True)])
+def test_row_tile_column_scan_with_many_tiles(device, kind, reverse):
+    """[3 * 2^24 + 5, 3] u32 along axis 0: row tiles of 5460 rows, 9219
+    tiles, so each thread of the carry pass owns 10 tiles (past its
+    one-batch case).  Every element is 1 except x[r0][c0] = 1000, as in
+    the narrow case above."""
+    R, C = 3 * (1 << 24) + 5, 3
+    r0, c0 = (1 << 24) + 7, 2
+    x = device.alloc_uninitialized(np.uint32, R * C)
+    device.fill_uniform_int(x, seed=9, lo=1, hi=1)
+    device.write_sub_buffer(x, r0 * C + c0, np.array([1000], np.uint32))
+    out = device.alloc_uninitialized(np.uint32, R * C)
+    lay = Layout.c_contiguous([R, C])
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0,
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive if kind == "exclusive" else hx.ScanKind.Inclusive)
+    for r in (0, 1, 5459, 5460, r0 - 1, r0, r0 + 1, R - 5461, R - 5460, R - 1):
+        got = _slice(device, out, r * C, C)
+        want = np.full(C, (R - 1 - r) if reverse else (r + 1), np.uint64)
+        if (r < r0) if reverse else (r >= r0):
+            want[c0] += 999
+        assert np.array_equal(got, want.astype(np.uint32)), r
+    x.free()
+    out.free()
+
+
 def test_row_scans_of_2_26_lines(device):
     """[2^26 + 5, 4] u32 scanned along axis 1: every line is one 64-lane
     tile, so one launch would need 2^32 + 320 work-items, past the 32-bit
