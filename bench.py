@@ -50,7 +50,8 @@ sys.path.insert(0, str(REPO))
 PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30",
              "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
-             "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colsum_period_f32")
+             "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colscan_rowtile_wide_u32",
+             "colsum_period_f32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "sum_f32_2_20": "full_reduce_kernel<",
              "rows_f32": "rows_kernel", "segmented_i32": "segmented_sum_kernel",
@@ -58,7 +59,8 @@ KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", 
              "copy_u32": "copy_tiles_kernel", "dot_f32": "map_reduce_kernel<", "axpy_f32": "vector_tiles_kernel<1",
              "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel",
              "colscan_narrow_u32": "col_narrow_scan_kernel", "segmented_long_i32": "segmented_sum_kernel",
-             "colscan_rowtile_u32": "col_rowtile_scan_kernel", "colsum_period_f32": "cols_period_kernel"}
+             "colscan_rowtile_u32": "col_rowtile_lookback_kernel", "colscan_rowtile_wide_u32": "col_rowtile_scan_kernel",
+             "colsum_period_f32": "cols_period_kernel"}
 
 
 def log(msg: str) -> None:
@@ -579,28 +581,9 @@ def bench_colscan_u32(hx, dev, args):
     return {"n": rows * cols, "ms": ms, "bytes": 8 * rows * cols}
 
 
-def bench_colscan_narrow_u32(hx, dev, args):
-    """Axis-0 inclusive scans of 2^28-element row-major u32 matrices with 4,
-    16, 64 and 128 columns (the narrow-column form); "ms" is their mean."""
-    from hephaestus_amd import Layout, StridedView
-
-    n = 1 << 28
-    x = dev.alloc_uninitialized(np.uint32, n)
-    dev.fill_uniform_int(x, seed=3, lo=0, hi=255)
-    out = dev.alloc_uninitialized(np.uint32, n)
-    per = {}
-    for c in (4, 16, 64, 128):
-        lay = Layout.c_contiguous([n // c, c])
-        plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0,
-                                                  hx.ScanDirection.Forward, StridedView(out, lay))
-        per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
-        log(f"colscan_narrow_u32: {c} columns {per[c]:.4f} ms/launch")
-    return {"n": n, "ms": statistics.mean(per.values()), "bytes": 8 * n}
-
-
-def bench_colscan_rowtile_u32(hx, dev, args):
-    """Axis-0 inclusive scans of 2^28-element row-major u32 matrices with 3,
-    12, 100 and 255 columns (the row-tile form); "ms" is their mean."""
+def _colscans_u32(hx, dev, args, name, widths):
+    """Axis-0 inclusive scans of 2^28-element row-major u32 matrices, one
+    per column count; "ms" is their mean."""
     from hephaestus_amd import Layout, StridedView
 
     n = 1 << 28
@@ -608,15 +591,30 @@ def bench_colscan_rowtile_u32(hx, dev, args):
     dev.fill_uniform_int(x, seed=3, lo=0, hi=255)
     out = dev.alloc_uninitialized(np.uint32, n)
     per, nbytes = {}, []
-    for c in (3, 12, 100, 255):
-        m = (n // c) * c
+    for c in widths:
         lay = Layout.c_contiguous([n // c, c])
         plan = hx.RocmScanOps().prepare_scan_axis(dev, hx.CumSumOp, StridedView(x, lay), 0,
                                                   hx.ScanDirection.Forward, StridedView(out, lay))
         per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
-        nbytes.append(8 * m)
-        log(f"colscan_rowtile_u32: {c} columns {per[c]:.4f} ms/launch")
+        nbytes.append(8 * (n // c) * c)
+        log(f"{name}: {c} columns {per[c]:.4f} ms/launch")
     return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
+
+
+def bench_colscan_narrow_u32(hx, dev, args):
+    """32, 64 and 128 columns: the narrow-column form (three passes)."""
+    return _colscans_u32(hx, dev, args, "colscan_narrow_u32", (32, 64, 128))
+
+
+def bench_colscan_rowtile_u32(hx, dev, args):
+    """3, 4, 12 and 16 columns: single-pass row tiles (look-back over
+    C-wide carries)."""
+    return _colscans_u32(hx, dev, args, "colscan_rowtile_u32", (3, 4, 12, 16))
+
+
+def bench_colscan_rowtile_wide_u32(hx, dev, args):
+    """100 and 255 columns: three-pass row tiles."""
+    return _colscans_u32(hx, dev, args, "colscan_rowtile_wide_u32", (100, 255))
 
 
 def bench_colsum_period_f32(hx, dev, args):
@@ -1110,7 +1108,8 @@ def main() -> int:
     if args.workload == "all":
         extra = {}
         for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
-                     "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colsum_period_f32"):
+                     "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32",
+                     "colscan_rowtile_wide_u32", "colsum_period_f32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             g = gbs(r["bytes"], r["ms"])
             extra[name] = {"value": round(g, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

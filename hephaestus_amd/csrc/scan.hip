@@ -101,7 +101,7 @@ using PackedStatus = PackedStatusT<1>;                             // column loo
 using TilePackedStatus = PackedStatusT<kTileStatusBytes / 8>;      // tile scans
 
 // f64 carries of the tile scans: one 16-byte slot per entry (at the start of
-// the entry's 128-byte line), overwritten by
+// the entry's 128-byte line; adjacent slots for row-tile columns), overwritten by
 // its single writer (aggregate, then inclusive prefix) and read with ONE
 // 16-byte load per lane.  Dword i of the slot is (check << 16) | bits
 // [63-16i : 48-16i] of the f64, with check = (tag << 2) | flag (tags below
@@ -115,12 +115,12 @@ using TilePackedStatus = PackedStatusT<kTileStatusBytes / 8>;      // tile scans
 // 2^30 f32 inclusive scan on MI355X: 1360 -> 1315 us; the number of loads
 // per poll, not their cache scope, set the difference (agent and system
 // scope both 1360 us).
-struct F64QuadStatus {
+template <uint32_t STRIDE> struct F64QuadStatusT {
     using C = double;
     typedef uint32_t slot_t __attribute__((ext_vector_type(4)));
     uint64_t *words;
     __device__ __forceinline__ volatile __attribute__((address_space(1))) slot_t *slot(uint64_t t) const {
-        return (volatile __attribute__((address_space(1))) slot_t *)(words + t * (kTileStatusBytes / 8));
+        return (volatile __attribute__((address_space(1))) slot_t *)(words + t * STRIDE);
     }
     __device__ __forceinline__ void publish(uint64_t t, uint32_t tag, uint32_t flag, C v) const {
         uint32_t w[4];
@@ -146,6 +146,8 @@ struct F64QuadStatus {
         v = __builtin_bit_cast(double, b);
     }
 };
+using F64QuadStatus = F64QuadStatusT<kTileStatusBytes / 8>; // tile scans: one slot per 128-byte line
+using F64QuadDense = F64QuadStatusT<2>;                     // row-tile columns: adjacent slots
 
 // f64 values for the single-pass column scan: one slot of two self-tagged
 // words (high and low halves) per entry, which the owner writes twice --
@@ -174,7 +176,7 @@ struct F64PairStatus {
 // Whether waiters that compute a missing status publish it for others
 // (publish_if_unset, a CAS on a single word) or keep it to themselves.
 template <typename S> struct SharedFallback { static constexpr bool value = true; };
-template <> struct SharedFallback<F64QuadStatus> { static constexpr bool value = false; };
+template <uint32_t STRIDE> struct SharedFallback<F64QuadStatusT<STRIDE>> { static constexpr bool value = false; };
 
 struct ScanParams {
     const void *in;
@@ -1150,22 +1152,8 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     }
 }
 
-// Narrow column scans: axis 0 of a dense row-major [R, C] matrix with C a
-// power of two from 4 to 128 (fewer lines than the single pass takes).  The
-// matrix is one contiguous range of R*C/4 16-byte vectors, and logical
-// vector g (the range mirrored, components reversed, for a suffix scan)
-// holds in component k the element of column (4g + k) mod C (reverse:
-// C-1 minus that).  Waves take chunks of whole 256-vector trips, so lane l
-// of every step sees the same columns: lanes l, l+s, l+2s, ... (s = C/4)
-// share columns, and a step's per-column scan is a strided lane scan.  The
-// column-tile forms gave such matrices one live lane in 64/C (2^28 u32 as
-// [2^26, 4]: 3.4 ms).  Three launches, as the chunked column scan:
-//   col_narrow_totals_kernel  per chunk and column, the total;
-//   col_narrow_carry_kernel   per column, an exclusive scan of its totals;
-//   col_narrow_scan_kernel    every chunk rescanned from its carries.
-// f32 steps scan in f32 and add f64 carries; integers wrap.
 // Narrow column scans: axis 0 of a dense row-major [R, C] matrix, C a power
-// of two from 4 to 128, read as the one contiguous range of 16-byte vectors
+// of two from 32 to 128, read as the one contiguous range of 16-byte vectors
 // it is.  Component k of vector g holds column (4g + k) mod C, and since C
 // divides 256 that is column (4l + k) mod C for lane l of every step: a lane
 // always holds the same four columns, and the lanes of one column in a step
@@ -1174,8 +1162,15 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
 // components reversed), so every pass works in logical order and logical
 // columns.  Tiles are the scan's own: 8 waves x 16 steps of 64 vectors
 // (128 KiB, two blocks per CU), each wave streaming its own 16 KiB run with
-// all 16 loads in flight.  Three passes: tile totals per column (one read), an exclusive
-// scan of the tile totals per column, and the rescan (one read, one write).
+// all 16 loads in flight.  Three launches:
+//   col_narrow_totals_kernel  per tile and column, the total (one read);
+//   col_narrow_carry_kernel   per column, an exclusive scan of its totals;
+//   col_narrow_scan_kernel    every tile rescanned from its carries (one
+//                             read, one write).
+// f32 steps scan in f32 and add f64 carries; integers wrap.  The column-tile
+// forms gave such matrices one live lane in 64/C.  Narrower powers of two
+// take the single-pass row tiles (2^28 u32 at C = 4 / 8 / 16: 515 / 522 /
+// 525 us here, 439 / 450 / 455 there).
 constexpr int kNarrowWaves = 8, kNarrowSteps = 16;
 constexpr int kNarrowWavesPerEu = 4; // two 8-wave blocks per CU: at most 128 VGPRs
 constexpr uint64_t kNarrowTileVecs = (uint64_t)kNarrowWaves * kNarrowSteps * kWave;
@@ -1504,9 +1499,6 @@ void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carrie
         }
     };
     switch (s) { // wave-uniform: C is a launch parameter
-    case 1: narrow_wave_scan<1, T, Op, EXCL>(x, outer, lane, store); break;
-    case 2: narrow_wave_scan<2, T, Op, EXCL>(x, outer, lane, store); break;
-    case 4: narrow_wave_scan<4, T, Op, EXCL>(x, outer, lane, store); break;
     case 8: narrow_wave_scan<8, T, Op, EXCL>(x, outer, lane, store); break;
     case 16: narrow_wave_scan<16, T, Op, EXCL>(x, outer, lane, store); break;
     default: narrow_wave_scan<32, T, Op, EXCL>(x, outer, lane, store); break;
@@ -1514,13 +1506,16 @@ void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carrie
 }
 
 // Row-tile column scans: axis 0 of a dense row-major [R, C] matrix for the
-// other column counts below 256 (C = 2, or C not a power of two), where
-// the 16-byte lanes of the narrow form would not see fixed columns.  A tile
+// other column counts from 2 to 255 (every C but 32, 64 and 128).  Unless C
+// divides 256 the 16-byte lanes of the narrow form would not see fixed
+// columns.  Up to kRowTileLbMaxCols columns the tiles look back in one pass
+// (col_rowtile_lookback_kernel, below); wider matrices take three.  A tile
 // of `rows` whole rows (a multiple of 4, at most kRowTileElems elements)
 // moves between HBM and LDS as coalesced 16-byte vectors.  In LDS, thread j
-// owns column j mod C over row group j / C, one of G = 256 / C contiguous
-// groups of `rpg` rows: pass 1 (col_rowtile_totals_kernel) folds each group
-// and then the groups in order into the tile's column totals; pass 2 is
+// owns column j mod C over row group j / C, one of G = 512 / C contiguous
+// groups of `rpg` rows: pass 1 (col_rowtile_totals_kernel) folds each group,
+// then scans the group totals along the groups (row_group_scan), whose last
+// group holds the tile's column totals; pass 2 is
 // col_narrow_carry_kernel; pass 3 (col_rowtile_scan_kernel) folds the
 // groups again, then rescans each group's rows in place from the tile's
 // carry and the earlier groups' totals before the tile is stored.  Every
@@ -1624,6 +1619,53 @@ __device__ __forceinline__ typename ColAcc<T>::type row_group_fold(const T *tile
     return acc;
 }
 
+// Inclusive scan of the group totals gtot[g * C + c] along the groups of
+// each column, in place: Hillis-Steele steps over LDS, two barriers each,
+// in an order fixed by the shape.  Folding the earlier groups one LDS read
+// at a time took a thread up to 169 dependent reads (C = 3) per tile.  Every
+// thread of the block calls it.
+template <typename A, typename Op>
+__device__ __forceinline__ void row_group_scan(A *gtot, uint32_t groups, uint32_t C, uint32_t j, bool owner,
+                                               uint32_t g) {
+    for (uint32_t d = 1; d < groups; d <<= 1) {
+        const bool take = owner && g >= d;
+        A o = Op::template identity<A>();
+        if (take) o = gtot[j - d * C];
+        __syncthreads();
+        if (take) gtot[j] = Op::combine(o, gtot[j]);
+        __syncthreads();
+    }
+}
+
+// Rescan of column c over logical rows [lo, hi) in place from `pre` (the
+// carry into the group), eight rows read before they are rewritten.
+template <typename T, typename Op, bool EXCL, bool REV>
+__device__ __forceinline__ void row_group_rescan(T *tile, uint32_t n, uint32_t C, uint32_t c, uint32_t lo,
+                                                 uint32_t hi, typename ColAcc<T>::type pre) {
+    using A = typename ColAcc<T>::type;
+    auto step = [&](T &slot, T x) {
+        if constexpr (EXCL) {
+            slot = (T)pre;
+            pre = Op::combine(pre, (A)x);
+        } else {
+            pre = Op::combine(pre, (A)x);
+            slot = (T)pre;
+        }
+    };
+    uint32_t i = lo;
+    for (; i + 8 <= hi; i += 8) {
+        T x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = tile[(REV ? n - 1 - (i + u) : i + u) * C + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) step(tile[(REV ? n - 1 - (i + u) : i + u) * C + c], x[u]);
+    }
+    for (; i < hi; ++i) {
+        T &slot = tile[(REV ? n - 1 - i : i) * C + c];
+        step(slot, slot);
+    }
+}
+
 template <typename T, typename Op, bool REV>
 __global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void col_rowtile_totals_kernel(ScanParams p, RowTileShape s,
                                                                              typename ColAcc<T>::type *totals) {
@@ -1638,17 +1680,15 @@ __global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu
     row_tile_load<T>((const T *)p.in + p.in_offset + r0 * C, n * C, tile);
     __syncthreads();
     const uint32_t j = threadIdx.x, g = j / C, c = j - g * C;
-    if (g < s.groups) {
+    const bool owner = g < s.groups;
+    if (owner) {
         const uint32_t lo = g * s.rpg < n ? g * s.rpg : n;
         const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
         gtot[j] = row_group_fold<T, Op, REV>(tile, n, C, c, lo, hi);
     }
     __syncthreads();
-    if (j < C) {
-        A tot = Op::template identity<A>();
-        for (uint32_t q = 0; q < s.groups; ++q) tot = Op::combine(tot, gtot[q * C + j]);
-        totals[t * C + j] = tot;
-    }
+    row_group_scan<A, Op>(gtot, s.groups, C, j, owner, g);
+    if (j < C) totals[t * C + j] = gtot[(s.groups - 1) * C + j];
 }
 
 template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
@@ -1670,31 +1710,163 @@ __global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu
     const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
     if (owner) gtot[j] = row_group_fold<T, Op, REV>(tile, n, C, c, lo, hi);
     __syncthreads();
+    row_group_scan<A, Op>(gtot, s.groups, C, j, owner, g);
     if (owner) {
         A pre = CARRY ? carries[t * C + c] : Op::template identity<A>();
-        for (uint32_t q = 0; q < g; ++q) pre = Op::combine(pre, gtot[q * C + c]);
-        // Eight rows read, then rescanned and written (distinct slots).
-        auto step = [&](T &slot, T x) {
-            if constexpr (EXCL) {
-                slot = (T)pre;
-                pre = Op::combine(pre, (A)x);
-            } else {
-                pre = Op::combine(pre, (A)x);
-                slot = (T)pre;
+        if (g > 0) pre = Op::combine(pre, gtot[j - C]);
+        row_group_rescan<T, Op, EXCL, REV>(tile, n, C, c, lo, hi, pre);
+    }
+    __syncthreads();
+    row_tile_store<T>(tile, n * C, (T *)p.out + p.out_offset + r0 * C);
+}
+
+// Single-pass row-tile column scan: the row tiles above with a decoupled
+// look-back over C-wide carries, so every element is read once and written
+// once.  Status entry (tile u, column c) is u * C + c.  After its groups'
+// totals, tile t publishes its column aggregates (threads c < C), and the
+// whole block looks back in rounds: thread j reads predecessor k = j / C
+// (tile t - 1 - base - k) in column c = j mod C, so a round covers 512 / C
+// predecessors; per column the nearest inclusive prefix of the round is an
+// LDS atomicMin of k; entries up to it that are not ready are polled again,
+// and after p.spin_limit polls the waiter rebuilds that predecessor's column
+// aggregate from the input (rowtile_column_aggregate: the same group sums,
+// folded in group order, so integers match the owner's bits and f32 its value
+// to rounding) and uses it, so progress never depends on dispatch order.  The round's needed values fold over k through an LDS tree
+// into the column carry, which is published with the tile's aggregate as the
+// inclusive prefix.  Tile 0's value is always its prefix.  f32 carries are
+// f64 in 16-byte slots (F64QuadDense), integers packed words.  Unlike the
+// three-pass form, an f32 carry's f64 rounding depends on which predecessors
+// had published prefixes: results agree with the f64 scan to within its
+// bound, not bit for bit across runs.  2^28 u32, us, three passes -> one:
+// C = 2 556 -> 474, 3 599 -> 471, 7 608 -> 473, 12 606 -> 468, 24 579 ->
+// 514; at C = 48 / 100 / 255 (a round covering 10 / 5 / 2 predecessors)
+// one pass took 622 / 800 / 1093, and several statuses per thread and
+// round (up to 8) 572 / 687 / 909 against 578 / 585 / 635 in three passes.
+template <typename T, typename Op, bool REV>
+__device__ __forceinline__ typename ColAcc<T>::type rowtile_column_aggregate(const ScanParams &p, const RowTileShape &s,
+                                                                         uint64_t u, uint32_t c) {
+    using A = typename ColAcc<T>::type;
+    const uint32_t C = s.C;
+    uint64_t r0;
+    uint32_t n;
+    row_tile_span<REV>(s, u, r0, n);
+    const T *base = (const T *)p.in + p.in_offset + r0 * C + c;
+    A tot = Op::template identity<A>();
+    for (uint32_t g = 0; g < s.groups; ++g) {
+        const uint32_t lo = g * s.rpg < n ? g * s.rpg : n;
+        const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
+        A acc = Op::template identity<A>();
+        for (uint32_t i = lo; i < hi; ++i) acc = Op::combine(acc, (A)base[(uint64_t)(REV ? n - 1 - i : i) * C]);
+        tot = Op::combine(tot, acc);
+    }
+    return tot;
+}
+
+template <typename T, typename Op, typename Status, bool EXCL, bool REV>
+__global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void col_rowtile_lookback_kernel(ScanParams p, RowTileShape s, Status st) {
+    using A = typename ColAcc<T>::type;
+    __shared__ __attribute__((aligned(16))) T tile[kRowTileElems];
+    __shared__ A gtot[kRowTileThreads];
+    __shared__ A lb_val[kRowTileThreads];
+    __shared__ A s_agg[256], s_carry[256];
+    __shared__ uint32_t s_first[256], s_done[256];
+    __shared__ uint32_t s_rows;
+    const uint64_t t = p.tile0 + blockIdx.x; // scan order: the look-back needs dispatch order
+    const uint32_t C = s.C;
+    const A aid = Op::template identity<A>();
+    uint64_t r0;
+    uint32_t n;
+    row_tile_span<REV>(s, t, r0, n);
+    row_tile_load<T>((const T *)p.in + p.in_offset + r0 * C, n * C, tile);
+    __syncthreads();
+    const uint32_t j = threadIdx.x, g = j / C, c = j - g * C;
+    const bool owner = g < s.groups;
+    const uint32_t lo = g * s.rpg < n ? g * s.rpg : n;
+    const uint32_t hi = lo + s.rpg < n ? lo + s.rpg : n;
+    if (owner) gtot[j] = row_group_fold<T, Op, REV>(tile, n, C, c, lo, hi);
+    __syncthreads();
+    row_group_scan<A, Op>(gtot, s.groups, C, j, owner, g);
+    if (j < C) {
+        const A tot = gtot[(s.groups - 1) * C + j];
+        s_agg[j] = tot;
+        st.publish_tile(t * C + j, p.tag, t == 0 ? kPrefix : kAggregate, tot);
+        s_carry[j] = aid;
+        s_done[j] = t == 0 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (t > 0) {
+        const uint32_t KP = kRowTileThreads / C; // predecessors per round
+        const uint32_t k = j / C, kc = j - k * C;
+        // Lanes of this wave below this one in the same column (l - C,
+        // l - 2C, ...): of a wave's prefix flags in one column only the
+        // lowest lane's goes to LDS, so the atomics on a column's word stay
+        // at one per wave (one per thread took C = 3 scans from 456 to
+        // about 580 us).
+        const int lane = lane_id();
+        uint64_t below = 0;
+        for (int l = lane - (int)C; l >= 0; l -= (int)C) below |= 1ull << l;
+        uint64_t base = 0;
+        for (;;) {
+            const bool item = k < KP && base + k < t && s_done[kc] == 0u;
+            const uint64_t u = t - 1 - base - k;
+            uint32_t flag = kInvalid;
+            A val = aid;
+            if (item) st.read(u * C + kc, p.tag, flag, val);
+            uint32_t spins = 0;
+            bool need;
+            for (;;) {
+                if (j < C) s_first[j] = KP;
+                if (j == 0) s_rows = 0;
+                __syncthreads();
+                const bool pre = item && flag == kPrefix;
+                const uint64_t pm = ballot(pre);
+                if (pre && (pm & below) == 0ull) atomicMin(&s_first[kc], k);
+                __syncthreads();
+                need = item && k <= s_first[kc];
+                const bool missing = need && flag == kInvalid;
+                if (!__syncthreads_or(missing)) break;
+                if (++spins >= p.spin_limit) {
+                    if (missing) {
+                        val = rowtile_column_aggregate<T, Op, REV>(p, s, u, kc);
+                        flag = u == 0 ? kPrefix : kAggregate; // tile 0's aggregate is its prefix
+                    }
+                    spins = 0;
+                } else {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (missing) st.read(u * C + kc, p.tag, flag, val);
+                }
             }
-        };
-        uint32_t i = lo;
-        for (; i + 8 <= hi; i += 8) {
-            T x[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = tile[(REV ? n - 1 - (i + u) : i + u) * C + c];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) step(tile[(REV ? n - 1 - (i + u) : i + u) * C + c], x[u]);
+            // Fold the round's needed values over k (rows of a [KP][C]
+            // array) in a fixed tree as deep as the deepest needed row, then
+            // into the column carries.
+            lb_val[j] = need ? val : aid;
+            const uint32_t deep =
+                group_reduce<64>(need ? k + 1 : 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+            if (lane == 0 && deep > 0) atomicMax(&s_rows, deep);
+            __syncthreads();
+            for (uint32_t cur = s_rows; cur > 1;) {
+                const uint32_t half = (cur + 1) / 2;
+                if (j < (cur - half) * C) lb_val[j] = Op::combine(lb_val[j], lb_val[j + half * C]);
+                __syncthreads();
+                cur = half;
+            }
+            bool pending = false;
+            if (j < C && s_done[j] == 0u) {
+                s_carry[j] = Op::combine(s_carry[j], lb_val[j]);
+                if (s_first[j] < KP) s_done[j] = 1u;
+                else pending = true;
+            }
+            if (!__syncthreads_or(pending)) break;
+            base += KP;
         }
-        for (; i < hi; ++i) {
-            T &slot = tile[(REV ? n - 1 - i : i) * C + c];
-            step(slot, slot);
-        }
+        if (j < C) st.publish_tile(t * C + j, p.tag, kPrefix, Op::combine(s_carry[j], s_agg[j]));
+        __syncthreads();
+    }
+    if (owner) {
+        A pre = s_carry[c];
+        if (g > 0) pre = Op::combine(pre, gtot[j - C]);
+        row_group_rescan<T, Op, EXCL, REV>(tile, n, C, c, lo, hi, pre);
     }
     __syncthreads();
     row_tile_store<T>(tile, n * C, (T *)p.out + p.out_offset + r0 * C);
@@ -2243,7 +2415,7 @@ bool narrow_column_scan(const ScanArgs &a) {
     const uint64_t c = a.lines;
     const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
     const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
-    return c >= 4 && c < kSinglePassMinLines && (c & (c - 1)) == 0 && a.in_line_stride == 1 &&
+    return c >= 32 && c < kSinglePassMinLines && (c & (c - 1)) == 0 && a.in_line_stride == 1 &&
            a.out_line_stride == 1 && a.in_elem_stride == (int64_t)c && a.out_elem_stride == (int64_t)c &&
            ibase % 4 == 0 && obase % 4 == 0;
 }
@@ -2298,6 +2470,15 @@ bool rowtile_column_scan(const ScanArgs &a) {
            ibase % 4 == 0 && obase % 4 == 0;
 }
 
+// Row-tile scans of more than one tile and at most kRowTileLbMaxCols columns
+// look back (col_rowtile_lookback_kernel) instead of taking three passes:
+// a look-back round covers 512 / C predecessors, and with fewer the chain of
+// tiles falls behind.
+constexpr uint64_t kRowTileLbMaxCols = 24;
+bool rowtile_single_pass(const ScanArgs &a) {
+    return a.lines <= kRowTileLbMaxCols && row_tile_shape(a.lines, a.len).tiles > 1;
+}
+
 uint64_t rowtile_bytes(const ScanArgs &a) {
     const RowTileShape s = row_tile_shape(a.lines, a.len);
     if (s.tiles <= 1) return 0;
@@ -2325,6 +2506,46 @@ hx_status launch_rowtile_dir(const ScanParams &p, const RowTileShape &s, void *w
     return check_launch("col_rowtile_scan_kernel");
 }
 
+uint64_t rowtile_lb_bytes(const ScanArgs &a) {
+    const RowTileShape s = row_tile_shape(a.lines, a.len);
+    return kLookbackOffset + s.tiles * a.lines * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
+}
+
+template <typename T, typename Op, typename Status, bool EXCL>
+hx_status launch_rowtile_lb_dir(const ScanParams &p, const RowTileShape &s, const Status &st, bool rev,
+                                hipStream_t stream) {
+    const dim3 grid((uint32_t)s.tiles), block(kRowTileThreads);
+    if (rev)
+        hipLaunchKernelGGL((col_rowtile_lookback_kernel<T, Op, Status, EXCL, true>), grid, block, 0, stream, p, s, st);
+    else
+        hipLaunchKernelGGL((col_rowtile_lookback_kernel<T, Op, Status, EXCL, false>), grid, block, 0, stream, p, s, st);
+    return check_launch("col_rowtile_lookback_kernel");
+}
+
+template <typename T, typename Op>
+hx_status launch_rowtile_lb(const ScanArgs &a, ScanParams p, void *ws, uint64_t ws_bytes, LookbackState &lb,
+                            hipStream_t stream) {
+    const RowTileShape s = row_tile_shape(a.lines, a.len);
+    if (s.tiles > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "column scan exceeds the grid range");
+    if (ws_bytes < rowtile_lb_bytes(a))
+        return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
+    HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
+    p.tile0 = 0;
+    uint64_t *words = (uint64_t *)((char *)ws + kLookbackOffset);
+    hx_status r;
+    if constexpr (std::is_same<T, float>::value) {
+        const F64QuadDense st{words};
+        r = a.exclusive ? launch_rowtile_lb_dir<T, Op, F64QuadDense, true>(p, s, st, a.reverse, stream)
+                        : launch_rowtile_lb_dir<T, Op, F64QuadDense, false>(p, s, st, a.reverse, stream);
+    } else {
+        const PackedStatus st{words};
+        r = a.exclusive ? launch_rowtile_lb_dir<T, Op, PackedStatus, true>(p, s, st, a.reverse, stream)
+                        : launch_rowtile_lb_dir<T, Op, PackedStatus, false>(p, s, st, a.reverse, stream);
+    }
+    if (r == HX_OK) commit_lookback_launch(lb);
+    return r;
+}
+
 template <typename T, typename Op>
 hx_status launch_rowtile(const ScanArgs &a, const ScanParams &p, void *ws, uint64_t ws_bytes, hipStream_t stream) {
     const RowTileShape s = row_tile_shape(a.lines, a.len);
@@ -2340,7 +2561,7 @@ hx_status launch_rowtile(const ScanArgs &a, const ScanParams &p, void *ws, uint6
 uint64_t scan_bytes(const ScanArgs &a) {
     if (short_line_scan(a)) return 0;
     if (narrow_column_scan(a)) return narrow_bytes(a);
-    if (rowtile_column_scan(a)) return rowtile_bytes(a);
+    if (rowtile_column_scan(a)) return rowtile_single_pass(a) ? rowtile_lb_bytes(a) : rowtile_bytes(a);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape c = col_lb_shape(a);
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
@@ -2374,7 +2595,9 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 
     if (short_line_scan(a)) return launch_short<T, Op>(a, stream);
     if (narrow_column_scan(a)) return launch_narrow<T, Op>(a, p, ws, ws_bytes, stream);
-    if (rowtile_column_scan(a)) return launch_rowtile<T, Op>(a, p, ws, ws_bytes, stream);
+    if (rowtile_column_scan(a))
+        return rowtile_single_pass(a) ? launch_rowtile_lb<T, Op>(a, p, ws, ws_bytes, lb, stream)
+                                      : launch_rowtile<T, Op>(a, p, ws, ws_bytes, stream);
     if (column_mode(a) && column_single_pass(a)) {
         const ColLbShape cs = col_lb_shape(a);
         if (cs.groups * cs.chunks > 0x7FFFFFFFull)
@@ -2426,7 +2649,8 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
 uint64_t scan_workspace_bytes(const ScanArgs &a) { return scan_bytes(a); }
 
 bool scan_uses_lookback(const ScanArgs &a) {
-    if (short_line_scan(a) || narrow_column_scan(a) || rowtile_column_scan(a)) return false;
+    if (rowtile_column_scan(a)) return rowtile_single_pass(a);
+    if (short_line_scan(a) || narrow_column_scan(a)) return false;
     return !column_mode(a) || column_single_pass(a);
 }
 

@@ -298,17 +298,18 @@ def run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exc
 
 # (rows, cols) scanned along axis 0.  Single-pass look-back (256 lines and
 # more): vector lanes over many chunks, scalar lanes, one tile only.
-# Chunked reduce-then-scan (fewer lines): 100 lines (vector lanes), 16 lines x
-# 65536 steps.
-COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256), (3000, 100), (65536, 16),
-                 # narrow columns (4 to 128, powers of two): the dense range
-                 # scanned with strided lane scans, one or many chunks
-                 ((1 << 20) + 3, 4), (70001, 8), (4097, 32), (1000, 64), (3001, 128), (5, 4),
-                 # other columns below 256 (row tiles of about 8192 elements
-                 # staged through LDS, a thread per column and row group): many
+COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256),
+                 # narrow columns (32, 64, 128): the dense range scanned with
+                 # strided lane scans, one or many chunks
+                 (4097, 32), (1000, 64), (3001, 128),
+                 # other columns below 256: row tiles of up to 16384 elements
+                 # staged through LDS, a thread per column and row group.  Up
+                 # to 24 columns one pass with a look-back over C-wide carries
+                 # (257 tiles for 2 and 4 columns), wider three passes; many
                  # tiles with a partial last one, a single tile, one row
-                 ((1 << 20) + 1, 2), (70001, 3), (30001, 5), (4099, 7), (20001, 12), (5000, 24), (1000, 200),
-                 (3001, 255), (5, 3), (1, 6)]
+                 ((1 << 20) + 1, 2), ((1 << 20) + 3, 4), (70001, 3), (30001, 5), (4099, 7), (70001, 8),
+                 (20001, 12), (65536, 16), (5000, 24), (3000, 100), (1000, 200), (3001, 255), (5, 3), (5, 4),
+                 (1, 6)]
 
 
 @pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
@@ -348,11 +349,24 @@ def test_row_scan_tile_shapes(device, oracle, shape, dtype, variant):
 @pytest.mark.parametrize("shape", [(3001, 1000), (3000, 100), (100003, 8), (100003, 3), (30001, 6)])
 def test_column_scan_off_16_byte_boundaries(device, oracle, shape, dtype):
     # offset 1: every line's vectors start 4 bytes past a 16-byte boundary
-    # (single pass for 1000 lines, chunked for 100, narrow for 8); vectors need only 4-byte
+    # (single pass for 1000 lines, row tiles for the others); vectors need only 4-byte
     # alignment, so both keep one 16-byte access per lane and step
     r, c = shape
     run_column_scan(device, oracle, "sum", dtype, shape, (c, 1), 1, 0, False, False, seed=r + c)
     run_column_scan(device, oracle, "sum", dtype, shape, (c, 1), 1, 0, True, True, seed=r + c + 1)
+
+
+@pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("op", ["sum", "prod"])
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32])
+@pytest.mark.parametrize("shape,ld", [((3000, 100), 104), ((65536, 16), 17)])
+def test_chunked_column_scan_of_padded_rows(device, oracle, shape, ld, dtype, op, reverse, kind):
+    # rows padded past their width (line stride 1, element stride ld > C):
+    # not the dense range of the row-tile or narrow forms, so fewer than 256
+    # lines take the chunked reduce-then-scan
+    r, c = shape
+    run_column_scan(device, oracle, op, dtype, shape, (ld, 1), 0, 0, kind == "exclusive", reverse, seed=r + ld)
 
 
 @pytest.mark.parametrize("op", ["sum", "prod"])
@@ -405,10 +419,12 @@ def test_prepared_axis_reduction_batch(device, oracle):
 
 
 @pytest.mark.parametrize("reverse", [False, True])
-def test_prepared_narrow_column_scan_rebinds(device, oracle, reverse):
-    # narrow-column scan through a prepared plan: the workspace for the chunk
-    # carries comes with the plan; later writes to the input are observed
-    r, c = 300001, 8
+@pytest.mark.parametrize("c", [32, 8, 100])
+def test_prepared_narrow_column_scan_rebinds(device, oracle, reverse, c):
+    # narrow-column scans through a prepared plan (narrow form, one-pass and
+    # three-pass row tiles): the workspace for the carries or look-back
+    # statuses comes with the plan; later writes to the input are observed
+    r = 300001
     lay = Layout.c_contiguous([r, c])
     x = oracle.uniform_int(r * c, seed=4, lo=0, hi=1000)
     buf = device.upload(x)

@@ -124,6 +124,19 @@ def test_column_lookback_scans_under_forced_fallbacks(device, oracle, limits, dt
         run_column_scan(device, oracle, "prod", dtype, (3001, 512), (512, 1), 0, 0, True, reverse, seed=19)
 
 
+# Row-tile column look-back (axis 0 of dense matrices with 2 to 255 columns
+# outside the narrow form): a missing predecessor's column aggregate is
+# rebuilt from the input by the waiting thread.  13, 15 and 47 tiles.
+@pytest.mark.parametrize("limits", FORCED)
+@pytest.mark.parametrize("dtype", [np.uint32, np.float32])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_row_tile_lookback_scans_under_forced_fallbacks(device, oracle, limits, dtype, reverse):
+    with wait_limits(*limits):
+        run_column_scan(device, oracle, "sum", dtype, (70001, 3), (3, 1), 0, 0, False, reverse, seed=23)
+        run_column_scan(device, oracle, "prod", dtype, (20001, 12), (12, 1), 0, 0, True, reverse, seed=29)
+        run_column_scan(device, oracle, "sum", dtype, (3001, 255), (255, 1), 0, 0, True, reverse, seed=31)
+
+
 def _segmented(device, values, offsets):
     vb = device.upload(values)
     ob = device.upload(offsets.astype(np.uint32))

@@ -207,13 +207,15 @@ def test_narrow_column_scan_with_many_tiles(device, kind, reverse):
 
 
 @pytest.mark.parametrize("kind,reverse", [("inclusive", False), ("exclusive", True)])
-def test_row_tile_column_scan_with_many_tiles(device, kind, reverse):
-    """[3 * 2^24 + 5, 3] u32 along axis 0: row tiles of 5460 rows, 9219
-    tiles, so each thread of the carry pass owns 10 tiles (past its
-    one-batch case).  Every element is 1 except x[r0][c0] = 1000, as in
-    the narrow case above."""
-    R, C = 3 * (1 << 24) + 5, 3
-    r0, c0 = (1 << 24) + 7, 2
+@pytest.mark.parametrize("C,R,tile_rows", [(3, 3 * (1 << 24) + 5, 5460), (100, 1500007, 160)])
+def test_row_tile_column_scan_with_many_tiles(device, kind, reverse, C, R, tile_rows):
+    """Row tiles along axis 0, u32, with about 9200 tiles: [3 * 2^24 + 5, 3]
+    (tiles of 5460 rows) looks back in one pass over 9219 tiles;
+    [1500007, 100] (tiles of 160 rows, 9376 tiles) takes three passes, and
+    each thread of its carry pass owns 10 tiles (past its one-batch case).
+    Every element is 1 except x[r0][c0] = 1000, as in the narrow case
+    above."""
+    r0, c0 = R // 3 + 7, C - 1
     x = device.alloc_uninitialized(np.uint32, R * C)
     device.fill_uniform_int(x, seed=9, lo=1, hi=1)
     device.write_sub_buffer(x, r0 * C + c0, np.array([1000], np.uint32))
@@ -222,7 +224,8 @@ def test_row_tile_column_scan_with_many_tiles(device, kind, reverse):
     SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, lay), 0,
                         hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
                         hx.ScanKind.Exclusive if kind == "exclusive" else hx.ScanKind.Inclusive)
-    for r in (0, 1, 5459, 5460, r0 - 1, r0, r0 + 1, R - 5461, R - 5460, R - 1):
+    tr = tile_rows
+    for r in (0, 1, tr - 1, tr, r0 - 1, r0, r0 + 1, R - tr - 1, R - tr, R - 1):
         got = _slice(device, out, r * C, C)
         want = np.full(C, (R - 1 - r) if reverse else (r + 1), np.uint64)
         if (r < r0) if reverse else (r >= r0):
