@@ -26,9 +26,8 @@
 //                      thousands of waves however tall the matrix is.
 //   cols_block_kernel  small column reductions in one launch (slices of the
 //                      axis folded through LDS).
-//   cols_narrow_kernel / cols_period_kernel
-//                      axis 0 of dense matrices with fewer than 96 columns,
-//                      read as one contiguous range of 1 KiB wave loads.
+//   cols_period_kernel axis 0 of dense matrices with 2 to 95 columns, read
+//                      as one contiguous range of 1 KiB wave loads.
 //   split_fold_kernel  folds the chunk partials of either split form in a
 //                      fixed order, so f32 sums do not depend on scheduling.
 #include "hx_device.hpp"
@@ -284,6 +283,18 @@ template <typename T, int FLAGS> struct Stats {
         if constexpr ((FLAGS & F_MIN) != 0) o.mink = __shfl_xor(mink, m, kWave);
         merge(o);
     }
+    // The statistics one store_partial wrote.
+    static __device__ __forceinline__ Stats from_partial(const uint64_t *w, uint64_t plane) {
+        Stats s;
+        int q = 0;
+        if constexpr ((FLAGS & (F_SUM | F_MEAN)) != 0) s.sum = from_word<S>(w[(q++) * plane]);
+        if constexpr ((FLAGS & F_PROD) != 0) s.prod = from_word<Pr>(w[(q++) * plane]);
+        if constexpr ((FLAGS & F_ARG) != 0) s.arg = w[(q++) * plane];
+        else if constexpr ((FLAGS & F_MAX) != 0) s.maxk = (uint32_t)w[(q++) * plane];
+        if constexpr ((FLAGS & F_MIN) != 0) s.mink = (uint32_t)w[(q++) * plane];
+        (void)q;
+        return s;
+    }
     // Fold a later chunk's partial into this one.
     __device__ __forceinline__ void merge_partial(const uint64_t *w, uint64_t plane) {
         int q = 0;
@@ -513,107 +524,40 @@ __global__ __launch_bounds__(kWave *kFoldSlices) void cols_block_kernel(RowParam
     }
 }
 
-// Narrow column reductions: axis 0 of a dense row-major [R, C] matrix with
-// C a power of two from 2 to 32.  The matrix is one contiguous range; with
-// 16-byte vectors v = lane + 64 t (chunks start on multiples of 64 vectors),
-// component k of lane l's vector always lands in column (4 l + k) mod C, so
-// each lane keeps four statistics -- one per component -- and every load is a
-// coalesced 1 KiB wave access.  The column-tile form gave such matrices one
-// live lane per wave (65536^2 x 4 f32: 5.0 ms).  A wave owns a chunk of the
-// range; at its end components of the same column fold (C = 2), then lanes
-// of the same columns fold with xor butterflies from mask 32 down to C/4, and
-// lanes l < C/4 (lane 0 for C = 2) hold columns 4l..4l+3.  Chunk statistics
-// go to the partial planes that split_fold_kernel folds in chunk order.
-template <typename T, int FLAGS>
-__global__ __launch_bounds__(kBlock) void cols_narrow_kernel(RowParams p, uint64_t *partials, uint64_t chunk,
-                                                             uint32_t nchunks) {
-    using V = typename Vec4A4<T>::type;
-    const uint64_t w = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) / kWave;
-    if (w >= nchunks) return; // uniform across the wave
-    const int lane = lane_id();
-    const uint32_t C = (uint32_t)p.rows;
-    const uint32_t shift = (uint32_t)__builtin_ctz(C);
-    const V *src = (const V *)((const T *)p.base + p.offset);
-    const uint64_t nvec = (p.cols * C) >> 2;
-    const uint64_t v0 = w * chunk;
-    const uint64_t v1 = v0 + chunk < nvec ? v0 + chunk : nvec;
-    Stats<T, FLAGS> st[4];
-    auto visit4 = [&](const V &x, uint64_t vv) {
-        const uint64_t e = 4 * vv;
-        st[0].visit((T)x.x, (uint32_t)(e >> shift));
-        st[1].visit((T)x.y, (uint32_t)((e + 1) >> shift));
-        st[2].visit((T)x.z, (uint32_t)((e + 2) >> shift));
-        st[3].visit((T)x.w, (uint32_t)((e + 3) >> shift));
-    };
-    // Whole trips of 256 vectors, then one trip with per-lane predicates: the
-    // trip count is the same for every lane.
-    const uint64_t full = (v1 - v0) / (4 * kWave);
-    uint64_t v = v0 + lane;
-    for (uint64_t t = 0; t < full; ++t, v += 4 * kWave) {
-        V x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(&src[v + u * kWave]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) visit4(x[u], v + u * kWave);
-    }
-    if (v0 + full * 4 * kWave < v1) {
-        V x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (v + u * kWave < v1) x[u] = __builtin_nontemporal_load(&src[v + u * kWave]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (v + u * kWave < v1) visit4(x[u], v + u * kWave);
-    }
-    if (C == 2) {
-        st[0].merge(st[2]);
-        st[1].merge(st[3]);
-    }
-    const int lowest = C >= 4 ? (int)(C / 4) : 1;
-    for (int m = kWave / 2; m >= lowest; m >>= 1)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) st[k].merge_xor(m);
-    const int owners = C >= 4 ? (int)(C / 4) : 1;
-    if (lane >= owners) return;
-    const int ncomp = C >= 4 ? 4 : (int)C;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        if (k >= ncomp) break;
-        const uint64_t col = (uint64_t)(4 * lane + k);
-        if (nchunks > 1)
-            st[k].store_partial(partials + w * C + col, (uint64_t)nchunks * C);
-        else
-            st[k].write(p, col);
-    }
-}
-
 // Statistic planes a flag set keeps (sum or mean, product, max or argmax, min).
 template <int FLAGS> constexpr int kPlanes = ((FLAGS & (F_SUM | F_MEAN)) != 0) + ((FLAGS & F_PROD) != 0) +
                                              ((FLAGS & (F_ARG | F_MAX)) != 0) + ((FLAGS & F_MIN) != 0);
 
-// Narrow column reductions for other C below 96: axis 0 of a dense
-// row-major [R, C] matrix.  The matrix is one contiguous range of 1 KiB
-// blocks (256 elements); component k of lane l's vector in block b holds
-// element 256 b + 4 l + k, in column (256 b + 4 l + k) mod C.  Blocks b and
-// b + P, P = C / gcd(C, 256), give every lane-component the same column, so
-// wave w takes the blocks rho + P m of one residue rho = w mod P for m in
-// its chunk (w / P): each lane keeps four statistics and every load is a
-// coalesced 1 KiB wave access, as in cols_narrow_kernel.  Lane-components
-// that share a column fold through the wave's LDS in ascending lane-component
-// order, and lane c (c + 64, ...) stores column c's statistics to plane w,
-// which split_fold_kernel folds in wave order, so f32 sums depend only on
-// the shape (a single wave writes the outputs).  Column tiles gave such matrices C live lanes per wave
-// (2^28 f32 with C = 3: 2.9 ms against 0.19 ms at C = 4).
+constexpr uint64_t kPeriodMaxCols = 95; // the period form's widest matrix
+
+// Narrow column reductions, C from 2 to 95: axis 0 of a dense row-major
+// [R, C] matrix.  The matrix is one contiguous range of 1 KiB blocks (256
+// elements); component k of lane l's vector in block b holds element
+// 256 b + 4 l + k, in column (256 b + 4 l + k) mod C.  Blocks b and b + P,
+// P = C / gcd(C, 256), give every lane-component the same column, so wave w
+// takes the blocks rho + P m of one residue rho = w mod P for m in its chunk
+// (w / P): each lane keeps four statistics and every load is a coalesced
+// 1 KiB wave access.  Lane-components that share a column fold through the
+// wave's LDS in ascending lane-component order, the block's four waves'
+// column statistics fold in wave order, and the block stores them to its
+// partial plane, which split_fold_kernel folds in block order, so f32 sums
+// depend only on the shape (a single block writes the outputs).  Column
+// tiles gave such matrices C live lanes per wave (2^28 f32 with C = 3:
+// 2.7 ms).  A plane per wave instead of per block left the fold at 34 us of
+// 193 (C = 3); an xor-butterfly form for powers of two up to 32 (the lanes
+// of one column folded in registers, a plane per wave) took 180 us against
+// 165-170 here.
 template <typename T, int FLAGS>
 __global__ __launch_bounds__(kBlock) void cols_period_kernel(RowParams p, uint64_t *partials, uint32_t period,
                                                              uint64_t chunk, uint32_t nwaves) {
     using V = typename Vec4A4<T>::type;
     constexpr int kBlockWaves = kBlock / kWave;
     __shared__ uint64_t sh[kBlockWaves][kPlanes<FLAGS> * 4 * kWave];
+    __shared__ uint64_t sh_tot[kBlockWaves][kPlanes<FLAGS> * (kPeriodMaxCols + 1)];
     const int lane = lane_id();
     const int wv = threadIdx.x / kWave;
     const uint64_t w = (uint64_t)blockIdx.x * kBlockWaves + wv;
-    const bool live = w < nwaves; // uniform across the wave
+    const bool live = w < nwaves; // uniform across the wave; the others fold identities
     const uint32_t C = (uint32_t)p.rows;
     const uint64_t n = p.cols * C;
     const uint64_t nblk = (n + 4 * kWave - 1) / (4 * kWave);
@@ -668,13 +612,24 @@ __global__ __launch_bounds__(kBlock) void cols_period_kernel(RowParams p, uint64
 #pragma unroll
     for (int k = 0; k < 4; ++k) st[k].store_partial(&sh[wv][4 * lane + k], kPlane);
     __syncthreads();
-    if (!live) return;
+    // Each wave's column totals (waves past nwaves hold identities), then the
+    // block's: the waves' totals in wave order, one partial plane per block.
+    constexpr uint64_t kColPlane = kPeriodMaxCols + 1;
     for (uint32_t c = lane; c < C; c += kWave) {
         // Lane-components i = 4 l + k in column c: i = c - col0 (mod C).
         Stats<T, FLAGS> total;
         for (uint32_t i = (c + C - col0) % C; i < 4 * kWave; i += C) total.merge_partial(&sh[wv][i], kPlane);
-        if (nwaves > 1)
-            total.store_partial(partials + w * C + c, (uint64_t)nwaves * C);
+        total.store_partial(&sh_tot[wv][c], kColPlane);
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    const uint32_t nblocks = (nwaves + kBlockWaves - 1) / kBlockWaves;
+    for (uint32_t c = lane; c < C; c += kWave) {
+        Stats<T, FLAGS> total;
+#pragma unroll
+        for (int q = 0; q < kBlockWaves; ++q) total.merge_partial(&sh_tot[q][c], kColPlane);
+        if (nblocks > 1)
+            total.store_partial(partials + (uint64_t)blockIdx.x * C + c, (uint64_t)nblocks * C);
         else
             total.write(p, c);
     }
@@ -721,8 +676,21 @@ __global__ __launch_bounds__(kWave *kFoldSlices) void split_fold_kernel(RowParam
     const uint32_t k0 = s * per < nchunks ? s * per : nchunks;
     const uint32_t k1 = k0 + per < nchunks ? k0 + per : nchunks;
     Stats<T, FLAGS> st;
-    if (o < p.rows)
-        for (uint32_t k = k0; k < k1; ++k) st.merge_partial(partials + (uint64_t)k * p.rows + o, plane);
+    if (o < p.rows) {
+        // Eight partials loaded together, then merged in chunk order (one
+        // dependent load per chunk left a 3-output fold of 2049 chunks at
+        // 34 us).
+        uint32_t k = k0;
+        for (; k + 8 <= k1; k += 8) {
+            Stats<T, FLAGS> b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                b[u] = Stats<T, FLAGS>::from_partial(partials + (uint64_t)(k + u) * p.rows + o, plane);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) st.merge(b[u]);
+        }
+        for (; k < k1; ++k) st.merge_partial(partials + (uint64_t)k * p.rows + o, plane);
+    }
     st.store_partial(&sh[s * kWave + lane], (uint64_t)kFoldSlices * kWave);
     __syncthreads();
     if (s != 0 || o >= p.rows) return;
@@ -739,16 +707,6 @@ constexpr uint64_t kTargetWaves = 2048;
 constexpr uint64_t kMinColChunk = 32;    // lines per column-tile chunk
 constexpr uint64_t kMinRowChunk = 8192;  // elements per split-row chunk
 constexpr uint64_t kRowTargetWaves = 4096; // split rows when fewer than half this many
-constexpr uint64_t kMinNarrowChunk = 4096; // 16-byte vectors per narrow-column chunk
-
-// Axis 0 of a dense row-major matrix with 2 to 32 columns (a power of two),
-// in whole 16-byte vectors (which need only 4-byte alignment): the
-// narrow-column form.
-bool narrow_columns(const RowParams &p, uintptr_t base) {
-    const uint64_t c = p.rows;
-    return c >= 2 && c <= 32 && (c & (c - 1)) == 0 && p.row_stride == 1 && p.col_stride == (int64_t)c &&
-           base % 4 == 0 && (p.cols * c) % 4 == 0 && p.cols <= 0xFFFFFFFFull;
-}
 
 // Column reductions that would split their axis take one launch
 // (cols_block_kernel) when the matrix is small: at most kBlockFoldLines lines
@@ -762,7 +720,6 @@ constexpr uint64_t kBlockFoldElems = 1ull << 20;
 // columns the column tiles keep enough lanes busy (2^28 f32 sums, period
 // form against column tiles: C = 65 212 / 227 us, 80 199 / 212, 96 200 /
 // 198, 100 200 / 196, 255 201 / 172).
-constexpr uint64_t kPeriodMaxCols = 95;
 constexpr uint64_t kMinPeriodChunk = 64; // 1 KiB blocks per period-form wave
 bool period_columns(const RowParams &p, uintptr_t base) {
     const uint64_t c = p.rows;
@@ -771,9 +728,9 @@ bool period_columns(const RowParams &p, uintptr_t base) {
 }
 
 struct Shape {
-    bool cols = false, vec = false, narrow = false;
+    bool cols = false, vec = false;
     bool period = false; // cols_period_kernel over residues mod P of 1 KiB blocks
-    uint32_t P = 1;
+    uint32_t P = 1, waves = 0;
     bool block = false; // cols_block_kernel: one launch, no partials
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
@@ -806,17 +763,6 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
     s.cols = cols_layout;
     const uintptr_t base = (uintptr_t)p.base + 4u * p.offset; // every element type is 4 bytes
     uint64_t k = 1;
-    if (cols_layout && narrow_columns(p, base)) {
-        // Chunks of whole 256-vector trips, about kTargetWaves of them.
-        s.narrow = true;
-        const uint64_t nvec = (p.cols * p.rows) >> 2;
-        uint64_t chunk = ceil_div(nvec, kTargetWaves);
-        if (chunk < kMinNarrowChunk) chunk = kMinNarrowChunk;
-        chunk = ceil_div(chunk, 4 * kWave) * 4 * kWave;
-        s.chunk = chunk;
-        s.nchunks = (uint32_t)ceil_div(nvec, chunk);
-        return s;
-    }
     if (cols_layout && period_columns(p, base)) {
         // Chunks of whole 4-block trips, about kTargetWaves waves in all;
         // nchunks counts waves (one partial plane each).
@@ -832,7 +778,8 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         uint64_t chunk = ceil_div(nblk, kTargetWaves);
         if (chunk < kMinPeriodChunk) chunk = kMinPeriodChunk;
         s.chunk = ceil_div(chunk, 4) * 4;
-        s.nchunks = s.P * (uint32_t)ceil_div(ceil_div(nblk, s.P), s.chunk);
+        s.waves = s.P * (uint32_t)ceil_div(ceil_div(nblk, s.P), s.chunk);
+        s.nchunks = (uint32_t)ceil_div((uint64_t)s.waves, kBlock / kWave); // one partial plane per block
         return s;
     }
     if (cols_layout) {
@@ -892,15 +839,9 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
     if (split && ws_bytes < shape_bytes(p, s, FLAGS))
         return fail(HX_ERR_DISPATCH_FAILED, "axis reduction workspace of %llu bytes is too small",
                     (unsigned long long)ws_bytes);
-    if (s.narrow) {
-        const uint64_t blocks = ceil_div((uint64_t)s.nchunks, kBlock / kWave);
-        hipLaunchKernelGGL((cols_narrow_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
-                           s.chunk, s.nchunks);
-        HX_TRY(check_launch("cols_narrow_kernel"));
-    } else if (s.period) {
-        const uint64_t blocks = ceil_div((uint64_t)s.nchunks, kBlock / kWave);
-        hipLaunchKernelGGL((cols_period_kernel<T, FLAGS>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream, p, partials,
-                           s.P, s.chunk, s.nchunks);
+    if (s.period) {
+        hipLaunchKernelGGL((cols_period_kernel<T, FLAGS>), dim3(s.nchunks), dim3(kBlock), 0, stream, p, partials, s.P,
+                           s.chunk, s.waves);
         HX_TRY(check_launch("cols_period_kernel"));
     } else if (s.block) {
         if (s.groups > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");

@@ -107,16 +107,14 @@ def host_for(oracle, dtype, n, seed, op):
 # chunk, few long rows (vector and scalar), and a [N,1] column.
 SHAPES = [((4099, 1000), 0), ((3001, 999), 0), ((20, 256), 0), ((3, 100003), 1), ((5, 65536), 1),
           ((100000, 1), 0),
-          # narrow columns (2 to 32, powers of two): one range of whole vectors,
-          # several chunks for the tall ones; 2 columns x odd rows is not whole
-          # vectors and takes the column tiles
+          # narrow columns, 2 to 95, past 1024 lines (the period form: the
+          # dense range in 1 KiB blocks, every P-th block per wave,
+          # P = C / gcd(C, 256)): powers of two (P = 1), ranges that end
+          # inside a vector or a block, many waves per residue, C = 95
+          # (P = 95), 1025 lines; below 1025 lines the one-launch block form,
+          # from 96 columns the column tiles again
           ((1048577, 4), 0), ((70001, 8), 0), ((5000, 16), 0), ((3001, 32), 0), ((4096, 2), 0), ((4097, 2), 0),
           ((1, 4), 0),
-          # other column counts below 96 past 1024 lines (the period form:
-          # every P-th 1 KiB block per wave, P = C / gcd(C, 256)): ranges that
-          # end inside a vector or a block, many waves per residue, C = 95
-          # (P = 95), a power of two above 32 (P = 1), 1025 lines; from 96
-          # columns the column tiles again
           ((1048577, 3), 0), ((70001, 5), 0), ((30001, 6), 0), ((20000, 90), 0), ((4099, 95), 0),
           ((9000, 64), 0), ((1025, 7), 0), ((20000, 100), 0), ((4099, 255), 0)]
 
@@ -190,8 +188,8 @@ def test_small_column_f32_sums_are_deterministic(device, oracle):
 @pytest.mark.parametrize("offset", [4, 1])
 @pytest.mark.parametrize("c", [8, 3, 90])
 def test_narrow_columns_offset_views(device, oracle, op, offset, c):
-    # offset 4 keeps the range 16-byte aligned, offset 1 does not (both forms
-    # load 16-byte vectors at 4-byte alignment)
+    # offset 4 keeps the range 16-byte aligned, offset 1 does not (16-byte
+    # vectors need only 4-byte alignment)
     r = 30001
     host = host_for(oracle, np.float32, offset + r * c, seed=offset, op=op)
     got = run_axis(device, op, np.float32, host, (r, c), (c, 1), offset, 0)
