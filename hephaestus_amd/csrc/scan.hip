@@ -1378,11 +1378,15 @@ __global__ __launch_bounds__(kNarrowWaves *kWave) void col_narrow_totals_kernel(
 // per launch.)
 constexpr int kNarrowCarryThreads = 1024;
 constexpr int kNarrowCarryBatch = 8;
+// Entry (tile k, column c) is totals[k * ks + c * cs]: row-major (ks = C,
+// cs = 1) for the narrow form, column-major (ks = 1, cs = tiles) for the row
+// tiles, whose carry launch read row-major totals C words apart (2^28 u32 at
+// C = 100 and 255, about 16400 tiles: 76 us per launch).
 template <typename A, typename Op>
-__global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A *totals, uint32_t C,
+__global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A *totals, uint64_t ks, uint64_t cs,
                                                                                uint64_t ntiles) {
     __shared__ A sh[kNarrowCarryThreads / kWave];
-    const uint64_t c = blockIdx.x;
+    A *col = totals + (uint64_t)blockIdx.x * cs;
     const int lane = lane_id();
     const int w = threadIdx.x / kWave;
     const uint64_t per = (ntiles + kNarrowCarryThreads - 1) / kNarrowCarryThreads;
@@ -1393,7 +1397,7 @@ __global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A
     A sum = id;
     for (uint64_t k = k0; k < k1; k += kNarrowCarryBatch) {
 #pragma unroll
-        for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? totals[(k + u) * C + c] : id;
+        for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? col[(k + u) * ks] : id;
 #pragma unroll
         for (int u = 0; u < kNarrowCarryBatch; ++u) sum = Op::combine(sum, v[u]);
     }
@@ -1414,11 +1418,11 @@ __global__ __launch_bounds__(kNarrowCarryThreads) void col_narrow_carry_kernel(A
     for (uint64_t k = k0; k < k1; k += kNarrowCarryBatch) {
         if (per > kNarrowCarryBatch) { // the range spans several batches: reload this one
 #pragma unroll
-            for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? totals[(k + u) * C + c] : id;
+            for (int u = 0; u < kNarrowCarryBatch; ++u) v[u] = k + u < k1 ? col[(k + u) * ks] : id;
         }
 #pragma unroll
         for (int u = 0; u < kNarrowCarryBatch; ++u) {
-            if (k + u < k1) totals[(k + u) * C + c] = acc;
+            if (k + u < k1) col[(k + u) * ks] = acc;
             acc = Op::combine(acc, v[u]);
         }
     }
@@ -1688,7 +1692,7 @@ __global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu
     }
     __syncthreads();
     row_group_scan<A, Op>(gtot, s.groups, C, j, owner, g);
-    if (j < C) totals[t * C + j] = gtot[(s.groups - 1) * C + j];
+    if (j < C) totals[(uint64_t)j * s.tiles + t] = gtot[(s.groups - 1) * C + j]; // column-major
 }
 
 template <typename T, typename Op, bool EXCL, bool REV, bool CARRY>
@@ -1712,7 +1716,7 @@ __global__ __launch_bounds__(kRowTileThreads) __attribute__((amdgpu_waves_per_eu
     __syncthreads();
     row_group_scan<A, Op>(gtot, s.groups, C, j, owner, g);
     if (owner) {
-        A pre = CARRY ? carries[t * C + c] : Op::template identity<A>();
+        A pre = CARRY ? carries[(uint64_t)c * s.tiles + t] : Op::template identity<A>();
         if (g > 0) pre = Op::combine(pre, gtot[j - C]);
         row_group_rescan<T, Op, EXCL, REV>(tile, n, C, c, lo, hi, pre);
     }
@@ -2437,7 +2441,7 @@ hx_status launch_narrow_dir(const ScanParams &p, uint64_t tiles, void *ws, hipSt
         hipLaunchKernelGGL((col_narrow_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, totals);
         HX_TRY(check_launch("col_narrow_totals_kernel"));
         hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3((uint32_t)p.lines), dim3(kNarrowCarryThreads), 0,
-                           stream, totals, (uint32_t)p.lines, tiles);
+                           stream, totals, p.lines, (uint64_t)1, tiles);
         HX_TRY(check_launch("col_narrow_carry_kernel"));
         hipLaunchKernelGGL((col_narrow_scan_kernel<T, Op, EXCL, REV, true>), grid, block, 0, stream, p,
                            (const A *)totals);
@@ -2495,7 +2499,7 @@ hx_status launch_rowtile_dir(const ScanParams &p, const RowTileShape &s, void *w
         hipLaunchKernelGGL((col_rowtile_totals_kernel<T, Op, REV>), grid, block, 0, stream, p, s, totals);
         HX_TRY(check_launch("col_rowtile_totals_kernel"));
         hipLaunchKernelGGL((col_narrow_carry_kernel<A, Op>), dim3(s.C), dim3(kNarrowCarryThreads), 0, stream, totals,
-                           s.C, s.tiles);
+                           (uint64_t)1, s.tiles, s.tiles);
         HX_TRY(check_launch("col_narrow_carry_kernel"));
         hipLaunchKernelGGL((col_rowtile_scan_kernel<T, Op, EXCL, REV, true>), grid, block, 0, stream, p, s,
                            (const A *)totals);
