@@ -128,6 +128,16 @@ class Workloads:
         self.offsets = oracle.geometric_offsets(self.n_seg, 300.0, seed=7)
         self.offs = device.upload(self.offsets)
         self.out_seg = device.alloc_zeroed(np.int32, self.offsets.size - 1)
+        # Axis-0 scans of narrow matrices: the row-tile look-back over C-wide
+        # carries (u32: 7 tiles of 5460 rows; f32, mirrored and exclusive:
+        # 6 tiles of 1364 rows with f64 carries).
+        self.rc = (6 * 5460 + 7, 3)
+        self.fc = (5 * 1364 + 3, 12)
+        self.xc = device.alloc_zeroed(np.uint32, self.rc[0] * self.rc[1])
+        self.yc = device.alloc_zeroed(np.uint32, self.rc[0] * self.rc[1])
+        self.xfc = device.alloc_zeroed(np.float32, self.fc[0] * self.fc[1])
+        self.yfc = device.alloc_zeroed(np.float32, self.fc[0] * self.fc[1])
+        lay_c, lay_f = Layout.c_contiguous(list(self.rc)), Layout.c_contiguous(list(self.fc))
         self.plans = [
             SCAN.prepare_scan_axis(device, hx.CumSumOp, _flat(self.xs), 0, hx.ScanDirection.Forward,
                                    _flat(self.ys), hx.ScanKind.Exclusive),
@@ -136,6 +146,10 @@ class Workloads:
             FULL.prepare_reduce_full(device, hx.SumOp, _flat(self.xr), _one(self.out_sum)),
             FULL.prepare_reduce_full(device, hx.MaxOp, _flat(self.xm), _one(self.out_max)),
             SEG.prepare_segmented_sum(device, self.vals, self.offs, self.out_seg),
+            SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(self.xc, lay_c), 0, hx.ScanDirection.Forward,
+                                   StridedView(self.yc, lay_c), hx.ScanKind.Inclusive),
+            SCAN.prepare_scan_axis(device, hx.CumSumOp, StridedView(self.xfc, lay_f), 0, hx.ScanDirection.Reverse,
+                                   StridedView(self.yfc, lay_f), hx.ScanKind.Exclusive),
         ]
 
     def refill(self, seed):
@@ -145,10 +159,13 @@ class Workloads:
         self.h_xr = o.uniform_real(self.n_sum, seed=seed + 2, lo=-1.0, hi=1.0)
         self.h_xm = o.uniform_int(self.n_sum, seed=seed + 3, lo=0, hi=2**32 - 1)
         self.h_vals = o.uniform_int(self.n_seg, seed=seed + 4, lo=-1000, hi=1000, dtype=np.int32)
+        self.h_xc = o.uniform_int(self.rc[0] * self.rc[1], seed=seed + 5, lo=0, hi=2**32 - 1)
+        self.h_xfc = o.uniform_real(self.fc[0] * self.fc[1], seed=seed + 6, lo=-1.0, hi=1.0)
         for buf, host in ((self.xs, self.h_xs), (self.xf, self.h_xf), (self.xr, self.h_xr),
-                          (self.xm, self.h_xm), (self.vals, self.h_vals)):
+                          (self.xm, self.h_xm), (self.vals, self.h_vals), (self.xc, self.h_xc),
+                          (self.xfc, self.h_xfc)):
             d.write_buffer(buf, host)
-        for buf in (self.ys, self.yf, self.out_sum, self.out_max, self.out_seg):
+        for buf in (self.ys, self.yf, self.out_sum, self.out_max, self.out_seg, self.yc, self.yfc):
             d.write_buffer(buf, np.zeros(len(buf), buf.dtype))
 
     def check(self, what):
@@ -161,6 +178,16 @@ class Workloads:
         assert d.download_owned(self.out_max)[0] == self.h_xm.max(), f"{what}: u32 max"
         assert np.array_equal(d.download_owned(self.out_seg), o.segmented_sum(self.h_vals, self.offsets)), \
             f"{what}: segmented sum"
+        r, c = self.rc
+        want = np.cumsum(self.h_xc.reshape(r, c), axis=0, dtype=np.uint32)
+        assert np.array_equal(d.download_owned(self.yc).reshape(r, c), want), f"{what}: u32 column scan"
+        r, c = self.fc
+        got = d.download_owned(self.yfc).reshape(r, c)
+        cols = self.h_xfc.reshape(r, c)
+        for j in range(c):
+            ref, absref = o.scan_sum(np.ascontiguousarray(cols[:, j]), exclusive=True, reverse=True)
+            bad, _ = o.check_f32_bound(np.ascontiguousarray(got[:, j]), ref, absref, r)
+            assert bad == 0, f"{what}: f32 column scan, column {j}"
 
 
 def test_captured_plans_replay_with_new_inputs(device, oracle):
