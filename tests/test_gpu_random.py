@@ -149,6 +149,42 @@ def test_random_axis_scan(device, oracle, shape, strides, offset, axis, dtype, o
     run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exclusive, reverse, seed)
 
 
+def _narrow_cases(seed, count, scan):
+    """Axis 0 of dense row-major matrices with 2 to 255 columns and more
+    than 1024 rows, at element offsets 0-4: the period-form sums (up to 95
+    columns), the column tiles beyond, and the row-tile scans (one pass up
+    to 24 columns, three beyond)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        c = min(255, int(np.exp(rng.uniform(np.log(2.0), np.log(256.0)))))  # log-uniform widths
+        r = int(rng.integers(1025, max(1026, (1 << 21) // c)))
+        offset = int(rng.integers(0, 5))
+        dtype = DTYPES[int(rng.integers(0, 3))]
+        if scan:
+            op = ["sum", "prod"][int(rng.integers(0, 2))]
+            extra = (bool(rng.integers(0, 2)), bool(rng.integers(0, 2)))  # exclusive, reverse
+        else:
+            op = list(OPS)[int(rng.integers(0, len(OPS)))]
+            extra = ()
+        out.append(pytest.param((r, c), (c, 1), offset, 0, dtype, op, extra, 1000 * seed + i,
+                                id=f"n{i}-{r}x{c}-off{offset}-{np.dtype(dtype).name}-{op}"))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,strides,offset,axis,dtype,op,extra,seed", _narrow_cases(13, 40, scan=False))
+def test_random_narrow_axis_reduce(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed):
+    test_random_axis_reduce(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,strides,offset,axis,dtype,op,extra,seed", _narrow_cases(14, 40, scan=True))
+def test_random_narrow_axis_scan(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed,
+                                 monkeypatch):
+    test_random_axis_scan(device, oracle, shape, strides, offset, axis, dtype, op, extra, seed, monkeypatch)
+
+
 def test_case_lists_cover_the_layouts_and_paths():
     """The fixed seeds reach every layout, both axes, narrow (at most 8
     columns) and tall (more than 4096 rows) shapes (CPU only)."""
@@ -159,6 +195,13 @@ def test_case_lists_cover_the_layouts_and_paths():
         assert {c[3] for c in cases} == {0, 1}
         assert any(c[0][1] <= 8 for c in cases) and any(c[0][0] > 4096 for c in cases)
         assert all(c[0][0] * c[0][1] <= (1 << 21) for c in cases)
+    # The narrow sweeps reach each form: period sums (<= 95 columns) and
+    # column tiles, one-pass (<= 24) and three-pass row-tile scans.
+    widths = [p.values[0][1] for p in _narrow_cases(13, 40, False)]
+    assert any(c <= 95 for c in widths) and any(c >= 96 for c in widths)
+    widths = [p.values[0][1] for p in _narrow_cases(14, 40, True)]
+    assert any(c <= 24 for c in widths) and any(c > 24 and c not in (32, 64, 128) for c in widths)
+    assert all(p.values[0][0] > 1024 for p in _narrow_cases(14, 40, True) + _narrow_cases(13, 40, False))
 
 
 # ------------------------------------------------------------ 1-D forms
