@@ -67,7 +67,12 @@ static int f_greater(float a, float b) {
     return 0;
 }
 
-/* Neumaier compensated accumulator. */
+/* Neumaier compensated accumulator.  Terms here are f32 values (or exact
+ * products of two), so a finite set of them never overflows the f64 running
+ * sum: a non-finite running sum means an infinity or a NaN among the terms,
+ * and is then the IEEE sum itself (+inf, -inf, or NaN for a NaN or for
+ * infinities of both signs).  The compensation is NaN from the first
+ * infinity on (inf - inf) and is not added then. */
 typedef struct {
     double s, c;
 } kacc;
@@ -77,7 +82,7 @@ static void kadd(kacc *k, double v) {
     else k->c += (v - t) + k->s;
     k->s = t;
 }
-static double kval(const kacc *k) { return k->s + k->c; }
+static double kval(const kacc *k) { return isfinite(k->s) ? k->s + k->c : k->s; }
 
 /* --------------------------------------------------- map-reductions
  * crates/hephaestus-rocm/src/application/linalg/norms.rs:32-490: DotMap

@@ -248,6 +248,29 @@ def test_special_values(oracle):
     assert oracle.full_max(np.zeros(0, np.uint32)) == 0
 
 
+def test_compensated_sums_of_infinities_and_nans_are_ieee_sums(oracle):
+    """Once a term is infinite or NaN the compensated sums return what IEEE
+    addition gives in any order: +inf or -inf for infinities of one sign
+    among finite terms, NaN for infinities of both signs or any NaN.  (The
+    compensation itself turns NaN at the first infinity, inf - inf; a sum
+    that added it returned NaN for a row holding +inf.)  f32 extremes that
+    overflow f32 stay finite in f64, compensated exactly."""
+    nan, inf = np.float32("nan"), np.float32("inf")
+    cases = [([inf, 2.0, 1.0], math.inf), ([1.0, -inf, 3.0, -inf], -math.inf), ([2.0, inf, -inf], None),
+             ([1.0, nan, inf], None), ([F32_MAX, F32_MAX, 1.0], 2.0 * float(F32_MAX) + 1.0),
+             ([F32_MAX, 1.0, F32_MIN], 1.0)]
+    for terms, want in cases:
+        x = np.array(terms, np.float32)
+        got = [oracle.full_sum(x)[0], oracle.rows(x, 1, x.size)[0][0], oracle.scan_sum(x)[0][-1],
+               oracle.dot(x, np.ones_like(x))[0]]
+        for g in got:
+            assert math.isnan(g) if want is None else g == want, (terms, got)
+    # Magnitudes: |inf| terms make the absolute sums +inf, with or without NaN.
+    x = np.array([1.0, -inf, 2.0], np.float32)
+    assert oracle.full_sum(x)[1] == math.inf and oracle.norm_l1(x) == math.inf
+    assert oracle.norm_l2(x) == math.inf
+
+
 def test_prologue_is_correctly_rounded_fma(oracle):
     rng = np.random.default_rng(2)
     x = rng.standard_normal(200).astype(np.float32) * np.float32(1e3)
