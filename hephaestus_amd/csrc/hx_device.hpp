@@ -76,6 +76,34 @@ template <typename V> __device__ __forceinline__ void stream_store(V v, __amdgpu
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r, (int)off, 0, kStreamStorePolicy);
 }
 
+// ------------------------------------------------------ direct LDS loads
+// ne 4-byte elements from src (dword aligned) into a 16-byte aligned LDS
+// tile with global_load_lds_dwordx4: each wave's 64 vectors of a step land
+// at its LDS base + 16 * lane, with no register round trip and no LDS write
+// instructions.  THREADS threads move up to VPT vectors each (THREADS * VPT
+// * 4 >= ne); a partial tile's last ne mod 4 elements move one per thread.
+// Every load has landed in LDS when this returns; the caller's barrier
+// publishes the tile to the block.
+constexpr int kLoadLdsNt = 2; // cache policy of the direct LDS loads: nt (streamed through)
+template <int THREADS, int VPT, typename T>
+__device__ __forceinline__ void tile_load_lds(const T *src, uint32_t ne, T *tile) {
+    static_assert(sizeof(T) == 4, "4-byte elements");
+    const uint32_t nv = ne / 4;
+    const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x & ~(uint32_t)(kWave - 1));
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const uint32_t v = threadIdx.x + (uint32_t)u * THREADS;
+        if (v < nv)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(src + 4 * v),
+                (__attribute__((address_space(3))) void *)(tile + 4 * (wbase + (uint32_t)u * THREADS)), 16, 0,
+                kLoadLdsNt);
+    }
+    const uint32_t e = 4 * nv + threadIdx.x;
+    if (e < ne) tile[e] = __builtin_nontemporal_load(src + e);
+    __builtin_amdgcn_s_waitcnt(0); // vmcnt(0): the direct loads are in LDS
+}
+
 // ----------------------------------------------------------------- lanes
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }

@@ -19,6 +19,9 @@
 //                      stride is unit).
 //   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
 //                      chunk statistics to partial planes.
+//   rows_tile_kernel   rows of 1 to 127 elements, back to back: a block stages
+//                      a tile of whole rows in LDS with 16-byte loads, then
+//                      folds a row per thread.
 //   cols_tiles_kernel  the outputs are adjacent and the reduced axis strided
 //                      (axis-0 reduction of a row-major matrix): a wave owns
 //                      256 adjacent outputs (one 16-byte load per lane per
@@ -373,7 +376,7 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
 }
 
 // Row groups of G lanes: G = 1 is a thread per row (rows of fewer than 16
-// elements), G = 4 or 16 puts 16 or 4 rows in each wave, G = 64 a wave per
+// elements; back-to-back rows of up to 127 take rows_tile_kernel), G = 4 or 16 puts 16 or 4 rows in each wave, G = 64 a wave per
 // row, G = 128 or 256 two or four waves of the block per row.  The
 // host picks G so that each lane holds at least three 16-byte vectors of its
 // row: fewer leaves a lane too little in flight, and the per-row combine then
@@ -420,6 +423,59 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
         st.template group_combine<G>();
     }
     if (gl == 0 && r < p.rows) st.write(p, r);
+}
+
+// Short dense rows (1 to kTileRowMaxCols elements, rows back to back).  A
+// thread per row (rows_kernel, G = 1) holds only a few elements and reads
+// them with 4-byte loads wherever rows start off a 16-byte boundary, so
+// the launch is bound by lanes and waves, not bytes; groups of 4 lanes
+// (16 elements and more) leave lanes idle in partly filled trips.  Here a
+// block stages a tile of whole rows in LDS with 16-byte direct loads (every
+// wave load moves 1 KiB of contiguous input), then thread i folds rows i,
+// i + 256, ... of the tile out of LDS, elements in index order, and writes
+// their outputs (adjacent lanes, adjacent rows).  Rows of even length are
+// read as 8- or 16-byte LDS vectors: lanes C words apart would otherwise
+// share banks.  Over 2^28 f32 (sum, max, argmax), microseconds per launch,
+// lane groups -> tiles: 1: 865 -> 385; 2: 578 -> 269; 3: 451 -> 257;
+// 12: 275 -> 189; 20: 235 -> 184; 64: 183 -> 163-178; 80: 215 -> 167-171;
+// 96: 185 -> 164-178.  At 128 the lane groups hold 167 us while the tiles'
+// argmax (one 64-bit compare per element on a quarter of the threads)
+// takes 184.
+constexpr uint32_t kRowsTileElems = 8192;
+constexpr uint64_t kTileRowMaxCols = 127;
+
+template <typename T, bool AFFINE, int FLAGS>
+__global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t tile_rows) {
+    __shared__ __attribute__((aligned(16))) T tile[kRowsTileElems];
+    const uint32_t C = (uint32_t)p.cols;
+    const uint64_t r0 = p.row0 + (uint64_t)xcd_contiguous(blockIdx.x, gridDim.x) * tile_rows;
+    const uint32_t n = p.rows - r0 < tile_rows ? (uint32_t)(p.rows - r0) : tile_rows;
+    tile_load_lds<kBlock, kRowsTileElems / 4 / kBlock>((const T *)p.base + (p.offset + r0 * C), n * C, tile);
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < n; r += kBlock) {
+        Stats<T, FLAGS> st;
+        const T *row = tile + r * C;
+        if (C % 4 == 0) {
+            using V = typename Vec4<T>::type;
+            for (uint32_t j = 0; j < C; j += 4) {
+                const V x = *(const V *)(row + j);
+                st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
+                st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
+                st.visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), j + 2);
+                st.visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), j + 3);
+            }
+        } else if (C % 2 == 0) {
+            typedef T V2 __attribute__((ext_vector_type(2)));
+            for (uint32_t j = 0; j < C; j += 2) {
+                const V2 x = *(const V2 *)(row + j);
+                st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
+                st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
+            }
+        } else {
+            for (uint32_t j = 0; j < C; ++j) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), j);
+        }
+        st.write(p, r0 + r);
+    }
 }
 
 // Statistics of lines [j0, j1) of the 64*V adjacent outputs from o0 (V per
@@ -732,6 +788,8 @@ struct Shape {
     bool period = false; // cols_period_kernel over residues mod P of 1 KiB blocks
     uint32_t P = 1, waves = 0;
     bool block = false; // cols_block_kernel: one launch, no partials
+    bool tile = false;  // rows_tile_kernel: tiles of tile_rows short rows
+    uint32_t tile_rows = 0;
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
     uint64_t groups = 0, chunk = 0;
@@ -794,6 +852,12 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         }
     } else {
         s.vec = p.col_stride == 1 && base % 4 == 0;
+        if (p.cols >= 1 && p.cols <= kTileRowMaxCols && (p.col_stride == 1 || p.cols == 1) &&
+            p.row_stride == (int64_t)p.cols && base % 4 == 0) {
+            s.tile = true;
+            s.tile_rows = (kRowsTileElems / (uint32_t)p.cols) & ~3u;
+            return s;
+        }
         s.G = row_group_lanes(p.cols, s.vec);
         if (p.rows < kRowTargetWaves / 2 && p.cols >= 2 * kMinRowChunk) {
             k = ceil_div(kRowTargetWaves, p.rows);
@@ -872,6 +936,18 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
                                    s.chunk, s.nchunks, s.groups);
         }
         HX_TRY(check_launch("cols_tiles_kernel"));
+    } else if (s.tile) {
+        // Batches of whole tiles below 2^32 work-items per launch.
+        const uint64_t max_blocks = 0xFFFFFFFFull / kBlock;
+        const uint64_t blocks = ceil_div(p.rows, (uint64_t)s.tile_rows);
+        RowParams q = p;
+        for (uint64_t b0 = 0; b0 < blocks; b0 += max_blocks) {
+            q.row0 = b0 * s.tile_rows;
+            const dim3 grid((uint32_t)std::min<uint64_t>(max_blocks, blocks - b0)), block(kBlock);
+            hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS>), grid, block, 0, stream, q, s.tile_rows);
+            HX_TRY(check_launch("rows_tile_kernel"));
+        }
+        return HX_OK;
     } else if (split) {
         const uint64_t blocks = ceil_div(p.rows * s.nchunks, kBlock / kWave);
         if (blocks > 0x7FFFFFFFull) return fail(HX_ERR_DISPATCH_FAILED, "axis reduction exceeds the grid range");

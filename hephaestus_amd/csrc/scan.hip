@@ -1534,7 +1534,6 @@ void col_narrow_scan_kernel(ScanParams p, const typename ColAcc<T>::type *carrie
 constexpr int kRowTileThreads = 512;
 constexpr uint32_t kRowTileElems = 16384;
 constexpr int kRowTileVecsPerThread = (int)(kRowTileElems / 4 / kRowTileThreads);
-constexpr int kLoadLdsNt = 2; // cache policy of the direct LDS loads: nt (streamed through)
 
 struct RowTileShape {
     uint64_t R = 0, tiles = 0;
@@ -1568,27 +1567,11 @@ __device__ __forceinline__ void row_tile_span(const RowTileShape &s, uint64_t t,
 }
 
 // ne elements from src (4-byte aligned) straight into the 16-byte aligned LDS
-// tile with global_load_lds_dwordx4: each wave's 64 vectors of a step land
-// at its LDS base + 16 * lane, with no register round trip and no LDS write
+// tile (tile_load_lds): no register round trip and no LDS write
 // instructions (2^28 u32 scans, 2-4% faster than loads into registers and
-// 16-byte LDS writes: C = 4 437 -> 422 us, C = 24 514 -> 502).  A partial
-// tile's last ne mod 4 elements move one by one.  Every load has landed in
-// LDS when this returns; the caller's barrier publishes them to the block.
+// 16-byte LDS writes: C = 4 437 -> 422 us, C = 24 514 -> 502).
 template <typename T> __device__ __forceinline__ void row_tile_load(const T *src, uint32_t ne, T *tile) {
-    const uint32_t nv = ne / 4;
-    const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x & ~(uint32_t)(kWave - 1));
-#pragma unroll
-    for (int u = 0; u < kRowTileVecsPerThread; ++u) {
-        const uint32_t v = threadIdx.x + (uint32_t)u * kRowTileThreads;
-        if (v < nv)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(src + 4 * v),
-                (__attribute__((address_space(3))) void *)(tile + 4 * (wbase + (uint32_t)u * kRowTileThreads)), 16, 0,
-                kLoadLdsNt);
-    }
-    const uint32_t e = 4 * nv + threadIdx.x;
-    if (e < ne) tile[e] = __builtin_nontemporal_load(src + e);
-    __builtin_amdgcn_s_waitcnt(0); // vmcnt(0): the direct loads are in LDS
+    tile_load_lds<kRowTileThreads, kRowTileVecsPerThread>(src, ne, tile);
 }
 
 template <typename T> __device__ __forceinline__ void row_tile_store(const T *tile, uint32_t ne, T *dst) {

@@ -204,6 +204,53 @@ def test_split_f32_sums_are_deterministic(device, oracle, r, c):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+# Short dense rows along axis 1 (1 to 127 elements a row, rows back to
+# back): tiles of (8192 // C) & ~3 whole rows staged in LDS, a row per
+# thread.  Row counts give several tiles and a ragged last one; offsets 1-3
+# start the matrix off a 16-byte boundary.  (128, 300) is the first length
+# past the tiles (lane groups again).
+SHORT_ROWS = [(1, 3 * 8192 + 5, 0), (2, 3 * 4096 + 1, 1), (3, 2 * 2728 + 7, 2), (4, 5 * 2048 + 3, 3),
+              (5, 2 * 1636 + 1, 0), (6, 3000, 1), (7, 5000, 2), (8, 2049, 0), (12, 1366, 3), (15, 2 * 544 + 9, 1),
+              (16, 1000, 0), (33, 3 * 248 + 5, 1), (64, 3 * 128 + 1, 0), (100, 2 * 80 + 3, 2), (127, 3 * 64 + 1, 3),
+              (128, 300, 1)]
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+@pytest.mark.parametrize("c,rows,offset", SHORT_ROWS)
+def test_short_row_axis_reduce(device, oracle, c, rows, offset, dtype, op):
+    host = host_for(oracle, dtype, offset + rows * c + 3, seed=7 * c + rows, op=op)
+    got = run_axis(device, op, dtype, host, (rows, c), (c, 1), offset, 1)
+    check(oracle, op, dtype, got, lines_of(host, (rows, c), (c, 1), offset, 1))
+
+
+def test_single_column_rows_of_any_column_stride(device, oracle):
+    """[N, 1] views reduced along axis 1: the column stride of a one-element
+    row is never used, so every stride takes the short-row tiles."""
+    rows = 3 * 8192 + 11
+    host = oracle.normal(rows + 5, seed=3)
+    for strides in [(1, 1), (1, 5), (1, 0), (1, -3)]:
+        got = run_axis(device, "max", np.float32, host, (rows, 1), strides, 2, 1)
+        assert np.array_equal(got.view(np.uint32), host[2:2 + rows].view(np.uint32))
+
+
+@pytest.mark.parametrize("c", [1, 2, 3, 5, 8, 15, 24, 64, 127])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_fused_short_rows_many_tiles(device, oracle, c, offset):
+    rows = 3 * ((8192 // c) & ~3) + 77
+    host = oracle.normal(offset + rows * c, seed=c + 40 * offset)
+    s_ref, a_ref, m_ref, i_ref = oracle.rows(host[offset:], rows, c, prologue=(0.5, 0.25))
+    buf = device.upload(host)
+    s = device.alloc_zeroed(np.float32, rows)
+    m = device.alloc_zeroed(np.float32, rows)
+    i = device.alloc_zeroed(np.uint32, rows)
+    AXIS.reduce_rows_fused(device, buf, rows, c, c, offset, (0.5, 0.25), s, m, i)
+    assert np.array_equal(device.download_owned(i), i_ref)
+    assert np.array_equal(device.download_owned(m).view(np.uint32), m_ref.view(np.uint32))
+    bound = np.array([f32_bound(c, a) for a in a_ref])
+    assert np.all(np.abs(device.download_owned(s).astype(np.float64) - s_ref) <= bound)
+
+
 @pytest.mark.parametrize("subset", ["sum+max+argmax", "sum", "argmax"])
 def test_fused_rows_with_few_long_rows(device, oracle, subset):
     rows, cols = 3, (1 << 20) + 12

@@ -342,7 +342,7 @@ def test_rows_fused_f32(device, oracle, rows, cols, ld, offset):
 # 256 lanes, about four 16-byte vectors per lane), with 67 rows so the last
 # block of the 4- and 16-lane forms is partly empty, and starts off 16-byte
 # boundaries (offset 1, row stride cols + 1).
-@pytest.mark.parametrize("cols", [1, 2, 3, 15, 16, 17, 63, 64, 65, 255, 256, 257, 1023, 1024, 1025,
+@pytest.mark.parametrize("cols", [1, 2, 3, 15, 16, 17, 63, 64, 65, 127, 128, 255, 256, 257, 1023, 1024, 1025,
                                   2047, 2048, 2049, 4095, 4096, 4097, 8191])
 @pytest.mark.parametrize("aligned", [True, False])
 def test_rows_fused_across_group_sizes(device, oracle, cols, aligned):
@@ -419,7 +419,8 @@ def _special_rows(rng, rows, cols):
     return x
 
 
-@pytest.mark.parametrize("rows,cols", [(96, 4096), (48, 16384), (60, 1000), (64, 64), (6, 70001)])
+@pytest.mark.parametrize("rows,cols", [(96, 4096), (48, 16384), (60, 1000), (64, 64), (6, 70001), (9000, 3),
+                                       (20000, 1), (5000, 8)])
 @pytest.mark.parametrize("prologue", [None, (0.5, 0.25)])
 def test_rows_special_values(device, oracle, rows, cols, prologue):
     """Max and argmax bit-exact with the oracle on NaNs, signed zeros,
