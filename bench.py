@@ -51,7 +51,7 @@ PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOADS = ("scan_u32", "sum_f32", "sum_f32_2_20", "rows_f32", "segmented_i32", "scan_f32_2_30",
              "segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
              "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32", "colscan_rowtile_wide_u32",
-             "colsum_period_f32")
+             "colsum_period_f32", "rows_short_f32")
 # Dominant kernel of each workload (substring of its name in rocprofv3 output).
 KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", "sum_f32_2_20": "full_reduce_kernel<",
              "rows_f32": "rows_kernel", "segmented_i32": "segmented_sum_kernel",
@@ -60,7 +60,7 @@ KERNEL_OF = {"scan_u32": "scan_tiles_kernel", "sum_f32": "full_reduce_kernel<", 
              "colsum_f32": "cols_tiles_kernel", "colscan_u32": "col_lookback_kernel",
              "colscan_narrow_u32": "col_narrow_scan_kernel", "segmented_long_i32": "segmented_sum_kernel",
              "colscan_rowtile_u32": "col_rowtile_lookback_kernel", "colscan_rowtile_wide_u32": "col_rowtile_scan_kernel",
-             "colsum_period_f32": "cols_period_kernel"}
+             "colsum_period_f32": "cols_period_kernel", "rows_short_f32": "rows_tile_kernel"}
 
 
 def log(msg: str) -> None:
@@ -638,6 +638,30 @@ def bench_colsum_period_f32(hx, dev, args):
     return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
 
 
+def bench_rows_short_f32(hx, dev, args):
+    """The fused row reduce (sum, max and argmax of fmaf(.5, x, .25) per
+    row, cfg3's statistics) over 2^28 f32 in back-to-back rows of 1, 3, 12
+    and 100 elements (the LDS row tiles); "ms" is their mean."""
+    n = 1 << 28
+    x = dev.alloc_uninitialized(np.float32, n)
+    dev.fill_uniform_real(x, seed=7, lo=-1.0, hi=1.0)
+    per, nbytes = {}, []
+    for c in (1, 3, 12, 100):
+        rows = n // c
+        s = dev.alloc_uninitialized(np.float32, rows)
+        m = dev.alloc_uninitialized(np.float32, rows)
+        i = dev.alloc_uninitialized(np.uint32, rows)
+        plan = hx.RocmAxisReductionOps().prepare_reduce_rows_fused(dev, x, rows, c, prologue=(0.5, 0.25), out_sum=s,
+                                                                   out_max=m, out_argmax=i)
+        per[c] = time_plan(dev, plan.dispatch, args.steps, args.warmup)
+        nbytes.append(4 * rows * c + 12 * rows)
+        plan.destroy()
+        for b in (s, m, i):
+            b.free()
+        log(f"rows_short_f32: {c} elements a row {per[c]:.4f} ms/launch")
+    return {"n": n, "ms": statistics.mean(per.values()), "bytes": statistics.mean(nbytes)}
+
+
 def bench_segmented_long_i32(hx, dev, args):
     """Segmented sums of 2^27 i32 values with geometric segment lengths of
     mean 3000, 10^5, 10^6 and 10^7 (long segments: tiles without a segment
@@ -1109,7 +1133,7 @@ def main() -> int:
         extra = {}
         for name in ("segmented_short_i32", "copy_u32", "dot_f32", "axpy_f32", "colsum_f32", "colscan_u32",
                      "colscan_narrow_u32", "segmented_long_i32", "colscan_rowtile_u32",
-                     "colscan_rowtile_wide_u32", "colsum_period_f32"):
+                     "colscan_rowtile_wide_u32", "colsum_period_f32", "rows_short_f32"):
             r = globals()[f"bench_{name}"](hx, dev, args)
             g = gbs(r["bytes"], r["ms"])
             extra[name] = {"value": round(g, 1), "unit": "GB/s", "ms_per_launch": round(r["ms"], 5),

@@ -2208,7 +2208,22 @@ ColLbShape col_lb_shape(const ScanArgs &a) {
 // 1048576 x 256 0.46 against 0.71; 65536 x 4096 0.35 against 0.54; f32
 // 65536 x 4096 0.48 against 0.56).
 constexpr uint64_t kSinglePassMinLines = 256;
-bool column_single_pass(const ScanArgs &a) { return column_mode(a) && a.lines >= kSinglePassMinLines; }
+// Many short lines: a scan of at most kColShortMaxLen steps whose chunked
+// form needs one chunk over at least kColShortMinGroups line groups reads and
+// writes each element once in col_scan_kernel, with no carries and no
+// look-back.  The single pass's tiles hold 240 steps, so at 4 steps a
+// sixteenth of its waves had data: u32 [4, 2^24] along axis 0 took 760 us
+// single-pass and takes 85 this way ([16, 2^22] 207 -> 131, [64, 2^20] 109
+// -> 100).  Longer lines keep the single pass ([240, 2^20]: 373 us against
+// 435), and so do fewer groups, which leave the chip too few waves for
+// serial steps ([32, 2^16]: 5.3 us against 7.5).
+constexpr uint64_t kColShortMaxLen = 64;
+constexpr uint64_t kColShortMinGroups = 1024;
+bool column_single_pass(const ScanArgs &a) {
+    if (!column_mode(a) || a.lines < kSinglePassMinLines) return false;
+    const ColShape s = column_shape(a);
+    return !(s.nchunks == 1 && a.len <= kColShortMaxLen && s.groups >= kColShortMinGroups);
+}
 
 uint64_t column_bytes(const ScanArgs &a) {
     const ColShape s = column_shape(a);

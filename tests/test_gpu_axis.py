@@ -368,6 +368,57 @@ def test_column_scan(device, oracle, shape, dtype, op, reverse, kind):
                     seed=r * 7 + c)
 
 
+# Many short lines in the column layout (lines adjacent, steps far apart):
+# up to 64 steps over at least 1024 line groups take one read-and-write pass
+# with no carries.  Axis 0 of row-major [L, M] with vector lanes (M a
+# multiple of 4) and scalar lanes, and axis 1 of a column-major [M, 3].
+# Expected values: numpy's wrapped integer scans, and for f32 sums an f64
+# scan with the usual bound.
+SHORT_COLUMN_SCANS = [((4, 1 << 20), (1 << 20, 1), 0), ((3, (1 << 18) + 1), ((1 << 18) + 1, 1), 0),
+                      ((32, 1 << 18), (1 << 18, 1), 0), (((1 << 18) + 3, 3), (1, (1 << 18) + 3), 1)]
+
+
+@pytest.mark.parametrize("kind", ["inclusive", "exclusive"])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("op,dtype", [("sum", np.uint32), ("sum", np.int32), ("prod", np.uint32),
+                                      ("sum", np.float32)])
+@pytest.mark.parametrize("shape,strides,axis", SHORT_COLUMN_SCANS)
+def test_column_scan_of_many_short_lines(device, oracle, shape, strides, axis, op, dtype, reverse, kind):
+    size = shape[0] * shape[1]
+    if dtype == np.float32:
+        host = oracle.uniform_real(size, 41, -1.0, 1.0)
+    elif dtype == np.int32:
+        host = oracle.uniform_int(size, 42, -1000, 1000, dtype=np.int32)
+    else:
+        host = oracle.uniform_int(size, 43, 0, 2**32 - 1)
+    buf = device.upload(host)
+    out = device.upload(np.full(size, 7, dtype))
+    lay = Layout.try_new(list(shape), list(strides), 0)
+    SCAN.scan_axis_into(device, hx.CumSumOp if op == "sum" else hx.CumProdOp, StridedView(buf, lay), axis,
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanKind.Exclusive if kind == "exclusive" else hx.ScanKind.Inclusive)
+    lines = lines_of(host, shape, strides, 0, axis).T  # steps along axis 0
+    got = lines_of(device.download_owned(out), shape, strides, 0, axis).T
+    v = lines[::-1] if reverse else lines
+    acc = np.float64 if dtype == np.float32 else np.uint32
+    with np.errstate(over="ignore"):
+        want = np.cumsum(v, axis=0, dtype=acc) if op == "sum" else np.cumprod(v, axis=0, dtype=acc)
+        ab = np.cumsum(np.abs(v.astype(np.float64)), axis=0)
+    if kind == "exclusive":
+        first = np.zeros if op == "sum" else np.ones
+        want = np.concatenate([first((1, v.shape[1]), acc), want[:-1]])
+        ab = np.concatenate([np.zeros((1, v.shape[1])), ab[:-1]])
+    if reverse:
+        want, ab = want[::-1], ab[::-1]
+    if dtype == np.float32:
+        n = lines.shape[0]
+        bad, worst = oracle.check_f32_bound(np.ascontiguousarray(got).ravel(), np.ascontiguousarray(want).ravel(),
+                                            np.ascontiguousarray(ab).ravel(), n)
+        assert bad == 0, worst
+    else:
+        assert np.array_equal(got.view(np.uint32), want.astype(np.uint32))
+
+
 # Row-wise (axis 1) scans of many lines: a line of up to 32768 elements is one
 # tile of the smallest shape that holds it (256, 512, 1024, 2048, 4096, 8192,
 # 16384 or 32768 elements), longer lines chain 32768-element tiles.  Lengths either
