@@ -22,6 +22,13 @@ bool same_shape(const hx_layout &a, const hx_layout &b) {
     return true;
 }
 
+// Same strides over every extent above one (the shapes already match).
+bool same_strides(const hx_layout &a, const hx_layout &b) {
+    for (uint32_t d = 0; d < a.rank; ++d)
+        if (a.shape[d] > 1 && a.strides[d] != b.strides[d]) return false;
+    return true;
+}
+
 // One operand of a map-reduction: layout checks of the reference's
 // StridedOperand (leto Layout validation) against its buffer.
 hx_status check_operand(const void *buf, uint64_t buf_len, const hx_layout *l, const char *what, uint64_t *n) {
@@ -58,13 +65,23 @@ hx_status plan_map(hx_map_reduction map, hx_dtype dtype, const void *a, uint64_t
     args->b_layout = map == HX_MAP_DOT ? *b_layout : *a_layout;
     args->n = n;
     // The order of a sum does not change its value here (exact integer
-    // arithmetic; f64 accumulation of exact f32 products), so dense views
-    // are streamed with vector loads.  For a dot both operands must be dense
-    // row-major; their vector loads need only 4-byte alignment, so the two
-    // may start at any element offsets.
-    bool flat = layout_is_c_contiguous(*a_layout);
-    if (map == HX_MAP_DOT) flat = flat && layout_is_c_contiguous(*b_layout);
+    // arithmetic; f64 accumulation of exact f32 products), so views that
+    // cover a dense range (transposed or reversed) are streamed as that range
+    // with vector loads, from its lowest element.  A dot pairs a[k] with b[k]
+    // along both ranges, which pairs the right elements when both views have
+    // the same strides; their vector loads need only 4-byte alignment, so
+    // the two may start at any element offsets.
+    uint64_t a0 = 0, b0 = 0;
+    bool flat = layout_covers_dense_range(*a_layout, &a0);
+    if (map == HX_MAP_DOT)
+        flat = flat && same_strides(*a_layout, *b_layout) && layout_covers_dense_range(*b_layout, &b0);
+    else
+        b0 = a0;
     args->flat = flat;
+    if (flat) {
+        args->a_layout.offset = a0;
+        args->b_layout.offset = b0;
+    }
     args->out = out;
     return HX_OK;
 }

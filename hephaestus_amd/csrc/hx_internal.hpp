@@ -141,6 +141,10 @@ bool layout_is_c_contiguous(const hx_layout &l);
 // Strides are a permutation of a dense row-major stride set (all positive):
 // the view covers exactly [offset, offset + size) in some order.
 bool layout_is_permuted_dense(const hx_layout &l);
+// The view covers exactly [*first, *first + size) in some order: with the
+// signs of its strides dropped (each reversed dimension read from its other
+// end) it is a permuted dense view.  *first is the lowest element it reaches.
+bool layout_covers_dense_range(const hx_layout &l, uint64_t *first);
 // A view as rows: `rows` rows of `cols` elements, element c of a row at
 // c * cstride, the row index split over up to three outer dimensions
 // (innermost first) from the view's offset.  Each dimension also carries a

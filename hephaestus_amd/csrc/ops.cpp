@@ -100,9 +100,11 @@ hx_status plan_full(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
     a->n = n;
     // Sum, product, min, max and mean are order-independent here (exact
     // integer / key arithmetic, f64 accumulation), so any view that covers a
-    // dense block of memory is streamed as that block.
-    a->flat = layout_is_c_contiguous(*in_layout) || layout_is_permuted_dense(*in_layout);
-    a->flat_offset = in_layout->offset;
+    // dense block of memory, transposed or reversed, is streamed as that
+    // block from its lowest element.
+    uint64_t first = in_layout->offset;
+    a->flat = layout_covers_dense_range(*in_layout, &first);
+    a->flat_offset = first;
     a->affine = affine;
     a->a = pa;
     a->b = pb;
@@ -165,6 +167,21 @@ hx_status plan_axis(hx_op op, hx_dtype dtype, const void *in, uint64_t in_buf_le
     a->in_offset = in_layout->offset;
     a->out_stride = out_layout->strides[1 - axis];
     a->out_offset = out_layout->offset;
+    // Reversed dimensions are read from their other end, so lines and
+    // neighbouring outputs ascend in memory (unit strides take the vector
+    // paths).  The reduced axis only where the order of its elements cannot
+    // show: argmax reports the first index of the maximum.  The outer axis
+    // always, together with the outputs, which keep pairing with their lines.
+    if (op != HX_OP_ARGMAX && axis_len > 1 && a->in_axis_stride < 0) {
+        a->in_offset += (axis_len - 1) * a->in_axis_stride;
+        a->in_axis_stride = -a->in_axis_stride;
+    }
+    if (out_len > 1 && a->in_outer_stride < 0) {
+        a->in_offset += (out_len - 1) * a->in_outer_stride;
+        a->out_offset += (out_len - 1) * a->out_stride;
+        a->in_outer_stride = -a->in_outer_stride;
+        a->out_stride = -a->out_stride;
+    }
     return HX_OK;
 }
 
@@ -257,6 +274,16 @@ hx_status plan_scan(hx_op op, hx_dtype dtype, hx_scan_kind kind, hx_scan_directi
     a->out_line_stride = out_layout->rank == 2 ? out_layout->strides[1 - axis] : 0;
     a->in_offset = in_layout->offset;
     a->out_offset = out_layout->offset;
+    if (len > 1 && a->in_elem_stride < 0 && a->out_elem_stride < 0) {
+        // Lines that run backwards in both operands: the same elements in
+        // the same order are the mirrored lines scanned the other way, and
+        // those read and write with ascending addresses.
+        a->in_offset += (len - 1) * a->in_elem_stride;
+        a->out_offset += (len - 1) * a->out_elem_stride;
+        a->in_elem_stride = -a->in_elem_stride;
+        a->out_elem_stride = -a->out_elem_stride;
+        a->reverse = !a->reverse;
+    }
     return HX_OK;
 }
 

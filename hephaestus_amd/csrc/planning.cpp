@@ -151,6 +151,21 @@ bool layout_is_permuted_dense(const hx_layout &l) {
     return true;
 }
 
+bool layout_covers_dense_range(const hx_layout &l, uint64_t *first) {
+    hx_layout m = l;
+    int64_t lo = (int64_t)l.offset;
+    for (uint32_t d = 0; d < l.rank; ++d)
+        if (l.strides[d] < 0 && l.shape[d] > 1) {
+            lo += (int64_t)(l.shape[d] - 1) * l.strides[d];
+            m.strides[d] = -l.strides[d];
+        }
+    if (lo < 0) return false;
+    m.offset = (uint64_t)lo;
+    if (!layout_is_c_contiguous(m) && !layout_is_permuted_dense(m)) return false;
+    *first = m.offset;
+    return true;
+}
+
 } // namespace hx
 
 using namespace hx;

@@ -142,6 +142,11 @@ def test_axis_reduce_transposed_and_reversed_views(device, oracle, op):
     shape, strides, offset = (r, c), (c, -1), c - 1
     got = run_axis(device, op, np.float32, host, shape, strides, offset, 0)
     check(oracle, op, np.float32, got, lines_of(host, shape, strides, offset, 0))
+    # rows read from their ends (axis 1 at stride -1): every op but argmax
+    # reads them forwards; then rows in reverse order as well
+    for strides, offset in (((c, -1), c - 1), ((-c, -1), r * c - 1)):
+        got = run_axis(device, op, np.float32, host, (r, c), strides, offset, 1)
+        check(oracle, op, np.float32, got, lines_of(host, (r, c), strides, offset, 1))
 
 
 # Axis-0 reductions of small matrices (at most 1024 lines and 2^20 elements,

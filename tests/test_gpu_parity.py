@@ -145,6 +145,11 @@ ROW_VIEWS = [
     ([9, 5, 4], [20, 1, 5], 3),                # rank-3 permutation, offset
     ([20, 30], [2, 60], 1),                    # inner stride 60
     ([33, 17], [-1, 40], 32),                  # negative inner stride
+    # dense ranges read backwards: streamed flat from the lowest element
+    # (argmax keeps the row walk, whose indices follow the view)
+    ([5000], [-1], 4999),                      # reversed
+    ([40, 33], [-33, -1], 1319),               # fully reversed
+    ([33, 40], [-1, 33], 32),                  # reversed transpose
 ]
 
 
@@ -185,6 +190,41 @@ def test_full_reduce_row_walks(device, oracle, view, dtype):
     want = oracle.full_argmax(sel)
     assert int(device.download_owned(idx)[0]) == want
     assert device.download_owned(val)[0] == sel[want]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.uint32, np.int32])
+def test_full_reduce_of_a_long_reversed_view(device, oracle, dtype):
+    """A reversed dense view of 2^20 + 3 elements (many blocks, a ragged
+    end) reduced by every kind: the flat stream from its lowest element."""
+    n = (1 << 20) + 3
+    host = inputs(oracle, dtype, n + 2, seed=23)
+    if dtype != np.float32:
+        host = (host % 977).astype(dtype)
+    lay = Layout.try_new([n], [-1], n)  # elements n .. 1 of the buffer
+    sel = np.ascontiguousarray(host[1:n + 1][::-1])
+    buf = device.upload(host)
+    one = Layout.c_contiguous([1])
+    out = device.alloc_zeroed(dtype, 1)
+
+    def run(op, prologue=None):
+        FULL.reduce_full_into(device, op, StridedView(buf, lay), StridedView(out, one), prologue=prologue)
+        return device.download_owned(out)[0]
+
+    if dtype == np.float32:
+        ref, ab = oracle.full_sum(sel)
+        assert abs(float(run(hx.SumOp)) - ref) <= f32_bound(n, ab)
+        assert abs(float(run(hx.MeanOp)) - ref / n) <= f32_bound(n, ab) / n + EPS * abs(ref / n)
+        ref, ab = oracle.full_sum(sel, prologue=(0.5, 0.25))
+        assert abs(float(run(hx.SumOp, (0.5, 0.25))) - ref) <= f32_bound(n, ab)
+    else:
+        assert run(hx.SumOp) == oracle.full_sum(sel)
+        assert run(hx.ProdOp) == oracle.full_prod(sel)
+    assert run(hx.MaxOp) == oracle.full_max(sel)
+    assert run(hx.MinOp) == oracle.full_min(sel)
+    idx = device.alloc_zeroed(np.uint32, 1)
+    val = device.alloc_zeroed(dtype, 1)
+    FULL.argmax_full_into(device, StridedView(buf, lay), idx, val)
+    assert int(device.download_owned(idx)[0]) == oracle.full_argmax(sel)
 
 
 def test_full_reduce_row_walk_with_prologue(device, oracle):
@@ -545,6 +585,51 @@ def test_reverse_scans_of_rank2_lines(device, oracle, shape):
                         StridedView(out, lay))
     want = np.cumsum(x.reshape(r, c)[:, ::-1], axis=1, dtype=np.int32)[:, ::-1]
     assert np.array_equal(device.download_owned(out).reshape(r, c), want)
+
+
+@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
+@pytest.mark.parametrize("direction", [hx.ScanDirection.Forward, hx.ScanDirection.Reverse])
+def test_scans_of_views_read_backwards(device, oracle, kind, direction):
+    """Lines that run backwards in both operands (stride -1): the planner
+    scans the mirrored lines the other way, with ascending addresses, which
+    must equal the view's own scan.  A long 1-D line (look-back tiles, a
+    ragged end) of u32 and f32, and every row of a matrix read from its
+    end."""
+    excl = kind == hx.ScanKind.Exclusive
+    rev = direction == hx.ScanDirection.Reverse
+    n = (1 << 21) + 5
+    x = oracle.uniform_int(n + 1, seed=51, lo=0, hi=2**32 - 1)
+    buf = device.upload(x)
+    out = device.upload(np.full(n + 1, 7, np.uint32))
+    lay = Layout.try_new([n], [-1], n)  # elements n .. 1
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 0, direction, StridedView(out, lay), kind)
+    got = device.download_owned(out)
+    assert got[0] == 7
+    assert np.array_equal(got[1:][::-1], oracle.scan_sum(np.ascontiguousarray(x[1:][::-1]), exclusive=excl,
+                                                           reverse=rev))
+    xf = oracle.uniform_real(n + 1, seed=52, lo=-1.0, hi=1.0)
+    fb = device.upload(xf)
+    fo = device.upload(np.full(n + 1, 7.0, np.float32))
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(fb, lay), 0, direction, StridedView(fo, lay), kind)
+    ref, ab = oracle.scan_sum(np.ascontiguousarray(xf[1:][::-1]), exclusive=excl, reverse=rev)
+    gf = device.download_owned(fo)
+    assert gf[0] == 7.0
+    bad, worst = oracle.check_f32_bound(np.ascontiguousarray(gf[1:][::-1]), ref, ab, n)
+    assert bad == 0, worst
+    r, c = 300, 1001
+    xi = oracle.uniform_int(r * c, seed=53, lo=-1000, hi=1000, dtype=np.int32)
+    ib = device.upload(xi)
+    ob = device.alloc_zeroed(np.int32, r * c)
+    rl = Layout.try_new([r, c], [c, -1], c - 1)  # every row read from its end
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(ib, rl), 1, direction, StridedView(ob, rl), kind)
+    m = xi.reshape(r, c)[:, ::-1]
+    v = m[:, ::-1] if rev else m
+    want = np.cumsum(v, axis=1, dtype=np.int32)
+    if excl:
+        want = np.concatenate([np.zeros((r, 1), np.int32), want[:, :-1]], axis=1)
+    if rev:
+        want = want[:, ::-1]
+    assert np.array_equal(device.download_owned(ob).reshape(r, c)[:, ::-1], want)
 
 
 @pytest.mark.parametrize("n", SCAN_EDGES)

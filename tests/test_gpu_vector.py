@@ -257,6 +257,12 @@ PAIR_VIEWS = [
     ([40, 33], [-40, 1], 1563, [33, 1], 0),          # reversed rows
     ([500], [3], 4, [-2, ], 1200),                   # stride 3 . stride -2
     ([300, 3], [7, 1], 1, [3, 1], 0),                # rows of 3
+    # views that cover a dense range, reversed or transposed, with the same
+    # strides: streamed as flat ranges from their lowest elements
+    ([5000], [-1], 4999, [-1], 9999),                # both reversed
+    ([40, 33], [-33, -1], 1319, [-33, -1], 6319),    # both fully reversed
+    ([33, 40], [-1, 33], 32, [-1, 33], 2032),        # reversed transpose
+    ([5000], [-1], 4999, [1], 7),                    # reversed . forward: element walk
 ]
 
 
