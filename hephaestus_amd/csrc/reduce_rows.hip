@@ -19,7 +19,8 @@
 //                      stride is unit).
 //   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
 //                      chunk statistics to partial planes.
-//   rows_tile_kernel   rows of 1 to 127 elements, back to back: a block stages
+//   rows_tile_kernel   rows of 1 to 127 elements, back to back or a little
+//                      apart: a block stages
 //                      a tile of whole rows in LDS with 16-byte loads, then
 //                      folds a row per thread.
 //   cols_tiles_kernel  the outputs are adjacent and the reduced axis strided
@@ -425,7 +426,8 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     if (gl == 0 && r < p.rows) st.write(p, r);
 }
 
-// Short dense rows (1 to kTileRowMaxCols elements, rows back to back).  A
+// Short rows (1 to kTileRowMaxCols elements at unit stride, rows back to back
+// or a little apart: tile_rows_fit).  A
 // thread per row (rows_kernel, G = 1) holds only a few elements and reads
 // them with 4-byte loads wherever rows start off a 16-byte boundary, so
 // the launch is bound by lanes and waves, not bytes; groups of 4 lanes
@@ -433,9 +435,10 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
 // block stages a tile of whole rows in LDS with 16-byte direct loads (every
 // wave load moves 1 KiB of contiguous input), then thread i folds rows i,
 // i + 256, ... of the tile out of LDS, elements in index order, and writes
-// their outputs (adjacent lanes, adjacent rows).  Rows of even length are
-// read as 8- or 16-byte LDS vectors: lanes C words apart would otherwise
-// share banks.  Over 2^28 f32 (sum, max, argmax), microseconds per launch,
+// their outputs (adjacent lanes, adjacent rows).  Padded rows load their
+// padding with them.  Rows whose length and start distance are even are
+// read as 8- or 16-byte LDS vectors: lanes an even number of words apart
+// would otherwise share banks.  Over 2^28 f32 (sum, max, argmax), microseconds per launch,
 // lane groups -> tiles: 1: 865 -> 385; 2: 578 -> 269; 3: 451 -> 257;
 // 12: 275 -> 189; 20: 235 -> 184; 64: 183 -> 163-178; 80: 215 -> 167-171;
 // 96: 185 -> 164-178.  At 128 the lane groups hold 167 us while the tiles'
@@ -448,14 +451,17 @@ template <typename T, bool AFFINE, int FLAGS>
 __global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t tile_rows) {
     __shared__ __attribute__((aligned(16))) T tile[kRowsTileElems];
     const uint32_t C = (uint32_t)p.cols;
+    const uint32_t L = (uint32_t)p.row_stride; // C, or more for padded rows
     const uint64_t r0 = p.row0 + (uint64_t)xcd_contiguous(blockIdx.x, gridDim.x) * tile_rows;
     const uint32_t n = p.rows - r0 < tile_rows ? (uint32_t)(p.rows - r0) : tile_rows;
-    tile_load_lds<kBlock, kRowsTileElems / 4 / kBlock>((const T *)p.base + (p.offset + r0 * C), n * C, tile);
+    tile_load_lds<kBlock, kRowsTileElems / 4 / kBlock>((const T *)p.base + (p.offset + r0 * L), (n - 1) * L + C,
+                                                       tile);
     __syncthreads();
+    const uint32_t w = C | L; // vector LDS reads where every row start and length allow them
     for (uint32_t r = threadIdx.x; r < n; r += kBlock) {
         Stats<T, FLAGS> st;
-        const T *row = tile + r * C;
-        if (C % 4 == 0) {
+        const T *row = tile + r * L;
+        if (w % 4 == 0) {
             using V = typename Vec4<T>::type;
             for (uint32_t j = 0; j < C; j += 4) {
                 const V x = *(const V *)(row + j);
@@ -464,7 +470,7 @@ __global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t
                 st.visit(prologue<T, AFFINE>((T)x.z, p.a, p.b), j + 2);
                 st.visit(prologue<T, AFFINE>((T)x.w, p.a, p.b), j + 3);
             }
-        } else if (C % 2 == 0) {
+        } else if (w % 2 == 0) {
             typedef T V2 __attribute__((ext_vector_type(2)));
             for (uint32_t j = 0; j < C; j += 2) {
                 const V2 x = *(const V2 *)(row + j);
@@ -816,6 +822,18 @@ int row_group_lanes(uint64_t cols, bool vec) {
     return 1;
 }
 
+// Rows for rows_tile_kernel: 1 to kTileRowMaxCols elements at unit stride,
+// row starts L >= C elements apart with at least 64 rows to a tile.  The
+// tile loads the whole span, padding included, so L stays within twice the
+// row or within 32 elements (128 bytes, the line any row read fetches).
+bool tile_rows_fit(const RowParams &p, uintptr_t base) {
+    const uint64_t C = p.cols;
+    if (C < 1 || C > kTileRowMaxCols || (p.col_stride != 1 && C != 1) || base % 4 != 0) return false;
+    if (p.row_stride < (int64_t)C) return false;
+    const uint64_t L = (uint64_t)p.row_stride;
+    return L <= kTileRowMaxCols && (L <= 2 * C || L <= 32);
+}
+
 Shape plan_shape(const RowParams &p, bool cols_layout) {
     Shape s;
     s.cols = cols_layout;
@@ -852,10 +870,9 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         }
     } else {
         s.vec = p.col_stride == 1 && base % 4 == 0;
-        if (p.cols >= 1 && p.cols <= kTileRowMaxCols && (p.col_stride == 1 || p.cols == 1) &&
-            p.row_stride == (int64_t)p.cols && base % 4 == 0) {
+        if (tile_rows_fit(p, base)) {
             s.tile = true;
-            s.tile_rows = (kRowsTileElems / (uint32_t)p.cols) & ~3u;
+            s.tile_rows = (uint32_t)(((kRowsTileElems - p.cols) / (uint64_t)p.row_stride + 1) & ~3ull);
             return s;
         }
         s.G = row_group_lanes(p.cols, s.vec);

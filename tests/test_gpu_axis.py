@@ -229,6 +229,24 @@ def test_short_row_axis_reduce(device, oracle, c, rows, offset, dtype, op):
     check(oracle, op, dtype, got, lines_of(host, (rows, c), (c, 1), offset, 1))
 
 
+# Short rows a little apart (row stride L > C, within 2C or 32 elements):
+# the tiles load the padding with the rows, ((8192 - C) // L + 1) & ~3 rows a
+# tile.  Odd and even distances (scalar and vector LDS reads), one-element
+# rows of a wider matrix, and past the limits (L = 40 for 4 elements, L =
+# 130 for 100): the lane groups again.
+PADDED_ROWS = [(4, 5, 5000, 1), (3, 4, 7000, 0), (1, 7, 9000, 2), (12, 16, 2000, 3), (2, 32, 1000, 1),
+               (7, 9, 3000, 0), (100, 120, 300, 2), (4, 40, 500, 0), (100, 130, 100, 1)]
+
+
+@pytest.mark.parametrize("op", ["sum", "max", "argmax", "prod"])
+@pytest.mark.parametrize("dtype", [np.float32, np.int32])
+@pytest.mark.parametrize("c,ld,rows,offset", PADDED_ROWS)
+def test_padded_short_row_axis_reduce(device, oracle, c, ld, rows, offset, dtype, op):
+    host = host_for(oracle, dtype, offset + rows * ld + 3, seed=11 * c + ld, op=op)
+    got = run_axis(device, op, dtype, host, (rows, c), (ld, 1), offset, 1)
+    check(oracle, op, dtype, got, lines_of(host, (rows, c), (ld, 1), offset, 1))
+
+
 def test_single_column_rows_of_any_column_stride(device, oracle):
     """[N, 1] views reduced along axis 1: the column stride of a one-element
     row is never used, so every stride takes the short-row tiles."""
