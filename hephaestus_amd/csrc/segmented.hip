@@ -23,7 +23,7 @@
 //      prefix, so a look-back almost always stops at the nearest
 //      predecessor.
 //
-// Segments averaging at most 14.5 values take a segment-parallel path instead
+// Segments averaging at most 29 values take a segment-parallel path instead
 // (seg_short_kernel below), which needs no look-back.
 //
 // Integer addition mod 2^32 is associative, so every output is bit-exact.
@@ -629,18 +629,18 @@ __global__ __launch_bounds__(kBlock) void seg_tile_map_kernel(SegParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Short segments (mean length n / S of at most kShortSpan / 512).  Cut by
+// Short segments (mean length n / S of at most kShortSpan / 256).  Cut by
 // elements, a tile of 8192 values holds hundreds to thousands of segment
 // ends, and segmented_sum_kernel spends its time ranking them in rounds of
 // kSlots.  Here the work is cut by SEGMENTS instead: block b takes the
-// SB = 256 * J consecutive segments [s0, s1), whose values are the one
+// SB <= 256 * J consecutive segments [s0, s1), whose values are the one
 // contiguous span [off(s0), off(s1)).  The block loads the span's first
 // chunk (up to 8192 values, 16-byte loads from the 4-aligned element at or
 // below off(s0)), writes the chunk's inclusive prefix sums to LDS, and
 // thread t forms out[s] = P(end - 1) - P(start - 1) for s = s0 + t + 256 j:
 // offsets are read and outputs written coalesced, and no segment needs a
-// carry from another block.  J is the largest (up to 16) whose expected
-// span, 256 J n / S values, stays within kShortSpan.
+// carry from another block.  SB is the most segments (up to 16 per thread)
+// whose expected span, SB n / S values, stays within kShortSpan.
 //
 // A span longer than one chunk (a long segment among short ones) is not
 // walked by one block: the block stores the first chunk's part of each of
@@ -790,7 +790,7 @@ __device__ __forceinline__ void short_chunk_range(uint64_t base, uint64_t l, uin
 template <int J>
 __global__ __launch_bounds__(kShortThreads) void seg_short_kernel(ShortParams p) {
     __shared__ __align__(16) uint32_t s_p[kShortChunk];
-    constexpr uint64_t SB = (uint64_t)J * kShortThreads;
+    const uint64_t SB = p.seg_per_block; // at most J * kShortThreads
     const int lane = lane_id();
     const uint64_t s0 = (uint64_t)blockIdx.x * SB;
     const uint64_t s1 = s0 + SB < p.segments ? s0 + SB : p.segments;
@@ -972,25 +972,40 @@ __global__ void validate_offsets_kernel(const uint32_t *offsets, uint64_t count,
 
 namespace {
 
-// Taken when a block can hold two segments per thread, mean n / S up to
-// kShortSpan / 512 = 14.5: at 2^27 values it beats the element tiles from
-// 4.5x (mean 1) to 1.4x (mean 12); at one segment per thread the two paths
-// tie (mean 16: 141 us each).
+// Segments per block: as many as keep the block's expected span (SB n / S
+// values) within kShortSpan, at most kShortMaxJ per thread, rounded down to
+// whole groups of 256 (one segment per thread each) when that keeps 80% of
+// them.  A partly filled last group costs a whole j step; too few segments
+// leave blocks short of work.  2^27 values, us with the exact count against
+// whole groups: mean 2 236 / 237, 4 156 / 149, 8 129 / 131, 14 120 / 115,
+// 16 115 / 149 (464 segments against 256), 20 115 / 128, 24 114 / 107,
+// 28 114 / 105.
+uint64_t short_seg_per_block(const SegmentedArgs &a) {
+    const uint64_t cap = (uint64_t)kShortMaxJ * kShortThreads;
+    if (a.n == 0) return cap;
+    uint64_t sb = kShortSpan * a.num_segments / a.n;
+    if (sb > cap) sb = cap;
+    const uint64_t whole = sb / kShortThreads * kShortThreads;
+    return 5 * whole >= 4 * sb ? whole : sb;
+}
+
+// Taken when a block holds at least one segment per thread, mean n / S up
+// to kShortSpan / 256 = 29.  At 2^27 values it beats the element tiles from
+// 4.5x (mean 1) to 1.4x (mean 12), and at 2^26 values, mean 16 / 20 / 24 /
+// 28, 83.5 / 75.8 / 72.8 / 68.9 us on the tiles against 60.6 / 59.3 / 56.1
+// / 54.7 here.  From mean 30 the tiles hold their own (67 us either way;
+// mean 40 59 against 61).
 bool short_path(const SegmentedArgs &a) {
-    return a.num_segments > 0 && a.n > 0 && 2 * (uint64_t)kShortThreads * a.n <= kShortSpan * a.num_segments;
+    return a.num_segments > 0 && a.n > 0 && short_seg_per_block(a) >= (uint64_t)kShortThreads;
 }
 
-// Segments per thread: the largest J up to kShortMaxJ that keeps a block's
-// expected span (256 J n / S values) within kShortSpan.
+// Segments per thread: J covers the block's segments, the last group of 256
+// partly filled.
 int short_j(const SegmentedArgs &a) {
-    int j = 1;
-    while (j < kShortMaxJ && (uint64_t)(j + 1) * kShortThreads * a.n <= kShortSpan * a.num_segments) ++j;
-    return j;
+    return (int)ceil_div(short_seg_per_block(a), (uint64_t)kShortThreads);
 }
 
-uint64_t short_blocks(const SegmentedArgs &a) {
-    return ceil_div(a.num_segments, (uint64_t)short_j(a) * kShortThreads);
-}
+uint64_t short_blocks(const SegmentedArgs &a) { return ceil_div(a.num_segments, short_seg_per_block(a)); }
 
 // Every block defers at most ceil((span + 3) / chunk) - 1 < (span + 3) / chunk
 // chunks, and the spans of sorted offsets add up to n.
@@ -1016,7 +1031,7 @@ hx_status launch_short(const SegmentedArgs &a, void *ws, uint64_t ws_bytes, hipS
     p.segments = a.num_segments;
     p.out = (uint32_t *)a.out;
     const int j = short_j(a);
-    p.seg_per_block = (uint64_t)j * kShortThreads;
+    p.seg_per_block = short_seg_per_block(a);
     p.work_count = (unsigned long long *)ws;
     p.work = (uint2 *)((char *)ws + kWorkHeader);
     p.work_cap = short_work_cap(a);

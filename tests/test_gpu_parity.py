@@ -878,11 +878,13 @@ def test_segmented_sum_geometric(device, oracle, n, mean):
     assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
 
 
-# Mean segment lengths up to 14.5 take the segment-parallel path: blocks of
-# 256 * J consecutive segments (J = 16, 16, 14, 7, 3 at means 0.5 to 8), a
-# span of up to 8192 values per block, longer spans deferred to a chunk
-# worklist; means 16 and 17 take the element-tile path beside them.
-@pytest.mark.parametrize("mean", [0.5, 1.0, 2.0, 4.0, 8.0, 16.0, 17.0])
+# Mean segment lengths up to 29 take the segment-parallel path: blocks of
+# up to 7424 S / n consecutive segments (at most 4096, 16 a thread), whole
+# groups of 256 where that keeps 80% of them (3584, 1792, 768, 512 at
+# means 2, 4, 8, 14, 256 at 28) and a partly filled last group otherwise (464
+# at 16, 371 at 20); a span of up to 8192 values per block, longer spans
+# deferred to a chunk worklist; means 31 and 40 take the element-tile path.
+@pytest.mark.parametrize("mean", [0.5, 1.0, 2.0, 4.0, 8.0, 14.0, 16.0, 20.0, 28.0, 31.0, 40.0])
 @pytest.mark.parametrize("dtype", [np.int32, np.uint32])
 def test_segmented_sum_short_segments(device, oracle, mean, dtype):
     n = (1 << 20) + 13
@@ -918,7 +920,7 @@ SHORT_LONG_CASES = [
 def test_segmented_sum_short_with_long_segments(device, oracle, n, mean, longs):
     x = oracle.uniform_int(n, seed=n % 1000, lo=-1 << 30, hi=1 << 30, dtype=np.int32)
     off = _short_with_long(n, mean, longs, seed=n % 997)
-    assert 512 * n <= 7424 * (off.size - 1), "case must take the short path"
+    assert 256 * n <= 7424 * (off.size - 1), "case must take the short path"
     assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
 
 
@@ -989,8 +991,8 @@ def _crowded(n, mean, clusters, seed):
 
 
 CROWDED_CASES = [
-    ("trailing empties", [((1 << 22) + 5, 1 << 17)]),
-    ("leading empties", [(0, 1 << 17)]),
+    ("trailing empties", [((1 << 22) + 5, 1 << 16)]),
+    ("leading empties", [(0, 1 << 16)]),
     ("mid-tile run", [(3 * 8192 + 1000, 50000)]),
     ("runs at a tile edge and mid-tile", [(5 * 8192, 9000), (9 * 8192 + 77, 4097), (20 * 8192 + 5, 4095)]),
 ]
@@ -1005,7 +1007,7 @@ def test_segmented_sum_crowded_tiles(device, oracle, name, clusters):
     n = (1 << 22) + 5
     x = oracle.uniform_int(n, seed=len(name), lo=-1 << 30, hi=1 << 30, dtype=np.int32)
     off = _crowded(n, 300.0, clusters, seed=len(name))
-    assert 512 * n > 7424 * (off.size - 1), "case must take the element-tile path"
+    assert 256 * n > 7424 * (off.size - 1), "case must take the element-tile path"
     assert np.array_equal(_segmented(device, x, off), oracle.segmented_sum(x, off))
 
 
