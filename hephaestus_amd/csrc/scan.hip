@@ -1001,6 +1001,8 @@ template <typename T> struct ColIO<T, 1> {
     using A = typename ColAcc<T>::type;
     static __device__ __forceinline__ void load(const T *p, A (&x)[1]) { x[0] = (A)__builtin_nontemporal_load(p); }
     static __device__ __forceinline__ void store(T *p, const A (&y)[1]) { __builtin_nontemporal_store((T)y[0], p); }
+    static __device__ __forceinline__ void load_n(const T *p, uint32_t, A, A (&x)[1]) { load(p, x); }
+    static __device__ __forceinline__ void store_n(T *p, uint32_t, const A (&y)[1]) { store(p, y); }
 };
 template <typename T> struct ColIO<T, 4> {
     using A = typename ColAcc<T>::type;
@@ -1020,7 +1022,32 @@ template <typename T> struct ColIO<T, 4> {
         v.w = (T)y[3];
         __builtin_nontemporal_store(v, (Vt *)p);
     }
+    // The lane of a partial group (the last nv < 4 lines, when the line
+    // count is not a multiple of 4) moves its lines one by one; the others
+    // read as `ident` and are never stored.
+    static __device__ __forceinline__ void load_n(const T *p, uint32_t nv, A ident, A (&x)[4]) {
+        if (nv >= 4) {
+            load(p, x);
+            return;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) x[v] = (uint32_t)v < nv ? (A)__builtin_nontemporal_load(p + v) : ident;
+    }
+    static __device__ __forceinline__ void store_n(T *p, uint32_t nv, const A (&y)[4]) {
+        if (nv >= 4) {
+            store(p, y);
+            return;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            if ((uint32_t)v < nv) __builtin_nontemporal_store((T)y[v], p + v);
+    }
 };
+
+// Lines of this lane's group that exist (V, or fewer in the last group).
+__device__ __forceinline__ uint32_t col_valid_lines(uint64_t lines, uint64_t line0, int V) {
+    return lines - line0 < (uint64_t)V ? (uint32_t)(lines - line0) : (uint32_t)V;
+}
 
 // Wave w -> (line group g, chunk k); adjacent waves take adjacent groups of
 // the same chunk.  Returns false for lanes with no line.
@@ -1048,16 +1075,18 @@ __global__ __launch_bounds__(kBlock) void col_totals_kernel(ScanParams p, typena
     ColWork w;
     if (!col_work(p, chunk, nchunks, groups, V, &w)) return;
     const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)w.line0 * p.in_line_stride);
+    const uint32_t nv = col_valid_lines(p.lines, w.line0, V);
+    const A aid = Op::template identity<A>();
     A acc[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v) acc[v] = Op::template identity<A>();
+    for (int v = 0; v < V; ++v) acc[v] = aid;
     uint64_t i = w.i0;
     for (; i + kU <= w.i1; i += kU) {
         A x[kU][V];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const uint64_t li = REV ? p.len - 1 - (i + u) : i + u;
-            ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x[u]);
+            ColIO<T, V>::load_n(in + (int64_t)li * p.in_elem_stride, nv, aid, x[u]);
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u)
@@ -1067,12 +1096,13 @@ __global__ __launch_bounds__(kBlock) void col_totals_kernel(ScanParams p, typena
     for (; i < w.i1; ++i) {
         const uint64_t li = REV ? p.len - 1 - i : i;
         A x[V];
-        ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x);
+        ColIO<T, V>::load_n(in + (int64_t)li * p.in_elem_stride, nv, aid, x);
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[v] = Op::combine(acc[v], x[v]);
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) totals[w.k * p.lines + w.line0 + v] = acc[v];
+    for (int v = 0; v < V; ++v)
+        if ((uint32_t)v < nv) totals[w.k * p.lines + w.line0 + v] = acc[v];
 }
 
 // Exclusive scan of each line's chunk totals, in place.  A block owns 64
@@ -1115,10 +1145,11 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     if (!col_work(p, chunk, nchunks, groups, V, &w)) return;
     const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)w.line0 * p.in_line_stride);
     T *out = (T *)p.out + ((int64_t)p.out_offset + (int64_t)w.line0 * p.out_line_stride);
+    const uint32_t nv = col_valid_lines(p.lines, w.line0, V);
+    const A aid = Op::template identity<A>();
     A acc[V];
 #pragma unroll
-    for (int v = 0; v < V; ++v)
-        acc[v] = CARRY ? carries[w.k * p.lines + w.line0 + v] : Op::template identity<A>();
+    for (int v = 0; v < V; ++v) acc[v] = CARRY && (uint32_t)v < nv ? carries[w.k * p.lines + w.line0 + v] : aid;
     auto step = [&](uint64_t li, const A (&x)[V]) {
         A y[V];
 #pragma unroll
@@ -1131,7 +1162,7 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
                 y[v] = acc[v];
             }
         }
-        ColIO<T, V>::store(out + (int64_t)li * p.out_elem_stride, y);
+        ColIO<T, V>::store_n(out + (int64_t)li * p.out_elem_stride, nv, y);
     };
     uint64_t i = w.i0;
     for (; i + kU <= w.i1; i += kU) {
@@ -1139,7 +1170,7 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const uint64_t li = REV ? p.len - 1 - (i + u) : i + u;
-            ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x[u]);
+            ColIO<T, V>::load_n(in + (int64_t)li * p.in_elem_stride, nv, aid, x[u]);
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u) step(REV ? p.len - 1 - (i + u) : i + u, x[u]);
@@ -1147,7 +1178,7 @@ __global__ __launch_bounds__(kBlock) void col_scan_kernel(ScanParams p, const ty
     for (; i < w.i1; ++i) {
         const uint64_t li = REV ? p.len - 1 - i : i;
         A x[V];
-        ColIO<T, V>::load(in + (int64_t)li * p.in_elem_stride, x);
+        ColIO<T, V>::load_n(in + (int64_t)li * p.in_elem_stride, nv, aid, x);
         step(li, x);
     }
 }
@@ -1915,6 +1946,29 @@ __device__ __forceinline__ void col_store_t(T *p, const T (&y)[V]) {
     }
 }
 
+// The same for the lane of a partial group: its nv < V lines one by one,
+// the others read as `ident` and never stored.
+template <typename T, int V>
+__device__ __forceinline__ void col_load_n(const T *p, uint32_t nv, T ident, T (&x)[V]) {
+    if (V == 1 || nv >= (uint32_t)V) {
+        col_load_t<T, V>(p, x);
+        return;
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) x[v] = (uint32_t)v < nv ? __builtin_nontemporal_load(p + v) : ident;
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void col_store_n(T *p, uint32_t nv, const T (&y)[V]) {
+    if (V == 1 || nv >= (uint32_t)V) {
+        col_store_t<T, V>(p, y);
+        return;
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+        if ((uint32_t)v < nv) __builtin_nontemporal_store(y[v], p + v);
+}
+
 // Aggregate of chunk c for the V lines starting at line0, exactly as the
 // owner computes it (the decoupled fallback).
 template <typename T, typename Op, int V, bool REV>
@@ -1922,6 +1976,7 @@ __device__ void col_tile_aggregate(const ScanParams &p, uint64_t c, uint64_t lin
                                    typename ColAcc<T>::type (&agg)[V]) {
     using A = typename ColAcc<T>::type;
     const T *in = (const T *)p.in + ((int64_t)p.in_offset + (int64_t)line0 * p.in_line_stride);
+    const uint32_t nv = col_valid_lines(p.lines, line0, V);
 #pragma unroll
     for (int v = 0; v < V; ++v) agg[v] = Op::template identity<A>();
     // Rolled loops: this rare path must not add register pressure to the
@@ -1937,7 +1992,7 @@ __device__ void col_tile_aggregate(const ScanParams &p, uint64_t c, uint64_t lin
             if (i >= p.len) break;
             const uint64_t li = REV ? p.len - 1 - i : i;
             T x[V];
-            col_load_t<T, V>(in + (int64_t)li * p.in_elem_stride, x);
+            col_load_n<T, V>(in + (int64_t)li * p.in_elem_stride, nv, Op::template identity<T>(), x);
 #pragma unroll
             for (int v = 0; v < V; ++v) run[v] = Op::combine(run[v], x[v]);
         }
@@ -2075,6 +2130,7 @@ __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanPara
     const uint64_t g = tile % groups, c = tile / groups;
     const uint64_t line0 = (g * kWave + (uint64_t)lane) * V;
     const bool active = line0 < p.lines;
+    const uint32_t nv = active ? col_valid_lines(p.lines, line0, V) : 0u;
     const A aid = Op::template identity<A>();
 
     if (w == kColDataWaves) {
@@ -2106,7 +2162,7 @@ __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanPara
         if (active && i < p.len) {
             const int64_t li = (int64_t)(REV ? p.len - 1 - i : i);
             const char *row = (const char *)((const T *)p.in + (ia.base + li * p.in_elem_stride));
-            col_load_t<T, V>((const T *)(row + ia.lane_off), x[r]);
+            col_load_n<T, V>((const T *)(row + ia.lane_off), nv, tid, x[r]);
         } else {
 #pragma unroll
             for (int v = 0; v < V; ++v) x[r][v] = tid;
@@ -2143,7 +2199,7 @@ __global__ __launch_bounds__(kColWaves *kWave) void col_lookback_kernel(ScanPara
         }
         const int64_t li = (int64_t)(REV ? p.len - 1 - i : i);
         char *row = (char *)((T *)p.out + (oa.base + li * p.out_elem_stride));
-        col_store_t<T, V>((T *)(row + oa.lane_off), y);
+        col_store_n<T, V>((T *)(row + oa.lane_off), nv, y);
     }
 }
 
@@ -2165,9 +2221,11 @@ ColShape column_shape(const ScanArgs &a) {
     const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
     // A lane's four adjacent lines are one 16-byte vector per step; the
     // vectors need only 4-byte alignment (Vec4A4), so any element stride and
-    // start qualify.
-    const bool vec = a.in_line_stride == 1 && a.out_line_stride == 1 && a.lines % 4 == 0 && ibase % 4 == 0 &&
-                     obase % 4 == 0;
+    // start qualify.  When the line count is not a multiple of 4, the lane
+    // of the last group moves its 1-3 lines one by one (col_load_n,
+    // ColIO::load_n): u32 [8191, 8191] and [1023, 65537] along axis 0 took
+    // 189 and 293 us with one line per lane everywhere.
+    const bool vec = a.in_line_stride == 1 && a.out_line_stride == 1 && ibase % 4 == 0 && obase % 4 == 0;
     s.V = vec ? 4 : 1;
     s.groups = ceil_div(a.lines, (uint64_t)kWave * s.V);
     uint64_t k = 1;

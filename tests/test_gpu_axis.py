@@ -365,8 +365,10 @@ def run_column_scan(device, oracle, op, dtype, shape, strides, offset, axis, exc
 
 
 # (rows, cols) scanned along axis 0.  Single-pass look-back (256 lines and
-# more): vector lanes over many chunks, scalar lanes, one tile only.
-COLUMN_SHAPES = [(4099, 1000), (3001, 999), (20, 256),
+# more): 16-byte lanes over many chunks, line counts 3, 1 and 2 past a
+# multiple of 4 (the last group's lane moves its lines one by one), one tile
+# only; the chunked form with 130 lines.
+COLUMN_SHAPES = [(4099, 1000), (3001, 999), (3001, 1001), (2000, 1022), (20, 256), (5000, 130),
                  # narrow columns (32, 64, 128): the dense range scanned with
                  # strided lane scans, one or many chunks
                  (4097, 32), (1000, 64), (3001, 128),

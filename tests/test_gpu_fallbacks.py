@@ -114,7 +114,8 @@ def test_scans_under_forced_fallbacks(device, oracle, limits, exclusive, reverse
 
 
 # Single-pass column look-back (256 lines and more): integer and f32 lines,
-# sums and products, forward and reverse.
+# sums and products, forward and reverse; 1003 lines leave a partial last
+# group, whose rebuilt aggregates read only the lines that exist.
 @pytest.mark.parametrize("limits", FORCED)
 @pytest.mark.parametrize("dtype", [np.uint32, np.float32])
 @pytest.mark.parametrize("reverse", [False, True])
@@ -122,6 +123,7 @@ def test_column_lookback_scans_under_forced_fallbacks(device, oracle, limits, dt
     with wait_limits(*limits):
         run_column_scan(device, oracle, "sum", dtype, (4099, 1000), (1000, 1), 0, 0, False, reverse, seed=17)
         run_column_scan(device, oracle, "prod", dtype, (3001, 512), (512, 1), 0, 0, True, reverse, seed=19)
+        run_column_scan(device, oracle, "sum", dtype, (2001, 1003), (1003, 1), 0, 0, True, reverse, seed=21)
 
 
 # Row-tile column look-back (axis 0 of dense matrices with 2 to 255 columns
