@@ -188,15 +188,16 @@ struct ScanParams {
     uint32_t tag;        // this launch's status tag
     uint32_t spin_limit; // polls before a waiter computes a missing value (64)
     uint64_t tile0;      // tile of block 0 (tile kernels launched in batches)
+    uint32_t head;       // tile lines: elements [0, head) of the line are virtual (scan_out_head)
 };
 
 // The four elements of one lane and step (logical index e..e+3 of the
-// line), identity past the end.
+// line), identity past the end and before p.head.
 template <typename T, bool VEC, bool REV, bool NT>
 __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t ib, uint64_t e, T ident,
                                       T (&v)[4]) {
     if constexpr (VEC && !REV) {
-        if (e + 3 < p.len) {
+        if (e + 3 < p.len && e >= p.head) {
             using V = typename Vec4A4<T>::type;
             const V q = load_a4<NT>((const V *)(in + ib + (int64_t)e));
             v[0] = (T)q.x;
@@ -210,7 +211,7 @@ __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t 
     for (int c = 0; c < 4; ++c) {
         const uint64_t i = e + c;
         const uint64_t li = REV ? (p.len - 1 - i) : i;
-        v[c] = (i < p.len) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
+        v[c] = (i < p.len && i >= p.head) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
     }
 }
 
@@ -559,7 +560,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     // Wave index made explicitly uniform so lane offsets stay 32-bit.
     const uint32_t lane_off =
         ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * (uint32_t)sizeof(T);
-    const bool full = VEC && (tin + 1) * kTileElems <= p.len;
+    const bool full = VEC && (tin + 1) * kTileElems <= p.len && (tin > 0 || p.head == 0);
     // Reverse: the tile's lowest physical element, and the mirrored offset.
     const int64_t rev_tile = REV ? (int64_t)(p.len - (tin + 1) * kTileElems) : 0;
     const uint32_t rev_off = (uint32_t)(kTileElems - 4) * (uint32_t)sizeof(T) - lane_off;
@@ -714,7 +715,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
             r[c] = tile_carry.apply(Op::combine(wave_excl, xv));
         }
         if constexpr (VEC && !REV) {
-            if (e + 3 < p.len) {
+            if (e + 3 < p.len && e >= p.head) {
                 using V = typename Vec4A4<T>::type;
                 V v;
                 v.x = r[0];
@@ -729,7 +730,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         for (int c = 0; c < 4; ++c) {
             const uint64_t i = e + c;
             const uint64_t li = REV ? (p.len - 1 - i) : i;
-            if (i < p.len) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
+            if (i < p.len && i >= p.head) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
         }
     }
 }
@@ -2618,6 +2619,22 @@ hx_status launch_rowtile(const ScanArgs &a, const ScanParams &p, void *ws, uint6
                      : launch_rowtile_dir<T, Op, false, false>(p, s, ws, stream);
 }
 
+// Forward 16-byte scans of lines longer than one tile whose outputs start
+// off a 16-byte boundary (by the same amount on every line) run on virtual
+// lines `head` elements longer, the virtual elements [0, head) read as the
+// identity and never stored, so that every whole tile's 16-byte stores are
+// aligned.  2^28 u32 exclusive scan, output at element offset 1: 418-424 us
+// with tiles on the line's own grid, against 331 aligned.  Misaligned loads
+// cost nothing measurable (input offset 1, output aligned: 333 us).
+uint32_t scan_out_head(const ScanArgs &a) {
+    if (a.reverse || a.len <= 32768 || a.in_elem_stride != 1 || a.out_elem_stride != 1) return 0;
+    if (a.lines > 1 && a.out_line_stride % 4 != 0) return 0;
+    const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
+    const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
+    if (ibase % 4 != 0 || obase % 4 != 0) return 0;
+    return (uint32_t)((obase / 4) % 4);
+}
+
 uint64_t scan_bytes(const ScanArgs &a) {
     if (short_line_scan(a)) return 0;
     if (narrow_column_scan(a)) return narrow_bytes(a);
@@ -2627,7 +2644,8 @@ uint64_t scan_bytes(const ScanArgs &a) {
         return kLookbackOffset + c.chunks * c.lpad * (a.dtype == HX_DTYPE_F32 ? 16u : 8u);
     }
     if (column_mode(a)) return column_bytes(a);
-    const uint64_t tpl = ceil_div(a.len, tile_shape(a.len).elems());
+    const uint64_t vlen = a.len + scan_out_head(a);
+    const uint64_t tpl = ceil_div(vlen, tile_shape(vlen).elems());
     // Lines of one tile never look back and publish no status.
     if (tpl <= 1) return kLookbackOffset;
     return kLookbackOffset + status_bytes(tpl * a.lines) + status_bytes(ceil_div(tpl, kSuper) * a.lines);
@@ -2680,6 +2698,18 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
     }
     if (ws_bytes < scan_bytes(a))
         return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
+    const uint32_t head = scan_out_head(a);
+    if (head != 0) {
+        // Virtual lines head elements longer, both offsets moved back by
+        // head: virtual element head is each line's first.
+        p.head = head;
+        p.len = a.len + head;
+        p.in_offset = a.in_offset - head;
+        p.out_offset = a.out_offset - head;
+        p.tiles_per_line = ceil_div(p.len, shape.elems());
+        p.total_tiles = p.tiles_per_line * a.lines;
+        p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);
+    }
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
     const bool contiguous = a.in_elem_stride == 1 && a.out_elem_stride == 1;
     const uintptr_t ibase = (uintptr_t)((const T *)a.in + a.in_offset);

@@ -83,15 +83,16 @@ def test_full_and_map_reductions_bit_identical_under_forced_fallbacks(device, or
     assert abs(float(got) - ref) <= 2 * (n - 1).bit_length() * 2.0**-23 * ab + abs(ref) * 2.0**-24
 
 
-def _scan(device, x, exclusive, reverse):
+def _scan(device, x, exclusive, reverse, out_off=0):
     n = x.size
     buf = device.upload(x)
-    out = device.alloc_zeroed(x.dtype, n)
+    out = device.alloc_zeroed(x.dtype, n + out_off)
     lay = Layout.c_contiguous([n])
     SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, lay), 0,
-                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward, StridedView(out, lay),
+                        hx.ScanDirection.Reverse if reverse else hx.ScanDirection.Forward,
+                        StridedView(out, Layout.try_new([n], [1], out_off)),
                         hx.ScanKind.Exclusive if exclusive else hx.ScanKind.Inclusive)
-    return device.download_owned(out)
+    return device.download_owned(out)[out_off:]
 
 
 # 2^21 + 5 u32: 65 tiles of 32768, so both look-back levels (superblocks of
@@ -106,7 +107,11 @@ def test_scans_under_forced_fallbacks(device, oracle, limits, exclusive, reverse
     with wait_limits(*limits):
         forced_u = _scan(device, xu, exclusive, reverse)
         forced_f = _scan(device, xf, exclusive, reverse)
+        # an output off a 16-byte boundary: forward lines then run on the
+        # output's grid, their first tile partial (rebuilt with its bounds)
+        shifted_u = _scan(device, xu, exclusive, reverse, out_off=3)
     assert np.array_equal(forced_u, normal_u)
+    assert np.array_equal(shifted_u, normal_u)
     assert np.array_equal(forced_u, oracle.scan_sum(xu, exclusive=exclusive, reverse=reverse))
     ref, ab = oracle.scan_sum(xf, exclusive=exclusive, reverse=reverse)
     bad, worst = oracle.check_f32_bound(forced_f, ref, ab, n)
