@@ -196,14 +196,23 @@ struct ScanParams {
 template <typename T, bool VEC, bool REV, bool NT>
 __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t ib, uint64_t e, T ident,
                                       T (&v)[4]) {
-    if constexpr (VEC && !REV) {
+    if constexpr (VEC) {
         if (e + 3 < p.len && e >= p.head) {
             using V = typename Vec4A4<T>::type;
-            const V q = load_a4<NT>((const V *)(in + ib + (int64_t)e));
-            v[0] = (T)q.x;
-            v[1] = (T)q.y;
-            v[2] = (T)q.z;
-            v[3] = (T)q.w;
+            if constexpr (REV) {
+                // Logical e..e+3 are physical len-1-e down to len-4-e.
+                const V q = load_a4<NT>((const V *)(in + ib + (int64_t)(p.len - 4 - e)));
+                v[0] = (T)q.w;
+                v[1] = (T)q.z;
+                v[2] = (T)q.y;
+                v[3] = (T)q.x;
+            } else {
+                const V q = load_a4<NT>((const V *)(in + ib + (int64_t)e));
+                v[0] = (T)q.x;
+                v[1] = (T)q.y;
+                v[2] = (T)q.z;
+                v[3] = (T)q.w;
+            }
             return;
         }
     }
@@ -714,15 +723,23 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
             asm volatile("" : "+v"(xv));
             r[c] = tile_carry.apply(Op::combine(wave_excl, xv));
         }
-        if constexpr (VEC && !REV) {
+        if constexpr (VEC) {
             if (e + 3 < p.len && e >= p.head) {
                 using V = typename Vec4A4<T>::type;
                 V v;
-                v.x = r[0];
-                v.y = r[1];
-                v.z = r[2];
-                v.w = r[3];
-                store_a4<NT>(v, (V *)(out + ob + (int64_t)e));
+                if constexpr (REV) {
+                    v.w = r[0];
+                    v.z = r[1];
+                    v.y = r[2];
+                    v.x = r[3];
+                    store_a4<NT>(v, (V *)(out + ob + (int64_t)(p.len - 4 - e)));
+                } else {
+                    v.x = r[0];
+                    v.y = r[1];
+                    v.z = r[2];
+                    v.w = r[3];
+                    store_a4<NT>(v, (V *)(out + ob + (int64_t)e));
+                }
                 continue;
             }
         }
@@ -2619,20 +2636,27 @@ hx_status launch_rowtile(const ScanArgs &a, const ScanParams &p, void *ws, uint6
                      : launch_rowtile_dir<T, Op, false, false>(p, s, ws, stream);
 }
 
-// Forward 16-byte scans of lines longer than one tile whose outputs start
-// off a 16-byte boundary (by the same amount on every line) run on virtual
-// lines `head` elements longer, the virtual elements [0, head) read as the
-// identity and never stored, so that every whole tile's 16-byte stores are
-// aligned.  2^28 u32 exclusive scan, output at element offset 1: 418-424 us
-// with tiles on the line's own grid, against 331 aligned.  Misaligned loads
+// 16-byte scans of lines longer than one tile whose outputs start off a
+// 128-byte boundary (by the same amount on every line) run on virtual lines
+// `head` (1-31) elements longer, the virtual elements (logical [0, head))
+// read as the identity and never stored, so that every whole tile's stores
+// cover whole lines.  Forward lines gain the elements before their start
+// (both offsets move back by head), reverse lines after their end (logical
+// index 0 is the physical last).  2^28 u32 exclusive scans, output (and
+// input) at element offset k, tiles on the line's own grid: k = 0, 16, 32:
+// 331-336 us; k = 1, 4, 5, 8: 418-428.  Stores that start 16 or 32 bytes
+// into a 64-byte segment cost as much as unaligned ones; misaligned loads
 // cost nothing measurable (input offset 1, output aligned: 333 us).
+constexpr uint64_t kOutGrid = 32; // elements: 128 bytes
 uint32_t scan_out_head(const ScanArgs &a) {
-    if (a.reverse || a.len <= 32768 || a.in_elem_stride != 1 || a.out_elem_stride != 1) return 0;
-    if (a.lines > 1 && a.out_line_stride % 4 != 0) return 0;
+    if (a.len <= 32768 || a.in_elem_stride != 1 || a.out_elem_stride != 1) return 0;
+    if (a.lines > 1 && a.out_line_stride % (int64_t)kOutGrid != 0) return 0;
     const uintptr_t ibase = (uintptr_t)a.in + 4u * a.in_offset; // every element type is 4 bytes
     const uintptr_t obase = (uintptr_t)a.out + 4u * a.out_offset;
     if (ibase % 4 != 0 || obase % 4 != 0) return 0;
-    return (uint32_t)((obase / 4) % 4);
+    const uint64_t first = obase / 4;
+    return a.reverse ? (uint32_t)((kOutGrid - (first + a.len) % kOutGrid) % kOutGrid)
+                     : (uint32_t)(first % kOutGrid);
 }
 
 uint64_t scan_bytes(const ScanArgs &a) {
@@ -2700,12 +2724,15 @@ hx_status launch_op(const ScanArgs &a, void *ws, uint64_t ws_bytes, LookbackStat
         return fail(HX_ERR_DISPATCH_FAILED, "scan workspace of %llu bytes is too small", (unsigned long long)ws_bytes);
     const uint32_t head = scan_out_head(a);
     if (head != 0) {
-        // Virtual lines head elements longer, both offsets moved back by
-        // head: virtual element head is each line's first.
+        // Virtual lines head elements longer.  Forward: both offsets move
+        // back by head, so virtual element head is each line's first.
+        // Reverse: the virtual elements lie past the line's physical end.
         p.head = head;
         p.len = a.len + head;
-        p.in_offset = a.in_offset - head;
-        p.out_offset = a.out_offset - head;
+        if (!a.reverse) {
+            p.in_offset = a.in_offset - head;
+            p.out_offset = a.out_offset - head;
+        }
         p.tiles_per_line = ceil_div(p.len, shape.elems());
         p.total_tiles = p.tiles_per_line * a.lines;
         p.supers_per_line = ceil_div(p.tiles_per_line, kSuper);

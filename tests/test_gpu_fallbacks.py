@@ -107,8 +107,8 @@ def test_scans_under_forced_fallbacks(device, oracle, limits, exclusive, reverse
     with wait_limits(*limits):
         forced_u = _scan(device, xu, exclusive, reverse)
         forced_f = _scan(device, xf, exclusive, reverse)
-        # an output off a 16-byte boundary: forward lines then run on the
-        # output's grid, their first tile partial (rebuilt with its bounds)
+        # an output off a 16-byte boundary: lines then run on the output's
+        # grid, their first tile partial (rebuilt with its bounds)
         shifted_u = _scan(device, xu, exclusive, reverse, out_off=3)
     assert np.array_equal(forced_u, normal_u)
     assert np.array_equal(shifted_u, normal_u)

@@ -633,43 +633,48 @@ def test_scans_of_views_read_backwards(device, oracle, kind, direction):
 
 
 @pytest.mark.parametrize("dtype", [np.uint32, np.float32])
-@pytest.mark.parametrize("in_off,out_off", [(1, 1), (0, 3), (2, 1), (3, 0), (2, 2)])
-@pytest.mark.parametrize("kind", [hx.ScanKind.Inclusive, hx.ScanKind.Exclusive])
-def test_scans_of_views_off_16_byte_boundaries(device, oracle, dtype, in_off, out_off, kind):
-    """Long lines whose output starts off a 16-byte boundary run on a
-    virtual line 1-3 elements longer, tiles on the output's 16-byte grid:
-    the virtual elements are never read or stored, and every other element
-    is.  Input offsets independent of the output's; a second pass scans
-    rows whose starts share one misalignment (row stride a multiple of 4)."""
+@pytest.mark.parametrize("in_off,out_off", [(1, 1), (0, 3), (2, 1), (3, 0), (8, 8), (0, 17), (31, 5)])
+@pytest.mark.parametrize("kind,direction", [(hx.ScanKind.Inclusive, hx.ScanDirection.Forward),
+                                            (hx.ScanKind.Exclusive, hx.ScanDirection.Forward),
+                                            (hx.ScanKind.Exclusive, hx.ScanDirection.Reverse)])
+def test_scans_of_views_off_16_byte_boundaries(device, oracle, dtype, in_off, out_off, kind, direction):
+    """Long lines whose output starts off a 128-byte boundary run on a
+    virtual line 1-31 elements longer, tiles on the output's 128-byte grid:
+    the virtual elements (before a forward line, past a reverse line's end)
+    are never read or stored, and every other element is.  Input offsets
+    independent of the output's; a second pass scans rows whose starts share
+    one misalignment (row stride a multiple of 32)."""
     excl = kind == hx.ScanKind.Exclusive
+    rev = direction == hx.ScanDirection.Reverse
     n = (1 << 21) + 7
     if dtype == np.uint32:
-        x = oracle.uniform_int(n + 8, seed=61, lo=0, hi=2**32 - 1)
+        x = oracle.uniform_int(n + 32, seed=61, lo=0, hi=2**32 - 1)
     else:
-        x = oracle.uniform_real(n + 8, seed=62, lo=-1.0, hi=1.0)
+        x = oracle.uniform_real(n + 32, seed=62, lo=-1.0, hi=1.0)
     buf = device.upload(x)
-    out = device.upload(np.full(n + 8, 7, dtype))
+    out = device.upload(np.full(n + 32, 7, dtype))
     SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(buf, Layout.try_new([n], [1], in_off)), 0,
-                        hx.ScanDirection.Forward, StridedView(out, Layout.try_new([n], [1], out_off)), kind)
+                        direction, StridedView(out, Layout.try_new([n], [1], out_off)), kind)
     got = device.download_owned(out)
     assert np.all(got[:out_off] == 7) and np.all(got[out_off + n:] == 7)
     xs = np.ascontiguousarray(x[in_off:in_off + n])
     if dtype == np.uint32:
-        assert np.array_equal(got[out_off:out_off + n], oracle.scan_sum(xs, exclusive=excl))
+        assert np.array_equal(got[out_off:out_off + n], oracle.scan_sum(xs, exclusive=excl, reverse=rev))
     else:
-        ref, ab = oracle.scan_sum(xs, exclusive=excl)
+        ref, ab = oracle.scan_sum(xs, exclusive=excl, reverse=rev)
         bad, worst = oracle.check_f32_bound(np.ascontiguousarray(got[out_off:out_off + n]), ref, ab, n)
         assert bad == 0, worst
     if dtype == np.uint32:
-        r, c, ld = 3, 70001, 70004
-        xi = oracle.uniform_int(r * ld + 8, seed=63, lo=0, hi=2**32 - 1)
+        r, c, ld = 3, 70001, 70016
+        xi = oracle.uniform_int(r * ld + 32, seed=63, lo=0, hi=2**32 - 1)
         ib = device.upload(xi)
-        ob = device.upload(np.full(r * ld + 8, 7, np.uint32))
+        ob = device.upload(np.full(r * ld + 32, 7, np.uint32))
         SCAN.scan_axis_into(device, hx.CumProdOp, StridedView(ib, Layout.try_new([r, c], [ld, 1], in_off)), 1,
-                            hx.ScanDirection.Forward, StridedView(ob, Layout.try_new([r, c], [ld, 1], out_off)), kind)
+                            direction, StridedView(ob, Layout.try_new([r, c], [ld, 1], out_off)), kind)
         g = device.download_owned(ob)
         for k in range(r):
-            want = oracle.scan_prod(np.ascontiguousarray(xi[in_off + k * ld:in_off + k * ld + c]), exclusive=excl)
+            want = oracle.scan_prod(np.ascontiguousarray(xi[in_off + k * ld:in_off + k * ld + c]), exclusive=excl,
+                                    reverse=rev)
             assert np.array_equal(g[out_off + k * ld:out_off + k * ld + c], want), k
             assert np.all(g[out_off + k * ld + c:out_off + (k + 1) * ld] == 7), k
 
