@@ -129,10 +129,10 @@ class Workloads:
         self.offs = device.upload(self.offsets)
         self.out_seg = device.alloc_zeroed(np.int32, self.offsets.size - 1)
         # Axis-0 scans of narrow matrices: the row-tile look-back over C-wide
-        # carries (u32: 7 tiles of 5460 rows; f32, mirrored and exclusive:
-        # 6 tiles of 1364 rows with f64 carries).
-        self.rc = (6 * 5460 + 7, 3)
-        self.fc = (5 * 1364 + 3, 12)
+        # carries (u32: 7 tiles of 5440 rows; f32, mirrored and exclusive:
+        # 6 tiles of 1360 rows with f64 carries).
+        self.rc = (6 * 5440 + 7, 3)
+        self.fc = (5 * 1360 + 3, 12)
         self.xc = device.alloc_zeroed(np.uint32, self.rc[0] * self.rc[1])
         self.yc = device.alloc_zeroed(np.uint32, self.rc[0] * self.rc[1])
         self.xfc = device.alloc_zeroed(np.float32, self.fc[0] * self.fc[1])

@@ -207,10 +207,11 @@ def test_narrow_column_scan_with_many_tiles(device, kind, reverse):
 
 
 @pytest.mark.parametrize("kind,reverse", [("inclusive", False), ("exclusive", True)])
-@pytest.mark.parametrize("C,R,tile_rows", [(3, 3 * (1 << 24) + 5, 5460), (100, 1500007, 160)])
+@pytest.mark.parametrize("C,R,tile_rows", [(3, 3 * (1 << 24) + 5, 5440), (100, 1500007, 160)])
 def test_row_tile_column_scan_with_many_tiles(device, kind, reverse, C, R, tile_rows):
     """Row tiles along axis 0, u32, with about 9200 tiles: [3 * 2^24 + 5, 3]
-    (tiles of 5460 rows) looks back in one pass over 9219 tiles;
+    (tiles of 5440 rows, whole 128-byte lines) looks back in one pass over
+    9253 tiles;
     [1500007, 100] (tiles of 160 rows, 9376 tiles) takes three passes, and
     each thread of its carry pass owns 10 tiles (past its one-batch case).
     Every element is 1 except x[r0][c0] = 1000, as in the narrow case
