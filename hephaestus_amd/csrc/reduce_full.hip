@@ -35,17 +35,19 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 768; // 16-byte partial slots: 12 KiB of status words
 
-// The grid: a function of n only (so is the combination tree), one block
-// per 4096 elements (two trips) up to 768 blocks, three per CU on 256 CUs.
-// At 2^28 f32 a sweep over 512..4096 blocks and 1/2/4 loads in flight per
-// lane put 768 blocks with two 16-byte non-temporal loads per lane at 7.08
-// TB/s (151.6 us), ahead of 1024 blocks (6.9) and 8192 (3.9).  Small,
-// launch-bound operands gain from fewer blocks (fewer partials to gather):
-// 2^20 elements, per-launch median, 512 / 256 / 128 / 64 blocks: f32 4.96 /
-// 4.12 / 3.88 / 4.31 us, u32 4.51 / 3.72 / 4.06 / 4.36.
-constexpr uint64_t kElemsPerBlock = 4096;
-inline uint32_t full_reduce_blocks(uint64_t n) {
-    uint64_t blocks = ceil_div(n, kElemsPerBlock);
+// The grid: a function of n and the element type only (so is the
+// combination tree), one block per 4096 integer or 8192 f32 elements up to
+// 768 blocks, three per CU on 256 CUs.  At 2^28 f32 a sweep over 512..4096
+// blocks and 1/2/4 loads in flight per lane put 768 blocks with two 16-byte
+// non-temporal loads per lane at 7.08 TB/s (151.6 us), ahead of 1024 blocks
+// (6.9) and 8192 (3.9).  Small, launch-bound operands gain from fewer blocks
+// (fewer partials to gather): 2^20 elements, per-launch median, 512 / 256 /
+// 128 / 64 blocks: f32 4.96 / 4.12 / 3.88 / 4.31 us, u32 4.51 / 3.72 / 4.06
+// / 4.36; the bench's 2^20 f32 sum, three interleaved runs of 2000 launches:
+// 256 blocks 4.26-4.40 us, 128 blocks 3.97-4.29, 64 blocks 4.36-4.47.
+constexpr uint64_t kElemsPerBlock = 4096, kElemsPerBlockF32 = 8192;
+inline uint32_t full_reduce_blocks(uint64_t n, bool f32) {
+    uint64_t blocks = ceil_div(n, f32 ? kElemsPerBlockF32 : kElemsPerBlock);
     if (blocks > kMaxBlocks) blocks = kMaxBlocks;
     return blocks < 1 ? 1u : (uint32_t)blocks;
 }
@@ -357,7 +359,7 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Loo
             return check_launch("full_reduce_empty_kernel");
         }
     }
-    const uint32_t blocks = full_reduce_blocks(a.n);
+    const uint32_t blocks = full_reduce_blocks(a.n, std::is_same<T, float>::value);
     if (ws_bytes < full_reduce_workspace_bytes(a.n))
         return fail(HX_ERR_DISPATCH_FAILED, "full-reduction workspace of %llu bytes is below %llu",
                     (unsigned long long)ws_bytes, (unsigned long long)full_reduce_workspace_bytes(a.n));
@@ -397,9 +399,10 @@ hx_status launch_kind(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Look
 } // namespace
 
 // Two 64-bit slot words per block (the widest partial) after the header,
-// where every tagged status word of a workspace lives.
+// where every tagged status word of a workspace lives; sized for the larger
+// (integer) grid, whatever the element type.
 uint64_t full_reduce_workspace_bytes(uint64_t n) {
-    return kLookbackOffset + (uint64_t)full_reduce_blocks(n) * 16;
+    return kLookbackOffset + (uint64_t)full_reduce_blocks(n, false) * 16;
 }
 
 // High half of a tagged word as the kernels build it (the host-side copy of
