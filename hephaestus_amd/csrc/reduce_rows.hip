@@ -445,10 +445,12 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
 // argmax (one 64-bit compare per element on a quarter of the threads)
 // takes 184.
 constexpr uint32_t kRowsTileElems = 8192;
-constexpr uint64_t kTileRowMaxCols = 127;
+constexpr uint64_t kTileRowMaxCols = 255;
 
-template <typename T, bool AFFINE, int FLAGS>
+template <typename T, bool AFFINE, int FLAGS, int G>
 __global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t tile_rows) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8, "row groups of 1 to 8 lanes");
+    constexpr uint32_t kRowsPerPass = kBlock / G;
     __shared__ __attribute__((aligned(16))) T tile[kRowsTileElems];
     const uint32_t C = (uint32_t)p.cols;
     const uint32_t L = (uint32_t)p.row_stride; // C, or more for padded rows
@@ -458,12 +460,15 @@ __global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t
                                                        tile);
     __syncthreads();
     const uint32_t w = C | L; // vector LDS reads where every row start and length allow them
-    for (uint32_t r = threadIdx.x; r < n; r += kBlock) {
+    const uint32_t gl = threadIdx.x % G;
+    // The G lanes of a row group share r, so they leave the loop together
+    // and their xor shuffles never read a lane that has left.
+    for (uint32_t r = threadIdx.x / G; r < n; r += kRowsPerPass) {
         Stats<T, FLAGS> st;
         const T *row = tile + r * L;
         if (w % 4 == 0) {
             using V = typename Vec4<T>::type;
-            for (uint32_t j = 0; j < C; j += 4) {
+            for (uint32_t j = 4 * gl; j < C; j += 4 * G) {
                 const V x = *(const V *)(row + j);
                 st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
                 st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
@@ -472,15 +477,17 @@ __global__ __launch_bounds__(kBlock) void rows_tile_kernel(RowParams p, uint32_t
             }
         } else if (w % 2 == 0) {
             typedef T V2 __attribute__((ext_vector_type(2)));
-            for (uint32_t j = 0; j < C; j += 2) {
+            for (uint32_t j = 2 * gl; j < C; j += 2 * G) {
                 const V2 x = *(const V2 *)(row + j);
                 st.visit(prologue<T, AFFINE>((T)x.x, p.a, p.b), j);
                 st.visit(prologue<T, AFFINE>((T)x.y, p.a, p.b), j + 1);
             }
         } else {
-            for (uint32_t j = 0; j < C; ++j) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), j);
+            for (uint32_t j = gl; j < C; j += G) st.visit(prologue<T, AFFINE>(row[j], p.a, p.b), j);
         }
-        st.write(p, r0 + r);
+#pragma unroll
+        for (int m = 1; m < G; m <<= 1) st.merge_xor(m);
+        if (gl == 0) st.write(p, r0 + r);
     }
 }
 
@@ -796,6 +803,7 @@ struct Shape {
     bool block = false; // cols_block_kernel: one launch, no partials
     bool tile = false;  // rows_tile_kernel: tiles of tile_rows short rows
     uint32_t tile_rows = 0;
+    int tile_group = 1; // lanes per row of the tile
     int V = 1;
     int G = kWave; // lanes per row for rows_kernel
     uint64_t groups = 0, chunk = 0;
@@ -873,6 +881,7 @@ Shape plan_shape(const RowParams &p, bool cols_layout) {
         if (tile_rows_fit(p, base)) {
             s.tile = true;
             s.tile_rows = (uint32_t)(((kRowsTileElems - p.cols) / (uint64_t)p.row_stride + 1) & ~3ull);
+            while (s.tile_group < 8 && (uint64_t)s.tile_rows * s.tile_group * 2 <= (uint64_t)kBlock) s.tile_group *= 2;
             return s;
         }
         s.G = row_group_lanes(p.cols, s.vec);
@@ -961,7 +970,14 @@ hx_status launch_rows_typed(const RowParams &p, bool cols_layout, void *ws, uint
         for (uint64_t b0 = 0; b0 < blocks; b0 += max_blocks) {
             q.row0 = b0 * s.tile_rows;
             const dim3 grid((uint32_t)std::min<uint64_t>(max_blocks, blocks - b0)), block(kBlock);
-            hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS>), grid, block, 0, stream, q, s.tile_rows);
+            if (s.tile_group == 8)
+                hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS, 8>), grid, block, 0, stream, q, s.tile_rows);
+            else if (s.tile_group == 4)
+                hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS, 4>), grid, block, 0, stream, q, s.tile_rows);
+            else if (s.tile_group == 2)
+                hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS, 2>), grid, block, 0, stream, q, s.tile_rows);
+            else
+                hipLaunchKernelGGL((rows_tile_kernel<T, AFFINE, FLAGS, 1>), grid, block, 0, stream, q, s.tile_rows);
             HX_TRY(check_launch("rows_tile_kernel"));
         }
         return HX_OK;

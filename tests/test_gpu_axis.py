@@ -209,15 +209,16 @@ def test_split_f32_sums_are_deterministic(device, oracle, r, c):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-# Short dense rows along axis 1 (1 to 127 elements a row, rows back to
+# Short dense rows along axis 1 (1 to 255 elements a row, rows back to
 # back): tiles of (8192 // C) & ~3 whole rows staged in LDS, a row per
-# thread.  Row counts give several tiles and a ragged last one; offsets 1-3
-# start the matrix off a 16-byte boundary.  (128, 300) is the first length
-# past the tiles (lane groups again).
+# thread up to 63 elements and groups of 2, 4 or 8 lanes a row beyond
+# (64: 2, 127-200: 4, 255: 8).  Row counts give several tiles and a ragged
+# last one; offsets 1-3 start the matrix off a 16-byte boundary.  (256,
+# 100) is the first length past the tiles (lane groups again).
 SHORT_ROWS = [(1, 3 * 8192 + 5, 0), (2, 3 * 4096 + 1, 1), (3, 2 * 2728 + 7, 2), (4, 5 * 2048 + 3, 3),
               (5, 2 * 1636 + 1, 0), (6, 3000, 1), (7, 5000, 2), (8, 2049, 0), (12, 1366, 3), (15, 2 * 544 + 9, 1),
               (16, 1000, 0), (33, 3 * 248 + 5, 1), (64, 3 * 128 + 1, 0), (100, 2 * 80 + 3, 2), (127, 3 * 64 + 1, 3),
-              (128, 300, 1)]
+              (128, 300, 1), (160, 2 * 48 + 5, 2), (255, 3 * 32 + 1, 3), (256, 100, 0)]
 
 
 @pytest.mark.parametrize("op", list(OPS))
@@ -232,10 +233,12 @@ def test_short_row_axis_reduce(device, oracle, c, rows, offset, dtype, op):
 # Short rows a little apart (row stride L > C, within 2C or 32 elements):
 # the tiles load the padding with the rows, ((8192 - C) // L + 1) & ~3 rows a
 # tile.  Odd and even distances (scalar and vector LDS reads), one-element
-# rows of a wider matrix, and past the limits (L = 40 for 4 elements, L =
-# 130 for 100): the lane groups again.
+# rows of a wider matrix, groups of lanes a row (100 of 130, 200 of 203),
+# and past the limits (L = 40 for 4 elements, L = 260 for 150): the lane
+# groups again.
 PADDED_ROWS = [(4, 5, 5000, 1), (3, 4, 7000, 0), (1, 7, 9000, 2), (12, 16, 2000, 3), (2, 32, 1000, 1),
-               (7, 9, 3000, 0), (100, 120, 300, 2), (4, 40, 500, 0), (100, 130, 100, 1)]
+               (7, 9, 3000, 0), (100, 120, 300, 2), (100, 130, 100, 1), (200, 203, 100, 3), (4, 40, 500, 0),
+               (150, 260, 100, 1)]
 
 
 @pytest.mark.parametrize("op", ["sum", "max", "argmax", "prod"])
@@ -257,7 +260,7 @@ def test_single_column_rows_of_any_column_stride(device, oracle):
         assert np.array_equal(got.view(np.uint32), host[2:2 + rows].view(np.uint32))
 
 
-@pytest.mark.parametrize("c", [1, 2, 3, 5, 8, 15, 24, 64, 127])
+@pytest.mark.parametrize("c", [1, 2, 3, 5, 8, 15, 24, 64, 127, 192, 255])
 @pytest.mark.parametrize("offset", [0, 1])
 def test_fused_short_rows_many_tiles(device, oracle, c, offset):
     rows = 3 * ((8192 // c) & ~3) + 77
