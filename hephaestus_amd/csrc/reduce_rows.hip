@@ -19,10 +19,10 @@
 //                      stride is unit).
 //   rows_split_kernel  the same for few long rows: one wave per (row, chunk),
 //                      chunk statistics to partial planes.
-//   rows_tile_kernel   rows of 1 to 127 elements, back to back or a little
-//                      apart: a block stages
-//                      a tile of whole rows in LDS with 16-byte loads, then
-//                      folds a row per thread.
+//   rows_tile_kernel   rows of 1 to 255 elements, back to back or a little
+//                      apart: a block stages a tile of whole rows in LDS
+//                      with 16-byte loads, then folds each row with one
+//                      thread or a group of 2 to 8 lanes.
 //   cols_tiles_kernel  the outputs are adjacent and the reduced axis strided
 //                      (axis-0 reduction of a row-major matrix): a wave owns
 //                      256 adjacent outputs (one 16-byte load per lane per
@@ -377,8 +377,10 @@ __device__ __forceinline__ void visit_unit_span(Stats<T, FLAGS> &st, const T *sr
 }
 
 // Row groups of G lanes: G = 1 is a thread per row (rows of fewer than 16
-// elements; back-to-back rows of up to 127 take rows_tile_kernel), G = 4 or 16 puts 16 or 4 rows in each wave, G = 64 a wave per
-// row, G = 128 or 256 two or four waves of the block per row.  The
+// elements), G = 4 or 16 puts 16 or 4 rows in each wave, G = 64 a wave per
+// row, G = 128 or 256 two or four waves of the block per row.  Rows of up
+// to 255 elements at most a little apart take rows_tile_kernel instead
+// (tile_rows_fit).  The
 // host picks G so that each lane holds at least three 16-byte vectors of its
 // row: fewer leaves a lane too little in flight, and the per-row combine then
 // dominates.  Multi-wave groups fold per-lane partials through LDS in wave
@@ -426,24 +428,28 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(RowParams p) {
     if (gl == 0 && r < p.rows) st.write(p, r);
 }
 
-// Short rows (1 to kTileRowMaxCols elements at unit stride, rows back to back
-// or a little apart: tile_rows_fit).  A
-// thread per row (rows_kernel, G = 1) holds only a few elements and reads
-// them with 4-byte loads wherever rows start off a 16-byte boundary, so
-// the launch is bound by lanes and waves, not bytes; groups of 4 lanes
-// (16 elements and more) leave lanes idle in partly filled trips.  Here a
-// block stages a tile of whole rows in LDS with 16-byte direct loads (every
-// wave load moves 1 KiB of contiguous input), then thread i folds rows i,
-// i + 256, ... of the tile out of LDS, elements in index order, and writes
-// their outputs (adjacent lanes, adjacent rows).  Padded rows load their
-// padding with them.  Rows whose length and start distance are even are
-// read as 8- or 16-byte LDS vectors: lanes an even number of words apart
-// would otherwise share banks.  Over 2^28 f32 (sum, max, argmax), microseconds per launch,
-// lane groups -> tiles: 1: 865 -> 385; 2: 578 -> 269; 3: 451 -> 257;
-// 12: 275 -> 189; 20: 235 -> 184; 64: 183 -> 163-178; 80: 215 -> 167-171;
-// 96: 185 -> 164-178.  At 128 the lane groups hold 167 us while the tiles'
-// argmax (one 64-bit compare per element on a quarter of the threads)
-// takes 184.
+// Short rows (1 to kTileRowMaxCols elements at unit stride, rows back to
+// back or a little apart: tile_rows_fit).  A thread per row (rows_kernel,
+// G = 1) holds only a few elements and reads them with 4-byte loads
+// wherever rows start off a 16-byte boundary, so the launch is bound by
+// lanes and waves, not bytes; groups of 4 lanes (16 elements and more)
+// leave lanes idle in partly filled trips.  Here a block stages a tile of
+// whole rows in LDS with 16-byte direct loads (every wave load moves 1 KiB
+// of contiguous input), then each row is folded out of LDS by one thread,
+// or from 64 elements by a group of G = 2, 4 or 8 lanes (the most that
+// keeps the tile's rows times G within the block), each lane taking every
+// G-th element (or vector) in index order, the group combined with xor
+// shuffles; the group's first lane writes the outputs (adjacent groups,
+// adjacent rows).  Padded rows load their padding with them.  Rows whose
+// length and start distance are even are read as 8- or 16-byte LDS
+// vectors: lanes an even number of words apart would otherwise share
+// banks.  Over 2^28 f32 (sum, max, argmax), microseconds per launch, lane
+// groups -> tiles: 1: 865 -> 385; 2: 578 -> 269; 3: 451 -> 257; 12: 275 ->
+// 189; 20: 235 -> 184; 64: 183 -> 160-163; 100: 272 -> 164-167; 128: 167
+// -> 155-157; 160: 185 -> 159-164; 255: 171 -> 154-155; 192: 156 ->
+// 159-163 (40 rows a tile, 160 of 256 threads at G = 4).  With a thread
+// per row the tiles' argmax had fallen behind from 100 elements (188 us
+// at 127, 283 at 255).
 constexpr uint32_t kRowsTileElems = 8192;
 constexpr uint64_t kTileRowMaxCols = 255;
 
