@@ -781,8 +781,8 @@ def pmc_summary(root: Path) -> int:
 TRACE_CONFIGS = [
     ("scan_u32", "u32 exclusive scan 2^28 (headline)", [("scan_tiles_kernel<unsigned int", 8192 * 512)], 8 << 28),
     ("sum_f32", "f32 sum 2^28", [("full_reduce_kernel<float", 768 * 256)], (4 << 28) + 4),
-    # one 256-thread block per 4096 elements below 768 blocks
-    ("sum_f32_2_20", "f32 sum 2^20 (cfg1)", [("full_reduce_kernel<float", (1 << 20) // 4096 * 256)], (4 << 20) + 4),
+    # f32: one 256-thread block per 8192 elements below 768 blocks
+    ("sum_f32_2_20", "f32 sum 2^20 (cfg1)", [("full_reduce_kernel<float", (1 << 20) // 8192 * 256)], (4 << 20) + 4),
     ("rows_f32", "rows 65536 x 4096 (cfg3)", [("rows_kernel<float", 65536 * 256)], (4 << 28) + 12 * 65536),
     ("segmented_i32", "segmented 2^27 (cfg4)", [("seg_tile_map_kernel", None), ("segmented_sum_kernel", None)], None),
     ("scan_f32_2_30", "f32 inclusive scan 2^30 (cfg5)", [("scan_tiles_kernel<float", None)], 8 << 30),

@@ -192,12 +192,13 @@ struct ScanParams {
 };
 
 // The four elements of one lane and step (logical index e..e+3 of the
-// line), identity past the end and before p.head.
-template <typename T, bool VEC, bool REV, bool NT>
+// line), identity past the end and, with HEAD, before p.head.
+template <typename T, bool VEC, bool REV, bool NT, bool HEAD>
 __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t ib, uint64_t e, T ident,
                                       T (&v)[4]) {
+    const uint64_t head = HEAD ? p.head : 0u;
     if constexpr (VEC) {
-        if (e + 3 < p.len && e >= p.head) {
+        if (e + 3 < p.len && e >= head) {
             using V = typename Vec4A4<T>::type;
             if constexpr (REV) {
                 // Logical e..e+3 are physical len-1-e down to len-4-e.
@@ -220,7 +221,7 @@ __device__ __forceinline__ void load4(const ScanParams &p, const T *in, int64_t 
     for (int c = 0; c < 4; ++c) {
         const uint64_t i = e + c;
         const uint64_t li = REV ? (p.len - 1 - i) : i;
-        v[c] = (i < p.len && i >= p.head) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
+        v[c] = (i < p.len && i >= head) ? in[ib + (int64_t)li * p.in_elem_stride] : ident;
     }
 }
 
@@ -233,7 +234,7 @@ __device__ __forceinline__ T lane_fold(const T (&v)[4]) {
 
 // Aggregate of tile `u` computed by ONE wave, step by step, with the same
 // operations and order as the four owner waves (fallback path).
-template <typename T, typename Op, bool VEC, bool REV, bool NT, int STEPS, int WAVES>
+template <typename T, typename Op, bool VEC, bool REV, bool NT, int STEPS, int WAVES, bool HEAD>
 __device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
     constexpr int kWaveElems = kWave * 4 * STEPS;
     constexpr int kTileElems = WAVES * kWaveElems;
@@ -247,7 +248,7 @@ __device__ T tile_aggregate(const ScanParams &p, uint64_t u) {
         T carry = ident;
         for (int j = 0; j < STEPS; ++j) {
             T v[4];
-            load4<T, VEC, REV, NT>(p, in, ib,
+            load4<T, VEC, REV, NT, HEAD>(p, in, ib,
                                    tin * kTileElems + (uint64_t)w * kWaveElems + (uint64_t)j * (kWave * 4) +
                                        (uint64_t)lane_id() * 4,
                                    ident, v);
@@ -287,7 +288,7 @@ template <typename Op, typename C> __device__ __forceinline__ C lookback_reduce(
 // that stays unpublished is computed by tile_aggregate: published for every
 // waiter where the status takes shared fallbacks, else kept in the lane that
 // reads that tile.
-template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES,
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES, bool HEAD,
           typename Hook>
 __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, uint64_t tile_end, int count,
                                          bool &found, Hook &hook) {
@@ -320,7 +321,7 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
         if (++spins >= p.spin_limit) {
             const int k = __ffsll((long long)missing) - 1;
             const uint64_t u = tile_end - 1 - (uint64_t)k;
-            const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS, WAVES>(p, u);
+            const T a = tile_aggregate<T, Op, VEC, REV, NT, STEPS, WAVES, HEAD>(p, u);
             if constexpr (kShared) {
                 if (lane == 0) st.publish_if_unset(u, p.tag, kAggregate, (C)a);
             } else if (lane == k) {
@@ -341,7 +342,7 @@ __device__ typename Status::C fold_tiles(const ScanParams &p, const Status &st, 
 // Exclusive prefix of tile `tile` (position `tin` in its line), computed by
 // one wave.  The last tile of a superblock publishes the superblock
 // aggregate on the way (it needs the tile's own aggregate: hook.agg()).
-template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES,
+template <typename T, typename Op, typename Status, bool VEC, bool REV, bool NT, int STEPS, int WAVES, bool HEAD,
           typename Hook>
 __device__ typename Status::C lookback(const ScanParams &p, const Status &st, const Status &st1, uint64_t tile,
                                        uint64_t line, uint64_t tin, Hook &hook) {
@@ -355,7 +356,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
 
     // Level 0: predecessors in the tile's own superblock.
     bool found = false;
-    C excl = pos > 0 ? fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, tile, pos, found, hook) : ident;
+    C excl = pos > 0 ? fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES, HEAD>(p, st, tile, pos, found, hook) : ident;
     if (found) return excl; // superblock 0 always ends here (tile 0 is a prefix)
     if (last_in_super) {
         const C a = hook.agg();
@@ -396,7 +397,7 @@ __device__ typename Status::C lookback(const ScanParams &p, const Status &st, co
                 const uint64_t s = (uint64_t)(pred - k);
                 const uint64_t s_end = line * p.tiles_per_line + (s - line_super + 1) * kSuper;
                 bool f = false;
-                const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, s_end, kSuper, f, hook);
+                const C v = fold_tiles<T, Op, Status, VEC, REV, NT, STEPS, WAVES, HEAD>(p, st, s_end, kSuper, f, hook);
                 if constexpr (kShared) {
                     if (lane == 0) st1.publish_if_unset(s, p.tag, f ? kPrefix : kAggregate, v);
                 } else if (lane == k) {
@@ -540,7 +541,7 @@ __device__ __forceinline__ void load_full_tile(const T *base, uint32_t lane_off,
 // suffix scan (logical element i is physical len-1-i).  NT: non-temporal
 // vector accesses.
 template <typename T, typename Op, typename Status, bool EXCL, bool VEC, bool REV, int STEPS = kSteps,
-          bool NT = true, int WAVES = kWaves>
+          bool NT = true, int WAVES = kWaves, bool HEAD = false>
 __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(ScanWavesPerEu<T>::value)))
 void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     using C = typename Status::C;
@@ -569,7 +570,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     // Wave index made explicitly uniform so lane offsets stay 32-bit.
     const uint32_t lane_off =
         ((uint32_t)__builtin_amdgcn_readfirstlane(w) * kWaveElems + (uint32_t)lane * 4) * (uint32_t)sizeof(T);
-    const bool full = VEC && (tin + 1) * kTileElems <= p.len && (tin > 0 || p.head == 0);
+    const bool full = VEC && (tin + 1) * kTileElems <= p.len && (!HEAD || tin > 0);
     // Reverse: the tile's lowest physical element, and the mirrored offset.
     const int64_t rev_tile = REV ? (int64_t)(p.len - (tin + 1) * kTileElems) : 0;
     const uint32_t rev_off = (uint32_t)(kTileElems - 4) * (uint32_t)sizeof(T) - lane_off;
@@ -584,7 +585,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
     } else {
 #pragma unroll
         for (int j = 0; j < STEPS; ++j)
-            load4<T, VEC, REV, NT>(p, in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
+            load4<T, VEC, REV, NT, HEAD>(p, in, ib, e0 + (uint64_t)j * (kWave * 4), ident, x[j]);
     }
 
     // Per step: register scan of 4, wave scan of lane totals, running carry.
@@ -653,7 +654,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         } else {
             if (lane == 0) st.publish_tile(tile, p.tag, kAggregate, agg);
             KnownAgg<C> hook{agg};
-            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS, WAVES>(p, st, st1, tile, line, tin, hook);
+            excl = lookback<T, Op, Status, VEC, REV, NT, STEPS, WAVES, HEAD>(p, st, st1, tile, line, tin, hook);
             if (lane == 0) st.publish_tile(tile, p.tag, kPrefix, Op::combine(excl, agg));
         }
         if (lane == 0 && tin % kSuper == kSuper - 1 && tin + 1 < p.tiles_per_line)
@@ -724,7 +725,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
             r[c] = tile_carry.apply(Op::combine(wave_excl, xv));
         }
         if constexpr (VEC) {
-            if (e + 3 < p.len && e >= p.head) {
+            if (e + 3 < p.len && e >= (HEAD ? p.head : 0u)) {
                 using V = typename Vec4A4<T>::type;
                 V v;
                 if constexpr (REV) {
@@ -747,7 +748,7 @@ void scan_tiles_kernel(ScanParams p, Status st, Status st1) {
         for (int c = 0; c < 4; ++c) {
             const uint64_t i = e + c;
             const uint64_t li = REV ? (p.len - 1 - i) : i;
-            if (i < p.len && i >= p.head) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
+            if (i < p.len && i >= (HEAD ? p.head : 0u)) out[ob + (int64_t)li * p.out_elem_stride] = r[c];
         }
     }
 }
@@ -2421,6 +2422,24 @@ hx_status launch_tiles_shaped(ScanParams p, const Status &st, const Status &st1,
     for (uint64_t t0 = 0; t0 < total; t0 += max_blocks) {
         p.tile0 = t0;
         const dim3 grid((uint32_t)std::min<uint64_t>(max_blocks, total - t0)), block(WAVES * kWave);
+        if (p.head != 0) {
+            // Only long lines of 16-byte accesses run on virtual lines
+            // (scan_out_head); the bounds cost the other launches registers,
+            // so they have kernels of their own.
+            if constexpr (STEPS == kSteps && WAVES == kWaves) {
+                if (!vec) return fail(HX_ERR_DISPATCH_FAILED, "virtual line heads need 16-byte accesses");
+                if (rev)
+                    hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true, STEPS, true, WAVES, true>),
+                                       grid, block, 0, stream, p, st, st1);
+                else
+                    hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, false, STEPS, true, WAVES, true>),
+                                       grid, block, 0, stream, p, st, st1);
+                HX_TRY(check_launch("scan_tiles_kernel"));
+                continue;
+            } else {
+                return fail(HX_ERR_DISPATCH_FAILED, "virtual line heads need the long-line tiles");
+            }
+        }
         if (vec && rev)
             hipLaunchKernelGGL((scan_tiles_kernel<T, Op, Status, EXCL, true, true, STEPS, true, WAVES>), grid, block,
                                0, stream, p, st, st1);
