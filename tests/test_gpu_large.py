@@ -285,3 +285,57 @@ def test_strided_row_sums_of_2_26_rows(device):
         assert _slice(device, out, start, 4).tolist() == want, start
     x.free()
     out.free()
+
+
+def test_single_element_rows_past_2_32_rows(device):
+    """[2^32 + 1029, 1] u32 summed along axis 1 takes the short-row LDS tiles
+    (8192 rows a tile, row indices past 2^32): out[r] = x[r].  Every element
+    is 1 except planted 7s either side of 2^32."""
+    x = device.alloc_uninitialized(np.uint32, N)
+    device.fill_uniform_int(x, seed=13, lo=1, hi=1)
+    planted = [0, (1 << 32) - 1, 1 << 32, N - 1]
+    for r in planted:
+        device.write_sub_buffer(x, r, np.array([7], np.uint32))
+    out = device.alloc_zeroed(np.uint32, N)
+    hx.RocmAxisReductionOps().reduce_axis_into(device, hx.SumOp, StridedView(x, Layout.c_contiguous([N, 1])), 1,
+                                               StridedView(out, Layout.c_contiguous([N, 1])))
+    for start in (0, (1 << 32) - 4, N - 4):
+        want = [7 if start + i in planted else 1 for i in range(4)]
+        assert _slice(device, out, start, 4).tolist() == want, start
+    x.free()
+    out.free()
+
+
+def test_reversed_view_reductions_past_2_32_elements(device):
+    """A stride -1 view of N u32 streamed as the dense range it covers: sum
+    3N mod 2^32 of all-3s, and the max of one planted value."""
+    x = device.alloc_uninitialized(np.uint32, N)
+    device.fill_uniform_int(x, seed=14, lo=3, hi=3)
+    view = StridedView(x, Layout.try_new([N], [-1], N - 1))
+    out = device.alloc_zeroed(np.uint32, 1)
+    FULL.reduce_full_into(device, hx.SumOp, view, StridedView(out, ONE))
+    assert int(device.download_owned(out)[0]) == (3 * N) % 2**32
+    device.write_sub_buffer(x, (1 << 32) + 3, np.array([11], np.uint32))
+    FULL.reduce_full_into(device, hx.MaxOp, view, StridedView(out, ONE))
+    assert int(device.download_owned(out)[0]) == 11
+    x.free()
+    out.free()
+
+
+def test_exclusive_scan_off_the_line_grid_past_2_32_elements(device):
+    """All-ones u32 scanned into an output 5 elements past a 128-byte
+    boundary: the line runs on a virtual line 5 longer, tiles on the
+    output's grid; out[5 + i] = i mod 2^32 and the 5 elements before it stay
+    untouched."""
+    x = device.alloc_uninitialized(np.uint32, N)
+    device.fill_uniform_int(x, seed=15, lo=1, hi=1)
+    out = device.alloc_uninitialized(np.uint32, N + 5)
+    device.write_sub_buffer(out, 0, np.full(5, 0xABCD, np.uint32))
+    SCAN.scan_axis_into(device, hx.CumSumOp, StridedView(x, Layout.c_contiguous([N])), 0, hx.ScanDirection.Forward,
+                        StridedView(out, Layout.try_new([N], [1], 5)), hx.ScanKind.Exclusive)
+    assert _slice(device, out, 0, 5).tolist() == [0xABCD] * 5
+    for start in (0, (1 << 31) - 4, (1 << 32) - 4, N - 8):
+        want = [(start + i) % 2**32 for i in range(8)]
+        assert _slice(device, out, 5 + start, 8).tolist() == want, start
+    x.free()
+    out.free()
