@@ -29,9 +29,12 @@ def f32_bound(n, abs_sum):
 
 def prod_bound(n):
     """gamma_{n-1} = (n-1)u / (1 - (n-1)u), u = 2^-24: the relative error
-    bound of any evaluation order of a product of n f32 factors."""
+    bound of any evaluation order of a product of n f32 factors.  It exists
+    only while (n-1)u < 1; from 2^24 + 1 factors no relative bound holds,
+    and the result is inf (a check against it then rejects only NaN; the
+    tests' factors lie near 1, so the reference is never 0)."""
     k = (int(n) - 1) * 2.0**-24
-    return k / (1.0 - k)
+    return k / (1.0 - k) if k < 1.0 else float("inf")
 
 
 def lines_of(host, shape, strides, offset, axis):
