@@ -145,6 +145,10 @@ bool layout_is_permuted_dense(const hx_layout &l);
 // signs of its strides dropped (each reversed dimension read from its other
 // end) it is a permuted dense view.  *first is the lowest element it reaches.
 bool layout_covers_dense_range(const hx_layout &l, uint64_t *first);
+// Every dimension runs backwards and, read from its other end, the view is
+// row-major: element k of the view (row-major order) is element n - 1 - k of
+// the dense range [*first, *first + size).
+bool layout_is_reversed_c_contiguous(const hx_layout &l, uint64_t *first);
 // A view as rows: `rows` rows of `cols` elements, element c of a row at
 // c * cstride, the row index split over up to three outer dimensions
 // (innermost first) from the view's offset.  Each dimension also carries a
@@ -231,6 +235,7 @@ struct FullReduceArgs {
     uint64_t n;          // logical size
     bool flat;           // view is the flat range [flat_offset, +n)
     bool memory_order;   // not flat: walk rows in memory order (argmax of a permuted dense view)
+    bool reversed;       // flat: the view reads the range from its far end (view index n - 1 - e)
     uint64_t flat_offset;
     bool affine;
     float a, b;

@@ -407,8 +407,17 @@ hx_status hx_argmax_full(hx_device *dev, hx_dtype dtype, const void *in, uint64_
     // a permuted dense one (a transpose) is read in memory order with each
     // element's logical index carried along.
     a.flat = layout_is_c_contiguous(*in_layout);
-    a.memory_order = !a.flat && layout_is_permuted_dense(*in_layout);
     a.flat_offset = in_layout->offset;
+    // A view read entirely backwards is the flat range from its far end:
+    // view index n - 1 - e, so the first index of the maximum is still found
+    // by the smallest index on ties.
+    uint64_t first = 0;
+    if (!a.flat && layout_is_reversed_c_contiguous(*in_layout, &first)) {
+        a.flat = true;
+        a.reversed = true;
+        a.flat_offset = first;
+    }
+    a.memory_order = !a.flat && layout_is_permuted_dense(*in_layout);
     a.affine = affine;
     a.a = pa;
     a.b = pb;

@@ -166,6 +166,24 @@ bool layout_covers_dense_range(const hx_layout &l, uint64_t *first) {
     return true;
 }
 
+bool layout_is_reversed_c_contiguous(const hx_layout &l, uint64_t *first) {
+    hx_layout m = l;
+    int64_t lo = (int64_t)l.offset;
+    bool any = false;
+    for (uint32_t d = 0; d < l.rank; ++d) {
+        if (l.shape[d] <= 1) continue;
+        if (l.strides[d] >= 0) return false;
+        lo += (int64_t)(l.shape[d] - 1) * l.strides[d];
+        m.strides[d] = -l.strides[d];
+        any = true;
+    }
+    if (!any || lo < 0) return false;
+    m.offset = (uint64_t)lo;
+    if (!layout_is_c_contiguous(m)) return false;
+    *first = m.offset;
+    return true;
+}
+
 } // namespace hx
 
 using namespace hx;

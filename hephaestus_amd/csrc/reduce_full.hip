@@ -122,6 +122,11 @@ struct FullParams {
     uint64_t *slots;     // partial slots (PartialSlot), 16 bytes per block
     uint32_t tag;        // this launch's tag
     uint32_t poll_limit; // gather polls per partial before recomputing it
+    // Flat views: element e of the range has view index e, or n - 1 - e
+    // when the view reads the range from its far end (rev; argmax reports
+    // view indices).
+    uint64_t idx_last;
+    uint32_t rev;
 };
 
 template <typename T, bool AFFINE> __device__ __forceinline__ T prologue(T x, float, float) { return x; }
@@ -172,13 +177,14 @@ __device__ __forceinline__ void write_result_impl(const FullParams &p, typename 
 }
 
 
+// Four elements with view indices e .. e + 3, or e .. e - 3 when rev.
 template <typename P, typename T, bool AFFINE, typename V>
-__device__ __forceinline__ typename P::Acc fold4(const V &v, uint64_t e, float a, float b) {
+__device__ __forceinline__ typename P::Acc fold4(const V &v, uint64_t e, bool rev, float a, float b) {
     using Acc = typename P::Acc;
     const Acc a0 = P::lift(prologue<T, AFFINE>((T)v.x, a, b), e);
-    const Acc a1 = P::lift(prologue<T, AFFINE>((T)v.y, a, b), e + 1);
-    const Acc a2 = P::lift(prologue<T, AFFINE>((T)v.z, a, b), e + 2);
-    const Acc a3 = P::lift(prologue<T, AFFINE>((T)v.w, a, b), e + 3);
+    const Acc a1 = P::lift(prologue<T, AFFINE>((T)v.y, a, b), rev ? e - 1 : e + 1);
+    const Acc a2 = P::lift(prologue<T, AFFINE>((T)v.z, a, b), rev ? e - 2 : e + 2);
+    const Acc a3 = P::lift(prologue<T, AFFINE>((T)v.w, a, b), rev ? e - 3 : e + 3);
     return P::combine(P::combine(a0, a1), P::combine(a2, a3));
 }
 
@@ -258,7 +264,9 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
         uint64_t mis = ((uintptr_t)src >> 2) & 3u;
         uint64_t head = mis ? (4 - mis) : 0;
         if (head > n) head = n;
-        if (tid < head) acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[tid], p.a, p.b), tid));
+        const bool rev = p.rev != 0;
+        auto vidx = [&](uint64_t e) { return rev ? p.idx_last - e : e; };
+        if (tid < head) acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[tid], p.a, p.b), vidx(tid)));
         const uint64_t nvec = (n - head) >> 2;
         using V = typename Vec4<T>::type;
         const V *vsrc = (const V *)(src + head);
@@ -269,14 +277,14 @@ __device__ __forceinline__ typename P::Acc thread_fold(const FullParams &p, uint
             for (int u = 0; u < UNROLL; ++u) v[u] = load_vec<NT>(&vsrc[vi + u * nthreads]);
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
-                acc = P::combine(acc, fold4<P, T, AFFINE>(v[u], head + 4 * (vi + u * nthreads), p.a, p.b));
+                acc = P::combine(acc, fold4<P, T, AFFINE>(v[u], vidx(head + 4 * (vi + u * nthreads)), rev, p.a, p.b));
         }
         for (; vi < nvec; vi += nthreads)
-            acc = P::combine(acc, fold4<P, T, AFFINE>(load_vec<NT>(&vsrc[vi]), head + 4 * vi, p.a, p.b));
+            acc = P::combine(acc, fold4<P, T, AFFINE>(load_vec<NT>(&vsrc[vi]), vidx(head + 4 * vi), rev, p.a, p.b));
         const uint64_t tail0 = head + 4 * nvec;
         if (tail0 + tid < n) {
             const uint64_t e = tail0 + tid;
-            acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[e], p.a, p.b), e));
+            acc = P::combine(acc, P::lift(prologue<T, AFFINE>(src[e], p.a, p.b), vidx(e)));
         }
     } else {
         constexpr int W = Walkers<MODE>::value;
@@ -351,6 +359,8 @@ hx_status launch_typed(const FullReduceArgs &a, void *ws, uint64_t ws_bytes, Loo
     p.out_index = a.out_index;
     p.slots = (uint64_t *)((char *)ws + kLookbackOffset);
     p.poll_limit = gather_poll_limit();
+    p.idx_last = a.n - 1;
+    p.rev = a.reversed ? 1u : 0u;
     if (a.n == 0) {
         if constexpr (K == kMean) {
             return fail(HX_ERR_DISPATCH_FAILED, "mean is undefined for an empty operand");
