@@ -21,6 +21,7 @@
 #include "rows_walk.hpp"
 
 #include <type_traits>
+#include <utility>
 
 namespace hx {
 namespace {
@@ -76,6 +77,10 @@ struct MapParams {
     uint64_t n;
     uint64_t a_off, b_off; // element offsets (layout offsets)
     RowsGeom g;            // non-flat views: rows of a, form 2 walks b
+    // kPairTile: a is contiguous along the rows, (i, j) at a_off + i + j *
+    // col_ld; b along the columns, (i, j) at b_off + i * row_ld + j.
+    uint64_t rows, cols, tiles, tiles_c;
+    int64_t col_ld, row_ld;
     void *out;
     uint64_t *slots;     // partial slots (PartialSlot), 16 bytes per block
     uint32_t tag;        // this launch's tag
@@ -83,8 +88,14 @@ struct MapParams {
 };
 // How the operands are walked: flat element ranges, or rows (RowsGeom) of
 // 16-byte vector units (both operands' rows contiguous) or of single
-// elements.
-enum Mode { kFlat = 0, kRowsVec = 1, kRowsScalar = 2 };
+// elements, or (a dot of a transposed matrix with a row-major one) 64 x 64
+// tiles, the transposed operand's tile turned through LDS.
+enum Mode { kFlat = 0, kRowsVec = 1, kRowsScalar = 2, kPairTile = 3 };
+// Tile edge of kPairTile and the LDS pitch of its staged tile: column j of
+// the tile at j * 65, so the 16 columns a wave reads at one row fall in
+// distinct banks.
+constexpr int kPairEdge = 64;
+constexpr int kPairPitch = kPairEdge + 1;
 // Units in flight per thread in the row modes: two for a dot (two loads per
 // unit; four walkers took 113 VGPRs against 80 and stride-2 dots 195 us
 // against 185 at 2^27 pairs), four for one-operand maps.
@@ -148,8 +159,15 @@ template <typename P> __device__ __forceinline__ typename P::Acc block_reduce(ty
 // at any element offsets from each other.
 // Row modes: a's rows walked with b's offsets as the second form
 // (layout_rows_pair), MapWalkers units in flight.
+// kPairTile: block vb takes tiles vb, vb + G, ...; each thread loads four
+// 16-byte vectors of the tile's columns of a (16 lanes a column) and four of
+// its rows of b (16 lanes a row), parks a's vectors in `tile` (column j at
+// j * kPairPitch) and pairs each element of b with the tile's (i, j).  Tiles
+// on the right or bottom edge load and pair only elements inside the
+// matrix.
 template <typename T, int M, int MODE>
-__device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const MapParams &p, uint32_t vb, uint32_t G) {
+__device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const MapParams &p, uint32_t vb, uint32_t G,
+                                                                        T *tile) {
     using P = MapPolicy<T, M>;
     using Acc = typename P::Acc;
     using V = typename Vec4A4<T>::type;
@@ -190,6 +208,73 @@ __device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const M
         }
         const uint64_t tail0 = head + 4 * nvec;
         if (tail0 + tid < n) acc = P::combine(acc, P::elem(a[tail0 + tid], b[tail0 + tid]));
+    } else if constexpr (MODE == kPairTile) {
+        const T *a = (const T *)p.a + p.a_off;
+        const T *b = (const T *)p.b + p.b_off;
+        const uint32_t q4 = 4 * (threadIdx.x & 15), r16 = threadIdx.x >> 4;
+        for (uint64_t tb = vb; tb < p.tiles; tb += G) {
+            const uint64_t i0 = tb / p.tiles_c * kPairEdge, j0 = tb % p.tiles_c * kPairEdge;
+            const bool full = i0 + kPairEdge <= p.rows && j0 + kPairEdge <= p.cols;
+            T x[4][4], y[4][4];
+            if (full) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const V u = load_a4<true>((const V *)(a + (i0 + q4) + (j0 + r16 + 16 * k) * p.col_ld));
+                    const V w = load_a4<true>((const V *)(b + (i0 + r16 + 16 * k) * p.row_ld + j0 + q4));
+                    x[k][0] = (T)u.x, x[k][1] = (T)u.y, x[k][2] = (T)u.z, x[k][3] = (T)u.w;
+                    y[k][0] = (T)w.x, y[k][1] = (T)w.y, y[k][2] = (T)w.z, y[k][3] = (T)w.w;
+                }
+            } else {
+                // Edge tiles.  Every lane issues its vector loads, so they
+                // are in flight together as in a full tile: a vector not
+                // wholly inside the matrix is read as the view's first
+                // vector (elements (0..3, 0) of a, (0, 0..3) of b: inside,
+                // as both extents are at least kPairMinEdge) and dropped.
+                // The vector of a line that straddles the matrix's edge is
+                // then read element by element.
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint64_t jc = j0 + r16 + 16 * k, ir = i0 + r16 + 16 * k;
+                    const bool wa = jc < p.cols && i0 + q4 + 4 <= p.rows;
+                    const bool wb = ir < p.rows && j0 + q4 + 4 <= p.cols;
+                    const V u = load_a4<true>((const V *)(wa ? a + (i0 + q4) + jc * p.col_ld : a));
+                    const V w = load_a4<true>((const V *)(wb ? b + ir * p.row_ld + j0 + q4 : b));
+                    x[k][0] = wa ? (T)u.x : T(0), x[k][1] = wa ? (T)u.y : T(0);
+                    x[k][2] = wa ? (T)u.z : T(0), x[k][3] = wa ? (T)u.w : T(0);
+                    y[k][0] = wb ? (T)w.x : T(0), y[k][1] = wb ? (T)w.y : T(0);
+                    y[k][2] = wb ? (T)w.z : T(0), y[k][3] = wb ? (T)w.w : T(0);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint64_t jc = j0 + r16 + 16 * k, ir = i0 + r16 + 16 * k;
+                    if (jc < p.cols && i0 + q4 < p.rows && i0 + q4 + 4 > p.rows) {
+                        const T *pa = a + (i0 + q4) + jc * p.col_ld;
+#pragma unroll
+                        for (int c = 0; c < 3; ++c) x[k][c] = i0 + q4 + c < p.rows ? pa[c] : T(0);
+                    }
+                    if (ir < p.rows && j0 + q4 < p.cols && j0 + q4 + 4 > p.cols) {
+                        const T *pb = b + ir * p.row_ld + j0 + q4;
+#pragma unroll
+                        for (int c = 0; c < 3; ++c) y[k][c] = j0 + q4 + c < p.cols ? pb[c] : T(0);
+                    }
+                }
+            }
+            __syncthreads(); // the previous tile's reads of `tile` are done
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) tile[(r16 + 16 * k) * kPairPitch + q4 + c] = x[k][c];
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t il = r16 + 16 * k;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const T t = tile[(q4 + c) * kPairPitch + il];
+                    if (full || (i0 + il < p.rows && j0 + q4 + c < p.cols)) acc = P::combine(acc, P::elem(t, y[k][c]));
+                }
+            }
+        }
     } else {
         // Rows (RowsGeom): kWalkers walkers, each stepping kWalkers * nthreads units.
         const RowsGeom &g = p.g;
@@ -238,14 +323,15 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
     __shared__ Acc lds[kBlock / kWave];
     __shared__ Acc vals[kMaxBlocks];
     __shared__ uint32_t missing[kMaxBlocks / 32];
+    __shared__ T tile[MODE == kPairTile ? kPairEdge * kPairPitch : 1];
     const uint32_t G = gridDim.x;
-    const Acc part = block_reduce<P>(map_thread_fold<T, M, MODE>(p, blockIdx.x, G), lds);
+    const Acc part = block_reduce<P>(map_thread_fold<T, M, MODE>(p, blockIdx.x, G, tile), lds);
     if (blockIdx.x + 1 != G) {
         if (threadIdx.x == 0) Slot::publish(p.slots + (uint64_t)blockIdx.x * Slot::kWords, p.tag, part);
         return;
     }
     gather_partials<kBlock, kMaxBlocks>(p.slots, p.tag, p.poll_limit, G, part, vals, missing, [&](uint32_t k) {
-        return block_reduce<P>(map_thread_fold<T, M, MODE>(p, k, G), lds);
+        return block_reduce<P>(map_thread_fold<T, M, MODE>(p, k, G, tile), lds);
     });
     Acc r = P::identity();
     for (uint32_t k = threadIdx.x; k < G; k += kBlock) r = P::combine(r, vals[k]);
@@ -256,6 +342,10 @@ __global__ __launch_bounds__(kBlock) void map_reduce_kernel(MapParams p) {
 template <typename T, int M> __global__ void map_reduce_empty_kernel(MapParams p) {
     if (threadIdx.x == 0 && blockIdx.x == 0) write_map_result<T, M>(p, MapPolicy<T, M>::identity());
 }
+
+// Smallest extent the tiled pairing takes (narrower matrices are walked as
+// rows).
+constexpr uint64_t kPairMinEdge = 16;
 
 // One block per 4096 elements up to 768 (the full reduction's grid rule).
 uint32_t map_blocks(uint64_t n) {
@@ -284,8 +374,25 @@ hx_status launch_typed(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, Look
         return fail(HX_ERR_DISPATCH_FAILED, "map-reduction workspace of %llu bytes is below %llu",
                     (unsigned long long)ws_bytes, (unsigned long long)map_reduce_workspace_bytes(a.n));
     HX_TRY(next_lookback_launch(lb, ws, ws_bytes, stream, &p.tag));
+    PairTranspose pt;
     if (a.flat) {
         hipLaunchKernelGGL((map_reduce_kernel<T, M, kFlat>), dim3(blocks), dim3(kBlock), 0, stream, p);
+    } else if (M == kMapDot && layout_pair_transposed(a.a_layout, a.b_layout, &pt) && pt.rows >= kPairMinEdge &&
+               pt.cols >= kPairMinEdge) {
+        // The product is symmetric, so the operand contiguous along the
+        // rows goes first.
+        if (!pt.a_is_col) {
+            std::swap(p.a, p.b);
+            std::swap(p.a_off, p.b_off);
+        }
+        p.rows = pt.rows;
+        p.cols = pt.cols;
+        p.tiles_c = ceil_div(pt.cols, (uint64_t)kPairEdge);
+        p.tiles = ceil_div(pt.rows, (uint64_t)kPairEdge) * p.tiles_c;
+        p.col_ld = pt.col_ld;
+        p.row_ld = pt.row_ld;
+        hipLaunchKernelGGL((map_reduce_kernel<T, M, M == kMapDot ? kPairTile : kRowsScalar>), dim3(blocks),
+                           dim3(kBlock), 0, stream, p);
     } else {
         const RowsView rv = layout_rows_pair(a.a_layout, M == kMapDot ? a.b_layout : a.a_layout);
         const bool vec = rv.cstride == 1 && rv.cstride2 == 1 && rv.cols >= 4;

@@ -105,6 +105,31 @@ RowsView layout_rows_pair(const hx_layout &a, const hx_layout &b) {
     return rows_from_dims(a.shape, a.strides, b.strides, (int)a.rank);
 }
 
+bool layout_pair_transposed(const hx_layout &a, const hx_layout &b, PairTranspose *t) {
+    if (a.rank != b.rank) return false;
+    int dims[2], m = 0;
+    for (uint32_t d = 0; d < a.rank; ++d) {
+        if (a.shape[d] != b.shape[d]) return false;
+        if (a.shape[d] <= 1) continue;
+        if (m == 2) return false;
+        dims[m++] = (int)d;
+    }
+    if (m != 2) return false;
+    const int d0 = dims[0], d1 = dims[1];
+    bool a_col;
+    if (a.strides[d0] == 1 && b.strides[d1] == 1) a_col = true;
+    else if (a.strides[d1] == 1 && b.strides[d0] == 1) a_col = false;
+    else return false;
+    const hx_layout &c = a_col ? a : b, &r = a_col ? b : a;
+    if (c.strides[d1] <= 0 || r.strides[d0] <= 0) return false;
+    t->a_is_col = a_col;
+    t->rows = a.shape[d0];
+    t->cols = a.shape[d1];
+    t->col_ld = c.strides[d1];
+    t->row_ld = r.strides[d0];
+    return true;
+}
+
 RowsView layout_rows_memory_order(const hx_layout &l) {
     int64_t lstride[HX_MAX_RANK];
     logical_strides(l, lstride);

@@ -263,6 +263,16 @@ PAIR_VIEWS = [
     ([40, 33], [-33, -1], 1319, [-33, -1], 6319),    # both fully reversed
     ([33, 40], [-1, 33], 32, [-1, 33], 2032),        # reversed transpose
     ([5000], [-1], 4999, [1], 7),                    # reversed . forward: element walk
+    # a transposed matrix paired with a row-major one: 64 x 64 tiles, the
+    # transposed tile turned through LDS (edge tiles ragged in both
+    # directions, padded leading dimensions, any element offsets)
+    ([130, 70], [1, 131], 3, [75, 1], 17),
+    ([64, 128], [128, 1], 0, [1, 64], 0),            # row-major . transposed
+    ([256, 256], [1, 256], 0, [256, 1], 1000),       # full tiles only
+    ([16, 200], [1, 16], 5, [200, 1], 9),            # smallest tiled extent
+    ([200, 15], [1, 200], 0, [15, 1], 0),            # below it: element walk
+    ([1, 96, 80], [9999, 1, 96], 2, [7680, 80, 1], 1),  # a unit dimension
+    ([97, 3, 33], [1, 97, 291], 0, [99, 33, 1], 0),  # three extents: element walk
 ]
 
 
@@ -297,3 +307,29 @@ def test_map_reductions_of_strided_views(device, oracle, view, dtype):
         assert one(device, hx.dot(device, va, vb)) == oracle.dot(xa, xb)
         assert one(device, hx.norm_l1(device, va)) == oracle.norm_l1(xa)
     assert one(device, hx.norm_max(device, va)) == oracle.norm_max(xa)
+
+
+@pytest.mark.parametrize("shape", [(2048, 3000), (3001, 2047), (40000, 17)])
+@pytest.mark.parametrize("dtype", [np.float32, np.int32])
+def test_dot_of_a_transpose_with_a_row_major_matrix(device, oracle, shape, dtype):
+    """Many tiles per block and both operand orders."""
+    r, c = shape
+    if dtype == np.float32:
+        ha = oracle.uniform_real(r * c + 3, seed=r, lo=-2.0, hi=2.0)
+        hb = oracle.uniform_real(r * c + 5, seed=c, lo=-2.0, hi=2.0)
+    else:
+        ha = oracle.uniform_int(r * c + 3, seed=r, lo=-70000, hi=70000, dtype=np.int32)
+        hb = oracle.uniform_int(r * c + 5, seed=c, lo=-70000, hi=70000, dtype=np.int32)
+    ba, bb = device.upload(ha), device.upload(hb)
+    la = Layout.try_new([r, c], [1, r], 3)  # column-major
+    lb = Layout.try_new([r, c], [c, 1], 5)  # row-major
+    xa = ha[3:3 + r * c].reshape(c, r).T.ravel()
+    xb = hb[5:5 + r * c]
+    for va, vb, pa, pb in ((StridedView(ba, la), StridedView(bb, lb), xa, xb),
+                           (StridedView(bb, lb), StridedView(ba, la), xb, xa)):
+        if dtype == np.float32:
+            want, mags = oracle.dot(pa, pb)
+            got = float(one(device, hx.dot(device, va, vb)))
+            assert abs(got - want) <= f32_bound(r * c, mags) + abs(want) * EPS / 2, (got, want)
+        else:
+            assert one(device, hx.dot(device, va, vb)) == oracle.dot(pa, pb)
