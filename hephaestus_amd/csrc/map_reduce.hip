@@ -123,13 +123,14 @@ __device__ __forceinline__ uint32_t load_pair(const RowsGeom &g, const T *a, con
             }
             return 4;
         }
+        // Every slot is written on both paths: stores of some slots only
+        // get merged into one store at a run-time index, which keeps the
+        // arrays in scratch memory.
         const uint32_t cnt = (uint32_t)(g.cols - c0);
 #pragma unroll
-        for (uint32_t c = 0; c < 3; ++c) {
-            if (c < cnt) {
-                x[c] = a[w.off + c];
-                if constexpr (TWO) y[c] = b[w.off2 + c];
-            }
+        for (uint32_t c = 0; c < 4; ++c) {
+            x[c] = c < cnt ? a[w.off + c] : T(0);
+            if constexpr (TWO) y[c] = c < cnt ? b[w.off2 + c] : T(0);
         }
         return cnt;
     } else {
