@@ -333,3 +333,25 @@ def test_dot_of_a_transpose_with_a_row_major_matrix(device, oracle, shape, dtype
             assert abs(got - want) <= f32_bound(r * c, mags) + abs(want) * EPS / 2, (got, want)
         else:
             assert one(device, hx.dot(device, va, vb)) == oracle.dot(pa, pb)
+
+
+def test_dot_of_transposed_pairs_random_geometry(device, oracle):
+    """Seeded sweep of the tiled pairing: extents 16-300, padded leading
+    dimensions, element offsets and either operand transposed, bit-exact in
+    i32."""
+    rng = np.random.default_rng(2029)
+    host = oracle.uniform_int(400000, seed=77, lo=-5000, hi=5000, dtype=np.int32)
+    buf = device.upload(host)
+    for _ in range(60):
+        r, c = (int(v) for v in rng.integers(16, 301, size=2))
+        cld = r + int(rng.integers(0, 9))
+        rld = c + int(rng.integers(0, 9))
+        oa = int(rng.integers(0, 400000 - cld * c))
+        ob = int(rng.integers(0, 400000 - rld * r))
+        la = Layout.try_new([r, c], [1, cld], oa)
+        lb = Layout.try_new([r, c], [rld, 1], ob)
+        xa, xb = _elems(host, [r, c], [1, cld], oa), _elems(host, [r, c], [rld, 1], ob)
+        va, vb = StridedView(buf, la), StridedView(buf, lb)
+        if rng.integers(0, 2):
+            va, vb, xa, xb = vb, va, xb, xa
+        assert one(device, hx.dot(device, va, vb)) == oracle.dot(xa, xb), (r, c, cld, rld, oa, ob)
