@@ -175,16 +175,17 @@ RowsView layout_rows_memory_order(const hx_layout &l);
 // Rows of two same-shape views in logical order: the first form walks `a`,
 // the second `b`'s strides.
 RowsView layout_rows_pair(const hx_layout &a, const hx_layout &b);
-// Two same-shape views with exactly two extents above one, (rows, cols),
-// one view contiguous along the first of them and the other along the
-// second (a transposed matrix paired with a row-major one), both other
-// strides positive: element (i, j) of the first at its offset + i + j *
-// col_ld, of the second at its offset + i * row_ld + j.  a_is_col says
-// which operand is contiguous along the rows.
+// Two same-shape views with two or three extents above one: one view
+// contiguous along one of them (the rows), the other along another (the
+// columns), both other strides of those two positive, and any third
+// extent a batch of such matrices (a transposed matrix paired with a
+// row-major one).  Element (b, i, j) of the first at its offset + b *
+// col_bs + i + j * col_ld, of the second at its offset + b * row_bs + i *
+// row_ld + j.  a_is_col says which operand is contiguous along the rows.
 struct PairTranspose {
     bool a_is_col = false;
-    uint64_t rows = 0, cols = 0;
-    int64_t col_ld = 0, row_ld = 0;
+    uint64_t rows = 0, cols = 0, batch = 1;
+    int64_t col_ld = 0, row_ld = 0, col_bs = 0, row_bs = 0;
 };
 bool layout_pair_transposed(const hx_layout &a, const hx_layout &b, PairTranspose *t);
 hx_status layout_basic_check(const hx_layout *l, const char *what);

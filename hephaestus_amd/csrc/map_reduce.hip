@@ -77,10 +77,11 @@ struct MapParams {
     uint64_t n;
     uint64_t a_off, b_off; // element offsets (layout offsets)
     RowsGeom g;            // non-flat views: rows of a, form 2 walks b
-    // kPairTile: a is contiguous along the rows, (i, j) at a_off + i + j *
-    // col_ld; b along the columns, (i, j) at b_off + i * row_ld + j.
-    uint64_t rows, cols, tiles, tiles_c;
-    int64_t col_ld, row_ld;
+    // kPairTile: a is contiguous along the rows, (k, i, j) at a_off + k *
+    // col_bs + i + j * col_ld; b along the columns, (k, i, j) at b_off + k *
+    // row_bs + i * row_ld + j, for matrices k of a batch.
+    uint64_t rows, cols, tiles, tiles_c, tiles_m;
+    int64_t col_ld, row_ld, col_bs, row_bs;
     void *out;
     uint64_t *slots;     // partial slots (PartialSlot), 16 bytes per block
     uint32_t tag;        // this launch's tag
@@ -160,7 +161,8 @@ template <typename P> __device__ __forceinline__ typename P::Acc block_reduce(ty
 // at any element offsets from each other.
 // Row modes: a's rows walked with b's offsets as the second form
 // (layout_rows_pair), MapWalkers units in flight.
-// kPairTile: block vb takes tiles vb, vb + G, ...; each thread loads four
+// kPairTile: block vb takes tiles vb, vb + G, ... (the tiles of matrix k of
+// a batch follow those of matrix k - 1); each thread loads four
 // 16-byte vectors of the tile's columns of a (16 lanes a column) and four of
 // its rows of b (16 lanes a row), parks a's vectors in `tile` (column j at
 // j * kPairPitch) and pairs each element of b with the tile's (i, j).  Tiles
@@ -210,11 +212,14 @@ __device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const M
         const uint64_t tail0 = head + 4 * nvec;
         if (tail0 + tid < n) acc = P::combine(acc, P::elem(a[tail0 + tid], b[tail0 + tid]));
     } else if constexpr (MODE == kPairTile) {
-        const T *a = (const T *)p.a + p.a_off;
-        const T *b = (const T *)p.b + p.b_off;
+        const T *a0 = (const T *)p.a + p.a_off;
+        const T *b0 = (const T *)p.b + p.b_off;
         const uint32_t q4 = 4 * (threadIdx.x & 15), r16 = threadIdx.x >> 4;
         for (uint64_t tb = vb; tb < p.tiles; tb += G) {
-            const uint64_t i0 = tb / p.tiles_c * kPairEdge, j0 = tb % p.tiles_c * kPairEdge;
+            const uint64_t mk = tb / p.tiles_m, tm = tb - mk * p.tiles_m;
+            const T *a = a0 + (int64_t)mk * p.col_bs;
+            const T *b = b0 + (int64_t)mk * p.row_bs;
+            const uint64_t i0 = tm / p.tiles_c * kPairEdge, j0 = tm % p.tiles_c * kPairEdge;
             const bool full = i0 + kPairEdge <= p.rows && j0 + kPairEdge <= p.cols;
             T x[4][4], y[4][4];
             if (full) {
@@ -228,7 +233,7 @@ __device__ __forceinline__ typename MapPolicy<T, M>::Acc map_thread_fold(const M
             } else {
                 // Edge tiles.  Every lane issues its vector loads, so they
                 // are in flight together as in a full tile: a vector not
-                // wholly inside the matrix is read as the view's first
+                // wholly inside the matrix is read as the matrix's first
                 // vector (elements (0..3, 0) of a, (0, 0..3) of b: inside,
                 // as both extents are at least kPairMinEdge) and dropped.
                 // The vector of a line that straddles the matrix's edge is
@@ -389,7 +394,10 @@ hx_status launch_typed(const MapReduceArgs &a, void *ws, uint64_t ws_bytes, Look
         p.rows = pt.rows;
         p.cols = pt.cols;
         p.tiles_c = ceil_div(pt.cols, (uint64_t)kPairEdge);
-        p.tiles = ceil_div(pt.rows, (uint64_t)kPairEdge) * p.tiles_c;
+        p.tiles_m = ceil_div(pt.rows, (uint64_t)kPairEdge) * p.tiles_c;
+        p.tiles = pt.batch * p.tiles_m;
+        p.col_bs = pt.col_bs;
+        p.row_bs = pt.row_bs;
         p.col_ld = pt.col_ld;
         p.row_ld = pt.row_ld;
         hipLaunchKernelGGL((map_reduce_kernel<T, M, M == kMapDot ? kPairTile : kRowsScalar>), dim3(blocks),

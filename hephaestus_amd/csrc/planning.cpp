@@ -107,27 +107,38 @@ RowsView layout_rows_pair(const hx_layout &a, const hx_layout &b) {
 
 bool layout_pair_transposed(const hx_layout &a, const hx_layout &b, PairTranspose *t) {
     if (a.rank != b.rank) return false;
-    int dims[2], m = 0;
+    int dims[3], m = 0;
     for (uint32_t d = 0; d < a.rank; ++d) {
         if (a.shape[d] != b.shape[d]) return false;
         if (a.shape[d] <= 1) continue;
-        if (m == 2) return false;
+        if (m == 3) return false;
         dims[m++] = (int)d;
     }
-    if (m != 2) return false;
-    const int d0 = dims[0], d1 = dims[1];
-    bool a_col;
-    if (a.strides[d0] == 1 && b.strides[d1] == 1) a_col = true;
-    else if (a.strides[d1] == 1 && b.strides[d0] == 1) a_col = false;
-    else return false;
-    const hx_layout &c = a_col ? a : b, &r = a_col ? b : a;
-    if (c.strides[d1] <= 0 || r.strides[d0] <= 0) return false;
-    t->a_is_col = a_col;
-    t->rows = a.shape[d0];
-    t->cols = a.shape[d1];
-    t->col_ld = c.strides[d1];
-    t->row_ld = r.strides[d0];
-    return true;
+    if (m < 2) return false;
+    for (int pass = 0; pass < 2; ++pass) {
+        const bool a_col = pass == 0;
+        const hx_layout &c = a_col ? a : b, &r = a_col ? b : a;
+        int di = -1, dj = -1;
+        for (int k = 0; k < m; ++k) {
+            if (di < 0 && c.strides[dims[k]] == 1) di = dims[k];
+            if (dj < 0 && r.strides[dims[k]] == 1) dj = dims[k];
+        }
+        if (di < 0 || dj < 0 || di == dj) continue;
+        if (c.strides[dj] <= 0 || r.strides[di] <= 0) continue;
+        int db = -1;
+        for (int k = 0; k < m; ++k)
+            if (dims[k] != di && dims[k] != dj) db = dims[k];
+        t->a_is_col = a_col;
+        t->rows = a.shape[di];
+        t->cols = a.shape[dj];
+        t->col_ld = c.strides[dj];
+        t->row_ld = r.strides[di];
+        t->batch = db < 0 ? 1 : a.shape[db];
+        t->col_bs = db < 0 ? 0 : c.strides[db];
+        t->row_bs = db < 0 ? 0 : r.strides[db];
+        return true;
+    }
+    return false;
 }
 
 RowsView layout_rows_memory_order(const hx_layout &l) {

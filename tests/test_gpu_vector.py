@@ -272,7 +272,13 @@ PAIR_VIEWS = [
     ([16, 200], [1, 16], 5, [200, 1], 9),            # smallest tiled extent
     ([200, 15], [1, 200], 0, [15, 1], 0),            # below it: element walk
     ([1, 96, 80], [9999, 1, 96], 2, [7680, 80, 1], 1),  # a unit dimension
-    ([97, 3, 33], [1, 97, 291], 0, [99, 33, 1], 0),  # three extents: element walk
+    # three extents: a batch of transposed . row-major pairs, the batch
+    # extent in any position and its strides of any sign
+    ([97, 3, 33], [1, 97, 291], 0, [99, 33, 1], 0),
+    ([5, 40, 70], [2800, 1, 40], 7, [2800, 70, 1], 3),
+    ([4, 30, 20], [-600, 1, 30], 1805, [600, 20, 1], 0),
+    ([20, 6, 30], [30, 600, 1], 2, [1, 20, 600], 11),  # the batch in the middle
+    ([3, 17, 15], [255, 1, 17], 0, [255, 15, 1], 0),   # below the tiled extent
 ]
 
 
