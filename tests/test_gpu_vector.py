@@ -361,3 +361,34 @@ def test_dot_of_transposed_pairs_random_geometry(device, oracle):
         if rng.integers(0, 2):
             va, vb, xa, xb = vb, va, xb, xa
         assert one(device, hx.dot(device, va, vb)) == oracle.dot(xa, xb), (r, c, cld, rld, oa, ob)
+
+
+def test_dot_of_batched_transposed_pairs_random_geometry(device, oracle):
+    """Seeded sweep of batches of transposed . row-major pairs: the batch
+    extent in any position, batch strides of either sign, bit-exact in i32."""
+    rng = np.random.default_rng(2030)
+    size = 400000
+    host = oracle.uniform_int(size, seed=78, lo=-5000, hi=5000, dtype=np.int32)
+    buf = device.upload(host)
+    for _ in range(40):
+        nb = int(rng.integers(2, 5))
+        r, c = (int(v) for v in rng.integers(16, 121, size=2))
+        cld, rld = r + int(rng.integers(0, 5)), c + int(rng.integers(0, 5))
+        abs_, bbs = cld * c, rld * r
+        sa = [1, cld]   # (i, j) strides of the transposed operand
+        sb = [rld, 1]   # (i, j) strides of the row-major one
+        sga = abs_ if rng.integers(0, 2) else -abs_
+        sgb = bbs if rng.integers(0, 2) else -bbs
+        pos = int(rng.integers(0, 3))  # where the batch extent sits
+        shape, stra, strb = [r, c], list(sa), list(sb)
+        shape.insert(pos, nb)
+        stra.insert(pos, sga)
+        strb.insert(pos, sgb)
+        oa = int(rng.integers(0, size - nb * abs_)) + (abs_ * (nb - 1) if sga < 0 else 0)
+        ob = int(rng.integers(0, size - nb * bbs)) + (bbs * (nb - 1) if sgb < 0 else 0)
+        la, lb = Layout.try_new(shape, stra, oa), Layout.try_new(shape, strb, ob)
+        xa, xb = _elems(host, shape, stra, oa), _elems(host, shape, strb, ob)
+        va, vb = StridedView(buf, la), StridedView(buf, lb)
+        if rng.integers(0, 2):
+            va, vb, xa, xb = vb, va, xb, xa
+        assert one(device, hx.dot(device, va, vb)) == oracle.dot(xa, xb), (shape, stra, strb, oa, ob)
